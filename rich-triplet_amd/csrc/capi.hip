@@ -1,0 +1,203 @@
+// capi.hip -- extern "C" boundary of librt_hip.so (declared in include/rt_hip.h).
+//
+// Validation happens here, before any kernel is launched: every shape the
+// kernels assume (K multiple of 256 or 8, 16-byte alignment, non-null
+// pointers, int32 row counts) is checked on the host and reported as
+// RT_EINVAL instead of reaching the GPU.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <map>
+#include <mutex>
+#include <string>
+#include <utility>
+
+#include "../../include/rt_hip.h"
+#include "rt_capi_util.hpp"
+#include "rt_kernels.hpp"
+
+namespace rt {
+
+static thread_local std::string g_last_error;
+
+rt_status set_error(rt_status code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+rt_status hip_error(hipError_t e, const char *what) {
+  if (e == hipSuccess) return RT_OK;
+  if (e == hipErrorOutOfMemory) return set_error(RT_ENOMEM, "%s: %s", what, hipGetErrorString(e));
+  return set_error(RT_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace rt
+
+using namespace rt;
+
+extern "C" {
+
+const char *rt_last_error(void) { return g_last_error.c_str(); }
+
+int32_t rt_abi_version(void) { return 1; }
+
+rt_status rt_q4k_dequant_f32(const void *blocks, size_t n_blocks, float *out, void *stream) {
+  if (n_blocks == 0) return RT_OK;
+  if (!blocks || !out) return set_error(RT_EINVAL, "rt_q4k_dequant_f32: null pointer");
+  if (!aligned16(blocks) || !aligned16(out)) return set_error(RT_EINVAL, "rt_q4k_dequant_f32: buffers must be 16-byte aligned");
+  return hip_error(launch_q4k_dequant(blocks, n_blocks, out, false, (hipStream_t)stream), "rt_q4k_dequant_f32");
+}
+
+rt_status rt_q4k_dequant_bf16(const void *blocks, size_t n_blocks, uint16_t *out, void *stream) {
+  if (n_blocks == 0) return RT_OK;
+  if (!blocks || !out) return set_error(RT_EINVAL, "rt_q4k_dequant_bf16: null pointer");
+  if (!aligned16(blocks) || !aligned16(out)) return set_error(RT_EINVAL, "rt_q4k_dequant_bf16: buffers must be 16-byte aligned");
+  return hip_error(launch_q4k_dequant(blocks, n_blocks, out, true, (hipStream_t)stream), "rt_q4k_dequant_bf16");
+}
+
+rt_status check_gemv_shape(const char *who, const void *w, const float *x, const float *y, int64_t n, int64_t k,
+                           int64_t kmult) {
+  if (n <= 0 || k <= 0) return set_error(RT_EINVAL, "%s: n=%lld k=%lld must be positive", who, (long long)n, (long long)k);
+  if (k % kmult != 0) return set_error(RT_EINVAL, "%s: k=%lld must be a multiple of %lld", who, (long long)k, (long long)kmult);
+  if (n > INT32_MAX || k > INT32_MAX) return set_error(RT_EINVAL, "%s: n or k exceeds int32", who);
+  if (!w || !x || !y) return set_error(RT_EINVAL, "%s: null pointer", who);
+  if (!aligned16(w) || !aligned16(x)) return set_error(RT_EINVAL, "%s: w and x must be 16-byte aligned", who);
+  return RT_OK;
+}
+
+rt_status rt_q4k_gemv(const void *w, const float *x, float *y, int64_t n, int64_t k, void *stream) {
+  rt_status st = check_gemv_shape("rt_q4k_gemv", w, x, y, n, k, 256);
+  if (st != RT_OK) return st;
+  return hip_error(launch_q4k_gemv(w, x, y, (int)n, (int)k, (hipStream_t)stream), "rt_q4k_gemv");
+}
+
+rt_status rt_bf16_gemv(const uint16_t *w, const float *x, float *y, int64_t n, int64_t k, void *stream) {
+  rt_status st = check_gemv_shape("rt_bf16_gemv", w, x, y, n, k, 8);
+  if (st != RT_OK) return st;
+  return hip_error(launch_bf16_gemv(w, x, y, (int)n, (int)k, (hipStream_t)stream), "rt_bf16_gemv");
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Host-pointer drop-ins with a weight cache keyed by (host pointer, bytes).
+// ---------------------------------------------------------------------------
+namespace {
+
+struct CacheKey {
+  int device;
+  const void *ptr;
+  size_t bytes;
+  bool operator<(const CacheKey &o) const {
+    if (device != o.device) return device < o.device;
+    if (ptr != o.ptr) return ptr < o.ptr;
+    return bytes < o.bytes;
+  }
+};
+
+std::mutex g_cache_mu;
+std::map<CacheKey, void *> g_weight_cache;
+
+rt_status cached_upload(const void *host, size_t bytes, void **dev_out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_error(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lk(g_cache_mu);
+  CacheKey key{dev, host, bytes};
+  auto it = g_weight_cache.find(key);
+  if (it != g_weight_cache.end()) {
+    *dev_out = it->second;
+    return RT_OK;
+  }
+  void *d = nullptr;
+  e = hipMalloc(&d, bytes);
+  if (e != hipSuccess) return hip_error(e, "weight upload hipMalloc");
+  e = hipMemcpy(d, host, bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(d);
+    return hip_error(e, "weight upload hipMemcpy");
+  }
+  g_weight_cache[key] = d;
+  *dev_out = d;
+  return RT_OK;
+}
+
+// Per-call activation/output staging (the reference's scratch_act / output buffers).
+struct Staging {
+  void *buf = nullptr;
+  size_t cap = 0;
+};
+thread_local Staging g_stage;
+
+rt_status stage(size_t bytes, void **out) {
+  if (g_stage.cap < bytes) {
+    if (g_stage.buf) (void)hipFree(g_stage.buf);
+    g_stage.buf = nullptr;
+    g_stage.cap = 0;
+    hipError_t e = hipMalloc(&g_stage.buf, bytes);
+    if (e != hipSuccess) return hip_error(e, "staging hipMalloc");
+    g_stage.cap = bytes;
+  }
+  *out = g_stage.buf;
+  return RT_OK;
+}
+
+template <typename LaunchFn>
+rt_status host_gemv(const char *who, const float *a, size_t k, const void *w_host, size_t w_bytes, size_t rows,
+                    float *out, LaunchFn launch) {
+  void *wdev = nullptr, *buf = nullptr;
+  rt_status st = cached_upload(w_host, w_bytes, &wdev);
+  if (st != RT_OK) return st;
+  const size_t xbytes = (k * sizeof(float) + 255) & ~size_t(255);
+  st = stage(xbytes + rows * sizeof(float), &buf);
+  if (st != RT_OK) return st;
+  float *xd = static_cast<float *>(buf);
+  float *yd = reinterpret_cast<float *>(static_cast<char *>(buf) + xbytes);
+  hipError_t e = hipMemcpy(xd, a, k * sizeof(float), hipMemcpyHostToDevice);
+  if (e != hipSuccess) return hip_error(e, who);
+  e = launch(wdev, xd, yd);
+  if (e != hipSuccess) return hip_error(e, who);
+  e = hipMemcpy(out, yd, rows * sizeof(float), hipMemcpyDeviceToHost);
+  return hip_error(e, who);
+}
+
+}  // namespace
+
+extern "C" {
+
+rt_status rt_gemv_q4k_t(const float *a, size_t k, const uint8_t *blocks, size_t rows, float *out) {
+  if (!a || !blocks || !out) return set_error(RT_EINVAL, "rt_gemv_q4k_t: null pointer");
+  if (k == 0 || rows == 0 || k % 256 != 0 || k > INT32_MAX || rows > INT32_MAX)
+    return set_error(RT_EINVAL, "rt_gemv_q4k_t: k=%zu rows=%zu (k must be a positive multiple of 256)", k, rows);
+  const size_t bytes = rows * (k / 256) * 144;
+  return host_gemv("rt_gemv_q4k_t", a, k, blocks, bytes, rows, out, [&](void *w, float *x, float *y) {
+    return launch_q4k_gemv(w, x, y, (int)rows, (int)k, nullptr);
+  });
+}
+
+rt_status rt_gemv_bf16_t(const float *a, size_t k, const uint16_t *w, size_t rows, float *out) {
+  if (!a || !w || !out) return set_error(RT_EINVAL, "rt_gemv_bf16_t: null pointer");
+  if (k == 0 || rows == 0 || k % 8 != 0 || k > INT32_MAX || rows > INT32_MAX)
+    return set_error(RT_EINVAL, "rt_gemv_bf16_t: k=%zu rows=%zu (k must be a positive multiple of 8)", k, rows);
+  const size_t bytes = rows * k * 2;
+  return host_gemv("rt_gemv_bf16_t", a, k, w, bytes, rows, out, [&](void *wd, float *x, float *y) {
+    return launch_bf16_gemv(static_cast<const uint16_t *>(wd), x, y, (int)rows, (int)k, nullptr);
+  });
+}
+
+rt_status rt_weight_cache_clear(void) {
+  std::lock_guard<std::mutex> lk(g_cache_mu);
+  for (auto &kv : g_weight_cache) (void)hipFree(kv.second);
+  g_weight_cache.clear();
+  return RT_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,17 @@
+// rt_kernels.hpp -- host-side launchers for the rich-triplet HIP kernels.
+// Shapes are validated by the C ABI layer before any of these is called.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace rt {
+
+hipError_t launch_q4k_dequant(const void *blocks, size_t n_blocks, void *out, bool bf16, hipStream_t s);
+hipError_t launch_q4k_gemv(const void *W, const float *x, float *y, int N, int K, hipStream_t s);
+hipError_t launch_q4k_gemv_generic(const void *W, const float *x, float *y, int N, int K, hipStream_t s);
+int q4k_gemv_rows_per_wg(int N, int K);
+hipError_t launch_bf16_gemv(const uint16_t *W, const float *x, float *y, int N, int K, hipStream_t s);
+
+}  // namespace rt

@@ -1,0 +1,58 @@
+"""The C-ABI library loads, exports every symbol include/*.h declares, and
+rejects bad shapes on the host before any GPU work (no GPU needed)."""
+from __future__ import annotations
+
+import ctypes as C
+import pathlib
+import re
+
+import pytest
+
+from conftest import REPO
+
+
+def declared_symbols() -> set[str]:
+    names = set()
+    for h in (REPO / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(rt_[a-z0-9_]+)\s*\(", text))
+    return names
+
+
+def test_header_declares_entry_points():
+    names = declared_symbols()
+    assert {"rt_q4k_gemv", "rt_bf16_gemv", "rt_q4k_dequant_f32", "rt_last_error"} <= names
+
+
+def test_library_exports_every_declared_symbol(rt):
+    lib = rt.lib()
+    missing = [n for n in sorted(declared_symbols()) if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(rt.exported_symbols()) <= declared_symbols()
+    assert lib.rt_abi_version() >= 1
+
+
+@pytest.mark.parametrize("n,k,what", [(16, 100, "multiple of 256"), (0, 256, "positive"), (16, -256, "positive")])
+def test_q4k_gemv_rejects_bad_shapes_before_launch(rt, n, k, what):
+    buf = (C.c_uint8 * 64)()
+    addr = (C.addressof(buf) + 15) & ~15
+    st = rt.lib().rt_q4k_gemv(addr, addr, addr, n, k, None)
+    assert st == rt.RT_EINVAL
+    assert what in rt.lib().rt_last_error().decode()
+
+
+def test_null_and_misaligned_pointers_are_rejected(rt):
+    L = rt.lib()
+    assert L.rt_q4k_gemv(None, None, None, 16, 256, None) == rt.RT_EINVAL
+    buf = (C.c_uint8 * 64)()
+    addr = ((C.addressof(buf) + 15) & ~15) + 4
+    assert L.rt_bf16_gemv(addr, addr, addr, 16, 256, None) == rt.RT_EINVAL
+    assert "aligned" in L.rt_last_error().decode()
+    assert L.rt_bf16_gemv(addr - 4, addr - 4, addr - 4, 16, 12, None) == rt.RT_EINVAL
+    assert L.rt_gemv_q4k_t(None, 256, None, 4, None) == rt.RT_EINVAL
+    with pytest.raises(rt.RtError):
+        rt.check(L.rt_gemv_bf16_t(addr, 7, addr, 4, addr))
+
+
+def test_zero_block_dequant_is_a_no_op(rt):
+    assert rt.lib().rt_q4k_dequant_f32(None, 0, None, None) == rt.RT_OK

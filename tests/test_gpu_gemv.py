@@ -1,0 +1,128 @@
+"""GPU parity of the Q4_K dequant and the Q4_K / BF16 GEMV kernels against the
+CPU oracle, called through the C ABI (librt_hip.so)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import rel_l2, to_dev
+from test_oracle import MAKE_TEST_Q4K_FIRST_HALF, _make_test_q4k
+
+pytestmark = pytest.mark.gpu
+
+GEMV_TOL = 1e-3  # rel-L2 vs the reference's sequential f32 CPU order
+
+
+def _sync():
+    import torch
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("rows,cols,seed", [(1, 256, 1), (24, 1024, 2), (10240, 2560, 3)])
+def test_dequant_f32_bit_exact(rt, orc, dev, rows, cols, seed):
+    import torch
+    blocks = orc.synth_q4k(seed, rows, cols)
+    if rows == 24:  # plant subnormal / zero / large d, dmin in a few blocks
+        b = blocks.reshape(-1, 144)
+        for i, (d, m) in enumerate([(0x0001, 0x0003), (0x03FF, 0x0200), (0x0000, 0x0000), (0x7BFF, 0x3C00),
+                                    (0x8001, 0x83FF)]):
+            b[i, 0:2] = np.array([d], np.uint16).view(np.uint8)
+            b[i, 2:4] = np.array([m], np.uint16).view(np.uint8)
+    wd = to_dev(blocks, dev)
+    out = torch.empty(rows * cols, dtype=torch.float32, device=dev)
+    rt.q4k_dequant_f32(wd, out)
+    _sync()
+    got = out.cpu().numpy()
+    if rows * cols <= 24 * 1024:
+        ref = orc.q4k_dequant(blocks, rows, cols).reshape(-1)
+    else:
+        ref = orc.q4k_dequant_gguf(blocks, rows * cols)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_dequant_bf16_is_rne_of_f32(rt, orc, dev):
+    import torch
+    blocks = orc.synth_q4k(9, 64, 512)
+    wd = to_dev(blocks, dev)
+    out = torch.empty(64 * 512, dtype=torch.int16, device=dev)
+    rt.q4k_dequant_bf16(wd, out)
+    _sync()
+    ref = torch.from_numpy(orc.q4k_dequant_gguf(blocks, 64 * 512)).to(torch.bfloat16).view(torch.int16)
+    assert torch.equal(out.cpu(), ref)
+
+
+def test_dequant_make_test_q4k(rt, dev):
+    import torch
+    blocks = _make_test_q4k(4, 512)
+    out = torch.empty(4 * 512, dtype=torch.float32, device=dev)
+    rt.q4k_dequant_f32(to_dev(blocks, dev), out)
+    _sync()
+    expect = np.tile(np.r_[np.full(128, MAKE_TEST_Q4K_FIRST_HALF), np.zeros(128)], 8).astype(np.float32)
+    assert np.array_equal(out.cpu().numpy(), expect)
+
+
+@pytest.mark.parametrize("n,k", [(4, 256), (64, 512), (2048, 2560), (1024, 2560), (10240, 2560), (2560, 2048),
+                                 (2560, 10240), (1000, 2560), (37, 1792), (3, 10240)])
+def test_q4k_gemv_matches_oracle(rt, orc, dev, n, k):
+    import torch
+    blocks = orc.synth_q4k(1000 + n + k, n, k)
+    a = orc.synth_normal(2000 + n + k, k)
+    y = torch.full((n,), float("nan"), dtype=torch.float32, device=dev)
+    rt.q4k_gemv(to_dev(blocks, dev), to_dev(a, dev), y, n, k)
+    _sync()
+    got = y.cpu().numpy()
+    ref = orc.q4k_gemv(blocks, n, k, a)
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, ref) < GEMV_TOL
+    assert rel_l2(got, orc.q4k_gemv_f64(blocks, n, k, a)) < 1e-5
+
+
+def test_q4k_gemv_reference_fixtures(rt, orc):
+    """metal_ops.rs:1154-1235 through the host-pointer drop-in (rel < 1e-3 per row)."""
+    for n, k, fn in ((4, 256, lambda c: (c + 1) * 0.01), (64, 512, lambda c: ((c % 7) - 3.0) * 0.1)):
+        blocks = _make_test_q4k(n, k)
+        a = np.array([fn(c) for c in range(k)], np.float32)
+        got = rt.gemv_q4k_t(a, blocks, n)
+        w = orc.q4k_dequant(blocks, n, k)
+        exp = (w * a).sum(axis=1)
+        assert np.all(np.abs(got - exp) / (np.abs(exp) + 1e-6) < 1e-3)
+    # cache reuse: same weights, two activations
+    blocks = _make_test_q4k(4, 256)
+    a1 = np.arange(256, dtype=np.float32) * 0.01
+    a2 = (256 - np.arange(256, dtype=np.float32)) * 0.01
+    r1, r2 = rt.gemv_q4k_t(a1, blocks, 4), rt.gemv_q4k_t(a2, blocks, 4)
+    assert not np.array_equal(r1, r2)
+    for a, r in ((a1, r1), (a2, r2)):
+        exp = (orc.q4k_dequant(blocks, 4, 256) * a).sum(axis=1)
+        assert np.all(np.abs(r - exp) / (np.abs(exp) + 1e-6) < 1e-3)
+    rt.weight_cache_clear()
+
+
+@pytest.mark.parametrize("n,k", [(8, 64), (128, 256), (4096, 2560), (262144, 2560), (1001, 2560), (77, 1000)])
+def test_bf16_gemv_matches_oracle(rt, orc, dev, n, k):
+    import torch
+    w = orc.synth_bf16(3000 + n, n * k)
+    a = orc.synth_normal(4000 + n, k)
+    y = torch.full((n,), float("nan"), dtype=torch.float32, device=dev)
+    rt.bf16_gemv(to_dev(w, dev), to_dev(a, dev), y, n, k)
+    _sync()
+    got = y.cpu().numpy()
+    if n <= 4096:
+        ref = orc.bf16_gemv(w, n, k, a)
+        assert rel_l2(got, orc.bf16_gemv_f64(w, n, k, a)) < 1e-5
+    else:  # full lm_head shape: the f32 oracle over 671M weights takes a few seconds
+        ref = orc.bf16_gemv(w, n, k, a)
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, ref) < GEMV_TOL
+
+
+def test_bf16_gemv_reference_fixtures(rt, orc):
+    """metal_ops.rs:1239-1305 (abs < 1e-2) through the host-pointer drop-in."""
+    for n, k, wf, af in ((8, 64, lambda i: ((i % 17) - 8.0) * 0.1, lambda c: (c + 1.0) * 0.05),
+                         (128, 256, lambda i: ((i % 31) - 15.0) * 0.01, lambda c: ((c % 13) - 6.0) * 0.1)):
+        w = np.array([orc.f32_to_bf16(wf(i)) for i in range(n * k)], np.uint16)
+        a = np.array([af(c) for c in range(k)], np.float32)
+        got = rt.gemv_bf16_t(a, w, n)
+        exp = orc.bf16_gemv(w, n, k, a)
+        assert np.all(np.abs(got - exp) < 1e-2)
+    rt.weight_cache_clear()
