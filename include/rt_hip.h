@@ -73,6 +73,63 @@ rt_status rt_gemv_q4k_t(const float *a_host, size_t k, const uint8_t *blocks_hos
 rt_status rt_gemv_bf16_t(const float *a_host, size_t k, const uint16_t *w_host, size_t rows, float *out_host);
 rt_status rt_weight_cache_clear(void);
 
+/* ---------------------------------------------------------------------------
+ * Gemma-3 decode engine -- replaces MetalDecodeContext (metal_decode.rs:754-829).
+ * One step = embedding lookup, n_layers Gemma-3 blocks (4-norm, GQA with
+ * sliding-window / global layers, NeoX RoPE, gated GELU-tanh) and the BF16
+ * tied lm_head, executed as one hipGraph on the context's stream.  The KV
+ * cache is f32 and device-resident, [max_seq, n_kv_heads*head_dim] per layer.
+ * Semantics follow the reference CPU path (transformer4.rs:1900-1964,
+ * 2358-2385); the GPU path of the reference keeps an f16 cache capped at
+ * 2048 rows (metal_decode.rs:1186), this engine does not.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    /* Config4 fields (transformer4.rs:112-131). */
+    int32_t hidden, ffn, n_q_heads, n_kv_heads, head_dim, n_layers, vocab;
+    int32_t sliding_window;   /* keys attended by local layers, 0 = none */
+    int32_t global_every;     /* layer i is global iff i % global_every == global_every-1 (6 for Gemma 3) */
+    int32_t max_seq;          /* KV rows allocated per layer */
+    float rope_theta_local, rope_theta_global, rope_fs_local, rope_fs_global;
+    float eps, attn_scale;    /* rms_norm_eps; 1/sqrt(query_pre_attn_scalar) */
+} rt_gemma3_config;
+
+/* One layer's weights: Q4_K blocks (rows = out features) and RMSNorm gammas
+ * as used in x/rms*(1+gamma).  LayerWeightBuffers, metal_decode.rs:720-748. */
+typedef struct {
+    const void *q, *k, *v, *o, *gate, *up, *down;
+    const float *in_norm, *post_attn_norm, *pre_ffn_norm, *post_ffn_norm, *q_norm, *k_norm;
+} rt_gemma3_layer;
+
+typedef struct rt_decode rt_decode;
+
+/* MetalDecodeContext::new (metal_decode.rs:971-1254) minus the weight upload,
+ * which the two calls below perform.  Supported shapes: hidden 512|2560,
+ * n_q_heads*head_dim 512|2048, ffn 1024|10240, head_dim 128|256, group 1|2|4. */
+rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out);
+rt_status rt_decode_destroy(rt_decode *d);
+/* device_ptrs = 0: host pointers, copied (Q4_K bytes verbatim, 144-B blocks
+ * stay packed; upload_linear_detect_type, metal_decode.rs:1259-1277).
+ * device_ptrs = 1: device pointers, borrowed; the caller keeps them alive. */
+rt_status rt_decode_set_layer(rt_decode *d, int32_t layer, const rt_gemma3_layer *w, int32_t device_ptrs);
+/* BF16 [vocab, hidden] embedding, also the tied lm_head (1097-1105), and the final norm gamma. */
+rt_status rt_decode_set_embed(rt_decode *d, const uint16_t *embed, const float *final_norm, int32_t device_ptrs);
+/* sync_kv_from_cpu (metal_decode.rs:1366-1396) for one layer: seq_len rows of K and V. */
+rt_status rt_decode_sync_kv(rt_decode *d, int32_t layer, const float *k, const float *v, int32_t seq_len,
+                            int32_t device_ptrs);
+/* decode_step (metal_decode.rs:2028-2074): appends K/V at row `position`
+ * and writes vocab logits to logits_host (may be NULL); synchronous. */
+rt_status rt_decode_step(rt_decode *d, int32_t token, int32_t position, float *logits_host);
+/* Same step, only enqueued on the context stream; logits stay on the device. */
+rt_status rt_decode_step_async(rt_decode *d, int32_t token, int32_t position);
+rt_status rt_decode_synchronize(rt_decode *d);
+/* Use the captured hipGraph (default) or launch the kernels one by one. */
+rt_status rt_decode_set_graph(rt_decode *d, int32_t enabled);
+/* Device buffers of the context, for inspection. */
+rt_status rt_decode_logits(rt_decode *d, float **logits_dev);
+rt_status rt_decode_kv(rt_decode *d, int32_t layer, float **k_dev, float **v_dev);
+rt_status rt_decode_hidden(rt_decode *d, float **x2_dev, float **dn_dev);
+rt_status rt_decode_get_stream(rt_decode *d, void **stream);
+
 #ifdef __cplusplus
 }
 #endif

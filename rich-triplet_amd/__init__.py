@@ -50,6 +50,19 @@ _SIGNATURES = {
     "rt_gemv_q4k_t": (_i32, [_vp, _sz, _vp, _sz, _vp]),
     "rt_gemv_bf16_t": (_i32, [_vp, _sz, _vp, _sz, _vp]),
     "rt_weight_cache_clear": (_i32, []),
+    "rt_decode_create": (_i32, [_vp, C.POINTER(_vp)]),
+    "rt_decode_destroy": (_i32, [_vp]),
+    "rt_decode_set_layer": (_i32, [_vp, _i32, _vp, _i32]),
+    "rt_decode_set_embed": (_i32, [_vp, _vp, _vp, _i32]),
+    "rt_decode_sync_kv": (_i32, [_vp, _i32, _vp, _vp, _i32, _i32]),
+    "rt_decode_step": (_i32, [_vp, _i32, _i32, _vp]),
+    "rt_decode_step_async": (_i32, [_vp, _i32, _i32]),
+    "rt_decode_synchronize": (_i32, [_vp]),
+    "rt_decode_set_graph": (_i32, [_vp, _i32]),
+    "rt_decode_logits": (_i32, [_vp, C.POINTER(_vp)]),
+    "rt_decode_kv": (_i32, [_vp, _i32, C.POINTER(_vp), C.POINTER(_vp)]),
+    "rt_decode_hidden": (_i32, [_vp, C.POINTER(_vp), C.POINTER(_vp)]),
+    "rt_decode_get_stream": (_i32, [_vp, C.POINTER(_vp)]),
 }
 
 
@@ -138,3 +151,115 @@ def gemv_bf16_t(a, w, rows: int):
 
 def weight_cache_clear() -> None:
     check(lib().rt_weight_cache_clear())
+
+
+# ---------------------------------------------------------------------------
+# Gemma-3 decode engine (rt_decode_*), mirrors MetalDecodeContext
+# ---------------------------------------------------------------------------
+class Gemma3Config(C.Structure):
+    """rt_gemma3_config (Config4, transformer4.rs:112-131)."""
+    _fields_ = [(n, C.c_int32) for n in ("hidden", "ffn", "n_q_heads", "n_kv_heads", "head_dim", "n_layers",
+                                         "vocab", "sliding_window", "global_every", "max_seq")] + \
+               [(n, C.c_float) for n in ("rope_theta_local", "rope_theta_global", "rope_fs_local",
+                                         "rope_fs_global", "eps", "attn_scale")]
+
+
+class Gemma3Layer(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("q", "k", "v", "o", "gate", "up", "down", "in_norm", "post_attn_norm",
+                                          "pre_ffn_norm", "post_ffn_norm", "q_norm", "k_norm")]
+
+
+GEMMA3_4B = dict(hidden=2560, ffn=10240, n_q_heads=8, n_kv_heads=4, head_dim=256, n_layers=34, vocab=262144,
+                 sliding_window=1024, global_every=6, rope_theta_local=10000.0, rope_theta_global=1000000.0,
+                 rope_fs_local=1.0, rope_fs_global=0.125, eps=1e-6, attn_scale=1.0 / 16.0)
+"""Config4::gemma3_4b (transformer4.rs:112-131) with vocab 262144 (the GGUF
+embedding table size, metal_decode.rs lm_head_vocab)."""
+
+
+def _addr(x) -> int:
+    if isinstance(x, int):
+        return x
+    if hasattr(x, "data_ptr"):
+        return x.data_ptr()
+    import numpy as np
+    assert isinstance(x, np.ndarray) and x.flags["C_CONTIGUOUS"]
+    return x.ctypes.data
+
+
+class HipDecodeContext:
+    """One Gemma-3 decode context on the current HIP device.
+
+    new / set_layer / set_embed / sync_kv_from_cpu / decode_step mirror
+    MetalDecodeContext::{new, sync_kv_from_cpu, decode_step}
+    (metal_decode.rs:971, 1366, 2028).  Arrays may be numpy (host, copied) or
+    torch cuda tensors (device, borrowed: keep them alive)."""
+
+    def __init__(self, cfg: dict, max_seq: int):
+        fields = {k: cfg[k] for k, _ in Gemma3Config._fields_ if k != "max_seq"}
+        self.cfg = dict(cfg, max_seq=max_seq)
+        self._c = Gemma3Config(max_seq=max_seq, **fields)
+        h = C.c_void_p()
+        check(lib().rt_decode_create(C.byref(self._c), C.byref(h)))
+        self._h = h
+        self._keep = []
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            lib().rt_decode_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @staticmethod
+    def _on_device(x) -> int:
+        return int(hasattr(x, "is_cuda") and x.is_cuda)
+
+    def set_layer(self, i: int, w: dict) -> None:
+        dev = self._on_device(w["q"])
+        L = Gemma3Layer(**{k: _addr(w[k]) for k, _ in Gemma3Layer._fields_})
+        if dev:
+            self._keep.append(w)
+        check(lib().rt_decode_set_layer(self._h, i, C.byref(L), dev))
+
+    def set_embed(self, embed, final_norm) -> None:
+        dev = self._on_device(embed)
+        if dev:
+            self._keep.append((embed, final_norm))
+        check(lib().rt_decode_set_embed(self._h, _addr(embed), _addr(final_norm), dev))
+
+    def sync_kv_from_cpu(self, layer: int, k, v, seq_len: int) -> None:
+        check(lib().rt_decode_sync_kv(self._h, layer, _addr(k), _addr(v), seq_len, self._on_device(k)))
+
+    def decode_step(self, token: int, position: int):
+        import numpy as np
+        out = np.empty(self.cfg["vocab"], np.float32)
+        check(lib().rt_decode_step(self._h, token, position, out.ctypes.data))
+        return out
+
+    def decode_step_async(self, token: int, position: int) -> None:
+        check(lib().rt_decode_step_async(self._h, token, position))
+
+    def synchronize(self) -> None:
+        check(lib().rt_decode_synchronize(self._h))
+
+    def set_graph(self, enabled: bool) -> None:
+        check(lib().rt_decode_set_graph(self._h, int(enabled)))
+
+    def logits_ptr(self) -> int:
+        p = C.c_void_p()
+        check(lib().rt_decode_logits(self._h, C.byref(p)))
+        return p.value
+
+    def kv_ptrs(self, layer: int) -> tuple[int, int]:
+        k, v = C.c_void_p(), C.c_void_p()
+        check(lib().rt_decode_kv(self._h, layer, C.byref(k), C.byref(v)))
+        return k.value, v.value
+
+    def stream_ptr(self) -> int:
+        s = C.c_void_p()
+        check(lib().rt_decode_get_stream(self._h, C.byref(s)))
+        return s.value

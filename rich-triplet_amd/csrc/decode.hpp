@@ -1,0 +1,45 @@
+// decode.hpp -- shared declarations of the Gemma-3 decode engine (device
+// kernel arguments and the host-side encoder).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rt {
+
+// Keys per attention chunk are bounded so the chunk scores fit in LDS; the
+// host sizes the chunk count from max_seq accordingly.
+constexpr int kAttnMaxChunk = 256;
+
+struct DecodeShape {
+  int hidden, ffn, n_q_heads, n_kv_heads, head_dim, n_layers, vocab;
+  int nchunk_local, nchunk_global;
+};
+
+// Per-layer device pointers and constants (all device memory).
+struct LayerArgs {
+  const uint8_t *wq, *wk, *wv, *wo, *wgate, *wup, *wdown;  // Q4_K, rows=out
+  const float *g_in, *g_post_attn, *g_pre_ffn, *g_post_ffn, *g_q, *g_k;
+  float *kc, *vc;          // [max_seq, n_kv_heads*head_dim] f32
+  const float *rope_den;   // [head_dim/2] theta^(2i/d), from the host's powf
+  float rope_fs;           // linear RoPE scaling (1 local, 1/8 global for 4B)
+  int window;              // sliding window in keys, 0 = global layer
+};
+
+// Step-wide device buffers and constants.
+struct DecodeArgs {
+  const int *params;       // {token, position}
+  const uint16_t *embed;   // [vocab, hidden] bf16, also the tied lm_head
+  const float *g_final;
+  float *hid, *x2, *q, *k, *v, *attn, *o, *h, *dn, *logits;
+  float *part_m, *part_l, *part_o;  // [n_q_heads, nchunk(, head_dim)]
+  unsigned *counters;               // [n_kv_heads], zero between launches
+  float embed_scale, eps, attn_scale;
+  int vocab, n_q_heads, n_kv_heads, head_dim;
+};
+
+bool decode_shape_supported(const DecodeShape &s, const char **why);
+bool decode_rows_divisible(const DecodeShape &s, const char **why);
+hipError_t enqueue_decode_step(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers, hipStream_t stream);
+
+}  // namespace rt

@@ -1,0 +1,400 @@
+// decode_engine.hip -- the Gemma-3 decode context behind rt_decode_* (the
+// MI355X counterpart of MetalDecodeContext, metal_decode.rs:754-829).
+//
+// Owns the device KV cache (f32, [max_seq, n_kv_heads*head_dim] per layer),
+// the activation buffers and, unless the caller binds its own device
+// pointers, the uploaded weights (Q4_K blocks copied verbatim).  A step is the
+// kernel sequence of enqueue_decode_step(), captured once into a hipGraph and
+// replayed; token id and position travel through a device buffer.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "../../include/rt_hip.h"
+#include "decode.hpp"
+#include "rt_capi_util.hpp"
+
+using namespace rt;
+
+struct rt_decode {
+  rt_gemma3_config cfg{};
+  DecodeShape shape{};
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::vector<void *> owned;             // every hipMalloc of this context
+  std::vector<LayerArgs> layers;
+  std::vector<char> layer_set;
+  std::vector<void *> owned_layer[64];  // per-layer uploads (replaced on re-set)
+  bool embed_set = false;
+  void *embed_owned = nullptr, *final_owned = nullptr;
+  DecodeArgs args{};
+  int *params_dev = nullptr;
+  int *params_host = nullptr;            // pinned
+  hipEvent_t params_copied = nullptr;
+  bool params_pending = false;
+  float *rope_den_local = nullptr, *rope_den_global = nullptr;
+  hipGraphExec_t exec = nullptr;
+  bool graph_enabled = true;
+  bool graph_dirty = true;
+};
+
+namespace {
+
+rt_status dalloc(rt_decode *d, size_t bytes, void **out) {
+  void *p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes);
+  if (e != hipSuccess) return hip_error(e, "rt_decode hipMalloc");
+  d->owned.push_back(p);
+  *out = p;
+  return RT_OK;
+}
+
+void dfree(rt_decode *d, void *p) {
+  if (!p) return;
+  for (auto &q : d->owned)
+    if (q == p) {
+      (void)hipFree(q);
+      q = nullptr;
+    }
+}
+
+size_t q4k_bytes(size_t rows, size_t cols) { return rows * (cols / 256) * 144; }
+
+void drop_graph(rt_decode *d) {
+  if (d->exec) (void)hipGraphExecDestroy(d->exec);
+  d->exec = nullptr;
+  d->graph_dirty = true;
+}
+
+bool is_global(const rt_gemma3_config &c, int layer) {
+  // Config4::is_global_layer (transformer4.rs:141-143): layer % 6 == 5 for Gemma 3.
+  return c.global_every > 0 && (layer % c.global_every) == c.global_every - 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
+  if (!cfg || !out) return set_error(RT_EINVAL, "rt_decode_create: null pointer");
+  *out = nullptr;
+  const rt_gemma3_config &c = *cfg;
+  if (c.n_layers <= 0 || c.n_layers > 64 || c.vocab <= 0 || c.max_seq <= 0 || c.max_seq > (1 << 22))
+    return set_error(RT_EINVAL, "rt_decode_create: n_layers (1..64), vocab and max_seq must be positive");
+  if (!(c.eps > 0.f) || c.global_every < 0 || c.sliding_window < 0)
+    return set_error(RT_EINVAL, "rt_decode_create: eps must be > 0, global_every and sliding_window >= 0");
+  DecodeShape s{};
+  s.hidden = c.hidden;
+  s.ffn = c.ffn;
+  s.n_q_heads = c.n_q_heads;
+  s.n_kv_heads = c.n_kv_heads;
+  s.head_dim = c.head_dim;
+  s.n_layers = c.n_layers;
+  s.vocab = c.vocab;
+  const char *why = "";
+  if (c.hidden <= 0 || c.ffn <= 0 || c.n_q_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0 ||
+      !decode_shape_supported(s, &why) || !decode_rows_divisible(s, &why))
+    return set_error(RT_EINVAL, "rt_decode_create: unsupported shape: %s", why);
+  const int window = c.sliding_window;
+  const int local_span = window > 0 ? std::min(window, c.max_seq) : c.max_seq;
+  s.nchunk_local = std::max(1, std::min(128, (local_span + 15) / 16));
+  s.nchunk_global = std::max(64, (c.max_seq + kAttnMaxChunk - 1) / kAttnMaxChunk);
+  if ((local_span + s.nchunk_local - 1) / s.nchunk_local > kAttnMaxChunk)
+    return set_error(RT_EINVAL, "rt_decode_create: sliding window too large for the attention chunking");
+
+  rt_decode *d = new rt_decode();
+  d->cfg = c;
+  d->shape = s;
+  hipError_t e = hipGetDevice(&d->device);
+  rt_status st = RT_OK;
+#define TRY(x)                  \
+  do {                          \
+    st = (x);                   \
+    if (st != RT_OK) goto fail; \
+  } while (0)
+#define TRYH(x, what)                          \
+  do {                                         \
+    e = (x);                                   \
+    if (e != hipSuccess) {                     \
+      st = hip_error(e, what);                 \
+      goto fail;                               \
+    }                                          \
+  } while (0)
+  {
+    TRYH(e, "hipGetDevice");
+    TRYH(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking), "hipStreamCreate");
+    TRYH(hipEventCreateWithFlags(&d->params_copied, hipEventDisableTiming), "hipEventCreate");
+    TRYH(hipHostMalloc((void **)&d->params_host, 4 * sizeof(int), hipHostMallocDefault), "hipHostMalloc");
+    const size_t H = c.hidden, F = c.ffn, D = c.head_dim;
+    const size_t QD = (size_t)c.n_q_heads * D, KVD = (size_t)c.n_kv_heads * D;
+    const int nch = std::max(s.nchunk_local, s.nchunk_global);
+    void *p;
+    TRY(dalloc(d, 64, &p)); d->params_dev = (int *)p;
+    TRYH(hipMemset(d->params_dev, 0, 64), "hipMemset");
+    DecodeArgs &a = d->args;
+    auto fbuf = [&](size_t n, float **dst) -> rt_status {
+      void *q = nullptr;
+      rt_status r = dalloc(d, std::max<size_t>(n, 4) * sizeof(float), &q);
+      if (r == RT_OK) {
+        *dst = (float *)q;
+        hipError_t z = hipMemset(q, 0, std::max<size_t>(n, 4) * sizeof(float));
+        if (z != hipSuccess) r = hip_error(z, "hipMemset");
+      }
+      return r;
+    };
+    TRY(fbuf(H, &a.hid)); TRY(fbuf(H, &a.x2)); TRY(fbuf(QD, &a.q)); TRY(fbuf(KVD, &a.k)); TRY(fbuf(KVD, &a.v));
+    TRY(fbuf(QD, &a.attn)); TRY(fbuf(H, &a.o)); TRY(fbuf(F, &a.h)); TRY(fbuf(H, &a.dn));
+    TRY(fbuf((size_t)c.vocab, &a.logits));
+    TRY(fbuf((size_t)c.n_q_heads * nch, &a.part_m)); TRY(fbuf((size_t)c.n_q_heads * nch, &a.part_l));
+    TRY(fbuf((size_t)c.n_q_heads * nch * D, &a.part_o));
+    TRY(dalloc(d, 64 * sizeof(unsigned), &p)); a.counters = (unsigned *)p;
+    TRYH(hipMemset(a.counters, 0, 64 * sizeof(unsigned)), "hipMemset");
+    a.params = d->params_dev;
+    a.embed_scale = std::sqrt((float)c.hidden);   // transformer4.rs:2092
+    a.eps = c.eps;
+    a.attn_scale = c.attn_scale;
+    a.vocab = c.vocab;
+    a.n_q_heads = c.n_q_heads;
+    a.n_kv_heads = c.n_kv_heads;
+    a.head_dim = c.head_dim;
+    // RoPE denominators theta^(2i/d), computed with the host libm exactly as
+    // apply_rope_at_offset does (transformer4.rs:2755).
+    std::vector<float> dl(D / 2), dg(D / 2);
+    for (size_t i = 0; i < D / 2; ++i) {
+      const float ex = 2.0f * (float)i / (float)D;
+      dl[i] = powf(c.rope_theta_local, ex);
+      dg[i] = powf(c.rope_theta_global, ex);
+    }
+    TRY(fbuf(D / 2, &d->rope_den_local)); TRY(fbuf(D / 2, &d->rope_den_global));
+    TRYH(hipMemcpy(d->rope_den_local, dl.data(), dl.size() * 4, hipMemcpyHostToDevice), "hipMemcpy");
+    TRYH(hipMemcpy(d->rope_den_global, dg.data(), dg.size() * 4, hipMemcpyHostToDevice), "hipMemcpy");
+    d->layers.resize(c.n_layers);
+    d->layer_set.assign(c.n_layers, 0);
+    for (int l = 0; l < c.n_layers; ++l) {
+      LayerArgs &L = d->layers[l];
+      std::memset(&L, 0, sizeof L);
+      TRY(fbuf((size_t)c.max_seq * KVD, &L.kc));
+      TRY(fbuf((size_t)c.max_seq * KVD, &L.vc));
+      const bool g = is_global(c, l);
+      L.rope_den = g ? d->rope_den_global : d->rope_den_local;
+      L.rope_fs = g ? c.rope_fs_global : c.rope_fs_local;
+      L.window = g ? 0 : c.sliding_window;
+    }
+  }
+#undef TRY
+#undef TRYH
+  *out = d;
+  return RT_OK;
+fail:
+  rt_decode_destroy(d);
+  return st;
+}
+
+rt_status rt_decode_destroy(rt_decode *d) {
+  if (!d) return RT_OK;
+  if (d->stream) (void)hipStreamSynchronize(d->stream);
+  drop_graph(d);
+  for (void *p : d->owned)
+    if (p) (void)hipFree(p);
+  if (d->params_host) (void)hipHostFree(d->params_host);
+  if (d->params_copied) (void)hipEventDestroy(d->params_copied);
+  if (d->stream) (void)hipStreamDestroy(d->stream);
+  delete d;
+  return RT_OK;
+}
+
+static rt_status bind_buf(rt_decode *d, const void *src, size_t bytes, int32_t device_ptrs, std::vector<void *> &owned,
+                      const void **dst, const char *what) {
+  if (!src) return set_error(RT_EINVAL, "rt_decode: %s is null", what);
+  if ((reinterpret_cast<uintptr_t>(src) & 15u) != 0 && device_ptrs)
+    return set_error(RT_EINVAL, "rt_decode: %s must be 16-byte aligned", what);
+  if (device_ptrs) {
+    *dst = src;
+    return RT_OK;
+  }
+  void *p = nullptr;
+  rt_status st = dalloc(d, bytes, &p);
+  if (st != RT_OK) return st;
+  hipError_t e = hipMemcpy(p, src, bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return hip_error(e, what);
+  owned.push_back(p);
+  *dst = p;
+  return RT_OK;
+}
+
+rt_status rt_decode_set_layer(rt_decode *d, int32_t layer, const rt_gemma3_layer *w, int32_t device_ptrs) {
+  if (!d || !w) return set_error(RT_EINVAL, "rt_decode_set_layer: null pointer");
+  const rt_gemma3_config &c = d->cfg;
+  if (layer < 0 || layer >= c.n_layers) return set_error(RT_EINVAL, "rt_decode_set_layer: layer %d out of range", layer);
+  (void)hipStreamSynchronize(d->stream);
+  for (void *p : d->owned_layer[layer]) dfree(d, p);
+  d->owned_layer[layer].clear();
+  const size_t H = c.hidden, F = c.ffn, D = c.head_dim;
+  const size_t QD = (size_t)c.n_q_heads * D, KVD = (size_t)c.n_kv_heads * D;
+  LayerArgs &L = d->layers[layer];
+  std::vector<void *> &own = d->owned_layer[layer];
+  const void *p;
+  rt_status st;
+#define B(field, src, bytes, cast)                                         \
+  st = bind_buf(d, src, bytes, device_ptrs, own, &p, #field);                  \
+  if (st != RT_OK) return st;                                              \
+  L.field = (cast)p;
+  B(wq, w->q, q4k_bytes(QD, H), const uint8_t *);
+  B(wk, w->k, q4k_bytes(KVD, H), const uint8_t *);
+  B(wv, w->v, q4k_bytes(KVD, H), const uint8_t *);
+  B(wo, w->o, q4k_bytes(H, QD), const uint8_t *);
+  B(wgate, w->gate, q4k_bytes(F, H), const uint8_t *);
+  B(wup, w->up, q4k_bytes(F, H), const uint8_t *);
+  B(wdown, w->down, q4k_bytes(H, F), const uint8_t *);
+  B(g_in, w->in_norm, H * 4, const float *);
+  B(g_post_attn, w->post_attn_norm, H * 4, const float *);
+  B(g_pre_ffn, w->pre_ffn_norm, H * 4, const float *);
+  B(g_post_ffn, w->post_ffn_norm, H * 4, const float *);
+  B(g_q, w->q_norm, D * 4, const float *);
+  B(g_k, w->k_norm, D * 4, const float *);
+#undef B
+  d->layer_set[layer] = 1;
+  drop_graph(d);
+  return RT_OK;
+}
+
+rt_status rt_decode_set_embed(rt_decode *d, const uint16_t *embed, const float *final_norm, int32_t device_ptrs) {
+  if (!d) return set_error(RT_EINVAL, "rt_decode_set_embed: null pointer");
+  (void)hipStreamSynchronize(d->stream);
+  std::vector<void *> own;
+  dfree(d, d->embed_owned);
+  dfree(d, d->final_owned);
+  d->embed_owned = d->final_owned = nullptr;
+  const void *p;
+  rt_status st = bind_buf(d, embed, (size_t)d->cfg.vocab * d->cfg.hidden * 2, device_ptrs, own, &p, "embed");
+  if (st != RT_OK) return st;
+  d->args.embed = (const uint16_t *)p;
+  if (!device_ptrs) d->embed_owned = (void *)p;
+  st = bind_buf(d, final_norm, (size_t)d->cfg.hidden * 4, device_ptrs, own, &p, "final_norm");
+  if (st != RT_OK) return st;
+  d->args.g_final = (const float *)p;
+  if (!device_ptrs) d->final_owned = (void *)p;
+  d->embed_set = true;
+  drop_graph(d);
+  return RT_OK;
+}
+
+// sync_kv_from_cpu (metal_decode.rs:1366-1396) for one layer: rows
+// [0, seq_len) of K and V, each [seq_len, n_kv_heads*head_dim] f32.
+rt_status rt_decode_sync_kv(rt_decode *d, int32_t layer, const float *k, const float *v, int32_t seq_len,
+                            int32_t device_ptrs) {
+  if (!d || !k || !v) return set_error(RT_EINVAL, "rt_decode_sync_kv: null pointer");
+  if (layer < 0 || layer >= d->cfg.n_layers) return set_error(RT_EINVAL, "rt_decode_sync_kv: layer %d out of range", layer);
+  if (seq_len < 0 || seq_len > d->cfg.max_seq)
+    return set_error(RT_EINVAL, "rt_decode_sync_kv: seq_len %d outside [0, max_seq=%d]", seq_len, d->cfg.max_seq);
+  const size_t bytes = (size_t)seq_len * d->cfg.n_kv_heads * d->cfg.head_dim * 4;
+  const hipMemcpyKind kind = device_ptrs ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+  hipError_t e = hipMemcpyAsync(d->layers[layer].kc, k, bytes, kind, d->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(d->layers[layer].vc, v, bytes, kind, d->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
+  return hip_error(e, "rt_decode_sync_kv");
+}
+
+static rt_status check_ready(rt_decode *d, int32_t token, int32_t position) {
+  if (!d) return set_error(RT_EINVAL, "rt_decode_step: null context");
+  if (!d->embed_set) return set_error(RT_ESTATE, "rt_decode_step: embedding not set");
+  for (int l = 0; l < d->cfg.n_layers; ++l)
+    if (!d->layer_set[l]) return set_error(RT_ESTATE, "rt_decode_step: layer %d weights not set", l);
+  if (token < 0 || token >= d->cfg.vocab)
+    return set_error(RT_EINVAL, "rt_decode_step: token %d outside [0, vocab=%d)", token, d->cfg.vocab);
+  if (position < 0 || position >= d->cfg.max_seq)
+    return set_error(RT_EINVAL, "rt_decode_step: position %d outside [0, max_seq=%d)", position, d->cfg.max_seq);
+  return RT_OK;
+}
+
+rt_status rt_decode_step_async(rt_decode *d, int32_t token, int32_t position) {
+  rt_status st = check_ready(d, token, position);
+  if (st != RT_OK) return st;
+  hipError_t e = hipSuccess;
+  if (d->params_pending) {
+    e = hipEventSynchronize(d->params_copied);  // the previous copy has left the pinned buffer
+    if (e != hipSuccess) return hip_error(e, "rt_decode_step");
+  }
+  d->params_host[0] = token;
+  d->params_host[1] = position;
+  e = hipMemcpyAsync(d->params_dev, d->params_host, 2 * sizeof(int), hipMemcpyHostToDevice, d->stream);
+  if (e == hipSuccess) e = hipEventRecord(d->params_copied, d->stream);
+  if (e != hipSuccess) return hip_error(e, "rt_decode_step params");
+  d->params_pending = true;
+  if (!d->graph_enabled) return hip_error(enqueue_decode_step(d->shape, d->args, d->layers.data(), d->stream), "rt_decode_step");
+  if (d->graph_dirty || !d->exec) {
+    drop_graph(d);
+    hipGraph_t g = nullptr;
+    e = hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return hip_error(e, "hipStreamBeginCapture");
+    hipError_t le = enqueue_decode_step(d->shape, d->args, d->layers.data(), d->stream);
+    e = hipStreamEndCapture(d->stream, &g);
+    if (le != hipSuccess) {
+      if (g) (void)hipGraphDestroy(g);
+      return hip_error(le, "rt_decode_step capture");
+    }
+    if (e != hipSuccess) return hip_error(e, "hipStreamEndCapture");
+    e = hipGraphInstantiate(&d->exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) {
+      d->exec = nullptr;
+      return hip_error(e, "hipGraphInstantiate");
+    }
+    d->graph_dirty = false;
+  }
+  return hip_error(hipGraphLaunch(d->exec, d->stream), "hipGraphLaunch");
+}
+
+rt_status rt_decode_step(rt_decode *d, int32_t token, int32_t position, float *logits_host) {
+  rt_status st = rt_decode_step_async(d, token, position);
+  if (st != RT_OK) return st;
+  hipError_t e = hipSuccess;
+  if (logits_host)
+    e = hipMemcpyAsync(logits_host, d->args.logits, (size_t)d->cfg.vocab * 4, hipMemcpyDeviceToHost, d->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
+  return hip_error(e, "rt_decode_step");
+}
+
+rt_status rt_decode_synchronize(rt_decode *d) {
+  if (!d) return set_error(RT_EINVAL, "rt_decode_synchronize: null context");
+  return hip_error(hipStreamSynchronize(d->stream), "rt_decode_synchronize");
+}
+
+rt_status rt_decode_set_graph(rt_decode *d, int32_t enabled) {
+  if (!d) return set_error(RT_EINVAL, "rt_decode_set_graph: null context");
+  (void)hipStreamSynchronize(d->stream);
+  d->graph_enabled = enabled != 0;
+  drop_graph(d);
+  return RT_OK;
+}
+
+rt_status rt_decode_logits(rt_decode *d, float **logits_dev) {
+  if (!d || !logits_dev) return set_error(RT_EINVAL, "rt_decode_logits: null pointer");
+  *logits_dev = d->args.logits;
+  return RT_OK;
+}
+
+rt_status rt_decode_kv(rt_decode *d, int32_t layer, float **k_dev, float **v_dev) {
+  if (!d || !k_dev || !v_dev) return set_error(RT_EINVAL, "rt_decode_kv: null pointer");
+  if (layer < 0 || layer >= d->cfg.n_layers) return set_error(RT_EINVAL, "rt_decode_kv: layer %d out of range", layer);
+  *k_dev = d->layers[layer].kc;
+  *v_dev = d->layers[layer].vc;
+  return RT_OK;
+}
+
+rt_status rt_decode_hidden(rt_decode *d, float **x2_dev, float **dn_dev) {
+  if (!d || !x2_dev || !dn_dev) return set_error(RT_EINVAL, "rt_decode_hidden: null pointer");
+  *x2_dev = d->args.x2;
+  *dn_dev = d->args.dn;
+  return RT_OK;
+}
+
+rt_status rt_decode_get_stream(rt_decode *d, void **stream) {
+  if (!d || !stream) return set_error(RT_EINVAL, "rt_decode_get_stream: null pointer");
+  *stream = d->stream;
+  return RT_OK;
+}
+
+}  // extern "C"

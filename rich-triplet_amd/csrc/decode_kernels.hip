@@ -1,0 +1,573 @@
+// decode_kernels.hip -- the fused kernels of one Gemma-3 decode step.
+//
+// Per layer five launches replace the reference's 21 dispatches
+// (metal_decode.rs:1930-2024):
+//   k_qkv      residual+post-FFN norm of the previous layer (or the embedding
+//              row for layer 0), input RMSNorm, then one GEMV over the stacked
+//              q|k|v rows;
+//   k_attn     q/k per-head RMSNorm + NeoX RoPE, K/V append at `pos`, split-K
+//              attention over the f32 cache with an in-kernel combine by the
+//              last workgroup of each KV head;
+//   k_gemv     o projection;
+//   k_gateup   residual + post-attention norm, pre-FFN norm, gate and up
+//              GEMVs of the same rows, gelu_tanh(gate)*up epilogue;
+//   k_gemv     down projection.
+// After the last layer k_lmhead applies the final residual, the final norm
+// and the BF16 lm_head GEMV.  Token id and position are read from device
+// memory so the whole step replays as one hipGraph.
+#include "decode.hpp"
+#include "q4k_gemv.hpp"
+#include "rt_device.hpp"
+
+namespace rt {
+
+// ---------------------------------------------------------------------------
+// Prologues: build the normalised activation vector in the LDS x layout.
+// Arithmetic order follows rms_norm_gemma3 (autograd2.rs:3477-3496):
+//   rinv = 1/sqrt(sum(x^2) * (1/K) + eps);  out = (x * rinv) * (1 + gamma)
+// ---------------------------------------------------------------------------
+RT_DEV float rms_inv_from_sumsq(float ss, float inv_k, float eps) {
+#pragma clang fp contract(off)
+  return 1.0f / sqrtf(ss * inv_k + eps);
+}
+
+RT_DEV float4 norm4(float4 x, float rinv, float4 g) {
+#pragma clang fp contract(off)
+  return make_float4((x.x * rinv) * (1.0f + g.x), (x.y * rinv) * (1.0f + g.y), (x.z * rinv) * (1.0f + g.z),
+                     (x.w * rinv) * (1.0f + g.w));
+}
+
+RT_DEV float4 add4(float4 a, float4 b) {
+#pragma clang fp contract(off)
+  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
+RT_DEV float mul_nc(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+
+RT_DEV float sumsq4(float4 v) { return v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w; }
+
+enum class Pro { Embed, Resid };
+
+// x = Embed: bf16(E[token]) * embed_scale        (transformer4.rs:2360-2368)
+//     Resid: base + rms(add)*(1+g_add)           (post-norm residual, 1954-1964)
+// then xn = rms(x)*(1+g_out) into LDS; workgroup 0 stores x to x_out.
+template <int K, int T, Pro MODE>
+RT_DEV void prologue(const DecodeArgs &a, const float *__restrict__ base, const float *__restrict__ add,
+                     const float *__restrict__ g_add, const float *__restrict__ g_out, float *__restrict__ x_out,
+                     float *xl, float *red) {
+  constexpr int F4 = K / 4;
+  constexpr int PER = (F4 + T - 1) / T;
+  const float inv_k = 1.0f / (float)K;
+  float4 x[PER];
+  if constexpr (MODE == Pro::Embed) {
+    const int token = a.params[0];
+    const uint2 *row = reinterpret_cast<const uint2 *>(a.embed + (size_t)token * K);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int f = threadIdx.x + i * T;
+      if (f < F4) {
+        const uint2 w = row[f];
+        x[i] = make_float4(mul_nc(bf16_lo(w.x), a.embed_scale), mul_nc(bf16_hi(w.x), a.embed_scale),
+                           mul_nc(bf16_lo(w.y), a.embed_scale), mul_nc(bf16_hi(w.y), a.embed_scale));
+      } else {
+        x[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+  } else {
+    float4 ad[PER];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int f = threadIdx.x + i * T;
+      ad[i] = f < F4 ? reinterpret_cast<const float4 *>(add)[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+      ss += sumsq4(ad[i]);
+    }
+    const float ra = rms_inv_from_sumsq(block_sum<T>(ss, red), inv_k, a.eps);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int f = threadIdx.x + i * T;
+      if (f < F4) {
+        const float4 b = reinterpret_cast<const float4 *>(base)[f];
+        const float4 g = reinterpret_cast<const float4 *>(g_add)[f];
+        x[i] = add4(b, norm4(ad[i], ra, g));
+      } else {
+        x[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) ss += sumsq4(x[i]);
+  const float rx = rms_inv_from_sumsq(block_sum<T>(ss, red), inv_k, a.eps);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int f = threadIdx.x + i * T;
+    if (f < F4) {
+      if (x_out && blockIdx.x == 0) reinterpret_cast<float4 *>(x_out)[f] = x[i];
+      const float4 g = reinterpret_cast<const float4 *>(g_out)[f];
+      *reinterpret_cast<float4 *>(xl + xlds_index(4 * f)) = norm4(x[i], rx, g);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// k_qkv: [prologue] + GEMV over q|k|v rows (each workgroup inside one matrix).
+// ---------------------------------------------------------------------------
+template <int NB, int T, int ITERS, Pro MODE>
+__global__ __launch_bounds__(T) void k_qkv(DecodeArgs a, LayerArgs L, LayerArgs prev) {
+  using Tile = Q4KTile<NB, T, ITERS>;
+  constexpr int K = NB * 256;
+  __shared__ __attribute__((aligned(16))) float xl[NB * 4 * kXPitch];
+  __shared__ float red[Tile::ROWS * NB];
+  __shared__ float bred[T / 64];
+  const int qd = a.n_q_heads * a.head_dim, kvd = a.n_kv_heads * a.head_dim;
+  const int row0 = (int)blockIdx.x * Tile::ROWS;  // ROWS divides qd and kvd (checked on the host)
+  const uint8_t *W;
+  float *y;
+  int r0;
+  if (row0 < qd) {
+    W = L.wq, y = a.q, r0 = row0;
+  } else if (row0 < qd + kvd) {
+    W = L.wk, y = a.k, r0 = row0 - qd;
+  } else {
+    W = L.wv, y = a.v, r0 = row0 - qd - kvd;
+  }
+  const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
+  Tile tile;
+  tile.load([&](int rl) -> const uint8_t * { return W + (size_t)(r0 + rl) * row_bytes; });
+  if constexpr (MODE == Pro::Embed)
+    prologue<K, T, Pro::Embed>(a, nullptr, nullptr, nullptr, L.g_in, a.hid, xl, bred);
+  else
+    prologue<K, T, Pro::Resid>(a, a.x2, a.dn, prev.g_post_ffn, L.g_in, a.hid, xl, bred);
+  __syncthreads();
+  ChunkX cx;
+  chunkx_from_lds(xl, tile.slot, cx);
+  tile.compute(cx, red);
+  __syncthreads();
+  for (int i = threadIdx.x; i < Tile::ROWS; i += T) y[r0 + i] = reduce_row<NB>(red, i);
+}
+
+// ---------------------------------------------------------------------------
+// k_gateup: x2 = hid + rms(o)(1+g_pa); n2 = rms(x2)(1+g_pf); gate & up rows
+// j0..j0+ROWS; h[j] = gelu_tanh(gate[j]) * up[j]   (transformer4.rs:328-334)
+// ---------------------------------------------------------------------------
+template <int NB, int T, int ITERS>
+__global__ __launch_bounds__(T) void k_gateup(DecodeArgs a, LayerArgs L) {
+  using Tile = Q4KTile<NB, T, 2 * ITERS>;
+  constexpr int K = NB * 256;
+  constexpr int ROWS = Tile::ROWS / 2;
+  __shared__ __attribute__((aligned(16))) float xl[NB * 4 * kXPitch];
+  __shared__ float red[Tile::ROWS * NB];
+  __shared__ float bred[T / 64];
+  const int j0 = (int)blockIdx.x * ROWS;
+  const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
+  Tile tile;
+  tile.load([&](int rl) -> const uint8_t * {
+    return rl < ROWS ? L.wgate + (size_t)(j0 + rl) * row_bytes : L.wup + (size_t)(j0 + rl - ROWS) * row_bytes;
+  });
+  prologue<K, T, Pro::Resid>(a, a.hid, a.o, L.g_post_attn, L.g_pre_ffn, a.x2, xl, bred);
+  __syncthreads();
+  ChunkX cx;
+  chunkx_from_lds(xl, tile.slot, cx);
+  tile.compute(cx, red);
+  __syncthreads();
+  for (int i = threadIdx.x; i < ROWS; i += T) {
+    const float g = reduce_row<NB>(red, i);
+    const float u = reduce_row<NB>(red, ROWS + i);
+    a.h[j0 + i] = mul_nc(gelu_tanh(g), u);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// k_gemv: plain GEMV with the activation vector read from global memory.
+// ---------------------------------------------------------------------------
+template <int NB, int T, int ITERS>
+__global__ __launch_bounds__(T) void k_gemv(const uint8_t *__restrict__ W, const float *__restrict__ x,
+                                            float *__restrict__ y) {
+  using Tile = Q4KTile<NB, T, ITERS>;
+  __shared__ __attribute__((aligned(16))) float xl[NB * 4 * kXPitch];
+  __shared__ float red[Tile::ROWS * NB];
+  const int row0 = (int)blockIdx.x * Tile::ROWS;  // ROWS divides N (checked on the host)
+  const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
+  Tile tile;
+  tile.load([&](int rl) -> const uint8_t * { return W + (size_t)(row0 + rl) * row_bytes; });
+  stage_x_plain<NB * 256, T>(x, xl);
+  __syncthreads();
+  ChunkX cx;
+  chunkx_from_lds(xl, tile.slot, cx);
+  tile.compute(cx, red);
+  __syncthreads();
+  for (int i = threadIdx.x; i < Tile::ROWS; i += T) y[row0 + i] = reduce_row<NB>(red, i);
+}
+
+// ---------------------------------------------------------------------------
+// k_attn: per (key chunk, KV head) workgroup of 256 threads.
+//   1. q heads of this KV group: per-head RMSNorm (gamma shared, 2485-2508)
+//      and NeoX RoPE, angle = (pos*fs)/den[i] with den[i] = theta^(2i/D)
+//      tabulated on the host (2742-2772); the chunk holding `pos` also
+//      rotates k, and writes k and v into the cache row `pos` (1813-1823).
+//   2. scores s_c = (q.k_c)*scale for keys in the chunk (16 lanes per key)
+//   3. chunk-local softmax statistics m = max s, l = sum exp(s - m)
+//   4. o = sum_c exp(s_c - m) v_c (one thread per dimension)
+//   5. partials (m, l, o) to global; the last workgroup of the KV head
+//      merges all chunks: out = sum_i o_i e^(m_i-M) / sum_i l_i e^(m_i-M).
+// The result equals gqa_attention_cached's t_q == 1 branch (2806-2879).
+// ---------------------------------------------------------------------------
+template <int D>
+RT_DEV void norm_rope_head(const float *__restrict__ src, const float *__restrict__ gamma,
+                           const float *__restrict__ den, float pos_fs, float eps, float *dst) {
+  // One wave; lane owns pairs i = lane*P + p (p < P) with partners i + D/2.
+  constexpr int P = D / 128;
+  const int lane = threadIdx.x & 63;
+  float x0[P], x1[P];
+  float ss = 0.f;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int i = lane * P + p;
+    x0[p] = src[i];
+    x1[p] = src[i + D / 2];
+    ss += x0[p] * x0[p] + x1[p] * x1[p];
+  }
+  const float rinv = rms_inv_from_sumsq(wave_sum(ss), 1.0f / (float)D, eps);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+#pragma clang fp contract(off)
+    const int i = lane * P + p;
+    const float a0 = (x0[p] * rinv) * (1.0f + gamma[i]);
+    const float a1 = (x1[p] * rinv) * (1.0f + gamma[i + D / 2]);
+    const float ang = pos_fs / den[i];
+    float sn, cs;
+    sincosf(ang, &sn, &cs);
+    dst[i] = a0 * cs - a1 * sn;
+    dst[i + D / 2] = a0 * sn + a1 * cs;
+  }
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(256) void k_attn(DecodeArgs a, LayerArgs L) {
+  constexpr int MAXC = kAttnMaxChunk;
+  __shared__ float qs[G][D];
+  __shared__ float knew[D], vnew[D];
+  __shared__ float sc[G][MAXC];
+  __shared__ float stat[G][2];
+  __shared__ int last_flag;
+  const int kvh = blockIdx.y, chunk = blockIdx.x, nchunk = gridDim.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int pos = a.params[1];
+  const int t_end = pos + 1;
+  const int t_start = L.window > 0 ? max(0, t_end - L.window) : 0;
+  const int t_kv = t_end - t_start;
+  const int csize = (t_kv + nchunk - 1) / nchunk;  // <= MAXC (host sizes the grid)
+  const int c0 = t_start + chunk * csize;
+  const int c1 = min(c0 + csize, t_end);
+  const int n = max(0, c1 - c0);
+  const bool has_new = c0 <= pos && pos < c1;
+  const int kvd = a.n_kv_heads * D;
+  const float pos_fs = (float)pos * L.rope_fs;
+
+  // 1. rotations (waves 0..G-1: q heads; the next wave: k, and v copy)
+  if (wave < G) {
+    norm_rope_head<D>(a.q + (size_t)(kvh * G + wave) * D, L.g_q, L.rope_den, pos_fs, a.eps, qs[wave]);
+  }
+  if (has_new && wave == (G % 4)) {  // for G == 4 wave 0 rotates k after its q head
+    norm_rope_head<D>(a.k + (size_t)kvh * D, L.g_k, L.rope_den, pos_fs, a.eps, knew);
+    for (int i = lane; i < D; i += 64) vnew[i] = a.v[(size_t)kvh * D + i];
+  }
+  __syncthreads();
+  if (has_new && threadIdx.x < D) {
+    L.kc[(size_t)pos * kvd + (size_t)kvh * D + threadIdx.x] = knew[threadIdx.x];
+    L.vc[(size_t)pos * kvd + (size_t)kvh * D + threadIdx.x] = vnew[threadIdx.x];
+  }
+
+  // 2. scores: a wave takes 4 keys per step, 16 lanes per key, D/16 dims per lane
+  constexpr int DL = D / 16;
+  const int kg = lane >> 4, sub = lane & 15;
+  float qreg[G][DL];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < DL; ++j) qreg[g][j] = qs[g][sub * DL + j];
+  for (int base = 0; base < n; base += 16) {
+    const int ci = base + wave * 4 + kg;  // key index within chunk
+    const int c = c0 + ci;
+    const bool ok = ci < n;
+    float kv[DL];
+    if (ok && c == pos) {
+#pragma unroll
+      for (int j = 0; j < DL; ++j) kv[j] = knew[sub * DL + j];
+    } else if (ok) {
+      const float4 *kp = reinterpret_cast<const float4 *>(L.kc + (size_t)c * kvd + (size_t)kvh * D + sub * DL);
+#pragma unroll
+      for (int j = 0; j < DL / 4; ++j) {
+        const float4 v4 = kp[j];
+        kv[4 * j] = v4.x; kv[4 * j + 1] = v4.y; kv[4 * j + 2] = v4.z; kv[4 * j + 3] = v4.w;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < DL; ++j) kv[j] = 0.f;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float d = 0.f;
+#pragma unroll
+      for (int j = 0; j < DL; ++j) d += qreg[g][j] * kv[j];
+      d = row16_sum(d);
+      if (ok && sub == 0) sc[g][ci] = d * a.attn_scale;
+    }
+  }
+  __syncthreads();
+
+  // 3. chunk softmax statistics (wave g handles head g)
+  if (wave < G) {
+    float m = -INFINITY;
+    for (int i = lane; i < n; i += 64) m = fmaxf(m, sc[wave][i]);
+    m = wave_max(m);
+    float l = 0.f;
+    for (int i = lane; i < n; i += 64) {
+      const float p = expf(sc[wave][i] - m);
+      sc[wave][i] = p;
+      l += p;
+    }
+    l = wave_sum(l);
+    if (lane == 0) {
+      stat[wave][0] = m;
+      stat[wave][1] = l;
+    }
+  }
+  __syncthreads();
+
+  // 4. weighted V (thread per dimension)
+  for (int d = threadIdx.x; d < D; d += 256) {
+    float o[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) o[g] = 0.f;
+    const float *vp = L.vc + (size_t)kvh * D + d;
+    int i = 0;
+    for (; i + 4 <= n; i += 4) {
+      float v4[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int c = c0 + i + u;
+        v4[u] = c == pos ? vnew[d] : vp[(size_t)c * kvd];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int g = 0; g < G; ++g) o[g] += sc[g][i + u] * v4[u];
+    }
+    for (; i < n; ++i) {
+      const int c = c0 + i;
+      const float vv = c == pos ? vnew[d] : vp[(size_t)c * kvd];
+#pragma unroll
+      for (int g = 0; g < G; ++g) o[g] += sc[g][i] * vv;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int h = kvh * G + g;
+      a.part_o[((size_t)h * nchunk + chunk) * D + d] = o[g];
+    }
+  }
+  if (threadIdx.x < G) {
+    const int h = kvh * G + threadIdx.x;
+    a.part_m[(size_t)h * nchunk + chunk] = n > 0 ? stat[threadIdx.x][0] : -INFINITY;
+    a.part_l[(size_t)h * nchunk + chunk] = n > 0 ? stat[threadIdx.x][1] : 0.f;
+  }
+
+  // 5. the last workgroup of this KV head merges the chunks
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned prev = atomicAdd(&a.counters[kvh], 1u);
+    last_flag = prev == (unsigned)(nchunk - 1);
+  }
+  __syncthreads();
+  if (!last_flag) return;
+  __threadfence();
+  for (int d = threadIdx.x; d < D; d += 256) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int h = kvh * G + g;
+      const float *pm = a.part_m + (size_t)h * nchunk;
+      const float *pl = a.part_l + (size_t)h * nchunk;
+      float M = -INFINITY;
+      for (int i = 0; i < nchunk; ++i) M = fmaxf(M, pm[i]);
+      float Ls = 0.f, acc = 0.f;
+      for (int i = 0; i < nchunk; ++i) {
+        const float mi = pm[i];
+        const float w = mi == -INFINITY ? 0.f : expf(mi - M);
+        Ls += pl[i] * w;
+        acc += a.part_o[((size_t)h * nchunk + i) * D + d] * w;
+      }
+      a.attn[(size_t)h * D + d] = acc / Ls;
+    }
+  }
+  if (threadIdx.x == 0) a.counters[kvh] = 0u;
+}
+
+// ---------------------------------------------------------------------------
+// k_lmhead: x = x2 + rms(dn)(1+g_post_ffn_last); xn = rms(x)(1+g_final);
+// logits = E(bf16, tied embedding) . xn          (transformer4.rs:2380-2385)
+// ---------------------------------------------------------------------------
+template <int CPL>
+__global__ __launch_bounds__(256) void k_lmhead(DecodeArgs a, LayerArgs last) {
+  constexpr int K = CPL * 512;
+  constexpr int U = 2;
+  __shared__ __attribute__((aligned(16))) float xl[K / 64 * kXPitch];
+  __shared__ float bred[4];
+  prologue<K, 256, Pro::Resid>(a, a.x2, a.dn, last.g_post_ffn, a.g_final, nullptr, xl, bred);
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  float xr[CPL][8];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xr[i][j] = xl[xlds_index((i * 64 + lane) * 8 + j)];
+  const int wave = (int)((blockIdx.x * 256u + threadIdx.x) >> 6);
+  const int nwaves = (int)(gridDim.x * 4u);
+  const int N = a.vocab;
+  for (int r0 = wave * U; r0 < N; r0 += nwaves * U) {
+    uint4 wv[U][CPL];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int r = min(r0 + u, N - 1);
+      const uint4 *rp = reinterpret_cast<const uint4 *>(a.embed + (size_t)r * K);
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) wv[u][i] = rp[i * 64 + lane];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const uint4 w = wv[u][i];
+        acc0 += bf16_lo(w.x) * xr[i][0];
+        acc1 += bf16_hi(w.x) * xr[i][1];
+        acc0 += bf16_lo(w.y) * xr[i][2];
+        acc1 += bf16_hi(w.y) * xr[i][3];
+        acc0 += bf16_lo(w.z) * xr[i][4];
+        acc1 += bf16_hi(w.z) * xr[i][5];
+        acc0 += bf16_lo(w.w) * xr[i][6];
+        acc1 += bf16_hi(w.w) * xr[i][7];
+      }
+      const float acc = wave_sum(acc0 + acc1);
+      if (lane == 0 && r0 + u < N) a.logits[r0 + u] = acc;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host-side step encoder
+// ---------------------------------------------------------------------------
+template <int NB, int T>
+static constexpr int rows_per_iter() { return T / (NB * 4); }
+
+struct Launch {
+  hipStream_t s;
+  hipError_t err = hipSuccess;
+  void check() {
+    if (err == hipSuccess) err = hipGetLastError();
+  }
+};
+
+template <int NB, int T, int ITERS>
+static void launch_qkv(Launch &l, const DecodeArgs &a, const LayerArgs &L, const LayerArgs &prev, bool first,
+                       int rows_total) {
+  constexpr int ROWS = Q4KTile<NB, T, ITERS>::ROWS;
+  const dim3 grid(rows_total / ROWS);
+  if (first)
+    hipLaunchKernelGGL((k_qkv<NB, T, ITERS, Pro::Embed>), grid, dim3(T), 0, l.s, a, L, prev);
+  else
+    hipLaunchKernelGGL((k_qkv<NB, T, ITERS, Pro::Resid>), grid, dim3(T), 0, l.s, a, L, prev);
+  l.check();
+}
+
+template <int NB, int T, int ITERS>
+static void launch_gateup(Launch &l, const DecodeArgs &a, const LayerArgs &L, int ffn) {
+  constexpr int ROWS = Q4KTile<NB, T, ITERS>::ROWS;
+  hipLaunchKernelGGL((k_gateup<NB, T, ITERS>), dim3(ffn / ROWS), dim3(T), 0, l.s, a, L);
+  l.check();
+}
+
+template <int NB, int T, int ITERS>
+static void launch_gemv(Launch &l, const uint8_t *W, const float *x, float *y, int n) {
+  constexpr int ROWS = Q4KTile<NB, T, ITERS>::ROWS;
+  hipLaunchKernelGGL((k_gemv<NB, T, ITERS>), dim3(n / ROWS), dim3(T), 0, l.s, W, x, y);
+  l.check();
+}
+
+// Shape dispatch.  Supported K's (in super-blocks): hidden 2 | 10, q*d 2 | 8,
+// ffn 4 | 40; head_dim 128 | 256; group 1 | 2 | 4.  The host validates these
+// and the divisibility of every row count before creating an engine.
+bool decode_shape_supported(const DecodeShape &s, const char **why) {
+  auto nb = [](int k) { return k / 256; };
+  if (s.hidden % 512 != 0 || (nb(s.hidden) != 2 && nb(s.hidden) != 10)) return *why = "hidden must be 512 or 2560", false;
+  const int qd = s.n_q_heads * s.head_dim, kvd = s.n_kv_heads * s.head_dim;
+  if (qd % 256 != 0 || (nb(qd) != 2 && nb(qd) != 8)) return *why = "n_q_heads*head_dim must be 512 or 2048", false;
+  if (s.ffn % 256 != 0 || (nb(s.ffn) != 4 && nb(s.ffn) != 40)) return *why = "ffn must be 1024 or 10240", false;
+  if (s.head_dim != 128 && s.head_dim != 256) return *why = "head_dim must be 128 or 256", false;
+  if (s.n_kv_heads <= 0 || s.n_q_heads % s.n_kv_heads != 0) return *why = "n_q_heads must be a multiple of n_kv_heads", false;
+  const int g = s.n_q_heads / s.n_kv_heads;
+  if (g != 1 && g != 2 && g != 4) return *why = "GQA group must be 1, 2 or 4", false;
+  if (qd % 16 != 0 || kvd % 16 != 0) return *why = "q/kv widths must be multiples of 16", false;
+  return true;
+}
+
+template <int D>
+static void launch_attn_d(Launch &l, const DecodeArgs &a, const LayerArgs &L, int nchunk, int group) {
+  const dim3 grid(nchunk, a.n_kv_heads);
+  switch (group) {
+    case 1: hipLaunchKernelGGL((k_attn<D, 1>), grid, dim3(256), 0, l.s, a, L); break;
+    case 2: hipLaunchKernelGGL((k_attn<D, 2>), grid, dim3(256), 0, l.s, a, L); break;
+    default: hipLaunchKernelGGL((k_attn<D, 4>), grid, dim3(256), 0, l.s, a, L); break;
+  }
+  l.check();
+}
+
+hipError_t enqueue_decode_step(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers, hipStream_t stream) {
+  Launch l{stream};
+  const int qd = s.n_q_heads * s.head_dim, kvd = s.n_kv_heads * s.head_dim;
+  const int group = s.n_q_heads / s.n_kv_heads;
+  const bool big = s.hidden == 2560;
+  for (int li = 0; li < s.n_layers && l.err == hipSuccess; ++li) {
+    const LayerArgs &L = layers[li];
+    const LayerArgs &P = layers[li > 0 ? li - 1 : 0];
+    const int qkv_rows = qd + 2 * kvd;
+    if (big) launch_qkv<10, 320, 1>(l, a, L, P, li == 0, qkv_rows);
+    else launch_qkv<2, 256, 1>(l, a, L, P, li == 0, qkv_rows);
+    const int nchunk = L.window > 0 ? s.nchunk_local : s.nchunk_global;
+    if (s.head_dim == 256) launch_attn_d<256>(l, a, L, nchunk, group);
+    else launch_attn_d<128>(l, a, L, nchunk, group);
+    if (qd == 2048) launch_gemv<8, 256, 1>(l, L.wo, a.attn, a.o, s.hidden);
+    else launch_gemv<2, 256, 1>(l, L.wo, a.attn, a.o, s.hidden);
+    if (big) launch_gateup<10, 320, 1>(l, a, L, s.ffn);
+    else launch_gateup<2, 256, 1>(l, a, L, s.ffn);
+    if (s.ffn == 10240) launch_gemv<40, 320, 4>(l, L.wdown, a.h, a.dn, s.hidden);
+    else launch_gemv<4, 256, 1>(l, L.wdown, a.h, a.dn, s.hidden);
+  }
+  if (l.err == hipSuccess) {
+    const dim3 grid(1024);
+    if (big) hipLaunchKernelGGL((k_lmhead<5>), grid, dim3(256), 0, l.s, a, layers[s.n_layers - 1]);
+    else hipLaunchKernelGGL((k_lmhead<1>), grid, dim3(256), 0, l.s, a, layers[s.n_layers - 1]);
+    l.check();
+  }
+  return l.err;
+}
+
+// Row-count divisibility the launches above rely on.
+bool decode_rows_divisible(const DecodeShape &s, const char **why) {
+  const int qd = s.n_q_heads * s.head_dim, kvd = s.n_kv_heads * s.head_dim;
+  const bool big = s.hidden == 2560;
+  const int qkv_rows_per_wg = big ? rows_per_iter<10, 320>() : rows_per_iter<2, 256>();
+  if (qd % qkv_rows_per_wg || kvd % qkv_rows_per_wg) return *why = "q/kv rows must divide into workgroup tiles", false;
+  const int o_rows = qd == 2048 ? rows_per_iter<8, 256>() : rows_per_iter<2, 256>();
+  if (s.hidden % o_rows) return *why = "hidden rows must divide into o-proj tiles", false;
+  if (s.ffn % qkv_rows_per_wg) return *why = "ffn rows must divide into gate/up tiles", false;
+  const int d_rows = s.ffn == 10240 ? 4 * rows_per_iter<40, 320>() : rows_per_iter<4, 256>();
+  if (s.hidden % d_rows) return *why = "hidden rows must divide into down-proj tiles", false;
+  return true;
+}
+
+}  // namespace rt

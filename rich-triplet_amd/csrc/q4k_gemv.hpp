@@ -1,0 +1,145 @@
+// q4k_gemv.hpp -- device building blocks of the Q4_K GEMV (standalone and
+// fused into the decode-step kernels).
+//
+// Work split ("column resident"): a workgroup of T threads owns ROWS
+// consecutive output rows.  Thread t owns chunk slot s = t % S (S = 4*NB
+// 64-element chunks per row: super-block b = s/4, chunk c = s%4) and visits
+// rows rsub, rsub+RPI, ... (rsub = t / S, RPI = T / S).  Per row it loads the
+// 16-byte super-block header and its 32 nibble bytes (three 16-byte loads, the
+// four chunk lanes of a block read one contiguous 144-byte block), and keeps
+// the matching 64 activations in registers for all rows it visits.  The
+// activations are staged once per workgroup through LDS.
+//
+// Every load of the ITERS row-iterations is issued before any arithmetic so a
+// workgroup has all of its weights in flight at once.
+#pragma once
+
+#include "rt_device.hpp"
+
+namespace rt {
+
+// LDS layout of a staged activation vector: chunk slot s occupies floats
+// [s*kXPitch, s*kXPitch + 64).  The pitch of 68 floats keeps rows 16-byte
+// aligned and puts the eight lanes of a ds_read_b128 phase on distinct banks.
+constexpr int kXPitch = 68;
+RT_DEV int xlds_index(int e) { return (e >> 6) * kXPitch + (e & 63); }
+
+struct ChunkX {
+  float lo[32], hi[32];
+  float sum_lo, sum_hi;
+};
+
+RT_DEV void chunkx_from_lds(const float *xl, int slot, ChunkX &x) {
+  const float4 *p = reinterpret_cast<const float4 *>(xl + slot * kXPitch);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float4 v = p[i];
+    x.lo[4 * i] = v.x; x.lo[4 * i + 1] = v.y; x.lo[4 * i + 2] = v.z; x.lo[4 * i + 3] = v.w;
+    const float4 u = p[8 + i];
+    x.hi[4 * i] = u.x; x.hi[4 * i + 1] = u.y; x.hi[4 * i + 2] = u.z; x.hi[4 * i + 3] = u.w;
+  }
+  float a = 0.f, b = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) { a += x.lo[i]; b += x.hi[i]; }
+  x.sum_lo = a;
+  x.sum_hi = b;
+}
+
+// Copy x[0..K) (global, 16-byte aligned) into the LDS layout.
+template <int K, int T>
+RT_DEV void stage_x_plain(const float *__restrict__ x, float *xl) {
+  for (int f = threadIdx.x; f < K / 4; f += T) {
+    const float4 v = reinterpret_cast<const float4 *>(x)[f];
+    *reinterpret_cast<float4 *>(xl + xlds_index(4 * f)) = v;
+  }
+}
+
+// Dot of one 64-element chunk against resident activations with the
+// reference's integer trick, per sub-block: scale*sum(q*a) - min*sum(a)
+// (autograd2.rs:1671-1698).  High nibbles are converted as 16*q straight from
+// the byte (exact) and the 1/16 folds into the scale.
+RT_DEV float q4k_chunk_dot(const uint4 hd, const uint4 qa, const uint4 qb, int c, const ChunkX &x, uint32_t mlo,
+                           uint32_t mhi) {
+  const float d = half_bits_to_f32(hd.x & 0xFFFFu);
+  const float dm = half_bits_to_f32(hd.x >> 16);
+  uint32_t sv1, mv1, sv2, mv2;
+  q4k_scale_min(hd.y, hd.z, hd.w, 2 * c, sv1, mv1);
+  q4k_scale_min(hd.y, hd.z, hd.w, 2 * c + 1, sv2, mv2);
+  const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+  float dl0 = 0.f, dl1 = 0.f, dh0 = 0.f, dh1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t lo = w[i] & mlo;
+    const uint32_t hi = w[i] & mhi;
+    dl0 += ubyte0(lo) * x.lo[4 * i + 0];
+    dl1 += ubyte1(lo) * x.lo[4 * i + 1];
+    dl0 += ubyte2(lo) * x.lo[4 * i + 2];
+    dl1 += ubyte3(lo) * x.lo[4 * i + 3];
+    dh0 += ubyte0(hi) * x.hi[4 * i + 0];
+    dh1 += ubyte1(hi) * x.hi[4 * i + 1];
+    dh0 += ubyte2(hi) * x.hi[4 * i + 2];
+    dh1 += ubyte3(hi) * x.hi[4 * i + 3];
+  }
+  const float scale1 = d * (float)sv1, min1 = dm * (float)mv1;
+  const float scale2 = d * (float)sv2 * 0.0625f, min2 = dm * (float)mv2;
+  return scale1 * (dl0 + dl1) - min1 * x.sum_lo + scale2 * (dh0 + dh1) - min2 * x.sum_hi;
+}
+
+template <int NB, int T, int ITERS>
+struct Q4KTile {
+  static constexpr int S = NB * 4;
+  static constexpr int RPI = T / S;
+  static constexpr int ROWS = RPI * ITERS;
+  static_assert(T % S == 0 && T % 64 == 0, "a tile covers whole rows and whole waves");
+
+  int slot, rsub, b, c;
+  bool valid[ITERS];
+  uint4 hd[ITERS], qa[ITERS], qb[ITERS];
+
+  RT_DEV Q4KTile() {
+    slot = (int)threadIdx.x % S;
+    rsub = (int)threadIdx.x / S;
+    b = slot >> 2;
+    c = slot & 3;
+  }
+
+  // rowptr(rl) -> start of local row rl's blocks, or nullptr past the end.
+  template <class RowPtr>
+  RT_DEV void load(RowPtr rowptr) {
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      const uint8_t *row = rowptr(it * RPI + rsub);
+      valid[it] = row != nullptr;
+      if (row) {
+        const uint8_t *bp = row + (size_t)b * kQ4KBlockBytes;
+        hd[it] = *reinterpret_cast<const uint4 *>(bp);
+        qa[it] = *reinterpret_cast<const uint4 *>(bp + 16 + 32 * c);
+        qb[it] = *reinterpret_cast<const uint4 *>(bp + 32 + 32 * c);
+      } else {
+        hd[it] = qa[it] = qb[it] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
+
+  // Per-(row, super-block) partial sums into red[rl * NB + b].
+  RT_DEV void compute(const ChunkX &x, float *red) {
+    const uint32_t mlo = opaque_u32(0x0F0F0F0Fu), mhi = opaque_u32(0xF0F0F0F0u);
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      float p = q4k_chunk_dot(hd[it], qa[it], qb[it], c, x, mlo, mhi);
+      p = quad_sum(p);
+      if (c == 0 && valid[it]) red[(it * RPI + rsub) * NB + b] = p;
+    }
+  }
+};
+
+// Sum of one row's NB block partials, in block order.
+template <int NB>
+RT_DEV float reduce_row(const float *red, int rl) {
+  float s = 0.f;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) s += red[rl * NB + b];
+  return s;
+}
+
+}  // namespace rt

@@ -1,0 +1,167 @@
+"""GPU decode step (librt_hip.so rt_decode_*) against the CPU oracle's
+restatement of the reference decode step (transformer4.rs:1900-1964,
+2358-2385), on seeded synthetic weights."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import rel_l2
+from test_oracle import make_model
+
+pytestmark = pytest.mark.gpu
+
+LOGITS_TOL = 1e-3  # rel-L2 of the logits vs the oracle's f32 CPU order
+
+
+def tiny(group: int = 2, **kw):
+    base = dict(hidden=512, ffn=1024, n_q_heads=2, n_kv_heads=1, head_dim=256, n_layers=6, vocab=1000,
+                sliding_window=8, global_every=6, rope_theta_local=10000.0, rope_theta_global=1000000.0,
+                rope_fs_local=1.0, rope_fs_global=0.125, eps=1e-6, attn_scale=1.0 / 16.0)
+    if group == 4:
+        base.update(n_q_heads=4, n_kv_heads=1, head_dim=128, attn_scale=1.0 / np.sqrt(128.0))
+    elif group == 1:
+        base.update(n_q_heads=2, n_kv_heads=2, head_dim=256)
+    base.update(kw)
+    return base
+
+
+def build_ctx(rt, cfg, layers, embed, fnorm, ctx_len, max_seq):
+    d = rt.HipDecodeContext(cfg, max_seq)
+    for i, L in enumerate(layers):
+        d.set_layer(i, L)
+        d.sync_kv_from_cpu(i, np.ascontiguousarray(L["k_cache"][:ctx_len]),
+                           np.ascontiguousarray(L["v_cache"][:ctx_len]), ctx_len)
+    d.set_embed(embed, fnorm)
+    return d
+
+
+@pytest.mark.parametrize("group", [2, 4, 1])
+@pytest.mark.parametrize("pos", [0, 3, 20])
+def test_tiny_decode_step_matches_oracle(rt, orc, group, pos):
+    """Position 0 (first token, no history), 3 (inside the window of 8) and 20
+    (window slid; the global layer sees 21 keys)."""
+    cfg = tiny(group)
+    max_seq = 48
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=pos, seed=500 + group)
+    d = build_ctx(rt, cfg, layers, embed, fnorm, pos, max_seq)
+    got = d.decode_step(17, pos)
+    ref = orc.gemma3_decode_step(cfg, layers, embed, fnorm, token=17, pos=pos)
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, ref) < LOGITS_TOL
+    d.close()
+
+
+def test_tiny_multi_step_kv_append_and_graph_replay(rt, orc):
+    """Several consecutive steps replay one captured graph; K/V rows appended
+    by the GPU match the oracle's cache.append rows."""
+    cfg = tiny(2)
+    max_seq, ctx = 40, 5
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=ctx, seed=77)
+    d = build_ctx(rt, cfg, layers, embed, fnorm, ctx, max_seq)
+    tokens = [3, 999, 0, 512, 41, 7, 8, 9, 10, 11]
+    for i, tok in enumerate(tokens):
+        pos = ctx + i
+        got = d.decode_step(tok, pos)
+        ref = orc.gemma3_decode_step(cfg, layers, embed, fnorm, token=tok, pos=pos)
+        assert rel_l2(got, ref) < LOGITS_TOL, (i, rel_l2(got, ref))
+    kvd = cfg["n_kv_heads"] * cfg["head_dim"]
+    rows = ctx + len(tokens)
+    for li in (0, 5):
+        kp, vp = d.kv_ptrs(li)
+        k, v = d2h(kp, rows * kvd), d2h(vp, rows * kvd)
+        kr = layers[li]["k_cache"][:rows].reshape(-1)
+        vr = layers[li]["v_cache"][:rows].reshape(-1)
+        assert np.array_equal(k[:ctx * kvd], kr[:ctx * kvd])   # prefilled rows untouched
+        assert np.array_equal(v[:ctx * kvd], vr[:ctx * kvd])
+        assert rel_l2(k, kr) < 1e-4 and rel_l2(v, vr) < 1e-4  # appended rows
+    d.close()
+
+
+def d2h(ptr: int, n: int) -> np.ndarray:
+    """Copy n floats from a device pointer owned by the library."""
+    import ctypes
+    out = np.empty(n, np.float32)
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipDeviceSynchronize()
+    st = hip.hipMemcpy(ctypes.c_void_p(out.ctypes.data), ctypes.c_void_p(ptr), ctypes.c_size_t(n * 4), 2)
+    assert st == 0
+    return out
+
+
+def test_eager_and_graph_paths_agree(rt, orc):
+    cfg = tiny(2)
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=32, ctx=12, seed=91)
+    d1 = build_ctx(rt, cfg, layers, embed, fnorm, 12, 32)
+    d2 = build_ctx(rt, cfg, layers, embed, fnorm, 12, 32)
+    d2.set_graph(False)
+    a = d1.decode_step(5, 12)
+    b = d2.decode_step(5, 12)
+    assert np.array_equal(a, b)
+    d1.close()
+    d2.close()
+
+
+def test_decode_rejects_bad_calls(rt, orc):
+    cfg = tiny(2)
+    d = rt.HipDecodeContext(cfg, 16)
+    with pytest.raises(rt.RtError) as e:
+        d.decode_step(1, 0)  # weights not set
+    assert e.value.code == rt.RT_ESTATE
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=16, ctx=0, seed=3)
+    for i, L in enumerate(layers):
+        d.set_layer(i, L)
+    d.set_embed(embed, fnorm)
+    with pytest.raises(rt.RtError):
+        d.decode_step(cfg["vocab"], 0)   # token out of range
+    with pytest.raises(rt.RtError):
+        d.decode_step(0, 16)             # position beyond max_seq
+    d.close()
+    with pytest.raises(rt.RtError):
+        rt.HipDecodeContext(dict(cfg, hidden=768), 16)  # unsupported shape
+
+
+def test_gemma3_4b_shape_decode_step_matches_oracle(rt, orc, dev):
+    """34 layers, hidden 2560, FFN 10240, 8/4 heads of 256,
+    5 local (window 1024) : 1 global, vocab 262144, 4096 prefilled tokens of
+    N(0,1) K/V, f32 cache; decode at position 4096."""
+    cfg = dict(rt.GEMMA3_4B)
+    ctx = 4096
+    max_seq = ctx + 8
+    H, F, D = cfg["hidden"], cfg["ffn"], cfg["head_dim"]
+    QD, KVD = cfg["n_q_heads"] * D, cfg["n_kv_heads"] * D
+    layers = []
+    s = 9000
+    for _ in range(cfg["n_layers"]):
+        L = {}
+        for name, (rows, cols) in dict(q=(QD, H), k=(KVD, H), v=(KVD, H), o=(H, QD), gate=(F, H), up=(F, H),
+                                       down=(H, F)).items():
+            s += 1
+            L[name] = orc.synth_q4k(s, rows, cols)
+        for name, n in dict(in_norm=H, post_attn_norm=H, pre_ffn_norm=H, post_ffn_norm=H, q_norm=D,
+                            k_norm=D).items():
+            s += 1
+            L[name] = orc.synth_normal(s, n, 0.0, 0.1)
+        s += 1
+        kc = np.zeros((max_seq, KVD), np.float32)
+        kc[:ctx] = orc.synth_normal(s, ctx * KVD).reshape(ctx, KVD)
+        s += 1
+        vc = np.zeros((max_seq, KVD), np.float32)
+        vc[:ctx] = orc.synth_normal(s, ctx * KVD).reshape(ctx, KVD)
+        L["k_cache"], L["v_cache"] = kc, vc
+        layers.append(L)
+    embed = orc.synth_bf16(8888, cfg["vocab"] * H, 0.02)
+    fnorm = orc.synth_normal(8887, H, 0.0, 0.1)
+    d = build_ctx(rt, cfg, layers, embed, fnorm, ctx, max_seq)
+    got = d.decode_step(12345, ctx)
+    ref = orc.gemma3_decode_step(cfg, layers, embed, fnorm, token=12345, pos=ctx)
+    err = rel_l2(got, ref)
+    print(f"gemma3-4b shape logits rel-L2 {err:.3e}")
+    assert np.all(np.isfinite(got))
+    assert err < LOGITS_TOL
+    assert int(np.argmax(got)) == int(np.argmax(ref))
+    # next token continues from the appended row
+    got2 = d.decode_step(int(np.argmax(got)), ctx + 1)
+    ref2 = orc.gemma3_decode_step(cfg, layers, embed, fnorm, token=int(np.argmax(ref)), pos=ctx + 1)
+    assert rel_l2(got2, ref2) < LOGITS_TOL
+    d.close()
