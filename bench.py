@@ -1,0 +1,297 @@
+#!/usr/bin/env python3
+"""bench.py -- rich-triplet's Q4_K / BF16 decode hot path on one MI355X.
+
+Step (the `value` workload): every projection GEMV of one
+Gemma-3-4B decode token -- 34 layers x {q 2560->2048, k 2560->1024,
+v 2560->1024, o 2048->2560, gate/up 2560->10240, down 10240->2560} Q4_K
+GEMVs, each layer with its own weights, plus the BF16 lm_head 2560->262144 --
+captured in one hipGraph.  3.148 GB of weights per step, far beyond the 256 MB
+MALL, so every step streams from HBM.  value = algorithmic bytes / time.
+
+Also measured in the same run and reported next to it:
+  decode   -- BASELINE config 3: the full decode step (rt_decode_*) at
+              context 4096 with an f32 KV cache, tok/s;
+  roofline -- the dominant kernel (the 10240x2560 Q4_K GEMV of gate/up):
+              algorithmic bytes per launch / average launch time from HIP
+              events around a graph of back-to-back launches;
+  cpu_baseline -- the C restatement of the reference's x86 CPU path
+              (oracle/, "port") on a bounded sample, on this host's cores.
+
+Synthetic data (torch RNG on the GPU): Q4_K blocks with f16 d, dmin =
+|N(0,0.02)|, 6-bit scales/mins uniform 0..63, nibbles uniform; BF16 weights
+N(0,0.02); activations N(0,1); KV N(0,1).
+
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-decode] [--skip-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import pathlib
+import sys
+import time
+
+REPO = pathlib.Path(__file__).resolve().parent
+PEAK_HBM_GBS = 8000.0  # MI355X published HBM3E bandwidth
+
+H, F, QD, KVD, L, V = 2560, 10240, 2048, 1024, 34, 262144
+Q4K_SHAPES = [("q", QD, H), ("k", KVD, H), ("v", KVD, H), ("o", H, QD), ("gate", F, H), ("up", F, H),
+              ("down", H, F)]
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def load_pkg():
+    d = REPO / "rich-triplet_amd"
+    spec = importlib.util.spec_from_file_location("rich_triplet_amd", d / "__init__.py",
+                                                  submodule_search_locations=[str(d)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["rich_triplet_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def q4k_bytes(n: int, k: int) -> int:
+    return n * (k // 256) * 144
+
+
+def gemv_bytes(n: int, k: int, w_bytes: int) -> int:
+    """Algorithmic bytes of one GEMV: weights + x (f32) + y (f32)."""
+    return w_bytes + 4 * k + 4 * n
+
+
+def synth_q4k(torch, n: int, k: int, gen) -> "torch.Tensor":
+    """Random Q4_K blocks on the GPU, packed like pack_scales (autograd2.rs:1119-1132)."""
+    nb = n * k // 256
+    dev = "cuda"
+    blk = torch.randint(0, 256, (nb, 144), dtype=torch.uint8, device=dev, generator=gen)
+    dd = (torch.randn(nb, 2, device=dev, generator=gen).abs() * 0.02).half()
+    blk[:, 0:4] = dd.view(torch.uint8).view(nb, 4)
+    sv = torch.randint(0, 64, (nb, 8), dtype=torch.int32, device=dev, generator=gen)
+    mv = torch.randint(0, 64, (nb, 8), dtype=torch.int32, device=dev, generator=gen)
+    sc = torch.empty(nb, 12, dtype=torch.int32, device=dev)
+    sc[:, 0:4] = (sv[:, 0:4] & 63) | ((sv[:, 4:8] & 0x30) << 2)
+    sc[:, 4:8] = (mv[:, 0:4] & 63) | ((mv[:, 4:8] & 0x30) << 2)
+    sc[:, 8:12] = (sv[:, 4:8] & 15) | ((mv[:, 4:8] & 15) << 4)
+    blk[:, 4:16] = sc.to(torch.uint8)
+    return blk.reshape(-1)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--skip-decode", action="store_true")
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--seed", type=int, default=1234)
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the hot path is benchmarked on a single "
+                                   "MI355X (see DESIGN.md for how it would shard); run with --gpus 1"}))
+        return 2
+
+    import torch
+    rt = load_pkg()
+    rt.lib()  # fail loudly if the HIP library is missing
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    t0 = time.time()
+
+    # ---------------- weights: 34 distinct layers + tied BF16 embedding --------
+    layers = []
+    for li in range(L):
+        w = {name: synth_q4k(torch, n, k, gen) for name, n, k in Q4K_SHAPES}
+        for name in ("in_norm", "post_attn_norm", "pre_ffn_norm", "post_ffn_norm"):
+            w[name] = torch.randn(H, device=dev, generator=gen) * 0.1
+        w["q_norm"] = torch.randn(256, device=dev, generator=gen) * 0.1
+        w["k_norm"] = torch.randn(256, device=dev, generator=gen) * 0.1
+        layers.append(w)
+    embed = (torch.randn(V * H, device=dev, generator=gen) * 0.02).to(torch.bfloat16).view(torch.int16)
+    final_norm = torch.randn(H, device=dev, generator=gen) * 0.1
+    x_h = torch.randn(H, device=dev, generator=gen)
+    x_q = torch.randn(QD, device=dev, generator=gen)
+    x_f = torch.randn(F, device=dev, generator=gen)
+    outs = {name: torch.empty(n, device=dev) for name, n, _ in Q4K_SHAPES}
+    logits = torch.empty(V, device=dev)
+    torch.cuda.synchronize()
+    log(f"synthetic weights ready ({time.time() - t0:.1f}s)")
+
+    step_bytes = 0
+    for name, n, k in Q4K_SHAPES:
+        step_bytes += L * gemv_bytes(n, k, q4k_bytes(n, k))
+    q4k_step_bytes = step_bytes
+    step_bytes += gemv_bytes(V, H, V * H * 2)
+
+    # ---------------- the config-1 step as one graph ---------------------------
+    def enqueue_step(stream):
+        for w in layers:
+            for name, n, k in Q4K_SHAPES:
+                x = x_q if name == "o" else (x_f if name == "down" else x_h)
+                rt.q4k_gemv(w[name], x, outs[name], n, k, stream=stream)
+        rt.bf16_gemv(embed, x_h, logits, V, H, stream=stream)
+
+    cap = torch.cuda.Stream()
+    with torch.cuda.stream(cap):
+        enqueue_step(cap)  # eager warm-up on the capture stream
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cap):
+        enqueue_step(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    step_ms = e0.elapsed_time(e1) / args.steps
+    value = step_bytes / (step_ms * 1e-3) / 1e9
+    log(f"config-1 step {step_ms:.3f} ms -> {value:.0f} GB/s ({step_bytes / 1e9:.3f} GB per step)")
+
+    # ---------------- per-shape kernel timings (dominant kernel = gate/up) ------
+    per_shape = {}
+    reps = 10
+    for name, n, k in Q4K_SHAPES + [("lm_head", V, H)]:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap):
+            s = torch.cuda.current_stream()
+            if name == "lm_head":
+                rt.bf16_gemv(embed, x_h, logits, V, H, stream=s)
+            else:
+                x = x_q if name == "o" else (x_f if name == "down" else x_h)
+                for w in layers:
+                    rt.q4k_gemv(w[name], x, outs[name], n, k, stream=s)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        launches = reps * (1 if name == "lm_head" else L)
+        us = a.elapsed_time(b) * 1e3 / launches
+        wb = V * H * 2 if name == "lm_head" else q4k_bytes(n, k)
+        byts = gemv_bytes(n, k, wb)
+        per_shape[name] = {"n": n, "k": k, "us_per_launch": round(us, 3), "GBps": round(byts / us / 1e3, 1),
+                           "bytes_per_launch": byts}
+        del g
+    dom = per_shape["gate"]
+    roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(dom["GBps"] / PEAK_HBM_GBS, 4), "traffic": None,
+                "kernel": "k_q4k_gemv_cr<NB=10,T=320,ITERS=4> (Q4_K GEMV 10240x2560)",
+                "bytes_per_launch": dom["bytes_per_launch"], "us_per_launch": dom["us_per_launch"]}
+    log(f"dominant kernel gate 10240x2560: {dom['us_per_launch']} us/launch, {dom['GBps']} GB/s")
+
+    # ---------------- config 3: full decode step -------------------------------
+    decode = None
+    if not args.skip_decode:
+        ctx = 4096
+        cfg = dict(rt.GEMMA3_4B)
+        d = rt.HipDecodeContext(cfg, ctx + args.warmup + args.steps + 8)
+        for li, w in enumerate(layers):
+            d.set_layer(li, w)
+            kv = torch.randn(2, ctx, KVD, device=dev, generator=gen)
+            d.sync_kv_from_cpu(li, kv[0], kv[1], ctx)
+            del kv
+        d.set_embed(embed, final_norm)
+        torch.cuda.synchronize()
+        pos = ctx
+        for _ in range(args.warmup):
+            d.decode_step_async(pos % V, pos)
+            pos += 1
+        d.synchronize()
+        t_start = time.perf_counter()
+        for _ in range(args.steps):
+            d.decode_step_async(pos % V, pos)
+            pos += 1
+        d.synchronize()
+        dt = (time.perf_counter() - t_start) / args.steps
+        kv_read = (29 * 1024 + 5 * (ctx + 1)) * KVD * 4 * 2
+        q4k_weights = L * sum(q4k_bytes(n, k) for _, n, k in Q4K_SHAPES)
+        dec_bytes = q4k_weights + gemv_bytes(V, H, V * H * 2) + kv_read + H * 2 + L * 2 * KVD * 4
+        decode = {"workload": "config 3: Gemma-3-4B decode step, ctx 4096, f32 KV, 34 layers, vocab 262144",
+                  "tok_per_s": round(1.0 / dt, 1), "ms_per_token": round(dt * 1e3, 4),
+                  "bytes_per_token": dec_bytes, "GBps": round(dec_bytes / dt / 1e9, 1),
+                  "frac_of_hbm_peak": round(dec_bytes / dt / 1e9 / PEAK_HBM_GBS, 4),
+                  "launches_per_token": 5 * L + 1}
+        log(f"decode step {dt * 1e3:.3f} ms -> {1 / dt:.1f} tok/s")
+        d.close()
+
+    # ---------------- CPU baseline (oracle = C port of the reference path) -----
+    cpu = None
+    if not args.skip_cpu:
+        sys.path.insert(0, str(REPO))
+        from oracle import oracle as orc
+        threads = orc.hw_threads()
+        host = [(name, n, k, orc.synth_q4k(77 + i, n, k)) for i, (name, n, k) in enumerate(Q4K_SHAPES)]
+        xs = {H: orc.synth_normal(5, H), QD: orc.synth_normal(6, QD), F: orc.synth_normal(7, F)}
+        lm_rows = 16384
+        lm = orc.synth_bf16(8, lm_rows * H)
+        sample_bytes = sum(gemv_bytes(n, k, q4k_bytes(n, k)) for _, n, k, _ in host) + \
+            gemv_bytes(lm_rows, H, lm_rows * H * 2)
+        reps_done, t_cpu = 0, 0.0
+        while t_cpu < 10.0 or reps_done < 2:
+            t1 = time.perf_counter()
+            for name, n, k, blk in host:
+                orc.q4k_gemv(blk, n, k, xs[k], threads)
+            orc.bf16_gemv(lm, lm_rows, H, xs[H], threads)
+            t_cpu += time.perf_counter() - t1
+            reps_done += 1
+        cpu_gbs = sample_bytes * reps_done / t_cpu / 1e9
+        cpu = {"value": round(cpu_gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": f"one layer's 7 Q4_K projection GEMVs + {lm_rows} lm_head rows, "
+                         f"{reps_done} reps in {t_cpu:.1f}s; oracle/rt_oracle.c dot_row/gemv_mt "
+                         f"(scalar x86 branch of autograd2.rs), {threads} threads",
+               "cpu_model": cpu_model()}
+        log(f"cpu baseline {cpu_gbs:.2f} GB/s on {threads} threads")
+
+    out = {
+        "metric": "Q4_K GEMV HBM GB/s (% of peak); decode tok/s at Gemma-3-4B shape",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "frac_of_hbm_peak": round(value / PEAK_HBM_GBS, 4),
+        "config": {"workload": "config 1: Gemma-3-4B projection set of one decode token, 34 distinct layers x "
+                               "{q,k,v,o,gate,up,down} Q4_K GEMV + BF16 lm_head 2560->262144, one hipGraph",
+                   "bytes_per_step": step_bytes, "parallelism": "single GPU"},
+        "roofline": roofline,
+        "per_shape": per_shape,
+        "decode": decode,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -225,11 +225,14 @@ static void *band_main(void *p)
     return NULL;
 }
 
+/* Threads for the row bands: RT_ORACLE_THREADS if set, else the online CPU
+ * count capped at 16 (the share of host cores a one-GPU job may use). */
 int orc_hw_threads(void)
 {
     const char *env = getenv("RT_ORACLE_THREADS");
     if (env && atoi(env) > 0) return atoi(env);
     long n = sysconf(_SC_NPROCESSORS_ONLN);
+    if (n > 16) n = 16;
     return n > 0 ? (int)n : 1;
 }
 

@@ -10,6 +10,8 @@ namespace rt {
 // Keys per attention chunk are bounded so the chunk scores fit in LDS; the
 // host sizes the chunk count from max_seq accordingly.
 constexpr int kAttnMaxChunk = 256;
+// Upper bound on the number of chunks a KV head is split into.
+constexpr int kAttnMaxChunks = 512;
 
 struct DecodeShape {
   int hidden, ffn, n_q_heads, n_kv_heads, head_dim, n_layers, vocab;
@@ -33,7 +35,6 @@ struct DecodeArgs {
   const float *g_final;
   float *hid, *x2, *q, *k, *v, *attn, *o, *h, *dn, *logits;
   float *part_m, *part_l, *part_o;  // [n_q_heads, nchunk(, head_dim)]
-  unsigned *counters;               // [n_kv_heads], zero between launches
   float embed_scale, eps, attn_scale;
   int vocab, n_q_heads, n_kv_heads, head_dim;
 };

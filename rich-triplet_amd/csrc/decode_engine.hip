@@ -101,6 +101,8 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
   const int local_span = window > 0 ? std::min(window, c.max_seq) : c.max_seq;
   s.nchunk_local = std::max(1, std::min(128, (local_span + 15) / 16));
   s.nchunk_global = std::max(64, (c.max_seq + kAttnMaxChunk - 1) / kAttnMaxChunk);
+  if (s.nchunk_global > kAttnMaxChunks)
+    return set_error(RT_EINVAL, "rt_decode_create: max_seq %d exceeds %d", c.max_seq, kAttnMaxChunk * kAttnMaxChunks);
   if ((local_span + s.nchunk_local - 1) / s.nchunk_local > kAttnMaxChunk)
     return set_error(RT_EINVAL, "rt_decode_create: sliding window too large for the attention chunking");
 
@@ -149,8 +151,6 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
     TRY(fbuf((size_t)c.vocab, &a.logits));
     TRY(fbuf((size_t)c.n_q_heads * nch, &a.part_m)); TRY(fbuf((size_t)c.n_q_heads * nch, &a.part_l));
     TRY(fbuf((size_t)c.n_q_heads * nch * D, &a.part_o));
-    TRY(dalloc(d, 64 * sizeof(unsigned), &p)); a.counters = (unsigned *)p;
-    TRYH(hipMemset(a.counters, 0, 64 * sizeof(unsigned)), "hipMemset");
     a.params = d->params_dev;
     a.embed_scale = std::sqrt((float)c.hidden);   // transformer4.rs:2092
     a.eps = c.eps;

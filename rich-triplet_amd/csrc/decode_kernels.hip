@@ -1,13 +1,13 @@
 // decode_kernels.hip -- the fused kernels of one Gemma-3 decode step.
 //
-// Per layer five launches replace the reference's 21 dispatches
+// Per layer six launches replace the reference's 21 dispatches
 // (metal_decode.rs:1930-2024):
 //   k_qkv      residual+post-FFN norm of the previous layer (or the embedding
 //              row for layer 0), input RMSNorm, then one GEMV over the stacked
 //              q|k|v rows;
 //   k_attn     q/k per-head RMSNorm + NeoX RoPE, K/V append at `pos`, split-K
-//              attention over the f32 cache with an in-kernel combine by the
-//              last workgroup of each KV head;
+//              attention over the f32 cache (per-chunk softmax partials);
+//   k_attn_combine  merge of the chunk partials into the attention output;
 //   k_gemv     o projection;
 //   k_gateup   residual + post-attention norm, pre-FFN norm, gate and up
 //              GEMVs of the same rows, gelu_tanh(gate)*up epilogue;
@@ -108,7 +108,7 @@ RT_DEV void prologue(const DecodeArgs &a, const float *__restrict__ base, const 
     if (f < F4) {
       if (x_out && blockIdx.x == 0) reinterpret_cast<float4 *>(x_out)[f] = x[i];
       const float4 g = reinterpret_cast<const float4 *>(g_out)[f];
-      *reinterpret_cast<float4 *>(xl + xlds_index(4 * f)) = norm4(x[i], rx, g);
+      stage_x_store(xl, f, norm4(x[i], rx, g));
     }
   }
 }
@@ -212,9 +212,9 @@ __global__ __launch_bounds__(T) void k_gemv(const uint8_t *__restrict__ W, const
 //   2. scores s_c = (q.k_c)*scale for keys in the chunk (16 lanes per key)
 //   3. chunk-local softmax statistics m = max s, l = sum exp(s - m)
 //   4. o = sum_c exp(s_c - m) v_c (one thread per dimension)
-//   5. partials (m, l, o) to global; the last workgroup of the KV head
-//      merges all chunks: out = sum_i o_i e^(m_i-M) / sum_i l_i e^(m_i-M).
-// The result equals gqa_attention_cached's t_q == 1 branch (2806-2879).
+//   5. partials (m, l, o) to global; k_attn_combine merges the chunks:
+//      out = sum_i o_i e^(m_i-M) / sum_i l_i e^(m_i-M).
+// Together they equal gqa_attention_cached's t_q == 1 branch (2806-2879).
 // ---------------------------------------------------------------------------
 template <int D>
 RT_DEV void norm_rope_head(const float *__restrict__ src, const float *__restrict__ gamma,
@@ -253,7 +253,6 @@ __global__ __launch_bounds__(256) void k_attn(DecodeArgs a, LayerArgs L) {
   __shared__ float knew[D], vnew[D];
   __shared__ float sc[G][MAXC];
   __shared__ float stat[G][2];
-  __shared__ int last_flag;
   const int kvh = blockIdx.y, chunk = blockIdx.x, nchunk = gridDim.x;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int pos = a.params[1];
@@ -375,36 +374,48 @@ __global__ __launch_bounds__(256) void k_attn(DecodeArgs a, LayerArgs L) {
     a.part_m[(size_t)h * nchunk + chunk] = n > 0 ? stat[threadIdx.x][0] : -INFINITY;
     a.part_l[(size_t)h * nchunk + chunk] = n > 0 ? stat[threadIdx.x][1] : 0.f;
   }
+}
 
-  // 5. the last workgroup of this KV head merges the chunks
-  __threadfence();
+// ---------------------------------------------------------------------------
+// k_attn_combine: merge the chunk partials of one q head and 64 dimensions.
+//   out[d] = sum_i o_i[d] e^(m_i - M) / sum_i l_i e^(m_i - M),  M = max_i m_i
+// 256 threads = 4 chunk groups x 64 dimensions; grid (n_q_heads, D/64).
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void k_attn_combine(DecodeArgs a, int nchunk) {
+  __shared__ float wts[kAttnMaxChunks];
+  __shared__ float part[4][64];
+  __shared__ float bred[4];
+  const int h = blockIdx.x, d0 = blockIdx.y * 64;
+  const float *pm = a.part_m + (size_t)h * nchunk;
+  const float *pl = a.part_l + (size_t)h * nchunk;
+  float m = -INFINITY;
+  for (int i = threadIdx.x; i < nchunk; i += 256) m = fmaxf(m, pm[i]);
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) bred[threadIdx.x >> 6] = m;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned prev = atomicAdd(&a.counters[kvh], 1u);
-    last_flag = prev == (unsigned)(nchunk - 1);
-  }
+  const float M = fmaxf(fmaxf(bred[0], bred[1]), fmaxf(bred[2], bred[3]));
   __syncthreads();
-  if (!last_flag) return;
-  __threadfence();
-  for (int d = threadIdx.x; d < D; d += 256) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const int h = kvh * G + g;
-      const float *pm = a.part_m + (size_t)h * nchunk;
-      const float *pl = a.part_l + (size_t)h * nchunk;
-      float M = -INFINITY;
-      for (int i = 0; i < nchunk; ++i) M = fmaxf(M, pm[i]);
-      float Ls = 0.f, acc = 0.f;
-      for (int i = 0; i < nchunk; ++i) {
-        const float mi = pm[i];
-        const float w = mi == -INFINITY ? 0.f : expf(mi - M);
-        Ls += pl[i] * w;
-        acc += a.part_o[((size_t)h * nchunk + i) * D + d] * w;
-      }
-      a.attn[(size_t)h * D + d] = acc / Ls;
-    }
+  float l = 0.f;
+  for (int i = threadIdx.x; i < nchunk; i += 256) {
+    const float mi = pm[i];
+    const float w = mi == -INFINITY ? 0.f : expf(mi - M);
+    wts[i] = w;
+    l += pl[i] * w;
   }
-  if (threadIdx.x == 0) a.counters[kvh] = 0u;
+  const float L = block_sum<256>(l, bred);  // also orders the wts writes
+  const int cg = threadIdx.x >> 6, dl = threadIdx.x & 63;
+  const float *po = a.part_o + (size_t)h * nchunk * D + d0 + dl;
+  float acc0 = 0.f, acc1 = 0.f;
+  int i = cg;
+  for (; i + 4 < nchunk; i += 8) {
+    acc0 += po[(size_t)i * D] * wts[i];
+    acc1 += po[(size_t)(i + 4) * D] * wts[i + 4];
+  }
+  for (; i < nchunk; i += 4) acc0 += po[(size_t)i * D] * wts[i];
+  part[cg][dl] = acc0 + acc1;
+  __syncthreads();
+  if (cg == 0) a.attn[(size_t)h * D + d0 + dl] = (part[0][dl] + part[1][dl] + part[2][dl] + part[3][dl]) / L;
 }
 
 // ---------------------------------------------------------------------------
@@ -538,8 +549,14 @@ hipError_t enqueue_decode_step(const DecodeShape &s, const DecodeArgs &a, const 
     if (big) launch_qkv<10, 320, 1>(l, a, L, P, li == 0, qkv_rows);
     else launch_qkv<2, 256, 1>(l, a, L, P, li == 0, qkv_rows);
     const int nchunk = L.window > 0 ? s.nchunk_local : s.nchunk_global;
-    if (s.head_dim == 256) launch_attn_d<256>(l, a, L, nchunk, group);
-    else launch_attn_d<128>(l, a, L, nchunk, group);
+    if (s.head_dim == 256) {
+      launch_attn_d<256>(l, a, L, nchunk, group);
+      hipLaunchKernelGGL((k_attn_combine<256>), dim3(s.n_q_heads, 4), dim3(256), 0, l.s, a, nchunk);
+    } else {
+      launch_attn_d<128>(l, a, L, nchunk, group);
+      hipLaunchKernelGGL((k_attn_combine<128>), dim3(s.n_q_heads, 2), dim3(256), 0, l.s, a, nchunk);
+    }
+    l.check();
     if (qd == 2048) launch_gemv<8, 256, 1>(l, L.wo, a.attn, a.o, s.hidden);
     else launch_gemv<2, 256, 1>(l, L.wo, a.attn, a.o, s.hidden);
     if (big) launch_gateup<10, 320, 1>(l, a, L, s.ffn);

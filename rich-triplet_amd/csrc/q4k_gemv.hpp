@@ -19,8 +19,10 @@
 namespace rt {
 
 // LDS layout of a staged activation vector: chunk slot s occupies floats
-// [s*kXPitch, s*kXPitch + 64).  The pitch of 68 floats keeps rows 16-byte
-// aligned and puts the eight lanes of a ds_read_b128 phase on distinct banks.
+// [s*kXPitch, s*kXPitch + 64), followed by the sums of its low and high
+// halves (the per-sub-block sum(a) of the integer trick) at +64 and +65.
+// The pitch of 68 floats keeps slots 16-byte aligned and puts the eight lanes
+// of a ds_read_b128 phase on distinct banks.
 constexpr int kXPitch = 68;
 RT_DEV int xlds_index(int e) { return (e >> 6) * kXPitch + (e & 63); }
 
@@ -38,20 +40,31 @@ RT_DEV void chunkx_from_lds(const float *xl, int slot, ChunkX &x) {
     const float4 u = p[8 + i];
     x.hi[4 * i] = u.x; x.hi[4 * i + 1] = u.y; x.hi[4 * i + 2] = u.z; x.hi[4 * i + 3] = u.w;
   }
-  float a = 0.f, b = 0.f;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) { a += x.lo[i]; b += x.hi[i]; }
-  x.sum_lo = a;
-  x.sum_hi = b;
+  const float4 sums = p[16];
+  x.sum_lo = sums.x;
+  x.sum_hi = sums.y;
+}
+
+// Store one float4 of the staged vector (element 4f..4f+3) and, from the 16
+// lanes that hold one chunk, the sums of its two 32-element halves.  Lanes
+// f..f+15 of a chunk must be consecutive lanes of one wave (f = tid + i*T with
+// T a multiple of 16).
+RT_DEV void stage_x_store(float *xl, int f, float4 v) {
+  *reinterpret_cast<float4 *>(xl + xlds_index(4 * f)) = v;
+  float s = (v.x + v.y) + (v.z + v.w);
+  s += dpp<0xB1>(s);   // quad
+  s += dpp<0x4E>(s);
+  s += dpp<0x141>(s);  // half row: 8 lanes = 32 elements
+  const int sub = f & 15;
+  if (sub == 0) xl[(f >> 4) * kXPitch + 64] = s;
+  if (sub == 8) xl[(f >> 4) * kXPitch + 65] = s;
 }
 
 // Copy x[0..K) (global, 16-byte aligned) into the LDS layout.
 template <int K, int T>
 RT_DEV void stage_x_plain(const float *__restrict__ x, float *xl) {
-  for (int f = threadIdx.x; f < K / 4; f += T) {
-    const float4 v = reinterpret_cast<const float4 *>(x)[f];
-    *reinterpret_cast<float4 *>(xl + xlds_index(4 * f)) = v;
-  }
+  static_assert(T % 16 == 0 && (K / 4) % 16 == 0, "chunk lanes must be whole DPP rows");
+  for (int f = threadIdx.x; f < K / 4; f += T) stage_x_store(xl, f, reinterpret_cast<const float4 *>(x)[f]);
 }
 
 // Dot of one 64-element chunk against resident activations with the
