@@ -89,6 +89,9 @@ def main() -> int:
     ap.add_argument("--skip-decode", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only run the PMC probe: a 256 MiB copy (calibration) and 20 launches of the dominant "
+                         "kernel on distinct weights; meant to run under rocprofv3 --pmc")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -103,6 +106,22 @@ def main() -> int:
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed)
     t0 = time.time()
+
+    if args.traffic_probe:
+        a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        a.fill_(1)
+        torch.cuda.synchronize()
+        b.copy_(a)  # calibration: reads and writes exactly 256 MiB
+        torch.cuda.synchronize()
+        ws = [synth_q4k(torch, F, H, gen) for _ in range(20)]
+        x = torch.randn(H, device=dev, generator=gen)
+        y = torch.empty(F, device=dev)
+        for w in ws:
+            rt.q4k_gemv(w, x, y, F, H)
+        torch.cuda.synchronize()
+        print(json.dumps({"traffic_probe": "done", "copy_bytes": 256 << 20, "gemv_launches": len(ws)}))
+        return 0
 
     # ---------------- weights: 34 distinct layers + tied BF16 embedding --------
     layers = []
@@ -189,7 +208,7 @@ def main() -> int:
         del g
     dom = per_shape["gate"]
     roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(dom["GBps"] / PEAK_HBM_GBS, 4), "traffic": None,
+                "frac": round(dom["GBps"] / PEAK_HBM_GBS, 4), "traffic": measured_traffic(),
                 "kernel": "k_q4k_gemv_cr<NB=10,T=320,ITERS=4> (Q4_K GEMV 10240x2560)",
                 "bytes_per_launch": dom["bytes_per_launch"], "us_per_launch": dom["us_per_launch"]}
     log(f"dominant kernel gate 10240x2560: {dom['us_per_launch']} us/launch, {dom['GBps']} GB/s")
@@ -281,6 +300,20 @@ def main() -> int:
     }
     print(json.dumps(out), flush=True)
     return 0
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3
+    --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy calibration),
+    or None when the summary is absent."""
+    f = REPO / "profiles" / "q4k_gemv_10240x2560_traffic.txt"
+    try:
+        for line in f.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch="):
+                return int(float(line.split("=", 1)[1]))
+    except OSError:
+        pass
+    return None
 
 
 def cpu_model() -> str:

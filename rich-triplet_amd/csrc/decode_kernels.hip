@@ -54,61 +54,61 @@ enum class Pro { Embed, Resid };
 // x = Embed: bf16(E[token]) * embed_scale        (transformer4.rs:2360-2368)
 //     Resid: base + rms(add)*(1+g_add)           (post-norm residual, 1954-1964)
 // then xn = rms(x)*(1+g_out) into LDS; workgroup 0 stores x to x_out.
+// pro_load issues every global load of the prologue (call it before the
+// weight loads); pro_finish does the arithmetic and the LDS stores.
+template <int K, int T>
+struct ProRegs {
+  static constexpr int F4 = K / 4;
+  static constexpr int PER = (F4 + T - 1) / T;
+  float4 add[PER], base[PER], ga[PER], go[PER];
+};
+
 template <int K, int T, Pro MODE>
-RT_DEV void prologue(const DecodeArgs &a, const float *__restrict__ base, const float *__restrict__ add,
-                     const float *__restrict__ g_add, const float *__restrict__ g_out, float *__restrict__ x_out,
-                     float *xl, float *red) {
-  constexpr int F4 = K / 4;
-  constexpr int PER = (F4 + T - 1) / T;
-  const float inv_k = 1.0f / (float)K;
-  float4 x[PER];
-  if constexpr (MODE == Pro::Embed) {
-    const int token = a.params[0];
-    const uint2 *row = reinterpret_cast<const uint2 *>(a.embed + (size_t)token * K);
+RT_DEV void pro_load(const DecodeArgs &a, const float *__restrict__ base, const float *__restrict__ add,
+                     const float *__restrict__ g_add, const float *__restrict__ g_out, ProRegs<K, T> &r) {
+  using R = ProRegs<K, T>;
+  // Unconditional 16-byte loads at a clamped index (entries past the end are
+  // never stored): branch-free loads keep their own s_waitcnt.
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int f = threadIdx.x + i * T;
-      if (f < F4) {
-        const uint2 w = row[f];
-        x[i] = make_float4(mul_nc(bf16_lo(w.x), a.embed_scale), mul_nc(bf16_hi(w.x), a.embed_scale),
-                           mul_nc(bf16_lo(w.y), a.embed_scale), mul_nc(bf16_hi(w.y), a.embed_scale));
-      } else {
-        x[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+  for (int i = 0; i < R::PER; ++i) {
+    const int f = min((int)threadIdx.x + i * T, R::F4 - 1);
+    if constexpr (MODE == Pro::Embed) {
+      const uint2 w = reinterpret_cast<const uint2 *>(a.embed + (size_t)a.params[0] * K)[f];
+      r.add[i] = make_float4(mul_nc(bf16_lo(w.x), a.embed_scale), mul_nc(bf16_hi(w.x), a.embed_scale),
+                             mul_nc(bf16_lo(w.y), a.embed_scale), mul_nc(bf16_hi(w.y), a.embed_scale));
+    } else {
+      r.add[i] = reinterpret_cast<const float4 *>(add)[f];
+      r.base[i] = reinterpret_cast<const float4 *>(base)[f];
+      r.ga[i] = reinterpret_cast<const float4 *>(g_add)[f];
     }
-  } else {
-    float4 ad[PER];
+    r.go[i] = reinterpret_cast<const float4 *>(g_out)[f];
+  }
+}
+
+template <int K, int T, Pro MODE>
+RT_DEV void pro_finish(const DecodeArgs &a, ProRegs<K, T> &r, float *__restrict__ x_out, float *xl, float *red) {
+  using R = ProRegs<K, T>;
+  const float inv_k = 1.0f / (float)K;
+  float4 *x = r.add;  // Embed: the embedding row; Resid: overwritten with the residual sum
+  auto live = [&](int i) { return (int)threadIdx.x + i * T < R::F4; };
+  if constexpr (MODE == Pro::Resid) {
     float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int f = threadIdx.x + i * T;
-      ad[i] = f < F4 ? reinterpret_cast<const float4 *>(add)[f] : make_float4(0.f, 0.f, 0.f, 0.f);
-      ss += sumsq4(ad[i]);
-    }
+    for (int i = 0; i < R::PER; ++i) ss += live(i) ? sumsq4(r.add[i]) : 0.f;
     const float ra = rms_inv_from_sumsq(block_sum<T>(ss, red), inv_k, a.eps);
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int f = threadIdx.x + i * T;
-      if (f < F4) {
-        const float4 b = reinterpret_cast<const float4 *>(base)[f];
-        const float4 g = reinterpret_cast<const float4 *>(g_add)[f];
-        x[i] = add4(b, norm4(ad[i], ra, g));
-      } else {
-        x[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-    }
+    for (int i = 0; i < R::PER; ++i) x[i] = add4(r.base[i], norm4(r.add[i], ra, r.ga[i]));
   }
   float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) ss += sumsq4(x[i]);
+  for (int i = 0; i < R::PER; ++i) ss += live(i) ? sumsq4(x[i]) : 0.f;
   const float rx = rms_inv_from_sumsq(block_sum<T>(ss, red), inv_k, a.eps);
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
+  for (int i = 0; i < R::PER; ++i) {
     const int f = threadIdx.x + i * T;
-    if (f < F4) {
+    if (f < R::F4) {
       if (x_out && blockIdx.x == 0) reinterpret_cast<float4 *>(x_out)[f] = x[i];
-      const float4 g = reinterpret_cast<const float4 *>(g_out)[f];
-      stage_x_store(xl, f, norm4(x[i], rx, g));
+      stage_x_store(xl, f, norm4(x[i], rx, r.go[i]));
     }
   }
 }
@@ -136,12 +136,11 @@ __global__ __launch_bounds__(T) void k_qkv(DecodeArgs a, LayerArgs L, LayerArgs 
     W = L.wv, y = a.v, r0 = row0 - qd - kvd;
   }
   const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
+  ProRegs<K, T> pr;
+  pro_load<K, T, MODE>(a, a.x2, a.dn, prev.g_post_ffn, L.g_in, pr);
   Tile tile;
-  tile.load([&](int rl) -> const uint8_t * { return W + (size_t)(r0 + rl) * row_bytes; });
-  if constexpr (MODE == Pro::Embed)
-    prologue<K, T, Pro::Embed>(a, nullptr, nullptr, nullptr, L.g_in, a.hid, xl, bred);
-  else
-    prologue<K, T, Pro::Resid>(a, a.x2, a.dn, prev.g_post_ffn, L.g_in, a.hid, xl, bred);
+  tile.load([&](int rl) -> const uint8_t * { return W + (size_t)(r0 + rl) * row_bytes; }, W);
+  pro_finish<K, T, MODE>(a, pr, a.hid, xl, bred);
   __syncthreads();
   ChunkX cx;
   chunkx_from_lds(xl, tile.slot, cx);
@@ -164,11 +163,13 @@ __global__ __launch_bounds__(T) void k_gateup(DecodeArgs a, LayerArgs L) {
   __shared__ float bred[T / 64];
   const int j0 = (int)blockIdx.x * ROWS;
   const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
+  ProRegs<K, T> pr;
+  pro_load<K, T, Pro::Resid>(a, a.hid, a.o, L.g_post_attn, L.g_pre_ffn, pr);
   Tile tile;
   tile.load([&](int rl) -> const uint8_t * {
     return rl < ROWS ? L.wgate + (size_t)(j0 + rl) * row_bytes : L.wup + (size_t)(j0 + rl - ROWS) * row_bytes;
-  });
-  prologue<K, T, Pro::Resid>(a, a.hid, a.o, L.g_post_attn, L.g_pre_ffn, a.x2, xl, bred);
+  }, L.wgate);
+  pro_finish<K, T, Pro::Resid>(a, pr, a.x2, xl, bred);
   __syncthreads();
   ChunkX cx;
   chunkx_from_lds(xl, tile.slot, cx);
@@ -192,9 +193,11 @@ __global__ __launch_bounds__(T) void k_gemv(const uint8_t *__restrict__ W, const
   __shared__ float red[Tile::ROWS * NB];
   const int row0 = (int)blockIdx.x * Tile::ROWS;  // ROWS divides N (checked on the host)
   const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
+  XRegs<NB * 256, T> xr;
+  x_load<NB * 256, T>(x, xr);
   Tile tile;
-  tile.load([&](int rl) -> const uint8_t * { return W + (size_t)(row0 + rl) * row_bytes; });
-  stage_x_plain<NB * 256, T>(x, xl);
+  tile.load([&](int rl) -> const uint8_t * { return W + (size_t)(row0 + rl) * row_bytes; }, W);
+  x_store<NB * 256, T>(xr, xl);
   __syncthreads();
   ChunkX cx;
   chunkx_from_lds(xl, tile.slot, cx);
@@ -428,7 +431,9 @@ __global__ __launch_bounds__(256) void k_lmhead(DecodeArgs a, LayerArgs last) {
   constexpr int U = 2;
   __shared__ __attribute__((aligned(16))) float xl[K / 64 * kXPitch];
   __shared__ float bred[4];
-  prologue<K, 256, Pro::Resid>(a, a.x2, a.dn, last.g_post_ffn, a.g_final, nullptr, xl, bred);
+  ProRegs<K, 256> pr;
+  pro_load<K, 256, Pro::Resid>(a, a.x2, a.dn, last.g_post_ffn, a.g_final, pr);
+  pro_finish<K, 256, Pro::Resid>(a, pr, nullptr, xl, bred);
   __syncthreads();
   const int lane = threadIdx.x & 63;
   float xr[CPL][8];

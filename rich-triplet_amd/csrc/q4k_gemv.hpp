@@ -60,11 +60,32 @@ RT_DEV void stage_x_store(float *xl, int f, float4 v) {
   if (sub == 8) xl[(f >> 4) * kXPitch + 65] = s;
 }
 
-// Copy x[0..K) (global, 16-byte aligned) into the LDS layout.
+// Activation staging in two halves so the global loads of x can be issued
+// before the weight loads (x_load) and consumed after them (x_store): the
+// s_waitcnt for x then leaves every weight load in flight.
 template <int K, int T>
-RT_DEV void stage_x_plain(const float *__restrict__ x, float *xl) {
+struct XRegs {
+  static constexpr int PER = (K / 4 + T - 1) / T;
+  float4 v[PER];
+};
+
+template <int K, int T>
+RT_DEV void x_load(const float *__restrict__ x, XRegs<K, T> &r) {
   static_assert(T % 16 == 0 && (K / 4) % 16 == 0, "chunk lanes must be whole DPP rows");
-  for (int f = threadIdx.x; f < K / 4; f += T) stage_x_store(xl, f, reinterpret_cast<const float4 *>(x)[f]);
+#pragma unroll
+  for (int i = 0; i < XRegs<K, T>::PER; ++i) {
+    const int f = min((int)threadIdx.x + i * T, K / 4 - 1);  // clamped, unconditional 16-byte load
+    r.v[i] = reinterpret_cast<const float4 *>(x)[f];
+  }
+}
+
+template <int K, int T>
+RT_DEV void x_store(const XRegs<K, T> &r, float *xl) {
+#pragma unroll
+  for (int i = 0; i < XRegs<K, T>::PER; ++i) {
+    const int f = threadIdx.x + i * T;
+    if (f < K / 4) stage_x_store(xl, f, r.v[i]);
+  }
 }
 
 // Dot of one 64-element chunk against resident activations with the
@@ -117,20 +138,19 @@ struct Q4KTile {
   }
 
   // rowptr(rl) -> start of local row rl's blocks, or nullptr past the end.
+  // The loads themselves are unconditional (a row past the end re-reads
+  // `fallback`, a valid row, and is masked out of the result): branch-free
+  // loads let the compiler wait for exactly the loads an iteration needs.
   template <class RowPtr>
-  RT_DEV void load(RowPtr rowptr) {
+  RT_DEV void load(RowPtr rowptr, const uint8_t *fallback) {
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
       const uint8_t *row = rowptr(it * RPI + rsub);
       valid[it] = row != nullptr;
-      if (row) {
-        const uint8_t *bp = row + (size_t)b * kQ4KBlockBytes;
-        hd[it] = *reinterpret_cast<const uint4 *>(bp);
-        qa[it] = *reinterpret_cast<const uint4 *>(bp + 16 + 32 * c);
-        qb[it] = *reinterpret_cast<const uint4 *>(bp + 32 + 32 * c);
-      } else {
-        hd[it] = qa[it] = qb[it] = make_uint4(0, 0, 0, 0);
-      }
+      const uint8_t *bp = (row ? row : fallback) + (size_t)b * kQ4KBlockBytes;
+      hd[it] = *reinterpret_cast<const uint4 *>(bp);
+      qa[it] = *reinterpret_cast<const uint4 *>(bp + 16 + 32 * c);
+      qb[it] = *reinterpret_cast<const uint4 *>(bp + 32 + 32 * c);
     }
   }
 

@@ -82,11 +82,13 @@ __global__ __launch_bounds__(T) void k_q4k_gemv_cr(const uint8_t *__restrict__ W
   Tile tile;
   const int row0 = (int)blockIdx.x * Tile::ROWS;
   const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
+  XRegs<NB * 256, T> xr;
+  x_load<NB * 256, T>(x, xr);
   tile.load([&](int rl) -> const uint8_t * {
     const int r = row0 + rl;
     return r < N ? W + (size_t)r * row_bytes : nullptr;
-  });
-  stage_x_plain<NB * 256, T>(x, xl);
+  }, W);
+  x_store<NB * 256, T>(xr, xl);
   __syncthreads();
   ChunkX cx;
   chunkx_from_lds(xl, tile.slot, cx);
