@@ -7,11 +7,11 @@
 
 namespace rt {
 
-// Keys per attention chunk are bounded so the chunk scores fit in LDS; the
-// host sizes the chunk count from max_seq accordingly.
-constexpr int kAttnMaxChunk = 256;
+// Keys per attention chunk (at most): the host sizes the chunk count from
+// max_seq (global layers) or the sliding window (local layers).
+constexpr int kAttnChunkKeys = 16;
 // Upper bound on the number of chunks a KV head is split into.
-constexpr int kAttnMaxChunks = 512;
+constexpr int kAttnMaxChunks = 4096;
 
 struct DecodeShape {
   int hidden, ffn, n_q_heads, n_kv_heads, head_dim, n_layers, vocab;

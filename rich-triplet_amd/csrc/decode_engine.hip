@@ -99,12 +99,10 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
     return set_error(RT_EINVAL, "rt_decode_create: unsupported shape: %s", why);
   const int window = c.sliding_window;
   const int local_span = window > 0 ? std::min(window, c.max_seq) : c.max_seq;
-  s.nchunk_local = std::max(1, std::min(128, (local_span + 15) / 16));
-  s.nchunk_global = std::max(64, (c.max_seq + kAttnMaxChunk - 1) / kAttnMaxChunk);
+  s.nchunk_local = (local_span + kAttnChunkKeys - 1) / kAttnChunkKeys;
+  s.nchunk_global = (c.max_seq + kAttnChunkKeys - 1) / kAttnChunkKeys;
   if (s.nchunk_global > kAttnMaxChunks)
-    return set_error(RT_EINVAL, "rt_decode_create: max_seq %d exceeds %d", c.max_seq, kAttnMaxChunk * kAttnMaxChunks);
-  if ((local_span + s.nchunk_local - 1) / s.nchunk_local > kAttnMaxChunk)
-    return set_error(RT_EINVAL, "rt_decode_create: sliding window too large for the attention chunking");
+    return set_error(RT_EINVAL, "rt_decode_create: max_seq %d exceeds %d", c.max_seq, kAttnChunkKeys * kAttnMaxChunks);
 
   rt_decode *d = new rt_decode();
   d->cfg = c;

@@ -10,7 +10,7 @@
 //   k_attn_combine  merge of the chunk partials into the attention output;
 //   k_gemv     o projection;
 //   k_gateup   residual + post-attention norm, pre-FFN norm, gate and up
-//              GEMVs of the same rows, gelu_tanh(gate)*up epilogue;
+//              GEMVs of the same rows (persistent tiles), gelu_tanh(gate)*up;
 //   k_gemv     down projection.
 // After the last layer k_lmhead applies the final residual, the final norm
 // and the BF16 lm_head GEMV.  Token id and position are read from device
@@ -85,8 +85,8 @@ RT_DEV void pro_load(const DecodeArgs &a, const float *__restrict__ base, const 
   }
 }
 
-template <int K, int T, Pro MODE>
-RT_DEV void pro_finish(const DecodeArgs &a, ProRegs<K, T> &r, float *__restrict__ x_out, float *xl, float *red) {
+template <int K, int T, Pro MODE, bool DIG = false>
+RT_DEV void pro_finish(const DecodeArgs &a, ProRegs<K, T> &r, float *__restrict__ x_out, void *lds, float *red) {
   using R = ProRegs<K, T>;
   const float inv_k = 1.0f / (float)K;
   float4 *x = r.add;  // Embed: the embedding row; Resid: overwritten with the residual sum
@@ -108,7 +108,10 @@ RT_DEV void pro_finish(const DecodeArgs &a, ProRegs<K, T> &r, float *__restrict_
     const int f = threadIdx.x + i * T;
     if (f < R::F4) {
       if (x_out && blockIdx.x == 0) reinterpret_cast<float4 *>(x_out)[f] = x[i];
-      stage_x_store(xl, f, norm4(x[i], rx, r.go[i]));
+      if constexpr (DIG)
+        stage_digits_store(static_cast<uint32_t *>(lds), f, norm4(x[i], rx, r.go[i]));
+      else
+        stage_x_store(static_cast<float *>(lds), f, norm4(x[i], rx, r.go[i]));
     }
   }
 }
@@ -150,35 +153,48 @@ __global__ __launch_bounds__(T) void k_qkv(DecodeArgs a, LayerArgs L, LayerArgs 
 }
 
 // ---------------------------------------------------------------------------
-// k_gateup: x2 = hid + rms(o)(1+g_pa); n2 = rms(x2)(1+g_pf); gate & up rows
-// j0..j0+ROWS; h[j] = gelu_tanh(gate[j]) * up[j]   (transformer4.rs:328-334)
+// k_gateup: x2 = hid + rms(o)(1+g_pa); n2 = rms(x2)(1+g_pf); then persistent
+// workgroups walk tiles of RPI gate rows + the same RPI up rows (double
+// buffered) and store h[j] = gelu_tanh(gate[j]) * up[j]  (transformer4.rs:328-334)
 // ---------------------------------------------------------------------------
-template <int NB, int T, int ITERS>
-__global__ __launch_bounds__(T) void k_gateup(DecodeArgs a, LayerArgs L) {
-  using Tile = Q4KTile<NB, T, 2 * ITERS>;
+template <int NB, int T>
+__global__ __launch_bounds__(T) void k_gateup(DecodeArgs a, LayerArgs L, int ffn) {
+  using Tile = Q4KTile<NB, T, 2>;  // iteration 0: gate rows, 1: up rows
   constexpr int K = NB * 256;
-  constexpr int ROWS = Tile::ROWS / 2;
-  __shared__ __attribute__((aligned(16))) float xl[NB * 4 * kXPitch];
-  __shared__ float red[Tile::ROWS * NB];
+  constexpr int RPI = Tile::RPI;
+  __shared__ __attribute__((aligned(16))) uint32_t dl[NB * 4 * kDPitch];
+  __shared__ float red[2][Tile::ROWS * NB];
   __shared__ float bred[T / 64];
-  const int j0 = (int)blockIdx.x * ROWS;
   const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
+  const int ntiles = ffn / RPI;  // RPI divides ffn (checked on the host)
+  auto rows_of = [&](int tile) {
+    return [=](int rl) -> const uint8_t * {
+      if (tile >= ntiles) return nullptr;
+      const int j = tile * RPI + (rl < RPI ? rl : rl - RPI);
+      return (rl < RPI ? L.wgate : L.wup) + (size_t)j * row_bytes;
+    };
+  };
+  int t = (int)blockIdx.x;
   ProRegs<K, T> pr;
   pro_load<K, T, Pro::Resid>(a, a.hid, a.o, L.g_post_attn, L.g_pre_ffn, pr);
-  Tile tile;
-  tile.load([&](int rl) -> const uint8_t * {
-    return rl < ROWS ? L.wgate + (size_t)(j0 + rl) * row_bytes : L.wup + (size_t)(j0 + rl - ROWS) * row_bytes;
-  }, L.wgate);
-  pro_finish<K, T, Pro::Resid>(a, pr, a.x2, xl, bred);
+  Tile cur, nxt;
+  cur.load(rows_of(t), L.wgate);
+  pro_finish<K, T, Pro::Resid, true>(a, pr, a.x2, dl, bred);
   __syncthreads();
-  ChunkX cx;
-  chunkx_from_lds(xl, tile.slot, cx);
-  tile.compute(cx, red);
-  __syncthreads();
-  for (int i = threadIdx.x; i < ROWS; i += T) {
-    const float g = reduce_row<NB>(red, i);
-    const float u = reduce_row<NB>(red, ROWS + i);
-    a.h[j0 + i] = mul_nc(gelu_tanh(g), u);
+  ChunkD cx;
+  chunkd_from_lds(dl, cur.slot, cx);
+  int buf = 0;
+  for (; t < ntiles; t += (int)gridDim.x) {
+    nxt.load(rows_of(t + (int)gridDim.x), L.wgate);
+    cur.compute_digits(cx, red[buf]);
+    __syncthreads();
+    for (int i = threadIdx.x; i < RPI; i += T) {
+      const float g = reduce_row<NB>(red[buf], i);
+      const float u = reduce_row<NB>(red[buf], RPI + i);
+      a.h[t * RPI + i] = mul_nc(gelu_tanh(g), u);
+    }
+    buf ^= 1;
+    cur = nxt;
   }
 }
 
@@ -204,6 +220,39 @@ __global__ __launch_bounds__(T) void k_gemv(const uint8_t *__restrict__ W, const
   tile.compute(cx, red);
   __syncthreads();
   for (int i = threadIdx.x; i < Tile::ROWS; i += T) y[row0 + i] = reduce_row<NB>(red, i);
+}
+
+// Persistent, double-buffered variant (the K=10240 down projection).
+template <int NB, int T>
+__global__ __launch_bounds__(T) void k_gemv_persist(const uint8_t *__restrict__ W, const float *__restrict__ x,
+                                                    float *__restrict__ y, int n) {
+  using Tile = Q4KTile<NB, T, 1>;
+  constexpr int RPI = Tile::RPI;
+  __shared__ __attribute__((aligned(16))) float xl[NB * 4 * kXPitch];
+  __shared__ float red[2][RPI * NB];
+  const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
+  const int ntiles = n / RPI;  // RPI divides n (checked on the host)
+  auto rows_of = [&](int tile) {
+    return [=](int rl) -> const uint8_t * { return tile < ntiles ? W + (size_t)(tile * RPI + rl) * row_bytes : nullptr; };
+  };
+  int t = (int)blockIdx.x;
+  XRegs<NB * 256, T> xr;
+  x_load<NB * 256, T>(x, xr);
+  Tile cur, nxt;
+  cur.load(rows_of(t), W);
+  x_store<NB * 256, T>(xr, xl);
+  __syncthreads();
+  ChunkX cx;
+  chunkx_from_lds(xl, cur.slot, cx);
+  int buf = 0;
+  for (; t < ntiles; t += (int)gridDim.x) {
+    nxt.load(rows_of(t + (int)gridDim.x), W);
+    cur.compute(cx, red[buf]);
+    __syncthreads();
+    for (int i = threadIdx.x; i < RPI; i += T) y[t * RPI + i] = reduce_row<NB>(red[buf], i);
+    buf ^= 1;
+    cur = nxt;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -251,18 +300,24 @@ RT_DEV void norm_rope_head(const float *__restrict__ src, const float *__restric
 
 template <int D, int G>
 __global__ __launch_bounds__(256) void k_attn(DecodeArgs a, LayerArgs L) {
-  constexpr int MAXC = kAttnMaxChunk;
+  constexpr int KC = kAttnChunkKeys;       // keys per chunk (at most)
+  constexpr int DL = D / 16;               // score pass: 16 lanes per key, DL dims per lane
+  constexpr int VL = D / 4;                // value pass: lanes per key row (float4 each)
+  constexpr int VG = 256 / VL;             // key groups in the value pass
+  constexpr int VK = KC / VG;              // keys per thread in the value pass
+  static_assert(KC == 16 && (D == 128 || D == 256), "chunk layout assumes 16 keys and D in {128, 256}");
   __shared__ float qs[G][D];
   __shared__ float knew[D], vnew[D];
-  __shared__ float sc[G][MAXC];
+  __shared__ float sc[G][KC];
   __shared__ float stat[G][2];
+  __shared__ __attribute__((aligned(16))) float vpart[VG][G][D];
   const int kvh = blockIdx.y, chunk = blockIdx.x, nchunk = gridDim.x;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int pos = a.params[1];
   const int t_end = pos + 1;
   const int t_start = L.window > 0 ? max(0, t_end - L.window) : 0;
   const int t_kv = t_end - t_start;
-  const int csize = (t_kv + nchunk - 1) / nchunk;  // <= MAXC (host sizes the grid)
+  const int csize = (t_kv + nchunk - 1) / nchunk;  // <= KC: the host sizes nchunk for max_seq / window
   const int c0 = t_start + chunk * csize;
   const int c1 = min(c0 + csize, t_end);
   const int n = max(0, c1 - c0);
@@ -270,7 +325,30 @@ __global__ __launch_bounds__(256) void k_attn(DecodeArgs a, LayerArgs L) {
   const int kvd = a.n_kv_heads * D;
   const float pos_fs = (float)pos * L.rope_fs;
 
-  // 1. rotations (waves 0..G-1: q heads; the next wave: k, and v copy)
+  // 0. issue this chunk's K and V loads first (branch-free, clamped to a valid
+  //    row); they are consumed after the q/k rotations below.  Row `pos` is
+  //    replaced by the freshly rotated k / copied v.
+  const int kg = lane >> 4, sub = lane & 15;
+  const int kidx = wave * 4 + kg;                      // this lane's key in the score pass
+  const int kc_row = min(c0 + kidx, max(c1 - 1, 0));
+  float kv[DL];
+  {
+    const float4 *kp = reinterpret_cast<const float4 *>(L.kc + (size_t)kc_row * kvd + (size_t)kvh * D + sub * DL);
+#pragma unroll
+    for (int j = 0; j < DL / 4; ++j) {
+      const float4 v4 = kp[j];
+      kv[4 * j] = v4.x; kv[4 * j + 1] = v4.y; kv[4 * j + 2] = v4.z; kv[4 * j + 3] = v4.w;
+    }
+  }
+  const int vgrp = threadIdx.x / VL, vl = threadIdx.x % VL;
+  float4 vv[VK];
+#pragma unroll
+  for (int j = 0; j < VK; ++j) {
+    const int row = min(c0 + vgrp + VG * j, max(c1 - 1, 0));
+    vv[j] = *reinterpret_cast<const float4 *>(L.vc + (size_t)row * kvd + (size_t)kvh * D + 4 * vl);
+  }
+
+  // 1. rotations (waves 0..G-1: q heads; the next wave: k, and the v copy)
   if (wave < G) {
     norm_rope_head<D>(a.q + (size_t)(kvh * G + wave) * D, L.g_q, L.rope_den, pos_fs, a.eps, qs[wave]);
   }
@@ -284,56 +362,28 @@ __global__ __launch_bounds__(256) void k_attn(DecodeArgs a, LayerArgs L) {
     L.vc[(size_t)pos * kvd + (size_t)kvh * D + threadIdx.x] = vnew[threadIdx.x];
   }
 
-  // 2. scores: a wave takes 4 keys per step, 16 lanes per key, D/16 dims per lane
-  constexpr int DL = D / 16;
-  const int kg = lane >> 4, sub = lane & 15;
-  float qreg[G][DL];
+  // 2. scores s = (q.k) * scale, 16 lanes per key
+  if (c0 + kidx == pos) {
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+    for (int j = 0; j < DL; ++j) kv[j] = knew[sub * DL + j];
+  }
 #pragma unroll
-    for (int j = 0; j < DL; ++j) qreg[g][j] = qs[g][sub * DL + j];
-  for (int base = 0; base < n; base += 16) {
-    const int ci = base + wave * 4 + kg;  // key index within chunk
-    const int c = c0 + ci;
-    const bool ok = ci < n;
-    float kv[DL];
-    if (ok && c == pos) {
+  for (int g = 0; g < G; ++g) {
+    float d = 0.f;
 #pragma unroll
-      for (int j = 0; j < DL; ++j) kv[j] = knew[sub * DL + j];
-    } else if (ok) {
-      const float4 *kp = reinterpret_cast<const float4 *>(L.kc + (size_t)c * kvd + (size_t)kvh * D + sub * DL);
-#pragma unroll
-      for (int j = 0; j < DL / 4; ++j) {
-        const float4 v4 = kp[j];
-        kv[4 * j] = v4.x; kv[4 * j + 1] = v4.y; kv[4 * j + 2] = v4.z; kv[4 * j + 3] = v4.w;
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < DL; ++j) kv[j] = 0.f;
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float d = 0.f;
-#pragma unroll
-      for (int j = 0; j < DL; ++j) d += qreg[g][j] * kv[j];
-      d = row16_sum(d);
-      if (ok && sub == 0) sc[g][ci] = d * a.attn_scale;
-    }
+    for (int j = 0; j < DL; ++j) d += qs[g][sub * DL + j] * kv[j];
+    d = row16_sum(d);
+    if (kidx < n && sub == 0) sc[g][kidx] = d * a.attn_scale;
   }
   __syncthreads();
 
-  // 3. chunk softmax statistics (wave g handles head g)
+  // 3. chunk softmax statistics (wave g handles head g; n <= 16 keys)
   if (wave < G) {
-    float m = -INFINITY;
-    for (int i = lane; i < n; i += 64) m = fmaxf(m, sc[wave][i]);
-    m = wave_max(m);
-    float l = 0.f;
-    for (int i = lane; i < n; i += 64) {
-      const float p = expf(sc[wave][i] - m);
-      sc[wave][i] = p;
-      l += p;
-    }
-    l = wave_sum(l);
+    const float s_ = lane < n ? sc[wave][lane] : -INFINITY;
+    const float m = wave_max(s_);
+    const float p = lane < n ? expf(s_ - m) : 0.f;
+    const float l = wave_sum(p);
+    if (lane < n) sc[wave][lane] = p;
     if (lane == 0) {
       stat[wave][0] = m;
       stat[wave][1] = l;
@@ -341,36 +391,34 @@ __global__ __launch_bounds__(256) void k_attn(DecodeArgs a, LayerArgs L) {
   }
   __syncthreads();
 
-  // 4. weighted V (thread per dimension)
-  for (int d = threadIdx.x; d < D; d += 256) {
-    float o[G];
+  // 4. o = sum_c p_c v_c: thread owns 4 dimensions of VK keys, then the VG
+  //    key groups are summed through LDS
+  float4 o[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) o[g] = 0.f;
-    const float *vp = L.vc + (size_t)kvh * D + d;
-    int i = 0;
-    for (; i + 4 <= n; i += 4) {
-      float v4[4];
+  for (int g = 0; g < G; ++g) o[g] = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int c = c0 + i + u;
-        v4[u] = c == pos ? vnew[d] : vp[(size_t)c * kvd];
+  for (int j = 0; j < VK; ++j) {
+    const int ki = vgrp + VG * j;
+    float4 v4 = vv[j];
+    if (c0 + ki == pos) v4 = *reinterpret_cast<const float4 *>(&vnew[4 * vl]);
+    if (ki < n) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float p = sc[g][ki];
+        o[g].x += p * v4.x; o[g].y += p * v4.y; o[g].z += p * v4.z; o[g].w += p * v4.w;
       }
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int g = 0; g < G; ++g) o[g] += sc[g][i + u] * v4[u];
     }
-    for (; i < n; ++i) {
-      const int c = c0 + i;
-      const float vv = c == pos ? vnew[d] : vp[(size_t)c * kvd];
+  }
 #pragma unroll
-      for (int g = 0; g < G; ++g) o[g] += sc[g][i] * vv;
-    }
+  for (int g = 0; g < G; ++g) *reinterpret_cast<float4 *>(&vpart[vgrp][g][4 * vl]) = o[g];
+  __syncthreads();
+  for (int e = threadIdx.x; e < G * D; e += 256) {
+    const int g = e / D, d = e % D;
+    float acc = 0.f;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const int h = kvh * G + g;
-      a.part_o[((size_t)h * nchunk + chunk) * D + d] = o[g];
-    }
+    for (int q = 0; q < VG; ++q) acc += vpart[q][g][d];
+    const int h = kvh * G + g;
+    a.part_o[((size_t)h * nchunk + chunk) * D + d] = acc;
   }
   if (threadIdx.x < G) {
     const int h = kvh * G + threadIdx.x;
@@ -387,9 +435,9 @@ __global__ __launch_bounds__(256) void k_attn(DecodeArgs a, LayerArgs L) {
 template <int D>
 __global__ __launch_bounds__(256) void k_attn_combine(DecodeArgs a, int nchunk) {
   __shared__ float wts[kAttnMaxChunks];
-  __shared__ float part[4][64];
+  __shared__ float part[8][32];
   __shared__ float bred[4];
-  const int h = blockIdx.x, d0 = blockIdx.y * 64;
+  const int h = blockIdx.x, d0 = blockIdx.y * 32;
   const float *pm = a.part_m + (size_t)h * nchunk;
   const float *pl = a.part_l + (size_t)h * nchunk;
   float m = -INFINITY;
@@ -398,7 +446,6 @@ __global__ __launch_bounds__(256) void k_attn_combine(DecodeArgs a, int nchunk) 
   if ((threadIdx.x & 63) == 0) bred[threadIdx.x >> 6] = m;
   __syncthreads();
   const float M = fmaxf(fmaxf(bred[0], bred[1]), fmaxf(bred[2], bred[3]));
-  __syncthreads();
   float l = 0.f;
   for (int i = threadIdx.x; i < nchunk; i += 256) {
     const float mi = pm[i];
@@ -406,19 +453,26 @@ __global__ __launch_bounds__(256) void k_attn_combine(DecodeArgs a, int nchunk) 
     wts[i] = w;
     l += pl[i] * w;
   }
-  const float L = block_sum<256>(l, bred);  // also orders the wts writes
-  const int cg = threadIdx.x >> 6, dl = threadIdx.x & 63;
+  const float L = block_sum<256>(l, bred);  // its barriers also publish wts
+  const int cg = threadIdx.x >> 5, dl = threadIdx.x & 31;
   const float *po = a.part_o + (size_t)h * nchunk * D + d0 + dl;
-  float acc0 = 0.f, acc1 = 0.f;
+  float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
   int i = cg;
-  for (; i + 4 < nchunk; i += 8) {
+  for (; i + 24 < nchunk; i += 32) {
     acc0 += po[(size_t)i * D] * wts[i];
-    acc1 += po[(size_t)(i + 4) * D] * wts[i + 4];
+    acc1 += po[(size_t)(i + 8) * D] * wts[i + 8];
+    acc2 += po[(size_t)(i + 16) * D] * wts[i + 16];
+    acc3 += po[(size_t)(i + 24) * D] * wts[i + 24];
   }
-  for (; i < nchunk; i += 4) acc0 += po[(size_t)i * D] * wts[i];
-  part[cg][dl] = acc0 + acc1;
+  for (; i < nchunk; i += 8) acc0 += po[(size_t)i * D] * wts[i];
+  part[cg][dl] = (acc0 + acc1) + (acc2 + acc3);
   __syncthreads();
-  if (cg == 0) a.attn[(size_t)h * D + d0 + dl] = (part[0][dl] + part[1][dl] + part[2][dl] + part[3][dl]) / L;
+  if (cg == 0) {
+    float s = 0.f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) s += part[q][dl];
+    a.attn[(size_t)h * D + d0 + dl] = s / L;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -500,10 +554,19 @@ static void launch_qkv(Launch &l, const DecodeArgs &a, const LayerArgs &L, const
   l.check();
 }
 
-template <int NB, int T, int ITERS>
-static void launch_gateup(Launch &l, const DecodeArgs &a, const LayerArgs &L, int ffn) {
-  constexpr int ROWS = Q4KTile<NB, T, ITERS>::ROWS;
-  hipLaunchKernelGGL((k_gateup<NB, T, ITERS>), dim3(ffn / ROWS), dim3(T), 0, l.s, a, L);
+template <int NB, int T>
+static void launch_gateup(Launch &l, const DecodeArgs &a, const LayerArgs &L, int ffn, int grid) {
+  constexpr int RPI = T / (NB * 4);
+  const int ntiles = ffn / RPI;
+  hipLaunchKernelGGL((k_gateup<NB, T>), dim3(grid < ntiles ? grid : ntiles), dim3(T), 0, l.s, a, L, ffn);
+  l.check();
+}
+
+template <int NB, int T>
+static void launch_gemv_persist(Launch &l, const uint8_t *W, const float *x, float *y, int n, int grid) {
+  constexpr int RPI = T / (NB * 4);
+  const int ntiles = n / RPI;
+  hipLaunchKernelGGL((k_gemv_persist<NB, T>), dim3(grid < ntiles ? grid : ntiles), dim3(T), 0, l.s, W, x, y, n);
   l.check();
 }
 
@@ -556,17 +619,17 @@ hipError_t enqueue_decode_step(const DecodeShape &s, const DecodeArgs &a, const 
     const int nchunk = L.window > 0 ? s.nchunk_local : s.nchunk_global;
     if (s.head_dim == 256) {
       launch_attn_d<256>(l, a, L, nchunk, group);
-      hipLaunchKernelGGL((k_attn_combine<256>), dim3(s.n_q_heads, 4), dim3(256), 0, l.s, a, nchunk);
+      hipLaunchKernelGGL((k_attn_combine<256>), dim3(s.n_q_heads, 8), dim3(256), 0, l.s, a, nchunk);
     } else {
       launch_attn_d<128>(l, a, L, nchunk, group);
-      hipLaunchKernelGGL((k_attn_combine<128>), dim3(s.n_q_heads, 2), dim3(256), 0, l.s, a, nchunk);
+      hipLaunchKernelGGL((k_attn_combine<128>), dim3(s.n_q_heads, 4), dim3(256), 0, l.s, a, nchunk);
     }
     l.check();
     if (qd == 2048) launch_gemv<8, 256, 1>(l, L.wo, a.attn, a.o, s.hidden);
     else launch_gemv<2, 256, 1>(l, L.wo, a.attn, a.o, s.hidden);
-    if (big) launch_gateup<10, 320, 1>(l, a, L, s.ffn);
-    else launch_gateup<2, 256, 1>(l, a, L, s.ffn);
-    if (s.ffn == 10240) launch_gemv<40, 320, 4>(l, L.wdown, a.h, a.dn, s.hidden);
+    if (big) launch_gateup<10, 320>(l, a, L, s.ffn, 640);
+    else launch_gateup<2, 256>(l, a, L, s.ffn, 64);
+    if (s.ffn == 10240) launch_gemv_persist<40, 320>(l, L.wdown, a.h, a.dn, s.hidden, 512);
     else launch_gemv<4, 256, 1>(l, L.wdown, a.h, a.dn, s.hidden);
   }
   if (l.err == hipSuccess) {
@@ -587,7 +650,7 @@ bool decode_rows_divisible(const DecodeShape &s, const char **why) {
   const int o_rows = qd == 2048 ? rows_per_iter<8, 256>() : rows_per_iter<2, 256>();
   if (s.hidden % o_rows) return *why = "hidden rows must divide into o-proj tiles", false;
   if (s.ffn % qkv_rows_per_wg) return *why = "ffn rows must divide into gate/up tiles", false;
-  const int d_rows = s.ffn == 10240 ? 4 * rows_per_iter<40, 320>() : rows_per_iter<4, 256>();
+  const int d_rows = s.ffn == 10240 ? rows_per_iter<40, 320>() : rows_per_iter<4, 256>();
   if (s.hidden % d_rows) return *why = "hidden rows must divide into down-proj tiles", false;
   return true;
 }
