@@ -74,6 +74,32 @@ rt_status rt_gemv_bf16_t(const float *a_host, size_t k, const uint16_t *w_host, 
 rt_status rt_weight_cache_clear(void);
 
 /* ---------------------------------------------------------------------------
+ * Q4_K GEMM, C[m,n] = A[m,k] . W[n,k]^T, f32 out (row-major), on the matrix
+ * cores.  Replaces Q4KMat::matmul_q4k_t / matmul_q4k_t_exact
+ * (autograd2.rs:1437-1625), reached from QLinear::forward (qlinear.rs:82-111)
+ * and Linear2::fused_linear (nn2.rs:317-375), and the FLUX GPU GEMM
+ * flux_dequant_q4k + flux_gemm_bt (metal_flux.rs:108-190, gemm_into 809-835).
+ * Products use f16 operands (weights dequantised once, rounded to f16; each
+ * A row and W row carries a power-of-two scale so f16 cannot overflow) with
+ * f32 accumulation: ~2e-4 rel-L2 from the f32 CPU result, where bf16-rounded
+ * weights (the reference's GPU path) give ~1.6e-3.
+ * A is bf16 bits (rt_q4k_gemm_bf16) or f32 (rt_q4k_gemm_f32), row-major
+ * [m,k]; every row of A must start 16-byte aligned (k % 256 == 0 ensures it).
+ * The library keeps a per-thread, per-device workspace of about m*k*2 bytes,
+ * grown on demand (growth synchronises the device).
+ * ------------------------------------------------------------------------- */
+rt_status rt_q4k_gemm_bf16(const uint16_t *a_dev, const void *w_dev, float *c_dev, int64_t m, int64_t n, int64_t k,
+                           void *stream);
+rt_status rt_q4k_gemm_f32(const float *a_dev, const void *w_dev, float *c_dev, int64_t m, int64_t n, int64_t k,
+                          void *stream);
+/* Host drop-in for Q4KMat::matmul_q4k_t_exact (autograd2.rs:1490-1625):
+ * a is [m, k] f32, out receives [m, rows] f32.  m == 1 takes the GEMV path, as
+ * matmul_q4k_t does (autograd2.rs:1440-1443).  Weights are cached like
+ * rt_gemv_q4k_t's. */
+rt_status rt_matmul_q4k_t(const float *a_host, size_t m, size_t k, const uint8_t *blocks_host, size_t rows,
+                          float *out_host);
+
+/* ---------------------------------------------------------------------------
  * Gemma-3 decode engine -- replaces MetalDecodeContext (metal_decode.rs:754-829).
  * One step = embedding lookup, n_layers Gemma-3 blocks (4-norm, GQA with
  * sliding-window / global layers, NeoX RoPE, gated GELU-tanh) and the BF16

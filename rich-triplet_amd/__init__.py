@@ -50,6 +50,9 @@ _SIGNATURES = {
     "rt_gemv_q4k_t": (_i32, [_vp, _sz, _vp, _sz, _vp]),
     "rt_gemv_bf16_t": (_i32, [_vp, _sz, _vp, _sz, _vp]),
     "rt_weight_cache_clear": (_i32, []),
+    "rt_q4k_gemm_bf16": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "rt_q4k_gemm_f32": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "rt_matmul_q4k_t": (_i32, [_vp, _sz, _sz, _vp, _sz, _vp]),
     "rt_decode_create": (_i32, [_vp, C.POINTER(_vp)]),
     "rt_decode_destroy": (_i32, [_vp]),
     "rt_decode_set_layer": (_i32, [_vp, _i32, _vp, _i32]),
@@ -128,6 +131,18 @@ def bf16_gemv(w, x, y, n: int, k: int, stream=None) -> None:
     check(lib().rt_bf16_gemv(_p(w), _p(x), _p(y), n, k, _stream(stream)))
 
 
+def q4k_gemm(a, w, c, m: int, n: int, k: int, stream=None) -> None:
+    """C[m,n] = A[m,k] . W[n,k]^T on device; A is a bf16 or f32 tensor (bf16 may be
+    passed as int16/uint16 bits), W packed Q4_K bytes, C f32."""
+    import torch
+    if a.dtype in (torch.bfloat16, torch.int16, getattr(torch, "uint16", torch.int16)):
+        check(lib().rt_q4k_gemm_bf16(_p(a), _p(w), _p(c), m, n, k, _stream(stream)))
+    elif a.dtype == torch.float32:
+        check(lib().rt_q4k_gemm_f32(_p(a), _p(w), _p(c), m, n, k, _stream(stream)))
+    else:
+        raise TypeError(f"q4k_gemm: activations must be bfloat16 or float32, got {a.dtype}")
+
+
 # ---------------------------------------------------------------------------
 # host-pointer API (numpy arrays), mirrors metal_ops::metal_gemv_*_t
 # ---------------------------------------------------------------------------
@@ -146,6 +161,19 @@ def gemv_bf16_t(a, w, rows: int):
     w = np.ascontiguousarray(w, np.uint16)
     out = np.empty(rows, np.float32)
     check(lib().rt_gemv_bf16_t(a.ctypes.data, a.size, w.ctypes.data, rows, out.ctypes.data))
+    return out
+
+
+def matmul_q4k_t(a, blocks, rows: int):
+    """Q4KMat::matmul_q4k_t_exact: a [m, k] f32 (numpy) -> [m, rows] f32."""
+    import numpy as np
+    a = np.ascontiguousarray(a, np.float32)
+    if a.ndim == 1:
+        a = a.reshape(1, -1)
+    blocks = np.ascontiguousarray(blocks, np.uint8)
+    m, k = a.shape
+    out = np.empty((m, rows), np.float32)
+    check(lib().rt_matmul_q4k_t(a.ctypes.data, m, k, blocks.ctypes.data, rows, out.ctypes.data))
     return out
 
 

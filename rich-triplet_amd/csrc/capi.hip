@@ -87,6 +87,39 @@ rt_status rt_bf16_gemv(const uint16_t *w, const float *x, float *y, int64_t n, i
 
 }  // extern "C"
 
+namespace {
+rt_status gemm_workspace(size_t bytes, void **out);
+
+rt_status q4k_gemm_entry(const char *who, const void *a, bool a_bf16, const void *w, float *c, int64_t m, int64_t n,
+                         int64_t k, void *stream) {
+  if (m <= 0 || n <= 0 || k <= 0)
+    return set_error(RT_EINVAL, "%s: m=%lld n=%lld k=%lld must be positive", who, (long long)m, (long long)n,
+                     (long long)k);
+  if (k % 256 != 0) return set_error(RT_EINVAL, "%s: k=%lld must be a multiple of 256", who, (long long)k);
+  if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX) return set_error(RT_EINVAL, "%s: m, n or k exceeds int32", who);
+  if (!a || !w || !c) return set_error(RT_EINVAL, "%s: null pointer", who);
+  if (!aligned16(a) || !aligned16(w)) return set_error(RT_EINVAL, "%s: a and w must be 16-byte aligned", who);
+  if ((reinterpret_cast<uintptr_t>(c) & 3u) != 0) return set_error(RT_EINVAL, "%s: c must be 4-byte aligned", who);
+  void *ws = nullptr;
+  rt_status st = gemm_workspace(q4k_gemm_workspace_bytes((int)m, (int)n, (int)k), &ws);
+  if (st != RT_OK) return st;
+  return hip_error(launch_q4k_gemm(a, a_bf16, w, c, (int)m, (int)n, (int)k, ws, (hipStream_t)stream), who);
+}
+}  // namespace
+
+extern "C" {
+
+rt_status rt_q4k_gemm_bf16(const uint16_t *a, const void *w, float *c, int64_t m, int64_t n, int64_t k,
+                           void *stream) {
+  return q4k_gemm_entry("rt_q4k_gemm_bf16", a, true, w, c, m, n, k, stream);
+}
+
+rt_status rt_q4k_gemm_f32(const float *a, const void *w, float *c, int64_t m, int64_t n, int64_t k, void *stream) {
+  return q4k_gemm_entry("rt_q4k_gemm_f32", a, false, w, c, m, n, k, stream);
+}
+
+}  // extern "C"
+
 // ---------------------------------------------------------------------------
 // Host-pointer drop-ins with a weight cache keyed by (host pointer, bytes).
 // ---------------------------------------------------------------------------
@@ -150,6 +183,36 @@ rt_status stage(size_t bytes, void **out) {
   return RT_OK;
 }
 
+// GEMM workspace (A in f16 plus row exponents), one per (thread, device),
+// grow-only.  Growth synchronises the device before freeing the old buffer,
+// which kernels queued by earlier calls may still read.
+struct GemmWorkspace {
+  void *buf = nullptr;
+  size_t cap = 0;
+};
+thread_local std::map<int, GemmWorkspace> g_gemm_ws;
+
+rt_status gemm_workspace(size_t bytes, void **out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_error(e, "hipGetDevice");
+  GemmWorkspace &w = g_gemm_ws[dev];
+  if (w.cap < bytes) {
+    if (w.buf) {
+      e = hipDeviceSynchronize();
+      if (e != hipSuccess) return hip_error(e, "gemm workspace sync");
+      (void)hipFree(w.buf);
+    }
+    w.buf = nullptr;
+    w.cap = 0;
+    e = hipMalloc(&w.buf, bytes);
+    if (e != hipSuccess) return hip_error(e, "gemm workspace hipMalloc");
+    w.cap = bytes;
+  }
+  *out = w.buf;
+  return RT_OK;
+}
+
 template <typename LaunchFn>
 rt_status host_gemv(const char *who, const float *a, size_t k, const void *w_host, size_t w_bytes, size_t rows,
                     float *out, LaunchFn launch) {
@@ -191,6 +254,31 @@ rt_status rt_gemv_bf16_t(const float *a, size_t k, const uint16_t *w, size_t row
   return host_gemv("rt_gemv_bf16_t", a, k, w, bytes, rows, out, [&](void *wd, float *x, float *y) {
     return launch_bf16_gemv(static_cast<const uint16_t *>(wd), x, y, (int)rows, (int)k, nullptr);
   });
+}
+
+rt_status rt_matmul_q4k_t(const float *a, size_t m, size_t k, const uint8_t *blocks, size_t rows, float *out) {
+  if (!a || !blocks || !out) return set_error(RT_EINVAL, "rt_matmul_q4k_t: null pointer");
+  if (m == 0 || k == 0 || rows == 0 || k % 256 != 0 || k > INT32_MAX || rows > INT32_MAX || m > INT32_MAX)
+    return set_error(RT_EINVAL, "rt_matmul_q4k_t: m=%zu k=%zu rows=%zu (k must be a positive multiple of 256)", m, k,
+                     rows);
+  if (m == 1) return rt_gemv_q4k_t(a, k, blocks, rows, out);
+  void *wdev = nullptr, *buf = nullptr, *ws = nullptr;
+  const size_t wbytes = rows * (k / 256) * 144;
+  rt_status st = cached_upload(blocks, wbytes, &wdev);
+  if (st != RT_OK) return st;
+  const size_t abytes = (m * k * sizeof(float) + 255) & ~size_t(255);
+  st = stage(abytes + m * rows * sizeof(float), &buf);
+  if (st != RT_OK) return st;
+  st = gemm_workspace(q4k_gemm_workspace_bytes((int)m, (int)rows, (int)k), &ws);
+  if (st != RT_OK) return st;
+  float *ad = static_cast<float *>(buf);
+  float *cd = reinterpret_cast<float *>(static_cast<char *>(buf) + abytes);
+  hipError_t e = hipMemcpy(ad, a, m * k * sizeof(float), hipMemcpyHostToDevice);
+  if (e != hipSuccess) return hip_error(e, "rt_matmul_q4k_t");
+  e = launch_q4k_gemm(ad, false, wdev, cd, (int)m, (int)rows, (int)k, ws, nullptr);
+  if (e != hipSuccess) return hip_error(e, "rt_matmul_q4k_t");
+  e = hipMemcpy(out, cd, m * rows * sizeof(float), hipMemcpyDeviceToHost);
+  return hip_error(e, "rt_matmul_q4k_t");
 }
 
 rt_status rt_weight_cache_clear(void) {

@@ -13,5 +13,10 @@ hipError_t launch_q4k_gemv(const void *W, const float *x, float *y, int N, int K
 hipError_t launch_q4k_gemv_generic(const void *W, const float *x, float *y, int N, int K, hipStream_t s);
 int q4k_gemv_rows_per_wg(int N, int K);
 hipError_t launch_bf16_gemv(const uint16_t *W, const float *x, float *y, int N, int K, hipStream_t s);
+// Q4_K GEMM C[M,N] = A[M,K] . W[N,K]^T; A bf16 bits (a_bf16) or f32; ws holds
+// q4k_gemm_workspace_bytes(M, N, K) bytes of device scratch.
+size_t q4k_gemm_workspace_bytes(int M, int N, int K);
+hipError_t launch_q4k_gemm(const void *a, bool a_bf16, const void *w, float *c, int M, int N, int K, void *ws,
+                           hipStream_t s);
 
 }  // namespace rt

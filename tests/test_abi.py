@@ -54,5 +54,27 @@ def test_null_and_misaligned_pointers_are_rejected(rt):
         rt.check(L.rt_gemv_bf16_t(addr, 7, addr, 4, addr))
 
 
+@pytest.mark.parametrize("m,n,k,what", [(0, 16, 256, "positive"), (4, 16, 300, "multiple of 256"),
+                                        (4, -1, 256, "positive"), (2 ** 31, 16, 256, "int32")])
+def test_q4k_gemm_rejects_bad_shapes_before_launch(rt, m, n, k, what):
+    buf = (C.c_uint8 * 64)()
+    addr = (C.addressof(buf) + 15) & ~15
+    for fn in (rt.lib().rt_q4k_gemm_bf16, rt.lib().rt_q4k_gemm_f32):
+        assert fn(addr, addr, addr, m, n, k, None) == rt.RT_EINVAL
+        assert what in rt.lib().rt_last_error().decode()
+
+
+def test_q4k_gemm_rejects_null_and_misaligned(rt):
+    L = rt.lib()
+    buf = (C.c_uint8 * 64)()
+    addr = (C.addressof(buf) + 15) & ~15
+    assert L.rt_q4k_gemm_bf16(None, addr, addr, 4, 16, 256, None) == rt.RT_EINVAL
+    assert L.rt_q4k_gemm_f32(addr + 4, addr, addr, 4, 16, 256, None) == rt.RT_EINVAL
+    assert "aligned" in L.rt_last_error().decode()
+    assert L.rt_q4k_gemm_f32(addr, addr, addr + 2, 4, 16, 256, None) == rt.RT_EINVAL
+    assert L.rt_matmul_q4k_t(None, 2, 256, None, 4, None) == rt.RT_EINVAL
+    assert L.rt_matmul_q4k_t(addr, 2, 100, addr, 4, addr) == rt.RT_EINVAL
+
+
 def test_zero_block_dequant_is_a_no_op(rt):
     assert rt.lib().rt_q4k_dequant_f32(None, 0, None, None) == rt.RT_OK
