@@ -4,10 +4,11 @@
 // dequantise a band of rows to f32 and sgemm it) and the FLUX GPU path
 // flux_dequant_q4k + flux_gemm_bt (metal_flux.rs:108-190, dequantise the whole
 // weight to bfloat scratch, then a 64x64 simdgroup GEMM).  Here the weight
-// stays packed in HBM (144-byte super-blocks) and each workgroup dequantises
-// only the 64-column chunk it is about to multiply, into LDS.
+// stays packed in HBM (144-byte super-blocks): each workgroup copies the
+// packed bytes of the chunk it is about to multiply into LDS and every lane
+// dequantises its own column into registers.
 //
-// Arithmetic: v_mfma_f32_16x16x32_f16, f32 accumulation.
+// Arithmetic: v_mfma_f32_32x32x16_f16, f32 accumulation.
 //   Weights rounded to bf16 (8-bit significand, what the reference's GPU path
 //   does) land ~1.6e-3 rel-L2 away from the f32 CPU result at K=2560; rounded
 //   to f16 (11-bit significand) they land ~2e-4 away.  bf16 activations are
@@ -20,7 +21,7 @@
 // Dequantisation of one weight: w = (d*sv)*q - (dmin*mv) (autograd2.rs:1359-1363).
 // v_perm builds the f16 bit pattern 0x64qq = 1024 + q from a nibble, and one
 // v_fma_mix computes s*(1024+q) - (m + 1024*s) in f32 with a single rounding
-// to f16: two VALU operations per weight.
+// to f16: 1.5 VALU operations per weight.
 #include <hip/hip_runtime.h>
 
 #include "rt_device.hpp"
@@ -30,17 +31,15 @@ namespace rt {
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
 // Native vectors for staging registers: HIP's uint4 is a union-wrapped struct
 // whose copies become memcpys, which LLVM turns back into global reloads.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBK = 64;          // K per pipeline stage = one Q4_K chunk (32 qs bytes, 2 sub-blocks)
-constexpr int kPitch = kBK + 8;  // halves per LDS row: 144 bytes keeps 8 consecutive rows on distinct banks
+constexpr int kBK = 64;  // K per pipeline stage = one Q4_K chunk (32 qs bytes, 2 sub-blocks)
 
 // ---------------------------------------------------------------------------
 // Prep: A -> f16 with a per-row exponent; W row exponents from block headers.
-// Workgroups [0, M) take one A row each, the rest 256 W rows each.
+// Workgroups [0, M) take one A row each, the rest four W rows each.
 // ---------------------------------------------------------------------------
 RT_DEV int f16_exponent_for(float bound) {
   // 2^-e * bound in [2^14, 2^15); 0 for zero / non-finite bounds (those propagate).
@@ -101,196 +100,479 @@ __global__ __launch_bounds__(256) void k_gemm_prep(const TA *__restrict__ a, _Fl
       *reinterpret_cast<uint4 *>(out + g * 8) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
     }
   } else {
-    const int n = (b - M) * 256 + (int)threadIdx.x;
+    // One wave per W row, one block header per lane (a strided walk by a
+    // single thread is latency-bound at K = 12288).
+    const int n = (b - M) * 4 + (int)(threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (n >= N) return;
     const int kb = K / 256;
-    const uint8_t *blk = w + (size_t)n * kb * kQ4KBlockBytes;
+    const uint8_t *row = w + (size_t)n * kb * kQ4KBlockBytes;
     float bound = 0.f;  // |w| <= max(15*63*|d|, 63*|dmin|)
-    for (int i = 0; i < kb; ++i) {
-      const uint32_t h = *reinterpret_cast<const uint32_t *>(blk + (size_t)i * kQ4KBlockBytes);
+    for (int i = lane; i < kb; i += 64) {
+      const uint32_t h = *reinterpret_cast<const uint32_t *>(row + (size_t)i * kQ4KBlockBytes);
       bound = fmaxf(bound, fmaxf(945.f * fabsf(half_bits_to_f32(h & 0xFFFFu)), 63.f * fabsf(half_bits_to_f32(h >> 16))));
     }
-    ew[n] = f16_exponent_for(bound);
+    bound = wave_max(bound);
+    if (lane == 0) ew[n] = f16_exponent_for(bound);
   }
 }
 
 // ---------------------------------------------------------------------------
-// Main kernel.  256 threads = WGM x WGN waves; the workgroup owns a BM x BN
-// tile of C and walks K in 64-wide stages, double-buffered in LDS:
-//   registers <- global (stage s+1)  |  MFMA on LDS buffer s%2
-//   dequantise registers -> LDS buffer (s+1)%2;  one barrier per stage.
-// Loads are unconditional at clamped indices (rows past M / N repeat the last
-// row; their results are never stored) so the loop has no branches.
+// Matrix-core kernels.  Both use v_mfma_f32_32x32x16_f16 (lane l: A row / B
+// column l%32, k group g = l/32, 8 halves each) and the same K order inside a
+// 64-wide chunk (A and B agree on it, so the sum is unchanged):
+//   lane group g holds qs bytes [16g, 16g+16) of the chunk's 32; k-step t
+//   (0..3) covers chunk-local k = 16g + 8(t&1) + 32(t>>1) + [0, 8): t < 2 are
+//   the low nibbles (sub-block 2c), t >= 2 the high nibbles of the same
+//   bytes (sub-block 2c+1).
+// Operands reach LDS by global_load_lds_dwordx4 (no VGPRs, no ds_write); each
+// ring slot is its own __shared__ variable.  Every lane dequantises the qs
+// bytes of its own column straight into the MFMA B operand, so no
+// dequantised weight is written back to LDS.
 // ---------------------------------------------------------------------------
-template <int BM, int BN, int WGM, int WGN>
-struct GemmTile {
-  static_assert(WGM * WGN == 4, "four waves");
-  static constexpr int WM = BM / WGM, WN = BN / WGN;
-  static constexpr int TI = WM / 16, TJ = WN / 16;
-  static_assert(TI * 16 == WM && TJ * 16 == WN, "wave tile must be a multiple of 16");
-  static constexpr int A_LOADS = BM * (kBK / 8) / 256;  // 16-byte A loads per thread per stage
-  static constexpr int B_ITEMS = BN * 2 / 256;          // (row, 16-byte half of the chunk) items per thread
-  static_assert(A_LOADS * 256 == BM * (kBK / 8) && B_ITEMS * 256 == BN * 2, "tile / thread mismatch");
-};
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(1))) void gvoid;
+typedef __attribute__((address_space(3))) void lvoid;
 
-// Two weights from one v_perm result: halves hold 1024+q (or 1024+16q).
-RT_DEV uint32_t dq_pair(uint32_t p, float s, float negc) {
-  const _Float16 h0 = __builtin_bit_cast(_Float16, (uint16_t)(p & 0xFFFFu));
-  const _Float16 h1 = __builtin_bit_cast(_Float16, (uint16_t)(p >> 16));
-  const _Float16 r0 = (_Float16)__builtin_fmaf(s, (float)h0, negc);
-  const _Float16 r1 = (_Float16)__builtin_fmaf(s, (float)h1, negc);
-  return half_bits(r0) | (half_bits(r1) << 16);
+// s_waitcnt with only a vector-memory bound (expcnt / lgkmcnt left open), gfx9 encoding.
+template <int N>
+RT_DEV void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+// s_waitcnt lgkmcnt(0) alone (vmcnt 63 and expcnt 7 mean "no wait").
+RT_DEV void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); }
+// Workgroup barrier that keeps memory operations on their side of it in the
+// compiler (s_barrier alone is a no-memory intrinsic) without the release
+// fence's wait for every outstanding load.
+RT_DEV void wg_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
-template <int BM, int BN, int WGM, int WGN>
-__global__ __launch_bounds__(256) void k_q4k_gemm(const _Float16 *__restrict__ a16, const int *__restrict__ ea,
-                                                  const uint8_t *__restrict__ w, const int *__restrict__ ew,
-                                                  float *__restrict__ c, int M, int N, int K, int tiles_n) {
-  using T = GemmTile<BM, BN, WGM, WGN>;
-  __shared__ __attribute__((aligned(16))) _Float16 lds_a[2][BM * kPitch];
-  __shared__ __attribute__((aligned(16))) _Float16 lds_b[2][BN * kPitch];
+// LDS reads the compiler does not see as LDS reads.  Its wait insertion
+// cannot tell which ring slot an in-flight global_load_lds targets once the
+// loop back-edge merges its state, and would drain every copy (vmcnt(0))
+// before the first read of each block.  The kernel orders the copies itself
+// (explicit vmcnt + barrier per chunk) and waits for these reads with
+// lds_wait, whose register operands keep every consumer after the wait.
+RT_DEV u32x4 lds_read16(const void *p) {
+  u32x4 v;
+  const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a));
+  return v;
+}
+RT_DEV void lds_wait(u32x4 &a, u32x4 &b, u32x4 &c, u32x4 &d) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+}
 
-  const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WGN, wn = wave % WGN;
-  const int m0 = ((int)blockIdx.x / tiles_n) * BM, n0 = ((int)blockIdx.x % tiles_n) * BN;
-  const int kb = K / 256, nstages = K / kBK;
+// Eight f16 weights of one k-step from two qs words (low or high nibbles).
+// v_perm builds halves 1024+q (low nibbles) or 1024+16q (high nibbles), and
+// each v_fma_mix computes f16(s*h - c) from them in f32 with one rounding.
+// The eight v_fma_mix sit in one asm block that ends with two wait states:
+// the compiler's hazard recognizer cannot tell that an asm block is VALU
+// work, so it would not separate it from an MFMA that reads its result
+// (a VALU write followed by an MFMA read of that VGPR needs two wait states).
+template <bool HIGH>
+RT_DEV half8 dq_step(uint32_t w0, uint32_t w1, float s, float negc) {
+  const uint32_t mask = HIGH ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+  const uint32_t a = w0 & mask, b = w1 & mask;
+  const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, a, 0x04010400u);
+  const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u);
+  const uint32_t p2 = __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u);
+  const uint32_t p3 = __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u);
+  uint32_t r0, r1, r2, r3;
+  asm("v_fma_mixlo_f16 %0, %8, %4, %9 op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixhi_f16 %0, %8, %4, %9 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixlo_f16 %1, %8, %5, %9 op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixhi_f16 %1, %8, %5, %9 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixlo_f16 %2, %8, %6, %9 op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixhi_f16 %2, %8, %6, %9 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixlo_f16 %3, %8, %7, %9 op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixhi_f16 %3, %8, %7, %9 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+      "s_nop 1"
+      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
+      : "v"(p0), "v"(p1), "v"(p2), "v"(p3), "v"(s), "v"(negc));
+  const u32x4 r = {r0, r1, r2, r3};
+  return __builtin_bit_cast(half8, r);
+}
 
-  // Per-thread load slots (fixed for the whole K loop).
-  const _Float16 *a_src[T::A_LOADS];
-  int a_dst[T::A_LOADS];
+// ---------------------------------------------------------------------------
+// Eight-wave kernel, 64-wide K per barrier: C tile (128*WGM) x 256, waves
+// WGM (M) x 8/WGM (N), two waves per SIMD.  Wave tile 128 x (256*WGM/8) as
+// 4 x NT tiles of v_mfma_f32_32x32x16_f16; per barrier each wave issues
+// 4 k-steps x 4 x NT MFMAs.
+// Operands reach LDS by global_load_lds_dwordx4 two chunks ahead, in a ring
+// of three slots (the chunk loop is unrolled by three so the slot is a
+// compile-time constant; one __shared__ variable per slot):
+//   A slot: BM rows x 8 x 16-byte segments; physical segment = logical ^
+//           ((row >> 1) & 7), so the 16 rows served together (16 lanes of a
+//           16-byte read per cycle, 64 banks) hit 16 distinct bank groups.
+//   W slot: [part][column] 16-byte pieces for 256 columns: part 0 = qs bytes
+//           0..15 of the chunk, part 1 = qs bytes 16..31, part 2 = header,
+//           part 3 = a second copy of the header that nothing reads: it makes
+//           every wave issue the same two W copies, so the kernel has no
+//           wave-dependent branch and one vmcnt bound.
+// ---------------------------------------------------------------------------
+constexpr int kW8bSlotW = 4 * 256 * 16;  // 16 KB
+
+template <int WGM>
+__global__ __launch_bounds__(512) void k_q4k_gemm_w8b(const _Float16 *__restrict__ a16, const int *__restrict__ ea,
+                                                      const uint8_t *__restrict__ w, const int *__restrict__ ew,
+                                                      float *__restrict__ c, int M, int N, int K, int tiles_m,
+                                                      int tiles_n) {
+  constexpr int BM = 128 * WGM, WN = 8 / WGM, NT = 256 / WN / 32;
+  constexpr int IA = BM / 64;            // A copies per wave per chunk (BM rows x 128 B / 1 KB / 8 waves)
+  constexpr int SLOT_A = BM * 128;       // bytes
+  __shared__ __attribute__((aligned(1024))) uint8_t sa0[SLOT_A], sa1[SLOT_A], sa2[SLOT_A];
+  __shared__ __attribute__((aligned(1024))) uint8_t sw0[kW8bSlotW], sw1[kW8bSlotW], sw2[kW8bSlotW];
+  auto slotA = [&](int i) __attribute__((always_inline)) { return i == 0 ? sa0 : (i == 1 ? sa1 : sa2); };
+  auto slotW = [&](int i) __attribute__((always_inline)) { return i == 0 ? sw0 : (i == 1 ? sw1 : sw2); };
+
+  const int tid = (int)threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, kept in an SGPR
+  const int wm = wave / WN, wn = wave % WN;
+  const int ntiles = tiles_m * tiles_n, per_xcd = (ntiles + 7) / 8;
+  const int bid = (int)blockIdx.x;
+  int tile = (bid & 7) * per_xcd + (bid >> 3);
+  if (ntiles % 8 != 0) tile = bid;
+  const int group = tile / (4 * tiles_n), in_group = tile % (4 * tiles_n);
+  const int gm = min(4, tiles_m - group * 4);
+  const int tm = group * 4 + in_group % gm, tn = in_group / gm;
+  const int m0 = tm * BM, n0 = tn * 256;
+  const int nblocks = K / 256, nchunks = K / kBK;
+  const size_t row_bytes = (size_t)nblocks * kQ4KBlockBytes;
+
+  // A copy i of this wave: slot rows 8*(IA*wave+i) + [0,8); lane -> row
+  // r = 8*(IA*wave+i) + lane/8, physical segment lane%8, logical segment
+  // (lane%8) ^ ((r >> 1) & 7).
+  const _Float16 *a_src[IA];
 #pragma unroll
-  for (int i = 0; i < T::A_LOADS; ++i) {
-    const int idx = tid + 256 * i, r = idx >> 3, c8 = idx & 7;
-    a_src[i] = a16 + (size_t)min(m0 + r, M - 1) * K + c8 * 8;
-    a_dst[i] = r * kPitch + c8 * 8;
+  for (int i = 0; i < IA; ++i) {
+    const int r = 8 * (IA * wave + i) + (lane >> 3);
+    a_src[i] = a16 + (size_t)min(m0 + r, M - 1) * K + 8 * ((lane & 7) ^ ((r >> 1) & 7));
   }
-  const uint8_t *b_row[T::B_ITEMS];
-  int b_half[T::B_ITEMS], b_dst[T::B_ITEMS];
-  float b_pow[T::B_ITEMS];
-#pragma unroll
-  for (int j = 0; j < T::B_ITEMS; ++j) {
-    const int item = tid + 256 * j, r = item >> 1, h = item & 1, n = min(n0 + r, N - 1);
-    b_row[j] = w + (size_t)n * kb * kQ4KBlockBytes;
-    b_half[j] = h;
-    b_dst[j] = r * kPitch + h * 16;
-    b_pow[j] = __builtin_amdgcn_ldexpf(1.0f, -ew[n]);
-  }
+  // W copies: waves 0-3 load parts 0 and 1 (qs), waves 4-7 parts 2 and 3
+  // (header twice), for columns 64*(wave%4) + lane.
+  const uint8_t *w_src = w + (size_t)min(n0 + 64 * (wave & 3) + lane, N - 1) * row_bytes;
+  const int w_part0 = 2 * (wave >> 2);
+  const int w_off0 = wave < 4 ? 0 : -1;  // qs byte offset of part 0 / 1; -1 selects the header
 
-  u32x4 ra[T::A_LOADS], rh[T::B_ITEMS], rq[T::B_ITEMS];
-  auto load_stage = [&](int s) __attribute__((always_inline)) {
+  auto issue = [&](int kc, int slot) __attribute__((always_inline)) {
+    uint8_t *da = slotA(slot), *dw = slotW(slot);
 #pragma unroll
-    for (int i = 0; i < T::A_LOADS; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(a_src[i] + s * kBK);
-#pragma unroll
-    for (int j = 0; j < T::B_ITEMS; ++j) {
-      const uint8_t *blk = b_row[j] + (size_t)(s >> 2) * kQ4KBlockBytes;
-      rh[j] = *reinterpret_cast<const u32x4 *>(blk);
-      rq[j] = *reinterpret_cast<const u32x4 *>(blk + 16 + (s & 3) * 32 + b_half[j] * 16);
-    }
+    for (int i = 0; i < IA; ++i)
+      __builtin_amdgcn_global_load_lds((gvoid *)(a_src[i] + (size_t)kc * kBK), (lvoid *)(da + (IA * wave + i) * 1024),
+                                       16, 0, 0);
+    const uint8_t *blk = w_src + (size_t)(kc >> 2) * kQ4KBlockBytes;
+    const uint8_t *p0 = w_off0 < 0 ? blk : blk + 16 + 32 * (kc & 3);
+    const uint8_t *p1 = w_off0 < 0 ? blk : p0 + 16;
+    const int cw = 64 * (wave & 3) * 16;
+    __builtin_amdgcn_global_load_lds((gvoid *)p0, (lvoid *)(dw + w_part0 * 4096 + cw), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((gvoid *)p1, (lvoid *)(dw + (w_part0 + 1) * 4096 + cw), 16, 0, 0);
   };
-  auto store_stage = [&](int s, int buf) __attribute__((always_inline)) {
+
+  int colw[NT];
+  float bpw[NT];
 #pragma unroll
-    for (int i = 0; i < T::A_LOADS; ++i) *reinterpret_cast<u32x4 *>(&lds_a[buf][a_dst[i]]) = ra[i];
-    const int chunk = s & 3;
+  for (int j = 0; j < NT; ++j) {
+    colw[j] = (256 / WN) * wn + 32 * j + l32;
+    bpw[j] = __builtin_amdgcn_ldexpf(g ? 0.0625f : 1.0f, -ew[min(n0 + colw[j], N - 1)]);
+  }
+
+  floatx16 acc[4][NT];
 #pragma unroll
-    for (int j = 0; j < T::B_ITEMS; ++j) {
-      const float d = half_bits_to_f32(rh[j][0] & 0xFFFFu), dmin = half_bits_to_f32(rh[j][0] >> 16);
-      uint32_t sv0, mv0, sv1, mv1;
-      q4k_scale_min(rh[j][1], rh[j][2], rh[j][3], 2 * chunk, sv0, mv0);
-      q4k_scale_min(rh[j][1], rh[j][2], rh[j][3], 2 * chunk + 1, sv1, mv1);
-      // low nibbles (sub-block 2c): halves are 1024+q;  high (2c+1): 1024+16q.
-      const float s0 = d * (float)sv0 * b_pow[j], mn0 = dmin * (float)mv0 * b_pow[j];
-      const float s1 = d * (float)sv1 * b_pow[j], mn1 = dmin * (float)mv1 * b_pow[j];
-      const float neg0 = -(mn0 + 1024.f * s0), neg1 = -(mn1 + 64.f * s1), s1q = s1 * 0.0625f;
-      uint32_t lo[8], hi[8];
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const uint32_t qw = rq[j][t], ql = qw & 0x0F0F0F0Fu, qh = qw & 0xF0F0F0F0u;
-        lo[2 * t] = dq_pair(__builtin_amdgcn_perm(0x64646464u, ql, 0x04010400u), s0, neg0);
-        lo[2 * t + 1] = dq_pair(__builtin_amdgcn_perm(0x64646464u, ql, 0x04030402u), s0, neg0);
-        hi[2 * t] = dq_pair(__builtin_amdgcn_perm(0x64646464u, qh, 0x04010400u), s1q, neg1);
-        hi[2 * t + 1] = dq_pair(__builtin_amdgcn_perm(0x64646464u, qh, 0x04030402u), s1q, neg1);
+    for (int j = 0; j < NT; ++j) acc[i][j] = floatx16{};
+
+  issue(0, 0);
+  issue(min(1, nchunks - 1), 1);
+  wait_vmcnt<0>();
+  wg_barrier();
+
+  // One chunk: compute from ring slot `slot`, prefetch chunk kc+2 into slot (slot+2)%3.
+  auto chunk = [&](int kc, int slot) __attribute__((always_inline)) {
+    if (kc > 0) {
+      // chunk kc's copies have landed everywhere; chunk kc+1's may stay in flight
+      wait_vmcnt<IA + 2>();
+      wait_lgkmcnt0();
+      wg_barrier();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    issue(min(kc + 2, nchunks - 1), slot == 0 ? 2 : slot - 1);
+    __builtin_amdgcn_sched_barrier(0);
+
+    const uint8_t *pa = slotA(slot), *pw = slotW(slot);
+    auto read_a = [&](int t, u32x4 (&af)[4]) __attribute__((always_inline)) {
+      const int seg = 2 * g + (t & 1) + 4 * (t >> 1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rr = 128 * wm + 32 * i + l32;
+        af[i] = lds_read16(pa + rr * 128 + 16 * (seg ^ ((rr >> 1) & 7)));
       }
-      u32x4 *dl = reinterpret_cast<u32x4 *>(&lds_b[buf][b_dst[j]]);
-      u32x4 *dh = reinterpret_cast<u32x4 *>(&lds_b[buf][b_dst[j] + 32]);
-      dl[0] = u32x4{lo[0], lo[1], lo[2], lo[3]};
-      dl[1] = u32x4{lo[4], lo[5], lo[6], lo[7]};
-      dh[0] = u32x4{hi[0], hi[1], hi[2], hi[3]};
-      dh[1] = u32x4{hi[4], hi[5], hi[6], hi[7]};
+    };
+    u32x4 qv[NT], hw[NT], af[4], afn[4];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      qv[j] = lds_read16(pw + g * 4096 + 16 * colw[j]);
+      hw[j] = lds_read16(pw + 2 * 4096 + 16 * colw[j]);
+    }
+    read_a(0, afn);
+    if constexpr (NT == 2)
+      lds_wait(qv[0], qv[1], hw[0], hw[1]);
+    else
+      lds_wait(qv[0], hw[0], afn[0], afn[1]);
+    const int cc = kc & 3;
+    float sc_lo[NT], sc_hi[NT], nc_lo[NT], nc_hi[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const float d = half_bits_to_f32(hw[j][0] & 0xFFFFu), dmin = half_bits_to_f32(hw[j][0] >> 16);
+      uint32_t sv, mv;
+      q4k_scale_min(hw[j][1], hw[j][2], hw[j][3], 2 * cc + g, sv, mv);
+      const float sfac = d * (float)sv * bpw[j];
+      const float mn = dmin * (float)mv * (bpw[j] * (g ? 16.f : 1.f));
+      const float ncv = -(mn + 1024.f * sfac);
+      const auto s2 = __builtin_amdgcn_permlane32_swap(f32_bits(sfac), f32_bits(sfac), false, false);
+      const auto n2 = __builtin_amdgcn_permlane32_swap(f32_bits(ncv), f32_bits(ncv), false, false);
+      sc_lo[j] = bits_f32(s2[0]), sc_hi[j] = bits_f32(s2[1]);
+      nc_lo[j] = bits_f32(n2[0]), nc_hi[j] = bits_f32(n2[1]);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      half8 bf[NT];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const uint32_t w0 = qv[j][2 * (t & 1)], w1 = qv[j][2 * (t & 1) + 1];
+        bf[j] = t < 2 ? dq_step<false>(w0, w1, sc_lo[j], nc_lo[j]) : dq_step<true>(w0, w1, sc_hi[j], nc_hi[j]);
+      }
+      lds_wait(afn[0], afn[1], afn[2], afn[3]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) af[i] = afn[i];
+      if (t < 3) read_a(t + 1, afn);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, af[i]), bf[j], acc[i][j], 0, 0, 0);
     }
   };
 
-  floatx4 acc[T::TI][T::TJ];
-#pragma unroll
-  for (int i = 0; i < T::TI; ++i)
-#pragma unroll
-    for (int j = 0; j < T::TJ; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-  const int frag_row = lane & 15, frag_k = 8 * (lane >> 4);
-  load_stage(0);
-  store_stage(0, 0);
-  __syncthreads();
-  for (int s = 0; s < nstages; ++s) {
-    const int buf = s & 1;
-    load_stage(min(s + 1, nstages - 1));
-    // Keep the next stage's loads ahead of the MFMAs so their latency overlaps
-    // the matrix work (the scheduler would otherwise sink them to their use).
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      half8 af[T::TI], bf[T::TJ];
-#pragma unroll
-      for (int i = 0; i < T::TI; ++i)
-        af[i] = *reinterpret_cast<const half8 *>(
-            &lds_a[buf][(wm * T::WM + 16 * i + frag_row) * kPitch + 32 * sub + frag_k]);
-#pragma unroll
-      for (int j = 0; j < T::TJ; ++j)
-        bf[j] = *reinterpret_cast<const half8 *>(
-            &lds_b[buf][(wn * T::WN + 16 * j + frag_row) * kPitch + 32 * sub + frag_k]);
-#pragma unroll
-      for (int i = 0; i < T::TI; ++i)
-#pragma unroll
-        for (int j = 0; j < T::TJ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // Unconditional: on the last stage this refills the idle buffer, which is
-    // never read again.  A conditional store lets the compiler sink the loads
-    // above into the branch, after the MFMAs.
-    store_stage(s + 1, buf ^ 1);
-    __syncthreads();
+  int kc = 0;
+  for (; kc + 3 <= nchunks; kc += 3) {
+    chunk(kc, 0);
+    chunk(kc + 1, 1);
+    chunk(kc + 2, 2);
   }
+  if (kc < nchunks) chunk(kc, 0);
+  if (kc + 1 < nchunks) chunk(kc + 1, 1);
 
-  // Epilogue: lane holds C[4*(lane/16)+r][lane%16] of every 16x16 tile.
-  int ecol[T::TJ];
+  // Epilogue: register r of tile (i, j) is C[128wm + 32i + 8(r/4) + 4g + r%4][colw[j]].
+  int ecol[NT];
+  bool cok[NT];
 #pragma unroll
-  for (int j = 0; j < T::TJ; ++j) {
-    const int col = n0 + wn * T::WN + 16 * j + frag_row;
-    ecol[j] = col < N ? ew[col] : 0;
+  for (int j = 0; j < NT; ++j) {
+    const int col = n0 + colw[j];
+    cok[j] = col < N;
+    ecol[j] = cok[j] ? ew[col] : 0;
   }
 #pragma unroll
-  for (int i = 0; i < T::TI; ++i) {
+  for (int i = 0; i < 4; ++i) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = m0 + wm * T::WM + 16 * i + 4 * (lane >> 4) + r;
+    for (int r = 0; r < 16; ++r) {
+      const int row = m0 + 128 * wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
       if (row >= M) continue;
       const int er = ea[row];
-      float *crow = c + (size_t)row * N;
+      float *crow = c + (size_t)row * N + n0;
 #pragma unroll
-      for (int j = 0; j < T::TJ; ++j) {
-        const int col = n0 + wn * T::WN + 16 * j + frag_row;
-        if (col < N) crow[col] = __builtin_amdgcn_ldexpf(acc[i][j][r], er + ecol[j]);
-      }
+      for (int j = 0; j < NT; ++j)
+        if (cok[j]) crow[colw[j]] = __builtin_amdgcn_ldexpf(acc[i][j][r], er + ecol[j]);
     }
   }
 }
 
-template <int BM, int BN, int WGM, int WGN>
-hipError_t launch_tile(const _Float16 *a16, const int *ea, const uint8_t *w, const int *ew, float *c, int M, int N,
-                       int K, hipStream_t s) {
-  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  hipLaunchKernelGGL((k_q4k_gemm<BM, BN, WGM, WGN>), dim3(tiles_m * tiles_n), dim3(256), 0, s, a16, ea, w, ew, c, M,
-                     N, K, tiles_n);
-  return hipGetLastError();
+// ---------------------------------------------------------------------------
+// Half-block kernel: C tile 128 x 256, four waves side by side in N (wave
+// tile 128 x 64 = 4 x 2 tiles of v_mfma_f32_32x32x16_f16), two workgroups
+// per CU so one workgroup's barrier and LDS waits overlap the other's MFMAs.
+//   A (f16): one 64-wide chunk per copy (128 rows x 128 B), two LDS slots,
+//            one chunk ahead.  Row segments XOR-swizzled by (row >> 1) & 7.
+//   W (Q4_K): one half-block per copy (two chunks): for each of the 256
+//            columns the block header and the 64 qs bytes of those chunks,
+//            80 contiguous LDS bytes per column, two slots.  Five adjacent
+//            lanes read one column's bytes, so a copy instruction touches a
+//            few cache lines instead of one line per lane.
+// ---------------------------------------------------------------------------
+constexpr int kHSlotA = 128 * 128;       // bytes
+constexpr int kHSlotW = 256 * 80;        // bytes
+
+__global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restrict__ a16, const int *__restrict__ ea,
+                                                       const uint8_t *__restrict__ w, const int *__restrict__ ew,
+                                                       float *__restrict__ c, int M, int N, int K, int tiles_m,
+                                                       int tiles_n) {
+  __shared__ __attribute__((aligned(1024))) uint8_t sa0[kHSlotA], sa1[kHSlotA];
+  __shared__ __attribute__((aligned(1024))) uint8_t sw0[kHSlotW], sw1[kHSlotW];
+
+  const int tid = (int)threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ntiles = tiles_m * tiles_n, per_xcd = (ntiles + 7) / 8;
+  const int bid = (int)blockIdx.x;
+  int tile = (bid & 7) * per_xcd + (bid >> 3);
+  if (ntiles % 8 != 0) tile = bid;
+  const int group = tile / (4 * tiles_n), in_group = tile % (4 * tiles_n);
+  const int gm = min(4, tiles_m - group * 4);
+  const int tm = group * 4 + in_group % gm, tn = in_group / gm;
+  const int m0 = tm * 128, n0 = tn * 256;
+  const int nblocks = K / 256, nchunks = K / kBK;
+  const size_t row_bytes = (size_t)nblocks * kQ4KBlockBytes;
+
+  // A copy i (0..3) of this wave: rows 8*(4*wave+i) + [0,8); lane -> row
+  // r = 8*(4*wave+i) + lane/8, physical segment lane%8, logical segment
+  // (lane%8) ^ ((r >> 1) & 7).
+  const _Float16 *a_src[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 8 * (4 * wave + i) + (lane >> 3);
+    a_src[i] = a16 + (size_t)min(m0 + r, M - 1) * K + 8 * ((lane & 7) ^ ((r >> 1) & 7));
+  }
+  // W copy i (0..4) of this wave: piece p = 64*(5*wave+i) + lane of the slot,
+  // column p/5, part p%5 (0 = header, 1..4 = qs bytes 16*(part-1) of the half).
+  const uint8_t *w_src[5];
+  int w_qs[5];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) {
+    const int p = 64 * (5 * wave + i) + lane, col = p / 5, part = p - 5 * col;
+    w_src[i] = w + (size_t)min(n0 + col, N - 1) * row_bytes;
+    w_qs[i] = part == 0 ? 0 : 16 + 16 * (part - 1);  // plus 64 per half when part > 0
+  }
+
+  auto issue_a = [&](int kc, uint8_t *slot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_global_load_lds((gvoid *)(a_src[i] + (size_t)kc * kBK), (lvoid *)(slot + (4 * wave + i) * 1024),
+                                       16, 0, 0);
+  };
+  auto issue_w = [&](int half, uint8_t *slot) __attribute__((always_inline)) {
+    const size_t boff = (size_t)(half >> 1) * kQ4KBlockBytes;
+    const int hoff = 64 * (half & 1);
+#pragma unroll
+    for (int i = 0; i < 5; ++i)
+      __builtin_amdgcn_global_load_lds((gvoid *)(w_src[i] + boff + w_qs[i] + (w_qs[i] ? hoff : 0)),
+                                       (lvoid *)(slot + (5 * wave + i) * 1024), 16, 0, 0);
+  };
+
+  int colw[2];
+  float bpw[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    colw[j] = 64 * wave + 32 * j + l32;
+    bpw[j] = __builtin_amdgcn_ldexpf(g ? 0.0625f : 1.0f, -ew[min(n0 + colw[j], N - 1)]);
+  }
+
+  floatx16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = floatx16{};
+
+  issue_w(0, sw0);
+  issue_a(0, sa0);
+  wait_vmcnt<0>();
+  wg_barrier();
+
+  const int nhalves = 2 * nblocks;
+  for (int b = 0; b < nblocks; ++b) {
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      const int kc = 4 * b + cc;
+      uint8_t *pa = (cc & 1) ? sa1 : sa0;
+      uint8_t *pw = (cc >> 1) ? sw1 : sw0;
+      // Chunk kc's A copy and (at an even chunk) its half-block's W copy were
+      // issued one chunk ago: drain, then every wave's copies are in LDS and
+      // every wave has finished with the slots the copies below overwrite.
+      if (kc > 0) {
+        wait_vmcnt<0>();
+        wait_lgkmcnt0();
+        wg_barrier();
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if ((cc & 1) == 0) issue_w(min(2 * b + (cc >> 1) + 1, nhalves - 1), (cc >> 1) ? sw0 : sw1);
+      issue_a(min(kc + 1, nchunks - 1), (cc & 1) ? sa0 : sa1);
+      __builtin_amdgcn_sched_barrier(0);
+
+      auto read_a = [&](int t, u32x4 (&af)[4]) __attribute__((always_inline)) {
+        const int seg = 2 * g + (t & 1) + 4 * (t >> 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int rr = 32 * i + l32;
+          af[i] = lds_read16(pa + rr * 128 + 16 * (seg ^ ((rr >> 1) & 7)));
+        }
+      };
+      u32x4 hw[2], qw[2], af[4], afn[4];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        hw[j] = lds_read16(pw + 80 * colw[j]);
+        qw[j] = lds_read16(pw + 80 * colw[j] + 16 + 32 * (cc & 1) + 16 * g);
+      }
+      read_a(0, afn);
+      lds_wait(hw[0], hw[1], qw[0], qw[1]);
+      float sc_lo[2], sc_hi[2], nc_lo[2], nc_hi[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float d = half_bits_to_f32(hw[j][0] & 0xFFFFu), dmin = half_bits_to_f32(hw[j][0] >> 16);
+        uint32_t sv, mv;
+        q4k_scale_min(hw[j][1], hw[j][2], hw[j][3], 2 * cc + g, sv, mv);
+        const float sfac = d * (float)sv * bpw[j];
+        const float mn = dmin * (float)mv * (bpw[j] * (g ? 16.f : 1.f));
+        const float ncv = -(mn + 1024.f * sfac);
+        const auto s2 = __builtin_amdgcn_permlane32_swap(f32_bits(sfac), f32_bits(sfac), false, false);
+        const auto n2 = __builtin_amdgcn_permlane32_swap(f32_bits(ncv), f32_bits(ncv), false, false);
+        sc_lo[j] = bits_f32(s2[0]), sc_hi[j] = bits_f32(s2[1]);
+        nc_lo[j] = bits_f32(n2[0]), nc_hi[j] = bits_f32(n2[1]);
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        half8 bf[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const uint32_t w0 = qw[j][2 * (t & 1)], w1 = qw[j][2 * (t & 1) + 1];
+          bf[j] = t < 2 ? dq_step<false>(w0, w1, sc_lo[j], nc_lo[j]) : dq_step<true>(w0, w1, sc_hi[j], nc_hi[j]);
+        }
+        lds_wait(afn[0], afn[1], afn[2], afn[3]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) af[i] = afn[i];
+        if (t < 3) read_a(t + 1, afn);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, af[i]), bf[j], acc[i][j], 0,
+                                                               0, 0);
+      }
+    }
+  }
+
+  int ecol[2];
+  bool cok[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int col = n0 + colw[j];
+    cok[j] = col < N;
+    ecol[j] = cok[j] ? ew[col] : 0;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = m0 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+      if (row >= M) continue;
+      const int er = ea[row];
+      float *crow = c + (size_t)row * N + n0;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        if (cok[j]) crow[colw[j]] = __builtin_amdgcn_ldexpf(acc[i][j][r], er + ecol[j]);
+    }
+  }
 }
 
 }  // namespace
@@ -308,7 +590,7 @@ hipError_t launch_q4k_gemm(const void *a, bool a_bf16, const void *w, float *c, 
   int *ea = reinterpret_cast<int *>(p + r256((size_t)M * K * 2));
   int *ew = reinterpret_cast<int *>(p + r256((size_t)M * K * 2) + r256((size_t)M * 4));
   const uint8_t *wb = static_cast<const uint8_t *>(w);
-  const int prep_blocks = M + (N + 255) / 256;
+  const int prep_blocks = M + (N + 3) / 4;
   if (a_bf16)
     hipLaunchKernelGGL((k_gemm_prep<uint16_t>), dim3(prep_blocks), dim3(256), 0, s,
                        static_cast<const uint16_t *>(a), a16, ea, wb, ew, M, N, K);
@@ -317,7 +599,17 @@ hipError_t launch_q4k_gemm(const void *a, bool a_bf16, const void *w, float *c, 
                        ea, wb, ew, M, N, K);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  return launch_tile<128, 128, 2, 2>(a16, ea, wb, ew, c, M, N, K, s);
+  // Up to 1024 rows: 128 x 256 tiles on eight waves (a prefill of a few
+  // hundred tokens gives too few 256-row tiles to fill the chip); above that
+  // the half-block kernel, two workgroups per CU.
+  const int tiles_m = (M + 127) / 128, tiles_n = (N + 255) / 256;
+  if (M <= 1024)
+    hipLaunchKernelGGL(k_q4k_gemm_w8b<1>, dim3(tiles_m * tiles_n), dim3(512), 0, s, a16, ea, wb, ew, c, M, N, K,
+                       tiles_m, tiles_n);
+  else
+    hipLaunchKernelGGL(k_q4k_gemm_h, dim3(tiles_m * tiles_n), dim3(256), 0, s, a16, ea, wb, ew, c, M, N, K, tiles_m,
+                       tiles_n);
+  return hipGetLastError();
 }
 
 }  // namespace rt
