@@ -14,6 +14,10 @@ Also measured in the same run and reported next to it:
   roofline -- the dominant kernel (the 10240x2560 Q4_K GEMV of gate/up):
               algorithmic bytes per launch / average launch time from HIP
               events around a graph of back-to-back launches;
+  gemm     -- BASELINE configs 2 and 4: the Q4_K GEMM (bf16 activations,
+              f32 output) on the matrix cores, TFLOP/s and the fraction of
+              the 2.5 PFLOP/s dense f16 peak, with a plain f16 library GEMM
+              of the same shape timed beside it for reference;
   cpu_baseline -- the C restatement of the reference's x86 CPU path
               (oracle/, "port") on a bounded sample, on this host's cores.
 
@@ -21,7 +25,7 @@ Synthetic data (torch RNG on the GPU): Q4_K blocks with f16 d, dmin =
 |N(0,0.02)|, 6-bit scales/mins uniform 0..63, nibbles uniform; BF16 weights
 N(0,0.02); activations N(0,1); KV N(0,1).
 
-usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-decode] [--skip-cpu]
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-decode] [--skip-gemm] [--skip-cpu]
 """
 from __future__ import annotations
 
@@ -35,6 +39,11 @@ import time
 
 REPO = pathlib.Path(__file__).resolve().parent
 PEAK_HBM_GBS = 8000.0  # MI355X published HBM3E bandwidth
+PEAK_F16_TFLOPS = 2500.0  # MI355X dense f16/bf16 matrix peak
+# configs 2 (prefill, Gemma-3-4B shapes) and 4 (FLUX-12B transformer shapes): (label, M, N, K)
+GEMM_SHAPES = [("config2_gate_up", 512, 10240, 2560), ("config2_down", 512, 2560, 10240),
+               ("config4_qkv", 4608, 9216, 3072), ("config4_mlp_up", 4608, 12288, 3072),
+               ("config4_mlp_down", 4608, 3072, 12288)]
 
 H, F, QD, KVD, L, V = 2560, 10240, 2048, 1024, 34, 262144
 Q4K_SHAPES = [("q", QD, H), ("k", KVD, H), ("v", KVD, H), ("o", H, QD), ("gate", F, H), ("up", F, H),
@@ -88,6 +97,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-decode", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-gemm", action="store_true")
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the PMC probe: a 256 MiB copy (calibration) and 20 launches of the dominant "
@@ -209,7 +219,7 @@ def main() -> int:
     dom = per_shape["gate"]
     roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(dom["GBps"] / PEAK_HBM_GBS, 4), "traffic": measured_traffic(),
-                "kernel": "k_q4k_gemv_cr<NB=10,T=320,ITERS=4> (Q4_K GEMV 10240x2560)",
+                "kernel": "k_q4k_gemv_dig<NB=10,T=320,ITERS=1> (Q4_K GEMV 10240x2560)",
                 "bytes_per_launch": dom["bytes_per_launch"], "us_per_launch": dom["us_per_launch"]}
     log(f"dominant kernel gate 10240x2560: {dom['us_per_launch']} us/launch, {dom['GBps']} GB/s")
 
@@ -244,9 +254,48 @@ def main() -> int:
                   "tok_per_s": round(1.0 / dt, 1), "ms_per_token": round(dt * 1e3, 4),
                   "bytes_per_token": dec_bytes, "GBps": round(dec_bytes / dt / 1e9, 1),
                   "frac_of_hbm_peak": round(dec_bytes / dt / 1e9 / PEAK_HBM_GBS, 4),
-                  "launches_per_token": 5 * L + 1}
+                  "launches_per_token": 6 * L + 1}
         log(f"decode step {dt * 1e3:.3f} ms -> {1 / dt:.1f} tok/s")
         d.close()
+
+    # ---------------- configs 2 and 4: Q4_K GEMM on the matrix cores ------------
+    gemm = None
+    if not args.skip_gemm:
+        gemm = {}
+        for label, m, n, k in GEMM_SHAPES:
+            w = synth_q4k(torch, n, k, gen)
+            a = torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16)
+            c = torch.empty(m, n, device=dev)
+            ab = a.view(torch.int16)
+            for _ in range(2):
+                rt.q4k_gemm(ab, w, c, m, n, k)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps_g = 10
+            e0.record()
+            for _ in range(reps_g):
+                rt.q4k_gemm(ab, w, c, m, n, k)
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / reps_g
+            tf = 2.0 * m * n * k / us / 1e6
+            # a plain f16 library GEMM of the same shape (weights already dequantised), for reference
+            af, wf = a.to(torch.float16), torch.randn(n, k, device=dev, generator=gen).to(torch.float16)
+            for _ in range(2):
+                cf = af @ wf.T
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(reps_g):
+                cf = af @ wf.T
+            e1.record()
+            torch.cuda.synchronize()
+            us_lib = e0.elapsed_time(e1) * 1e3 / reps_g
+            gemm[label] = {"m": m, "n": n, "k": k, "us": round(us, 1), "TFLOPs": round(tf, 1),
+                           "frac_of_mfma_peak": round(tf / PEAK_F16_TFLOPS, 4),
+                           "library_f16_gemm_us": round(us_lib, 1)}
+            log(f"gemm {label} {m}x{n}x{k}: {us:.1f} us, {tf:.1f} TFLOP/s "
+                f"({tf / PEAK_F16_TFLOPS * 100:.1f}% of peak); library f16 GEMM {us_lib:.1f} us")
+            del w, a, c, ab, af, wf, cf
 
     # ---------------- CPU baseline (oracle = C port of the reference path) -----
     cpu = None
@@ -296,6 +345,7 @@ def main() -> int:
         "roofline": roofline,
         "per_shape": per_shape,
         "decode": decode,
+        "gemm": gemm,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
