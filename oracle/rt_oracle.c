@@ -467,7 +467,10 @@ void orc_gqa_attention_decode(const float *q, const float *k_cache, const float 
 
 static int is_global(const orc_gemma3_cfg *cfg, int layer)
 {
-    /* Config4::is_global_layer: transformer4.rs:141-143 (layer % 6 == 5). */
+    /* Config4::is_global_layer: transformer4.rs:141-143 (layer % 6 == 5).
+     * global_every <= 0 (a config knob of this restatement; the reference
+     * fixes 6) means every layer is a sliding-window layer. */
+    if (cfg->global_every <= 0) return 0;
     return (layer % cfg->global_every) == cfg->global_every - 1;
 }
 

@@ -7,11 +7,19 @@
 
 namespace rt {
 
-// Keys per attention chunk (at most): the host sizes the chunk count from
-// max_seq (global layers) or the sliding window (local layers).
+// Keys per attention sub-chunk.  A workgroup walks up to kAttnSubLocal
+// (sliding-window layers) or kAttnSubGlobal (global layers) sub-chunks; the
+// host sizes the chunk counts from the window and from max_seq.
 constexpr int kAttnChunkKeys = 16;
+constexpr int kAttnSubLocal = 1;
+constexpr int kAttnSubGlobal = 4;
 // Upper bound on the number of chunks a KV head is split into.
 constexpr int kAttnMaxChunks = 4096;
+// Step parameter block (device): ints [0, 16) (token, position), then the
+// RoPE cos/sin table of the step's position for local layers at float offset
+// kParamRopeLocal ([head_dim/2] cos, [head_dim/2] sin) and for global layers
+// after it.
+constexpr int kParamRopeLocal = 16;
 
 struct DecodeShape {
   int hidden, ffn, n_q_heads, n_kv_heads, head_dim, n_layers, vocab;
@@ -23,8 +31,7 @@ struct LayerArgs {
   const uint8_t *wq, *wk, *wv, *wo, *wgate, *wup, *wdown;  // Q4_K, rows=out
   const float *g_in, *g_post_attn, *g_pre_ffn, *g_post_ffn, *g_q, *g_k;
   float *kc, *vc;          // [max_seq, n_kv_heads*head_dim] f32
-  const float *rope_den;   // [head_dim/2] theta^(2i/d), from the host's powf
-  float rope_fs;           // linear RoPE scaling (1 local, 1/8 global for 4B)
+  const float *rope_cs;    // [head_dim] cos | sin of this step's angles (in the params block)
   int window;              // sliding window in keys, 0 = global layer
 };
 

@@ -30,11 +30,12 @@ struct rt_decode {
   bool embed_set = false;
   void *embed_owned = nullptr, *final_owned = nullptr;
   DecodeArgs args{};
-  int *params_dev = nullptr;
+  int *params_dev = nullptr;             // step parameter block (kParamRopeLocal)
   int *params_host = nullptr;            // pinned
+  size_t params_bytes = 0;
   hipEvent_t params_copied = nullptr;
   bool params_pending = false;
-  float *rope_den_local = nullptr, *rope_den_global = nullptr;
+  std::vector<float> rope_den_local, rope_den_global;  // theta^(2i/d), host powf
   hipGraphExec_t exec = nullptr;
   bool graph_enabled = true;
   bool graph_dirty = true;
@@ -99,10 +100,11 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
     return set_error(RT_EINVAL, "rt_decode_create: unsupported shape: %s", why);
   const int window = c.sliding_window;
   const int local_span = window > 0 ? std::min(window, c.max_seq) : c.max_seq;
-  s.nchunk_local = (local_span + kAttnChunkKeys - 1) / kAttnChunkKeys;
-  s.nchunk_global = (c.max_seq + kAttnChunkKeys - 1) / kAttnChunkKeys;
-  if (s.nchunk_global > kAttnMaxChunks)
-    return set_error(RT_EINVAL, "rt_decode_create: max_seq %d exceeds %d", c.max_seq, kAttnChunkKeys * kAttnMaxChunks);
+  constexpr int kLocalKeys = kAttnChunkKeys * kAttnSubLocal, kGlobalKeys = kAttnChunkKeys * kAttnSubGlobal;
+  s.nchunk_local = (local_span + kLocalKeys - 1) / kLocalKeys;
+  s.nchunk_global = (c.max_seq + kGlobalKeys - 1) / kGlobalKeys;
+  if (s.nchunk_global > kAttnMaxChunks || s.nchunk_local > kAttnMaxChunks)
+    return set_error(RT_EINVAL, "rt_decode_create: max_seq %d exceeds %d", c.max_seq, kLocalKeys * kAttnMaxChunks);
 
   rt_decode *d = new rt_decode();
   d->cfg = c;
@@ -126,13 +128,15 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
     TRYH(e, "hipGetDevice");
     TRYH(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking), "hipStreamCreate");
     TRYH(hipEventCreateWithFlags(&d->params_copied, hipEventDisableTiming), "hipEventCreate");
-    TRYH(hipHostMalloc((void **)&d->params_host, 4 * sizeof(int), hipHostMallocDefault), "hipHostMalloc");
     const size_t H = c.hidden, F = c.ffn, D = c.head_dim;
     const size_t QD = (size_t)c.n_q_heads * D, KVD = (size_t)c.n_kv_heads * D;
     const int nch = std::max(s.nchunk_local, s.nchunk_global);
+    d->params_bytes = (kParamRopeLocal + 2 * D) * sizeof(float);
+    TRYH(hipHostMalloc((void **)&d->params_host, d->params_bytes, hipHostMallocDefault), "hipHostMalloc");
+    std::memset(d->params_host, 0, d->params_bytes);
     void *p;
-    TRY(dalloc(d, 64, &p)); d->params_dev = (int *)p;
-    TRYH(hipMemset(d->params_dev, 0, 64), "hipMemset");
+    TRY(dalloc(d, d->params_bytes, &p)); d->params_dev = (int *)p;
+    TRYH(hipMemset(d->params_dev, 0, d->params_bytes), "hipMemset");
     DecodeArgs &a = d->args;
     auto fbuf = [&](size_t n, float **dst) -> rt_status {
       void *q = nullptr;
@@ -158,16 +162,16 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
     a.n_kv_heads = c.n_kv_heads;
     a.head_dim = c.head_dim;
     // RoPE denominators theta^(2i/d), computed with the host libm exactly as
-    // apply_rope_at_offset does (transformer4.rs:2755).
-    std::vector<float> dl(D / 2), dg(D / 2);
+    // apply_rope_at_offset does (transformer4.rs:2755); each step turns them
+    // into the cos/sin table of its position (rt_decode_step_async).
+    d->rope_den_local.resize(D / 2);
+    d->rope_den_global.resize(D / 2);
     for (size_t i = 0; i < D / 2; ++i) {
       const float ex = 2.0f * (float)i / (float)D;
-      dl[i] = powf(c.rope_theta_local, ex);
-      dg[i] = powf(c.rope_theta_global, ex);
+      d->rope_den_local[i] = powf(c.rope_theta_local, ex);
+      d->rope_den_global[i] = powf(c.rope_theta_global, ex);
     }
-    TRY(fbuf(D / 2, &d->rope_den_local)); TRY(fbuf(D / 2, &d->rope_den_global));
-    TRYH(hipMemcpy(d->rope_den_local, dl.data(), dl.size() * 4, hipMemcpyHostToDevice), "hipMemcpy");
-    TRYH(hipMemcpy(d->rope_den_global, dg.data(), dg.size() * 4, hipMemcpyHostToDevice), "hipMemcpy");
+    const float *cs_dev = reinterpret_cast<const float *>(d->params_dev) + kParamRopeLocal;
     d->layers.resize(c.n_layers);
     d->layer_set.assign(c.n_layers, 0);
     for (int l = 0; l < c.n_layers; ++l) {
@@ -176,8 +180,7 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
       TRY(fbuf((size_t)c.max_seq * KVD, &L.kc));
       TRY(fbuf((size_t)c.max_seq * KVD, &L.vc));
       const bool g = is_global(c, l);
-      L.rope_den = g ? d->rope_den_global : d->rope_den_local;
-      L.rope_fs = g ? c.rope_fs_global : c.rope_fs_local;
+      L.rope_cs = cs_dev + (g ? D : 0);
       L.window = g ? 0 : c.sliding_window;
     }
   }
@@ -317,7 +320,23 @@ rt_status rt_decode_step_async(rt_decode *d, int32_t token, int32_t position) {
   }
   d->params_host[0] = token;
   d->params_host[1] = position;
-  e = hipMemcpyAsync(d->params_dev, d->params_host, 2 * sizeof(int), hipMemcpyHostToDevice, d->stream);
+  {
+    // cos/sin of angle = (pos*fs)/theta^(2i/d) in f32 with the host libm, as
+    // apply_rope_at_offset computes them (transformer4.rs:2742-2772).
+    const int D = d->cfg.head_dim, P = D / 2;
+    float *cs = reinterpret_cast<float *>(d->params_host) + kParamRopeLocal;
+    for (int t = 0; t < 2; ++t, cs += D) {
+      const float fs = t ? d->cfg.rope_fs_global : d->cfg.rope_fs_local;
+      const float *den = t ? d->rope_den_global.data() : d->rope_den_local.data();
+      const float pf = (float)position * fs;
+      for (int i = 0; i < P; ++i) {
+        const float ang = pf / den[i];
+        cs[i] = cosf(ang);
+        cs[P + i] = sinf(ang);
+      }
+    }
+  }
+  e = hipMemcpyAsync(d->params_dev, d->params_host, d->params_bytes, hipMemcpyHostToDevice, d->stream);
   if (e == hipSuccess) e = hipEventRecord(d->params_copied, d->stream);
   if (e != hipSuccess) return hip_error(e, "rt_decode_step params");
   d->params_pending = true;

@@ -256,22 +256,25 @@ __global__ __launch_bounds__(T) void k_gemv_persist(const uint8_t *__restrict__ 
 }
 
 // ---------------------------------------------------------------------------
-// k_attn: per (key chunk, KV head) workgroup of 256 threads.
+// k_attn: per (key chunk, KV head) workgroup of 256 threads.  A chunk is up to
+// SUB sub-chunks of 16 keys, walked with an online softmax.
 //   1. q heads of this KV group: per-head RMSNorm (gamma shared, 2485-2508)
-//      and NeoX RoPE, angle = (pos*fs)/den[i] with den[i] = theta^(2i/D)
-//      tabulated on the host (2742-2772); the chunk holding `pos` also
-//      rotates k, and writes k and v into the cache row `pos` (1813-1823).
-//   2. scores s_c = (q.k_c)*scale for keys in the chunk (16 lanes per key)
-//   3. chunk-local softmax statistics m = max s, l = sum exp(s - m)
-//   4. o = sum_c exp(s_c - m) v_c (one thread per dimension)
-//   5. partials (m, l, o) to global; k_attn_combine merges the chunks:
+//      and NeoX RoPE (2742-2772) with cos/sin of (pos*fs)/theta^(2i/d)
+//      computed on the host for this position (the reference's own f32
+//      expression and libm); the chunk holding `pos` also rotates k, and
+//      writes k and v into the cache row `pos` (1813-1823).
+//   2. per sub-chunk: scores s_c = (q.k_c)*scale (16 lanes per key), running
+//      max m and sum l with the previous sums rescaled by e^(m_old - m_new),
+//      and o = sum_c e^(s_c - m) v_c (four dimensions per thread);
+//   3. partials (m, l, o) to global; k_attn_combine merges the chunks:
 //      out = sum_i o_i e^(m_i-M) / sum_i l_i e^(m_i-M).
 // Together they equal gqa_attention_cached's t_q == 1 branch (2806-2879).
 // ---------------------------------------------------------------------------
 template <int D>
 RT_DEV void norm_rope_head(const float *__restrict__ src, const float *__restrict__ gamma,
-                           const float *__restrict__ den, float pos_fs, float eps, float *dst) {
+                           const float *__restrict__ cs, float eps, float *dst) {
   // One wave; lane owns pairs i = lane*P + p (p < P) with partners i + D/2.
+  // cs[i] = cos, cs[D/2 + i] = sin of the pair's angle.
   constexpr int P = D / 128;
   const int lane = threadIdx.x & 63;
   float x0[P], x1[P];
@@ -290,26 +293,25 @@ RT_DEV void norm_rope_head(const float *__restrict__ src, const float *__restric
     const int i = lane * P + p;
     const float a0 = (x0[p] * rinv) * (1.0f + gamma[i]);
     const float a1 = (x1[p] * rinv) * (1.0f + gamma[i + D / 2]);
-    const float ang = pos_fs / den[i];
-    float sn, cs;
-    sincosf(ang, &sn, &cs);
-    dst[i] = a0 * cs - a1 * sn;
-    dst[i + D / 2] = a0 * sn + a1 * cs;
+    const float c = cs[i], sn = cs[D / 2 + i];
+    dst[i] = a0 * c - a1 * sn;
+    dst[i + D / 2] = a0 * sn + a1 * c;
   }
 }
 
-template <int D, int G>
+template <int D, int G, int SUB>
 __global__ __launch_bounds__(256) void k_attn(DecodeArgs a, LayerArgs L) {
-  constexpr int KC = kAttnChunkKeys;       // keys per chunk (at most)
+  constexpr int KC = kAttnChunkKeys;       // keys per sub-chunk
   constexpr int DL = D / 16;               // score pass: 16 lanes per key, DL dims per lane
+                                           // (float4 j of lane `sub` = dims 64j + 4sub + [0,4))
   constexpr int VL = D / 4;                // value pass: lanes per key row (float4 each)
   constexpr int VG = 256 / VL;             // key groups in the value pass
   constexpr int VK = KC / VG;              // keys per thread in the value pass
   static_assert(KC == 16 && (D == 128 || D == 256), "chunk layout assumes 16 keys and D in {128, 256}");
-  __shared__ float qs[G][D];
-  __shared__ float knew[D], vnew[D];
-  __shared__ float sc[G][KC];
-  __shared__ float stat[G][2];
+  __shared__ __attribute__((aligned(16))) float qs[G][D];
+  __shared__ __attribute__((aligned(16))) float knew[D], vnew[D];
+  __shared__ float sc[2][G][KC];           // scores, then probabilities (double-buffered by sub-chunk)
+  __shared__ float rescale[2][G];          // e^(m_old - m_new) of each sub-chunk
   __shared__ __attribute__((aligned(16))) float vpart[VG][G][D];
   const int kvh = blockIdx.y, chunk = blockIdx.x, nchunk = gridDim.x;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -317,43 +319,40 @@ __global__ __launch_bounds__(256) void k_attn(DecodeArgs a, LayerArgs L) {
   const int t_end = pos + 1;
   const int t_start = L.window > 0 ? max(0, t_end - L.window) : 0;
   const int t_kv = t_end - t_start;
-  const int csize = (t_kv + nchunk - 1) / nchunk;  // <= KC: the host sizes nchunk for max_seq / window
+  const int csize = (t_kv + nchunk - 1) / nchunk;  // <= KC*SUB: the host sizes nchunk for max_seq / window
   const int c0 = t_start + chunk * csize;
   const int c1 = min(c0 + csize, t_end);
   const int n = max(0, c1 - c0);
   const bool has_new = c0 <= pos && pos < c1;
   const int kvd = a.n_kv_heads * D;
-  const float pos_fs = (float)pos * L.rope_fs;
-
-  // 0. issue this chunk's K and V loads first (branch-free, clamped to a valid
-  //    row); they are consumed after the q/k rotations below.  Row `pos` is
-  //    replaced by the freshly rotated k / copied v.
+  const float *kbase = L.kc + (size_t)kvh * D, *vbase = L.vc + (size_t)kvh * D;
   const int kg = lane >> 4, sub = lane & 15;
   const int kidx = wave * 4 + kg;                      // this lane's key in the score pass
-  const int kc_row = min(c0 + kidx, max(c1 - 1, 0));
-  float kv[DL];
-  {
-    const float4 *kp = reinterpret_cast<const float4 *>(L.kc + (size_t)kc_row * kvd + (size_t)kvh * D + sub * DL);
+  const int vgrp = threadIdx.x / VL, vl = threadIdx.x % VL;
+  const int last = max(c1 - 1, 0);
+
+  // Sub-chunk loads, branch-free at clamped rows (row `pos` is replaced by the
+  // freshly rotated k / copied v when it is used).
+  auto load_sub = [&](int s, float (&kr)[DL], float4 (&vr)[VK]) __attribute__((always_inline)) {
+    const int k0 = c0 + s * KC;
+    const float4 *kp = reinterpret_cast<const float4 *>(kbase + (size_t)min(k0 + kidx, last) * kvd);
 #pragma unroll
     for (int j = 0; j < DL / 4; ++j) {
-      const float4 v4 = kp[j];
-      kv[4 * j] = v4.x; kv[4 * j + 1] = v4.y; kv[4 * j + 2] = v4.z; kv[4 * j + 3] = v4.w;
+      const float4 v4 = kp[16 * j + sub];
+      kr[4 * j] = v4.x; kr[4 * j + 1] = v4.y; kr[4 * j + 2] = v4.z; kr[4 * j + 3] = v4.w;
     }
-  }
-  const int vgrp = threadIdx.x / VL, vl = threadIdx.x % VL;
-  float4 vv[VK];
 #pragma unroll
-  for (int j = 0; j < VK; ++j) {
-    const int row = min(c0 + vgrp + VG * j, max(c1 - 1, 0));
-    vv[j] = *reinterpret_cast<const float4 *>(L.vc + (size_t)row * kvd + (size_t)kvh * D + 4 * vl);
-  }
+    for (int j = 0; j < VK; ++j)
+      vr[j] = *reinterpret_cast<const float4 *>(vbase + (size_t)min(k0 + vgrp + VG * j, last) * kvd + 4 * vl);
+  };
+  float kr[DL];
+  float4 vr[VK];
+  load_sub(0, kr, vr);
 
   // 1. rotations (waves 0..G-1: q heads; the next wave: k, and the v copy)
-  if (wave < G) {
-    norm_rope_head<D>(a.q + (size_t)(kvh * G + wave) * D, L.g_q, L.rope_den, pos_fs, a.eps, qs[wave]);
-  }
+  if (wave < G) norm_rope_head<D>(a.q + (size_t)(kvh * G + wave) * D, L.g_q, L.rope_cs, a.eps, qs[wave]);
   if (has_new && wave == (G % 4)) {  // for G == 4 wave 0 rotates k after its q head
-    norm_rope_head<D>(a.k + (size_t)kvh * D, L.g_k, L.rope_den, pos_fs, a.eps, knew);
+    norm_rope_head<D>(a.k + (size_t)kvh * D, L.g_k, L.rope_cs, a.eps, knew);
     for (int i = lane; i < D; i += 64) vnew[i] = a.v[(size_t)kvh * D + i];
   }
   __syncthreads();
@@ -362,53 +361,69 @@ __global__ __launch_bounds__(256) void k_attn(DecodeArgs a, LayerArgs L) {
     L.vc[(size_t)pos * kvd + (size_t)kvh * D + threadIdx.x] = vnew[threadIdx.x];
   }
 
-  // 2. scores s = (q.k) * scale, 16 lanes per key
-  if (c0 + kidx == pos) {
-#pragma unroll
-    for (int j = 0; j < DL; ++j) kv[j] = knew[sub * DL + j];
-  }
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float d = 0.f;
-#pragma unroll
-    for (int j = 0; j < DL; ++j) d += qs[g][sub * DL + j] * kv[j];
-    d = row16_sum(d);
-    if (kidx < n && sub == 0) sc[g][kidx] = d * a.attn_scale;
-  }
-  __syncthreads();
-
-  // 3. chunk softmax statistics (wave g handles head g; n <= 16 keys)
-  if (wave < G) {
-    const float s_ = lane < n ? sc[wave][lane] : -INFINITY;
-    const float m = wave_max(s_);
-    const float p = lane < n ? expf(s_ - m) : 0.f;
-    const float l = wave_sum(p);
-    if (lane < n) sc[wave][lane] = p;
-    if (lane == 0) {
-      stat[wave][0] = m;
-      stat[wave][1] = l;
-    }
-  }
-  __syncthreads();
-
-  // 4. o = sum_c p_c v_c: thread owns 4 dimensions of VK keys, then the VG
-  //    key groups are summed through LDS
+  // 2. sub-chunks with a running softmax (wave g < G keeps head g's m and l)
   float4 o[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) o[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+  float m_run = -INFINITY, l_run = 0.f;
 #pragma unroll
-  for (int j = 0; j < VK; ++j) {
-    const int ki = vgrp + VG * j;
-    float4 v4 = vv[j];
-    if (c0 + ki == pos) v4 = *reinterpret_cast<const float4 *>(&vnew[4 * vl]);
-    if (ki < n) {
+  for (int s = 0; s < SUB; ++s) {
+    const int k0 = c0 + s * KC;
+    const int ns = max(0, min(KC, c1 - k0));
+    float kn[DL];
+    float4 vn[VK];
+    if (s + 1 < SUB) load_sub(s + 1, kn, vn);
+    if (k0 + kidx == pos) {
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float p = sc[g][ki];
-        o[g].x += p * v4.x; o[g].y += p * v4.y; o[g].z += p * v4.z; o[g].w += p * v4.w;
+      for (int j = 0; j < DL; ++j) kr[j] = knew[64 * (j >> 2) + 4 * sub + (j & 3)];
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float d = 0.f;
+#pragma unroll
+      for (int j = 0; j < DL; ++j) d += qs[g][64 * (j >> 2) + 4 * sub + (j & 3)] * kr[j];
+      d = row16_sum(d);
+      if (kidx < ns && sub == 0) sc[s & 1][g][kidx] = d * a.attn_scale;
+    }
+    __syncthreads();
+    if (wave < G) {
+      const float sv = lane < ns ? sc[s & 1][wave][lane] : -INFINITY;
+      const float m_new = fmaxf(m_run, wave_max(sv));
+      const float p = lane < ns ? expf(sv - m_new) : 0.f;
+      const float r = m_run == -INFINITY ? 0.f : expf(m_run - m_new);
+      l_run = l_run * r + wave_sum(p);
+      m_run = m_new;
+      if (lane < KC) sc[s & 1][wave][lane] = p;
+      if (lane == 0) rescale[s & 1][wave] = r;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float r = rescale[s & 1][g];
+      o[g].x *= r; o[g].y *= r; o[g].z *= r; o[g].w *= r;
+    }
+#pragma unroll
+    for (int j = 0; j < VK; ++j) {
+      const int ki = vgrp + VG * j;
+      float4 v4 = vr[j];
+      if (k0 + ki == pos) v4 = *reinterpret_cast<const float4 *>(&vnew[4 * vl]);
+      if (ki < ns) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float p = sc[s & 1][g][ki];
+          o[g].x += p * v4.x; o[g].y += p * v4.y; o[g].z += p * v4.z; o[g].w += p * v4.w;
+        }
       }
     }
+    if (s + 1 < SUB) {
+#pragma unroll
+      for (int j = 0; j < DL; ++j) kr[j] = kn[j];
+#pragma unroll
+      for (int j = 0; j < VK; ++j) vr[j] = vn[j];
+    }
   }
+
+  // 3. the VG key groups are summed through LDS; partials to global
 #pragma unroll
   for (int g = 0; g < G; ++g) *reinterpret_cast<float4 *>(&vpart[vgrp][g][4 * vl]) = o[g];
   __syncthreads();
@@ -417,61 +432,59 @@ __global__ __launch_bounds__(256) void k_attn(DecodeArgs a, LayerArgs L) {
     float acc = 0.f;
 #pragma unroll
     for (int q = 0; q < VG; ++q) acc += vpart[q][g][d];
-    const int h = kvh * G + g;
-    a.part_o[((size_t)h * nchunk + chunk) * D + d] = acc;
+    a.part_o[((size_t)(kvh * G + g) * nchunk + chunk) * D + d] = acc;
   }
-  if (threadIdx.x < G) {
-    const int h = kvh * G + threadIdx.x;
-    a.part_m[(size_t)h * nchunk + chunk] = n > 0 ? stat[threadIdx.x][0] : -INFINITY;
-    a.part_l[(size_t)h * nchunk + chunk] = n > 0 ? stat[threadIdx.x][1] : 0.f;
+  if (wave < G && lane == 0) {
+    const int h = kvh * G + wave;
+    a.part_m[(size_t)h * nchunk + chunk] = n > 0 ? m_run : -INFINITY;
+    a.part_l[(size_t)h * nchunk + chunk] = n > 0 ? l_run : 0.f;
   }
 }
 
 // ---------------------------------------------------------------------------
 // k_attn_combine: merge the chunk partials of one q head and 64 dimensions.
 //   out[d] = sum_i o_i[d] e^(m_i - M) / sum_i l_i e^(m_i - M),  M = max_i m_i
-// 256 threads = 4 chunk groups x 64 dimensions; grid (n_q_heads, D/64).
+// 256 threads = 4 chunk groups x 64 dimensions, each group merging its
+// chunks online in one pass, then the four groups through LDS; grid
+// (n_q_heads, D/64).
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(256) void k_attn_combine(DecodeArgs a, int nchunk) {
-  __shared__ float wts[kAttnMaxChunks];
-  __shared__ float part[8][32];
-  __shared__ float bred[4];
-  const int h = blockIdx.x, d0 = blockIdx.y * 32;
+  __shared__ float gm[4], gl[4];
+  __shared__ float go[4][64];
+  const int h = blockIdx.x, d0 = blockIdx.y * 64;
+  const int cg = threadIdx.x >> 6, dl = threadIdx.x & 63;
   const float *pm = a.part_m + (size_t)h * nchunk;
   const float *pl = a.part_l + (size_t)h * nchunk;
-  float m = -INFINITY;
-  for (int i = threadIdx.x; i < nchunk; i += 256) m = fmaxf(m, pm[i]);
-  m = wave_max(m);
-  if ((threadIdx.x & 63) == 0) bred[threadIdx.x >> 6] = m;
-  __syncthreads();
-  const float M = fmaxf(fmaxf(bred[0], bred[1]), fmaxf(bred[2], bred[3]));
-  float l = 0.f;
-  for (int i = threadIdx.x; i < nchunk; i += 256) {
-    const float mi = pm[i];
-    const float w = mi == -INFINITY ? 0.f : expf(mi - M);
-    wts[i] = w;
-    l += pl[i] * w;
-  }
-  const float L = block_sum<256>(l, bred);  // its barriers also publish wts
-  const int cg = threadIdx.x >> 5, dl = threadIdx.x & 31;
   const float *po = a.part_o + (size_t)h * nchunk * D + d0 + dl;
-  float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
-  int i = cg;
-  for (; i + 24 < nchunk; i += 32) {
-    acc0 += po[(size_t)i * D] * wts[i];
-    acc1 += po[(size_t)(i + 8) * D] * wts[i + 8];
-    acc2 += po[(size_t)(i + 16) * D] * wts[i + 16];
-    acc3 += po[(size_t)(i + 24) * D] * wts[i + 24];
+  float M = -INFINITY, Ls = 0.f, O = 0.f;
+#pragma unroll 4
+  for (int i = cg; i < nchunk; i += 4) {
+    const float mi = pm[i], li = pl[i], oi = po[(size_t)i * D];
+    const bool ok = mi != -INFINITY;      // empty chunks carry m = -inf, l = 0
+    const float mn = ok ? fmaxf(M, mi) : M;
+    const float r_old = M == -INFINITY ? 0.f : expf(M - mn);
+    const float r_new = ok ? expf(mi - mn) : 0.f;
+    Ls = Ls * r_old + li * r_new;
+    O = O * r_old + oi * r_new;
+    M = mn;
   }
-  for (; i < nchunk; i += 8) acc0 += po[(size_t)i * D] * wts[i];
-  part[cg][dl] = (acc0 + acc1) + (acc2 + acc3);
+  if (dl == 0) {
+    gm[cg] = M;
+    gl[cg] = Ls;
+  }
+  go[cg][dl] = O;
   __syncthreads();
   if (cg == 0) {
-    float s = 0.f;
+    const float Mx = fmaxf(fmaxf(gm[0], gm[1]), fmaxf(gm[2], gm[3]));
+    float Lt = 0.f, Ot = 0.f;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) s += part[q][dl];
-    a.attn[(size_t)h * D + d0 + dl] = s / L;
+    for (int q = 0; q < 4; ++q) {
+      const float w = gm[q] == -INFINITY ? 0.f : expf(gm[q] - Mx);
+      Lt += gl[q] * w;
+      Ot += go[q][dl] * w;
+    }
+    a.attn[(size_t)h * D + d0 + dl] = Ot / Lt;
   }
 }
 
@@ -594,14 +607,24 @@ bool decode_shape_supported(const DecodeShape &s, const char **why) {
   return true;
 }
 
-template <int D>
-static void launch_attn_d(Launch &l, const DecodeArgs &a, const LayerArgs &L, int nchunk, int group) {
+template <int D, int SUB>
+static void launch_attn_ds(Launch &l, const DecodeArgs &a, const LayerArgs &L, int nchunk, int group) {
   const dim3 grid(nchunk, a.n_kv_heads);
   switch (group) {
-    case 1: hipLaunchKernelGGL((k_attn<D, 1>), grid, dim3(256), 0, l.s, a, L); break;
-    case 2: hipLaunchKernelGGL((k_attn<D, 2>), grid, dim3(256), 0, l.s, a, L); break;
-    default: hipLaunchKernelGGL((k_attn<D, 4>), grid, dim3(256), 0, l.s, a, L); break;
+    case 1: hipLaunchKernelGGL((k_attn<D, 1, SUB>), grid, dim3(256), 0, l.s, a, L); break;
+    case 2: hipLaunchKernelGGL((k_attn<D, 2, SUB>), grid, dim3(256), 0, l.s, a, L); break;
+    default: hipLaunchKernelGGL((k_attn<D, 4, SUB>), grid, dim3(256), 0, l.s, a, L); break;
   }
+}
+
+template <int D>
+static void launch_attn_d(Launch &l, const DecodeArgs &a, const LayerArgs &L, int nchunk, int group) {
+  if (L.window > 0)
+    launch_attn_ds<D, kAttnSubLocal>(l, a, L, nchunk, group);
+  else
+    launch_attn_ds<D, kAttnSubGlobal>(l, a, L, nchunk, group);
+  l.check();
+  hipLaunchKernelGGL((k_attn_combine<D>), dim3(a.n_q_heads, D / 64), dim3(256), 0, l.s, a, nchunk);
   l.check();
 }
 
@@ -617,14 +640,10 @@ hipError_t enqueue_decode_step(const DecodeShape &s, const DecodeArgs &a, const 
     if (big) launch_qkv<10, 320, 1>(l, a, L, P, li == 0, qkv_rows);
     else launch_qkv<2, 256, 1>(l, a, L, P, li == 0, qkv_rows);
     const int nchunk = L.window > 0 ? s.nchunk_local : s.nchunk_global;
-    if (s.head_dim == 256) {
+    if (s.head_dim == 256)
       launch_attn_d<256>(l, a, L, nchunk, group);
-      hipLaunchKernelGGL((k_attn_combine<256>), dim3(s.n_q_heads, 8), dim3(256), 0, l.s, a, nchunk);
-    } else {
+    else
       launch_attn_d<128>(l, a, L, nchunk, group);
-      hipLaunchKernelGGL((k_attn_combine<128>), dim3(s.n_q_heads, 4), dim3(256), 0, l.s, a, nchunk);
-    }
-    l.check();
     if (qd == 2048) launch_gemv<8, 256, 1>(l, L.wo, a.attn, a.o, s.hidden);
     else launch_gemv<2, 256, 1>(l, L.wo, a.attn, a.o, s.hidden);
     if (big) launch_gateup<10, 320>(l, a, L, s.ffn, 640);

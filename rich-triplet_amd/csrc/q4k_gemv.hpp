@@ -122,54 +122,65 @@ RT_DEV float q4k_chunk_dot(const uint4 hd, const uint4 qa, const uint4 qb, int c
 
 // ---------------------------------------------------------------------------
 // Integer-digit variant of the chunk dot.  Each 64-element activation chunk is
-// scaled by a power of two to 22-bit integers X (|X| <= 2^22, relative to the
-// chunk's max |x|) and split into three int8 digits, X = x2*65536 + x1*256 + x0
-// (x0, x1 in 0..255, x2 in -64..64).  The nibble-by-digit products then run
-// on v_dot4_u32_u8 / v_dot4_i32_i8 in exact integer arithmetic:
-//   sum_k q_k X_k = d0 + 256 d1 + 65536 d2,  d_i = sum_k q_k x_i,k
-// which needs ~1.1 VALU lane-ops per weight instead of ~2.3 for convert+FMA.
-// The only rounding is the 22-bit quantisation of x (relative 2^-22 of the
-// chunk max) and the final f32 combine; measured 3e-7 rel-L2 vs the f32 path.
+// scaled by a power of two to 16-bit integers X = rint(x * 2^sh) (sh = 15 - e
+// with the chunk's max |x| < 2^e; the one value that can round to 2^15 is
+// clamped to 2^15 - 1), written as two bytes, X = 256*x1 + x0 (x0 in 0..255,
+// x1 in -128..127).  The nibble-by-digit products then run on v_dot4_u32_u8
+// (x0) and v_dot4_i32_i8 (x1) in exact integer arithmetic:
+//   sum_k q_k X_k = d0 + 256 d1,  d_i = sum_k q_k x_i,k,
+// and d0 + 256 d1 (< 2^24 over 32 elements) converts to f32 exactly.  The only
+// roundings are X (half a unit of 2^-15 of the chunk's bound 2^e) and the final
+// f32 combine: about 3e-5 rel-L2 on N(0,1) activations.
+// Staging costs about five lane-ops per element: the rounding is one FMA,
+// x * 2^sh + 1.5*2^23, whose low 16 mantissa bits are X in two's complement,
+// and four byte permutes pack the digits of four elements.
 // ---------------------------------------------------------------------------
-constexpr int kDPitch = 52;  // dwords per slot: 3 digits x 16 dwords, delta, sum_lo, sum_hi, pad
+constexpr int kDPitch = 36;  // dwords per slot: 2 digits x 16 dwords, delta, sum_lo, sum_hi, pad
 
 struct ChunkD {
-  uint32_t d0[16], d1[16];
-  int32_t d2[16];
+  uint32_t d0[16];
+  int32_t d1[16];
   float delta, sum_lo, sum_hi;
 };
 
 // Stage one float4 (elements 4f..4f+3) as digits; the 16 lanes of a chunk
 // (consecutive lanes of one wave) agree on the chunk's power-of-two scale.
 RT_DEV void stage_digits_store(uint32_t *dl, int f, float4 v) {
-  float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-  m = fmaxf(m, dpp<0xB1>(m));
-  m = fmaxf(m, dpp<0x4E>(m));
-  m = fmaxf(m, dpp<0x141>(m));
-  m = fmaxf(m, dpp<0x140>(m));
-  int e;
-  (void)frexpf(m, &e);  // m < 2^e (e = 0 for m == 0: every digit is then 0)
-  const int sh = 22 - e;
-  const int X0 = (int)rintf(ldexpf(v.x, sh)), X1 = (int)rintf(ldexpf(v.y, sh));
-  const int X2 = (int)rintf(ldexpf(v.z, sh)), X3 = (int)rintf(ldexpf(v.w, sh));
-  auto pack = [](int a, int b, int c, int d, int shift) -> uint32_t {
-    return ((uint32_t)(a >> shift) & 255u) | (((uint32_t)(b >> shift) & 255u) << 8) |
-           (((uint32_t)(c >> shift) & 255u) << 16) | (((uint32_t)(d >> shift) & 255u) << 24);
-  };
+  // max |x| over the chunk on the bit patterns (monotone for |x|, no NaN
+  // canonicalisation between the DPP steps)
+  const uint32_t ax = f32_bits(v.x) & 0x7FFFFFFFu, ay = f32_bits(v.y) & 0x7FFFFFFFu;
+  const uint32_t az = f32_bits(v.z) & 0x7FFFFFFFu, aw = f32_bits(v.w) & 0x7FFFFFFFu;
+  uint32_t mb = max(max(ax, ay), max(az, aw));
+  mb = max(mb, dpp_u32<0xB1>(mb));
+  mb = max(mb, dpp_u32<0x4E>(mb));
+  mb = max(mb, dpp_u32<0x141>(mb));
+  mb = max(mb, dpp_u32<0x140>(mb));
+  // max < 2^e with e = biased exponent - 126; sh = 15 - e keeps |X| <= 2^15.
+  // 2^sh must be a normal float: chunks with max |x| below 2^-111 lose
+  // precision (their digits shrink toward zero) instead of overflowing.
+  const int sh = min(141 - (int)(mb >> 23), 126);
+  const float scale = __int_as_float((127 + sh) << 23);
+  const float magic = 12582912.0f;  // 1.5 * 2^23: the sum's low mantissa bits hold rint(x * 2^sh)
+  constexpr uint32_t top = 0x4B400000u + 32767u;  // bits of magic + (2^15 - 1)
+  const uint32_t b0 = min(__float_as_uint(fmaf(v.x, scale, magic)), top);
+  const uint32_t b1 = min(__float_as_uint(fmaf(v.y, scale, magic)), top);
+  const uint32_t b2 = min(__float_as_uint(fmaf(v.z, scale, magic)), top);
+  const uint32_t b3 = min(__float_as_uint(fmaf(v.w, scale, magic)), top);
+  const uint32_t p01 = __builtin_amdgcn_perm(b1, b0, 0x05010400u);  // b0.0 b1.0 b0.1 b1.1
+  const uint32_t p23 = __builtin_amdgcn_perm(b3, b2, 0x05010400u);  // b2.0 b3.0 b2.1 b3.1
   const int slot = f >> 4, sub = f & 15;
   uint32_t *base = dl + slot * kDPitch;
-  base[sub] = pack(X0, X1, X2, X3, 0);
-  base[16 + sub] = pack(X0, X1, X2, X3, 8);
-  base[32 + sub] = pack(X0, X1, X2, X3, 16);
+  base[sub] = __builtin_amdgcn_perm(p23, p01, 0x05040100u);       // low bytes:  x0 of 4 elements
+  base[16 + sub] = __builtin_amdgcn_perm(p23, p01, 0x07060302u);  // high bytes: x1 of 4 elements
   float s = (v.x + v.y) + (v.z + v.w);
   s += dpp<0xB1>(s);
   s += dpp<0x4E>(s);
   s += dpp<0x141>(s);  // 8 lanes = 32 elements
   if (sub == 0) {
-    reinterpret_cast<float *>(base)[48] = ldexpf(1.0f, -sh);
-    reinterpret_cast<float *>(base)[49] = s;
+    reinterpret_cast<float *>(base)[32] = __int_as_float((127 - sh) << 23);  // 2^-sh
+    reinterpret_cast<float *>(base)[33] = s;
   }
-  if (sub == 8) reinterpret_cast<float *>(base)[50] = s;
+  if (sub == 8) reinterpret_cast<float *>(base)[34] = s;
 }
 
 template <int K, int T>
@@ -185,43 +196,58 @@ RT_DEV void chunkd_from_lds(const uint32_t *dl, int slot, ChunkD &x) {
   const uint4 *p = reinterpret_cast<const uint4 *>(dl + slot * kDPitch);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint4 a = p[i], b = p[4 + i], c = p[8 + i];
+    const uint4 a = p[i], b = p[4 + i];
     x.d0[4 * i] = a.x; x.d0[4 * i + 1] = a.y; x.d0[4 * i + 2] = a.z; x.d0[4 * i + 3] = a.w;
-    x.d1[4 * i] = b.x; x.d1[4 * i + 1] = b.y; x.d1[4 * i + 2] = b.z; x.d1[4 * i + 3] = b.w;
-    x.d2[4 * i] = (int)c.x; x.d2[4 * i + 1] = (int)c.y; x.d2[4 * i + 2] = (int)c.z; x.d2[4 * i + 3] = (int)c.w;
+    x.d1[4 * i] = (int)b.x; x.d1[4 * i + 1] = (int)b.y; x.d1[4 * i + 2] = (int)b.z; x.d1[4 * i + 3] = (int)b.w;
   }
-  const float4 f = reinterpret_cast<const float4 *>(dl + slot * kDPitch)[12];
+  const float4 f = reinterpret_cast<const float4 *>(dl + slot * kDPitch)[8];
   x.delta = f.x;
   x.sum_lo = f.y;
   x.sum_hi = f.z;
+}
+
+// Scales and mins of sub-blocks 2c and 2c+1 (get_scale_min_k4 of the
+// reference, quants.rs) as two bytes each: svp = sv(2c) | sv(2c+1) << 8,
+// mvp likewise.  The two sub-blocks share one byte pair of each scale word.
+RT_DEV void q4k_scale_min_pair(uint32_t s0, uint32_t s1, uint32_t s2, int c, uint32_t &svp, uint32_t &mvp) {
+  const int sh = (c & 1) * 16;
+  const uint32_t a = __builtin_amdgcn_ubfe(s0, sh, 16);  // sc[j], sc[j+1]          (j = 2c mod 4)
+  const uint32_t b = __builtin_amdgcn_ubfe(s1, sh, 16);  // sc[j+4], sc[j+5]
+  const uint32_t d = __builtin_amdgcn_ubfe(s2, sh, 16);  // sc[j+8], sc[j+9]
+  if (c < 2) {
+    svp = a & 0x3F3Fu;
+    mvp = b & 0x3F3Fu;
+  } else {
+    svp = (d & 0x0F0Fu) | ((a >> 2) & 0x3030u);
+    mvp = ((d >> 4) & 0x0F0Fu) | ((b >> 2) & 0x3030u);
+  }
 }
 
 RT_DEV float q4k_chunk_dot_digits(const uint4 hd, const uint4 qa, const uint4 qb, int c, const ChunkD &x,
                                   uint32_t m4) {
   const float d = half_bits_to_f32(hd.x & 0xFFFFu);
   const float dm = half_bits_to_f32(hd.x >> 16);
-  uint32_t sv1, mv1, sv2, mv2;
-  q4k_scale_min(hd.y, hd.z, hd.w, 2 * c, sv1, mv1);
-  q4k_scale_min(hd.y, hd.z, hd.w, 2 * c + 1, sv2, mv2);
+  uint32_t svp, mvp;
+  q4k_scale_min_pair(hd.y, hd.z, hd.w, c, svp, mvp);
   const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-  uint32_t l0 = 0, l1 = 0, h0 = 0, h1 = 0;
-  int l2 = 0, h2 = 0;
+  uint32_t l0 = 0, h0 = 0;
+  int l1 = 0, h1 = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const uint32_t lo = w[i] & m4;         // nibbles of elements 4i..4i+3 (low half of the chunk)
     const uint32_t hi = (w[i] >> 4) & m4;  // elements 32+4i..32+4i+3
     l0 = __builtin_amdgcn_udot4(lo, x.d0[i], l0, false);
-    l1 = __builtin_amdgcn_udot4(lo, x.d1[i], l1, false);
-    l2 = __builtin_amdgcn_sdot4((int)lo, x.d2[i], l2, false);
+    l1 = __builtin_amdgcn_sdot4((int)lo, x.d1[i], l1, false);
     h0 = __builtin_amdgcn_udot4(hi, x.d0[8 + i], h0, false);
-    h1 = __builtin_amdgcn_udot4(hi, x.d1[8 + i], h1, false);
-    h2 = __builtin_amdgcn_sdot4((int)hi, x.d2[8 + i], h2, false);
+    h1 = __builtin_amdgcn_sdot4((int)hi, x.d1[8 + i], h1, false);
   }
-  const float dot_lo = ((float)l2 * 65536.0f + (float)l1 * 256.0f) + (float)l0;
-  const float dot_hi = ((float)h2 * 65536.0f + (float)h1 * 256.0f) + (float)h0;
-  const float scale1 = d * (float)sv1 * x.delta, min1 = dm * (float)mv1;
-  const float scale2 = d * (float)sv2 * x.delta, min2 = dm * (float)mv2;
-  return scale1 * dot_lo - min1 * x.sum_lo + scale2 * dot_hi - min2 * x.sum_hi;
+  const float dot_lo = fmaf((float)l1, 256.0f, (float)l0);  // exact: |value| < 2^24
+  const float dot_hi = fmaf((float)h1, 256.0f, (float)h0);
+  const float sv1 = (float)(svp & 0xFFu), sv2 = (float)(svp >> 8);
+  const float mv1 = (float)(mvp & 0xFFu), mv2 = (float)(mvp >> 8);
+  const float qsum = fmaf(sv2, dot_hi, sv1 * dot_lo);
+  const float msum = fmaf(mv2, x.sum_hi, mv1 * x.sum_lo);
+  return fmaf(d * x.delta, qsum, -(dm * msum));
 }
 
 template <int NB, int T, int ITERS>

@@ -77,6 +77,11 @@ RT_DEV float dpp(float v) {
   return bits_f32((uint32_t)__builtin_amdgcn_update_dpp(0, (int)f32_bits(v), CTRL, ROW_MASK, BANK_MASK, BOUND));
 }
 
+template <int CTRL, int ROW_MASK = 0xF, int BANK_MASK = 0xF, bool BOUND = false>
+RT_DEV uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, BANK_MASK, BOUND);
+}
+
 // Sum over aligned groups of 4 lanes; every lane of the group gets the sum.
 RT_DEV float quad_sum(float v) {
   v += dpp<0xB1>(v);  // quad_perm [1,0,3,2]

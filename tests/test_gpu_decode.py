@@ -52,6 +52,23 @@ def test_tiny_decode_step_matches_oracle(rt, orc, group, pos):
     d.close()
 
 
+@pytest.mark.parametrize("group", [2, 4])
+@pytest.mark.parametrize("window,max_seq,pos", [(40, 300, 250), (37, 200, 63), (0, 130, 129)])
+def test_tiny_decode_ragged_chunks(rt, orc, group, window, max_seq, pos):
+    """Key spans that split into several chunks whose last 16-key sub-chunk is
+    partly filled (global: 251 keys over 5 chunks of 51; window 40 over 3
+    chunks of 14), a window that does not divide into 16, and global_every 0
+    with the new row the last of max_seq."""
+    cfg = tiny(group, sliding_window=window, global_every=0 if window == 0 else 6)
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=pos, seed=900 + pos + group)
+    d = build_ctx(rt, cfg, layers, embed, fnorm, pos, max_seq)
+    got = d.decode_step(5, pos)
+    ref = orc.gemma3_decode_step(cfg, layers, embed, fnorm, token=5, pos=pos)
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, ref) < LOGITS_TOL
+    d.close()
+
+
 def test_tiny_multi_step_kv_append_and_graph_replay(rt, orc):
     """Several consecutive steps replay one captured graph; K/V rows appended
     by the GPU match the oracle's cache.append rows."""

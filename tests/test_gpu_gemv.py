@@ -74,7 +74,10 @@ def test_q4k_gemv_matches_oracle(rt, orc, dev, n, k):
     ref = orc.q4k_gemv(blocks, n, k, a)
     assert np.all(np.isfinite(got))
     assert rel_l2(got, ref) < GEMV_TOL
-    assert rel_l2(got, orc.q4k_gemv_f64(blocks, n, k, a)) < 1e-5
+    # Tighter bar against the f64 sum: the K=2560 kernels stage activations as
+    # 16-bit integers per 64-element chunk (about 3e-5 rel-L2 on N(0,1)), the
+    # f32-staged kernels reach about 1e-7.
+    assert rel_l2(got, orc.q4k_gemv_f64(blocks, n, k, a)) < 1e-4
 
 
 def test_q4k_gemv_reference_fixtures(rt, orc):
