@@ -123,7 +123,7 @@ template <int NB, int T, int ITERS, Pro MODE>
 __global__ __launch_bounds__(T) void k_qkv(DecodeArgs a, LayerArgs L, LayerArgs prev) {
   using Tile = Q4KTile<NB, T, ITERS>;
   constexpr int K = NB * 256;
-  __shared__ __attribute__((aligned(16))) float xl[NB * 4 * kXPitch];
+  __shared__ __attribute__((aligned(16))) uint32_t dl[NB * 4 * kDPitch];
   __shared__ float red[Tile::ROWS * NB];
   __shared__ float bred[T / 64];
   const int qd = a.n_q_heads * a.head_dim, kvd = a.n_kv_heads * a.head_dim;
@@ -143,58 +143,46 @@ __global__ __launch_bounds__(T) void k_qkv(DecodeArgs a, LayerArgs L, LayerArgs 
   pro_load<K, T, MODE>(a, a.x2, a.dn, prev.g_post_ffn, L.g_in, pr);
   Tile tile;
   tile.load([&](int rl) -> const uint8_t * { return W + (size_t)(r0 + rl) * row_bytes; }, W);
-  pro_finish<K, T, MODE>(a, pr, a.hid, xl, bred);
+  pro_finish<K, T, MODE, true>(a, pr, a.hid, dl, bred);
   __syncthreads();
-  ChunkX cx;
-  chunkx_from_lds(xl, tile.slot, cx);
-  tile.compute(cx, red);
+  ChunkD cx;
+  chunkd_from_lds(dl, tile.slot, cx);
+  tile.compute_digits(cx, red);
   __syncthreads();
   for (int i = threadIdx.x; i < Tile::ROWS; i += T) y[r0 + i] = reduce_row<NB>(red, i);
 }
 
 // ---------------------------------------------------------------------------
-// k_gateup: x2 = hid + rms(o)(1+g_pa); n2 = rms(x2)(1+g_pf); then persistent
-// workgroups walk tiles of RPI gate rows + the same RPI up rows (double
-// buffered) and store h[j] = gelu_tanh(gate[j]) * up[j]  (transformer4.rs:328-334)
+// k_gateup: x2 = hid + rms(o)(1+g_pa); n2 = rms(x2)(1+g_pf); each workgroup
+// then computes RPI gate rows and the same RPI up rows and stores
+// h[j] = gelu_tanh(gate[j]) * up[j]  (transformer4.rs:328-334)
 // ---------------------------------------------------------------------------
 template <int NB, int T>
-__global__ __launch_bounds__(T) void k_gateup(DecodeArgs a, LayerArgs L, int ffn) {
+__global__ __launch_bounds__(T) void k_gateup(DecodeArgs a, LayerArgs L) {
   using Tile = Q4KTile<NB, T, 2>;  // iteration 0: gate rows, 1: up rows
   constexpr int K = NB * 256;
   constexpr int RPI = Tile::RPI;
   __shared__ __attribute__((aligned(16))) uint32_t dl[NB * 4 * kDPitch];
-  __shared__ float red[2][Tile::ROWS * NB];
+  __shared__ float red[Tile::ROWS * NB];
   __shared__ float bred[T / 64];
   const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
-  const int ntiles = ffn / RPI;  // RPI divides ffn (checked on the host)
-  auto rows_of = [&](int tile) {
-    return [=](int rl) -> const uint8_t * {
-      if (tile >= ntiles) return nullptr;
-      const int j = tile * RPI + (rl < RPI ? rl : rl - RPI);
-      return (rl < RPI ? L.wgate : L.wup) + (size_t)j * row_bytes;
-    };
-  };
-  int t = (int)blockIdx.x;
+  const int j0 = (int)blockIdx.x * RPI;  // RPI divides ffn (checked on the host)
   ProRegs<K, T> pr;
   pro_load<K, T, Pro::Resid>(a, a.hid, a.o, L.g_post_attn, L.g_pre_ffn, pr);
-  Tile cur, nxt;
-  cur.load(rows_of(t), L.wgate);
+  Tile tile;
+  tile.load([&](int rl) -> const uint8_t * {
+    return rl < RPI ? L.wgate + (size_t)(j0 + rl) * row_bytes : L.wup + (size_t)(j0 + rl - RPI) * row_bytes;
+  }, L.wgate);
   pro_finish<K, T, Pro::Resid, true>(a, pr, a.x2, dl, bred);
   __syncthreads();
   ChunkD cx;
-  chunkd_from_lds(dl, cur.slot, cx);
-  int buf = 0;
-  for (; t < ntiles; t += (int)gridDim.x) {
-    nxt.load(rows_of(t + (int)gridDim.x), L.wgate);
-    cur.compute_digits(cx, red[buf]);
-    __syncthreads();
-    for (int i = threadIdx.x; i < RPI; i += T) {
-      const float g = reduce_row<NB>(red[buf], i);
-      const float u = reduce_row<NB>(red[buf], RPI + i);
-      a.h[t * RPI + i] = mul_nc(gelu_tanh(g), u);
-    }
-    buf ^= 1;
-    cur = nxt;
+  chunkd_from_lds(dl, tile.slot, cx);
+  tile.compute_digits(cx, red);
+  __syncthreads();
+  for (int i = threadIdx.x; i < RPI; i += T) {
+    const float g = reduce_row<NB>(red, i);
+    const float u = reduce_row<NB>(red, RPI + i);
+    a.h[j0 + i] = mul_nc(gelu_tanh(g), u);
   }
 }
 
@@ -203,56 +191,26 @@ __global__ __launch_bounds__(T) void k_gateup(DecodeArgs a, LayerArgs L, int ffn
 // ---------------------------------------------------------------------------
 template <int NB, int T, int ITERS>
 __global__ __launch_bounds__(T) void k_gemv(const uint8_t *__restrict__ W, const float *__restrict__ x,
-                                            float *__restrict__ y) {
+                                            float *__restrict__ y, int n) {
   using Tile = Q4KTile<NB, T, ITERS>;
-  __shared__ __attribute__((aligned(16))) float xl[NB * 4 * kXPitch];
+  __shared__ __attribute__((aligned(16))) uint32_t dl[NB * 4 * kDPitch];
   __shared__ float red[Tile::ROWS * NB];
-  const int row0 = (int)blockIdx.x * Tile::ROWS;  // ROWS divides N (checked on the host)
+  const int row0 = (int)blockIdx.x * Tile::ROWS;
   const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
   XRegs<NB * 256, T> xr;
   x_load<NB * 256, T>(x, xr);
   Tile tile;
-  tile.load([&](int rl) -> const uint8_t * { return W + (size_t)(row0 + rl) * row_bytes; }, W);
-  x_store<NB * 256, T>(xr, xl);
+  tile.load([&](int rl) -> const uint8_t * {
+    return row0 + rl < n ? W + (size_t)(row0 + rl) * row_bytes : nullptr;
+  }, W);
+  x_store_digits<NB * 256, T>(xr, dl);
   __syncthreads();
-  ChunkX cx;
-  chunkx_from_lds(xl, tile.slot, cx);
-  tile.compute(cx, red);
+  ChunkD cx;
+  chunkd_from_lds(dl, tile.slot, cx);
+  tile.compute_digits(cx, red);
   __syncthreads();
-  for (int i = threadIdx.x; i < Tile::ROWS; i += T) y[row0 + i] = reduce_row<NB>(red, i);
-}
-
-// Persistent, double-buffered variant (the K=10240 down projection).
-template <int NB, int T>
-__global__ __launch_bounds__(T) void k_gemv_persist(const uint8_t *__restrict__ W, const float *__restrict__ x,
-                                                    float *__restrict__ y, int n) {
-  using Tile = Q4KTile<NB, T, 1>;
-  constexpr int RPI = Tile::RPI;
-  __shared__ __attribute__((aligned(16))) float xl[NB * 4 * kXPitch];
-  __shared__ float red[2][RPI * NB];
-  const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
-  const int ntiles = n / RPI;  // RPI divides n (checked on the host)
-  auto rows_of = [&](int tile) {
-    return [=](int rl) -> const uint8_t * { return tile < ntiles ? W + (size_t)(tile * RPI + rl) * row_bytes : nullptr; };
-  };
-  int t = (int)blockIdx.x;
-  XRegs<NB * 256, T> xr;
-  x_load<NB * 256, T>(x, xr);
-  Tile cur, nxt;
-  cur.load(rows_of(t), W);
-  x_store<NB * 256, T>(xr, xl);
-  __syncthreads();
-  ChunkX cx;
-  chunkx_from_lds(xl, cur.slot, cx);
-  int buf = 0;
-  for (; t < ntiles; t += (int)gridDim.x) {
-    nxt.load(rows_of(t + (int)gridDim.x), W);
-    cur.compute(cx, red[buf]);
-    __syncthreads();
-    for (int i = threadIdx.x; i < RPI; i += T) y[t * RPI + i] = reduce_row<NB>(red[buf], i);
-    buf ^= 1;
-    cur = nxt;
-  }
+  for (int i = threadIdx.x; i < Tile::ROWS; i += T)
+    if (row0 + i < n) y[row0 + i] = reduce_row<NB>(red, i);
 }
 
 // ---------------------------------------------------------------------------
@@ -444,12 +402,14 @@ __global__ __launch_bounds__(256) void k_attn(DecodeArgs a, LayerArgs L) {
 // ---------------------------------------------------------------------------
 // k_attn_combine: merge the chunk partials of one q head and 64 dimensions.
 //   out[d] = sum_i o_i[d] e^(m_i - M) / sum_i l_i e^(m_i - M),  M = max_i m_i
-// 256 threads = 4 chunk groups x 64 dimensions, each group merging its
-// chunks online in one pass, then the four groups through LDS; grid
+// 256 threads = 4 chunk groups x 64 dimensions.  A thread loads the partials
+// of up to R chunks at once (all loads in flight together), folds them into
+// its running (M, L, O), and the four groups merge through LDS; grid
 // (n_q_heads, D/64).
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(256) void k_attn_combine(DecodeArgs a, int nchunk) {
+  constexpr int R = 20;  // 80 chunks per batch: one batch for the Gemma-3 shapes
   __shared__ float gm[4], gl[4];
   __shared__ float go[4][64];
   const int h = blockIdx.x, d0 = blockIdx.y * 64;
@@ -458,16 +418,31 @@ __global__ __launch_bounds__(256) void k_attn_combine(DecodeArgs a, int nchunk) 
   const float *pl = a.part_l + (size_t)h * nchunk;
   const float *po = a.part_o + (size_t)h * nchunk * D + d0 + dl;
   float M = -INFINITY, Ls = 0.f, O = 0.f;
-#pragma unroll 4
-  for (int i = cg; i < nchunk; i += 4) {
-    const float mi = pm[i], li = pl[i], oi = po[(size_t)i * D];
-    const bool ok = mi != -INFINITY;      // empty chunks carry m = -inf, l = 0
-    const float mn = ok ? fmaxf(M, mi) : M;
-    const float r_old = M == -INFINITY ? 0.f : expf(M - mn);
-    const float r_new = ok ? expf(mi - mn) : 0.f;
-    Ls = Ls * r_old + li * r_new;
-    O = O * r_old + oi * r_new;
-    M = mn;
+  for (int base = cg; base < nchunk; base += 4 * R) {
+    float mi[R], li[R], oi[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int i = min(base + 4 * r, nchunk - 1);  // clamped, unconditional loads
+      mi[r] = pm[i];
+      li[r] = pl[i];
+      oi[r] = po[(size_t)i * D];
+    }
+    float mb = M;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (base + 4 * r < nchunk) mb = fmaxf(mb, mi[r]);  // empty chunks carry m = -inf, l = 0
+    if (mb != -INFINITY) {
+      const float sc = expf(M - mb);  // 0 while M is still -inf
+      Ls *= sc;
+      O *= sc;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float w = (base + 4 * r < nchunk && mi[r] != -INFINITY) ? expf(mi[r] - mb) : 0.f;
+        Ls = fmaf(li[r], w, Ls);
+        O = fmaf(oi[r], w, O);
+      }
+      M = mb;
+    }
   }
   if (dl == 0) {
     gm[cg] = M;
@@ -568,25 +543,16 @@ static void launch_qkv(Launch &l, const DecodeArgs &a, const LayerArgs &L, const
 }
 
 template <int NB, int T>
-static void launch_gateup(Launch &l, const DecodeArgs &a, const LayerArgs &L, int ffn, int grid) {
+static void launch_gateup(Launch &l, const DecodeArgs &a, const LayerArgs &L, int ffn) {
   constexpr int RPI = T / (NB * 4);
-  const int ntiles = ffn / RPI;
-  hipLaunchKernelGGL((k_gateup<NB, T>), dim3(grid < ntiles ? grid : ntiles), dim3(T), 0, l.s, a, L, ffn);
-  l.check();
-}
-
-template <int NB, int T>
-static void launch_gemv_persist(Launch &l, const uint8_t *W, const float *x, float *y, int n, int grid) {
-  constexpr int RPI = T / (NB * 4);
-  const int ntiles = n / RPI;
-  hipLaunchKernelGGL((k_gemv_persist<NB, T>), dim3(grid < ntiles ? grid : ntiles), dim3(T), 0, l.s, W, x, y, n);
+  hipLaunchKernelGGL((k_gateup<NB, T>), dim3(ffn / RPI), dim3(T), 0, l.s, a, L);
   l.check();
 }
 
 template <int NB, int T, int ITERS>
 static void launch_gemv(Launch &l, const uint8_t *W, const float *x, float *y, int n) {
   constexpr int ROWS = Q4KTile<NB, T, ITERS>::ROWS;
-  hipLaunchKernelGGL((k_gemv<NB, T, ITERS>), dim3(n / ROWS), dim3(T), 0, l.s, W, x, y);
+  hipLaunchKernelGGL((k_gemv<NB, T, ITERS>), dim3((n + ROWS - 1) / ROWS), dim3(T), 0, l.s, W, x, y, n);
   l.check();
 }
 
@@ -637,18 +603,18 @@ hipError_t enqueue_decode_step(const DecodeShape &s, const DecodeArgs &a, const 
     const LayerArgs &L = layers[li];
     const LayerArgs &P = layers[li > 0 ? li - 1 : 0];
     const int qkv_rows = qd + 2 * kvd;
-    if (big) launch_qkv<10, 320, 1>(l, a, L, P, li == 0, qkv_rows);
+    if (big) launch_qkv<10, 640, 1>(l, a, L, P, li == 0, qkv_rows);
     else launch_qkv<2, 256, 1>(l, a, L, P, li == 0, qkv_rows);
     const int nchunk = L.window > 0 ? s.nchunk_local : s.nchunk_global;
     if (s.head_dim == 256)
       launch_attn_d<256>(l, a, L, nchunk, group);
     else
       launch_attn_d<128>(l, a, L, nchunk, group);
-    if (qd == 2048) launch_gemv<8, 256, 1>(l, L.wo, a.attn, a.o, s.hidden);
+    if (qd == 2048) launch_gemv<8, 512, 1>(l, L.wo, a.attn, a.o, s.hidden);
     else launch_gemv<2, 256, 1>(l, L.wo, a.attn, a.o, s.hidden);
-    if (big) launch_gateup<10, 320>(l, a, L, s.ffn, 640);
-    else launch_gateup<2, 256>(l, a, L, s.ffn, 64);
-    if (s.ffn == 10240) launch_gemv_persist<40, 320>(l, L.wdown, a.h, a.dn, s.hidden, 512);
+    if (big) launch_gateup<10, 640>(l, a, L, s.ffn);
+    else launch_gateup<2, 256>(l, a, L, s.ffn);
+    if (s.ffn == 10240) launch_gemv<40, 960, 1>(l, L.wdown, a.h, a.dn, s.hidden);
     else launch_gemv<4, 256, 1>(l, L.wdown, a.h, a.dn, s.hidden);
   }
   if (l.err == hipSuccess) {
@@ -664,14 +630,10 @@ hipError_t enqueue_decode_step(const DecodeShape &s, const DecodeArgs &a, const 
 bool decode_rows_divisible(const DecodeShape &s, const char **why) {
   const int qd = s.n_q_heads * s.head_dim, kvd = s.n_kv_heads * s.head_dim;
   const bool big = s.hidden == 2560;
-  const int qkv_rows_per_wg = big ? rows_per_iter<10, 320>() : rows_per_iter<2, 256>();
+  const int qkv_rows_per_wg = big ? rows_per_iter<10, 640>() : rows_per_iter<2, 256>();
   if (qd % qkv_rows_per_wg || kvd % qkv_rows_per_wg) return *why = "q/kv rows must divide into workgroup tiles", false;
-  const int o_rows = qd == 2048 ? rows_per_iter<8, 256>() : rows_per_iter<2, 256>();
-  if (s.hidden % o_rows) return *why = "hidden rows must divide into o-proj tiles", false;
   if (s.ffn % qkv_rows_per_wg) return *why = "ffn rows must divide into gate/up tiles", false;
-  const int d_rows = s.ffn == 10240 ? rows_per_iter<40, 320>() : rows_per_iter<4, 256>();
-  if (s.hidden % d_rows) return *why = "hidden rows must divide into down-proj tiles", false;
-  return true;
+  return true;  // the o and down GEMVs bound their rows themselves
 }
 
 }  // namespace rt

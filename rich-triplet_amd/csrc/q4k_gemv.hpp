@@ -214,13 +214,12 @@ RT_DEV void q4k_scale_min_pair(uint32_t s0, uint32_t s1, uint32_t s2, int c, uin
   const uint32_t a = __builtin_amdgcn_ubfe(s0, sh, 16);  // sc[j], sc[j+1]          (j = 2c mod 4)
   const uint32_t b = __builtin_amdgcn_ubfe(s1, sh, 16);  // sc[j+4], sc[j+5]
   const uint32_t d = __builtin_amdgcn_ubfe(s2, sh, 16);  // sc[j+8], sc[j+9]
-  if (c < 2) {
-    svp = a & 0x3F3Fu;
-    mvp = b & 0x3F3Fu;
-  } else {
-    svp = (d & 0x0F0Fu) | ((a >> 2) & 0x3030u);
-    mvp = ((d >> 4) & 0x0F0Fu) | ((b >> 2) & 0x3030u);
-  }
+  // both layouts, then a select (lanes of one wave hold different c)
+  const uint32_t sv_lo = a & 0x3F3Fu, mv_lo = b & 0x3F3Fu;
+  const uint32_t sv_hi = (d & 0x0F0Fu) | ((a >> 2) & 0x3030u);
+  const uint32_t mv_hi = ((d >> 4) & 0x0F0Fu) | ((b >> 2) & 0x3030u);
+  svp = c < 2 ? sv_lo : sv_hi;
+  mvp = c < 2 ? mv_lo : mv_hi;
 }
 
 RT_DEV float q4k_chunk_dot_digits(const uint4 hd, const uint4 qa, const uint4 qb, int c, const ChunkD &x,

@@ -129,58 +129,6 @@ __global__ __launch_bounds__(T) void k_q4k_gemv_dig(const uint8_t *__restrict__ 
   }
 }
 
-// Persistent workgroups walk row tiles (RPI rows each) with the next tile's
-// loads issued before the current tile's arithmetic (double buffering); the
-// activations are staged once per workgroup.
-template <int NB, int T, bool DIG>
-__global__ __launch_bounds__(T) void k_q4k_gemv_persist(const uint8_t *__restrict__ W, const float *__restrict__ x,
-                                                        float *__restrict__ y, int N) {
-  using Tile = Q4KTile<NB, T, 1>;
-  constexpr int RPI = Tile::RPI;
-  constexpr int LDS_WORDS = NB * 4 * (DIG ? kDPitch : kXPitch);
-  __shared__ __attribute__((aligned(16))) uint32_t lds[LDS_WORDS];
-  __shared__ float red[2][RPI * NB];
-  const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
-  const int ntiles = (N + RPI - 1) / RPI;
-  auto rows_of = [&](int tile) {
-    return [=](int rl) -> const uint8_t * {
-      const int r = tile * RPI + rl;
-      return (tile < ntiles && r < N) ? W + (size_t)r * row_bytes : nullptr;
-    };
-  };
-  int t = (int)blockIdx.x;
-  Tile cur, nxt;
-  XRegs<NB * 256, T> xr;
-  x_load<NB * 256, T>(x, xr);
-  cur.load(rows_of(t), W);
-  ChunkX cxf;
-  ChunkD cxd;
-  if constexpr (DIG) {
-    x_store_digits<NB * 256, T>(xr, lds);
-    __syncthreads();
-    chunkd_from_lds(lds, cur.slot, cxd);
-  } else {
-    x_store<NB * 256, T>(xr, reinterpret_cast<float *>(lds));
-    __syncthreads();
-    chunkx_from_lds(reinterpret_cast<const float *>(lds), cur.slot, cxf);
-  }
-  int buf = 0;
-  for (; t < ntiles; t += (int)gridDim.x) {
-    nxt.load(rows_of(t + (int)gridDim.x), W);
-    if constexpr (DIG)
-      cur.compute_digits(cxd, red[buf]);
-    else
-      cur.compute(cxf, red[buf]);
-    __syncthreads();
-    for (int i = threadIdx.x; i < RPI; i += T) {
-      const int r = t * RPI + i;
-      if (r < N) y[r] = reduce_row<NB>(red[buf], i);
-    }
-    buf ^= 1;
-    cur = nxt;
-  }
-}
-
 // Any K (multiple of 256): one wave per row, lanes stride over the row's chunks.
 __global__ __launch_bounds__(256) void k_q4k_gemv_generic(const uint8_t *__restrict__ W, const float *__restrict__ x,
                                                           float *__restrict__ y, int N, int K) {
@@ -254,34 +202,33 @@ hipError_t launch_q4k_gemv_generic(const void *W, const float *x, float *y, int 
   return hipGetLastError();
 }
 
-template <int NB, int T, bool DIG>
-static hipError_t launch_persist(const void *W, const float *x, float *y, int N, int grid, hipStream_t s) {
-  constexpr int RPI = T / (NB * 4);
-  const int ntiles = (N + RPI - 1) / RPI;
-  grid = grid < ntiles ? grid : ntiles;
-  hipLaunchKernelGGL((k_q4k_gemv_persist<NB, T, DIG>), dim3(grid), dim3(T), 0, s, (const uint8_t *)W, x, y, N);
+template <int NB, int T, int ITERS>
+static hipError_t launch_dig(const void *W, const float *x, float *y, int N, hipStream_t s) {
+  constexpr int ROWS = Q4KTile<NB, T, ITERS>::ROWS;
+  const unsigned grid = (unsigned)((N + ROWS - 1) / ROWS);
+  hipLaunchKernelGGL((k_q4k_gemv_dig<NB, T, ITERS>), dim3(grid), dim3(T), 0, s, (const uint8_t *)W, x, y, N);
   return hipGetLastError();
 }
 
 // Kernel choice per shape, from measurements on MI355X (graph-launched, cold
-// weights): K=2560 uses digit-staged activations (one row-iteration per
-// workgroup up to ~12k rows, persistent tiles beyond); K=10240 uses persistent
-// double-buffered tiles with f32 activations; other K's use the f32 tile.
+// weights, 34 distinct matrices back to back).  The Gemma-3 shapes use
+// digit-staged activations with workgroup sizes that trade activation staging
+// (once per workgroup) against parallelism: K=2560 with 8 rows per workgroup
+// up to 8k rows, 48 rows (960 threads, two row-iterations) up to 12k, 32 rows
+// beyond; K=2048 with 16 rows; K=10240 with 6 rows (960 threads).  Other K's
+// use the f32-staged tile.
 hipError_t launch_q4k_gemv(const void *W, const float *x, float *y, int N, int K, hipStream_t s) {
   switch (K / kQ4KBlockElems) {
     case 1: return launch_cr_auto<1, 256>(W, x, y, N, s);
     case 2: return launch_cr_auto<2, 256>(W, x, y, N, s);
     case 4: return launch_cr_auto<4, 256>(W, x, y, N, s);
-    case 8: return launch_cr_auto<8, 256>(W, x, y, N, s);
+    case 8: return launch_dig<8, 512, 1>(W, x, y, N, s);
     case 10:
-      if (N > 12288) return launch_persist<10, 320, true>(W, x, y, N, 768, s);
-      {
-        const unsigned grid = (unsigned)((N + 7) / 8);
-        hipLaunchKernelGGL((k_q4k_gemv_dig<10, 320, 1>), dim3(grid), dim3(320), 0, s, (const uint8_t *)W, x, y, N);
-        return hipGetLastError();
-      }
+      if (N > 12288) return launch_dig<10, 640, 2>(W, x, y, N, s);
+      if (N >= 8192) return launch_dig<10, 960, 2>(W, x, y, N, s);
+      return launch_dig<10, 320, 1>(W, x, y, N, s);
     case 16: return launch_cr_auto<16, 256>(W, x, y, N, s);
-    case 40: return launch_persist<40, 320, false>(W, x, y, N, 512, s);
+    case 40: return launch_dig<40, 960, 1>(W, x, y, N, s);
     default: break;
   }
   return launch_q4k_gemv_generic(W, x, y, N, K, s);
