@@ -219,7 +219,7 @@ def main() -> int:
     dom = per_shape["gate"]
     roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(dom["GBps"] / PEAK_HBM_GBS, 4), "traffic": measured_traffic(),
-                "kernel": "k_q4k_gemv_dig<NB=10,T=320,ITERS=1> (Q4_K GEMV 10240x2560)",
+                "kernel": "k_q4k_gemv_dig<NB=10,T=960,ITERS=2> (Q4_K GEMV 10240x2560)",
                 "bytes_per_launch": dom["bytes_per_launch"], "us_per_launch": dom["us_per_launch"]}
     log(f"dominant kernel gate 10240x2560: {dom['us_per_launch']} us/launch, {dom['GBps']} GB/s")
 
