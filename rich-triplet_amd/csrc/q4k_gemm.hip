@@ -24,6 +24,8 @@
 // to f16: 1.5 VALU operations per weight.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "rt_device.hpp"
 #include "rt_kernels.hpp"
 
@@ -216,11 +218,14 @@ RT_DEV half8 dq_step(uint32_t w0, uint32_t w1, float s, float negc) {
 // ---------------------------------------------------------------------------
 constexpr int kW8bSlotW = 4 * 256 * 16;  // 16 KB
 
+// Split-K: blockIdx.y = s takes chunks [s*nchunks/ksplit, (s+1)*nchunks/ksplit)
+// and, when ksplit > 1, writes its scaled partial tile to c + s*M*N for
+// k_gemm_splitk_sum.
 template <int WGM>
 __global__ __launch_bounds__(512) void k_q4k_gemm_w8b(const _Float16 *__restrict__ a16, const int *__restrict__ ea,
                                                       const uint8_t *__restrict__ w, const int *__restrict__ ew,
                                                       float *__restrict__ c, int M, int N, int K, int tiles_m,
-                                                      int tiles_n) {
+                                                      int tiles_n, int ksplit) {
   constexpr int BM = 128 * WGM, WN = 8 / WGM, NT = 256 / WN / 32;
   constexpr int IA = BM / 64;            // A copies per wave per chunk (BM rows x 128 B / 1 KB / 8 waves)
   constexpr int SLOT_A = BM * 128;       // bytes
@@ -242,6 +247,10 @@ __global__ __launch_bounds__(512) void k_q4k_gemm_w8b(const _Float16 *__restrict
   const int m0 = tm * BM, n0 = tn * 256;
   const int nblocks = K / 256, nchunks = K / kBK;
   const size_t row_bytes = (size_t)nblocks * kQ4KBlockBytes;
+  const int split = (int)blockIdx.y;
+  const int kc0 = split * nchunks / ksplit, kc1 = (split + 1) * nchunks / ksplit;  // >= 1 chunk (host: ksplit <= nchunks)
+  const int nloc = kc1 - kc0;
+  if (ksplit > 1) c += (size_t)split * M * N;
 
   // A copy i of this wave: slot rows 8*(IA*wave+i) + [0,8); lane -> row
   // r = 8*(IA*wave+i) + lane/8, physical segment lane%8, logical segment
@@ -286,21 +295,23 @@ __global__ __launch_bounds__(512) void k_q4k_gemm_w8b(const _Float16 *__restrict
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[i][j] = floatx16{};
 
-  issue(0, 0);
-  issue(min(1, nchunks - 1), 1);
+  issue(kc0, 0);
+  issue(min(kc0 + 1, kc1 - 1), 1);
   wait_vmcnt<0>();
   wg_barrier();
 
-  // One chunk: compute from ring slot `slot`, prefetch chunk kc+2 into slot (slot+2)%3.
-  auto chunk = [&](int kc, int slot) __attribute__((always_inline)) {
-    if (kc > 0) {
+  // One chunk (local index lc, absolute kc): compute from ring slot `slot`,
+  // prefetch chunk kc+2 into slot (slot+2)%3.
+  auto chunk = [&](int lc, int slot) __attribute__((always_inline)) {
+    const int kc = kc0 + lc;
+    if (lc > 0) {
       // chunk kc's copies have landed everywhere; chunk kc+1's may stay in flight
       wait_vmcnt<IA + 2>();
       wait_lgkmcnt0();
       wg_barrier();
     }
     __builtin_amdgcn_sched_barrier(0);
-    issue(min(kc + 2, nchunks - 1), slot == 0 ? 2 : slot - 1);
+    issue(min(kc + 2, kc1 - 1), slot == 0 ? 2 : slot - 1);
     __builtin_amdgcn_sched_barrier(0);
 
     const uint8_t *pa = slotA(slot), *pw = slotW(slot);
@@ -358,14 +369,14 @@ __global__ __launch_bounds__(512) void k_q4k_gemm_w8b(const _Float16 *__restrict
     }
   };
 
-  int kc = 0;
-  for (; kc + 3 <= nchunks; kc += 3) {
-    chunk(kc, 0);
-    chunk(kc + 1, 1);
-    chunk(kc + 2, 2);
+  int lc = 0;
+  for (; lc + 3 <= nloc; lc += 3) {
+    chunk(lc, 0);
+    chunk(lc + 1, 1);
+    chunk(lc + 2, 2);
   }
-  if (kc < nchunks) chunk(kc, 0);
-  if (kc + 1 < nchunks) chunk(kc + 1, 1);
+  if (lc < nloc) chunk(lc, 0);
+  if (lc + 1 < nloc) chunk(lc + 1, 1);
 
   // Epilogue: register r of tile (i, j) is C[128wm + 32i + 8(r/4) + 4g + r%4][colw[j]].
   int ecol[NT];
@@ -577,9 +588,41 @@ __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restric
 
 }  // namespace
 
+// Sums the split-K partial tiles in split order (deterministic):
+// c[i] = sum_s part[s*mn + i].
+__global__ __launch_bounds__(256) void k_gemm_splitk_sum(const float *__restrict__ part, float *__restrict__ c,
+                                                         size_t mn, int ksplit) {
+  const size_t n4 = mn / 4;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
+    float4 acc = reinterpret_cast<const float4 *>(part)[i];
+    for (int s = 1; s < ksplit; ++s) {
+      const float4 v = reinterpret_cast<const float4 *>(part + (size_t)s * mn)[i];
+      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+    }
+    reinterpret_cast<float4 *>(c)[i] = acc;
+  }
+  for (size_t i = n4 * 4 + (size_t)blockIdx.x * 256 + threadIdx.x; i < mn; i += (size_t)gridDim.x * 256) {
+    float acc = part[i];
+    for (int s = 1; s < ksplit; ++s) acc += part[(size_t)s * mn + i];
+    c[i] = acc;
+  }
+}
+
+// Split-K count for the eight-wave kernel: enough workgroups to cover the 256
+// CUs when the output has few 128x256 tiles (a prefill's down projection,
+// M=512 N=2560: 40 tiles), keeping at least 16 chunks (K=1024) per split.
+int gemm_ksplit(int M, int N, int K) {
+  if (M > 1024) return 1;
+  const int ntiles = ((M + 127) / 128) * ((N + 255) / 256);
+  const int by_cus = 256 / ntiles, by_k = (K / kBK) / 16;
+  return max(1, min(by_cus, by_k));
+}
+
 size_t q4k_gemm_workspace_bytes(int M, int N, int K) {
   auto r256 = [](size_t b) { return (b + 255) & ~size_t(255); };
-  return r256((size_t)M * K * 2) + r256((size_t)M * 4) + r256((size_t)N * 4);
+  const int ks = gemm_ksplit(M, N, K);
+  return r256((size_t)M * K * 2) + r256((size_t)M * 4) + r256((size_t)N * 4) +
+         (ks > 1 ? r256((size_t)ks * M * N * 4) : 0);
 }
 
 hipError_t launch_q4k_gemm(const void *a, bool a_bf16, const void *w, float *c, int M, int N, int K, void *ws,
@@ -603,9 +646,19 @@ hipError_t launch_q4k_gemm(const void *a, bool a_bf16, const void *w, float *c, 
   // hundred tokens gives too few 256-row tiles to fill the chip); above that
   // the half-block kernel, two workgroups per CU.
   const int tiles_m = (M + 127) / 128, tiles_n = (N + 255) / 256;
-  if (M <= 1024)
+  const int ks = gemm_ksplit(M, N, K);
+  if (ks > 1) {
+    float *part = reinterpret_cast<float *>(p + r256((size_t)M * K * 2) + r256((size_t)M * 4) + r256((size_t)N * 4));
+    hipLaunchKernelGGL(k_q4k_gemm_w8b<1>, dim3(tiles_m * tiles_n, ks), dim3(512), 0, s, a16, ea, wb, ew, part, M, N,
+                       K, tiles_m, tiles_n, ks);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const size_t mn = (size_t)M * N;
+    const unsigned grid = (unsigned)std::min<size_t>((mn / 4 + 255) / 256 + 1, 2048);
+    hipLaunchKernelGGL(k_gemm_splitk_sum, dim3(grid), dim3(256), 0, s, part, c, mn, ks);
+  } else if (M <= 1024)
     hipLaunchKernelGGL(k_q4k_gemm_w8b<1>, dim3(tiles_m * tiles_n), dim3(512), 0, s, a16, ea, wb, ew, c, M, N, K,
-                       tiles_m, tiles_n);
+                       tiles_m, tiles_n, 1);
   else
     hipLaunchKernelGGL(k_q4k_gemm_h, dim3(tiles_m * tiles_n), dim3(256), 0, s, a16, ea, wb, ew, c, M, N, K, tiles_m,
                        tiles_n);
