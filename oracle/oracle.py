@@ -48,6 +48,14 @@ def lib() -> C.CDLL:
             "orc_q4k_pack_scales": (None, [_u8p, _u8p, _u8p]),
             "orc_q4k_dequant_row": (None, [_u8p, _sz, _sz, _f32p]),
             "orc_q4k_dequant_gguf": (None, [_u8p, _sz, _f32p]),
+            "orc_f32_to_f16_trunc": (C.c_uint16, [C.c_float]),
+            "orc_q4k_quantize_block": (None, [_f32p, _u8p]),
+            "orc_q4k_quantize": (None, [_f32p, _sz, _sz, _u8p]),
+            "orc_q4_0_dequant": (None, [_u8p, _sz, _f32p]),
+            "orc_q4_0_to_q4k": (None, [_u8p, _sz, _sz, _u8p]),
+            "orc_q6k_dequant": (None, [_u8p, _sz, _f32p]),
+            "orc_q5k_dequant": (None, [_u8p, _sz, _f32p]),
+            "orc_q8_0_dequant": (None, [_u8p, _sz, _f32p]),
             "orc_q4k_dot_row": (C.c_float, [_u8p, _sz, _sz, _f32p]),
             "orc_q4k_gemv_mt": (None, [_u8p, _sz, _sz, _f32p, _f32p, C.c_int]),
             "orc_q4k_gemv_f64": (None, [_u8p, _sz, _sz, _f32p, _f64p]),
@@ -132,6 +140,44 @@ def q4k_dequant_gguf(blocks: np.ndarray, n_elem: int) -> np.ndarray:
     """gguf_loader.rs:551-621"""
     out = np.empty(n_elem, np.float32)
     lib().orc_q4k_dequant_gguf(np.ascontiguousarray(blocks, np.uint8), n_elem, out)
+    return out
+
+
+def f32_to_f16_trunc(v: float) -> int:
+    """Q4KMat::f32_to_f16 (autograd2.rs:1090-1117): mantissa truncated."""
+    return int(lib().orc_f32_to_f16_trunc(float(v)))
+
+
+def q4k_quantize(m: np.ndarray) -> np.ndarray:
+    """Q4KMat::quantize (autograd2.rs:1138-1168, quantize_block 1171-1245); m is [rows, cols]."""
+    m = np.ascontiguousarray(m, np.float32)
+    rows, cols = m.shape
+    out = np.zeros(rows * (cols // 256) * 144, np.uint8)
+    lib().orc_q4k_quantize(m, rows, cols, out)
+    return out
+
+
+def _dequant(fn: str, nbytes_per_block: int, elems_per_block: int):
+    def run(data: np.ndarray, n_elem: int) -> np.ndarray:
+        data = np.ascontiguousarray(data, np.uint8)
+        assert data.size >= (n_elem + elems_per_block - 1) // elems_per_block * nbytes_per_block
+        out = np.empty(n_elem, np.float32)
+        getattr(lib(), fn)(data, n_elem, out)
+        return out
+    return run
+
+
+q4_0_dequant = _dequant("orc_q4_0_dequant", 18, 32)    # gguf_loader.rs:425-480
+q6k_dequant = _dequant("orc_q6k_dequant", 210, 256)    # gguf_loader.rs:482-549
+q5k_dequant = _dequant("orc_q5k_dequant", 176, 256)    # gguf_loader.rs:664-743
+q8_0_dequant = _dequant("orc_q8_0_dequant", 34, 32)    # gguf_loader.rs:628-650
+
+
+def q4_0_to_q4k(data: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """load_linear_from_gguf's Q4_0 branch (transformer4.rs:1198-1207): Q4_0 bytes
+    of a [cols, rows] GGUF tensor -> Q4_K blocks of the [rows, cols] matrix."""
+    out = np.zeros(rows * (cols // 256) * 144, np.uint8)
+    lib().orc_q4_0_to_q4k(np.ascontiguousarray(data, np.uint8), rows, cols, out)
     return out
 
 

@@ -176,6 +176,231 @@ void orc_q4k_dequant_gguf(const uint8_t *bytes, size_t n_elem, float *out)
     }
 }
 
+/* ---- GGUF tensor formats and Q4_K quantisation ------------------------- */
+
+/* Q4KMat::f32_to_f16 (autograd2.rs:1090-1117).  Its comment says
+ * round-to-nearest, but the code drops the low 13 mantissa bits: truncation
+ * toward zero.  Restated as the code computes it (the quantiser stores d and
+ * dmin with it, so quantised bytes depend on it). */
+uint16_t orc_f32_to_f16_trunc(float val)
+{
+    uint32_t bits = f32_as_u32(val);
+    uint32_t sign = (bits >> 16) & 0x8000u;
+    int32_t exp = (int32_t)((bits >> 23) & 0xFFu);
+    uint32_t mant = bits & 0x7FFFFFu;
+    if (exp == 0xFF) return (uint16_t)(sign | 0x7C00u | (mant >> 13));
+    int32_t new_exp = exp - 127 + 15;
+    if (new_exp >= 0x1F) return (uint16_t)(sign | 0x7C00u);
+    if (new_exp <= 0) {
+        if (new_exp < -10) return (uint16_t)sign;
+        uint32_t m = mant | 0x800000u;
+        uint32_t shift = (uint32_t)(1 - new_exp) + 13u;
+        return (uint16_t)(sign | (m >> shift));
+    }
+    return (uint16_t)(sign | ((uint32_t)new_exp << 10) | (mant >> 13));
+}
+
+/* Rust's `f as u8`: saturating, NaN -> 0, truncation toward zero. */
+static uint8_t rust_f32_as_u8(float x)
+{
+    if (!(x > 0.0f)) return 0;
+    if (x >= 255.0f) return 255;
+    return (uint8_t)x;
+}
+
+/* Q4KMat::quantize_block (autograd2.rs:1171-1245). */
+void orc_q4k_quantize_block(const float *x, uint8_t out[144])
+{
+    float sub_scales[8], sub_mins[8];
+    for (int sb = 0; sb < 8; sb++) {
+        const float *sub = x + sb * 32;
+        float smin = INFINITY, smax = -INFINITY;
+        for (int i = 0; i < 32; i++) {
+            float v = sub[i];
+            if (v < smin) smin = v;
+            if (v > smax) smax = v;
+        }
+        if (smin >= 0.0f) {
+            sub_mins[sb] = 0.0f;
+            sub_scales[sb] = smax > 0.0f ? smax / 15.0f : 0.0f;
+        } else {
+            sub_mins[sb] = smin;
+            sub_scales[sb] = smax > smin ? (smax - smin) / 15.0f : 0.0f;
+        }
+    }
+    /* fold(0.0, f32::max): f32::max returns the non-NaN operand, like fmaxf */
+    float max_scale = 0.0f, max_min = 0.0f;
+    for (int j = 0; j < 8; j++) {
+        max_scale = fmaxf(max_scale, sub_scales[j]);
+        max_min = fmaxf(max_min, -sub_mins[j]);
+    }
+    float d = max_scale > 0.0f ? max_scale / 63.0f : 0.0f;
+    float dmin = max_min > 0.0f ? max_min / 63.0f : 0.0f;
+    uint8_t sv[8] = {0}, mv[8] = {0};
+    if (d > 0.0f) {
+        float inv_d = 1.0f / d;
+        for (int j = 0; j < 8; j++) {
+            uint8_t q = rust_f32_as_u8(sub_scales[j] * inv_d + 0.5f);
+            sv[j] = q < 63 ? q : 63;
+        }
+    }
+    if (dmin > 0.0f) {
+        float inv_dmin = 1.0f / dmin;
+        for (int j = 0; j < 8; j++) {
+            uint8_t q = rust_f32_as_u8((-sub_mins[j]) * inv_dmin + 0.5f);
+            mv[j] = q < 63 ? q : 63;
+        }
+    }
+    uint16_t d16 = orc_f32_to_f16_trunc(d), dmin16 = orc_f32_to_f16_trunc(dmin);
+    out[0] = (uint8_t)(d16 & 0xFF); out[1] = (uint8_t)(d16 >> 8);
+    out[2] = (uint8_t)(dmin16 & 0xFF); out[3] = (uint8_t)(dmin16 >> 8);
+    orc_q4k_pack_scales(sv, mv, out + 4);
+    float d_val = orc_f16_to_f32(d16), dmin_val = orc_f16_to_f32(dmin16);
+    for (int chunk = 0; chunk < 4; chunk++) {
+        float scale1 = d_val * (float)sv[chunk * 2];
+        float min1 = dmin_val * (float)mv[chunk * 2];
+        float scale2 = d_val * (float)sv[chunk * 2 + 1];
+        float min2 = dmin_val * (float)mv[chunk * 2 + 1];
+        const float *lo = x + chunk * 64, *hi = x + chunk * 64 + 32;
+        for (int l = 0; l < 32; l++) {
+            uint8_t q_lo = 0, q_hi = 0;
+            if (scale1 > 0.0f) {
+                q_lo = rust_f32_as_u8((lo[l] + min1) / scale1 + 0.5f);
+                if (q_lo > 15) q_lo = 15;
+            }
+            if (scale2 > 0.0f) {
+                q_hi = rust_f32_as_u8((hi[l] + min2) / scale2 + 0.5f);
+                if (q_hi > 15) q_hi = 15;
+            }
+            out[16 + chunk * 32 + l] = (uint8_t)(q_lo | (q_hi << 4));
+        }
+    }
+}
+
+/* Q4KMat::quantize (autograd2.rs:1138-1168): block by block, row-major. */
+void orc_q4k_quantize(const float *m, size_t rows, size_t cols, uint8_t *blocks)
+{
+    size_t nb = cols / 256;
+    for (size_t r = 0; r < rows; r++)
+        for (size_t b = 0; b < nb; b++)
+            orc_q4k_quantize_block(m + r * cols + b * 256, blocks + (r * nb + b) * 144);
+}
+
+/* decode_q4_0_to_f32 (gguf_loader.rs:425-480): 18-byte blocks, f16 scale then
+ * 16 bytes whose low nibble is element k and high nibble element k+16. */
+void orc_q4_0_dequant(const uint8_t *bytes, size_t n_elem, float *out)
+{
+    size_t n_blocks = (n_elem + 31) / 32;
+    for (size_t b = 0; b < n_blocks; b++) {
+        const uint8_t *bp = bytes + b * 18;
+        float scale = orc_f16_to_f32(rd16(bp));
+        size_t start = b * 32, end = start + 32 < n_elem ? start + 32 : n_elem;
+        for (size_t k = 0; k < 16; k++) {
+            uint8_t src = bp[2 + k];
+            if (start + k < end) out[start + k] = (float)((int)(src & 0x0F) - 8) * scale;
+            if (start + k + 16 < end) out[start + k + 16] = (float)((int)((src >> 4) & 0x0F) - 8) * scale;
+        }
+    }
+}
+
+/* load_linear_from_gguf's Q4_0 branch (transformer4.rs:1198-1207):
+ * decode_q4_0_to_q4mat (gguf_loader.rs:282-357) stores the nibbles as signed
+ * v-8 with the block's scale, Q4Mat::dequantize_row_into (autograd2.rs:
+ * 2390-2414) returns q*scale for each element of a row, and
+ * Q4KMat::from_q4mat (autograd2.rs:1291-1320) requantises every 256 of them. */
+void orc_q4_0_to_q4k(const uint8_t *bytes, size_t rows, size_t cols, uint8_t *blocks)
+{
+    float *row = (float *)malloc(cols * sizeof(float));
+    size_t nb = cols / 256;
+    for (size_t r = 0; r < rows; r++) {
+        for (size_t p = 0; p < cols; p++) {
+            size_t flat = r * cols + p, blk = flat / 32, k = flat % 32;
+            const uint8_t *bp = bytes + blk * 18;
+            uint8_t nib = k < 16 ? (bp[2 + k] & 0x0F) : ((bp[2 + k - 16] >> 4) & 0x0F);
+            int q = (int)((uint8_t)(nib - 8) & 0x0F);   /* the stored two's complement nibble */
+            if (q >= 8) q -= 16;
+            row[p] = (float)q * orc_f16_to_f32(rd16(bp));
+        }
+        for (size_t b = 0; b < nb; b++) orc_q4k_quantize_block(row + b * 256, blocks + (r * nb + b) * 144);
+    }
+    free(row);
+}
+
+/* decode_q6k_to_f32 (gguf_loader.rs:482-549): 210-byte blocks of ql[128],
+ * qh[64], int8 scales[16], f16 d; two halves of 128 elements. */
+void orc_q6k_dequant(const uint8_t *bytes, size_t n_elem, float *out)
+{
+    size_t n_blocks = (n_elem + 255) / 256;
+    for (size_t b = 0; b < n_blocks; b++) {
+        const uint8_t *bp = bytes + b * 210;
+        const uint8_t *ql_all = bp, *qh_all = bp + 128, *sc_all = bp + 192;
+        float d = orc_f16_to_f32(rd16(bp + 208));
+        size_t base = b * 256, end = base + 256 < n_elem ? base + 256 : n_elem;
+        for (int j = 0; j < 2; j++) {
+            const uint8_t *ql = ql_all + j * 64, *qh = qh_all + j * 32, *sc = sc_all + j * 8;
+            size_t y = base + (size_t)j * 128;
+            for (int l = 0; l < 32; l++) {
+                int is = l / 16;
+                int q1 = (int)((ql[l] & 0x0F) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                int q2 = (int)((ql[l + 32] & 0x0F) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                float s0 = d * (float)(int8_t)sc[is], s1 = d * (float)(int8_t)sc[is + 2];
+                float s2 = d * (float)(int8_t)sc[is + 4], s3 = d * (float)(int8_t)sc[is + 6];
+                if (y + l < end) out[y + l] = s0 * (float)q1;
+                if (y + l + 32 < end) out[y + l + 32] = s1 * (float)q2;
+                if (y + l + 64 < end) out[y + l + 64] = s2 * (float)q3;
+                if (y + l + 96 < end) out[y + l + 96] = s3 * (float)q4;
+            }
+        }
+    }
+}
+
+/* decode_q5k_to_f32 (gguf_loader.rs:664-743): 176-byte blocks of f16 d, f16
+ * dmin, scales[12] (Q4_K packing), qh[32], qs[128]. */
+void orc_q5k_dequant(const uint8_t *bytes, size_t n_elem, float *out)
+{
+    size_t n_blocks = (n_elem + 255) / 256;
+    for (size_t b = 0; b < n_blocks; b++) {
+        const uint8_t *bp = bytes + b * 176;
+        float d = orc_f16_to_f32(rd16(bp)), dmin = orc_f16_to_f32(rd16(bp + 2));
+        const uint8_t *sc = bp + 4, *qh = bp + 16, *qs = bp + 48;
+        size_t base = b * 256, end = base + 256 < n_elem ? base + 256 : n_elem;
+        size_t q_off = 0, elem = 0;
+        int is = 0;
+        for (int c = 0; c < 4; c++) {
+            float d1, m1, d2, m2;
+            orc_q4k_scale_min(sc, is, &d1, &m1);
+            orc_q4k_scale_min(sc, is + 1, &d2, &m2);
+            float scale1 = d * d1, min1 = dmin * m1, scale2 = d * d2, min2 = dmin * m2;
+            for (size_t l = 0; l < 32; l++, elem++) {
+                unsigned lo = qs[q_off + l] & 0x0F, hi = (qh[l] >> is) & 1;
+                if (base + elem < end) out[base + elem] = scale1 * (float)(lo | (hi << 4)) - min1;
+            }
+            for (size_t l = 0; l < 32; l++, elem++) {
+                unsigned lo = qs[q_off + l] >> 4, hi = (qh[l] >> (is + 1)) & 1;
+                if (base + elem < end) out[base + elem] = scale2 * (float)(lo | (hi << 4)) - min2;
+            }
+            q_off += 32;
+            is += 2;
+        }
+    }
+}
+
+/* decode_q8_0_to_f32 (gguf_loader.rs:628-650): 34-byte blocks, f16 d then 32
+ * int8 quants. */
+void orc_q8_0_dequant(const uint8_t *bytes, size_t n_elem, float *out)
+{
+    size_t n_blocks = (n_elem + 31) / 32;
+    for (size_t b = 0; b < n_blocks; b++) {
+        const uint8_t *bp = bytes + b * 34;
+        float d = orc_f16_to_f32(rd16(bp));
+        size_t base = b * 32;
+        for (size_t i = 0; i < 32; i++)
+            if (base + i < n_elem) out[base + i] = d * (float)(int8_t)bp[2 + i];
+    }
+}
+
 /* dot_row, x86 scalar branch: autograd2.rs:1654-1701 ("integer trick"). */
 float orc_q4k_dot_row(const uint8_t *blocks, size_t cols, size_t row, const float *a)
 {

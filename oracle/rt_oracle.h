@@ -33,6 +33,17 @@ void orc_q4k_pack_scales(const uint8_t sv[8], const uint8_t mv[8], uint8_t out[1
 void orc_q4k_dequant_row(const uint8_t *blocks, size_t cols, size_t row, float *out); /* autograd2.rs:1326-1366 */
 void orc_q4k_dequant_gguf(const uint8_t *bytes, size_t n_elem, float *out); /* gguf_loader.rs:551-621 */
 
+/* ---- GGUF tensor formats and Q4_K quantisation --------------------------- */
+uint16_t orc_f32_to_f16_trunc(float v);            /* autograd2.rs:1090-1117 (Q4KMat::f32_to_f16: truncates) */
+void orc_q4k_quantize_block(const float *x256, uint8_t out[144]);          /* autograd2.rs:1171-1245 */
+void orc_q4k_quantize(const float *m, size_t rows, size_t cols, uint8_t *blocks); /* autograd2.rs:1138-1168 */
+void orc_q4_0_dequant(const uint8_t *bytes, size_t n_elem, float *out);    /* gguf_loader.rs:425-480 */
+void orc_q4_0_to_q4k(const uint8_t *bytes, size_t rows, size_t cols, uint8_t *blocks);
+     /* gguf_loader.rs:282-357 + autograd2.rs:1291-1320 (Q4KMat::from_q4mat) + 2390-2414 */
+void orc_q6k_dequant(const uint8_t *bytes, size_t n_elem, float *out);     /* gguf_loader.rs:482-549 */
+void orc_q5k_dequant(const uint8_t *bytes, size_t n_elem, float *out);     /* gguf_loader.rs:664-743 */
+void orc_q8_0_dequant(const uint8_t *bytes, size_t n_elem, float *out);    /* gguf_loader.rs:628-650 */
+
 /* ---- GEMV -------------------------------------------------------------- */
 float orc_q4k_dot_row(const uint8_t *blocks, size_t cols, size_t row, const float *a); /* autograd2.rs:1654-1701 */
 void  orc_q4k_gemv_mt(const uint8_t *blocks, size_t rows, size_t cols,

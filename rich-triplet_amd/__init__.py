@@ -66,6 +66,25 @@ _SIGNATURES = {
     "rt_decode_kv": (_i32, [_vp, _i32, C.POINTER(_vp), C.POINTER(_vp)]),
     "rt_decode_hidden": (_i32, [_vp, C.POINTER(_vp), C.POINTER(_vp)]),
     "rt_decode_get_stream": (_i32, [_vp, C.POINTER(_vp)]),
+    # GGUF reader and loader (include/rt_gguf.h)
+    "rt_gguf_open": (_i32, [C.c_char_p, C.POINTER(_vp)]),
+    "rt_gguf_close": (_i32, [_vp]),
+    "rt_gguf_n_tensors": (_i64, [_vp]),
+    "rt_gguf_n_metadata": (_i64, [_vp]),
+    "rt_gguf_data_start": (C.c_uint64, [_vp]),
+    "rt_gguf_tensor_info": (_i32, [_vp, _i64, _vp]),
+    "rt_gguf_find_tensor": (_i64, [_vp, C.c_char_p]),
+    "rt_gguf_meta_key": (_i32, [_vp, _i64, C.POINTER(C.c_char_p)]),
+    "rt_gguf_meta_type": (_i32, [_vp, C.c_char_p, C.POINTER(_i32), C.POINTER(_i32), C.POINTER(C.c_uint64)]),
+    "rt_gguf_meta_u64": (_i32, [_vp, C.c_char_p, C.POINTER(C.c_uint64)]),
+    "rt_gguf_meta_f32": (_i32, [_vp, C.c_char_p, C.POINTER(C.c_float)]),
+    "rt_gguf_meta_str": (_i32, [_vp, C.c_char_p, C.POINTER(C.c_char_p)]),
+    "rt_gguf_meta_array_str": (_i32, [_vp, C.c_char_p, C.c_uint64, C.POINTER(C.c_char_p)]),
+    "rt_gguf_read_tensor": (_i32, [_vp, _i64, _vp, C.c_uint64]),
+    "rt_gguf_tensor_to_f32": (_i32, [_vp, _i64, _vp, C.c_uint64]),
+    "rt_q4k_quantize": (_i32, [_vp, _sz, _sz, _vp]),
+    "rt_gguf_load_linear": (_i32, [_vp, _i64, _vp]),
+    "rt_linear_free": (_i32, [_vp]),
 }
 
 
@@ -291,3 +310,6 @@ class HipDecodeContext:
         s = C.c_void_p()
         check(lib().rt_decode_get_stream(self._h, C.byref(s)))
         return s.value
+
+
+from .gguf import GgufFile, GgufTensorInfo, Linear, load_linear_from_gguf, q4k_quantize  # noqa: E402,F401
