@@ -226,6 +226,8 @@ embedding table size, metal_decode.rs lm_head_vocab)."""
 def _addr(x) -> int:
     if isinstance(x, int):
         return x
+    if hasattr(x, "ptr") and hasattr(x, "format"):  # a Linear loaded from GGUF (device memory)
+        return x.ptr
     if hasattr(x, "data_ptr"):
         return x.data_ptr()
     import numpy as np
@@ -263,9 +265,17 @@ class HipDecodeContext:
 
     @staticmethod
     def _on_device(x) -> int:
-        return int(hasattr(x, "is_cuda") and x.is_cuda)
+        return int((hasattr(x, "is_cuda") and x.is_cuda) or (hasattr(x, "ptr") and hasattr(x, "format")))
 
     def set_layer(self, i: int, w: dict) -> None:
+        """w: the 7 Q4_K projections and 6 norm vectors (Gemma3Layer fields); all
+        host arrays, or all device memory (torch cuda tensors or GGUF-loaded
+        `Linear`s, whose projections must be Q4_K)."""
+        for k in ("q", "k", "v", "o", "gate", "up", "down"):
+            fmt = getattr(w[k], "format", None)
+            if fmt is not None and fmt != 1:
+                raise RtError(RT_EINVAL, f"layer {i} projection {k} is not Q4_K (format {fmt}); "
+                                         "the decode step runs Q4_K projections")
         dev = self._on_device(w["q"])
         L = Gemma3Layer(**{k: _addr(w[k]) for k, _ in Gemma3Layer._fields_})
         if dev:
