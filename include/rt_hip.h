@@ -147,6 +147,16 @@ rt_status rt_decode_sync_kv(rt_decode *d, int32_t layer, const float *k, const f
 rt_status rt_decode_step(rt_decode *d, int32_t token, int32_t position, float *logits_host);
 /* Same step, only enqueued on the context stream; logits stay on the device. */
 rt_status rt_decode_step_async(rt_decode *d, int32_t token, int32_t position);
+/* decode_step_batch (metal_decode.rs:2079-2179): m (1..8) tokens at positions
+ * start_position .. start_position+m-1, as used by speculative verify.  Each
+ * token attends to the K/V of the tokens before it in the batch; logits_host
+ * (may be NULL) receives m x vocab floats, row i for token i.  The lm_head
+ * reads the embedding once for all m tokens. */
+rt_status rt_decode_step_batch(rt_decode *d, const int32_t *tokens, int32_t m, int32_t start_position,
+                               float *logits_host);
+rt_status rt_decode_step_batch_async(rt_decode *d, const int32_t *tokens, int32_t m, int32_t start_position);
+/* Device buffer of the last batch's logits, [8][vocab]. */
+rt_status rt_decode_logits_batch(rt_decode *d, float **logits_dev);
 rt_status rt_decode_synchronize(rt_decode *d);
 /* Use the captured hipGraph (default) or launch the kernels one by one. */
 rt_status rt_decode_set_graph(rt_decode *d, int32_t enabled);

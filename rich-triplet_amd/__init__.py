@@ -66,6 +66,9 @@ _SIGNATURES = {
     "rt_decode_kv": (_i32, [_vp, _i32, C.POINTER(_vp), C.POINTER(_vp)]),
     "rt_decode_hidden": (_i32, [_vp, C.POINTER(_vp), C.POINTER(_vp)]),
     "rt_decode_get_stream": (_i32, [_vp, C.POINTER(_vp)]),
+    "rt_decode_step_batch": (_i32, [_vp, _vp, _i32, _i32, _vp]),
+    "rt_decode_step_batch_async": (_i32, [_vp, _vp, _i32, _i32]),
+    "rt_decode_logits_batch": (_i32, [_vp, C.POINTER(_vp)]),
     # GGUF reader and loader (include/rt_gguf.h)
     "rt_gguf_open": (_i32, [C.c_char_p, C.POINTER(_vp)]),
     "rt_gguf_close": (_i32, [_vp]),
@@ -296,6 +299,20 @@ class HipDecodeContext:
         out = np.empty(self.cfg["vocab"], np.float32)
         check(lib().rt_decode_step(self._h, token, position, out.ctypes.data))
         return out
+
+    def decode_step_batch(self, tokens, start_position: int):
+        """decode_step_batch (metal_decode.rs:2079-2179): logits [m, vocab] for
+        m <= 8 tokens at start_position, start_position+1, ..."""
+        import numpy as np
+        t = np.ascontiguousarray(np.asarray(tokens, np.int32))
+        out = np.empty((t.size, self.cfg["vocab"]), np.float32)
+        check(lib().rt_decode_step_batch(self._h, t.ctypes.data, t.size, start_position, out.ctypes.data))
+        return out
+
+    def decode_step_batch_async(self, tokens, start_position: int) -> None:
+        import numpy as np
+        t = np.ascontiguousarray(np.asarray(tokens, np.int32))
+        check(lib().rt_decode_step_batch_async(self._h, t.ctypes.data, t.size, start_position))
 
     def decode_step_async(self, token: int, position: int) -> None:
         check(lib().rt_decode_step_async(self._h, token, position))

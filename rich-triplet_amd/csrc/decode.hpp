@@ -20,6 +20,10 @@ constexpr int kAttnMaxChunks = 4096;
 // kParamRopeLocal ([head_dim/2] cos, [head_dim/2] sin) and for global layers
 // after it.
 constexpr int kParamRopeLocal = 16;
+// Batched verify (decode_step_batch): up to kMaxBatch tokens per call, each
+// with its own parameter slot of kParamRopeLocal + 2*head_dim floats.
+constexpr int kMaxBatch = 8;
+inline int param_slot_floats(int head_dim) { return kParamRopeLocal + 2 * head_dim; }
 
 struct DecodeShape {
   int hidden, ffn, n_q_heads, n_kv_heads, head_dim, n_layers, vocab;
@@ -49,5 +53,10 @@ struct DecodeArgs {
 bool decode_shape_supported(const DecodeShape &s, const char **why);
 bool decode_rows_divisible(const DecodeShape &s, const char **why);
 hipError_t enqueue_decode_step(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers, hipStream_t stream);
+// M tokens at consecutive positions (params slots 0..M-1): the layer kernels
+// of each token in turn, the final norm of each into xn[m][hidden], then one
+// batched lm_head into logits_b[m][vocab].
+hipError_t enqueue_decode_batch(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers, int m,
+                                float *xn, float *logits_b, hipStream_t stream);
 
 }  // namespace rt

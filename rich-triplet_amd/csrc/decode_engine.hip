@@ -30,9 +30,11 @@ struct rt_decode {
   bool embed_set = false;
   void *embed_owned = nullptr, *final_owned = nullptr;
   DecodeArgs args{};
-  int *params_dev = nullptr;             // step parameter block (kParamRopeLocal)
+  int *params_dev = nullptr;             // kMaxBatch step parameter slots (kParamRopeLocal)
   int *params_host = nullptr;            // pinned
-  size_t params_bytes = 0;
+  size_t params_bytes = 0, slot_bytes = 0;
+  float *xn_batch = nullptr, *logits_batch = nullptr;  // decode_step_batch: [kMaxBatch][hidden | vocab]
+  hipGraphExec_t exec_batch[kMaxBatch + 1] = {};
   hipEvent_t params_copied = nullptr;
   bool params_pending = false;
   std::vector<float> rope_den_local, rope_den_global;  // theta^(2i/d), host powf
@@ -66,6 +68,10 @@ size_t q4k_bytes(size_t rows, size_t cols) { return rows * (cols / 256) * 144; }
 void drop_graph(rt_decode *d) {
   if (d->exec) (void)hipGraphExecDestroy(d->exec);
   d->exec = nullptr;
+  for (auto &x : d->exec_batch) {
+    if (x) (void)hipGraphExecDestroy(x);
+    x = nullptr;
+  }
   d->graph_dirty = true;
 }
 
@@ -131,7 +137,8 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
     const size_t H = c.hidden, F = c.ffn, D = c.head_dim;
     const size_t QD = (size_t)c.n_q_heads * D, KVD = (size_t)c.n_kv_heads * D;
     const int nch = std::max(s.nchunk_local, s.nchunk_global);
-    d->params_bytes = (kParamRopeLocal + 2 * D) * sizeof(float);
+    d->slot_bytes = (size_t)param_slot_floats((int)D) * sizeof(float);
+    d->params_bytes = kMaxBatch * d->slot_bytes;
     TRYH(hipHostMalloc((void **)&d->params_host, d->params_bytes, hipHostMallocDefault), "hipHostMalloc");
     std::memset(d->params_host, 0, d->params_bytes);
     void *p;
@@ -153,6 +160,8 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
     TRY(fbuf((size_t)c.vocab, &a.logits));
     TRY(fbuf((size_t)c.n_q_heads * nch, &a.part_m)); TRY(fbuf((size_t)c.n_q_heads * nch, &a.part_l));
     TRY(fbuf((size_t)c.n_q_heads * nch * D, &a.part_o));
+    TRY(fbuf((size_t)kMaxBatch * H, &d->xn_batch));
+    TRY(fbuf((size_t)kMaxBatch * c.vocab, &d->logits_batch));
     a.params = d->params_dev;
     a.embed_scale = std::sqrt((float)c.hidden);   // transformer4.rs:2092
     a.eps = c.eps;
@@ -310,58 +319,115 @@ static rt_status check_ready(rt_decode *d, int32_t token, int32_t position) {
   return RT_OK;
 }
 
-rt_status rt_decode_step_async(rt_decode *d, int32_t token, int32_t position) {
-  rt_status st = check_ready(d, token, position);
-  if (st != RT_OK) return st;
-  hipError_t e = hipSuccess;
-  if (d->params_pending) {
-    e = hipEventSynchronize(d->params_copied);  // the previous copy has left the pinned buffer
-    if (e != hipSuccess) return hip_error(e, "rt_decode_step");
-  }
-  d->params_host[0] = token;
-  d->params_host[1] = position;
-  {
-    // cos/sin of angle = (pos*fs)/theta^(2i/d) in f32 with the host libm, as
-    // apply_rope_at_offset computes them (transformer4.rs:2742-2772).
-    const int D = d->cfg.head_dim, P = D / 2;
-    float *cs = reinterpret_cast<float *>(d->params_host) + kParamRopeLocal;
-    for (int t = 0; t < 2; ++t, cs += D) {
-      const float fs = t ? d->cfg.rope_fs_global : d->cfg.rope_fs_local;
-      const float *den = t ? d->rope_den_global.data() : d->rope_den_local.data();
-      const float pf = (float)position * fs;
-      for (int i = 0; i < P; ++i) {
-        const float ang = pf / den[i];
-        cs[i] = cosf(ang);
-        cs[P + i] = sinf(ang);
-      }
+// Token id, position and the RoPE cos/sin tables of slot `slot`: angle =
+// (pos*fs)/theta^(2i/d) in f32 with the host libm, as apply_rope_at_offset
+// computes it (transformer4.rs:2742-2772).
+static void fill_slot(rt_decode *d, int slot, int32_t token, int32_t position) {
+  int *ip = reinterpret_cast<int *>(reinterpret_cast<char *>(d->params_host) + (size_t)slot * d->slot_bytes);
+  ip[0] = token;
+  ip[1] = position;
+  const int D = d->cfg.head_dim, P = D / 2;
+  float *cs = reinterpret_cast<float *>(ip) + kParamRopeLocal;
+  for (int t = 0; t < 2; ++t, cs += D) {
+    const float fs = t ? d->cfg.rope_fs_global : d->cfg.rope_fs_local;
+    const float *den = t ? d->rope_den_global.data() : d->rope_den_local.data();
+    const float pf = (float)position * fs;
+    for (int i = 0; i < P; ++i) {
+      const float ang = pf / den[i];
+      cs[i] = cosf(ang);
+      cs[P + i] = sinf(ang);
     }
   }
-  e = hipMemcpyAsync(d->params_dev, d->params_host, d->params_bytes, hipMemcpyHostToDevice, d->stream);
+}
+
+// Waits until the previous parameter copy has left the pinned buffer.
+static rt_status params_ready(rt_decode *d) {
+  if (!d->params_pending) return RT_OK;
+  return hip_error(hipEventSynchronize(d->params_copied), "rt_decode_step");
+}
+
+static rt_status params_send(rt_decode *d, int slots) {
+  hipError_t e = hipMemcpyAsync(d->params_dev, d->params_host, (size_t)slots * d->slot_bytes, hipMemcpyHostToDevice,
+                                d->stream);
   if (e == hipSuccess) e = hipEventRecord(d->params_copied, d->stream);
   if (e != hipSuccess) return hip_error(e, "rt_decode_step params");
   d->params_pending = true;
-  if (!d->graph_enabled) return hip_error(enqueue_decode_step(d->shape, d->args, d->layers.data(), d->stream), "rt_decode_step");
-  if (d->graph_dirty || !d->exec) {
-    drop_graph(d);
+  return RT_OK;
+}
+
+// Launch `enqueue` through a graph captured on first use (or eagerly when
+// graphs are off).
+extern "C++" template <class F>
+static rt_status run_graph(rt_decode *d, hipGraphExec_t &exec, F enqueue, const char *what) {
+  if (!d->graph_enabled) return hip_error(enqueue(), what);
+  if (d->graph_dirty) drop_graph(d);
+  if (!exec) {
     hipGraph_t g = nullptr;
-    e = hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal);
+    hipError_t e = hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal);
     if (e != hipSuccess) return hip_error(e, "hipStreamBeginCapture");
-    hipError_t le = enqueue_decode_step(d->shape, d->args, d->layers.data(), d->stream);
+    hipError_t le = enqueue();
     e = hipStreamEndCapture(d->stream, &g);
     if (le != hipSuccess) {
       if (g) (void)hipGraphDestroy(g);
-      return hip_error(le, "rt_decode_step capture");
+      return hip_error(le, what);
     }
     if (e != hipSuccess) return hip_error(e, "hipStreamEndCapture");
-    e = hipGraphInstantiate(&d->exec, g, nullptr, nullptr, 0);
+    e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
     if (e != hipSuccess) {
-      d->exec = nullptr;
+      exec = nullptr;
       return hip_error(e, "hipGraphInstantiate");
     }
-    d->graph_dirty = false;
   }
-  return hip_error(hipGraphLaunch(d->exec, d->stream), "hipGraphLaunch");
+  d->graph_dirty = false;
+  return hip_error(hipGraphLaunch(exec, d->stream), "hipGraphLaunch");
+}
+
+rt_status rt_decode_step_async(rt_decode *d, int32_t token, int32_t position) {
+  rt_status st = check_ready(d, token, position);
+  if (st == RT_OK) st = params_ready(d);
+  if (st != RT_OK) return st;
+  fill_slot(d, 0, token, position);
+  if ((st = params_send(d, 1)) != RT_OK) return st;
+  return run_graph(d, d->exec, [&] { return enqueue_decode_step(d->shape, d->args, d->layers.data(), d->stream); },
+                   "rt_decode_step");
+}
+
+// decode_step_batch (metal_decode.rs:2079-2179): m <= 8 tokens at positions
+// start .. start+m-1.  Each token sees the keys of the ones before it, as in
+// the reference (its K/V rows are appended before its attention); the
+// logits of token i land in row i of the batch logits buffer.
+rt_status rt_decode_step_batch_async(rt_decode *d, const int32_t *tokens, int32_t m, int32_t start_position) {
+  if (!d || !tokens) return set_error(RT_EINVAL, "rt_decode_step_batch: null pointer");
+  if (m < 1 || m > kMaxBatch) return set_error(RT_EINVAL, "rt_decode_step_batch: M=%d outside [1, %d]", m, kMaxBatch);
+  for (int i = 0; i < m; ++i) {
+    rt_status st = check_ready(d, tokens[i], start_position + i);
+    if (st != RT_OK) return st;
+  }
+  rt_status st = params_ready(d);
+  if (st != RT_OK) return st;
+  for (int i = 0; i < m; ++i) fill_slot(d, i, tokens[i], start_position + i);
+  if ((st = params_send(d, m)) != RT_OK) return st;
+  return run_graph(d, d->exec_batch[m], [&] {
+    return enqueue_decode_batch(d->shape, d->args, d->layers.data(), m, d->xn_batch, d->logits_batch, d->stream);
+  }, "rt_decode_step_batch");
+}
+
+rt_status rt_decode_step_batch(rt_decode *d, const int32_t *tokens, int32_t m, int32_t start_position,
+                               float *logits_host) {
+  rt_status st = rt_decode_step_batch_async(d, tokens, m, start_position);
+  if (st != RT_OK) return st;
+  hipError_t e = hipSuccess;
+  if (logits_host)
+    e = hipMemcpyAsync(logits_host, d->logits_batch, (size_t)m * d->cfg.vocab * 4, hipMemcpyDeviceToHost, d->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
+  return hip_error(e, "rt_decode_step_batch");
+}
+
+rt_status rt_decode_logits_batch(rt_decode *d, float **logits_dev) {
+  if (!d || !logits_dev) return set_error(RT_EINVAL, "rt_decode_logits_batch: null pointer");
+  *logits_dev = d->logits_batch;
+  return RT_OK;
 }
 
 rt_status rt_decode_step(rt_decode *d, int32_t token, int32_t position, float *logits_host) {

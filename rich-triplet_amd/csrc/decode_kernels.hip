@@ -15,6 +15,8 @@
 // After the last layer k_lmhead applies the final residual, the final norm
 // and the BF16 lm_head GEMV.  Token id and position are read from device
 // memory so the whole step replays as one hipGraph.
+#include <vector>
+
 #include "decode.hpp"
 #include "q4k_gemv.hpp"
 #include "rt_device.hpp"
@@ -517,6 +519,110 @@ __global__ __launch_bounds__(256) void k_lmhead(DecodeArgs a, LayerArgs last) {
 }
 
 // ---------------------------------------------------------------------------
+// k_final_norm: one token's x = x2 + rms(dn)(1+g_post_ffn_last) and
+// xn = rms(x)(1+g_final) (transformer4.rs:2370-2380) into out[hidden]; the
+// batched lm_head then reads every token's xn.
+// ---------------------------------------------------------------------------
+template <int K>
+__global__ __launch_bounds__(256) void k_final_norm(DecodeArgs a, LayerArgs last, float *__restrict__ out) {
+  constexpr int T = 256;
+  __shared__ float bred[T / 64];
+  ProRegs<K, T> pr;
+  pro_load<K, T, Pro::Resid>(a, a.x2, a.dn, last.g_post_ffn, a.g_final, pr);
+  using R = ProRegs<K, T>;
+  const float inv_k = 1.0f / (float)K;
+  auto live = [&](int i) { return (int)threadIdx.x + i * T < R::F4; };
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < R::PER; ++i) ss += live(i) ? sumsq4(pr.add[i]) : 0.f;
+  const float ra = rms_inv_from_sumsq(block_sum<T>(ss, bred), inv_k, a.eps);
+  float4 x[R::PER];
+#pragma unroll
+  for (int i = 0; i < R::PER; ++i) x[i] = add4(pr.base[i], norm4(pr.add[i], ra, pr.ga[i]));
+  float sx = 0.f;
+#pragma unroll
+  for (int i = 0; i < R::PER; ++i) sx += live(i) ? sumsq4(x[i]) : 0.f;
+  const float rx = rms_inv_from_sumsq(block_sum<T>(sx, bred), inv_k, a.eps);
+#pragma unroll
+  for (int i = 0; i < R::PER; ++i)
+    if (live(i)) reinterpret_cast<float4 *>(out)[threadIdx.x + i * T] = norm4(x[i], rx, pr.go[i]);
+}
+
+// ---------------------------------------------------------------------------
+// k_lmhead_batch: logits[v][r] = E[r] . xn[v] for v < M <= 8 on
+// v_mfma_f32_16x16x32_bf16 (decode_step_batch's lm_head, metal_decode.rs:
+// 2162-2172).  Each xn[v] is split into bf16 parts hi + lo (x - hi rounded
+// again: 2^-17 relative), and A row 2v+p carries part p of vector v (rows of
+// absent vectors are zero), so one pass over the 1.34 GB embedding serves
+// every token.  B is 16 embedding rows as they are.  Lane (n = l%16,
+// g = l/16) holds C rows 4g..4g+3: vectors 2g and 2g+1, both parts, of
+// vocabulary row n.  A sits in LDS for the whole K: [segment][16][32] bf16
+// with the 16-byte groups XOR-swizzled by (row >> 2) so a ds_read_b128 of 16
+// lanes hits 64 distinct banks.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+template <int K>
+__global__ __launch_bounds__(256) void k_lmhead_batch(const uint16_t *__restrict__ E, const float *__restrict__ xn,
+                                                      float *__restrict__ logits, int N, int M) {
+  constexpr int SEG = K / 32;
+  __shared__ __attribute__((aligned(16))) uint16_t xa[SEG * 16 * 32];
+  // stage: element e of vector v -> hi, lo bf16 at A rows 2v, 2v+1
+#pragma unroll 1
+  for (int i = threadIdx.x; i < 8 * K; i += 256) {
+    const int v = i / K, e = i % K;
+    uint16_t hi = 0, lo = 0;
+    if (v < M) {
+      const float x = xn[(size_t)v * K + e];
+      hi = f32_to_bf16_bits(x);
+      lo = f32_to_bf16_bits(x - bf16_lo((uint32_t)hi));
+    }
+    const int seg = e >> 5, k = e & 31, grp = k >> 3;
+    for (int p = 0; p < 2; ++p) {
+      const int row = 2 * v + p;
+      xa[(seg * 16 + row) * 32 + 8 * (grp ^ ((row >> 2) & 3)) + (k & 7)] = p ? lo : hi;
+    }
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+  const int aoff = n * 32 + 8 * (g ^ ((n >> 2) & 3));  // this lane's A fragment inside a segment
+  const int wave = (int)((blockIdx.x * 256u + threadIdx.x) >> 6), nwaves = (int)(gridDim.x * 4u);
+  constexpr int B = 8;  // segments in flight per batch
+#pragma unroll 1
+  for (int r0 = wave * 16; r0 < N; r0 += nwaves * 16) {
+    const uint16_t *row = E + (size_t)min(r0 + n, N - 1) * K + 8 * g;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    u32x4_t bw[B];
+#pragma unroll
+    for (int j = 0; j < B; ++j) bw[j] = *reinterpret_cast<const u32x4_t *>(row + 32 * j);
+#pragma unroll 1
+    for (int s0 = 0; s0 < SEG; s0 += B) {
+      u32x4_t bn[B];
+      const int s1 = s0 + B < SEG ? s0 + B : s0;  // next batch (repeats the last one at the end)
+#pragma unroll
+      for (int j = 0; j < B; ++j) bn[j] = *reinterpret_cast<const u32x4_t *>(row + 32 * (s1 + j));
+#pragma unroll
+      for (int j = 0; j < B; ++j) {
+        const u32x4_t af = *reinterpret_cast<const u32x4_t *>(xa + (s0 + j) * 512 + aoff);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, af),
+                                                      __builtin_bit_cast(bf16x8_t, bw[j]), acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < B; ++j) bw[j] = bn[j];
+    }
+    if (r0 + n < N) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int v = 2 * g + h;
+        if (v < M) logits[(size_t)v * N + r0 + n] = acc[2 * h] + acc[2 * h + 1];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host-side step encoder
 // ---------------------------------------------------------------------------
 template <int NB, int T>
@@ -594,7 +700,8 @@ static void launch_attn_d(Launch &l, const DecodeArgs &a, const LayerArgs &L, in
   l.check();
 }
 
-hipError_t enqueue_decode_step(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers, hipStream_t stream) {
+// The six launches of every layer.
+static hipError_t enqueue_layers(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers, hipStream_t stream) {
   Launch l{stream};
   const int qd = s.n_q_heads * s.head_dim, kvd = s.n_kv_heads * s.head_dim;
   const int group = s.n_q_heads / s.n_kv_heads;
@@ -617,10 +724,44 @@ hipError_t enqueue_decode_step(const DecodeShape &s, const DecodeArgs &a, const 
     if (s.ffn == 10240) launch_gemv<40, 960, 1>(l, L.wdown, a.h, a.dn, s.hidden);
     else launch_gemv<4, 256, 1>(l, L.wdown, a.h, a.dn, s.hidden);
   }
+  return l.err;
+}
+
+hipError_t enqueue_decode_step(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers, hipStream_t stream) {
+  Launch l{stream};
+  const bool big = s.hidden == 2560;
+  l.err = enqueue_layers(s, a, layers, stream);
   if (l.err == hipSuccess) {
     const dim3 grid(1024);
     if (big) hipLaunchKernelGGL((k_lmhead<5>), grid, dim3(256), 0, l.s, a, layers[s.n_layers - 1]);
     else hipLaunchKernelGGL((k_lmhead<1>), grid, dim3(256), 0, l.s, a, layers[s.n_layers - 1]);
+    l.check();
+  }
+  return l.err;
+}
+
+hipError_t enqueue_decode_batch(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers, int m,
+                                float *xn, float *logits_b, hipStream_t stream) {
+  Launch l{stream};
+  const int slot = param_slot_floats(s.head_dim);
+  std::vector<LayerArgs> ls(layers, layers + s.n_layers);
+  for (int t = 0; t < m && l.err == hipSuccess; ++t) {
+    DecodeArgs at = a;
+    at.params = a.params + (size_t)t * slot;
+    for (int li = 0; li < s.n_layers; ++li) ls[li].rope_cs = layers[li].rope_cs + (size_t)t * slot;
+    l.err = enqueue_layers(s, at, ls.data(), stream);
+    if (l.err != hipSuccess) break;
+    if (s.hidden == 2560)
+      hipLaunchKernelGGL((k_final_norm<2560>), dim3(1), dim3(256), 0, l.s, at, ls[s.n_layers - 1], xn + (size_t)t * 2560);
+    else
+      hipLaunchKernelGGL((k_final_norm<512>), dim3(1), dim3(256), 0, l.s, at, ls[s.n_layers - 1], xn + (size_t)t * 512);
+    l.check();
+  }
+  if (l.err == hipSuccess) {
+    if (s.hidden == 2560)
+      hipLaunchKernelGGL((k_lmhead_batch<2560>), dim3(512), dim3(256), 0, l.s, a.embed, xn, logits_b, s.vocab, m);
+    else
+      hipLaunchKernelGGL((k_lmhead_batch<512>), dim3(512), dim3(256), 0, l.s, a.embed, xn, logits_b, s.vocab, m);
     l.check();
   }
   return l.err;

@@ -182,3 +182,124 @@ def test_gemma3_4b_shape_decode_step_matches_oracle(rt, orc, dev):
     ref2 = orc.gemma3_decode_step(cfg, layers, embed, fnorm, token=int(np.argmax(ref)), pos=ctx + 1)
     assert rel_l2(got2, ref2) < LOGITS_TOL
     d.close()
+
+
+# ---------------------------------------------------------------------------
+# decode_step_batch (metal_decode.rs:2079-2179)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("m", [1, 3, 8])
+def test_batch_matches_sequential_and_oracle(rt, orc, m):
+    """M tokens at consecutive positions: the window of 8 slides inside the
+    batch and the global layer sees every earlier batch token.  The batch runs
+    the same layer kernels as M single steps (identical hidden states and K/V
+    rows); only its lm_head differs (MFMA on bf16-split activations)."""
+    import copy
+    cfg = tiny(2)
+    max_seq, ctx = 48, 9
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=ctx, seed=300 + m)
+    toks = [(7 * i + 3) % cfg["vocab"] for i in range(m)]
+    d_batch = build_ctx(rt, cfg, layers, embed, fnorm, ctx, max_seq)
+    d_seq = build_ctx(rt, cfg, layers, embed, fnorm, ctx, max_seq)
+    got = d_batch.decode_step_batch(toks, ctx)
+    assert got.shape == (m, cfg["vocab"])
+    seq = np.stack([d_seq.decode_step(t, ctx + i) for i, t in enumerate(toks)])
+    olayers = copy.deepcopy(layers)
+    ref = np.stack([orc.gemma3_decode_step(cfg, olayers, embed, fnorm, token=t, pos=ctx + i)
+                    for i, t in enumerate(toks)])
+    for i in range(m):
+        assert rel_l2(got[i], seq[i]) < 1e-5, i
+        assert rel_l2(got[i], ref[i]) < LOGITS_TOL, i
+    for li in range(cfg["n_layers"]):
+        kb, vb = d_batch.kv_ptrs(li)
+        ks, vs = d_seq.kv_ptrs(li)
+        kvd = cfg["n_kv_heads"] * cfg["head_dim"]
+        n = (ctx + m) * kvd * 4
+        hb, hs = _read_dev(kb, n), _read_dev(ks, n)
+        assert np.array_equal(hb, hs), li
+        assert np.array_equal(_read_dev(vb, n), _read_dev(vs, n)), li
+    d_batch.close()
+    d_seq.close()
+
+
+def _read_dev(ptr: int, nbytes: int) -> np.ndarray:
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so")
+    out = np.empty(nbytes, np.uint8)
+    assert hip.hipMemcpy(C.c_void_p(out.ctypes.data), C.c_void_p(ptr), C.c_size_t(nbytes), 2) == 0
+    return out
+
+
+def test_batch_graph_replay_and_eager(rt, orc):
+    """Two batches in a row reuse the captured graph for their M; the eager
+    launch order gives the same logits bit for bit."""
+    cfg = tiny(4)
+    max_seq, ctx = 40, 6
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=ctx, seed=444)
+    d_g = build_ctx(rt, cfg, layers, embed, fnorm, ctx, max_seq)
+    d_e = build_ctx(rt, cfg, layers, embed, fnorm, ctx, max_seq)
+    d_e.set_graph(False)
+    a1 = d_g.decode_step_batch([1, 2, 3], ctx)
+    a2 = d_g.decode_step_batch([4, 5, 6], ctx + 3)
+    b1 = d_e.decode_step_batch([1, 2, 3], ctx)
+    b2 = d_e.decode_step_batch([4, 5, 6], ctx + 3)
+    assert np.array_equal(a1, b1) and np.array_equal(a2, b2)
+    # a single step after the batches continues the same cache
+    s1 = d_g.decode_step(9, ctx + 6)
+    s2 = d_e.decode_step(9, ctx + 6)
+    assert np.array_equal(s1, s2)
+    d_g.close()
+    d_e.close()
+
+
+def test_batch_rejects_bad_calls(rt, orc):
+    cfg = tiny(2)
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=16, ctx=4, seed=5)
+    d = build_ctx(rt, cfg, layers, embed, fnorm, 4, 16)
+    for toks, start in (([], 4), ([1] * 9, 4), ([1, 2], 15), ([1, cfg["vocab"]], 4), ([1], -1)):
+        with pytest.raises(rt.RtError):
+            d.decode_step_batch(toks, start)
+    d.close()
+
+
+def test_gemma3_4b_shape_batch_matches_sequential(rt, orc, dev):
+    """The K=2560 batched lm_head at the full vocabulary: three tokens against
+    three single steps (whose path the oracle test above checks)."""
+    cfg = dict(rt.GEMMA3_4B)
+    ctx = 1024
+    max_seq = ctx + 8
+    H, F, D = cfg["hidden"], cfg["ffn"], cfg["head_dim"]
+    QD, KVD = cfg["n_q_heads"] * D, cfg["n_kv_heads"] * D
+    layers = []
+    s = 12000
+    for _ in range(cfg["n_layers"]):
+        L = {}
+        for name, (rows, cols) in dict(q=(QD, H), k=(KVD, H), v=(KVD, H), o=(H, QD), gate=(F, H), up=(F, H),
+                                       down=(H, F)).items():
+            s += 1
+            L[name] = orc.synth_q4k(s, rows, cols)
+        for name, n in dict(in_norm=H, post_attn_norm=H, pre_ffn_norm=H, post_ffn_norm=H, q_norm=D,
+                            k_norm=D).items():
+            s += 1
+            L[name] = orc.synth_normal(s, n, 0.0, 0.1)
+        s += 1
+        kc = np.zeros((max_seq, KVD), np.float32)
+        kc[:ctx] = orc.synth_normal(s, ctx * KVD).reshape(ctx, KVD)
+        s += 1
+        vc = np.zeros((max_seq, KVD), np.float32)
+        vc[:ctx] = orc.synth_normal(s, ctx * KVD).reshape(ctx, KVD)
+        L["k_cache"], L["v_cache"] = kc, vc
+        layers.append(L)
+    embed = orc.synth_bf16(9888, cfg["vocab"] * H, 0.02)
+    fnorm = orc.synth_normal(9887, H, 0.0, 0.1)
+    toks = [11, 222, 3333]
+    d_b = build_ctx(rt, cfg, layers, embed, fnorm, ctx, max_seq)
+    got = d_b.decode_step_batch(toks, ctx)
+    d_b.close()
+    d_s = build_ctx(rt, cfg, layers, embed, fnorm, ctx, max_seq)
+    for i, t in enumerate(toks):
+        ref = d_s.decode_step(t, ctx + i)
+        err = rel_l2(got[i], ref)
+        print(f"gemma3-4b batch token {i}: rel-L2 vs single step {err:.2e}")
+        assert err < 1e-5
+        assert int(np.argmax(got[i])) == int(np.argmax(ref))
+    d_s.close()
