@@ -228,7 +228,7 @@ def main() -> int:
     if not args.skip_decode:
         ctx = 4096
         cfg = dict(rt.GEMMA3_4B)
-        d = rt.HipDecodeContext(cfg, ctx + args.warmup + args.steps + 8)
+        d = rt.HipDecodeContext(cfg, ctx + args.warmup + args.steps + 8 * (2 + max(2, args.steps // 4)) + 8)
         for li, w in enumerate(layers):
             d.set_layer(li, w)
             kv = torch.randn(2, ctx, KVD, device=dev, generator=gen)
@@ -256,6 +256,22 @@ def main() -> int:
                   "frac_of_hbm_peak": round(dec_bytes / dt / 1e9 / PEAK_HBM_GBS, 4),
                   "launches_per_token": 6 * L + 1}
         log(f"decode step {dt * 1e3:.3f} ms -> {1 / dt:.1f} tok/s")
+        # batched verify (decode_step_batch, M = 8 draft tokens per call)
+        bm = 8
+        reps = max(2, args.steps // 4)
+        for _ in range(2):
+            d.decode_step_batch_async([(pos + i) % V for i in range(bm)], pos)
+            pos += bm
+        d.synchronize()
+        t_start = time.perf_counter()
+        for _ in range(reps):
+            d.decode_step_batch_async([(pos + i) % V for i in range(bm)], pos)
+            pos += bm
+        d.synchronize()
+        dtb = (time.perf_counter() - t_start) / reps
+        decode["batch_verify"] = {"m": bm, "ms_per_call": round(dtb * 1e3, 4), "tok_per_s": round(bm / dtb, 1),
+                                  "note": "layers run per token, lm_head batched over the 8 tokens"}
+        log(f"decode_step_batch M={bm}: {dtb * 1e3:.3f} ms per call -> {bm / dtb:.1f} tok/s")
         d.close()
 
     # ---------------- configs 2 and 4: Q4_K GEMM on the matrix cores ------------
