@@ -157,6 +157,28 @@ rt_status rt_decode_step_batch(rt_decode *d, const int32_t *tokens, int32_t m, i
 rt_status rt_decode_step_batch_async(rt_decode *d, const int32_t *tokens, int32_t m, int32_t start_position);
 /* Device buffer of the last batch's logits, [8][vocab]. */
 rt_status rt_decode_logits_batch(rt_decode *d, float **logits_dev);
+/* Prefill on the GPU: replaces the CPU prefill of generate_cached_streaming
+ * (transformer4.rs:2103-2139, Gemma3Block::forward_cached over the prompt)
+ * plus sync_kv_from_cpu (metal_decode.rs:1366-1396).  Runs tokens[0..n) at
+ * positions start_position .. start_position+n-1 through every layer, fills
+ * those KV rows and leaves the last token's logits in the logits buffer
+ * (copied to logits_host when not NULL); synchronous.  Window rule of the
+ * sliding-window layers:
+ *   RT_PREFILL_REFERENCE  forward_cached's prefill (gqa_attention_cached,
+ *       transformer4.rs:2882-2940): the window is anchored at the end of the
+ *       prompt, so row r sees keys [max(0, n - window), r] and rows before
+ *       n - window get a zero attention output; start_position must be 0.
+ *   RT_PREFILL_SLIDING    each row r sees keys [r + 1 - window, r], the rule
+ *       of the uncached forward (gqa_attention_windowed, 2661-2700) and of
+ *       every decode step, so a prefill equals n decode steps. */
+#define RT_PREFILL_REFERENCE 0
+#define RT_PREFILL_SLIDING 1
+rt_status rt_decode_prefill(rt_decode *d, const int32_t *tokens, int32_t n, int32_t start_position, int32_t mode,
+                            float *logits_host);
+/* Rows per prefill chunk (default 4096): a prompt is processed in chunks of
+ * at most this many tokens, bounding the prefill scratch (about 180 KB per
+ * row at the Gemma-3-4B shape).  No counterpart in the reference. */
+rt_status rt_decode_set_prefill_chunk(rt_decode *d, int32_t rows);
 rt_status rt_decode_synchronize(rt_decode *d);
 /* Use the captured hipGraph (default) or launch the kernels one by one. */
 rt_status rt_decode_set_graph(rt_decode *d, int32_t enabled);

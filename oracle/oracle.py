@@ -317,6 +317,34 @@ def gemma3_decode_step(cfg: dict, layers: list[dict], embed: np.ndarray, final_n
     return (logits, hidden) if want_hidden else logits
 
 
+def gqa_attention_prefill(q, k_cache, v_cache, p0, T, lo_fixed, window, n_q_heads, n_kv_heads, d_head, scale):
+    """orc_gqa_attention_prefill: rows p0 .. p0+T-1, keys [lo(r), r]."""
+    q = np.ascontiguousarray(q, np.float32)
+    k_cache = np.ascontiguousarray(k_cache, np.float32)
+    v_cache = np.ascontiguousarray(v_cache, np.float32)
+    out = np.empty((T, n_q_heads * d_head), np.float32)
+    lib().orc_gqa_attention_prefill(C.c_void_p(_ptr(q)), C.c_void_p(_ptr(k_cache)), C.c_void_p(_ptr(v_cache)),
+                                    C.c_size_t(p0), C.c_size_t(T), C.c_size_t(lo_fixed), C.c_size_t(window),
+                                    C.c_size_t(n_q_heads), C.c_size_t(n_kv_heads), C.c_size_t(d_head),
+                                    C.c_float(scale), C.c_void_p(_ptr(out)))
+    return out
+
+
+def gemma3_prefill(cfg: dict, layers: list[dict], embed: np.ndarray, final_norm: np.ndarray, tokens,
+                   start: int = 0, mode: int = 0, threads: int = 0) -> np.ndarray:
+    """Prefill of `tokens` at positions start.. (forward_cached over the prompt,
+    transformer4.rs:1900-1964 and 2103-2139); mode 0 = the reference's prefill
+    window rule, 1 = per-row sliding window.  Mutates the layers' caches."""
+    c = make_cfg(cfg)
+    arr = make_layers(layers)
+    t = np.ascontiguousarray(np.asarray(tokens, np.uint32))
+    logits = np.empty(cfg["vocab"], np.float32)
+    lib().orc_gemma3_prefill(C.byref(c), arr, C.c_void_p(_ptr(embed)), C.c_void_p(_ptr(final_norm)),
+                             C.c_void_p(_ptr(t)), C.c_size_t(t.size), C.c_size_t(start), C.c_int(mode),
+                             C.c_void_p(_ptr(logits)), C.c_int(threads))
+    return logits
+
+
 # ---------------------------------------------------------------------------
 # seeded synthetic data
 # ---------------------------------------------------------------------------

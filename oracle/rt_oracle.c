@@ -770,6 +770,131 @@ void orc_gemma3_decode_step(const orc_gemma3_cfg *cfg, const orc_layer *layers,
 }
 
 /* ------------------------------------------------------------------------ */
+/* prefill (many query rows per layer)                                       */
+/* ------------------------------------------------------------------------ */
+
+/* Attention of T query rows at absolute positions p0 .. p0+T-1 against the
+ * cache.  Row t (position r = p0 + t) sees keys [lo(r), r] with
+ * lo(r) = max(lo_fixed, window > 0 ? r + 1 - window : 0); an empty range
+ * leaves the row zero.  With lo_fixed = seq_len - window (p0 = 0) this is
+ * gqa_attention_cached's prefill branch (transformer4.rs:2882-2940: k_start
+ * = lo_fixed, "r < k_start attends to nothing", max_kv = r - k_start); with
+ * lo_fixed = 0 and window = w it is gqa_attention_windowed's mask
+ * (2661-2700: c <= r && (r < w || c >= r + 1 - w)).  The arithmetic follows
+ * 2897-2940: scores (q.k)*scale, row max over the valid keys, exp, row sum,
+ * divide, then w.v accumulated over the keys. */
+void orc_gqa_attention_prefill(const float *q, const float *k_cache, const float *v_cache, size_t p0, size_t T,
+                               size_t lo_fixed, size_t window, size_t n_q_heads, size_t n_kv_heads, size_t d_head,
+                               float scale, float *out)
+{
+    size_t kv_stride = n_kv_heads * d_head, q_stride = n_q_heads * d_head;
+    size_t group = n_q_heads / n_kv_heads;
+    float *w = (float *)malloc((p0 + T) * sizeof(float));
+    memset(out, 0, T * q_stride * sizeof(float));
+    for (size_t qh = 0; qh < n_q_heads; qh++) {
+        size_t kv_off = (qh / group) * d_head;
+        for (size_t t = 0; t < T; t++) {
+            size_t r = p0 + t;
+            size_t lo = lo_fixed;
+            if (window > 0 && r + 1 > window && r + 1 - window > lo) lo = r + 1 - window;
+            if (lo > r) continue;  /* no key: the row stays zero */
+            const float *qr = q + t * q_stride + qh * d_head;
+            float row_max = -INFINITY;
+            for (size_t j = lo; j <= r; j++) {
+                const float *kr = k_cache + j * kv_stride + kv_off;
+                float dot = 0.0f;
+                for (size_t d = 0; d < d_head; d++) dot += qr[d] * kr[d];
+                w[j] = dot * scale;
+                row_max = fmaxf(row_max, w[j]);
+            }
+            float row_sum = 0.0f;
+            for (size_t j = lo; j <= r; j++) {
+                w[j] = expf(w[j] - row_max);
+                row_sum += w[j];
+            }
+            if (row_sum > 0.0f)
+                for (size_t j = lo; j <= r; j++) w[j] /= row_sum;
+            float *o = out + t * q_stride + qh * d_head;
+            for (size_t j = lo; j <= r; j++) {
+                const float *vr = v_cache + j * kv_stride + kv_off;
+                for (size_t d = 0; d < d_head; d++) o[d] += w[j] * vr[d];
+            }
+        }
+    }
+    free(w);
+}
+
+/* Prefill of tokens[0..T) at positions p0 .. p0+T-1: Gemma3Block::
+ * forward_cached over all rows at once (transformer4.rs:1900-1964, the
+ * projections through matmul_q4k_t), then the last row's final norm and
+ * lm_head (2131-2139).  mode 0: the reference's prefill window rule
+ * (lo_fixed = T - window for sliding-window layers, p0 must be 0); mode 1:
+ * per-row sliding window.  Appends rows p0 .. p0+T-1 to every layer's
+ * cache. */
+void orc_gemma3_prefill(const orc_gemma3_cfg *cfg, const orc_layer *layers, const uint16_t *embed_bf16,
+                        const float *final_norm, const uint32_t *tokens, size_t T, size_t p0, int mode,
+                        float *logits, int hw)
+{
+    size_t H = (size_t)cfg->hidden, F = (size_t)cfg->ffn, D = (size_t)cfg->head_dim;
+    size_t NQ = (size_t)cfg->n_q_heads, NKV = (size_t)cfg->n_kv_heads;
+    size_t QD = NQ * D, KVD = NKV * D;
+    float scale = sqrtf((float)H);
+    float *x = (float *)malloc(T * H * sizeof(float)), *xn = (float *)malloc(T * H * sizeof(float));
+    float *q = (float *)malloc(T * QD * sizeof(float)), *k = (float *)malloc(T * KVD * sizeof(float));
+    float *v = (float *)malloc(T * KVD * sizeof(float)), *att = (float *)malloc(T * QD * sizeof(float));
+    float *o = (float *)malloc(T * H * sizeof(float)), *x2 = (float *)malloc(T * H * sizeof(float));
+    float *g = (float *)malloc(T * F * sizeof(float)), *u = (float *)malloc(T * F * sizeof(float));
+    float *tmp = (float *)malloc((QD > H ? QD : H) * sizeof(float));
+    for (size_t t = 0; t < T; t++)
+        for (size_t c = 0; c < H; c++) x[t * H + c] = orc_bf16_to_f32(embed_bf16[(size_t)tokens[t] * H + c]) * scale;
+    for (int l = 0; l < cfg->n_layers; l++) {
+        const orc_layer *L = &layers[l];
+        int glob = is_global(cfg, l);
+        float theta = glob ? cfg->rope_theta_global : cfg->rope_theta_local;
+        float fs = glob ? cfg->rope_fs_global : cfg->rope_fs_local;
+        for (size_t t = 0; t < T; t++) orc_rms_norm_gemma3(x + t * H, L->in_norm, H, cfg->eps, xn + t * H);
+        orc_q4k_matmul(xn, T, L->q, QD, H, q, hw);
+        orc_q4k_matmul(xn, T, L->k, KVD, H, k, hw);
+        orc_q4k_matmul(xn, T, L->v, KVD, H, v, hw);
+        for (size_t t = 0; t < T; t++) {
+            orc_per_head_norm(q + t * QD, L->q_norm, NQ, D, cfg->eps, tmp);
+            memcpy(q + t * QD, tmp, QD * sizeof(float));
+            orc_per_head_norm(k + t * KVD, L->k_norm, NKV, D, cfg->eps, tmp);
+            memcpy(k + t * KVD, tmp, KVD * sizeof(float));
+            orc_rope_neox(q + t * QD, NQ, D, theta, p0 + t, fs);
+            orc_rope_neox(k + t * KVD, NKV, D, theta, p0 + t, fs);
+            /* Gemma3LayerKvCache::append (transformer4.rs:1813-1823) */
+            memcpy(L->k_cache + (p0 + t) * KVD, k + t * KVD, KVD * sizeof(float));
+            memcpy(L->v_cache + (p0 + t) * KVD, v + t * KVD, KVD * sizeof(float));
+        }
+        size_t lo_fixed = 0, window = 0;
+        if (!glob && cfg->sliding_window > 0) {
+            size_t w = (size_t)cfg->sliding_window, seq_len = p0 + T;
+            if (mode == 0) lo_fixed = seq_len > w ? seq_len - w : 0;  /* k_start, 1926-1929 */
+            else window = w;
+        }
+        orc_gqa_attention_prefill(q, L->k_cache, L->v_cache, p0, T, lo_fixed, window, NQ, NKV, D, cfg->attn_scale, att);
+        orc_q4k_matmul(att, T, L->o, H, QD, o, hw);
+        for (size_t t = 0; t < T; t++) {
+            orc_rms_norm_gemma3(o + t * H, L->post_attn_norm, H, cfg->eps, tmp);
+            for (size_t c = 0; c < H; c++) x2[t * H + c] = x[t * H + c] + tmp[c];
+            orc_rms_norm_gemma3(x2 + t * H, L->pre_ffn_norm, H, cfg->eps, xn + t * H);
+        }
+        orc_q4k_matmul(xn, T, L->gate, F, H, g, hw);
+        orc_q4k_matmul(xn, T, L->up, F, H, u, hw);
+        for (size_t i = 0; i < T * F; i++) g[i] = orc_gelu_tanh(g[i]) * u[i];
+        orc_q4k_matmul(g, T, L->down, H, F, o, hw);
+        for (size_t t = 0; t < T; t++) {
+            orc_rms_norm_gemma3(o + t * H, L->post_ffn_norm, H, cfg->eps, tmp);
+            for (size_t c = 0; c < H; c++) x[t * H + c] = x2[t * H + c] + tmp[c];
+        }
+    }
+    orc_rms_norm_gemma3(x + (T - 1) * H, final_norm, H, cfg->eps, xn);
+    orc_bf16_gemv_mt(embed_bf16, (size_t)cfg->vocab, H, xn, logits, hw);
+    free(x); free(xn); free(q); free(k); free(v); free(att); free(o); free(x2); free(g); free(u); free(tmp);
+}
+
+/* ------------------------------------------------------------------------ */
 /* seeded synthetic data                                                     */
 /* ------------------------------------------------------------------------ */
 

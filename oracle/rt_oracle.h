@@ -99,6 +99,19 @@ void orc_gemma3_decode_step(const orc_gemma3_cfg *cfg, const orc_layer *layers,
 void orc_gemma3_layer(const orc_gemma3_cfg *cfg, const orc_layer *L, int layer_idx,
                       float *x, uint32_t pos, int hw_threads);
 
+/* Attention of T query rows (positions p0 .. p0+T-1) against the cache; row
+ * r sees keys [max(lo_fixed, window ? r+1-window : 0), r] (transformer4.rs:
+ * 2882-2940 with lo_fixed = k_start; 2661-2700 with window). */
+void orc_gqa_attention_prefill(const float *q, const float *k_cache, const float *v_cache, size_t p0, size_t T,
+                               size_t lo_fixed, size_t window, size_t n_q_heads, size_t n_kv_heads, size_t d_head,
+                               float scale, float *out);
+
+/* Prefill of T tokens at positions p0.. (mode 0: the reference's prefill
+ * window rule, p0 = 0; mode 1: per-row sliding window); last row's logits. */
+void orc_gemma3_prefill(const orc_gemma3_cfg *cfg, const orc_layer *layers, const uint16_t *embed_bf16,
+                        const float *final_norm, const uint32_t *tokens, size_t T, size_t p0, int mode,
+                        float *logits, int hw_threads);
+
 /* ---- seeded synthetic data (counter-based splitmix64) -------------------- */
 uint64_t orc_rng_u64(uint64_t seed, uint64_t i);
 void orc_synth_normal_f32(uint64_t seed, size_t n, float mean, float std, float *out);

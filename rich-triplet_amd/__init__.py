@@ -69,6 +69,8 @@ _SIGNATURES = {
     "rt_decode_step_batch": (_i32, [_vp, _vp, _i32, _i32, _vp]),
     "rt_decode_step_batch_async": (_i32, [_vp, _vp, _i32, _i32]),
     "rt_decode_logits_batch": (_i32, [_vp, C.POINTER(_vp)]),
+    "rt_decode_prefill": (_i32, [_vp, _vp, _i32, _i32, _i32, _vp]),
+    "rt_decode_set_prefill_chunk": (_i32, [_vp, _i32]),
     # GGUF reader and loader (include/rt_gguf.h)
     "rt_gguf_open": (_i32, [C.c_char_p, C.POINTER(_vp)]),
     "rt_gguf_close": (_i32, [_vp]),
@@ -313,6 +315,24 @@ class HipDecodeContext:
         import numpy as np
         t = np.ascontiguousarray(np.asarray(tokens, np.int32))
         check(lib().rt_decode_step_batch_async(self._h, t.ctypes.data, t.size, start_position))
+
+    PREFILL_REFERENCE, PREFILL_SLIDING = 0, 1
+
+    def prefill(self, tokens, start_position: int = 0, mode: int = 0):
+        """GPU prefill (replaces the CPU prefill of generate_cached_streaming,
+        transformer4.rs:2103-2139, and sync_kv_from_cpu): fills KV rows
+        start_position .. start_position+len(tokens)-1 and returns the last
+        token's logits.  mode PREFILL_REFERENCE (0) keeps the reference's
+        prefill window rule (start_position 0); PREFILL_SLIDING (1) windows every
+        row like a decode step."""
+        import numpy as np
+        t = np.ascontiguousarray(np.asarray(tokens, np.int32))
+        out = np.empty(self.cfg["vocab"], np.float32)
+        check(lib().rt_decode_prefill(self._h, t.ctypes.data, t.size, start_position, mode, out.ctypes.data))
+        return out
+
+    def set_prefill_chunk(self, rows: int) -> None:
+        check(lib().rt_decode_set_prefill_chunk(self._h, rows))
 
     def decode_step_async(self, token: int, position: int) -> None:
         check(lib().rt_decode_step_async(self._h, token, position))

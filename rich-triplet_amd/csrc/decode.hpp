@@ -37,6 +37,7 @@ struct LayerArgs {
   float *kc, *vc;          // [max_seq, n_kv_heads*head_dim] f32
   const float *rope_cs;    // [head_dim] cos | sin of this step's angles (in the params block)
   int window;              // sliding window in keys, 0 = global layer
+  int global;              // 1: global layer (RoPE theta_global; never windowed)
 };
 
 // Step-wide device buffers and constants.
@@ -53,10 +54,36 @@ struct DecodeArgs {
 bool decode_shape_supported(const DecodeShape &s, const char **why);
 bool decode_rows_divisible(const DecodeShape &s, const char **why);
 hipError_t enqueue_decode_step(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers, hipStream_t stream);
+// Final residual, final norm and lm_head of the token whose last-layer x2
+// and down-projection output sit in a.x2 / a.dn; logits into a.logits.
+hipError_t enqueue_lm_head(const DecodeShape &s, const DecodeArgs &a, const LayerArgs &last, hipStream_t stream);
 // M tokens at consecutive positions (params slots 0..M-1): the layer kernels
 // of each token in turn, the final norm of each into xn[m][hidden], then one
 // batched lm_head into logits_b[m][vocab].
 hipError_t enqueue_decode_batch(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers, int m,
                                 float *xn, float *logits_b, hipStream_t stream);
+
+// ---------------------------------------------------------------------------
+// Prefill (prefill.hip): a prompt chunk of n tokens through every layer at
+// once.  Device scratch for up to `cap` rows per chunk.
+// ---------------------------------------------------------------------------
+struct PrefillBuffers {
+  int cap = 0;                      // rows the buffers hold
+  int *tokens = nullptr;            // [cap]
+  float *cs = nullptr;              // [cap][2][head_dim]: local cos|sin, global cos|sin of each row's position
+  float *hid = nullptr, *x2 = nullptr, *xn = nullptr, *o = nullptr, *dn = nullptr;  // [cap][hidden]
+  float *q = nullptr, *attn = nullptr;  // [cap][n_q_heads*head_dim]
+  float *k = nullptr, *v = nullptr;     // [cap][n_kv_heads*head_dim]
+  float *g = nullptr, *u = nullptr;     // [cap][ffn]
+  void *ws = nullptr;                   // Q4_K GEMM workspace
+};
+size_t prefill_gemm_workspace_bytes(const DecodeShape &s, int cap);
+// Rows p0 .. p0+n-1 of the prompt (tokens and cos/sin tables already in b).
+// Local layers attend keys [max(lo_fixed, pos + 1 - window), pos] of each row
+// (window 0: no per-row window).  With `logits`, the last row's final norm and
+// lm_head land in a.logits (a.x2 / a.dn are overwritten).
+hipError_t enqueue_prefill_chunk(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers,
+                                 const PrefillBuffers &b, int p0, int n, int lo_fixed, int window, bool logits,
+                                 hipStream_t stream);
 
 }  // namespace rt

@@ -8,8 +8,10 @@
 // replayed; token id and position travel through a device buffer.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <thread>
 #include <vector>
 
 #include "../../include/rt_hip.h"
@@ -41,6 +43,11 @@ struct rt_decode {
   hipGraphExec_t exec = nullptr;
   bool graph_enabled = true;
   bool graph_dirty = true;
+  PrefillBuffers pf;                     // rt_decode_prefill scratch (grown on demand)
+  int pf_chunk = 4096;                   // rows per prefill chunk (~180 KB of scratch per row at Gemma-3-4B)
+  std::vector<void *> pf_owned;
+  int *pf_tokens_host = nullptr;         // pinned staging: [pf.cap] tokens, [pf.cap][2][head_dim] cos/sin
+  float *pf_cs_host = nullptr;
 };
 
 namespace {
@@ -191,6 +198,7 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
       const bool g = is_global(c, l);
       L.rope_cs = cs_dev + (g ? D : 0);
       L.window = g ? 0 : c.sliding_window;
+      L.global = g ? 1 : 0;
     }
   }
 #undef TRY
@@ -209,6 +217,8 @@ rt_status rt_decode_destroy(rt_decode *d) {
   for (void *p : d->owned)
     if (p) (void)hipFree(p);
   if (d->params_host) (void)hipHostFree(d->params_host);
+  if (d->pf_tokens_host) (void)hipHostFree(d->pf_tokens_host);
+  if (d->pf_cs_host) (void)hipHostFree(d->pf_cs_host);
   if (d->params_copied) (void)hipEventDestroy(d->params_copied);
   if (d->stream) (void)hipStreamDestroy(d->stream);
   delete d;
@@ -438,6 +448,141 @@ rt_status rt_decode_step(rt_decode *d, int32_t token, int32_t position, float *l
     e = hipMemcpyAsync(logits_host, d->args.logits, (size_t)d->cfg.vocab * 4, hipMemcpyDeviceToHost, d->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
   return hip_error(e, "rt_decode_step");
+}
+
+// ---------------------------------------------------------------------------
+// Prefill
+// ---------------------------------------------------------------------------
+static rt_status prefill_reserve(rt_decode *d, int cap) {
+  PrefillBuffers &b = d->pf;
+  if (b.cap >= cap) return RT_OK;
+  hipError_t e = hipStreamSynchronize(d->stream);
+  if (e != hipSuccess) return hip_error(e, "rt_decode_prefill");
+  for (void *p : d->pf_owned) dfree(d, p);
+  d->pf_owned.clear();
+  if (d->pf_tokens_host) (void)hipHostFree(d->pf_tokens_host);
+  if (d->pf_cs_host) (void)hipHostFree(d->pf_cs_host);
+  d->pf_tokens_host = nullptr;
+  d->pf_cs_host = nullptr;
+  b = PrefillBuffers{};
+  const rt_gemma3_config &c = d->cfg;
+  const size_t H = c.hidden, F = c.ffn, D = c.head_dim, QD = (size_t)c.n_q_heads * D, KVD = (size_t)c.n_kv_heads * D;
+  const size_t rows = (size_t)cap;
+  auto get = [&](size_t bytes, void **dst) -> rt_status {
+    rt_status st = dalloc(d, std::max<size_t>(bytes, 256), dst);
+    if (st == RT_OK) d->pf_owned.push_back(*dst);
+    return st;
+  };
+  rt_status st = RT_OK;
+  void *p = nullptr;
+#define PF_GET(field, type, count)                     \
+  if ((st = get((count) * sizeof(type), &p)) != RT_OK) \
+    return st;                                         \
+  b.field = static_cast<type *>(p);
+  PF_GET(tokens, int, rows);
+  PF_GET(cs, float, rows * 2 * D);
+  PF_GET(hid, float, rows * H);
+  PF_GET(x2, float, rows * H);
+  PF_GET(xn, float, rows * H);
+  PF_GET(o, float, rows * H);
+  PF_GET(dn, float, rows * H);
+  PF_GET(q, float, rows * QD);
+  PF_GET(attn, float, rows * QD);
+  PF_GET(k, float, rows * KVD);
+  PF_GET(v, float, rows * KVD);
+  PF_GET(g, float, rows * F);
+  PF_GET(u, float, rows * F);
+#undef PF_GET
+  if ((st = get(prefill_gemm_workspace_bytes(d->shape, cap), &b.ws)) != RT_OK) return st;
+  e = hipHostMalloc((void **)&d->pf_tokens_host, rows * sizeof(int), hipHostMallocDefault);
+  if (e == hipSuccess) e = hipHostMalloc((void **)&d->pf_cs_host, rows * 2 * D * sizeof(float), hipHostMallocDefault);
+  if (e != hipSuccess) return hip_error(e, "rt_decode_prefill hipHostMalloc");
+  b.cap = cap;
+  return RT_OK;
+}
+
+// cos/sin tables of positions p0 .. p0+n-1, local then global per row, with
+// the host libm as fill_slot computes them for a decode step.
+static void prefill_rope_tables(rt_decode *d, int p0, int n) {
+  const int D = d->cfg.head_dim, P = D / 2;
+  auto rows = [&](int t0, int t1) {
+    for (int t = t0; t < t1; ++t) {
+      float *cs = d->pf_cs_host + (size_t)t * 2 * D;
+      for (int k = 0; k < 2; ++k, cs += D) {
+        const float fs = k ? d->cfg.rope_fs_global : d->cfg.rope_fs_local;
+        const float *den = k ? d->rope_den_global.data() : d->rope_den_local.data();
+        const float pf = (float)(p0 + t) * fs;
+        for (int i = 0; i < P; ++i) {
+          const float ang = pf / den[i];
+          cs[i] = cosf(ang);
+          cs[P + i] = sinf(ang);
+        }
+      }
+    }
+  };
+  const int nt = std::max(1, std::min({16, (int)std::thread::hardware_concurrency(), n / 64}));
+  if (nt == 1) {
+    rows(0, n);
+    return;
+  }
+  std::vector<std::thread> pool;
+  const int per = (n + nt - 1) / nt;
+  for (int i = 0; i < nt; ++i) pool.emplace_back(rows, std::min(n, i * per), std::min(n, (i + 1) * per));
+  for (auto &th : pool) th.join();
+}
+
+rt_status rt_decode_prefill(rt_decode *d, const int32_t *tokens, int32_t n, int32_t start_position, int32_t mode,
+                            float *logits_host) {
+  if (!d || !tokens) return set_error(RT_EINVAL, "rt_decode_prefill: null pointer");
+  if (n < 1) return set_error(RT_EINVAL, "rt_decode_prefill: n=%d must be >= 1", n);
+  if (mode != RT_PREFILL_REFERENCE && mode != RT_PREFILL_SLIDING)
+    return set_error(RT_EINVAL, "rt_decode_prefill: unknown mode %d", mode);
+  if (mode == RT_PREFILL_REFERENCE && start_position != 0)
+    return set_error(RT_EINVAL, "rt_decode_prefill: RT_PREFILL_REFERENCE starts at position 0 (got %d)",
+                     start_position);
+  if (start_position < 0 || (int64_t)start_position + n > d->cfg.max_seq)
+    return set_error(RT_EINVAL, "rt_decode_prefill: positions [%d, %lld) outside [0, max_seq=%d)", start_position,
+                     (long long)start_position + n, d->cfg.max_seq);
+  for (int i = 0; i < n; ++i) {
+    rt_status st = check_ready(d, tokens[i], start_position + i);
+    if (st != RT_OK) return st;
+  }
+  const int w = d->cfg.sliding_window;
+  int lo_fixed = 0, window = 0;
+  if (mode == RT_PREFILL_REFERENCE)
+    lo_fixed = (w > 0 && n > w) ? n - w : 0;  // k_start = seq_len - window (transformer4.rs:1926-1929)
+  else
+    window = w;
+  const int cap = std::min(n, d->pf_chunk);
+  rt_status st = prefill_reserve(d, cap);
+  if (st != RT_OK) return st;
+  const int D = d->cfg.head_dim;
+  hipError_t e = hipSuccess;
+  for (int c0 = 0; c0 < n && e == hipSuccess; c0 += cap) {
+    const int cn = std::min(cap, n - c0);
+    e = hipStreamSynchronize(d->stream);  // the staging buffers are free again
+    if (e != hipSuccess) break;
+    std::memcpy(d->pf_tokens_host, tokens + c0, (size_t)cn * sizeof(int));
+    prefill_rope_tables(d, start_position + c0, cn);
+    e = hipMemcpyAsync(d->pf.tokens, d->pf_tokens_host, (size_t)cn * sizeof(int), hipMemcpyHostToDevice, d->stream);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(d->pf.cs, d->pf_cs_host, (size_t)cn * 2 * D * sizeof(float), hipMemcpyHostToDevice,
+                         d->stream);
+    if (e == hipSuccess)
+      e = enqueue_prefill_chunk(d->shape, d->args, d->layers.data(), d->pf, start_position + c0, cn, lo_fixed,
+                                window, c0 + cn == n, d->stream);
+  }
+  if (e == hipSuccess && logits_host)
+    e = hipMemcpyAsync(logits_host, d->args.logits, (size_t)d->cfg.vocab * 4, hipMemcpyDeviceToHost, d->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
+  return hip_error(e, "rt_decode_prefill");
+}
+
+rt_status rt_decode_set_prefill_chunk(rt_decode *d, int32_t rows) {
+  if (!d) return set_error(RT_EINVAL, "rt_decode_set_prefill_chunk: null context");
+  if (rows < 1) return set_error(RT_EINVAL, "rt_decode_set_prefill_chunk: rows=%d must be >= 1", rows);
+  d->pf_chunk = rows;
+  return RT_OK;
 }
 
 rt_status rt_decode_synchronize(rt_decode *d) {

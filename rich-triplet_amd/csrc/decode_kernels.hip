@@ -18,6 +18,7 @@
 #include <vector>
 
 #include "decode.hpp"
+#include "gemma3_math.hpp"
 #include "q4k_gemv.hpp"
 #include "rt_device.hpp"
 
@@ -25,32 +26,7 @@ namespace rt {
 
 // ---------------------------------------------------------------------------
 // Prologues: build the normalised activation vector in the LDS x layout.
-// Arithmetic order follows rms_norm_gemma3 (autograd2.rs:3477-3496):
-//   rinv = 1/sqrt(sum(x^2) * (1/K) + eps);  out = (x * rinv) * (1 + gamma)
 // ---------------------------------------------------------------------------
-RT_DEV float rms_inv_from_sumsq(float ss, float inv_k, float eps) {
-#pragma clang fp contract(off)
-  return 1.0f / sqrtf(ss * inv_k + eps);
-}
-
-RT_DEV float4 norm4(float4 x, float rinv, float4 g) {
-#pragma clang fp contract(off)
-  return make_float4((x.x * rinv) * (1.0f + g.x), (x.y * rinv) * (1.0f + g.y), (x.z * rinv) * (1.0f + g.z),
-                     (x.w * rinv) * (1.0f + g.w));
-}
-
-RT_DEV float4 add4(float4 a, float4 b) {
-#pragma clang fp contract(off)
-  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
-}
-
-RT_DEV float mul_nc(float a, float b) {
-#pragma clang fp contract(off)
-  return a * b;
-}
-
-RT_DEV float sumsq4(float4 v) { return v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w; }
-
 enum class Pro { Embed, Resid };
 
 // x = Embed: bf16(E[token]) * embed_scale        (transformer4.rs:2360-2368)
@@ -230,34 +206,6 @@ __global__ __launch_bounds__(T) void k_gemv(const uint8_t *__restrict__ W, const
 //      out = sum_i o_i e^(m_i-M) / sum_i l_i e^(m_i-M).
 // Together they equal gqa_attention_cached's t_q == 1 branch (2806-2879).
 // ---------------------------------------------------------------------------
-template <int D>
-RT_DEV void norm_rope_head(const float *__restrict__ src, const float *__restrict__ gamma,
-                           const float *__restrict__ cs, float eps, float *dst) {
-  // One wave; lane owns pairs i = lane*P + p (p < P) with partners i + D/2.
-  // cs[i] = cos, cs[D/2 + i] = sin of the pair's angle.
-  constexpr int P = D / 128;
-  const int lane = threadIdx.x & 63;
-  float x0[P], x1[P];
-  float ss = 0.f;
-#pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int i = lane * P + p;
-    x0[p] = src[i];
-    x1[p] = src[i + D / 2];
-    ss += x0[p] * x0[p] + x1[p] * x1[p];
-  }
-  const float rinv = rms_inv_from_sumsq(wave_sum(ss), 1.0f / (float)D, eps);
-#pragma unroll
-  for (int p = 0; p < P; ++p) {
-#pragma clang fp contract(off)
-    const int i = lane * P + p;
-    const float a0 = (x0[p] * rinv) * (1.0f + gamma[i]);
-    const float a1 = (x1[p] * rinv) * (1.0f + gamma[i + D / 2]);
-    const float c = cs[i], sn = cs[D / 2 + i];
-    dst[i] = a0 * c - a1 * sn;
-    dst[i + D / 2] = a0 * sn + a1 * c;
-  }
-}
 
 template <int D, int G, int SUB>
 __global__ __launch_bounds__(256) void k_attn(DecodeArgs a, LayerArgs L) {
@@ -727,17 +675,18 @@ static hipError_t enqueue_layers(const DecodeShape &s, const DecodeArgs &a, cons
   return l.err;
 }
 
-hipError_t enqueue_decode_step(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers, hipStream_t stream) {
+hipError_t enqueue_lm_head(const DecodeShape &s, const DecodeArgs &a, const LayerArgs &last, hipStream_t stream) {
   Launch l{stream};
-  const bool big = s.hidden == 2560;
-  l.err = enqueue_layers(s, a, layers, stream);
-  if (l.err == hipSuccess) {
-    const dim3 grid(1024);
-    if (big) hipLaunchKernelGGL((k_lmhead<5>), grid, dim3(256), 0, l.s, a, layers[s.n_layers - 1]);
-    else hipLaunchKernelGGL((k_lmhead<1>), grid, dim3(256), 0, l.s, a, layers[s.n_layers - 1]);
-    l.check();
-  }
+  const dim3 grid(1024);
+  if (s.hidden == 2560) hipLaunchKernelGGL((k_lmhead<5>), grid, dim3(256), 0, l.s, a, last);
+  else hipLaunchKernelGGL((k_lmhead<1>), grid, dim3(256), 0, l.s, a, last);
+  l.check();
   return l.err;
+}
+
+hipError_t enqueue_decode_step(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers, hipStream_t stream) {
+  hipError_t e = enqueue_layers(s, a, layers, stream);
+  return e == hipSuccess ? enqueue_lm_head(s, a, layers[s.n_layers - 1], stream) : e;
 }
 
 hipError_t enqueue_decode_batch(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers, int m,

@@ -1,0 +1,461 @@
+// prefill.hip -- GPU prefill for the Gemma-3 decode context: every token of a
+// prompt chunk goes through each layer at once (one row per token), filling
+// the KV cache rows of the chunk and, for the last chunk, the logits of the
+// last token.
+//
+// Replaces the reference's CPU prefill in generate_cached_streaming
+// (transformer4.rs:2103-2139: Gemma3Block::forward_cached over the whole
+// prompt, 1900-1964) and the copy of its KV cache to the device that follows
+// (sync_kv_from_cpu, metal_decode.rs:1366-1396).  Per layer:
+//   k_pf_norm        input RMSNorm (layer 0) / post-norm residual + next norm
+//   Q4_K GEMM x3     q, k, v projections (q4k_gemm.hip, matrix cores)
+//   k_pf_qk_rope     per-head q/k RMSNorm + NeoX RoPE; k and v into the cache
+//   k_pf_attn        causal (windowed) attention on bf16 MFMA
+//   Q4_K GEMM        o projection
+//   k_pf_norm        residual + post-attention norm, pre-FFN norm
+//   Q4_K GEMM x2     gate, up
+//   k_pf_gelu_mul    gelu_tanh(gate) * up
+//   Q4_K GEMM        down projection
+// The per-element arithmetic (norms, RoPE, residuals, GELU) is the decode
+// step's (gemma3_math.hpp); the projections are GEMMs instead of GEMVs.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "decode.hpp"
+#include "gemma3_math.hpp"
+#include "rt_device.hpp"
+#include "rt_kernels.hpp"
+
+namespace rt {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// Row kernels
+// ---------------------------------------------------------------------------
+// x[t] = bf16(E[token_t]) * sqrt(hidden)   (transformer4.rs:2106-2121)
+__global__ __launch_bounds__(256) void k_pf_embed(const int *__restrict__ tokens, const uint16_t *__restrict__ E,
+                                                  float scale, float *__restrict__ x, int H) {
+  const uint16_t *row = E + (size_t)tokens[blockIdx.x] * H;
+  float *out = x + (size_t)blockIdx.x * H;
+  for (int c = threadIdx.x; c < H; c += 256) out[c] = mul_nc(bf16_lo((uint32_t)row[c]), scale);
+}
+
+// One row per workgroup, H <= 4096 (H % 4 == 0).
+//   RESID:  x = base + rms(add)(1 + g_add);  x_out = x;  xn = rms(x)(1 + g_out)
+//   !RESID: x = add;                                     xn = rms(x)(1 + g_out)
+template <bool RESID>
+__global__ __launch_bounds__(256) void k_pf_norm(const float *__restrict__ base, const float *__restrict__ add,
+                                                 const float *__restrict__ g_add, const float *__restrict__ g_out,
+                                                 float *__restrict__ x_out, float *__restrict__ xn_out, int H,
+                                                 float eps) {
+  constexpr int PER = 4;
+  __shared__ float red[4];
+  const size_t off = (size_t)blockIdx.x * (H / 4);
+  const int F4 = H / 4;
+  const float inv_k = 1.0f / (float)H;
+  const float4 *a4 = reinterpret_cast<const float4 *>(add) + off;
+  float4 x[PER];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int f = threadIdx.x + i * 256;
+    x[i] = f < F4 ? a4[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+    ss += sumsq4(x[i]);
+  }
+  if constexpr (RESID) {
+    const float ra = rms_inv_from_sumsq(block_sum<256>(ss, red), inv_k, eps);
+    const float4 *b4 = reinterpret_cast<const float4 *>(base) + off;
+    float4 *xo = reinterpret_cast<float4 *>(x_out) + off;
+    ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int f = threadIdx.x + i * 256;
+      if (f < F4) {
+        x[i] = add4(b4[f], norm4(x[i], ra, reinterpret_cast<const float4 *>(g_add)[f]));
+        xo[f] = x[i];
+        ss += sumsq4(x[i]);
+      }
+    }
+  }
+  const float rx = rms_inv_from_sumsq(block_sum<256>(ss, red), inv_k, eps);
+  float4 *xn = reinterpret_cast<float4 *>(xn_out) + off;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int f = threadIdx.x + i * 256;
+    if (f < F4) xn[f] = norm4(x[i], rx, reinterpret_cast<const float4 *>(g_out)[f]);
+  }
+}
+
+// One wave per (row, head): q heads in place, k heads into the cache row
+// p0 + t (with the matching v row copied next to it), as the decode step's
+// k_attn does for its single row (transformer4.rs:1912-1923).
+template <int D>
+__global__ __launch_bounds__(256) void k_pf_qk_rope(float *q, const float *__restrict__ k, const float *__restrict__ v,
+                                                    const float *__restrict__ g_q, const float *__restrict__ g_k,
+                                                    const float *__restrict__ cs, int cs_off, float *__restrict__ kc,
+                                                    float *__restrict__ vc, int p0, int n, int nq, int nkv, float eps) {
+  const int heads = nq + nkv;
+  const int item = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (item >= n * heads) return;  // whole waves
+  const int t = item / heads, h = item % heads;
+  const float *c = cs + (size_t)t * 2 * D + cs_off;
+  if (h < nq) {
+    float *qr = q + ((size_t)t * nq + h) * D;
+    norm_rope_head<D>(qr, g_q, c, eps, qr);
+  } else {
+    const int kh = h - nq;
+    const size_t src = ((size_t)t * nkv + kh) * D, dst = ((size_t)(p0 + t) * nkv + kh) * D;
+    norm_rope_head<D>(k + src, g_k, c, eps, kc + dst);
+    for (int i = threadIdx.x & 63; i < D; i += 64) vc[dst + i] = v[src + i];
+  }
+}
+
+// h = gelu_tanh(g) * u  (Gemma3Mlp::forward, transformer4.rs:328-334)
+// h may alias g (each element is read before it is written, by one thread).
+__global__ __launch_bounds__(256) void k_pf_gelu_mul(const float *g, const float *__restrict__ u, float *h,
+                                                     size_t n4) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
+    const float4 a = reinterpret_cast<const float4 *>(g)[i], b = reinterpret_cast<const float4 *>(u)[i];
+    reinterpret_cast<float4 *>(h)[i] = make_float4(mul_nc(gelu_tanh(a.x), b.x), mul_nc(gelu_tanh(a.y), b.y),
+                                                   mul_nc(gelu_tanh(a.z), b.z), mul_nc(gelu_tanh(a.w), b.w));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// k_pf_attn: causal attention of a chunk of query rows against the f32 KV
+// cache (gqa_attention_cached's prefill branch, transformer4.rs:2882-2940,
+// and the per-row window of gqa_attention_windowed, 2661-2700).
+//
+// Query row t (absolute position r = p0 + t) sees keys
+//   [lo(r), r],  lo(r) = max(lo_fixed, window ? r + 1 - window : 0),
+// and an empty range gives a zero output row (the reference's rows that
+// precede the window start).
+//
+// Matrix cores: v_mfma_f32_16x16x32_bf16 with every f32 operand x split into
+// bf16 parts hi = bf16(x), lo = bf16(x - hi) (|x - hi - lo| <= 2^-16 |x|) and
+// the products hi*hi + hi*lo + lo*hi accumulated in f32.
+//   scores   S^T[key][col] = K . Q^T  (A = 16 keys x 32 dims from LDS,
+//            B = this wave's 16 query columns, held in registers)
+//   output   O^T[dim][col] += V^T . P^T (A = 16 dims x 32 keys from LDS,
+//            B = the probabilities, taken from the lanes' own score registers)
+// A query column is a (row, head) pair; the G heads that share a KV head sit
+// in adjacent columns and share every K/V tile.  Lane (c = l%16, g = l/16)
+// holds score rows 4g..4g+3 of each 16-key tile; the MFMA's k index 8g + i
+// stands for key 4g + i (i < 4) or 16 + 4g + (i - 4) (i >= 4), for A and B
+// alike, so the probabilities feed the second MFMA without leaving the lane.
+// Softmax is online over stages of 32 keys (running max and sum per column).
+// ---------------------------------------------------------------------------
+constexpr int kPfKeys = 32;  // keys per LDS stage
+
+struct PfAttnArgs {
+  int p0, n, n_kv_heads;
+  int lo_fixed, window;
+  float scale;
+};
+
+template <int D>
+struct PfAttnSmem {
+  static constexpr int KP = D + 8;        // K row pitch (bf16): rows 16 B apart in the bank space
+  static constexpr int VP = kPfKeys + 4;  // V^T row pitch (bf16): 72 B
+  uint16_t khi[kPfKeys * KP], klo[kPfKeys * KP];
+  uint16_t vhi[D * VP], vlo[D * VP];
+};
+
+RT_DEV int pf_key_lo(const PfAttnArgs &p, int r) { return max(p.lo_fixed, p.window > 0 ? r - p.window + 1 : 0); }
+
+// Two f32 -> packed bf16 hi parts (.x) and lo parts (.y), RNE (v_cvt_pk_bf16_f32).
+RT_DEV uint2 split_pair(float a, float b) {
+  const f32x2_t x = {a, b};
+  const bf16x2_t h = __builtin_convertvector(x, bf16x2_t);
+  const f32x2_t r = x - __builtin_convertvector(h, f32x2_t);
+  return make_uint2(__builtin_bit_cast(uint32_t, h), __builtin_bit_cast(uint32_t, __builtin_convertvector(r, bf16x2_t)));
+}
+
+// Eight f32 -> a bf16x8 hi fragment and lo fragment.
+RT_DEV void split8(const float (&x)[8], u32x4_t &hi, u32x4_t &lo) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint2 v = split_pair(x[2 * i], x[2 * i + 1]);
+    hi[i] = v.x;
+    lo[i] = v.y;
+  }
+}
+
+RT_DEV f32x4_t mfma3(u32x4_t ahi, u32x4_t alo, u32x4_t bhi, u32x4_t blo, f32x4_t acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, alo), __builtin_bit_cast(bf16x8_t, bhi),
+                                                acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ahi), __builtin_bit_cast(bf16x8_t, blo),
+                                                acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ahi), __builtin_bit_cast(bf16x8_t, bhi),
+                                                 acc, 0, 0, 0);
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(256) void k_pf_attn(const float *__restrict__ q, const float *__restrict__ kc,
+                                                 const float *__restrict__ vc, float *__restrict__ out, PfAttnArgs p) {
+  constexpr int KB = kPfKeys;
+  constexpr int DS = D / 32;                  // k steps of the score MFMA
+  constexpr int DT = D / 16;                  // 16-dim tiles of the output
+  constexpr int KQ = D / 4;                   // float4 per cache row
+  constexpr int K_ITEMS = KB * KQ / 256;      // K float4 per thread per stage
+  constexpr int V_ITEMS = KB / 2 * KQ / 256;  // V key pairs x float4 per thread per stage
+  static_assert(K_ITEMS >= 1 && V_ITEMS >= 1, "D too small");
+  using S = PfAttnSmem<D>;
+  __shared__ __attribute__((aligned(16))) S sm;
+
+  const int b = (int)(gridDim.x - 1 - blockIdx.x);  // late rows (the longest key ranges) first
+  const int kvh = (int)blockIdx.y;
+  const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63), n16 = lane & 15, g = lane >> 4;
+  const size_t qd = (size_t)p.n_kv_heads * G * D, kvd = (size_t)p.n_kv_heads * D;
+  const int col0 = b * 64;
+  const int last_row = p.n - 1;
+  const int key_first = pf_key_lo(p, p.p0 + col0 / G) & ~(KB - 1);
+  const int key_last = p.p0 + min(last_row, (col0 + 63) / G);
+  const int wt0 = (col0 + 16 * wave) / G;
+  const bool wave_live = wt0 <= last_row;
+  const int wkey_lo = pf_key_lo(p, p.p0 + wt0);
+  const int wkey_hi = p.p0 + min(last_row, (col0 + 16 * wave + 15) / G);
+  const int col = col0 + 16 * wave + n16;
+  const int t = col / G;
+  const bool col_ok = t <= last_row;
+  const int r = p.p0 + t;
+  const int klo = pf_key_lo(p, r);
+  const int hq = kvh * G + col % G;
+
+  // this lane's query fragment: dims 32s + 8g + [0, 8) of column `col`
+  u32x4_t qh[DS], ql[DS];
+  {
+    const float *qrow = q + (size_t)min(t, last_row) * qd + (size_t)hq * D + 8 * g;
+#pragma unroll
+    for (int s = 0; s < DS; ++s) {
+      const float4 x0 = *reinterpret_cast<const float4 *>(qrow + 32 * s);
+      const float4 x1 = *reinterpret_cast<const float4 *>(qrow + 32 * s + 4);
+      const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      split8(x, qh[s], ql[s]);
+    }
+  }
+
+  // stage loads: rows clamped to key_last (keys past it are masked)
+  float4 kr[K_ITEMS], vr[V_ITEMS][2];
+  const float *kbase = kc + (size_t)kvh * D, *vbase = vc + (size_t)kvh * D;
+  auto load_stage = [&](int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < K_ITEMS; ++i) {
+      const int it = (int)threadIdx.x + 256 * i, key = it / KQ, qq = it % KQ;
+      kr[i] = *reinterpret_cast<const float4 *>(kbase + (size_t)min(k0 + key, key_last) * kvd + 4 * qq);
+    }
+#pragma unroll
+    for (int i = 0; i < V_ITEMS; ++i) {
+      const int it = (int)threadIdx.x + 256 * i, pr = it / KQ, qq = it % KQ;
+      vr[i][0] = *reinterpret_cast<const float4 *>(vbase + (size_t)min(k0 + 2 * pr, key_last) * kvd + 4 * qq);
+      vr[i][1] = *reinterpret_cast<const float4 *>(vbase + (size_t)min(k0 + 2 * pr + 1, key_last) * kvd + 4 * qq);
+    }
+  };
+  auto store_stage = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < K_ITEMS; ++i) {
+      const int it = (int)threadIdx.x + 256 * i, key = it / KQ, qq = it % KQ;
+      const uint2 p0 = split_pair(kr[i].x, kr[i].y), p1 = split_pair(kr[i].z, kr[i].w);
+      *reinterpret_cast<uint2 *>(&sm.khi[key * S::KP + 4 * qq]) = make_uint2(p0.x, p1.x);
+      *reinterpret_cast<uint2 *>(&sm.klo[key * S::KP + 4 * qq]) = make_uint2(p0.y, p1.y);
+    }
+#pragma unroll
+    for (int i = 0; i < V_ITEMS; ++i) {
+      const int it = (int)threadIdx.x + 256 * i, pr = it / KQ, qq = it % KQ;
+      const float a[4] = {vr[i][0].x, vr[i][0].y, vr[i][0].z, vr[i][0].w};
+      const float c[4] = {vr[i][1].x, vr[i][1].y, vr[i][1].z, vr[i][1].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint2 hl = split_pair(a[e], c[e]);
+        *reinterpret_cast<uint32_t *>(&sm.vhi[(4 * qq + e) * S::VP + 2 * pr]) = hl.x;
+        *reinterpret_cast<uint32_t *>(&sm.vlo[(4 * qq + e) * S::VP + 2 * pr]) = hl.y;
+      }
+    }
+  };
+
+  f32x4_t o[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  load_stage(key_first);
+#pragma unroll 1
+  for (int k0 = key_first; k0 <= key_last; k0 += KB) {
+    __syncthreads();  // every wave is done with the previous stage
+    store_stage();
+    __syncthreads();
+    if (k0 + KB <= key_last) load_stage(k0 + KB);  // lands during this stage's MFMAs
+    if (!wave_live || k0 > wkey_hi || k0 + KB - 1 < wkey_lo) continue;  // wave-uniform
+
+    f32x4_t sc[2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+      const int ko = (16 * tt + n16) * S::KP + 8 * g;
+#pragma unroll
+      for (int s = 0; s < DS; ++s) {
+        const u32x4_t ah = *reinterpret_cast<const u32x4_t *>(&sm.khi[ko + 32 * s]);
+        const u32x4_t al = *reinterpret_cast<const u32x4_t *>(&sm.klo[ko + 32 * s]);
+        acc = mfma3(ah, al, qh[s], ql[s], acc);
+      }
+      sc[tt] = acc;
+    }
+    // mask, scale (scores = (q.k) * scale, transformer4.rs:2897) and the running softmax
+    float sv[8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = k0 + 16 * tt + 4 * g + j;
+        const bool ok = col_ok && key <= r && key >= klo;
+        sv[4 * tt + j] = ok ? sc[tt][j] * p.scale : -INFINITY;
+        mx = fmaxf(mx, sv[4 * tt + j]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float mb = m_new == -INFINITY ? 0.f : m_new;  // a column with no key yet keeps zeros
+    const float alpha = expf(m_run - mb);
+    float pv[8], ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      pv[i] = expf(sv[i] - mb);
+      ps += pv[i];
+    }
+    ps += __shfl_xor(ps, 16);
+    ps += __shfl_xor(ps, 32);
+    l_run = l_run * alpha + ps;
+    m_run = m_new;
+    u32x4_t ph, pl;
+    split8(pv, ph, pl);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int vo = (16 * dt + n16) * S::VP + 4 * g;
+      const uint2 h0 = *reinterpret_cast<const uint2 *>(&sm.vhi[vo]);
+      const uint2 h1 = *reinterpret_cast<const uint2 *>(&sm.vhi[vo + 16]);
+      const uint2 l0 = *reinterpret_cast<const uint2 *>(&sm.vlo[vo]);
+      const uint2 l1 = *reinterpret_cast<const uint2 *>(&sm.vlo[vo + 16]);
+      const u32x4_t ah = {h0.x, h0.y, h1.x, h1.y}, al = {l0.x, l0.y, l1.x, l1.y};
+      o[dt] *= alpha;
+      o[dt] = mfma3(ah, al, ph, pl, o[dt]);
+    }
+  }
+
+  if (col_ok) {
+    const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
+    float *orow = out + (size_t)t * qd + (size_t)hq * D + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      *reinterpret_cast<float4 *>(orow + 16 * dt) =
+          make_float4(o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
+  }
+}
+
+template <int D>
+hipError_t launch_pf_attn(int G, dim3 grid, hipStream_t st, const float *q, const float *kc, const float *vc,
+                          float *out, const PfAttnArgs &p) {
+  switch (G) {
+    case 1: hipLaunchKernelGGL((k_pf_attn<D, 1>), grid, dim3(256), 0, st, q, kc, vc, out, p); break;
+    case 2: hipLaunchKernelGGL((k_pf_attn<D, 2>), grid, dim3(256), 0, st, q, kc, vc, out, p); break;
+    case 4: hipLaunchKernelGGL((k_pf_attn<D, 4>), grid, dim3(256), 0, st, q, kc, vc, out, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+size_t prefill_gemm_workspace_bytes(const DecodeShape &s, int cap) {
+  const int H = s.hidden, F = s.ffn, QD = s.n_q_heads * s.head_dim, KVD = s.n_kv_heads * s.head_dim;
+  const int shapes[5][2] = {{QD, H}, {KVD, H}, {H, QD}, {F, H}, {H, F}};
+  // A chunk may hold fewer rows than cap, and a smaller M may split K more
+  // ways: take the largest requirement over every row count up to cap.
+  size_t m = 0;
+  for (auto &nk : shapes) {
+    m = std::max(m, q4k_gemm_workspace_bytes(cap, nk[0], nk[1]));
+    for (int rows = 1; rows <= std::min(cap, 1024); ++rows)
+      m = std::max(m, q4k_gemm_workspace_bytes(rows, nk[0], nk[1]));
+  }
+  return m;
+}
+
+hipError_t enqueue_prefill_chunk(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers,
+                                 const PrefillBuffers &b, int p0, int n, int lo_fixed, int window, bool logits,
+                                 hipStream_t st) {
+  const int H = s.hidden, F = s.ffn, D = s.head_dim, nq = s.n_q_heads, nkv = s.n_kv_heads;
+  const int QD = nq * D, KVD = nkv * D, G = nq / nkv;
+  hipError_t e = hipSuccess;
+#define PF_CHECK(x)               \
+  do {                            \
+    x;                            \
+    e = hipGetLastError();        \
+    if (e != hipSuccess) return e; \
+  } while (0)
+#define PF_TRY(x)                 \
+  do {                            \
+    e = (x);                      \
+    if (e != hipSuccess) return e; \
+  } while (0)
+  auto gemm = [&](const float *A, const uint8_t *W, float *C, int N, int K) {
+    return launch_q4k_gemm(A, false, W, C, n, N, K, b.ws, st);
+  };
+  PF_CHECK(hipLaunchKernelGGL(k_pf_embed, dim3(n), dim3(256), 0, st, b.tokens, a.embed, a.embed_scale, b.hid, H));
+  for (int li = 0; li < s.n_layers; ++li) {
+    const LayerArgs &L = layers[li];
+    if (li == 0)
+      PF_CHECK(hipLaunchKernelGGL(k_pf_norm<false>, dim3(n), dim3(256), 0, st, nullptr, b.hid, nullptr, L.g_in,
+                                  nullptr, b.xn, H, a.eps));
+    PF_TRY(gemm(b.xn, L.wq, b.q, QD, H));
+    PF_TRY(gemm(b.xn, L.wk, b.k, KVD, H));
+    PF_TRY(gemm(b.xn, L.wv, b.v, KVD, H));
+    const int items = n * (nq + nkv);
+    const int cs_off = L.global ? D : 0;
+    if (D == 256)
+      PF_CHECK(hipLaunchKernelGGL(k_pf_qk_rope<256>, dim3((items + 3) / 4), dim3(256), 0, st, b.q, b.k, b.v, L.g_q,
+                                  L.g_k, b.cs, cs_off, L.kc, L.vc, p0, n, nq, nkv, a.eps));
+    else
+      PF_CHECK(hipLaunchKernelGGL(k_pf_qk_rope<128>, dim3((items + 3) / 4), dim3(256), 0, st, b.q, b.k, b.v, L.g_q,
+                                  L.g_k, b.cs, cs_off, L.kc, L.vc, p0, n, nq, nkv, a.eps));
+    PfAttnArgs pa;
+    pa.p0 = p0;
+    pa.n = n;
+    pa.n_kv_heads = nkv;
+    pa.lo_fixed = L.global ? 0 : lo_fixed;
+    pa.window = L.global ? 0 : window;
+    pa.scale = a.attn_scale;
+    const dim3 agrid((n * G + 63) / 64, nkv);
+    if (D == 256) PF_TRY(launch_pf_attn<256>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa));
+    else PF_TRY(launch_pf_attn<128>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa));
+    PF_TRY(gemm(b.attn, L.wo, b.o, H, QD));
+    PF_CHECK(hipLaunchKernelGGL(k_pf_norm<true>, dim3(n), dim3(256), 0, st, b.hid, b.o, L.g_post_attn, L.g_pre_ffn,
+                                b.x2, b.xn, H, a.eps));
+    PF_TRY(gemm(b.xn, L.wgate, b.g, F, H));
+    PF_TRY(gemm(b.xn, L.wup, b.u, F, H));
+    const size_t n4 = (size_t)n * F / 4;
+    const unsigned eg = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
+    PF_CHECK(hipLaunchKernelGGL(k_pf_gelu_mul, dim3(eg), dim3(256), 0, st, b.g, b.u, b.g, n4));
+    PF_TRY(gemm(b.g, L.wdown, b.dn, H, F));
+    if (li + 1 < s.n_layers)
+      PF_CHECK(hipLaunchKernelGGL(k_pf_norm<true>, dim3(n), dim3(256), 0, st, b.x2, b.dn, L.g_post_ffn,
+                                  layers[li + 1].g_in, b.hid, b.xn, H, a.eps));
+  }
+  if (logits) {
+    // the last row's final residual, final norm and lm_head (transformer4.rs:2131-2139)
+    PF_TRY(hipMemcpyAsync(a.x2, b.x2 + (size_t)(n - 1) * H, (size_t)H * 4, hipMemcpyDeviceToDevice, st));
+    PF_TRY(hipMemcpyAsync(a.dn, b.dn + (size_t)(n - 1) * H, (size_t)H * 4, hipMemcpyDeviceToDevice, st));
+    PF_TRY(enqueue_lm_head(s, a, layers[s.n_layers - 1], st));
+  }
+#undef PF_CHECK
+#undef PF_TRY
+  return hipSuccess;
+}
+
+}  // namespace rt

@@ -1,0 +1,283 @@
+"""Prefill: the oracle's restatement of the reference prefill (forward_cached
+over the whole prompt, transformer4.rs:1900-1964 and 2103-2139; attention
+2882-2940 / 2661-2700) pinned on the CPU, then the GPU prefill
+(rt_decode_prefill) against it."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import rel_l2
+from test_oracle import make_model
+
+LOGITS_TOL = 1e-3  # rel-L2 of logits vs the oracle's f32 CPU order
+# KV rows are intermediate values of later layers.  The prefill projections
+# run on the f16-operand GEMM (about 3e-4 rel-L2 per projection against f32),
+# and a row whose k projection nearly cancels (sum|w x| / |sum w x| of 15-1000
+# on single rows of these random-weight models) amplifies its input's error:
+# one such row puts a layer at ~3e-3 while the logits stay near 3e-5.
+KV_TOL = 5e-3
+
+
+def tiny(group: int = 2, **kw):
+    base = dict(hidden=512, ffn=1024, n_q_heads=2, n_kv_heads=1, head_dim=256, n_layers=3, vocab=1000,
+                sliding_window=8, global_every=3, rope_theta_local=10000.0, rope_theta_global=1000000.0,
+                rope_fs_local=1.0, rope_fs_global=0.125, eps=1e-6, attn_scale=1.0 / 16.0)
+    if group == 4:
+        base.update(n_q_heads=4, n_kv_heads=1, head_dim=128, attn_scale=1.0 / np.sqrt(128.0))
+    elif group == 1:
+        base.update(n_q_heads=2, n_kv_heads=2, head_dim=256)
+    base.update(kw)
+    return base
+
+
+def fresh_caches(layers, rows=None):
+    """Copies of the model with zeroed caches (a prefill fills them itself)."""
+    out = []
+    for L in layers:
+        M = dict(L)
+        M["k_cache"] = np.zeros_like(L["k_cache"])
+        M["v_cache"] = np.zeros_like(L["v_cache"])
+        out.append(M)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# oracle pins (CPU)
+# ---------------------------------------------------------------------------
+def np_attention_reference(q, kc, vc, T, k_start, nq, nkv, d, scale):
+    """float64 brute force of gqa_attention_cached's prefill branch written
+    from its own conditions (transformer4.rs:2909-2937): query row r attends
+    window index c (key k_start + c) iff r >= k_start and c <= r - k_start."""
+    out = np.zeros((T, nq * d))
+    t_kv = T - k_start
+    for qh in range(nq):
+        kvh = qh // (nq // nkv)
+        K = kc[k_start:T, kvh * d:(kvh + 1) * d].astype(np.float64)
+        V = vc[k_start:T, kvh * d:(kvh + 1) * d].astype(np.float64)
+        S = q[:, qh * d:(qh + 1) * d].astype(np.float64) @ K.T * scale
+        for r in range(T):
+            if r < k_start:
+                continue
+            max_kv = min(r - k_start, t_kv - 1)
+            e = np.exp(S[r, :max_kv + 1] - S[r, :max_kv + 1].max())
+            out[r, qh * d:(qh + 1) * d] = (e / e.sum()) @ V[:max_kv + 1]
+    return out
+
+
+def np_attention_windowed(q, k, v, T, window, nq, nkv, d, scale):
+    """float64 brute force of gqa_attention_windowed's mask (transformer4.rs:
+    2686-2695): causal_ok = c <= r, window_ok = r < window || c >= r + 1 - window."""
+    out = np.zeros((T, nq * d))
+    for qh in range(nq):
+        kvh = qh // (nq // nkv)
+        S = q[:, qh * d:(qh + 1) * d].astype(np.float64) @ k[:T, kvh * d:(kvh + 1) * d].astype(np.float64).T * scale
+        for r in range(T):
+            ok = np.array([c <= r and (r < window or c >= r + 1 - window) for c in range(T)])
+            s = np.where(ok, S[r], -np.inf)
+            e = np.exp(s - s.max())
+            out[r, qh * d:(qh + 1) * d] = (e / e.sum()) @ v[:T, kvh * d:(kvh + 1) * d].astype(np.float64)
+    return out
+
+
+@pytest.mark.parametrize("nq,nkv", [(2, 1), (4, 2), (2, 2)])
+@pytest.mark.parametrize("T,window", [(20, 8), (7, 8), (33, 1)])
+def test_oracle_prefill_attention_vs_bruteforce(orc, nq, nkv, T, window):
+    rng = np.random.default_rng(T * 10 + nq + nkv)
+    d = 16
+    q = rng.standard_normal((T, nq * d)).astype(np.float32)
+    kc = rng.standard_normal((T, nkv * d)).astype(np.float32)
+    vc = rng.standard_normal((T, nkv * d)).astype(np.float32)
+    scale = 0.25
+    k_start = max(0, T - window)
+    got = orc.gqa_attention_prefill(q, kc, vc, 0, T, k_start, 0, nq, nkv, d, scale)
+    ref = np_attention_reference(q, kc, vc, T, k_start, nq, nkv, d, scale)
+    assert np.abs(got - ref).max() < 1e-5
+    if k_start > 0:  # rows before the window start attend to nothing
+        assert not np.any(got[:k_start])
+    got = orc.gqa_attention_prefill(q, kc, vc, 0, T, 0, window, nq, nkv, d, scale)
+    ref = np_attention_windowed(q, kc, vc, T, window, nq, nkv, d, scale)
+    assert np.abs(got - ref).max() < 1e-5
+
+
+def test_oracle_prefill_attention_offset_rows(orc):
+    """Rows at p0 > 0 see the cache rows before the chunk: the last rows of a
+    full-prompt attention equal a chunk's rows at the same positions."""
+    rng = np.random.default_rng(5)
+    T, p0, d, nq, nkv = 30, 12, 16, 4, 2
+    q = rng.standard_normal((T, nq * d)).astype(np.float32)
+    kc = rng.standard_normal((T, nkv * d)).astype(np.float32)
+    vc = rng.standard_normal((T, nkv * d)).astype(np.float32)
+    for lo_fixed, window in [(0, 0), (0, 7), (10, 0)]:
+        full = orc.gqa_attention_prefill(q, kc, vc, 0, T, lo_fixed, window, nq, nkv, d, 0.3)
+        part = orc.gqa_attention_prefill(q[p0:], kc, vc, p0, T - p0, lo_fixed, window, nq, nkv, d, 0.3)
+        assert np.array_equal(full[p0:], part)
+
+
+@pytest.mark.parametrize("group", [2, 4])
+def test_oracle_sliding_prefill_equals_decode_steps(orc, group):
+    """Per-row sliding window: a prefill of T tokens is T decode steps (the
+    decode-step oracle, pinned separately, restates the t_q == 1 branch)."""
+    cfg = tiny(group)
+    T, max_seq = 14, 16
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=0, seed=4100 + group)
+    toks = [(7 * i + 3) % cfg["vocab"] for i in range(T)]
+    a = fresh_caches(layers)
+    got = orc.gemma3_prefill(cfg, a, embed, fnorm, toks, 0, mode=1)
+    b = fresh_caches(layers)
+    for i, t in enumerate(toks):
+        ref = orc.gemma3_decode_step(cfg, b, embed, fnorm, token=t, pos=i)
+    assert rel_l2(got, ref) < 2e-5
+    for La, Lb in zip(a, b):
+        assert rel_l2(La["k_cache"][:T], Lb["k_cache"][:T]) < 2e-5
+        assert rel_l2(La["v_cache"][:T], Lb["v_cache"][:T]) < 2e-5
+
+
+def test_oracle_reference_prefill_short_prompt_equals_sliding(orc):
+    """With T <= window both window rules select the same keys."""
+    cfg = tiny(2)
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=8, ctx=0, seed=4200)
+    toks = [1, 2, 3, 4, 5, 6, 7, 8]
+    a, b = fresh_caches(layers), fresh_caches(layers)
+    la = orc.gemma3_prefill(cfg, a, embed, fnorm, toks, 0, mode=0)
+    lb = orc.gemma3_prefill(cfg, b, embed, fnorm, toks, 0, mode=1)
+    assert np.array_equal(la, lb)
+
+
+def test_oracle_reference_prefill_long_prompt_differs(orc):
+    """T > window: the reference rule zeroes the attention of early rows, so
+    the result differs from the sliding rule (a dropped lo_fixed would not)."""
+    cfg = tiny(2)
+    T = 14
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=T, ctx=0, seed=4300)
+    toks = list(range(3, 3 + T))
+    a, b = fresh_caches(layers), fresh_caches(layers)
+    la = orc.gemma3_prefill(cfg, a, embed, fnorm, toks, 0, mode=0)
+    lb = orc.gemma3_prefill(cfg, b, embed, fnorm, toks, 0, mode=1)
+    assert rel_l2(la, lb) > 1e-6
+    # layer 0's K/V rows come before any attention, so they agree; layer 1's
+    # rows before the window start see a residual stream without attention
+    assert np.array_equal(a[0]["k_cache"], b[0]["k_cache"])
+    early = T - cfg["sliding_window"]
+    assert rel_l2(a[1]["k_cache"][:early], b[1]["k_cache"][:early]) > 1e-2
+
+
+# ---------------------------------------------------------------------------
+# GPU prefill vs the oracle
+# ---------------------------------------------------------------------------
+def gpu_ctx(rt, cfg, layers, embed, fnorm, max_seq):
+    d = rt.HipDecodeContext(cfg, max_seq)
+    for i, L in enumerate(layers):
+        d.set_layer(i, L)
+    d.set_embed(embed, fnorm)
+    return d
+
+
+def read_kv(d, cfg, layer, rows):
+    from test_gpu_decode import d2h
+    kvd = cfg["n_kv_heads"] * cfg["head_dim"]
+    kp, vp = d.kv_ptrs(layer)
+    return d2h(kp, rows * kvd).reshape(rows, kvd), d2h(vp, rows * kvd).reshape(rows, kvd)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("group", [2, 4, 1])
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("T", [1, 5, 20, 77])
+def test_gpu_prefill_matches_oracle(rt, orc, group, mode, T):
+    """T = 1 and 5 (inside the window of 8), 20 and 77 (window passed: the
+    reference rule zeroes early rows' attention; 77 rows span several 64-column
+    attention workgroups and 32-key stages)."""
+    cfg = tiny(group)
+    max_seq = 96
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=0, seed=5000 + 10 * group + T)
+    toks = [(13 * i + 5) % cfg["vocab"] for i in range(T)]
+    d = gpu_ctx(rt, cfg, layers, embed, fnorm, max_seq)
+    got = d.prefill(toks, 0, mode)
+    ref_layers = fresh_caches(layers)
+    ref = orc.gemma3_prefill(cfg, ref_layers, embed, fnorm, toks, 0, mode)
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, ref) < LOGITS_TOL, rel_l2(got, ref)
+    for li in range(cfg["n_layers"]):
+        k, v = read_kv(d, cfg, li, T)
+        assert rel_l2(k, ref_layers[li]["k_cache"][:T]) < KV_TOL
+        assert rel_l2(v, ref_layers[li]["v_cache"][:T]) < KV_TOL
+    d.close()
+
+
+@pytest.mark.gpu
+def test_gpu_prefill_chunks_and_continuation(rt, orc):
+    """Chunked prefill (7 rows per chunk) and a prefill continued at
+    start_position > 0 give the single-call result (sliding rule), and the
+    next decode step sees the prefilled cache."""
+    cfg = tiny(2)
+    T, max_seq = 30, 40
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=0, seed=6100)
+    toks = [(11 * i + 2) % cfg["vocab"] for i in range(T)]
+    d1 = gpu_ctx(rt, cfg, layers, embed, fnorm, max_seq)
+    full = d1.prefill(toks, 0, 1)
+    d2 = gpu_ctx(rt, cfg, layers, embed, fnorm, max_seq)
+    d2.set_prefill_chunk(7)
+    chunked = d2.prefill(toks, 0, 1)
+    d3 = gpu_ctx(rt, cfg, layers, embed, fnorm, max_seq)
+    d3.prefill(toks[:17], 0, 1)
+    cont = d3.prefill(toks[17:], 17, 1)
+    assert rel_l2(chunked, full) < 1e-5
+    assert rel_l2(cont, full) < 1e-5
+    for li in range(cfg["n_layers"]):
+        k1, v1 = read_kv(d1, cfg, li, T)
+        k3, v3 = read_kv(d3, cfg, li, T)
+        assert rel_l2(k3, k1) < 1e-5 and rel_l2(v3, v1) < 1e-5
+    ref_layers = fresh_caches(layers)
+    orc.gemma3_prefill(cfg, ref_layers, embed, fnorm, toks, 0, 1)
+    nxt = d1.decode_step(9, T)
+    ref = orc.gemma3_decode_step(cfg, ref_layers, embed, fnorm, token=9, pos=T)
+    assert rel_l2(nxt, ref) < LOGITS_TOL
+    for d in (d1, d2, d3):
+        d.close()
+
+
+@pytest.mark.gpu
+def test_gpu_prefill_rejects_bad_calls(rt, orc):
+    cfg = tiny(2)
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=16, ctx=0, seed=6200)
+    d = gpu_ctx(rt, cfg, layers, embed, fnorm, 16)
+    with pytest.raises(rt.RtError):
+        d.prefill([], 0, 0)
+    with pytest.raises(rt.RtError):
+        d.prefill([1, 2], 3, 0)  # the reference rule starts at position 0
+    with pytest.raises(rt.RtError):
+        d.prefill([1] * 10, 10, 1)  # past max_seq
+    with pytest.raises(rt.RtError):
+        d.prefill([1, cfg["vocab"]], 0, 1)  # token out of range
+    with pytest.raises(rt.RtError):
+        d.prefill([1, 2], 0, 2)  # unknown mode
+    with pytest.raises(rt.RtError):
+        d.set_prefill_chunk(0)
+    d.close()
+
+
+@pytest.mark.gpu
+def test_gemma3_4b_shape_prefill_equals_decode_steps(rt, orc):
+    """Gemma-3-4B layer shapes (2 layers, one local one global, vocab 4096):
+    a 300-token sliding-rule prefill on the matrix cores equals 300 GPU decode
+    steps (GEMV path, pinned to the oracle elsewhere) in logits and KV rows."""
+    cfg = dict(rt.GEMMA3_4B, n_layers=2, global_every=2, vocab=4096)
+    T, max_seq = 300, 320
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=0, seed=6300)
+    toks = [(97 * i + 1) % cfg["vocab"] for i in range(T)]
+    d1 = gpu_ctx(rt, cfg, layers, embed, fnorm, max_seq)
+    got = d1.prefill(toks, 0, 1)
+    d2 = gpu_ctx(rt, cfg, layers, embed, fnorm, max_seq)
+    for i, t in enumerate(toks):
+        d2.decode_step_async(t, i)
+    d2.synchronize()
+    from test_gpu_decode import d2h
+    ref = d2h(d2.logits_ptr(), cfg["vocab"])
+    assert rel_l2(got, ref) < LOGITS_TOL, rel_l2(got, ref)
+    for li in range(2):
+        k1, v1 = read_kv(d1, cfg, li, T)
+        k2, v2 = read_kv(d2, cfg, li, T)
+        assert rel_l2(k1, k2) < KV_TOL and rel_l2(v1, v2) < KV_TOL
+    d1.close()
+    d2.close()
