@@ -64,6 +64,24 @@ def load_pkg():
     return mod
 
 
+def prefill_flops(T: int, mode: int, window: int = 1024, global_every: int = 6, nq: int = 8, d: int = 256):
+    """Algorithmic flops of a T-token prefill: the 7 projections of every layer
+    (2*T*N*K each) and attention (2 flops per q.k product term and per p*v
+    term: 4*d*nq per visible key).  mode 0 (the reference's prefill window):
+    local rows r >= T - window see r - (T - window) + 1 keys, earlier rows none;
+    mode 1: min(r + 1, window) keys."""
+    gemm = 2 * T * L * sum(n * k for _, n, k in Q4K_SHAPES)
+    glob_keys = T * (T + 1) // 2
+    if mode == 0:
+        w = min(window, T)
+        loc_keys = w * (w + 1) // 2
+    else:
+        loc_keys = sum(min(r + 1, window) for r in range(T))
+    n_glob = sum(1 for i in range(L) if i % global_every == global_every - 1)
+    attn = 4 * d * nq * (n_glob * glob_keys + (L - n_glob) * loc_keys)
+    return gemm, attn
+
+
 def q4k_bytes(n: int, k: int) -> int:
     return n * (k // 256) * 144
 
@@ -272,6 +290,23 @@ def main() -> int:
         decode["batch_verify"] = {"m": bm, "ms_per_call": round(dtb * 1e3, 4), "tok_per_s": round(bm / dtb, 1),
                                   "note": "layers run per token, lm_head batched over the 8 tokens"}
         log(f"decode_step_batch M={bm}: {dtb * 1e3:.3f} ms per call -> {bm / dtb:.1f} tok/s")
+        # GPU prefill of a config-3-length prompt (4096 tokens) on the same weights
+        toks = [(7 * i + 3) % V for i in range(ctx)]
+        pf = {"tokens": ctx}
+        for mode, name in ((0, "reference_window"), (1, "sliding_window")):
+            d.prefill(toks, 0, mode)  # first call allocates the chunk scratch
+            reps_p = 3
+            t_start = time.perf_counter()
+            for _ in range(reps_p):
+                d.prefill(toks, 0, mode)
+            dtp = (time.perf_counter() - t_start) / reps_p
+            gf, af = prefill_flops(ctx, mode)
+            pf[name] = {"ms": round(dtp * 1e3, 2), "tok_per_s": round(ctx / dtp, 1),
+                        "gemm_TFLOP": round(gf / 1e12, 2), "attn_TFLOP": round(af / 1e12, 3),
+                        "TFLOPs": round((gf + af) / dtp / 1e12, 1)}
+            log(f"prefill {ctx} tokens ({name}): {dtp * 1e3:.1f} ms -> {ctx / dtp:.0f} tok/s, "
+                f"{(gf + af) / dtp / 1e12:.0f} TFLOP/s")
+        decode["prefill"] = pf
         d.close()
 
     # ---------------- configs 2 and 4: Q4_K GEMM on the matrix cores ------------
