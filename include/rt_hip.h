@@ -92,6 +92,29 @@ rt_status rt_q4k_gemm_bf16(const uint16_t *a_dev, const void *w_dev, float *c_de
                            void *stream);
 rt_status rt_q4k_gemm_f32(const float *a_dev, const void *w_dev, float *c_dev, int64_t m, int64_t n, int64_t k,
                           void *stream);
+/* ---------------------------------------------------------------------------
+ * Q6_K and Q8_0 weights kept packed on the device.  No counterpart in the
+ * reference, which widens both to f32 and then BF16 at load
+ * (load_linear_from_gguf, transformer4.rs:1233-1242; decode_q6k_to_f32,
+ * gguf_loader.rs:482-549; decode_q8_0_to_f32, 628-650) and runs its BF16
+ * GEMV on them.  The device layout is planar (each block field in its own
+ * plane, so every load is aligned), the same size as the GGUF tensor:
+ *   Q6_K (n_blocks 256-element blocks): ql [n][128] | qh [n][64] |
+ *        int8 scales [n][16] | f16 d [n]
+ *   Q8_0 (n_blocks 32-element blocks):  int8 q [n][32] | f16 d [n]
+ * Matrices are row-major [rows][k] in block order, as in the file.
+ * ------------------------------------------------------------------------- */
+/* GGUF block bytes (host) -> planar layout (host); n_blocks*210 / *34 bytes. */
+rt_status rt_q6k_repack(const void *gguf_blocks, size_t n_blocks, void *dst);
+rt_status rt_q8_0_repack(const void *gguf_blocks, size_t n_blocks, void *dst);
+/* Device dequantisation, bit-exact with decode_q6k_to_f32 / decode_q8_0_to_f32. */
+rt_status rt_q6k_dequant_f32(const void *w, size_t n_blocks, float *out, void *stream);
+rt_status rt_q8_0_dequant_f32(const void *w, size_t n_elem, float *out, void *stream);
+/* y[n] = W[n,k] . x[k] on planar Q6_K (k % 256 == 0) / Q8_0 (k % 32 == 0)
+ * weights; device pointers, w and x 16-byte aligned. */
+rt_status rt_q6k_gemv(const void *w, const float *x, float *y, int64_t n, int64_t k, void *stream);
+rt_status rt_q8_0_gemv(const void *w, const float *x, float *y, int64_t n, int64_t k, void *stream);
+
 /* Host drop-in for Q4KMat::matmul_q4k_t_exact (autograd2.rs:1490-1625):
  * a is [m, k] f32, out receives [m, rows] f32.  m == 1 takes the GEMV path, as
  * matmul_q4k_t does (autograd2.rs:1440-1443).  Weights are cached like

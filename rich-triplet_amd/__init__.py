@@ -50,6 +50,12 @@ _SIGNATURES = {
     "rt_gemv_q4k_t": (_i32, [_vp, _sz, _vp, _sz, _vp]),
     "rt_gemv_bf16_t": (_i32, [_vp, _sz, _vp, _sz, _vp]),
     "rt_weight_cache_clear": (_i32, []),
+    "rt_q6k_repack": (_i32, [_vp, _sz, _vp]),
+    "rt_q8_0_repack": (_i32, [_vp, _sz, _vp]),
+    "rt_q6k_dequant_f32": (_i32, [_vp, _sz, _vp, _vp]),
+    "rt_q8_0_dequant_f32": (_i32, [_vp, _sz, _vp, _vp]),
+    "rt_q6k_gemv": (_i32, [_vp, _vp, _vp, _i64, _i64, _vp]),
+    "rt_q8_0_gemv": (_i32, [_vp, _vp, _vp, _i64, _i64, _vp]),
     "rt_q4k_gemm_bf16": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "rt_q4k_gemm_f32": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "rt_matmul_q4k_t": (_i32, [_vp, _sz, _sz, _vp, _sz, _vp]),
@@ -153,6 +159,46 @@ def q4k_gemv(w, x, y, n: int, k: int, stream=None) -> None:
 
 def bf16_gemv(w, x, y, n: int, k: int, stream=None) -> None:
     check(lib().rt_bf16_gemv(_p(w), _p(x), _p(y), n, k, _stream(stream)))
+
+
+def q6k_gemv(w, x, y, n: int, k: int, stream=None) -> None:
+    """y = W x on planar Q6_K weights (q6k_repack)."""
+    check(lib().rt_q6k_gemv(_p(w), _p(x), _p(y), n, k, _stream(stream)))
+
+
+def q8_0_gemv(w, x, y, n: int, k: int, stream=None) -> None:
+    """y = W x on planar Q8_0 weights (q8_0_repack)."""
+    check(lib().rt_q8_0_gemv(_p(w), _p(x), _p(y), n, k, _stream(stream)))
+
+
+def q6k_dequant_f32(w, out, n_blocks: int, stream=None) -> None:
+    check(lib().rt_q6k_dequant_f32(_p(w), n_blocks, _p(out), _stream(stream)))
+
+
+def q8_0_dequant_f32(w, out, n_elem: int, stream=None) -> None:
+    check(lib().rt_q8_0_dequant_f32(_p(w), n_elem, _p(out), _stream(stream)))
+
+
+def q6k_repack(gguf_bytes):
+    """GGUF Q6_K block bytes (numpy uint8) -> the planar device layout (numpy)."""
+    import numpy as np
+    src = np.ascontiguousarray(gguf_bytes, np.uint8)
+    if src.size % 210:
+        raise RtError(RT_EINVAL, f"Q6_K data of {src.size} bytes is not whole 210-byte blocks")
+    out = np.empty_like(src)
+    check(lib().rt_q6k_repack(src.ctypes.data, src.size // 210, out.ctypes.data))
+    return out
+
+
+def q8_0_repack(gguf_bytes):
+    """GGUF Q8_0 block bytes (numpy uint8) -> the planar device layout (numpy)."""
+    import numpy as np
+    src = np.ascontiguousarray(gguf_bytes, np.uint8)
+    if src.size % 34:
+        raise RtError(RT_EINVAL, f"Q8_0 data of {src.size} bytes is not whole 34-byte blocks")
+    out = np.empty_like(src)
+    check(lib().rt_q8_0_repack(src.ctypes.data, src.size // 34, out.ctypes.data))
+    return out
 
 
 def q4k_gemm(a, w, c, m: int, n: int, k: int, stream=None) -> None:

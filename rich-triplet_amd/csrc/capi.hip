@@ -85,6 +85,47 @@ rt_status rt_bf16_gemv(const uint16_t *w, const float *x, float *y, int64_t n, i
   return hip_error(launch_bf16_gemv(w, x, y, (int)n, (int)k, (hipStream_t)stream), "rt_bf16_gemv");
 }
 
+rt_status rt_q6k_repack(const void *gguf_blocks, size_t n_blocks, void *dst) {
+  if (n_blocks == 0) return RT_OK;
+  if (!gguf_blocks || !dst) return set_error(RT_EINVAL, "rt_q6k_repack: null pointer");
+  q6k_repack_host(static_cast<const uint8_t *>(gguf_blocks), n_blocks, static_cast<uint8_t *>(dst));
+  return RT_OK;
+}
+
+rt_status rt_q8_0_repack(const void *gguf_blocks, size_t n_blocks, void *dst) {
+  if (n_blocks == 0) return RT_OK;
+  if (!gguf_blocks || !dst) return set_error(RT_EINVAL, "rt_q8_0_repack: null pointer");
+  q8_0_repack_host(static_cast<const uint8_t *>(gguf_blocks), n_blocks, static_cast<uint8_t *>(dst));
+  return RT_OK;
+}
+
+rt_status rt_q6k_dequant_f32(const void *w, size_t n_blocks, float *out, void *stream) {
+  if (n_blocks == 0) return RT_OK;
+  if (!w || !out) return set_error(RT_EINVAL, "rt_q6k_dequant_f32: null pointer");
+  if (!aligned16(w)) return set_error(RT_EINVAL, "rt_q6k_dequant_f32: w must be 16-byte aligned");
+  return hip_error(launch_q6k_dequant(w, n_blocks, out, (hipStream_t)stream), "rt_q6k_dequant_f32");
+}
+
+rt_status rt_q8_0_dequant_f32(const void *w, size_t n_elem, float *out, void *stream) {
+  if (n_elem == 0) return RT_OK;
+  if (!w || !out) return set_error(RT_EINVAL, "rt_q8_0_dequant_f32: null pointer");
+  if (n_elem % 32 != 0) return set_error(RT_EINVAL, "rt_q8_0_dequant_f32: n_elem=%zu must be a multiple of 32", n_elem);
+  if (!aligned16(w)) return set_error(RT_EINVAL, "rt_q8_0_dequant_f32: w must be 16-byte aligned");
+  return hip_error(launch_q8_0_dequant(w, n_elem, out, (hipStream_t)stream), "rt_q8_0_dequant_f32");
+}
+
+rt_status rt_q6k_gemv(const void *w, const float *x, float *y, int64_t n, int64_t k, void *stream) {
+  rt_status st = check_gemv_shape("rt_q6k_gemv", w, x, y, n, k, 256);
+  if (st != RT_OK) return st;
+  return hip_error(launch_q6k_gemv(w, x, y, (int)n, (int)k, (hipStream_t)stream), "rt_q6k_gemv");
+}
+
+rt_status rt_q8_0_gemv(const void *w, const float *x, float *y, int64_t n, int64_t k, void *stream) {
+  rt_status st = check_gemv_shape("rt_q8_0_gemv", w, x, y, n, k, 32);
+  if (st != RT_OK) return st;
+  return hip_error(launch_q8_0_gemv(w, x, y, (int)n, (int)k, (hipStream_t)stream), "rt_q8_0_gemv");
+}
+
 }  // extern "C"
 
 namespace {

@@ -1,0 +1,364 @@
+// kquant.hip -- Q6_K and Q8_0 weights kept packed in HBM: repacking, exact
+// dequantisation and the decode GEMV y = W x.
+//
+// The reference widens both types to f32 and then BF16 at load
+// (load_linear_from_gguf, transformer4.rs:1233-1242, via decode_q6k_to_f32
+// gguf_loader.rs:482-549 and decode_q8_0_to_f32 628-650), so its GPU GEMV
+// streams 16 bits per weight.  Here Q6_K stays at 6.5625 bits and Q8_0 at
+// 8.5: 2.4x and 1.9x fewer bytes for the same matrix.
+//
+// Device layout (planar, filled by rt_q6k_repack / rt_q8_0_repack from the
+// GGUF blocks).  GGUF interleaves fields inside 210-byte (Q6_K) and 34-byte
+// (Q8_0) blocks, which leaves most fields 2-byte aligned; each field gets its
+// own plane so every lane load is an aligned 16-byte load:
+//   Q6_K [N][K], nb = K/256 blocks per row, nbt = N*nb:
+//     QL [nbt][128] low nibbles | QH [nbt][64] high bit pairs |
+//     SC [nbt][16] int8 sub-block scales | D [nbt] f16 block scales
+//   Q8_0 [N][K], nb = K/32:
+//     QS [N][K] int8 | D [N*nb] f16
+// Both are exactly as many bytes as the GGUF tensor.
+//
+// GEMV arithmetic: the activation vector is staged once per workgroup as
+// 16-bit integer digits per 64-element chunk (stage_digits_store:
+// X = rint(x * 2^sh) = 256*x1 + x0), and the weight codes multiply the digits
+// in exact integer dot products:
+//   Q6_K  q = ql | qh << 4 in 0..63, w = d * sc * (q - 32):
+//         per 16-element sub-block  T = sum X q - 32 sum X  (|T| < 2^24, exact)
+//   Q8_0  q in -128..127, w = d * q:  with q' = q ^ 0x80 = q + 128 (unsigned),
+//         sum x0 q = sum x0 q' - 128 sum x0, so both digits use v_dot4 forms
+//         with matching signedness.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+
+#include "q4k_gemv.hpp"
+#include "rt_device.hpp"
+#include "rt_kernels.hpp"
+
+namespace rt {
+namespace {
+
+constexpr int kQ6KBlockBytes = 210;
+constexpr int kQ8Block = 32, kQ8BlockBytes = 34;
+
+struct Q6KPlanes {
+  const uint8_t *ql, *qh;
+  const uint8_t *sc;
+  const uint16_t *d;
+};
+
+__host__ __device__ inline Q6KPlanes q6k_planes(const void *w, size_t nbt) {
+  const uint8_t *p = static_cast<const uint8_t *>(w);
+  return {p, p + nbt * 128, p + nbt * 192, reinterpret_cast<const uint16_t *>(p + nbt * 208)};
+}
+
+// ---------------------------------------------------------------------------
+// Dequantisation (bit-exact with decode_q6k_to_f32 / decode_q8_0_to_f32:
+// s = d * sc in f32, then s * q)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_q6k_dequant(const uint8_t *__restrict__ w, size_t nbt,
+                                                     float *__restrict__ out) {
+#pragma clang fp contract(off)
+  const Q6KPlanes P = q6k_planes(w, nbt);
+  const size_t total = nbt * 256;
+  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (size_t)gridDim.x * 256) {
+    const size_t blk = e >> 8;
+    const int i = (int)(e & 255), j = i >> 7, h = i & 127, m = h >> 5, l = h & 31;
+    const uint8_t ql = P.ql[blk * 128 + 64 * j + 32 * (m & 1) + l];
+    const uint8_t qh = P.qh[blk * 64 + 32 * j + l];
+    const int q = (int)(((m < 2 ? ql & 15 : ql >> 4)) | (((qh >> (2 * m)) & 3) << 4)) - 32;
+    const float d = half_bits_to_f32(P.d[blk]);
+    const float s = d * (float)(int8_t)P.sc[blk * 16 + 8 * j + (l >> 4) + 2 * m];
+    out[e] = s * (float)q;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_q8_0_dequant(const uint8_t *__restrict__ w, size_t n_elem,
+                                                      float *__restrict__ out) {
+#pragma clang fp contract(off)
+  const uint16_t *D = reinterpret_cast<const uint16_t *>(w + n_elem);
+  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n_elem; e += (size_t)gridDim.x * 256)
+    out[e] = half_bits_to_f32(D[e / kQ8Block]) * (float)(int8_t)w[e];
+}
+
+// ---------------------------------------------------------------------------
+// Q6_K GEMV.  Slot s = threadIdx % S (S = 4*NB) of a row: block b = s/4, half
+// j = (s/2)%2, a = s%2.  The slot owns l in [16a, 16a+16) of its half, i.e.
+// the four 16-element sub-blocks 2m + a (m = 0..3) at elements
+// 128j + 32m + 16a + [0, 16): ql[16a..] (m = 0, 2: low / high nibbles),
+// ql[32+16a..] (m = 1, 3) and qh[16a..] (bit pair m), three 16-byte loads.
+// A workgroup of T threads covers RPI = T/S rows per iteration.
+// ---------------------------------------------------------------------------
+template <int NB, int T, int ITERS>
+__global__ __launch_bounds__(T) void k_q6k_gemv(const uint8_t *__restrict__ W, const float *__restrict__ x,
+                                                float *__restrict__ y, int n) {
+  constexpr int K = NB * 256, S = 4 * NB, RPI = T / S, ROWS = RPI * ITERS;
+  static_assert(T % S == 0 && T % 64 == 0, "a tile covers whole rows and whole waves");
+  __shared__ __attribute__((aligned(16))) uint32_t dl[K / 64 * kDPitch];
+  __shared__ float red[ROWS * NB];
+  const Q6KPlanes P = q6k_planes(W, (size_t)n * NB);
+  const int s = (int)threadIdx.x % S, rsub = (int)threadIdx.x / S;
+  const int b = s >> 2, j = (s >> 1) & 1, a = s & 1;
+  const int row0 = (int)blockIdx.x * ROWS;
+
+  XRegs<K, T> xr;
+  x_load<K, T>(x, xr);
+  uint4 qa[ITERS], qb[ITERS], qh[ITERS];
+  uint2 sc[ITERS];
+  uint32_t dd[ITERS];
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const size_t blk = (size_t)min(row0 + it * RPI + rsub, n - 1) * NB + b;  // rows past n: masked below
+    qa[it] = *reinterpret_cast<const uint4 *>(P.ql + blk * 128 + 64 * j + 16 * a);
+    qb[it] = *reinterpret_cast<const uint4 *>(P.ql + blk * 128 + 64 * j + 32 + 16 * a);
+    qh[it] = *reinterpret_cast<const uint4 *>(P.qh + blk * 64 + 32 * j + 16 * a);
+    sc[it] = *reinterpret_cast<const uint2 *>(P.sc + blk * 16 + 8 * j);
+    dd[it] = P.d[blk];
+  }
+  x_store_digits<K, T>(xr, dl);
+  __syncthreads();
+
+  // this slot's activation digits and 32 * sum(X) of each sub-block
+  uint32_t x0[4][4];
+  int x1[4][4], xs32[4];
+  float delta[2];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const uint32_t *p = dl + (4 * b + 2 * j + (m >> 1)) * kDPitch + 8 * (m & 1) + 4 * a;
+    const uint4 u0 = *reinterpret_cast<const uint4 *>(p), u1 = *reinterpret_cast<const uint4 *>(p + 16);
+    x0[m][0] = u0.x; x0[m][1] = u0.y; x0[m][2] = u0.z; x0[m][3] = u0.w;
+    x1[m][0] = (int)u1.x; x1[m][1] = (int)u1.y; x1[m][2] = (int)u1.z; x1[m][3] = (int)u1.w;
+    uint32_t s0 = 0;
+    int s1 = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      s0 = __builtin_amdgcn_udot4(x0[m][k], 0x01010101u, s0, false);
+      s1 = __builtin_amdgcn_sdot4(x1[m][k], 0x01010101, s1, false);
+    }
+    xs32[m] = 32 * ((int)s0 + 256 * s1);
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    delta[h] = __uint_as_float(dl[(4 * b + 2 * j + h) * kDPitch + 32]);
+
+  const uint32_t m4 = opaque_u32(0x0F0F0F0Fu), m2 = opaque_u32(0x30303030u);
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const uint32_t lo[4] = {qa[it].x, qa[it].y, qa[it].z, qa[it].w};
+    const uint32_t hi[4] = {qb[it].x, qb[it].y, qb[it].z, qb[it].w};
+    const uint32_t hb[4] = {qh[it].x, qh[it].y, qh[it].z, qh[it].w};
+    const uint32_t scw = a ? (sc[it].x >> 8) | (sc[it].y << 24) : sc[it].x;  // sc[a], sc[a+2] in bytes 0, 2
+    const uint32_t scw2 = a ? sc[it].y >> 8 : sc[it].y;                        // sc[a+4], sc[a+6]
+    float acc[2] = {0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      uint32_t s0 = 0;
+      int s1 = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t src = (m & 1) ? hi[k] : lo[k];
+        const uint32_t nib = (m < 2 ? src : src >> 4) & m4;
+        const int sh = 2 * m;  // bit pair m of qh moved to bits 4..5
+        const uint32_t q = nib | ((sh <= 4 ? hb[k] << (4 - sh) : hb[k] >> (sh - 4)) & m2);
+        s0 = __builtin_amdgcn_udot4(q, x0[m][k], s0, false);
+        s1 = __builtin_amdgcn_sdot4((int)q, x1[m][k], s1, false);
+      }
+      const int t = (int)s0 + 256 * s1 - xs32[m];  // sum X (q - 32), exact
+      const uint32_t word = m < 2 ? scw : scw2;
+      const float scf = (float)(int)__builtin_amdgcn_sbfe(word, 16 * (m & 1), 8);
+      acc[m >> 1] = fmaf(scf, (float)t, acc[m >> 1]);
+    }
+    float p = half_bits_to_f32(dd[it]) * fmaf(acc[1], delta[1], acc[0] * delta[0]);
+    p = quad_sum(p);
+    if ((s & 3) == 0) red[(it * RPI + rsub) * NB + b] = p;
+  }
+  __syncthreads();
+  for (int i = (int)threadIdx.x; i < ROWS; i += T)
+    if (row0 + i < n) y[row0 + i] = reduce_row<NB>(red, i);
+}
+
+// ---------------------------------------------------------------------------
+// Q8_0 GEMV.  Slot s = threadIdx % S (S = K/32) of a row owns one 32-element
+// block: two 16-byte loads of codes and its f16 scale.
+// ---------------------------------------------------------------------------
+template <int NB32, int T, int ITERS>
+__global__ __launch_bounds__(T) void k_q8_0_gemv(const uint8_t *__restrict__ W, const float *__restrict__ x,
+                                                 float *__restrict__ y, int n) {
+  constexpr int K = NB32 * kQ8Block, S = NB32, RPI = T / S, ROWS = RPI * ITERS;
+  constexpr int RED = (NB32 + 1) / 2;  // partials per row after the pair sum
+  static_assert(T % S == 0 && T % 64 == 0 && S % 2 == 0, "a tile covers whole rows and whole waves");
+  __shared__ __attribute__((aligned(16))) uint32_t dl[K / 64 * kDPitch];
+  __shared__ float red[ROWS * RED];
+  const uint16_t *D = reinterpret_cast<const uint16_t *>(W + (size_t)n * K);
+  const int s = (int)threadIdx.x % S, rsub = (int)threadIdx.x / S;
+  const int row0 = (int)blockIdx.x * ROWS;
+
+  XRegs<K, T> xr;
+  x_load<K, T>(x, xr);
+  uint4 qa[ITERS], qb[ITERS];
+  uint32_t dd[ITERS];
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const size_t r = (size_t)min(row0 + it * RPI + rsub, n - 1);
+    const uint8_t *p = W + r * K + 32 * s;
+    qa[it] = *reinterpret_cast<const uint4 *>(p);
+    qb[it] = *reinterpret_cast<const uint4 *>(p + 16);
+    dd[it] = D[r * NB32 + s];
+  }
+  x_store_digits<K, T>(xr, dl);
+  __syncthreads();
+
+  uint32_t x0[8];
+  int x1[8];
+  const uint32_t *px = dl + (s >> 1) * kDPitch + 8 * (s & 1);
+  uint32_t sx0 = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    x0[k] = px[k];
+    x1[k] = (int)px[16 + k];
+    sx0 = __builtin_amdgcn_udot4(x0[k], 0x01010101u, sx0, false);
+  }
+  const int corr = 128 * (int)sx0;
+  const float delta = __uint_as_float(dl[(s >> 1) * kDPitch + 32]);
+  const uint32_t flip = opaque_u32(0x80808080u);
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const uint32_t w[8] = {qa[it].x, qa[it].y, qa[it].z, qa[it].w, qb[it].x, qb[it].y, qb[it].z, qb[it].w};
+    uint32_t s0 = 0;
+    int s1 = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      s0 = __builtin_amdgcn_udot4(w[k] ^ flip, x0[k], s0, false);
+      s1 = __builtin_amdgcn_sdot4((int)w[k], x1[k], s1, false);
+    }
+    // sum X q = (sum x0 q' - 128 sum x0) + 256 sum x1 q; |.| < 2^31
+    const int t = (int)(s0 - (uint32_t)corr) + 256 * s1;
+    float p = half_bits_to_f32(dd[it]) * delta * (float)t;
+    p += dpp<0xB1>(p);  // pair of blocks = one 64-element chunk
+    if ((s & 1) == 0) red[(it * RPI + rsub) * RED + (s >> 1)] = p;
+  }
+  __syncthreads();
+  for (int i = (int)threadIdx.x; i < ROWS; i += T)
+    if (row0 + i < n) {
+      float acc = 0.f;
+#pragma unroll
+      for (int c = 0; c < RED; ++c) acc += red[i * RED + c];
+      y[row0 + i] = acc;
+    }
+}
+
+// Generic fallbacks (any K that is a whole number of blocks): one wave per
+// row, f32 arithmetic on activations read from global memory.
+__global__ __launch_bounds__(256) void k_q6k_gemv_generic(const uint8_t *__restrict__ W,
+                                                          const float *__restrict__ x, float *__restrict__ y, int n,
+                                                          int nb) {
+  const int row = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
+  if (row >= n) return;
+  const Q6KPlanes P = q6k_planes(W, (size_t)n * nb);
+  float acc = 0.f;
+  for (int e = lane; e < nb * 256; e += 64) {
+    const size_t blk = (size_t)row * nb + (e >> 8);
+    const int i = e & 255, j = i >> 7, h = i & 127, m = h >> 5, l = h & 31;
+    const uint8_t ql = P.ql[blk * 128 + 64 * j + 32 * (m & 1) + l];
+    const uint8_t qh = P.qh[blk * 64 + 32 * j + l];
+    const int q = (int)(((m < 2 ? ql & 15 : ql >> 4)) | (((qh >> (2 * m)) & 3) << 4)) - 32;
+    const float w = half_bits_to_f32(P.d[blk]) * (float)(int8_t)P.sc[blk * 16 + 8 * j + (l >> 4) + 2 * m];
+    acc = fmaf(w * (float)q, x[e], acc);
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) y[row] = acc;
+}
+
+__global__ __launch_bounds__(256) void k_q8_0_gemv_generic(const uint8_t *__restrict__ W,
+                                                           const float *__restrict__ x, float *__restrict__ y, int n,
+                                                           int k) {
+  const int row = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
+  if (row >= n) return;
+  const uint16_t *D = reinterpret_cast<const uint16_t *>(W + (size_t)n * k);
+  const int8_t *q = reinterpret_cast<const int8_t *>(W) + (size_t)row * k;
+  float acc = 0.f;
+  for (int e = lane; e < k; e += 64)
+    acc = fmaf(half_bits_to_f32(D[((size_t)row * k + e) / kQ8Block]) * (float)q[e], x[e], acc);
+  acc = wave_sum(acc);
+  if (lane == 0) y[row] = acc;
+}
+
+template <int NB, int T, int ITERS>
+hipError_t launch_q6k(const void *W, const float *x, float *y, int n, hipStream_t s) {
+  constexpr int ROWS = T / (4 * NB) * ITERS;
+  hipLaunchKernelGGL((k_q6k_gemv<NB, T, ITERS>), dim3((n + ROWS - 1) / ROWS), dim3(T), 0, s,
+                     static_cast<const uint8_t *>(W), x, y, n);
+  return hipGetLastError();
+}
+
+template <int NB32, int T, int ITERS>
+hipError_t launch_q8(const void *W, const float *x, float *y, int n, hipStream_t s) {
+  constexpr int ROWS = T / NB32 * ITERS;
+  hipLaunchKernelGGL((k_q8_0_gemv<NB32, T, ITERS>), dim3((n + ROWS - 1) / ROWS), dim3(T), 0, s,
+                     static_cast<const uint8_t *>(W), x, y, n);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+void q6k_repack_host(const uint8_t *src, size_t n_blocks, uint8_t *dst) {
+  uint8_t *ql = dst, *qh = dst + n_blocks * 128, *sc = dst + n_blocks * 192, *d = dst + n_blocks * 208;
+  for (size_t b = 0; b < n_blocks; ++b) {
+    const uint8_t *bp = src + b * kQ6KBlockBytes;
+    std::memcpy(ql + b * 128, bp, 128);
+    std::memcpy(qh + b * 64, bp + 128, 64);
+    std::memcpy(sc + b * 16, bp + 192, 16);
+    std::memcpy(d + b * 2, bp + 208, 2);
+  }
+}
+
+void q8_0_repack_host(const uint8_t *src, size_t n_blocks, uint8_t *dst) {
+  uint8_t *qs = dst, *d = dst + n_blocks * kQ8Block;
+  for (size_t b = 0; b < n_blocks; ++b) {
+    const uint8_t *bp = src + b * kQ8BlockBytes;
+    std::memcpy(d + b * 2, bp, 2);
+    std::memcpy(qs + b * kQ8Block, bp + 2, kQ8Block);
+  }
+}
+
+hipError_t launch_q6k_dequant(const void *w, size_t n_blocks, float *out, hipStream_t s) {
+  const unsigned grid = (unsigned)std::min<size_t>(n_blocks, 65536);
+  hipLaunchKernelGGL(k_q6k_dequant, dim3(grid), dim3(256), 0, s, static_cast<const uint8_t *>(w), n_blocks, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_q8_0_dequant(const void *w, size_t n_elem, float *out, hipStream_t s) {
+  const unsigned grid = (unsigned)std::min<size_t>((n_elem + 255) / 256, 65536);
+  hipLaunchKernelGGL(k_q8_0_dequant, dim3(grid), dim3(256), 0, s, static_cast<const uint8_t *>(w), n_elem, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_q6k_gemv(const void *W, const float *x, float *y, int N, int K, hipStream_t s) {
+  switch (K) {
+    case 2048: return launch_q6k<8, 256, 1>(W, x, y, N, s);
+    case 2560: return N >= 4096 ? launch_q6k<10, 320, 2>(W, x, y, N, s) : launch_q6k<10, 320, 1>(W, x, y, N, s);
+    case 10240: return launch_q6k<40, 640, 1>(W, x, y, N, s);
+    default:
+      hipLaunchKernelGGL(k_q6k_gemv_generic, dim3((N + 3) / 4), dim3(256), 0, s, static_cast<const uint8_t *>(W),
+                         x, y, N, K / 256);
+      return hipGetLastError();
+  }
+}
+
+hipError_t launch_q8_0_gemv(const void *W, const float *x, float *y, int N, int K, hipStream_t s) {
+  switch (K) {
+    case 2048: return launch_q8<64, 256, 1>(W, x, y, N, s);
+    case 2560: return N >= 4096 ? launch_q8<80, 320, 2>(W, x, y, N, s) : launch_q8<80, 320, 1>(W, x, y, N, s);
+    case 10240: return launch_q8<320, 640, 1>(W, x, y, N, s);
+    default:
+      hipLaunchKernelGGL(k_q8_0_gemv_generic, dim3((N + 3) / 4), dim3(256), 0, s, static_cast<const uint8_t *>(W),
+                         x, y, N, K);
+      return hipGetLastError();
+  }
+}
+
+}  // namespace rt

@@ -13,6 +13,13 @@ hipError_t launch_q4k_gemv(const void *W, const float *x, float *y, int N, int K
 hipError_t launch_q4k_gemv_generic(const void *W, const float *x, float *y, int N, int K, hipStream_t s);
 int q4k_gemv_rows_per_wg(int N, int K);
 hipError_t launch_bf16_gemv(const uint16_t *W, const float *x, float *y, int N, int K, hipStream_t s);
+// Q6_K / Q8_0 in the planar device layout of kquant.hip.
+void q6k_repack_host(const uint8_t *src, size_t n_blocks, uint8_t *dst);
+void q8_0_repack_host(const uint8_t *src, size_t n_blocks, uint8_t *dst);
+hipError_t launch_q6k_dequant(const void *w, size_t n_blocks, float *out, hipStream_t s);
+hipError_t launch_q8_0_dequant(const void *w, size_t n_elem, float *out, hipStream_t s);
+hipError_t launch_q6k_gemv(const void *W, const float *x, float *y, int N, int K, hipStream_t s);
+hipError_t launch_q8_0_gemv(const void *W, const float *x, float *y, int N, int K, hipStream_t s);
 // Q4_K GEMM C[M,N] = A[M,K] . W[N,K]^T; A bf16 bits (a_bf16) or f32; ws holds
 // q4k_gemm_workspace_bytes(M, N, K) bytes of device scratch.
 size_t q4k_gemm_workspace_bytes(int M, int N, int K);
