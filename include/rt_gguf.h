@@ -91,10 +91,8 @@ rt_status rt_gguf_tensor_to_f32(const rt_gguf *g, int64_t idx, float *dst, uint6
  * f32 [rows, cols] -> Q4_K blocks, cols % 256 == 0. */
 rt_status rt_q4k_quantize(const float *src, size_t rows, size_t cols, uint8_t *blocks);
 
-/* The weight of a linear layer as the hot path consumes it. */
-#define RT_LINEAR_Q4K 1
-#define RT_LINEAR_BF16 2
-#define RT_LINEAR_F32 3
+/* The weight of a linear layer as the hot path consumes it (RT_LINEAR_*
+ * formats are defined in rt_hip.h). */
 typedef struct {
     int32_t format;       /* RT_LINEAR_* */
     int32_t src_type;     /* ggml type id of the file tensor */
@@ -110,6 +108,13 @@ typedef struct {
  * and Q6_K widen to f32 and round to BF16; F32 stays F32.  Other types return
  * RT_EINVAL (the reference warns and skips the tensor). */
 rt_status rt_gguf_load_linear(const rt_gguf *g, int64_t idx, rt_linear *out);
+/* Same, with flags.  RT_LOAD_KEEP_PACKED keeps Q6_K (cols % 256 == 0) and
+ * Q8_0 (cols % 32 == 0) tensors packed, in the planar layout the native
+ * Q6_K / Q8_0 GEMVs read (formats RT_LINEAR_Q6K / RT_LINEAR_Q8_0), instead of
+ * widening them to BF16 as the reference does.  No counterpart in the
+ * reference. */
+#define RT_LOAD_KEEP_PACKED 1
+rt_status rt_gguf_load_linear_ex(const rt_gguf *g, int64_t idx, int32_t flags, rt_linear *out);
 rt_status rt_linear_free(rt_linear *l);
 
 #ifdef __cplusplus

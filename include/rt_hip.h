@@ -92,6 +92,13 @@ rt_status rt_q4k_gemm_bf16(const uint16_t *a_dev, const void *w_dev, float *c_de
                            void *stream);
 rt_status rt_q4k_gemm_f32(const float *a_dev, const void *w_dev, float *c_dev, int64_t m, int64_t n, int64_t k,
                           void *stream);
+/* Weight formats of a linear layer on the device. */
+#define RT_LINEAR_Q4K 1    /* 144-byte Q4_K blocks as in the file */
+#define RT_LINEAR_BF16 2   /* bf16 [rows][cols] */
+#define RT_LINEAR_F32 3    /* f32 [rows][cols] */
+#define RT_LINEAR_Q6K 4    /* planar Q6_K (rt_q6k_repack) */
+#define RT_LINEAR_Q8_0 5   /* planar Q8_0 (rt_q8_0_repack) */
+
 /* ---------------------------------------------------------------------------
  * Q6_K and Q8_0 weights kept packed on the device.  No counterpart in the
  * reference, which widens both to f32 and then BF16 at load
@@ -160,6 +167,14 @@ rt_status rt_decode_destroy(rt_decode *d);
  * stay packed; upload_linear_detect_type, metal_decode.rs:1259-1277).
  * device_ptrs = 1: device pointers, borrowed; the caller keeps them alive. */
 rt_status rt_decode_set_layer(rt_decode *d, int32_t layer, const rt_gemma3_layer *w, int32_t device_ptrs);
+/* Same, with the format of each projection in the order q, k, v, o, gate,
+ * up, down: RT_LINEAR_Q4K, RT_LINEAR_Q6K, RT_LINEAR_Q8_0 or RT_LINEAR_BF16
+ * (the device layouts of rt_gguf_load_linear_ex).  The reference's context
+ * takes Q4_K or BF16 per projection (upload_linear_detect_type,
+ * metal_decode.rs:1259-1277, with Q6_K/Q8_0 widened to BF16 at load); here
+ * Q6_K and Q8_0 also run natively.  rt_decode_prefill needs Q4_K projections. */
+rt_status rt_decode_set_layer_formats(rt_decode *d, int32_t layer, const rt_gemma3_layer *w,
+                                      const int32_t *formats, int32_t device_ptrs);
 /* BF16 [vocab, hidden] embedding, also the tied lm_head (1097-1105), and the final norm gamma. */
 rt_status rt_decode_set_embed(rt_decode *d, const uint16_t *embed, const float *final_norm, int32_t device_ptrs);
 /* sync_kv_from_cpu (metal_decode.rs:1366-1396) for one layer: seq_len rows of K and V. */

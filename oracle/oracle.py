@@ -281,7 +281,10 @@ class Gemma3Cfg(C.Structure):
 class Layer(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in ("q", "k", "v", "o", "gate", "up", "down", "in_norm", "post_attn_norm",
                                           "pre_ffn_norm", "post_ffn_norm", "q_norm", "k_norm", "k_cache",
-                                          "v_cache")]
+                                          "v_cache")] + [("fmt", C.c_int32 * 7)]
+
+
+PROJECTIONS = ("q", "k", "v", "o", "gate", "up", "down")
 
 
 def _ptr(a: np.ndarray) -> int:
@@ -294,10 +297,15 @@ def make_cfg(d: dict) -> Gemma3Cfg:
 
 
 def make_layers(layers: list[dict]) -> C.Array:
+    """Layer dicts -> orc_layer array.  An optional L["fmt"] maps projection
+    names to formats (1 Q4_K, 2 BF16, 4 Q6_K and 5 Q8_0 in GGUF block bytes)."""
     arr = (Layer * len(layers))()
     for i, L in enumerate(layers):
         for name, _ in Layer._fields_:
-            setattr(arr[i], name, _ptr(L[name]))
+            if name != "fmt":
+                setattr(arr[i], name, _ptr(L[name]))
+        fmt = L.get("fmt", {})
+        arr[i].fmt = (C.c_int32 * 7)(*[fmt.get(p, 1) for p in PROJECTIONS])
     return arr
 
 
@@ -315,6 +323,15 @@ def gemma3_decode_step(cfg: dict, layers: list[dict], embed: np.ndarray, final_n
                                  C.c_uint32(token), C.c_uint32(pos), C.c_void_p(_ptr(logits)),
                                  C.c_void_p(_ptr(hidden)), C.c_int(threads))
     return (logits, hidden) if want_hidden else logits
+
+
+def proj_gemv(fmt: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray, threads: int = 0) -> np.ndarray:
+    """orc_proj_gemv: y = W x for a projection of format fmt."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(rows, np.float32)
+    lib().orc_proj_gemv(C.c_int(fmt), C.c_void_p(_ptr(np.ascontiguousarray(w))), C.c_size_t(rows),
+                        C.c_size_t(cols), C.c_void_p(_ptr(x)), C.c_void_p(_ptr(y)), C.c_int(threads))
+    return y
 
 
 def gqa_attention_prefill(q, k_cache, v_cache, p0, T, lo_fixed, window, n_q_heads, n_kv_heads, d_head, scale):

@@ -12,6 +12,7 @@
 
 #include <math.h>
 #include <pthread.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 #include <unistd.h>
@@ -690,6 +691,32 @@ void orc_gqa_attention_decode(const float *q, const float *k_cache, const float 
     free(scores);
 }
 
+/* Per-format projection GEMV (formats of orc_layer.fmt). */
+typedef struct { int fmt; const uint8_t *w; size_t cols; const float *x; float *y; } pg_ctx;
+static void pg_band(void *p, size_t j0, size_t j1)
+{
+    pg_ctx *c = (pg_ctx *)p;
+    float *row = (float *)malloc(c->cols * sizeof(float));
+    for (size_t j = j0; j < j1; j++) {
+        if (c->fmt == 4) orc_q6k_dequant(c->w + j * (c->cols / 256) * 210, c->cols, row);
+        else orc_q8_0_dequant(c->w + j * (c->cols / 32) * 34, c->cols, row);
+        float acc = 0.0f;
+        for (size_t i = 0; i < c->cols; i++) acc += row[i] * c->x[i];
+        c->y[j] = acc;
+    }
+    free(row);
+}
+void orc_proj_gemv(int fmt, const uint8_t *w, size_t rows, size_t cols, const float *x, float *y, int hw)
+{
+    if (fmt == 2) { orc_bf16_gemv_mt((const uint16_t *)w, rows, cols, x, y, hw); return; }
+    if (fmt == 4 || fmt == 5) {
+        pg_ctx ctx = {fmt, w, cols, x, y};
+        run_bands(rows, hw, 1, pg_band, &ctx);
+        return;
+    }
+    orc_q4k_gemv_mt(w, rows, cols, x, y, hw);
+}
+
 static int is_global(const orc_gemma3_cfg *cfg, int layer)
 {
     /* Config4::is_global_layer: transformer4.rs:141-143 (layer % 6 == 5).
@@ -721,9 +748,9 @@ void orc_gemma3_layer(const orc_gemma3_cfg *cfg, const orc_layer *L, int layer_i
     float *m = (float *)malloc(H * sizeof(float)), *mn = (float *)malloc(H * sizeof(float));
 
     orc_rms_norm_gemma3(x, L->in_norm, H, cfg->eps, normed);
-    orc_q4k_gemv_mt(L->q, QD, H, normed, q, hw);
-    orc_q4k_gemv_mt(L->k, KVD, H, normed, k, hw);
-    orc_q4k_gemv_mt(L->v, KVD, H, normed, v, hw);
+    orc_proj_gemv(L->fmt[0], L->q, QD, H, normed, q, hw);
+    orc_proj_gemv(L->fmt[1], L->k, KVD, H, normed, k, hw);
+    orc_proj_gemv(L->fmt[2], L->v, KVD, H, normed, v, hw);
     orc_per_head_norm(q, L->q_norm, NQ, D, cfg->eps, qn);
     orc_per_head_norm(k, L->k_norm, NKV, D, cfg->eps, kn);
     orc_rope_neox(qn, NQ, D, theta, pos, fs);
@@ -736,14 +763,14 @@ void orc_gemma3_layer(const orc_gemma3_cfg *cfg, const orc_layer *L, int layer_i
     if (!glob && cfg->sliding_window > 0)
         k_start = k_end > (size_t)cfg->sliding_window ? k_end - (size_t)cfg->sliding_window : 0;
     orc_gqa_attention_decode(qn, L->k_cache, L->v_cache, k_start, k_end, NQ, NKV, D, cfg->attn_scale, attn);
-    orc_q4k_gemv_mt(L->o, H, QD, attn, o, hw);
+    orc_proj_gemv(L->fmt[3], L->o, H, QD, attn, o, hw);
     orc_rms_norm_gemma3(o, L->post_attn_norm, H, cfg->eps, on);
     for (size_t c = 0; c < H; c++) x2[c] = x[c] + on[c];
     orc_rms_norm_gemma3(x2, L->pre_ffn_norm, H, cfg->eps, n2);
-    orc_q4k_gemv_mt(L->gate, F, H, n2, g, hw);
-    orc_q4k_gemv_mt(L->up, F, H, n2, u, hw);
+    orc_proj_gemv(L->fmt[4], L->gate, F, H, n2, g, hw);
+    orc_proj_gemv(L->fmt[5], L->up, F, H, n2, u, hw);
     for (size_t c = 0; c < F; c++) g[c] = orc_gelu_tanh(g[c]) * u[c];
-    orc_q4k_gemv_mt(L->down, H, F, g, m, hw);
+    orc_proj_gemv(L->fmt[6], L->down, H, F, g, m, hw);
     orc_rms_norm_gemma3(m, L->post_ffn_norm, H, cfg->eps, mn);
     for (size_t c = 0; c < H; c++) x[c] = x2[c] + mn[c];
 
@@ -849,6 +876,8 @@ void orc_gemma3_prefill(const orc_gemma3_cfg *cfg, const orc_layer *layers, cons
         for (size_t c = 0; c < H; c++) x[t * H + c] = orc_bf16_to_f32(embed_bf16[(size_t)tokens[t] * H + c]) * scale;
     for (int l = 0; l < cfg->n_layers; l++) {
         const orc_layer *L = &layers[l];
+        for (int p = 0; p < 7; p++)
+            if (L->fmt[p] > 1) { fprintf(stderr, "orc_gemma3_prefill: Q4_K projections only\n"); abort(); }
         int glob = is_global(cfg, l);
         float theta = glob ? cfg->rope_theta_global : cfg->rope_theta_local;
         float fs = glob ? cfg->rope_fs_global : cfg->rope_fs_local;

@@ -81,10 +81,16 @@ typedef struct {
 
 /* Per-layer weights (transformer4.rs Gemma3Block); all host pointers. */
 typedef struct {
-    const uint8_t *q, *k, *v, *o, *gate, *up, *down;          /* Q4_K packed, rows=out, cols=in */
+    const uint8_t *q, *k, *v, *o, *gate, *up, *down;          /* rows=out, cols=in, format fmt[i] */
     const float *in_norm, *post_attn_norm, *pre_ffn_norm, *post_ffn_norm, *q_norm, *k_norm;
     float *k_cache, *v_cache;                                  /* [max_seq, n_kv_heads*head_dim] f32 */
+    int32_t fmt[7];  /* q, k, v, o, gate, up, down: 0 or 1 Q4_K, 2 BF16, 4 Q6_K (GGUF blocks), 5 Q8_0 (GGUF blocks) */
 } orc_layer;
+
+/* y = W x (rows x cols) for a projection of format fmt (as orc_layer.fmt):
+ * Q4_K through dot_row; Q6_K / Q8_0 dequantised per row by decode_q6k_to_f32
+ * / decode_q8_0_to_f32 and a sequential f32 dot; BF16 through its dot_row. */
+void orc_proj_gemv(int fmt, const uint8_t *w, size_t rows, size_t cols, const float *x, float *y, int hw_threads);
 
 /* One CPU decode step (transformer4.rs:2358-2385 with forward_cached 1900-1964).
  * Appends K/V at row `pos` of every layer's cache and writes vocab logits.

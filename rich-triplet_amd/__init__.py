@@ -25,6 +25,9 @@ LIB_PATH = PKG_DIR / "librt_hip.so"
 RT_OK, RT_EINVAL, RT_EHIP, RT_ENOMEM, RT_ESTATE = 0, 1, 2, 3, 4
 
 
+LINEAR_Q4K, LINEAR_BF16, LINEAR_F32, LINEAR_Q6K, LINEAR_Q8_0 = 1, 2, 3, 4, 5  # RT_LINEAR_* (rt_hip.h)
+
+
 class RtError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"rt status {code}: {msg}")
@@ -62,6 +65,7 @@ _SIGNATURES = {
     "rt_decode_create": (_i32, [_vp, C.POINTER(_vp)]),
     "rt_decode_destroy": (_i32, [_vp]),
     "rt_decode_set_layer": (_i32, [_vp, _i32, _vp, _i32]),
+    "rt_decode_set_layer_formats": (_i32, [_vp, _i32, _vp, _vp, _i32]),
     "rt_decode_set_embed": (_i32, [_vp, _vp, _vp, _i32]),
     "rt_decode_sync_kv": (_i32, [_vp, _i32, _vp, _vp, _i32, _i32]),
     "rt_decode_step": (_i32, [_vp, _i32, _i32, _vp]),
@@ -95,6 +99,7 @@ _SIGNATURES = {
     "rt_gguf_tensor_to_f32": (_i32, [_vp, _i64, _vp, C.c_uint64]),
     "rt_q4k_quantize": (_i32, [_vp, _sz, _sz, _vp]),
     "rt_gguf_load_linear": (_i32, [_vp, _i64, _vp]),
+    "rt_gguf_load_linear_ex": (_i32, [_vp, _i64, _i32, _vp]),
     "rt_linear_free": (_i32, [_vp]),
 }
 
@@ -318,20 +323,23 @@ class HipDecodeContext:
     def _on_device(x) -> int:
         return int((hasattr(x, "is_cuda") and x.is_cuda) or (hasattr(x, "ptr") and hasattr(x, "format")))
 
-    def set_layer(self, i: int, w: dict) -> None:
-        """w: the 7 Q4_K projections and 6 norm vectors (Gemma3Layer fields); all
+    PROJECTIONS = ("q", "k", "v", "o", "gate", "up", "down")
+
+    def set_layer(self, i: int, w: dict, formats=None) -> None:
+        """w: the 7 projections and 6 norm vectors (Gemma3Layer fields); all
         host arrays, or all device memory (torch cuda tensors or GGUF-loaded
-        `Linear`s, whose projections must be Q4_K)."""
-        for k in ("q", "k", "v", "o", "gate", "up", "down"):
-            fmt = getattr(w[k], "format", None)
-            if fmt is not None and fmt != 1:
-                raise RtError(RT_EINVAL, f"layer {i} projection {k} is not Q4_K (format {fmt}); "
-                                         "the decode step runs Q4_K projections")
+        `Linear`s).  formats: RT_LINEAR_* per projection (q, k, v, o, gate, up,
+        down); by default a `Linear`'s own format, else Q4_K."""
+        if formats is None:
+            formats = [getattr(w[k], "format", LINEAR_Q4K) for k in self.PROJECTIONS]
+        elif isinstance(formats, dict):
+            formats = [formats.get(k, LINEAR_Q4K) for k in self.PROJECTIONS]
         dev = self._on_device(w["q"])
         L = Gemma3Layer(**{k: _addr(w[k]) for k, _ in Gemma3Layer._fields_})
         if dev:
             self._keep.append(w)
-        check(lib().rt_decode_set_layer(self._h, i, C.byref(L), dev))
+        f = (C.c_int32 * 7)(*formats)
+        check(lib().rt_decode_set_layer_formats(self._h, i, C.byref(L), f, dev))
 
     def set_embed(self, embed, final_norm) -> None:
         dev = self._on_device(embed)

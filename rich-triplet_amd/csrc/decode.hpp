@@ -38,7 +38,9 @@ struct LayerArgs {
   const float *rope_cs;    // [head_dim] cos | sin of this step's angles (in the params block)
   int window;              // sliding window in keys, 0 = global layer
   int global;              // 1: global layer (RoPE theta_global; never windowed)
+  int fmt[7];              // RT_LINEAR_* of q, k, v, o, gate, up, down (Q4K for the fused kernels)
 };
+enum Proj { kProjQ, kProjK, kProjV, kProjO, kProjGate, kProjUp, kProjDown };
 
 // Step-wide device buffers and constants.
 struct DecodeArgs {
@@ -46,6 +48,7 @@ struct DecodeArgs {
   const uint16_t *embed;   // [vocab, hidden] bf16, also the tied lm_head
   const float *g_final;
   float *hid, *x2, *q, *k, *v, *attn, *o, *h, *dn, *logits;
+  float *xn, *u;           // normalised input of a split projection set [hidden]; up output [ffn]
   float *part_m, *part_l, *part_o;  // [n_q_heads, nchunk(, head_dim)]
   float embed_scale, eps, attn_scale;
   int vocab, n_q_heads, n_kv_heads, head_dim;

@@ -70,8 +70,6 @@ void dfree(rt_decode *d, void *p) {
     }
 }
 
-size_t q4k_bytes(size_t rows, size_t cols) { return rows * (cols / 256) * 144; }
-
 void drop_graph(rt_decode *d) {
   if (d->exec) (void)hipGraphExecDestroy(d->exec);
   d->exec = nullptr;
@@ -164,6 +162,7 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
     };
     TRY(fbuf(H, &a.hid)); TRY(fbuf(H, &a.x2)); TRY(fbuf(QD, &a.q)); TRY(fbuf(KVD, &a.k)); TRY(fbuf(KVD, &a.v));
     TRY(fbuf(QD, &a.attn)); TRY(fbuf(H, &a.o)); TRY(fbuf(F, &a.h)); TRY(fbuf(H, &a.dn));
+    TRY(fbuf(H, &a.xn)); TRY(fbuf(F, &a.u));
     TRY(fbuf((size_t)c.vocab, &a.logits));
     TRY(fbuf((size_t)c.n_q_heads * nch, &a.part_m)); TRY(fbuf((size_t)c.n_q_heads * nch, &a.part_l));
     TRY(fbuf((size_t)c.n_q_heads * nch * D, &a.part_o));
@@ -199,6 +198,7 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
       L.rope_cs = cs_dev + (g ? D : 0);
       L.window = g ? 0 : c.sliding_window;
       L.global = g ? 1 : 0;
+      for (int &f : L.fmt) f = RT_LINEAR_Q4K;
     }
   }
 #undef TRY
@@ -244,10 +244,36 @@ static rt_status bind_buf(rt_decode *d, const void *src, size_t bytes, int32_t d
   return RT_OK;
 }
 
+// Bytes of a [rows][cols] projection in format fmt; 0 if cols does not suit it.
+static size_t proj_bytes(int fmt, size_t rows, size_t cols) {
+  switch (fmt) {
+    case RT_LINEAR_Q4K: return cols % 256 ? 0 : rows * (cols / 256) * 144;
+    case RT_LINEAR_Q6K: return cols % 256 ? 0 : rows * (cols / 256) * 210;
+    case RT_LINEAR_Q8_0: return cols % 32 ? 0 : rows * (cols / 32) * 34;
+    case RT_LINEAR_BF16: return cols % 8 ? 0 : rows * cols * 2;
+    default: return 0;
+  }
+}
+
 rt_status rt_decode_set_layer(rt_decode *d, int32_t layer, const rt_gemma3_layer *w, int32_t device_ptrs) {
-  if (!d || !w) return set_error(RT_EINVAL, "rt_decode_set_layer: null pointer");
+  const int32_t all_q4k[7] = {RT_LINEAR_Q4K, RT_LINEAR_Q4K, RT_LINEAR_Q4K, RT_LINEAR_Q4K,
+                              RT_LINEAR_Q4K, RT_LINEAR_Q4K, RT_LINEAR_Q4K};
+  return rt_decode_set_layer_formats(d, layer, w, all_q4k, device_ptrs);
+}
+
+rt_status rt_decode_set_layer_formats(rt_decode *d, int32_t layer, const rt_gemma3_layer *w, const int32_t *formats,
+                                      int32_t device_ptrs) {
+  if (!d || !w || !formats) return set_error(RT_EINVAL, "rt_decode_set_layer: null pointer");
   const rt_gemma3_config &c = d->cfg;
   if (layer < 0 || layer >= c.n_layers) return set_error(RT_EINVAL, "rt_decode_set_layer: layer %d out of range", layer);
+  {
+    const size_t H = c.hidden, F = c.ffn, QD = (size_t)c.n_q_heads * c.head_dim, KVD = (size_t)c.n_kv_heads * c.head_dim;
+    const size_t shape[7][2] = {{QD, H}, {KVD, H}, {KVD, H}, {H, QD}, {F, H}, {F, H}, {H, F}};
+    static const char *names[7] = {"q", "k", "v", "o", "gate", "up", "down"};
+    for (int p = 0; p < 7; ++p)
+      if (!proj_bytes(formats[p], shape[p][0], shape[p][1]))
+        return set_error(RT_EINVAL, "rt_decode_set_layer: projection %s has unsupported format %d", names[p], formats[p]);
+  }
   (void)hipStreamSynchronize(d->stream);
   for (void *p : d->owned_layer[layer]) dfree(d, p);
   d->owned_layer[layer].clear();
@@ -261,13 +287,14 @@ rt_status rt_decode_set_layer(rt_decode *d, int32_t layer, const rt_gemma3_layer
   st = bind_buf(d, src, bytes, device_ptrs, own, &p, #field);                  \
   if (st != RT_OK) return st;                                              \
   L.field = (cast)p;
-  B(wq, w->q, q4k_bytes(QD, H), const uint8_t *);
-  B(wk, w->k, q4k_bytes(KVD, H), const uint8_t *);
-  B(wv, w->v, q4k_bytes(KVD, H), const uint8_t *);
-  B(wo, w->o, q4k_bytes(H, QD), const uint8_t *);
-  B(wgate, w->gate, q4k_bytes(F, H), const uint8_t *);
-  B(wup, w->up, q4k_bytes(F, H), const uint8_t *);
-  B(wdown, w->down, q4k_bytes(H, F), const uint8_t *);
+  B(wq, w->q, proj_bytes(formats[kProjQ], QD, H), const uint8_t *);
+  B(wk, w->k, proj_bytes(formats[kProjK], KVD, H), const uint8_t *);
+  B(wv, w->v, proj_bytes(formats[kProjV], KVD, H), const uint8_t *);
+  B(wo, w->o, proj_bytes(formats[kProjO], H, QD), const uint8_t *);
+  B(wgate, w->gate, proj_bytes(formats[kProjGate], F, H), const uint8_t *);
+  B(wup, w->up, proj_bytes(formats[kProjUp], F, H), const uint8_t *);
+  B(wdown, w->down, proj_bytes(formats[kProjDown], H, F), const uint8_t *);
+  for (int p = 0; p < 7; ++p) L.fmt[p] = formats[p];
   B(g_in, w->in_norm, H * 4, const float *);
   B(g_post_attn, w->post_attn_norm, H * 4, const float *);
   B(g_pre_ffn, w->pre_ffn_norm, H * 4, const float *);
@@ -547,6 +574,11 @@ rt_status rt_decode_prefill(rt_decode *d, const int32_t *tokens, int32_t n, int3
     rt_status st = check_ready(d, tokens[i], start_position + i);
     if (st != RT_OK) return st;
   }
+  for (int l = 0; l < d->cfg.n_layers; ++l)
+    for (int p = 0; p < 7; ++p)
+      if (d->layers[l].fmt[p] != RT_LINEAR_Q4K)
+        return set_error(RT_EINVAL, "rt_decode_prefill: layer %d has a projection in format %d; prefill runs Q4_K "
+                         "projections only", l, d->layers[l].fmt[p]);
   const int w = d->cfg.sliding_window;
   int lo_fixed = 0, window = 0;
   if (mode == RT_PREFILL_REFERENCE)

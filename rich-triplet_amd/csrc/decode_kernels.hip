@@ -17,10 +17,12 @@
 // memory so the whole step replays as one hipGraph.
 #include <vector>
 
+#include "../../include/rt_hip.h"
 #include "decode.hpp"
 #include "gemma3_math.hpp"
 #include "q4k_gemv.hpp"
 #include "rt_device.hpp"
+#include "rt_kernels.hpp"
 
 namespace rt {
 
@@ -64,7 +66,8 @@ RT_DEV void pro_load(const DecodeArgs &a, const float *__restrict__ base, const 
 }
 
 template <int K, int T, Pro MODE, bool DIG = false>
-RT_DEV void pro_finish(const DecodeArgs &a, ProRegs<K, T> &r, float *__restrict__ x_out, void *lds, float *red) {
+RT_DEV void pro_finish(const DecodeArgs &a, ProRegs<K, T> &r, float *__restrict__ x_out, void *lds, float *red,
+                       float *__restrict__ xn_out = nullptr) {
   using R = ProRegs<K, T>;
   const float inv_k = 1.0f / (float)K;
   float4 *x = r.add;  // Embed: the embedding row; Resid: overwritten with the residual sum
@@ -85,11 +88,15 @@ RT_DEV void pro_finish(const DecodeArgs &a, ProRegs<K, T> &r, float *__restrict_
   for (int i = 0; i < R::PER; ++i) {
     const int f = threadIdx.x + i * T;
     if (f < R::F4) {
-      if (x_out && blockIdx.x == 0) reinterpret_cast<float4 *>(x_out)[f] = x[i];
+      const float4 xn = norm4(x[i], rx, r.go[i]);
+      if (blockIdx.x == 0) {
+        if (x_out) reinterpret_cast<float4 *>(x_out)[f] = x[i];
+        if (xn_out) reinterpret_cast<float4 *>(xn_out)[f] = xn;
+      }
       if constexpr (DIG)
-        stage_digits_store(static_cast<uint32_t *>(lds), f, norm4(x[i], rx, r.go[i]));
+        stage_digits_store(static_cast<uint32_t *>(lds), f, xn);
       else
-        stage_x_store(static_cast<float *>(lds), f, norm4(x[i], rx, r.go[i]));
+        stage_x_store(static_cast<float *>(lds), f, xn);
     }
   }
 }
@@ -121,13 +128,57 @@ __global__ __launch_bounds__(T) void k_qkv(DecodeArgs a, LayerArgs L, LayerArgs 
   pro_load<K, T, MODE>(a, a.x2, a.dn, prev.g_post_ffn, L.g_in, pr);
   Tile tile;
   tile.load([&](int rl) -> const uint8_t * { return W + (size_t)(r0 + rl) * row_bytes; }, W);
-  pro_finish<K, T, MODE, true>(a, pr, a.hid, dl, bred);
+  pro_finish<K, T, MODE, true>(a, pr, a.hid, dl, bred, a.xn);
   __syncthreads();
   ChunkD cx;
   chunkd_from_lds(dl, tile.slot, cx);
   tile.compute_digits(cx, red);
   __syncthreads();
   for (int i = threadIdx.x; i < Tile::ROWS; i += T) y[r0 + i] = reduce_row<NB>(red, i);
+}
+
+// ---------------------------------------------------------------------------
+// Split projection sets (a projection that is not Q4_K): k_prologue forms the
+// same x and normalised xn as the fused kernels' prologues, one workgroup,
+// into global memory; the projections then run as plain GEMVs of their
+// format, and k_gelu_mul_vec finishes a split gate/up pair.
+// ---------------------------------------------------------------------------
+template <int K, Pro MODE>
+__global__ __launch_bounds__(256) void k_prologue(DecodeArgs a, const float *__restrict__ base,
+                                                  const float *__restrict__ add, const float *__restrict__ g_add,
+                                                  const float *__restrict__ g_out, float *__restrict__ x_out,
+                                                  float *__restrict__ xn_out) {
+  constexpr int T = 256;
+  __shared__ float bred[T / 64];
+  ProRegs<K, T> pr;
+  pro_load<K, T, MODE>(a, base, add, g_add, g_out, pr);
+  using R = ProRegs<K, T>;
+  const float inv_k = 1.0f / (float)K;
+  auto live = [&](int i) { return (int)threadIdx.x + i * T < R::F4; };
+  float4 *x = pr.add;
+  if constexpr (MODE == Pro::Resid) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < R::PER; ++i) ss += live(i) ? sumsq4(pr.add[i]) : 0.f;
+    const float ra = rms_inv_from_sumsq(block_sum<T>(ss, bred), inv_k, a.eps);
+#pragma unroll
+    for (int i = 0; i < R::PER; ++i) x[i] = add4(pr.base[i], norm4(pr.add[i], ra, pr.ga[i]));
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < R::PER; ++i) ss += live(i) ? sumsq4(x[i]) : 0.f;
+  const float rx = rms_inv_from_sumsq(block_sum<T>(ss, bred), inv_k, a.eps);
+#pragma unroll
+  for (int i = 0; i < R::PER; ++i)
+    if (live(i)) {
+      const int f = threadIdx.x + i * T;
+      reinterpret_cast<float4 *>(x_out)[f] = x[i];
+      reinterpret_cast<float4 *>(xn_out)[f] = norm4(x[i], rx, pr.go[i]);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_gelu_mul_vec(float *h, const float *__restrict__ u, int n) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) h[i] = mul_nc(gelu_tanh(h[i]), u[i]);
 }
 
 // ---------------------------------------------------------------------------
@@ -648,7 +699,29 @@ static void launch_attn_d(Launch &l, const DecodeArgs &a, const LayerArgs &L, in
   l.check();
 }
 
-// The six launches of every layer.
+// A projection that is not Q4_K: the plain GEMV of its format.
+static void launch_proj(Launch &l, int fmt, const uint8_t *W, const float *x, float *y, int n, int k) {
+  if (l.err != hipSuccess) return;
+  switch (fmt) {
+    case RT_LINEAR_Q6K: l.err = launch_q6k_gemv(W, x, y, n, k, l.s); break;
+    case RT_LINEAR_Q8_0: l.err = launch_q8_0_gemv(W, x, y, n, k, l.s); break;
+    case RT_LINEAR_BF16: l.err = launch_bf16_gemv(reinterpret_cast<const uint16_t *>(W), x, y, n, k, l.s); break;
+    default: l.err = launch_q4k_gemv(W, x, y, n, k, l.s); break;
+  }
+}
+
+template <Pro MODE>
+static void launch_prologue(Launch &l, const DecodeShape &s, const DecodeArgs &a, const float *base, const float *add,
+                            const float *g_add, const float *g_out, float *x_out) {
+  if (s.hidden == 2560)
+    hipLaunchKernelGGL((k_prologue<2560, MODE>), dim3(1), dim3(256), 0, l.s, a, base, add, g_add, g_out, x_out, a.xn);
+  else
+    hipLaunchKernelGGL((k_prologue<512, MODE>), dim3(1), dim3(256), 0, l.s, a, base, add, g_add, g_out, x_out, a.xn);
+  l.check();
+}
+
+// The six launches of every layer (all-Q4_K projections); a projection of
+// another format splits its set into a prologue and plain GEMVs.
 static hipError_t enqueue_layers(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers, hipStream_t stream) {
   Launch l{stream};
   const int qd = s.n_q_heads * s.head_dim, kvd = s.n_kv_heads * s.head_dim;
@@ -657,19 +730,42 @@ static hipError_t enqueue_layers(const DecodeShape &s, const DecodeArgs &a, cons
   for (int li = 0; li < s.n_layers && l.err == hipSuccess; ++li) {
     const LayerArgs &L = layers[li];
     const LayerArgs &P = layers[li > 0 ? li - 1 : 0];
-    const int qkv_rows = qd + 2 * kvd;
-    if (big) launch_qkv<10, 640, 1>(l, a, L, P, li == 0, qkv_rows);
-    else launch_qkv<2, 256, 1>(l, a, L, P, li == 0, qkv_rows);
+    auto q4 = [&](int p) { return L.fmt[p] == RT_LINEAR_Q4K; };
+    if (q4(kProjQ) && q4(kProjK)) {
+      // fused prologue + GEMV over q|k(|v) rows; it also leaves xn for a split v
+      const int qkv_rows = qd + kvd + (q4(kProjV) ? kvd : 0);
+      if (big) launch_qkv<10, 640, 1>(l, a, L, P, li == 0, qkv_rows);
+      else launch_qkv<2, 256, 1>(l, a, L, P, li == 0, qkv_rows);
+      if (!q4(kProjV)) launch_proj(l, L.fmt[kProjV], L.wv, a.xn, a.v, kvd, s.hidden);
+    } else {
+      if (li == 0) launch_prologue<Pro::Embed>(l, s, a, nullptr, nullptr, nullptr, L.g_in, a.hid);
+      else launch_prologue<Pro::Resid>(l, s, a, a.x2, a.dn, P.g_post_ffn, L.g_in, a.hid);
+      launch_proj(l, L.fmt[kProjQ], L.wq, a.xn, a.q, qd, s.hidden);
+      launch_proj(l, L.fmt[kProjK], L.wk, a.xn, a.k, kvd, s.hidden);
+      launch_proj(l, L.fmt[kProjV], L.wv, a.xn, a.v, kvd, s.hidden);
+    }
     const int nchunk = L.window > 0 ? s.nchunk_local : s.nchunk_global;
     if (s.head_dim == 256)
       launch_attn_d<256>(l, a, L, nchunk, group);
     else
       launch_attn_d<128>(l, a, L, nchunk, group);
-    if (qd == 2048) launch_gemv<8, 512, 1>(l, L.wo, a.attn, a.o, s.hidden);
+    if (!q4(kProjO)) launch_proj(l, L.fmt[kProjO], L.wo, a.attn, a.o, s.hidden, qd);
+    else if (qd == 2048) launch_gemv<8, 512, 1>(l, L.wo, a.attn, a.o, s.hidden);
     else launch_gemv<2, 256, 1>(l, L.wo, a.attn, a.o, s.hidden);
-    if (big) launch_gateup<10, 640>(l, a, L, s.ffn);
-    else launch_gateup<2, 256>(l, a, L, s.ffn);
-    if (s.ffn == 10240) launch_gemv<40, 960, 1>(l, L.wdown, a.h, a.dn, s.hidden);
+    if (q4(kProjGate) && q4(kProjUp)) {
+      if (big) launch_gateup<10, 640>(l, a, L, s.ffn);
+      else launch_gateup<2, 256>(l, a, L, s.ffn);
+    } else {
+      launch_prologue<Pro::Resid>(l, s, a, a.hid, a.o, L.g_post_attn, L.g_pre_ffn, a.x2);
+      launch_proj(l, L.fmt[kProjGate], L.wgate, a.xn, a.h, s.ffn, s.hidden);
+      launch_proj(l, L.fmt[kProjUp], L.wup, a.xn, a.u, s.ffn, s.hidden);
+      if (l.err == hipSuccess) {
+        hipLaunchKernelGGL(k_gelu_mul_vec, dim3((s.ffn + 255) / 256), dim3(256), 0, l.s, a.h, a.u, s.ffn);
+        l.check();
+      }
+    }
+    if (!q4(kProjDown)) launch_proj(l, L.fmt[kProjDown], L.wdown, a.h, a.dn, s.hidden, s.ffn);
+    else if (s.ffn == 10240) launch_gemv<40, 960, 1>(l, L.wdown, a.h, a.dn, s.hidden);
     else launch_gemv<4, 256, 1>(l, L.wdown, a.h, a.dn, s.hidden);
   }
   return l.err;

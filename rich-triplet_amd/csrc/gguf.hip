@@ -22,6 +22,7 @@
 
 #include "../../include/rt_gguf.h"
 #include "rt_capi_util.hpp"
+#include "rt_kernels.hpp"
 
 // The reference rounds every f32 product and difference separately.
 #pragma clang fp contract(off)
@@ -578,7 +579,7 @@ rt_status rt_q4k_quantize(const float *src, size_t rows, size_t cols, uint8_t *b
   return RT_OK;
 }
 
-rt_status rt_gguf_load_linear(const rt_gguf *g, int64_t idx, rt_linear *out) {
+rt_status rt_gguf_load_linear_ex(const rt_gguf *g, int64_t idx, int32_t flags, rt_linear *out) {
   const TensorEntry *t = entry(g, idx);
   if (!t || !out) return set_error(RT_EINVAL, "rt_gguf_load_linear: bad handle or index");
   std::memset(out, 0, sizeof *out);
@@ -628,7 +629,24 @@ rt_status rt_gguf_load_linear(const rt_gguf *g, int64_t idx, rt_linear *out) {
       if (rt_status s = read_bytes(g, *t, host.data()); s != RT_OK) return s;
       format = RT_LINEAR_F32;
       break;
-    case RT_GGUF_F16: case RT_GGUF_Q8_0: case RT_GGUF_Q5_K: case RT_GGUF_Q6_K: {
+    case RT_GGUF_Q6_K:
+    case RT_GGUF_Q8_0:
+      if ((flags & RT_LOAD_KEEP_PACKED) && cols % (t->type == RT_GGUF_Q6_K ? 256 : 32) == 0) {
+        // packed in the planar device layout (rows start on block boundaries)
+        std::vector<uint8_t> raw((size_t)t->n_bytes);
+        if (rt_status s = read_bytes(g, *t, raw.data()); s != RT_OK) return s;
+        host.resize(raw.size());
+        if (t->type == RT_GGUF_Q6_K) {
+          rt::q6k_repack_host(raw.data(), raw.size() / 210, host.data());
+          format = RT_LINEAR_Q6K;
+        } else {
+          rt::q8_0_repack_host(raw.data(), raw.size() / 34, host.data());
+          format = RT_LINEAR_Q8_0;
+        }
+        break;
+      }
+      [[fallthrough]];
+    case RT_GGUF_F16: case RT_GGUF_Q5_K: {
       // widen to f32, then f32s_to_bf16_and_drop (transformer4.rs:1084-1097)
       std::vector<float> f((size_t)t->n_elem);
       rt_status s = rt_gguf_tensor_to_f32(g, idx, f.data(), t->n_elem);
@@ -653,6 +671,10 @@ rt_status rt_gguf_load_linear(const rt_gguf *g, int64_t idx, rt_linear *out) {
   out->format = format, out->src_type = t->type, out->rows = rows, out->cols = cols;
   out->data = dev, out->bytes = host.size();
   return RT_OK;
+}
+
+rt_status rt_gguf_load_linear(const rt_gguf *g, int64_t idx, rt_linear *out) {
+  return rt_gguf_load_linear_ex(g, idx, 0, out);
 }
 
 rt_status rt_linear_free(rt_linear *l) {

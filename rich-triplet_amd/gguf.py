@@ -24,7 +24,8 @@ TYPE_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4K", Q
 META_U8, META_I8, META_U16, META_I16, META_U32, META_I32, META_F32, META_BOOL, META_STR, META_ARRAY, \
     META_U64, META_I64, META_F64 = range(13)
 
-LINEAR_Q4K, LINEAR_BF16, LINEAR_F32 = 1, 2, 3
+LINEAR_Q4K, LINEAR_BF16, LINEAR_F32, LINEAR_Q6K, LINEAR_Q8_0 = 1, 2, 3, 4, 5
+LOAD_KEEP_PACKED = 1
 
 
 class _Tensor(C.Structure):
@@ -179,8 +180,9 @@ class GgufFile:
 
 class Linear:
     """A weight resident in device memory, as load_linear_from_gguf leaves it:
-    format is LINEAR_Q4K (packed 144-B blocks), LINEAR_BF16 or LINEAR_F32,
-    row-major [rows=out_features, cols=in_features]."""
+    format is LINEAR_Q4K (packed 144-B blocks), LINEAR_BF16, LINEAR_F32, or
+    with keep_packed LINEAR_Q6K / LINEAR_Q8_0 (planar layout), row-major
+    [rows=out_features, cols=in_features]."""
 
     def __init__(self, raw: _Linear):
         self._raw = raw
@@ -202,10 +204,12 @@ class Linear:
             pass
 
 
-def load_linear_from_gguf(gguf: GgufFile, idx: int) -> Linear:
-    """transformer4.rs:1177-1256, then the device upload (metal_decode.rs:1259-1277)."""
+def load_linear_from_gguf(gguf: GgufFile, idx: int, keep_packed: bool = False) -> Linear:
+    """transformer4.rs:1177-1256, then the device upload (metal_decode.rs:1259-1277).
+    keep_packed: Q6_K and Q8_0 stay packed for the native GEMVs instead of
+    widening to BF16."""
     raw = _Linear()
-    check(lib().rt_gguf_load_linear(gguf._h, idx, C.byref(raw)))
+    check(lib().rt_gguf_load_linear_ex(gguf._h, idx, LOAD_KEEP_PACKED if keep_packed else 0, C.byref(raw)))
     return Linear(raw)
 
 

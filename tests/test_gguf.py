@@ -396,3 +396,38 @@ def test_gemv_on_loaded_weights(rt, orc, tmp_path, dev):
         assert np.sqrt(((got - ref) ** 2).sum() / (ref ** 2).sum()) < 1e-4, name
         lin.free()
     g.close()
+
+
+@pytest.mark.gpu
+def test_load_linear_keep_packed_feeds_native_gemvs(rt, orc, tmp_path, dev):
+    """keep_packed: Q6_K and Q8_0 tensors land in the planar device layout
+    (byte-equal to rt.q6k_repack / q8_0_repack of the file bytes) and feed the
+    native GEMVs; other types load as without the flag."""
+    import torch
+    rows, cols = 640, 2560
+    q6k = synth_blocks(orc, GG_Q6_K, rows * cols, 60)
+    q80 = synth_blocks(orc, GG_Q8_0, rows * cols, 61)
+    q4k = orc.synth_q4k(62, rows, cols)
+    path = tmp_path / "packed.gguf"
+    write_gguf(path, [], [("q6k", [cols, rows], GG_Q6_K, q6k), ("q80", [cols, rows], GG_Q8_0, q80),
+                          ("q4k", [cols, rows], GG_Q4_K, q4k)])
+    g = rt.GgufFile(str(path))
+    a = orc.synth_normal(63, cols)
+    x = torch.from_numpy(a).to(dev)
+    cases = (("q6k", 4, rt.q6k_repack(q6k), orc.q6k_dequant(q6k, rows * cols), rt.q6k_gemv),
+             ("q80", 5, rt.q8_0_repack(q80), orc.q8_0_dequant(q80, rows * cols), rt.q8_0_gemv))
+    for name, fmt, planar, deq, gemv in cases:
+        lin = rt.load_linear_from_gguf(g, g.find_tensor(name), keep_packed=True)
+        assert (lin.format, lin.rows, lin.cols, lin.bytes) == (fmt, rows, cols, planar.size), name
+        assert np.array_equal(_download(lin.ptr, lin.bytes), planar), name
+        y = torch.empty(rows, dtype=torch.float32, device=dev)
+        gemv(lin.ptr, x.data_ptr(), y.data_ptr(), rows, cols)
+        torch.cuda.synchronize()
+        ref = deq.reshape(rows, cols).astype(np.float64) @ a.astype(np.float64)
+        got = y.cpu().numpy().astype(np.float64)
+        assert np.sqrt(((got - ref) ** 2).sum() / (ref ** 2).sum()) < 1e-4, name
+        lin.free()
+    lin = rt.load_linear_from_gguf(g, g.find_tensor("q4k"), keep_packed=True)
+    assert lin.format == 1 and np.array_equal(_download(lin.ptr, lin.bytes), q4k)
+    lin.free()
+    g.close()

@@ -164,3 +164,134 @@ def test_q6k_gemv_scaled_and_onehot_inputs(rt, orc, dev):
     assert np.array_equal(y4.cpu().numpy(), 4 * y1.cpu().numpy())
     col = orc.q6k_dequant(src, n * k).reshape(n, k)[:, 1234]
     assert np.allclose(ye.cpu().numpy(), col, rtol=1e-6, atol=0)
+
+
+# ---------------------------------------------------------------------------
+# oracle: per-format projections (CPU)
+# ---------------------------------------------------------------------------
+def test_oracle_proj_gemv_formats(orc):
+    """orc_proj_gemv against float64 products of the pinned dequantisers."""
+    rng = np.random.default_rng(11)
+    rows, cols = 24, 512
+    x = rng.standard_normal(cols).astype(np.float32)
+    q6 = synth_q6k(rng, rows * cols // 256)
+    q8 = synth_q8_0(rng, rows * cols // 32)
+    bf = orc.synth_bf16(12, rows * cols)
+    q4 = orc.synth_q4k(13, rows, cols)
+    cases = [(4, q6, orc.q6k_dequant(q6, rows * cols)), (5, q8, orc.q8_0_dequant(q8, rows * cols)),
+             (2, bf, (bf.astype(np.uint32) << 16).view(np.float32)),
+             (1, q4, orc.q4k_dequant(q4, rows, cols).reshape(-1))]
+    for fmt, w, deq in cases:
+        y = orc.proj_gemv(fmt, w, rows, cols, x)
+        ref = deq.reshape(rows, cols).astype(np.float64) @ x.astype(np.float64)
+        assert rel_l2(y, ref) < 1e-6, fmt
+
+
+# ---------------------------------------------------------------------------
+# decode step with per-projection formats (GPU)
+# ---------------------------------------------------------------------------
+SHAPES = lambda cfg: dict(  # noqa: E731
+    q=(cfg["n_q_heads"] * cfg["head_dim"], cfg["hidden"]), k=(cfg["n_kv_heads"] * cfg["head_dim"], cfg["hidden"]),
+    v=(cfg["n_kv_heads"] * cfg["head_dim"], cfg["hidden"]), o=(cfg["hidden"], cfg["n_q_heads"] * cfg["head_dim"]),
+    gate=(cfg["ffn"], cfg["hidden"]), up=(cfg["ffn"], cfg["hidden"]), down=(cfg["hidden"], cfg["ffn"]))
+
+
+def apply_formats(orc, cfg, layers, plan, seed):
+    """Replace projections by Q6_K / Q8_0 (GGUF block bytes) or BF16 weights;
+    returns the device-side dicts (planar layouts) and their format lists."""
+    rng = np.random.default_rng(seed)
+    shapes = SHAPES(cfg)
+    dev_layers, fmts = [], []
+    for li, L in enumerate(layers):
+        plan_l = plan.get(li, {})
+        L["fmt"] = dict(plan_l)
+        D = dict(L)
+        for p, fmt in plan_l.items():
+            rows, cols = shapes[p]
+            if fmt == 4:
+                L[p] = synth_q6k(rng, rows * cols // 256)
+                D[p] = __import__("conftest").load_pkg().q6k_repack(L[p])
+            elif fmt == 5:
+                L[p] = synth_q8_0(rng, rows * cols // 32)
+                D[p] = __import__("conftest").load_pkg().q8_0_repack(L[p])
+            else:
+                L[p] = orc.synth_bf16(seed + li * 10 + len(p), rows * cols)
+                D[p] = L[p]
+        dev_layers.append(D)
+        fmts.append([plan_l.get(p, 1) for p in ("q", "k", "v", "o", "gate", "up", "down")])
+    return dev_layers, fmts
+
+
+MIXED_PLAN = {0: dict(v=4, down=4), 2: dict(q=5, o=4, gate=2), 3: dict(k=4, up=5), 4: dict(v=2, down=5),
+              5: dict(q=4, k=4, v=4, o=5, gate=4, up=4, down=2)}
+
+
+def mixed_ctx(rt, cfg, dev_layers, fmts, embed, fnorm, ctx, max_seq, layers):
+    d = rt.HipDecodeContext(cfg, max_seq)
+    for i, (D, f) in enumerate(zip(dev_layers, fmts)):
+        d.set_layer(i, D, formats=f)
+        d.sync_kv_from_cpu(i, np.ascontiguousarray(layers[i]["k_cache"][:ctx]),
+                           np.ascontiguousarray(layers[i]["v_cache"][:ctx]), ctx)
+    d.set_embed(embed, fnorm)
+    return d
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("pos", [0, 3, 20])
+def test_mixed_format_decode_matches_oracle(rt, orc, pos):
+    """Q4_K_M-like layers (v, down in Q6_K), a q in Q8_0 (split q/k/v set), a
+    gate in BF16 (split gate/up), and a global layer with every projection
+    outside Q4_K, against the oracle's exact dequantisation."""
+    from test_gpu_decode import tiny
+    from test_oracle import make_model
+    cfg = tiny(2)
+    max_seq = 32
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=pos, seed=7000 + pos)
+    dev_layers, fmts = apply_formats(orc, cfg, layers, MIXED_PLAN, seed=7100 + pos)
+    d = mixed_ctx(rt, cfg, dev_layers, fmts, embed, fnorm, pos, max_seq, layers)
+    got = d.decode_step(11, pos)
+    ref = orc.gemma3_decode_step(cfg, layers, embed, fnorm, token=11, pos=pos)
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, ref) < 1e-3, rel_l2(got, ref)
+    # the next steps replay the captured graph; the batch path runs the same layers
+    for i, tok in enumerate((3, 900)):
+        got = d.decode_step(tok, pos + 1 + i)
+        ref = orc.gemma3_decode_step(cfg, layers, embed, fnorm, token=tok, pos=pos + 1 + i)
+        assert rel_l2(got, ref) < 1e-3
+    batch = d.decode_step_batch([5, 6, 7], pos + 3)
+    for i, tok in enumerate((5, 6, 7)):
+        ref = orc.gemma3_decode_step(cfg, layers, embed, fnorm, token=tok, pos=pos + 3 + i)
+        assert rel_l2(batch[i], ref) < 1e-3, (i, rel_l2(batch[i], ref))
+    with pytest.raises(rt.RtError):
+        d.prefill([1, 2, 3], 0, 0)  # prefill runs Q4_K projections only
+    d.close()
+
+
+@pytest.mark.gpu
+def test_q4_k_m_layout_at_gemma3_4b_shape(rt, orc):
+    """Gemma-3-4B layer shapes with v and down in Q6_K (the Q4_K_M recipe):
+    the specialised Q6_K tiles (K = 2560, 10240) inside the decode graph.  The
+    native result is closer to the exact product than the reference's way of
+    running Q6_K (widened to BF16 at load, transformer4.rs:1233-1242)."""
+    from test_oracle import make_model
+    cfg = dict(rt.GEMMA3_4B, n_layers=2, global_every=2, vocab=4096)
+    ctx, max_seq = 40, 64
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=ctx, seed=7300)
+    plan = {0: dict(v=4, down=4), 1: dict(v=4, down=4)}
+    dev_layers, fmts = apply_formats(orc, cfg, layers, plan, seed=7301)
+    d = mixed_ctx(rt, cfg, dev_layers, fmts, embed, fnorm, ctx, max_seq, layers)
+    got = d.decode_step(17, ctx)
+    import copy
+    widened = copy.deepcopy(layers)
+    shapes = SHAPES(cfg)
+    for L in widened:
+        for p in ("v", "down"):
+            rows, cols = shapes[p]
+            bits = orc.q6k_dequant(L[p], rows * cols).view(np.uint32).astype(np.uint64)
+            L[p] = ((bits + 0x7FFF + ((bits >> 16) & 1)) >> 16).astype(np.uint16)  # f32 -> bf16, RNE
+            L["fmt"][p] = 2
+    ref = orc.gemma3_decode_step(cfg, layers, embed, fnorm, token=17, pos=ctx)
+    ref_bf16 = orc.gemma3_decode_step(cfg, widened, embed, fnorm, token=17, pos=ctx)
+    assert rel_l2(got, ref) < 1e-3, rel_l2(got, ref)
+    assert rel_l2(got, ref) < rel_l2(ref_bf16, ref)
+    d.close()
