@@ -234,6 +234,48 @@ def main() -> int:
         per_shape[name] = {"n": n, "k": k, "us_per_launch": round(us, 3), "GBps": round(byts / us / 1e3, 1),
                            "bytes_per_launch": byts}
         del g
+    # ---------------- Q6_K / Q8_0 kept packed vs widened to BF16 ---------------
+    # Q4_K_M files hold attn_v and ffn_down in Q6_K; the reference widens them
+    # (and Q8_0) to BF16 at load (transformer4.rs:1233-1242).
+    kquant = {}
+    for name, n, k in (("v", KVD, H), ("down", H, F)):
+        x = x_f if name == "down" else x_h
+        y = torch.empty(n, device=dev)
+        nb6, nb8 = n * k // 256, n * k // 32
+        ws = {"q6k": [], "q8_0": [], "bf16": []}
+        for _ in range(L):
+            w6 = torch.randint(0, 256, (nb6 * 210,), dtype=torch.uint8, device=dev, generator=gen)
+            w6[nb6 * 208:].view(torch.float16).copy_((torch.randn(nb6, device=dev, generator=gen) * 0.02).abs())
+            w8 = torch.randint(0, 256, (nb8 * 34,), dtype=torch.uint8, device=dev, generator=gen)
+            w8[n * k:].view(torch.float16).copy_((torch.randn(nb8, device=dev, generator=gen) * 0.02).abs())
+            ws["q6k"].append(w6)
+            ws["q8_0"].append(w8)
+            ws["bf16"].append((torch.randn(n * k, device=dev, generator=gen) * 0.02).to(torch.bfloat16).view(torch.int16))
+        for fmt, fn, wbytes in (("q6k", rt.q6k_gemv, nb6 * 210), ("q8_0", rt.q8_0_gemv, nb8 * 34),
+                                ("bf16", rt.bf16_gemv, n * k * 2)):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=cap):
+                s = torch.cuda.current_stream()
+                for w in ws[fmt]:
+                    fn(w, x, y, n, k, stream=s)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(reps):
+                g.replay()
+            b.record()
+            torch.cuda.synchronize()
+            us = a.elapsed_time(b) * 1e3 / (reps * L)
+            byts = gemv_bytes(n, k, wbytes)
+            kquant[f"{fmt}_{name}"] = {"n": n, "k": k, "us_per_launch": round(us, 3),
+                                       "GBps": round(byts / us / 1e3, 1), "bytes_per_launch": byts}
+            del g
+        del ws
+        log(f"{name} {n}x{k}: Q6_K {kquant['q6k_' + name]['us_per_launch']} us, "
+            f"Q8_0 {kquant['q8_0_' + name]['us_per_launch']} us, BF16 (reference widening) "
+            f"{kquant['bf16_' + name]['us_per_launch']} us")
     dom = per_shape["gate"]
     roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(dom["GBps"] / PEAK_HBM_GBS, 4), "traffic": measured_traffic(),
@@ -395,6 +437,7 @@ def main() -> int:
                    "bytes_per_step": step_bytes, "parallelism": "single GPU"},
         "roofline": roofline,
         "per_shape": per_shape,
+        "kquant_gemv": kquant,
         "decode": decode,
         "gemm": gemm,
         "cpu_baseline": cpu,
