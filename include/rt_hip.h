@@ -122,6 +122,12 @@ rt_status rt_q8_0_dequant_f32(const void *w, size_t n_elem, float *out, void *st
 rt_status rt_q6k_gemv(const void *w, const float *x, float *y, int64_t n, int64_t k, void *stream);
 rt_status rt_q8_0_gemv(const void *w, const float *x, float *y, int64_t n, int64_t k, void *stream);
 
+/* gemv_q4k_t_batch (metal_decode.rs:459-521): c[m][n] = a[m][k] . W[n][k]
+ * for m = 1..8 rows (the speculative verify batch), reading the weights once
+ * for all rows (int8 matrix cores); device pointers, a and w 16-byte
+ * aligned, k % 256 == 0. */
+rt_status rt_q4k_gemv_batch(const void *w, const float *a, float *c, int64_t m, int64_t n, int64_t k, void *stream);
+
 /* Host drop-in for Q4KMat::matmul_q4k_t_exact (autograd2.rs:1490-1625):
  * a is [m, k] f32, out receives [m, rows] f32.  m == 1 takes the GEMV path, as
  * matmul_q4k_t does (autograd2.rs:1440-1443).  Weights are cached like

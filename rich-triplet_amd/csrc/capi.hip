@@ -15,6 +15,7 @@
 
 #include "../../include/rt_hip.h"
 #include "rt_capi_util.hpp"
+#include "q4k_gemv_mb.hpp"
 #include "rt_kernels.hpp"
 
 namespace rt {
@@ -157,6 +158,25 @@ rt_status rt_q4k_gemm_bf16(const uint16_t *a, const void *w, float *c, int64_t m
 
 rt_status rt_q4k_gemm_f32(const float *a, const void *w, float *c, int64_t m, int64_t n, int64_t k, void *stream) {
   return q4k_gemm_entry("rt_q4k_gemm_f32", a, false, w, c, m, n, k, stream);
+}
+
+// gemv_q4k_t_batch (metal_decode.rs:459-521): c[m][n] = a[m][k] . W[n][k]
+// for m <= 8 rows, one pass over the weights.
+rt_status rt_q4k_gemv_batch(const void *w, const float *a, float *c, int64_t m, int64_t n, int64_t k, void *stream) {
+  rt_status st = check_gemv_shape("rt_q4k_gemv_batch", w, a, c, n, k, 256);
+  if (st != RT_OK) return st;
+  if (m < 1 || m > kMbMaxRows) return set_error(RT_EINVAL, "rt_q4k_gemv_batch: m=%lld outside [1, 8]", (long long)m);
+  const size_t stage = (mb_stage_bytes((int)k) + 255) & ~size_t(255);
+  void *ws = nullptr;
+  st = gemm_workspace(stage + mb_part_bytes((int)n, (int)k), &ws);
+  if (st != RT_OK) return st;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = launch_mb_stage(a, (int)m, (int)k, ws, s);
+  if (e == hipSuccess) {
+    MbMat mat{static_cast<const uint8_t *>(w), c, (int)n, 0, 0};
+    e = launch_q4k_gemv_mb(&mat, 1, (int)m, (int)k, ws, reinterpret_cast<float *>(static_cast<char *>(ws) + stage), s);
+  }
+  return hip_error(e, "rt_q4k_gemv_batch");
 }
 
 }  // extern "C"

@@ -79,14 +79,38 @@ struct PrefillBuffers {
   float *k = nullptr, *v = nullptr;     // [cap][n_kv_heads*head_dim]
   float *g = nullptr, *u = nullptr;     // [cap][ffn]
   void *ws = nullptr;                   // Q4_K GEMM workspace
+  void *mb_stage = nullptr;             // batched-GEMV staging (rows <= 8)
+  float *mb_part = nullptr;             // batched-GEMV partial sums
 };
 size_t prefill_gemm_workspace_bytes(const DecodeShape &s, int cap);
-// Rows p0 .. p0+n-1 of the prompt (tokens and cos/sin tables already in b).
-// Local layers attend keys [max(lo_fixed, pos + 1 - window), pos] of each row
-// (window 0: no per-row window).  With `logits`, the last row's final norm and
-// lm_head land in a.logits (a.x2 / a.dn are overwritten).
-hipError_t enqueue_prefill_chunk(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers,
-                                 const PrefillBuffers &b, int p0, int n, int lo_fixed, int window, bool logits,
+// Batched-GEMV staging and partial-sum bytes for every projection set.
+size_t rows_mb_stage_bytes(const DecodeShape &s);
+size_t rows_mb_part_bytes(const DecodeShape &s);
+
+// n rows through every layer: rows p0 .. p0+n-1 (p0 from *p0_dev when that
+// is set), token of row t at tokens[t*tok_stride], its cos/sin tables at
+// cs + t*cs_stride (local | global).  Local layers attend keys
+// [max(lo_fixed, pos + 1 - window), pos] of each row (window 0: no per-row
+// window).  Projections run on the Q4_K GEMM, or with mb (n <= 8) on the
+// batched GEMV.  Logits: none, the last row's into a.logits (a.x2 / a.dn are
+// overwritten), or every row's final norm into xn_b and logits into logits_b.
+struct RowsPlan {
+  enum { kNone = 0, kLastRow = 1, kEveryRow = 2 };
+  int n = 0, p0 = 0;
+  const int *p0_dev = nullptr;
+  const int *tokens = nullptr;
+  int tok_stride = 1;
+  const float *cs = nullptr;
+  int cs_stride = 0;
+  int lo_fixed = 0, window = 0;
+  bool mb = false;
+  int logits = kNone;
+  float *xn_b = nullptr, *logits_b = nullptr;
+};
+hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers, const PrefillBuffers &b,
+                        const RowsPlan &plan, hipStream_t stream);
+// Batched lm_head of m <= 8 final-normed rows xn[m][hidden] into logits_b[m][vocab].
+hipError_t enqueue_lm_head_batch(const DecodeShape &s, const DecodeArgs &a, const float *xn, float *logits_b, int m,
                                  hipStream_t stream);
 
 }  // namespace rt

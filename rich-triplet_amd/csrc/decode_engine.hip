@@ -44,6 +44,8 @@ struct rt_decode {
   bool graph_enabled = true;
   bool graph_dirty = true;
   PrefillBuffers pf;                     // rt_decode_prefill scratch (grown on demand)
+  PrefillBuffers vb;                     // decode_step_batch rows (kMaxBatch), allocated at create
+  bool all_q4k = true;                   // every projection Q4_K: batched-GEMV verify path
   int pf_chunk = 4096;                   // rows per prefill chunk (~180 KB of scratch per row at Gemma-3-4B)
   std::vector<void *> pf_owned;
   int *pf_tokens_host = nullptr;         // pinned staging: [pf.cap] tokens, [pf.cap][2][head_dim] cos/sin
@@ -168,6 +170,17 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
     TRY(fbuf((size_t)c.n_q_heads * nch * D, &a.part_o));
     TRY(fbuf((size_t)kMaxBatch * H, &d->xn_batch));
     TRY(fbuf((size_t)kMaxBatch * c.vocab, &d->logits_batch));
+    {
+      PrefillBuffers &vb = d->vb;
+      const size_t R = kMaxBatch;
+      TRY(fbuf(R * H, &vb.hid)); TRY(fbuf(R * H, &vb.x2)); TRY(fbuf(R * H, &vb.xn)); TRY(fbuf(R * H, &vb.o));
+      TRY(fbuf(R * H, &vb.dn)); TRY(fbuf(R * QD, &vb.q)); TRY(fbuf(R * QD, &vb.attn)); TRY(fbuf(R * KVD, &vb.k));
+      TRY(fbuf(R * KVD, &vb.v)); TRY(fbuf(R * F, &vb.g)); TRY(fbuf(R * F, &vb.u));
+      void *q = nullptr;
+      TRY(dalloc(d, rows_mb_stage_bytes(s), &q)); vb.mb_stage = q;
+      TRY(fbuf(rows_mb_part_bytes(s) / 4, &vb.mb_part));
+      vb.cap = kMaxBatch;
+    }
     a.params = d->params_dev;
     a.embed_scale = std::sqrt((float)c.hidden);   // transformer4.rs:2092
     a.eps = c.eps;
@@ -295,6 +308,9 @@ rt_status rt_decode_set_layer_formats(rt_decode *d, int32_t layer, const rt_gemm
   B(wup, w->up, proj_bytes(formats[kProjUp], F, H), const uint8_t *);
   B(wdown, w->down, proj_bytes(formats[kProjDown], H, F), const uint8_t *);
   for (int p = 0; p < 7; ++p) L.fmt[p] = formats[p];
+  d->all_q4k = true;
+  for (const LayerArgs &X : d->layers)
+    for (int p = 0; p < 7; ++p) d->all_q4k = d->all_q4k && X.fmt[p] == RT_LINEAR_Q4K;
   B(g_in, w->in_norm, H * 4, const float *);
   B(g_post_attn, w->post_attn_norm, H * 4, const float *);
   B(g_pre_ffn, w->pre_ffn_norm, H * 4, const float *);
@@ -446,7 +462,24 @@ rt_status rt_decode_step_batch_async(rt_decode *d, const int32_t *tokens, int32_
   for (int i = 0; i < m; ++i) fill_slot(d, i, tokens[i], start_position + i);
   if ((st = params_send(d, m)) != RT_OK) return st;
   return run_graph(d, d->exec_batch[m], [&] {
-    return enqueue_decode_batch(d->shape, d->args, d->layers.data(), m, d->xn_batch, d->logits_batch, d->stream);
+    if (!d->all_q4k)  // per-token layer kernels (any projection format)
+      return enqueue_decode_batch(d->shape, d->args, d->layers.data(), m, d->xn_batch, d->logits_batch, d->stream);
+    // all rows through each layer at once: batched GEMVs (one pass over the
+    // weights), the causal row attention, a batched lm_head
+    const int slot = param_slot_floats(d->cfg.head_dim);
+    RowsPlan plan;
+    plan.n = m;
+    plan.p0_dev = d->params_dev + 1;
+    plan.tokens = d->params_dev;
+    plan.tok_stride = slot;
+    plan.cs = reinterpret_cast<const float *>(d->params_dev) + kParamRopeLocal;
+    plan.cs_stride = slot;
+    plan.window = d->cfg.sliding_window;  // every row attends its own window, as a decode step does
+    plan.mb = true;
+    plan.logits = RowsPlan::kEveryRow;
+    plan.xn_b = d->xn_batch;
+    plan.logits_b = d->logits_batch;
+    return enqueue_rows(d->shape, d->args, d->layers.data(), d->vb, plan, d->stream);
   }, "rt_decode_step_batch");
 }
 
@@ -521,6 +554,9 @@ static rt_status prefill_reserve(rt_decode *d, int cap) {
   PF_GET(u, float, rows * F);
 #undef PF_GET
   if ((st = get(prefill_gemm_workspace_bytes(d->shape, cap), &b.ws)) != RT_OK) return st;
+  if ((st = get(rows_mb_stage_bytes(d->shape), &b.mb_stage)) != RT_OK) return st;
+  if ((st = get(rows_mb_part_bytes(d->shape), &p)) != RT_OK) return st;
+  b.mb_part = static_cast<float *>(p);
   e = hipHostMalloc((void **)&d->pf_tokens_host, rows * sizeof(int), hipHostMallocDefault);
   if (e == hipSuccess) e = hipHostMalloc((void **)&d->pf_cs_host, rows * 2 * D * sizeof(float), hipHostMallocDefault);
   if (e != hipSuccess) return hip_error(e, "rt_decode_prefill hipHostMalloc");
@@ -600,9 +636,19 @@ rt_status rt_decode_prefill(rt_decode *d, const int32_t *tokens, int32_t n, int3
     if (e == hipSuccess)
       e = hipMemcpyAsync(d->pf.cs, d->pf_cs_host, (size_t)cn * 2 * D * sizeof(float), hipMemcpyHostToDevice,
                          d->stream);
-    if (e == hipSuccess)
-      e = enqueue_prefill_chunk(d->shape, d->args, d->layers.data(), d->pf, start_position + c0, cn, lo_fixed,
-                                window, c0 + cn == n, d->stream);
+    if (e == hipSuccess) {
+      RowsPlan plan;
+      plan.n = cn;
+      plan.p0 = start_position + c0;
+      plan.tokens = d->pf.tokens;
+      plan.cs = d->pf.cs;
+      plan.cs_stride = 2 * D;
+      plan.lo_fixed = lo_fixed;
+      plan.window = window;
+      plan.mb = cn <= kMaxBatch;  // a few rows: one pass over the weights beats the GEMM's tiles
+      plan.logits = c0 + cn == n ? RowsPlan::kLastRow : RowsPlan::kNone;
+      e = enqueue_rows(d->shape, d->args, d->layers.data(), d->pf, plan, d->stream);
+    }
   }
   if (e == hipSuccess && logits_host)
     e = hipMemcpyAsync(logits_host, d->args.logits, (size_t)d->cfg.vocab * 4, hipMemcpyDeviceToHost, d->stream);

@@ -802,13 +802,17 @@ hipError_t enqueue_decode_batch(const DecodeShape &s, const DecodeArgs &a, const
       hipLaunchKernelGGL((k_final_norm<512>), dim3(1), dim3(256), 0, l.s, at, ls[s.n_layers - 1], xn + (size_t)t * 512);
     l.check();
   }
-  if (l.err == hipSuccess) {
-    if (s.hidden == 2560)
-      hipLaunchKernelGGL((k_lmhead_batch<2560>), dim3(512), dim3(256), 0, l.s, a.embed, xn, logits_b, s.vocab, m);
-    else
-      hipLaunchKernelGGL((k_lmhead_batch<512>), dim3(512), dim3(256), 0, l.s, a.embed, xn, logits_b, s.vocab, m);
-    l.check();
-  }
+  return l.err == hipSuccess ? enqueue_lm_head_batch(s, a, xn, logits_b, m, stream) : l.err;
+}
+
+hipError_t enqueue_lm_head_batch(const DecodeShape &s, const DecodeArgs &a, const float *xn, float *logits_b, int m,
+                                 hipStream_t stream) {
+  Launch l{stream};
+  if (s.hidden == 2560)
+    hipLaunchKernelGGL((k_lmhead_batch<2560>), dim3(512), dim3(256), 0, l.s, a.embed, xn, logits_b, s.vocab, m);
+  else
+    hipLaunchKernelGGL((k_lmhead_batch<512>), dim3(512), dim3(256), 0, l.s, a.embed, xn, logits_b, s.vocab, m);
+  l.check();
   return l.err;
 }
 

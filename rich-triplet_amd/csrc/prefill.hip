@@ -24,6 +24,7 @@
 
 #include "decode.hpp"
 #include "gemma3_math.hpp"
+#include "q4k_gemv_mb.hpp"
 #include "rt_device.hpp"
 #include "rt_kernels.hpp"
 
@@ -40,9 +41,10 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 // Row kernels
 // ---------------------------------------------------------------------------
 // x[t] = bf16(E[token_t]) * sqrt(hidden)   (transformer4.rs:2106-2121)
-__global__ __launch_bounds__(256) void k_pf_embed(const int *__restrict__ tokens, const uint16_t *__restrict__ E,
-                                                  float scale, float *__restrict__ x, int H) {
-  const uint16_t *row = E + (size_t)tokens[blockIdx.x] * H;
+__global__ __launch_bounds__(256) void k_pf_embed(const int *__restrict__ tokens, int tok_stride,
+                                                  const uint16_t *__restrict__ E, float scale, float *__restrict__ x,
+                                                  int H) {
+  const uint16_t *row = E + (size_t)tokens[(size_t)blockIdx.x * tok_stride] * H;
   float *out = x + (size_t)blockIdx.x * H;
   for (int c = threadIdx.x; c < H; c += 256) out[c] = mul_nc(bf16_lo((uint32_t)row[c]), scale);
 }
@@ -95,17 +97,22 @@ __global__ __launch_bounds__(256) void k_pf_norm(const float *__restrict__ base,
 
 // One wave per (row, head): q heads in place, k heads into the cache row
 // p0 + t (with the matching v row copied next to it), as the decode step's
-// k_attn does for its single row (transformer4.rs:1912-1923).
+// k_attn does for its single row (transformer4.rs:1912-1923).  Row t's
+// cos/sin table starts at cs + t*cs_stride (+ head_dim for global layers);
+// p0 comes from *p0_dev when that is set (graph replays).
 template <int D>
 __global__ __launch_bounds__(256) void k_pf_qk_rope(float *q, const float *__restrict__ k, const float *__restrict__ v,
                                                     const float *__restrict__ g_q, const float *__restrict__ g_k,
-                                                    const float *__restrict__ cs, int cs_off, float *__restrict__ kc,
-                                                    float *__restrict__ vc, int p0, int n, int nq, int nkv, float eps) {
+                                                    const float *__restrict__ cs, int cs_stride, int cs_off,
+                                                    float *__restrict__ kc, float *__restrict__ vc, int p0,
+                                                    const int *__restrict__ p0_dev, int n, int nq, int nkv,
+                                                    float eps) {
   const int heads = nq + nkv;
   const int item = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
   if (item >= n * heads) return;  // whole waves
+  if (p0_dev) p0 = p0_dev[0];
   const int t = item / heads, h = item % heads;
-  const float *c = cs + (size_t)t * 2 * D + cs_off;
+  const float *c = cs + (size_t)t * cs_stride + cs_off;
   if (h < nq) {
     float *qr = q + ((size_t)t * nq + h) * D;
     norm_rope_head<D>(qr, g_q, c, eps, qr);
@@ -158,6 +165,7 @@ struct PfAttnArgs {
   int p0, n, n_kv_heads;
   int lo_fixed, window;
   float scale;
+  const int *p0_dev;  // when set, p0 = *p0_dev (graph replays)
 };
 
 template <int D>
@@ -200,6 +208,7 @@ RT_DEV f32x4_t mfma3(u32x4_t ahi, u32x4_t alo, u32x4_t bhi, u32x4_t blo, f32x4_t
 template <int D, int G>
 __global__ __launch_bounds__(256) void k_pf_attn(const float *__restrict__ q, const float *__restrict__ kc,
                                                  const float *__restrict__ vc, float *__restrict__ out, PfAttnArgs p) {
+  if (p.p0_dev) p.p0 = p.p0_dev[0];
   constexpr int KB = kPfKeys;
   constexpr int DS = D / 32;                  // k steps of the score MFMA
   constexpr int DT = D / 16;                  // 16-dim tiles of the output
@@ -387,11 +396,19 @@ size_t prefill_gemm_workspace_bytes(const DecodeShape &s, int cap) {
   return m;
 }
 
-hipError_t enqueue_prefill_chunk(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers,
-                                 const PrefillBuffers &b, int p0, int n, int lo_fixed, int window, bool logits,
-                                 hipStream_t st) {
+size_t rows_mb_stage_bytes(const DecodeShape &s) {
+  return mb_stage_bytes(std::max({s.hidden, s.ffn, s.n_q_heads * s.head_dim}));
+}
+
+size_t rows_mb_part_bytes(const DecodeShape &s) {
+  const int H = s.hidden, F = s.ffn, QD = s.n_q_heads * s.head_dim, KVD = s.n_kv_heads * s.head_dim;
+  return std::max({mb_part_bytes(QD + 2 * KVD, H), mb_part_bytes(H, QD), mb_part_bytes(2 * F, H), mb_part_bytes(H, F)});
+}
+
+hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers, const PrefillBuffers &b,
+                        const RowsPlan &plan, hipStream_t st) {
   const int H = s.hidden, F = s.ffn, D = s.head_dim, nq = s.n_q_heads, nkv = s.n_kv_heads;
-  const int QD = nq * D, KVD = nkv * D, G = nq / nkv;
+  const int QD = nq * D, KVD = nkv * D, G = nq / nkv, n = plan.n;
   hipError_t e = hipSuccess;
 #define PF_CHECK(x)               \
   do {                            \
@@ -404,54 +421,71 @@ hipError_t enqueue_prefill_chunk(const DecodeShape &s, const DecodeArgs &a, cons
     e = (x);                      \
     if (e != hipSuccess) return e; \
   } while (0)
-  auto gemm = [&](const float *A, const uint8_t *W, float *C, int N, int K) {
-    return launch_q4k_gemm(A, false, W, C, n, N, K, b.ws, st);
+  // projections: the GEMM, or for a few rows the batched GEMV (one pass over
+  // the weights for all rows); up to three matrices share one input
+  auto proj = [&](const float *A, int K, std::initializer_list<MbMat> mats) -> hipError_t {
+    if (plan.mb) {
+      hipError_t r = launch_mb_stage(A, n, K, b.mb_stage, st);
+      return r == hipSuccess ? launch_q4k_gemv_mb(mats.begin(), (int)mats.size(), n, K, b.mb_stage, b.mb_part, st) : r;
+    }
+    for (const MbMat &m : mats) {
+      hipError_t r = launch_q4k_gemm(A, false, m.w, m.y, n, m.n, K, b.ws, st);
+      if (r != hipSuccess) return r;
+    }
+    return hipSuccess;
   };
-  PF_CHECK(hipLaunchKernelGGL(k_pf_embed, dim3(n), dim3(256), 0, st, b.tokens, a.embed, a.embed_scale, b.hid, H));
+  PF_CHECK(hipLaunchKernelGGL(k_pf_embed, dim3(n), dim3(256), 0, st, plan.tokens, plan.tok_stride, a.embed,
+                              a.embed_scale, b.hid, H));
   for (int li = 0; li < s.n_layers; ++li) {
     const LayerArgs &L = layers[li];
     if (li == 0)
       PF_CHECK(hipLaunchKernelGGL(k_pf_norm<false>, dim3(n), dim3(256), 0, st, nullptr, b.hid, nullptr, L.g_in,
                                   nullptr, b.xn, H, a.eps));
-    PF_TRY(gemm(b.xn, L.wq, b.q, QD, H));
-    PF_TRY(gemm(b.xn, L.wk, b.k, KVD, H));
-    PF_TRY(gemm(b.xn, L.wv, b.v, KVD, H));
+    PF_TRY(proj(b.xn, H, {MbMat{L.wq, b.q, QD, 0, 0}, MbMat{L.wk, b.k, KVD, 0, 0}, MbMat{L.wv, b.v, KVD, 0, 0}}));
     const int items = n * (nq + nkv);
     const int cs_off = L.global ? D : 0;
     if (D == 256)
       PF_CHECK(hipLaunchKernelGGL(k_pf_qk_rope<256>, dim3((items + 3) / 4), dim3(256), 0, st, b.q, b.k, b.v, L.g_q,
-                                  L.g_k, b.cs, cs_off, L.kc, L.vc, p0, n, nq, nkv, a.eps));
+                                  L.g_k, plan.cs, plan.cs_stride, cs_off, L.kc, L.vc, plan.p0, plan.p0_dev, n, nq,
+                                  nkv, a.eps));
     else
       PF_CHECK(hipLaunchKernelGGL(k_pf_qk_rope<128>, dim3((items + 3) / 4), dim3(256), 0, st, b.q, b.k, b.v, L.g_q,
-                                  L.g_k, b.cs, cs_off, L.kc, L.vc, p0, n, nq, nkv, a.eps));
+                                  L.g_k, plan.cs, plan.cs_stride, cs_off, L.kc, L.vc, plan.p0, plan.p0_dev, n, nq,
+                                  nkv, a.eps));
     PfAttnArgs pa;
-    pa.p0 = p0;
+    pa.p0 = plan.p0;
+    pa.p0_dev = plan.p0_dev;
     pa.n = n;
     pa.n_kv_heads = nkv;
-    pa.lo_fixed = L.global ? 0 : lo_fixed;
-    pa.window = L.global ? 0 : window;
+    pa.lo_fixed = L.global ? 0 : plan.lo_fixed;
+    pa.window = L.global ? 0 : plan.window;
     pa.scale = a.attn_scale;
     const dim3 agrid((n * G + 63) / 64, nkv);
     if (D == 256) PF_TRY(launch_pf_attn<256>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa));
     else PF_TRY(launch_pf_attn<128>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa));
-    PF_TRY(gemm(b.attn, L.wo, b.o, H, QD));
+    PF_TRY(proj(b.attn, QD, {MbMat{L.wo, b.o, H, 0, 0}}));
     PF_CHECK(hipLaunchKernelGGL(k_pf_norm<true>, dim3(n), dim3(256), 0, st, b.hid, b.o, L.g_post_attn, L.g_pre_ffn,
                                 b.x2, b.xn, H, a.eps));
-    PF_TRY(gemm(b.xn, L.wgate, b.g, F, H));
-    PF_TRY(gemm(b.xn, L.wup, b.u, F, H));
+    PF_TRY(proj(b.xn, H, {MbMat{L.wgate, b.g, F, 0, 0}, MbMat{L.wup, b.u, F, 0, 0}}));
     const size_t n4 = (size_t)n * F / 4;
     const unsigned eg = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
     PF_CHECK(hipLaunchKernelGGL(k_pf_gelu_mul, dim3(eg), dim3(256), 0, st, b.g, b.u, b.g, n4));
-    PF_TRY(gemm(b.g, L.wdown, b.dn, H, F));
+    PF_TRY(proj(b.g, F, {MbMat{L.wdown, b.dn, H, 0, 0}}));
     if (li + 1 < s.n_layers)
       PF_CHECK(hipLaunchKernelGGL(k_pf_norm<true>, dim3(n), dim3(256), 0, st, b.x2, b.dn, L.g_post_ffn,
                                   layers[li + 1].g_in, b.hid, b.xn, H, a.eps));
   }
-  if (logits) {
+  const LayerArgs &last = layers[s.n_layers - 1];
+  if (plan.logits == RowsPlan::kLastRow) {
     // the last row's final residual, final norm and lm_head (transformer4.rs:2131-2139)
     PF_TRY(hipMemcpyAsync(a.x2, b.x2 + (size_t)(n - 1) * H, (size_t)H * 4, hipMemcpyDeviceToDevice, st));
     PF_TRY(hipMemcpyAsync(a.dn, b.dn + (size_t)(n - 1) * H, (size_t)H * 4, hipMemcpyDeviceToDevice, st));
-    PF_TRY(enqueue_lm_head(s, a, layers[s.n_layers - 1], st));
+    PF_TRY(enqueue_lm_head(s, a, last, st));
+  } else if (plan.logits == RowsPlan::kEveryRow) {
+    // every row's final residual and final norm, then one pass over the embedding
+    PF_CHECK(hipLaunchKernelGGL(k_pf_norm<true>, dim3(n), dim3(256), 0, st, b.x2, b.dn, last.g_post_ffn, a.g_final,
+                                b.hid, plan.xn_b, H, a.eps));
+    PF_TRY(enqueue_lm_head_batch(s, a, plan.xn_b, plan.logits_b, n, st));
   }
 #undef PF_CHECK
 #undef PF_TRY

@@ -190,9 +190,10 @@ def test_gemma3_4b_shape_decode_step_matches_oracle(rt, orc, dev):
 @pytest.mark.parametrize("m", [1, 3, 8])
 def test_batch_matches_sequential_and_oracle(rt, orc, m):
     """M tokens at consecutive positions: the window of 8 slides inside the
-    batch and the global layer sees every earlier batch token.  The batch runs
-    the same layer kernels as M single steps (identical hidden states and K/V
-    rows); only its lm_head differs (MFMA on bf16-split activations)."""
+    batch and the global layer sees every earlier batch token.  The batch
+    runs every layer for all M rows at once (batched GEMVs on the int8
+    matrix cores, the causal row attention, a batched lm_head), so it agrees
+    with M single steps to the digit rounding of the two GEMV paths."""
     import copy
     cfg = tiny(2)
     max_seq, ctx = 48, 9
@@ -207,16 +208,17 @@ def test_batch_matches_sequential_and_oracle(rt, orc, m):
     ref = np.stack([orc.gemma3_decode_step(cfg, olayers, embed, fnorm, token=t, pos=ctx + i)
                     for i, t in enumerate(toks)])
     for i in range(m):
-        assert rel_l2(got[i], seq[i]) < 1e-5, i
+        assert rel_l2(got[i], seq[i]) < 2e-4, (i, rel_l2(got[i], seq[i]))
         assert rel_l2(got[i], ref[i]) < LOGITS_TOL, i
     for li in range(cfg["n_layers"]):
         kb, vb = d_batch.kv_ptrs(li)
         ks, vs = d_seq.kv_ptrs(li)
         kvd = cfg["n_kv_heads"] * cfg["head_dim"]
         n = (ctx + m) * kvd * 4
-        hb, hs = _read_dev(kb, n), _read_dev(ks, n)
-        assert np.array_equal(hb, hs), li
-        assert np.array_equal(_read_dev(vb, n), _read_dev(vs, n)), li
+        hb, hs = _read_dev(kb, n).view(np.float32), _read_dev(ks, n).view(np.float32)
+        assert np.array_equal(hb[:ctx * kvd], hs[:ctx * kvd]), li  # rows before the batch untouched
+        assert rel_l2(hb, hs) < 2e-4, li
+        assert rel_l2(_read_dev(vb, n).view(np.float32), _read_dev(vs, n).view(np.float32)) < 2e-4, li
     d_batch.close()
     d_seq.close()
 
@@ -262,8 +264,10 @@ def test_batch_rejects_bad_calls(rt, orc):
 
 
 def test_gemma3_4b_shape_batch_matches_sequential(rt, orc, dev):
-    """The K=2560 batched lm_head at the full vocabulary: three tokens against
-    three single steps (whose path the oracle test above checks)."""
+    """The batched path at the full Gemma-3-4B shape (34 layers, vocab
+    262144, ctx 1024): three tokens against three single steps (whose path
+    the oracle test above checks); the two GEMV paths differ only in their
+    activation digits."""
     cfg = dict(rt.GEMMA3_4B)
     ctx = 1024
     max_seq = ctx + 8
@@ -300,6 +304,6 @@ def test_gemma3_4b_shape_batch_matches_sequential(rt, orc, dev):
         ref = d_s.decode_step(t, ctx + i)
         err = rel_l2(got[i], ref)
         print(f"gemma3-4b batch token {i}: rel-L2 vs single step {err:.2e}")
-        assert err < 1e-5
+        assert err < 1e-3
         assert int(np.argmax(got[i])) == int(np.argmax(ref))
     d_s.close()

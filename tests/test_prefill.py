@@ -207,9 +207,10 @@ def test_gpu_prefill_matches_oracle(rt, orc, group, mode, T):
 
 @pytest.mark.gpu
 def test_gpu_prefill_chunks_and_continuation(rt, orc):
-    """Chunked prefill (7 rows per chunk) and a prefill continued at
-    start_position > 0 give the single-call result (sliding rule), and the
-    next decode step sees the prefilled cache."""
+    """Chunked prefill (7 rows per chunk: chunks of up to 8 rows run their
+    projections on the batched GEMV, larger ones on the GEMM) and a prefill
+    continued at start_position > 0 give the single-call result (sliding
+    rule), and the next decode step sees the prefilled cache."""
     cfg = tiny(2)
     T, max_seq = 30, 40
     layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=0, seed=6100)
@@ -222,8 +223,8 @@ def test_gpu_prefill_chunks_and_continuation(rt, orc):
     d3 = gpu_ctx(rt, cfg, layers, embed, fnorm, max_seq)
     d3.prefill(toks[:17], 0, 1)
     cont = d3.prefill(toks[17:], 17, 1)
-    assert rel_l2(chunked, full) < 1e-5
-    assert rel_l2(cont, full) < 1e-5
+    assert rel_l2(chunked, full) < LOGITS_TOL  # batched GEMV (16-bit digits) vs GEMM (f16 operands)
+    assert rel_l2(cont, full) < 1e-5           # both halves on the GEMM
     for li in range(cfg["n_layers"]):
         k1, v1 = read_kv(d1, cfg, li, T)
         k3, v3 = read_kv(d3, cfg, li, T)
