@@ -81,7 +81,14 @@ struct PrefillBuffers {
   void *ws = nullptr;                   // Q4_K GEMM workspace
   void *mb_stage = nullptr;             // batched-GEMV staging (rows <= 8)
   float *mb_part = nullptr;             // batched-GEMV partial sums
+  float *attn_ml = nullptr, *attn_o = nullptr;  // key-split attention partials, or null
+  int attn_rows = 0;                             // rows the partials hold
 };
+// Key splits of the attention of a few rows: at most this many per KV head.
+constexpr int kPfMaxSplits = 64;
+inline size_t attn_part_floats(const DecodeShape &s, int rows, bool o) {
+  return (size_t)kPfMaxSplits * rows * s.n_q_heads * (o ? s.head_dim : 2);
+}
 size_t prefill_gemm_workspace_bytes(const DecodeShape &s, int cap);
 // Batched-GEMV staging and partial-sum bytes for every projection set.
 size_t rows_mb_stage_bytes(const DecodeShape &s);
@@ -103,6 +110,7 @@ struct RowsPlan {
   const float *cs = nullptr;
   int cs_stride = 0;
   int lo_fixed = 0, window = 0;
+  int max_pos = 0;  // bound on p0 + n (sizes the key split of a device-side p0)
   bool mb = false;
   int logits = kNone;
   float *xn_b = nullptr, *logits_b = nullptr;

@@ -179,6 +179,9 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
       void *q = nullptr;
       TRY(dalloc(d, rows_mb_stage_bytes(s), &q)); vb.mb_stage = q;
       TRY(fbuf(rows_mb_part_bytes(s) / 4, &vb.mb_part));
+      TRY(fbuf(attn_part_floats(s, kMaxBatch, false), &vb.attn_ml));
+      TRY(fbuf(attn_part_floats(s, kMaxBatch, true), &vb.attn_o));
+      vb.attn_rows = kMaxBatch;
       vb.cap = kMaxBatch;
     }
     a.params = d->params_dev;
@@ -475,6 +478,7 @@ rt_status rt_decode_step_batch_async(rt_decode *d, const int32_t *tokens, int32_
     plan.cs = reinterpret_cast<const float *>(d->params_dev) + kParamRopeLocal;
     plan.cs_stride = slot;
     plan.window = d->cfg.sliding_window;  // every row attends its own window, as a decode step does
+    plan.max_pos = d->cfg.max_seq;
     plan.mb = true;
     plan.logits = RowsPlan::kEveryRow;
     plan.xn_b = d->xn_batch;
@@ -557,6 +561,13 @@ static rt_status prefill_reserve(rt_decode *d, int cap) {
   if ((st = get(rows_mb_stage_bytes(d->shape), &b.mb_stage)) != RT_OK) return st;
   if ((st = get(rows_mb_part_bytes(d->shape), &p)) != RT_OK) return st;
   b.mb_part = static_cast<float *>(p);
+  // key-split partials for chunks of up to 64 rows (one attention row block)
+  const int split_rows = std::min(cap, 64);
+  if ((st = get(attn_part_floats(d->shape, split_rows, false) * 4, &p)) != RT_OK) return st;
+  b.attn_ml = static_cast<float *>(p);
+  if ((st = get(attn_part_floats(d->shape, split_rows, true) * 4, &p)) != RT_OK) return st;
+  b.attn_o = static_cast<float *>(p);
+  b.attn_rows = split_rows;
   e = hipHostMalloc((void **)&d->pf_tokens_host, rows * sizeof(int), hipHostMallocDefault);
   if (e == hipSuccess) e = hipHostMalloc((void **)&d->pf_cs_host, rows * 2 * D * sizeof(float), hipHostMallocDefault);
   if (e != hipSuccess) return hip_error(e, "rt_decode_prefill hipHostMalloc");
@@ -645,6 +656,7 @@ rt_status rt_decode_prefill(rt_decode *d, const int32_t *tokens, int32_t n, int3
       plan.cs_stride = 2 * D;
       plan.lo_fixed = lo_fixed;
       plan.window = window;
+      plan.max_pos = start_position + c0 + cn;
       plan.mb = cn <= kMaxBatch;  // a few rows: one pass over the weights beats the GEMM's tiles
       plan.logits = c0 + cn == n ? RowsPlan::kLastRow : RowsPlan::kNone;
       e = enqueue_rows(d->shape, d->args, d->layers.data(), d->pf, plan, d->stream);

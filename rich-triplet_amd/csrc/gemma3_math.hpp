@@ -35,11 +35,11 @@ RT_DEV float sumsq4(float4 v) { return v.x * v.x + v.y * v.y + v.z * v.z + v.w *
 // shared by the heads) followed by NeoX RoPE (apply_rope_at_offset,
 // 2742-2772) of one head of D values, by one wave.  Lane owns pairs
 // i = lane*P + p (p < P) with partners i + D/2; cs[i] = cos and
-// cs[D/2 + i] = sin of the pair's angle.  src may equal dst: every lane reads
-// its own elements before it writes them.
-template <int D>
-RT_DEV void norm_rope_head(const float *src, const float *__restrict__ gamma, const float *__restrict__ cs,
-                           float eps, float *dst) {
+// cs[D/2 + i] = sin of the pair's angle; src(i) loads element i.  The source
+// may be dst: every lane reads its own elements before it writes them.
+template <int D, class Load>
+RT_DEV void norm_rope_head_ld(Load src, const float *__restrict__ gamma, const float *__restrict__ cs, float eps,
+                              float *dst) {
   constexpr int P = D / 128;
   const int lane = threadIdx.x & 63;
   float x0[P], x1[P];
@@ -47,8 +47,8 @@ RT_DEV void norm_rope_head(const float *src, const float *__restrict__ gamma, co
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int i = lane * P + p;
-    x0[p] = src[i];
-    x1[p] = src[i + D / 2];
+    x0[p] = src(i);
+    x1[p] = src(i + D / 2);
     ss += x0[p] * x0[p] + x1[p] * x1[p];
   }
   const float rinv = rms_inv_from_sumsq(wave_sum(ss), 1.0f / (float)D, eps);
@@ -62,6 +62,12 @@ RT_DEV void norm_rope_head(const float *src, const float *__restrict__ gamma, co
     dst[i] = a0 * c - a1 * sn;
     dst[i + D / 2] = a0 * sn + a1 * c;
   }
+}
+
+template <int D>
+RT_DEV void norm_rope_head(const float *src, const float *__restrict__ gamma, const float *__restrict__ cs,
+                           float eps, float *dst) {
+  norm_rope_head_ld<D>([&](int i) { return src[i]; }, gamma, cs, eps, dst);
 }
 
 }  // namespace rt

@@ -49,26 +49,28 @@ __global__ __launch_bounds__(256) void k_pf_embed(const int *__restrict__ tokens
   for (int c = threadIdx.x; c < H; c += 256) out[c] = mul_nc(bf16_lo((uint32_t)row[c]), scale);
 }
 
-// One row per workgroup, H <= 4096 (H % 4 == 0).
+// One row per workgroup, H <= 4096 (H % 64 == 0).
 //   RESID:  x = base + rms(add)(1 + g_add);  x_out = x;  xn = rms(x)(1 + g_out)
 //   !RESID: x = add;                                     xn = rms(x)(1 + g_out)
+// `add` may be split-K partial sums.  With st_dig, xn is also staged as the
+// input of a batched GEMV.
 template <bool RESID>
-__global__ __launch_bounds__(256) void k_pf_norm(const float *__restrict__ base, const float *__restrict__ add,
+__global__ __launch_bounds__(256) void k_pf_norm(const float *__restrict__ base, RowsIn add,
                                                  const float *__restrict__ g_add, const float *__restrict__ g_out,
                                                  float *__restrict__ x_out, float *__restrict__ xn_out, int H,
-                                                 float eps) {
+                                                 float eps, int8_t *__restrict__ st_dig) {
   constexpr int PER = 4;
   __shared__ float red[4];
-  const size_t off = (size_t)blockIdx.x * (H / 4);
+  const int t = (int)blockIdx.x;
+  const size_t off = (size_t)t * (H / 4);
   const int F4 = H / 4;
   const float inv_k = 1.0f / (float)H;
-  const float4 *a4 = reinterpret_cast<const float4 *>(add) + off;
   float4 x[PER];
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int f = threadIdx.x + i * 256;
-    x[i] = f < F4 ? a4[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+    x[i] = f < F4 ? rows_in4(add, t, 4 * f) : make_float4(0.f, 0.f, 0.f, 0.f);
     ss += sumsq4(x[i]);
   }
   if constexpr (RESID) {
@@ -88,10 +90,14 @@ __global__ __launch_bounds__(256) void k_pf_norm(const float *__restrict__ base,
   }
   const float rx = rms_inv_from_sumsq(block_sum<256>(ss, red), inv_k, eps);
   float4 *xn = reinterpret_cast<float4 *>(xn_out) + off;
+  float *st_stats = st_dig ? mb_stats(st_dig, H) : nullptr;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int f = threadIdx.x + i * 256;
-    if (f < F4) xn[f] = norm4(x[i], rx, reinterpret_cast<const float4 *>(g_out)[f]);
+    if (i * 256 >= F4) break;  // block-uniform
+    const float4 v = norm4(x[i], rx, reinterpret_cast<const float4 *>(g_out)[min(f, F4 - 1)]);
+    if (f < F4) xn[f] = v;
+    if (st_dig) mb_stage4(st_dig, st_stats, t, min(f, F4 - 1) >> 4, f & 15, v, f < F4);  // 16 lanes per chunk
   }
 }
 
@@ -101,7 +107,7 @@ __global__ __launch_bounds__(256) void k_pf_norm(const float *__restrict__ base,
 // cos/sin table starts at cs + t*cs_stride (+ head_dim for global layers);
 // p0 comes from *p0_dev when that is set (graph replays).
 template <int D>
-__global__ __launch_bounds__(256) void k_pf_qk_rope(float *q, const float *__restrict__ k, const float *__restrict__ v,
+__global__ __launch_bounds__(256) void k_pf_qk_rope(RowsIn q, RowsIn k, RowsIn v, float *q_out,
                                                     const float *__restrict__ g_q, const float *__restrict__ g_k,
                                                     const float *__restrict__ cs, int cs_stride, int cs_off,
                                                     float *__restrict__ kc, float *__restrict__ vc, int p0,
@@ -114,24 +120,32 @@ __global__ __launch_bounds__(256) void k_pf_qk_rope(float *q, const float *__res
   const int t = item / heads, h = item % heads;
   const float *c = cs + (size_t)t * cs_stride + cs_off;
   if (h < nq) {
-    float *qr = q + ((size_t)t * nq + h) * D;
-    norm_rope_head<D>(qr, g_q, c, eps, qr);
+    norm_rope_head_ld<D>([&](int i) { return rows_in1(q, t, h * D + i); }, g_q, c, eps,
+                         q_out + ((size_t)t * nq + h) * D);
   } else {
     const int kh = h - nq;
-    const size_t src = ((size_t)t * nkv + kh) * D, dst = ((size_t)(p0 + t) * nkv + kh) * D;
-    norm_rope_head<D>(k + src, g_k, c, eps, kc + dst);
-    for (int i = threadIdx.x & 63; i < D; i += 64) vc[dst + i] = v[src + i];
+    const size_t dst = ((size_t)(p0 + t) * nkv + kh) * D;
+    norm_rope_head_ld<D>([&](int i) { return rows_in1(k, t, kh * D + i); }, g_k, c, eps, kc + dst);
+    for (int i = threadIdx.x & 63; i < D; i += 64) vc[dst + i] = rows_in1(v, t, kh * D + i);
   }
 }
 
-// h = gelu_tanh(g) * u  (Gemma3Mlp::forward, transformer4.rs:328-334)
-// h may alias g (each element is read before it is written, by one thread).
-__global__ __launch_bounds__(256) void k_pf_gelu_mul(const float *g, const float *__restrict__ u, float *h,
-                                                     size_t n4) {
+// h = gelu_tanh(g) * u  (Gemma3Mlp::forward, transformer4.rs:328-334) over
+// n rows of F; g and u may be split-K partial sums, h may alias g (each
+// element is read before it is written, by one thread).  With st_dig, h is
+// also staged as the input of a batched GEMV.
+__global__ __launch_bounds__(256) void k_pf_gelu_mul(RowsIn g, RowsIn u, float *h, int n, int F,
+                                                     int8_t *__restrict__ st_dig) {
+  const int f4 = F / 4;  // a multiple of 16: the 16 lanes of a chunk stay in one row
+  const size_t n4 = (size_t)n * f4;
+  float *st_stats = st_dig ? mb_stats(st_dig, F) : nullptr;
   for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
-    const float4 a = reinterpret_cast<const float4 *>(g)[i], b = reinterpret_cast<const float4 *>(u)[i];
-    reinterpret_cast<float4 *>(h)[i] = make_float4(mul_nc(gelu_tanh(a.x), b.x), mul_nc(gelu_tanh(a.y), b.y),
-                                                   mul_nc(gelu_tanh(a.z), b.z), mul_nc(gelu_tanh(a.w), b.w));
+    const int t = (int)(i / f4), c4 = (int)(i % f4);
+    const float4 a = rows_in4(g, t, 4 * c4), b = rows_in4(u, t, 4 * c4);
+    const float4 r = make_float4(mul_nc(gelu_tanh(a.x), b.x), mul_nc(gelu_tanh(a.y), b.y),
+                                 mul_nc(gelu_tanh(a.z), b.z), mul_nc(gelu_tanh(a.w), b.w));
+    reinterpret_cast<float4 *>(h)[i] = r;
+    if (st_dig) mb_stage4(st_dig, st_stats, t, c4 >> 4, c4 & 15, r, true);
   }
 }
 
@@ -166,6 +180,12 @@ struct PfAttnArgs {
   int lo_fixed, window;
   float scale;
   const int *p0_dev;  // when set, p0 = *p0_dev (graph replays)
+  // Key split (few rows, long key ranges): workgroup z takes stages
+  // [z*split_stages, (z+1)*split_stages) of its key range and writes the
+  // unnormalised (max, sum, O) of each column for k_pf_attn_combine.
+  int split_stages;   // 0: no split, the kernel writes the output itself
+  float *part_ml;     // [splits][n*n_q_heads][2]
+  float *part_o;      // [splits][n*n_q_heads][D]
 };
 
 template <int D>
@@ -294,13 +314,18 @@ __global__ __launch_bounds__(256) void k_pf_attn(const float *__restrict__ q, co
   for (int i = 0; i < DT; ++i) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
-  load_stage(key_first);
+  int k_begin = key_first, k_end = key_last;
+  if (p.split_stages) {
+    k_begin = key_first + (int)blockIdx.z * p.split_stages * KB;
+    k_end = min(key_last, k_begin + p.split_stages * KB - 1);
+  }
+  load_stage(k_begin);
 #pragma unroll 1
-  for (int k0 = key_first; k0 <= key_last; k0 += KB) {
+  for (int k0 = k_begin; k0 <= k_end; k0 += KB) {
     __syncthreads();  // every wave is done with the previous stage
     store_stage();
     __syncthreads();
-    if (k0 + KB <= key_last) load_stage(k0 + KB);  // lands during this stage's MFMAs
+    if (k0 + KB <= k_end) load_stage(k0 + KB);  // lands during this stage's MFMAs
     if (!wave_live || k0 > wkey_hi || k0 + KB - 1 < wkey_lo) continue;  // wave-uniform
 
     f32x4_t sc[2];
@@ -358,7 +383,18 @@ __global__ __launch_bounds__(256) void k_pf_attn(const float *__restrict__ q, co
     }
   }
 
-  if (col_ok) {
+  if (col_ok && p.split_stages) {
+    // partial of this key split (an empty split leaves max -inf, sum 0, O 0)
+    const size_t cidx = (size_t)blockIdx.z * p.n * p.n_kv_heads * G + (size_t)t * p.n_kv_heads * G + hq;
+    if (g == 0) {
+      p.part_ml[2 * cidx] = m_run;
+      p.part_ml[2 * cidx + 1] = l_run;
+    }
+    float *po = p.part_o + cidx * D + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      *reinterpret_cast<float4 *>(po + 16 * dt) = make_float4(o[dt][0], o[dt][1], o[dt][2], o[dt][3]);
+  } else if (col_ok) {
     const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
     float *orow = out + (size_t)t * qd + (size_t)hq * D + 4 * g;
 #pragma unroll
@@ -368,15 +404,54 @@ __global__ __launch_bounds__(256) void k_pf_attn(const float *__restrict__ q, co
   }
 }
 
+// Merge of the key splits of every (row, head) column:
+//   out = sum_s O_s e^(m_s - M) / sum_s l_s e^(m_s - M),  M = max_s m_s
+// (0 for a column with no key at all, as the reference's empty rows).
+template <int D>
+__global__ __launch_bounds__(D) void k_pf_attn_combine(const float *__restrict__ part_ml,
+                                                       const float *__restrict__ part_o, float *__restrict__ out,
+                                                       int ncols, int splits, int nq, int8_t *__restrict__ st_dig) {
+  static_assert(D >= kPfMaxSplits, "one lane of wave 0 per split");
+  __shared__ float w_lds[kPfMaxSplits];
+  __shared__ float l_lds;
+  const int col = (int)blockIdx.x, d = (int)threadIdx.x;
+  if (d < 64) {  // wave 0: split z = lane
+    const bool live = d < splits;
+    const float m = live ? part_ml[2 * ((size_t)d * ncols + col)] : -INFINITY;
+    const float l = live ? part_ml[2 * ((size_t)d * ncols + col) + 1] : 0.f;
+    const float M = wave_max(m);
+    const float w = (m == -INFINITY) ? 0.f : expf(m - M);
+    if (live) w_lds[d] = w;
+    const float L = wave_sum(l * w);
+    if (d == 0) l_lds = L;
+  }
+  __syncthreads();
+  float O = 0.f;
+#pragma unroll 8
+  for (int z = 0; z < splits; ++z) O = fmaf(part_o[((size_t)z * ncols + col) * D + d], w_lds[z], O);
+  const float L = l_lds;
+  const float r = L > 0.f ? O / L : 0.f;
+  out[(size_t)col * D + d] = r;
+  if (st_dig) {  // element (col % nq)*D + d of row col / nq; one 64-element chunk per wave
+    const int t = col / nq, e = (col % nq) * D + d;
+    mb_stage1(st_dig, mb_stats(st_dig, nq * D), t, e >> 6, r);
+  }
+}
+
 template <int D>
 hipError_t launch_pf_attn(int G, dim3 grid, hipStream_t st, const float *q, const float *kc, const float *vc,
-                          float *out, const PfAttnArgs &p) {
+                          float *out, const PfAttnArgs &p, int8_t *st_dig) {
   switch (G) {
     case 1: hipLaunchKernelGGL((k_pf_attn<D, 1>), grid, dim3(256), 0, st, q, kc, vc, out, p); break;
     case 2: hipLaunchKernelGGL((k_pf_attn<D, 2>), grid, dim3(256), 0, st, q, kc, vc, out, p); break;
     case 4: hipLaunchKernelGGL((k_pf_attn<D, 4>), grid, dim3(256), 0, st, q, kc, vc, out, p); break;
     default: return hipErrorInvalidValue;
   }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !p.split_stages) return e;
+  const int ncols = p.n * p.n_kv_heads * G;
+  hipLaunchKernelGGL((k_pf_attn_combine<D>), dim3(ncols), dim3(D), 0, st, p.part_ml, p.part_o, out, ncols,
+                     (int)grid.z, p.n_kv_heads * G, st_dig);
   return hipGetLastError();
 }
 
@@ -421,16 +496,25 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
     e = (x);                      \
     if (e != hipSuccess) return e; \
   } while (0)
-  // projections: the GEMM, or for a few rows the batched GEMV (one pass over
-  // the weights for all rows); up to three matrices share one input
-  auto proj = [&](const float *A, int K, std::initializer_list<MbMat> mats) -> hipError_t {
+  // Projections: the GEMM on plain inputs, or (plan.mb, n <= 8) the batched
+  // GEMV.  On the batched path each producer kernel also stages its output
+  // as the next GEMV's input (stage != null), and the GEMV leaves split-K
+  // partial sums that the consumer adds while reading (views).
+  int8_t *stage = plan.mb ? static_cast<int8_t *>(b.mb_stage) : nullptr;
+  RowsIn vq, vk, vv, vo, vg, vu, vd;
+  auto proj = [&](const float *A, int K, std::initializer_list<MbMat> mats, std::initializer_list<RowsIn *> views) {
     if (plan.mb) {
-      hipError_t r = launch_mb_stage(A, n, K, b.mb_stage, st);
-      return r == hipSuccess ? launch_q4k_gemv_mb(mats.begin(), (int)mats.size(), n, K, b.mb_stage, b.mb_part, st) : r;
+      RowsIn out[3];
+      hipError_t r = launch_q4k_gemv_mb(mats.begin(), (int)mats.size(), n, K, b.mb_stage, b.mb_part, st, out);
+      int i = 0;
+      for (RowsIn *v : views) *v = out[i++];
+      return r;
     }
+    int i = 0;
     for (const MbMat &m : mats) {
       hipError_t r = launch_q4k_gemm(A, false, m.w, m.y, n, m.n, K, b.ws, st);
       if (r != hipSuccess) return r;
+      *views.begin()[i++] = rows_plain(m.y, m.n);
     }
     return hipSuccess;
   };
@@ -439,19 +523,20 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
   for (int li = 0; li < s.n_layers; ++li) {
     const LayerArgs &L = layers[li];
     if (li == 0)
-      PF_CHECK(hipLaunchKernelGGL(k_pf_norm<false>, dim3(n), dim3(256), 0, st, nullptr, b.hid, nullptr, L.g_in,
-                                  nullptr, b.xn, H, a.eps));
-    PF_TRY(proj(b.xn, H, {MbMat{L.wq, b.q, QD, 0, 0}, MbMat{L.wk, b.k, KVD, 0, 0}, MbMat{L.wv, b.v, KVD, 0, 0}}));
+      PF_CHECK(hipLaunchKernelGGL(k_pf_norm<false>, dim3(n), dim3(256), 0, st, nullptr, rows_plain(b.hid, H), nullptr,
+                                  L.g_in, nullptr, b.xn, H, a.eps, stage));
+    PF_TRY(proj(b.xn, H, {MbMat{L.wq, b.q, QD, 0, 0}, MbMat{L.wk, b.k, KVD, 0, 0}, MbMat{L.wv, b.v, KVD, 0, 0}},
+                {&vq, &vk, &vv}));
     const int items = n * (nq + nkv);
     const int cs_off = L.global ? D : 0;
     if (D == 256)
-      PF_CHECK(hipLaunchKernelGGL(k_pf_qk_rope<256>, dim3((items + 3) / 4), dim3(256), 0, st, b.q, b.k, b.v, L.g_q,
-                                  L.g_k, plan.cs, plan.cs_stride, cs_off, L.kc, L.vc, plan.p0, plan.p0_dev, n, nq,
-                                  nkv, a.eps));
+      PF_CHECK(hipLaunchKernelGGL(k_pf_qk_rope<256>, dim3((items + 3) / 4), dim3(256), 0, st, vq, vk, vv, b.q,
+                                  L.g_q, L.g_k, plan.cs, plan.cs_stride, cs_off, L.kc, L.vc, plan.p0, plan.p0_dev, n,
+                                  nq, nkv, a.eps));
     else
-      PF_CHECK(hipLaunchKernelGGL(k_pf_qk_rope<128>, dim3((items + 3) / 4), dim3(256), 0, st, b.q, b.k, b.v, L.g_q,
-                                  L.g_k, plan.cs, plan.cs_stride, cs_off, L.kc, L.vc, plan.p0, plan.p0_dev, n, nq,
-                                  nkv, a.eps));
+      PF_CHECK(hipLaunchKernelGGL(k_pf_qk_rope<128>, dim3((items + 3) / 4), dim3(256), 0, st, vq, vk, vv, b.q,
+                                  L.g_q, L.g_k, plan.cs, plan.cs_stride, cs_off, L.kc, L.vc, plan.p0, plan.p0_dev, n,
+                                  nq, nkv, a.eps));
     PfAttnArgs pa;
     pa.p0 = plan.p0;
     pa.p0_dev = plan.p0_dev;
@@ -460,32 +545,44 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
     pa.lo_fixed = L.global ? 0 : plan.lo_fixed;
     pa.window = L.global ? 0 : plan.window;
     pa.scale = a.attn_scale;
-    const dim3 agrid((n * G + 63) / 64, nkv);
-    if (D == 256) PF_TRY(launch_pf_attn<256>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa));
-    else PF_TRY(launch_pf_attn<128>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa));
-    PF_TRY(proj(b.attn, QD, {MbMat{L.wo, b.o, H, 0, 0}}));
-    PF_CHECK(hipLaunchKernelGGL(k_pf_norm<true>, dim3(n), dim3(256), 0, st, b.hid, b.o, L.g_post_attn, L.g_pre_ffn,
-                                b.x2, b.xn, H, a.eps));
-    PF_TRY(proj(b.xn, H, {MbMat{L.wgate, b.g, F, 0, 0}, MbMat{L.wup, b.u, F, 0, 0}}));
+    pa.split_stages = 0;
+    pa.part_ml = b.attn_ml;
+    pa.part_o = b.attn_o;
+    dim3 agrid((n * G + 63) / 64, nkv);
+    if (agrid.x == 1 && b.attn_ml && n <= b.attn_rows) {
+      // one row block: split the keys so about 256 workgroups share them
+      const int span = L.global || (plan.window <= 0 && plan.lo_fixed <= 0) ? plan.max_pos
+                       : std::min(plan.max_pos, (plan.window > 0 ? plan.window : plan.max_pos) + n + 32);
+      const int stages = (span + 31) / 32 + 1;
+      pa.split_stages = (stages + kPfMaxSplits - 1) / kPfMaxSplits;
+      agrid.z = (stages + pa.split_stages - 1) / pa.split_stages;
+    }
+    if (stage && !pa.split_stages) return hipErrorInvalidValue;  // the batched path stages in the merge kernel
+    if (D == 256) PF_TRY(launch_pf_attn<256>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa, stage));
+    else PF_TRY(launch_pf_attn<128>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa, stage));
+    PF_TRY(proj(b.attn, QD, {MbMat{L.wo, b.o, H, 0, 0}}, {&vo}));
+    PF_CHECK(hipLaunchKernelGGL(k_pf_norm<true>, dim3(n), dim3(256), 0, st, b.hid, vo, L.g_post_attn, L.g_pre_ffn,
+                                b.x2, b.xn, H, a.eps, stage));
+    PF_TRY(proj(b.xn, H, {MbMat{L.wgate, b.g, F, 0, 0}, MbMat{L.wup, b.u, F, 0, 0}}, {&vg, &vu}));
     const size_t n4 = (size_t)n * F / 4;
     const unsigned eg = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
-    PF_CHECK(hipLaunchKernelGGL(k_pf_gelu_mul, dim3(eg), dim3(256), 0, st, b.g, b.u, b.g, n4));
-    PF_TRY(proj(b.g, F, {MbMat{L.wdown, b.dn, H, 0, 0}}));
+    PF_CHECK(hipLaunchKernelGGL(k_pf_gelu_mul, dim3(eg), dim3(256), 0, st, vg, vu, b.g, n, F, stage));
+    PF_TRY(proj(b.g, F, {MbMat{L.wdown, b.dn, H, 0, 0}}, {&vd}));
     if (li + 1 < s.n_layers)
-      PF_CHECK(hipLaunchKernelGGL(k_pf_norm<true>, dim3(n), dim3(256), 0, st, b.x2, b.dn, L.g_post_ffn,
-                                  layers[li + 1].g_in, b.hid, b.xn, H, a.eps));
+      PF_CHECK(hipLaunchKernelGGL(k_pf_norm<true>, dim3(n), dim3(256), 0, st, b.x2, vd, L.g_post_ffn,
+                                  layers[li + 1].g_in, b.hid, b.xn, H, a.eps, stage));
   }
   const LayerArgs &last = layers[s.n_layers - 1];
-  if (plan.logits == RowsPlan::kLastRow) {
-    // the last row's final residual, final norm and lm_head (transformer4.rs:2131-2139)
-    PF_TRY(hipMemcpyAsync(a.x2, b.x2 + (size_t)(n - 1) * H, (size_t)H * 4, hipMemcpyDeviceToDevice, st));
-    PF_TRY(hipMemcpyAsync(a.dn, b.dn + (size_t)(n - 1) * H, (size_t)H * 4, hipMemcpyDeviceToDevice, st));
-    PF_TRY(enqueue_lm_head(s, a, last, st));
-  } else if (plan.logits == RowsPlan::kEveryRow) {
-    // every row's final residual and final norm, then one pass over the embedding
-    PF_CHECK(hipLaunchKernelGGL(k_pf_norm<true>, dim3(n), dim3(256), 0, st, b.x2, b.dn, last.g_post_ffn, a.g_final,
-                                b.hid, plan.xn_b, H, a.eps));
-    PF_TRY(enqueue_lm_head_batch(s, a, plan.xn_b, plan.logits_b, n, st));
+  if (plan.logits != RowsPlan::kNone) {
+    // the final residual and final norm of every row (transformer4.rs:2131-2139,
+    // 2370-2380), then the tied lm_head of the last row or of every row
+    float *xn_out = plan.logits == RowsPlan::kEveryRow ? plan.xn_b : b.xn;
+    PF_CHECK(hipLaunchKernelGGL(k_pf_norm<true>, dim3(n), dim3(256), 0, st, b.x2, vd, last.g_post_ffn, a.g_final,
+                                b.hid, xn_out, H, a.eps, nullptr));
+    if (plan.logits == RowsPlan::kEveryRow)
+      PF_TRY(enqueue_lm_head_batch(s, a, plan.xn_b, plan.logits_b, n, st));
+    else
+      PF_TRY(enqueue_lm_head_batch(s, a, b.xn + (size_t)(n - 1) * H, a.logits, 1, st));
   }
 #undef PF_CHECK
 #undef PF_TRY

@@ -27,8 +27,8 @@
 //   acc[m] += d*sv*delta_m * (256 C1 + C0) - dmin*mv * sum_m(sub-block)
 // and lanes (r, 0) and (r, 1) add their halves at the end.  A wave owns 16
 // weight rows (two B operands against one A), a workgroup 64 rows and a
-// slice of K (whole super-blocks); slices beyond one write partial sums that
-// k_mb_reduce adds in slice order.
+// slice of one or two super-blocks; with several slices each writes partial
+// sums that k_mb_reduce adds in slice order.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -45,102 +45,89 @@ __global__ __launch_bounds__(256) void k_mb_stage(const float *__restrict__ x, i
                                                   int8_t *__restrict__ dig, float *__restrict__ stats) {
   const int nchunk = k / 64;
   const int ci = (int)blockIdx.x * 16 + (int)(threadIdx.x >> 4), q = (int)(threadIdx.x & 15);
-  const int row = (int)blockIdx.y;  // 0..7
+  const int row = (int)blockIdx.y;  // 0..7; rows m..7 are staged as zeros
   const int c = min(ci, nchunk - 1);
   const float4 v = row < m ? *reinterpret_cast<const float4 *>(x + (size_t)row * k + 64 * c + 4 * q)
                            : make_float4(0.f, 0.f, 0.f, 0.f);
-  const uint32_t ax = f32_bits(v.x) & 0x7FFFFFFFu, ay = f32_bits(v.y) & 0x7FFFFFFFu;
-  const uint32_t az = f32_bits(v.z) & 0x7FFFFFFFu, aw = f32_bits(v.w) & 0x7FFFFFFFu;
-  uint32_t mb = max(max(ax, ay), max(az, aw));
-  mb = max(mb, dpp_u32<0xB1>(mb));
-  mb = max(mb, dpp_u32<0x4E>(mb));
-  mb = max(mb, dpp_u32<0x141>(mb));
-  mb = max(mb, dpp_u32<0x140>(mb));
-  // max < 2^e, e = biased exponent - 126; s = 32639 * 2^-e stays a normal
-  // float for e >= -111 (smaller chunks lose digits instead of overflowing)
-  const int e = max((int)(mb >> 23) - 126, -111);
-  const float s = bits_f32(f32_bits(32639.0f) - ((uint32_t)e << 23));
-  const float delta = bits_f32(f32_bits(1.0f / 32639.0f) + ((uint32_t)e << 23));
-  const float magic = 12583040.0f;  // 1.5*2^23 + 128
-  const uint32_t b0 = f32_bits(fmaf(v.x, s, magic)), b1 = f32_bits(fmaf(v.y, s, magic));
-  const uint32_t b2 = f32_bits(fmaf(v.z, s, magic)), b3 = f32_bits(fmaf(v.w, s, magic));
-  const uint32_t p01 = __builtin_amdgcn_perm(b1, b0, 0x05010400u);  // b0.0 b1.0 b0.1 b1.1
-  const uint32_t p23 = __builtin_amdgcn_perm(b3, b2, 0x05010400u);
-  const uint32_t d0 = __builtin_amdgcn_perm(p23, p01, 0x05040100u) ^ 0x80808080u;  // (X+128 mod 256) - 128
-  const uint32_t d1 = __builtin_amdgcn_perm(p23, p01, 0x07060302u);                // floor((X+128)/256)
-  float sum = (v.x + v.y) + (v.z + v.w);
-  sum += dpp<0xB1>(sum);
-  sum += dpp<0x4E>(sum);
-  sum += dpp<0x141>(sum);  // 8 lanes = one 32-element sub-block
-  if (ci < nchunk) {
-    int8_t *base = dig + ((size_t)c * 8 + row) * 128;
-    *reinterpret_cast<uint32_t *>(base + 4 * q) = d0;
-    *reinterpret_cast<uint32_t *>(base + 64 + 4 * q) = d1;
-    float *st = stats + ((size_t)c * 8 + row) * 4;
-    if (q == 0) {
-      st[0] = delta;
-      st[1] = sum;
-      st[3] = 0.f;
-    }
-    if (q == 8) st[2] = sum;
-  }
+  mb_stage4(dig, stats, row, c, q, v, ci < nchunk);
 }
 
-template <int RPW>
+template <int SB>
 __global__ __launch_bounds__(256) void k_q4k_gemv_mb(MbArgs p) {
-  constexpr int NG = RPW / 8;  // B operands (8-row groups) per wave
+  // A workgroup: 64 rows (16 per wave, two B operands of 8 rows) times a
+  // slice of SB super-blocks.  The slice's activation digits and stats are
+  // copied to LDS once; every weight load of the slice is issued before the
+  // first MFMA, so the many small workgroups hide each other's latency.
+  constexpr int CH = 4 * SB;  // chunks in the slice
+  __shared__ __attribute__((aligned(16))) int8_t a_lds[CH * 1024];
+  __shared__ __attribute__((aligned(16))) float4 st_lds[CH * 8];
   const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
   const int j = lane & 15, g = lane >> 4, r = j >> 1, h = j & 1;
-  // matrix of this row block
   int rb = (int)blockIdx.x, mi = 0;
   while (mi + 1 < p.nmat && rb >= p.mat[mi].row_blocks) rb -= p.mat[mi++].row_blocks;
   const MbMat &M = p.mat[mi];
   const int nb = p.k / 256, slice = (int)blockIdx.y;
-  const int sb0 = slice * nb / p.ksplit, sb1 = (slice + 1) * nb / p.ksplit;
+  const int sb0 = slice * SB;  // the launcher makes SB divide nb
   const size_t row_bytes = (size_t)nb * kQ4KBlockBytes;
-  int row[NG];
-  const uint8_t *wrow[NG];
+  int row[2];
+  const uint8_t *wp[2];
 #pragma unroll
-  for (int gi = 0; gi < NG; ++gi) {
-    row[gi] = rb * 4 * RPW + wave * RPW + 8 * gi + r;
-    wrow[gi] = M.w + (size_t)min(row[gi], M.n - 1) * row_bytes;  // rows past n: masked at the store
+  for (int gi = 0; gi < 2; ++gi) {
+    row[gi] = rb * 64 + wave * 16 + 8 * gi + r;
+    wp[gi] = M.w + (size_t)min(row[gi], M.n - 1) * row_bytes + (size_t)sb0 * kQ4KBlockBytes;
   }
   const bool carries = (g >> 1) == h;  // this lane's k-slots lie in sub-block half h
-  const int qoff = 16 * (g & 1);
+  const int qoff = 16 + 16 * (g & 1);
+  // weights of the whole slice
+  uint4 hd[2][SB], qw[2][SB][4];
+#pragma unroll
+  for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+    for (int b = 0; b < SB; ++b) {
+      hd[gi][b] = *reinterpret_cast<const uint4 *>(wp[gi] + b * kQ4KBlockBytes);
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc)
+        qw[gi][b][cc] = carries ? *reinterpret_cast<const uint4 *>(wp[gi] + b * kQ4KBlockBytes + qoff + 32 * cc)
+                                : make_uint4(0u, 0u, 0u, 0u);
+    }
+  // activations of the slice: CH KB of digits, CH*8 stats
+  {
+    const uint4 *src = reinterpret_cast<const uint4 *>(p.dig + (size_t)sb0 * 4 * 1024);
+    uint4 *dst = reinterpret_cast<uint4 *>(a_lds);
+#pragma unroll
+    for (int i = (int)threadIdx.x; i < CH * 64; i += 256) dst[i] = src[i];
+    const float4 *ssrc = reinterpret_cast<const float4 *>(p.stats) + (size_t)sb0 * 4 * 8;
+    for (int i = (int)threadIdx.x; i < CH * 8; i += 256) st_lds[i] = ssrc[i];
+  }
+  __syncthreads();
   const uint32_t m4 = opaque_u32(0x0F0F0F0Fu);
-  float acc[NG][2] = {};
-  const int8_t *dig = p.dig + j * 64 + 16 * g;  // row m = j/2, digit j%2
-  const float4 *stats = reinterpret_cast<const float4 *>(p.stats) + 2 * g;
-
-#pragma unroll 1
-  for (int sb = sb0; sb < sb1; ++sb) {
-    uint4 hd[NG];
+  float acc[2][2] = {};
 #pragma unroll
-    for (int gi = 0; gi < NG; ++gi) hd[gi] = *reinterpret_cast<const uint4 *>(wrow[gi] + (size_t)sb * kQ4KBlockBytes);
-    float dsv[NG][4], dmv[NG][4];
+  for (int b = 0; b < SB; ++b) {
+    float dsv[2][4], dmv[2][4];
 #pragma unroll
-    for (int gi = 0; gi < NG; ++gi) {
-      const float d = half_bits_to_f32(hd[gi].x & 0xFFFFu), dm = half_bits_to_f32(hd[gi].x >> 16);
+    for (int gi = 0; gi < 2; ++gi) {
+      const float d = half_bits_to_f32(hd[gi][b].x & 0xFFFFu), dm = half_bits_to_f32(hd[gi][b].x >> 16);
 #pragma unroll
       for (int cc = 0; cc < 4; ++cc) {
         uint32_t sv, mv;
-        q4k_scale_min(hd[gi].y, hd[gi].z, hd[gi].w, 2 * cc + h, sv, mv);
+        q4k_scale_min(hd[gi][b].y, hd[gi][b].z, hd[gi][b].w, 2 * cc + h, sv, mv);
         dsv[gi][cc] = d * (float)sv;
         dmv[gi][cc] = dm * (float)mv;
       }
     }
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) {
-      const int c = sb * 4 + cc;
-      const i32x4_t A = *reinterpret_cast<const i32x4_t *>(dig + (size_t)c * 1024);
-      const float4 st0 = stats[(size_t)c * 8], st1 = stats[(size_t)c * 8 + 1];  // rows 2g, 2g+1
+      const int c = 4 * b + cc;
+      const i32x4_t A = *reinterpret_cast<const i32x4_t *>(a_lds + c * 1024 + j * 64 + 16 * g);
+      const float4 st0 = st_lds[c * 8 + 2 * g], st1 = st_lds[c * 8 + 2 * g + 1];  // rows 2g, 2g+1
 #pragma unroll
-      for (int gi = 0; gi < NG; ++gi) {
-        const uint4 qw = *reinterpret_cast<const uint4 *>(wrow[gi] + (size_t)sb * kQ4KBlockBytes + 16 + 32 * cc + qoff);
-        const uint32_t w4[4] = {qw.x, qw.y, qw.z, qw.w};
+      for (int gi = 0; gi < 2; ++gi) {
+        const uint4 q = qw[gi][b][cc];
+        const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
         i32x4_t B;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) B[t] = carries ? (int)((h ? w4[t] >> 4 : w4[t]) & m4) : 0;
+        for (int t = 0; t < 4; ++t) B[t] = (int)((h ? w4[t] >> 4 : w4[t]) & m4);
         const i32x4_t C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, i32x4_t{0, 0, 0, 0}, 0, 0, 0);
         const float s0 = (float)(C[0] + 256 * C[1]), s1 = (float)(C[2] + 256 * C[3]);  // exact: < 2^24
         acc[gi][0] = fmaf(dsv[gi][cc] * st0.x, s0, fmaf(-dmv[gi][cc], h ? st0.z : st0.y, acc[gi][0]));
@@ -150,12 +137,12 @@ __global__ __launch_bounds__(256) void k_q4k_gemv_mb(MbArgs p) {
   }
   // add the two sub-block halves (lanes j and j^1), then rows 2g, 2g+1 out
 #pragma unroll
-  for (int gi = 0; gi < NG; ++gi)
+  for (int gi = 0; gi < 2; ++gi)
 #pragma unroll
     for (int t = 0; t < 2; ++t) acc[gi][t] += dpp<0xB1>(acc[gi][t]);
   if (h == 0) {
 #pragma unroll
-    for (int gi = 0; gi < NG; ++gi) {
+    for (int gi = 0; gi < 2; ++gi) {
       if (row[gi] >= M.n) continue;
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
@@ -188,12 +175,12 @@ __global__ __launch_bounds__(256) void k_mb_reduce(MbArgs p) {
 
 size_t mb_stage_bytes(int k) { return (size_t)(k / 64) * 8 * (128 + 16); }
 
+// Super-blocks per K slice: two where they divide the row, else one.
+static int mb_slice_sb(int k) { return (k / 256) % 2 == 0 ? 2 : 1; }
+
 int mb_ksplit(int n_total, int k) {
-  // enough workgroups of 64 rows to cover the CUs, slices of whole super-blocks
-  const int blocks = (n_total + 63) / 64, nb = k / 256;
-  int ks = 1;
-  while (blocks * ks < 256 && ks * 2 <= nb) ks *= 2;
-  return ks;
+  (void)n_total;
+  return (k / 256) / mb_slice_sb(k);
 }
 
 size_t mb_part_bytes(int n_total, int k) {
@@ -203,13 +190,13 @@ size_t mb_part_bytes(int n_total, int k) {
 
 hipError_t launch_mb_stage(const float *x, int m, int k, void *stage, hipStream_t s) {
   int8_t *dig = static_cast<int8_t *>(stage);
-  float *stats = reinterpret_cast<float *>(dig + (size_t)(k / 64) * 8 * 128);
+  float *stats = mb_stats(stage, k);
   hipLaunchKernelGGL(k_mb_stage, dim3((k / 64 + 15) / 16, 8), dim3(256), 0, s, x, m, k, dig, stats);
   return hipGetLastError();
 }
 
 hipError_t launch_q4k_gemv_mb(const MbMat *mats, int nmat, int m, int k, const void *stage, float *part,
-                              hipStream_t s) {
+                              hipStream_t s, RowsIn *views) {
   MbArgs p{};
   p.nmat = nmat;
   int ntot = 0, blocks = 0;
@@ -227,9 +214,16 @@ hipError_t launch_q4k_gemv_mb(const MbMat *mats, int nmat, int m, int k, const v
   p.ntot = ntot;
   p.ksplit = mb_ksplit(ntot, k);
   p.part = part;
-  hipLaunchKernelGGL(k_q4k_gemv_mb<16>, dim3(blocks, p.ksplit), dim3(256), 0, s, p);
+  if (mb_slice_sb(k) == 2)
+    hipLaunchKernelGGL(k_q4k_gemv_mb<2>, dim3(blocks, p.ksplit), dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(k_q4k_gemv_mb<1>, dim3(blocks, p.ksplit), dim3(256), 0, s, p);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.ksplit == 1) return e;
+  if (views)
+    for (int i = 0; i < nmat; ++i)
+      views[i] = p.ksplit == 1 ? rows_plain(mats[i].y, mats[i].n)
+                               : RowsIn{part, p.ksplit, (size_t)8 * ntot, ntot, p.mat[i].part_off};
+  if (e != hipSuccess || p.ksplit == 1 || views) return e;
   const size_t total = (size_t)m * ntot;
   hipLaunchKernelGGL(k_mb_reduce, dim3((unsigned)std::min<size_t>((total + 255) / 256, 2048)), dim3(256), 0, s, p);
   return hipGetLastError();
