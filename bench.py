@@ -330,7 +330,8 @@ def main() -> int:
         d.synchronize()
         dtb = (time.perf_counter() - t_start) / reps
         decode["batch_verify"] = {"m": bm, "ms_per_call": round(dtb * 1e3, 4), "tok_per_s": round(bm / dtb, 1),
-                                  "note": "layers run per token, lm_head batched over the 8 tokens"}
+                                  "note": "every layer runs the 8 rows at once: batched Q4_K GEMV (int8 MFMA, one "
+                                          "pass over the weights), key-split causal attention, batched lm_head"}
         log(f"decode_step_batch M={bm}: {dtb * 1e3:.3f} ms per call -> {bm / dtb:.1f} tok/s")
         # GPU prefill of a config-3-length prompt (4096 tokens) on the same weights
         toks = [(7 * i + 3) % V for i in range(ctx)]
