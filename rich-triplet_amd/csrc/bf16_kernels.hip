@@ -1,9 +1,12 @@
-// bf16_kernels.hip -- BF16 GEMV (the lm_head shape: K=2560, N=262144).
+// bf16_kernels.hip -- BF16 GEMV (the lm_head shape K=2560, N=262144, and any
+// K up to 16384 for BF16 projections).
 //
 // y[N] = W[N,K] (bf16, row-major) . x[K] (f32), f32 accumulation.
 // One wave per row: lane l reads 16-byte pieces l, l+64, ... of the row, so
 // every load instruction moves 1 KB of contiguous weights; the lane's 8*CPL
 // activations stay in registers for all rows the wave visits.
+#include <algorithm>
+
 #include "rt_device.hpp"
 #include "rt_kernels.hpp"
 
@@ -91,6 +94,46 @@ __global__ __launch_bounds__(256) void k_bf16_gemv_generic(const uint16_t *__res
   if (lane == 0) y[row] = acc;
 }
 
+// K up to 16384 (multiple of 8), x staged in LDS once per workgroup: each
+// wave takes U rows at a time and keeps 4 pieces of each in flight.
+template <int U>
+__global__ __launch_bounds__(256) void k_bf16_gemv_lds(const uint16_t *__restrict__ W, const float *__restrict__ x,
+                                                       float *__restrict__ y, int N, int K) {
+  __shared__ __attribute__((aligned(16))) float xs[16384];
+  for (int i = threadIdx.x; i < K / 4; i += 256)
+    reinterpret_cast<float4 *>(xs)[i] = reinterpret_cast<const float4 *>(x)[i];
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int wave = (int)((blockIdx.x * 256u + threadIdx.x) >> 6), nwaves = (int)(gridDim.x * 4u);
+  const int pieces = K / 8;
+  for (int r0 = wave * U; r0 < N; r0 += nwaves * U) {
+    const uint4 *rp[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) rp[u] = reinterpret_cast<const uint4 *>(W + (size_t)min(r0 + u, N - 1) * K);
+    float acc[U] = {};
+    for (int p0 = lane; p0 < pieces; p0 += 256) {
+      uint4 wv[U][4];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wv[u][j] = p0 + 64 * j < pieces ? rp[u][p0 + 64 * j] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int p = min(p0 + 64 * j, pieces - 1);
+        const float4 a = reinterpret_cast<const float4 *>(xs)[2 * p], b = reinterpret_cast<const float4 *>(xs)[2 * p + 1];
+        const float xv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc[u] += bf16_piece_dot<1>(wv[u][j], xv);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float v = wave_sum(acc[u]);
+      if (lane == 0 && r0 + u < N) y[r0 + u] = v;
+    }
+  }
+}
+
 hipError_t launch_bf16_gemv(const uint16_t *W, const float *x, float *y, int N, int K, hipStream_t s) {
   if (K == 2560) {
     constexpr int U = 2;
@@ -98,6 +141,12 @@ hipError_t launch_bf16_gemv(const uint16_t *W, const float *x, float *y, int N, 
     int grid = (waves_needed + 3) / 4;
     if (grid > 256 * 8) grid = 256 * 8;
     hipLaunchKernelGGL((k_bf16_gemv<5, U>), dim3(grid), dim3(256), 0, s, W, x, y, N);
+    return hipGetLastError();
+  }
+  if (K <= 16384) {
+    constexpr int U = 2;
+    const unsigned grid = (unsigned)std::min((N + 4 * U - 1) / (4 * U), 256 * 4);
+    hipLaunchKernelGGL(k_bf16_gemv_lds<U>, dim3(grid), dim3(256), 0, s, W, x, y, N, K);
     return hipGetLastError();
   }
   const unsigned grid = (unsigned)((N + 3) / 4);

@@ -101,7 +101,10 @@ def test_q4k_gemv_reference_fixtures(rt, orc):
     rt.weight_cache_clear()
 
 
-@pytest.mark.parametrize("n,k", [(8, 64), (128, 256), (4096, 2560), (262144, 2560), (1001, 2560), (77, 1000)])
+# K = 2560: register-resident x; other K up to 16384: x staged in LDS (BF16
+# projections of the decode step: 10240, 2048); beyond that one wave per row
+@pytest.mark.parametrize("n,k", [(8, 64), (128, 256), (4096, 2560), (262144, 2560), (1001, 2560), (77, 1000),
+                                 (2560, 10240), (2560, 2048), (9, 16392)])
 def test_bf16_gemv_matches_oracle(rt, orc, dev, n, k):
     import torch
     w = orc.synth_bf16(3000 + n, n * k)
