@@ -121,6 +121,17 @@ rt_status rt_q8_0_dequant_f32(const void *w, size_t n_elem, float *out, void *st
  * weights; device pointers, w and x 16-byte aligned. */
 rt_status rt_q6k_gemv(const void *w, const float *x, float *y, int64_t n, int64_t k, void *stream);
 rt_status rt_q8_0_gemv(const void *w, const float *x, float *y, int64_t n, int64_t k, void *stream);
+/* c[m][n] = a[m][k] . W[n][k] for a weight in any RT_LINEAR_* format but
+ * F32 (Q6_K and Q8_0 planar): the prefill GEMM of a projection.  Replaces
+ * MatBf16::matmul_by_t (autograd2.rs:757-852), which the reference runs on
+ * the BF16-widened Q6_K / Q8_0 weights, and matmul_q4k_t for RT_LINEAR_Q4K
+ * (as rt_q4k_gemm_f32).  Non-Q4_K rows are widened to f16 with a
+ * power-of-two scale per row, A likewise, f32 accumulation on the matrix
+ * cores; k % 256 == 0 (Q6_K, Q4_K) or k % 32 == 0; device pointers, a and w
+ * 16-byte aligned.  Uses the per-thread workspace of rt_q4k_gemm_f32, about
+ * (m + n) * k * 2 bytes. */
+rt_status rt_linear_gemm_f32(int32_t fmt, const void *w, const float *a, float *c, int64_t m, int64_t n, int64_t k,
+                             void *stream);
 
 /* gemv_q4k_t_batch (metal_decode.rs:459-521): c[m][n] = a[m][k] . W[n][k]
  * for m = 1..8 rows (the speculative verify batch), reading the weights once

@@ -334,6 +334,16 @@ def proj_gemv(fmt: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray, thre
     return y
 
 
+def proj_matmul(fmt: int, a: np.ndarray, w: np.ndarray, n: int, k: int, threads: int = 0) -> np.ndarray:
+    """orc_proj_matmul: C = A W^T for a projection of format fmt."""
+    a = np.ascontiguousarray(a, np.float32)
+    m = a.shape[0]
+    c = np.empty((m, n), np.float32)
+    lib().orc_proj_matmul(C.c_int(fmt), C.c_void_p(_ptr(a)), C.c_size_t(m), C.c_void_p(_ptr(np.ascontiguousarray(w))),
+                          C.c_size_t(n), C.c_size_t(k), C.c_void_p(_ptr(c)), C.c_int(threads))
+    return c
+
+
 def gqa_attention_prefill(q, k_cache, v_cache, p0, T, lo_fixed, window, n_q_heads, n_kv_heads, d_head, scale):
     """orc_gqa_attention_prefill: rows p0 .. p0+T-1, keys [lo(r), r]."""
     q = np.ascontiguousarray(q, np.float32)

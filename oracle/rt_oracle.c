@@ -563,13 +563,14 @@ void orc_bf16_gemv_f64(const uint16_t *w, size_t rows, size_t cols, const float 
 /* ------------------------------------------------------------------------ */
 /* GEMM                                                                      */
 /* ------------------------------------------------------------------------ */
-typedef struct { const float *a; size_t m; const uint8_t *blocks; size_t n, k; float *c; double *c64; } mm_ctx;
+typedef struct { const float *a; size_t m; const uint8_t *blocks; size_t n, k; float *c; double *c64; int fmt; } mm_ctx;
+static void proj_row(int fmt, const uint8_t *w, size_t cols, size_t j, float *row);
 static void mm_band(void *p, size_t j0, size_t j1)
 {
     mm_ctx *c = (mm_ctx *)p;
     float *row = (float *)malloc(c->k * sizeof(float));
     for (size_t j = j0; j < j1; j++) {
-        orc_q4k_dequant_row(c->blocks, c->k, j, row);
+        proj_row(c->fmt, c->blocks, c->k, j, row);
         for (size_t i = 0; i < c->m; i++) {
             const float *ai = c->a + i * c->k;
             if (c->c64) {
@@ -592,12 +593,21 @@ static void mm_band(void *p, size_t j0, size_t j1)
  * Threaded over output columns; every output is computed independently. */
 void orc_q4k_matmul(const float *a, size_t m, const uint8_t *blocks, size_t n, size_t k, float *c, int hw_threads)
 {
-    mm_ctx ctx = {a, m, blocks, n, k, c, NULL};
+    mm_ctx ctx = {a, m, blocks, n, k, c, NULL, 1};
+    run_bands(n, hw_threads, 1, mm_band, &ctx);
+}
+/* The same GEMM for a projection in any orc_layer.fmt format: row j is
+ * widened to f32 as the format's decoder does (the reference widens Q6_K and
+ * Q8_0 to BF16 at load, transformer4.rs:1233-1242, and multiplies with
+ * MatBf16::matmul_by_t, autograd2.rs:757-852), then a sequential f32 dot. */
+void orc_proj_matmul(int fmt, const float *a, size_t m, const uint8_t *w, size_t n, size_t k, float *c, int hw_threads)
+{
+    mm_ctx ctx = {a, m, w, n, k, c, NULL, fmt};
     run_bands(n, hw_threads, 1, mm_band, &ctx);
 }
 void orc_q4k_matmul_f64(const float *a, size_t m, const uint8_t *blocks, size_t n, size_t k, double *c, int hw_threads)
 {
-    mm_ctx ctx = {a, m, blocks, n, k, NULL, c};
+    mm_ctx ctx = {a, m, blocks, n, k, NULL, c, 1};
     run_bands(n, hw_threads, 1, mm_band, &ctx);
 }
 
@@ -691,6 +701,17 @@ void orc_gqa_attention_decode(const float *q, const float *k_cache, const float 
     free(scores);
 }
 
+/* Row j of a projection in format fmt (1 Q4_K, 2 BF16, 4 Q6_K, 5 Q8_0). */
+static void proj_row(int fmt, const uint8_t *w, size_t cols, size_t j, float *row)
+{
+    if (fmt == 2) {
+        const uint16_t *r = (const uint16_t *)w + j * cols;
+        for (size_t i = 0; i < cols; i++) row[i] = orc_bf16_to_f32(r[i]);
+    } else if (fmt == 4) orc_q6k_dequant(w + j * (cols / 256) * 210, cols, row);
+    else if (fmt == 5) orc_q8_0_dequant(w + j * (cols / 32) * 34, cols, row);
+    else orc_q4k_dequant_row(w, cols, j, row);
+}
+
 /* Per-format projection GEMV (formats of orc_layer.fmt). */
 typedef struct { int fmt; const uint8_t *w; size_t cols; const float *x; float *y; } pg_ctx;
 static void pg_band(void *p, size_t j0, size_t j1)
@@ -698,8 +719,7 @@ static void pg_band(void *p, size_t j0, size_t j1)
     pg_ctx *c = (pg_ctx *)p;
     float *row = (float *)malloc(c->cols * sizeof(float));
     for (size_t j = j0; j < j1; j++) {
-        if (c->fmt == 4) orc_q6k_dequant(c->w + j * (c->cols / 256) * 210, c->cols, row);
-        else orc_q8_0_dequant(c->w + j * (c->cols / 32) * 34, c->cols, row);
+        proj_row(c->fmt, c->w, c->cols, j, row);
         float acc = 0.0f;
         for (size_t i = 0; i < c->cols; i++) acc += row[i] * c->x[i];
         c->y[j] = acc;
@@ -876,15 +896,13 @@ void orc_gemma3_prefill(const orc_gemma3_cfg *cfg, const orc_layer *layers, cons
         for (size_t c = 0; c < H; c++) x[t * H + c] = orc_bf16_to_f32(embed_bf16[(size_t)tokens[t] * H + c]) * scale;
     for (int l = 0; l < cfg->n_layers; l++) {
         const orc_layer *L = &layers[l];
-        for (int p = 0; p < 7; p++)
-            if (L->fmt[p] > 1) { fprintf(stderr, "orc_gemma3_prefill: Q4_K projections only\n"); abort(); }
         int glob = is_global(cfg, l);
         float theta = glob ? cfg->rope_theta_global : cfg->rope_theta_local;
         float fs = glob ? cfg->rope_fs_global : cfg->rope_fs_local;
         for (size_t t = 0; t < T; t++) orc_rms_norm_gemma3(x + t * H, L->in_norm, H, cfg->eps, xn + t * H);
-        orc_q4k_matmul(xn, T, L->q, QD, H, q, hw);
-        orc_q4k_matmul(xn, T, L->k, KVD, H, k, hw);
-        orc_q4k_matmul(xn, T, L->v, KVD, H, v, hw);
+        orc_proj_matmul(L->fmt[0], xn, T, L->q, QD, H, q, hw);
+        orc_proj_matmul(L->fmt[1], xn, T, L->k, KVD, H, k, hw);
+        orc_proj_matmul(L->fmt[2], xn, T, L->v, KVD, H, v, hw);
         for (size_t t = 0; t < T; t++) {
             orc_per_head_norm(q + t * QD, L->q_norm, NQ, D, cfg->eps, tmp);
             memcpy(q + t * QD, tmp, QD * sizeof(float));
@@ -903,16 +921,16 @@ void orc_gemma3_prefill(const orc_gemma3_cfg *cfg, const orc_layer *layers, cons
             else window = w;
         }
         orc_gqa_attention_prefill(q, L->k_cache, L->v_cache, p0, T, lo_fixed, window, NQ, NKV, D, cfg->attn_scale, att);
-        orc_q4k_matmul(att, T, L->o, H, QD, o, hw);
+        orc_proj_matmul(L->fmt[3], att, T, L->o, H, QD, o, hw);
         for (size_t t = 0; t < T; t++) {
             orc_rms_norm_gemma3(o + t * H, L->post_attn_norm, H, cfg->eps, tmp);
             for (size_t c = 0; c < H; c++) x2[t * H + c] = x[t * H + c] + tmp[c];
             orc_rms_norm_gemma3(x2 + t * H, L->pre_ffn_norm, H, cfg->eps, xn + t * H);
         }
-        orc_q4k_matmul(xn, T, L->gate, F, H, g, hw);
-        orc_q4k_matmul(xn, T, L->up, F, H, u, hw);
+        orc_proj_matmul(L->fmt[4], xn, T, L->gate, F, H, g, hw);
+        orc_proj_matmul(L->fmt[5], xn, T, L->up, F, H, u, hw);
         for (size_t i = 0; i < T * F; i++) g[i] = orc_gelu_tanh(g[i]) * u[i];
-        orc_q4k_matmul(g, T, L->down, H, F, o, hw);
+        orc_proj_matmul(L->fmt[6], g, T, L->down, H, F, o, hw);
         for (size_t t = 0; t < T; t++) {
             orc_rms_norm_gemma3(o + t * H, L->post_ffn_norm, H, cfg->eps, tmp);
             for (size_t c = 0; c < H; c++) x[t * H + c] = x2[t * H + c] + tmp[c];

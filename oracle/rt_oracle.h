@@ -91,6 +91,10 @@ typedef struct {
  * Q4_K through dot_row; Q6_K / Q8_0 dequantised per row by decode_q6k_to_f32
  * / decode_q8_0_to_f32 and a sequential f32 dot; BF16 through its dot_row. */
 void orc_proj_gemv(int fmt, const uint8_t *w, size_t rows, size_t cols, const float *x, float *y, int hw_threads);
+/* C[m,n] = A[m,k] . W[n,k]^T for a projection of format fmt (as orc_layer.fmt);
+ * a sequential f32 dot per output, as orc_q4k_matmul. */
+void orc_proj_matmul(int fmt, const float *a, size_t m, const uint8_t *w, size_t n, size_t k, float *c,
+                     int hw_threads);
 
 /* One CPU decode step (transformer4.rs:2358-2385 with forward_cached 1900-1964).
  * Appends K/V at row `pos` of every layer's cache and writes vocab logits.

@@ -60,6 +60,7 @@ _SIGNATURES = {
     "rt_q8_0_dequant_f32": (_i32, [_vp, _sz, _vp, _vp]),
     "rt_q6k_gemv": (_i32, [_vp, _vp, _vp, _i64, _i64, _vp]),
     "rt_q8_0_gemv": (_i32, [_vp, _vp, _vp, _i64, _i64, _vp]),
+    "rt_linear_gemm_f32": (_i32, [_i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "rt_q4k_gemm_bf16": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "rt_q4k_gemm_f32": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "rt_matmul_q4k_t": (_i32, [_vp, _sz, _sz, _vp, _sz, _vp]),
@@ -180,6 +181,12 @@ def q6k_gemv(w, x, y, n: int, k: int, stream=None) -> None:
 def q8_0_gemv(w, x, y, n: int, k: int, stream=None) -> None:
     """y = W x on planar Q8_0 weights (q8_0_repack)."""
     check(lib().rt_q8_0_gemv(_p(w), _p(x), _p(y), n, k, _stream(stream)))
+
+
+def linear_gemm_f32(fmt: int, w, a, c, m: int, n: int, k: int, stream=None) -> None:
+    """c[m][n] = a[m][k] . W[n][k] for a weight in format fmt (LINEAR_Q4K,
+    LINEAR_BF16, LINEAR_Q6K or LINEAR_Q8_0, the last two planar)."""
+    check(lib().rt_linear_gemm_f32(fmt, _p(w), _p(a), _p(c), m, n, k, _stream(stream)))
 
 
 def q6k_dequant_f32(w, out, n_blocks: int, stream=None) -> None:

@@ -160,6 +160,29 @@ rt_status rt_q4k_gemm_f32(const float *a, const void *w, float *c, int64_t m, in
   return q4k_gemm_entry("rt_q4k_gemm_f32", a, false, w, c, m, n, k, stream);
 }
 
+// MatBf16::matmul_by_t (autograd2.rs:757-852) on the BF16, Q6_K or Q8_0
+// weight of a projection; Q4_K goes to the Q4_K GEMM.
+rt_status rt_linear_gemm_f32(int32_t fmt, const void *w, const float *a, float *c, int64_t m, int64_t n, int64_t k,
+                             void *stream) {
+  static const char *who = "rt_linear_gemm_f32";
+  if (fmt == RT_LINEAR_Q4K) return q4k_gemm_entry(who, a, false, w, c, m, n, k, stream);
+  if (fmt != RT_LINEAR_BF16 && fmt != RT_LINEAR_Q6K && fmt != RT_LINEAR_Q8_0)
+    return set_error(RT_EINVAL, "%s: unsupported format %d", who, fmt);
+  if (m <= 0 || n <= 0 || k <= 0)
+    return set_error(RT_EINVAL, "%s: m=%lld n=%lld k=%lld must be positive", who, (long long)m, (long long)n,
+                     (long long)k);
+  const int align = fmt == RT_LINEAR_Q6K ? 256 : 32;
+  if (k % align != 0) return set_error(RT_EINVAL, "%s: k=%lld must be a multiple of %d", who, (long long)k, align);
+  if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX) return set_error(RT_EINVAL, "%s: m, n or k exceeds int32", who);
+  if (!a || !w || !c) return set_error(RT_EINVAL, "%s: null pointer", who);
+  if (!aligned16(a) || !aligned16(w)) return set_error(RT_EINVAL, "%s: a and w must be 16-byte aligned", who);
+  if ((reinterpret_cast<uintptr_t>(c) & 3u) != 0) return set_error(RT_EINVAL, "%s: c must be 4-byte aligned", who);
+  void *ws = nullptr;
+  rt_status st = gemm_workspace(proj_gemm_workspace_bytes((int)m, (int)n, (int)k), &ws);
+  if (st != RT_OK) return st;
+  return hip_error(launch_proj_gemm(a, fmt, w, c, (int)m, (int)n, (int)k, ws, (hipStream_t)stream), who);
+}
+
 // gemv_q4k_t_batch (metal_decode.rs:459-521): c[m][n] = a[m][k] . W[n][k]
 // for m <= 8 rows, one pass over the weights.
 rt_status rt_q4k_gemv_batch(const void *w, const float *a, float *c, int64_t m, int64_t n, int64_t k, void *stream) {

@@ -621,11 +621,6 @@ rt_status rt_decode_prefill(rt_decode *d, const int32_t *tokens, int32_t n, int3
     rt_status st = check_ready(d, tokens[i], start_position + i);
     if (st != RT_OK) return st;
   }
-  for (int l = 0; l < d->cfg.n_layers; ++l)
-    for (int p = 0; p < 7; ++p)
-      if (d->layers[l].fmt[p] != RT_LINEAR_Q4K)
-        return set_error(RT_EINVAL, "rt_decode_prefill: layer %d has a projection in format %d; prefill runs Q4_K "
-                         "projections only", l, d->layers[l].fmt[p]);
   const int w = d->cfg.sliding_window;
   int lo_fixed = 0, window = 0;
   if (mode == RT_PREFILL_REFERENCE)
@@ -657,7 +652,7 @@ rt_status rt_decode_prefill(rt_decode *d, const int32_t *tokens, int32_t n, int3
       plan.lo_fixed = lo_fixed;
       plan.window = window;
       plan.max_pos = start_position + c0 + cn;
-      plan.mb = cn <= kMaxBatch;  // a few rows: one pass over the weights beats the GEMM's tiles
+      plan.mb = cn <= kMaxBatch && d->all_q4k;  // a few rows: one pass over the weights beats the GEMM's tiles
       plan.logits = c0 + cn == n ? RowsPlan::kLastRow : RowsPlan::kNone;
       e = enqueue_rows(d->shape, d->args, d->layers.data(), d->pf, plan, d->stream);
     }

@@ -22,6 +22,7 @@
 
 #include <algorithm>
 
+#include "../../include/rt_hip.h"
 #include "decode.hpp"
 #include "gemma3_math.hpp"
 #include "q4k_gemv_mb.hpp"
@@ -464,7 +465,7 @@ size_t prefill_gemm_workspace_bytes(const DecodeShape &s, int cap) {
   // ways: take the largest requirement over every row count up to cap.
   size_t m = 0;
   for (auto &nk : shapes) {
-    m = std::max(m, q4k_gemm_workspace_bytes(cap, nk[0], nk[1]));
+    m = std::max({m, q4k_gemm_workspace_bytes(cap, nk[0], nk[1]), proj_gemm_workspace_bytes(cap, nk[0], nk[1])});
     for (int rows = 1; rows <= std::min(cap, 1024); ++rows)
       m = std::max(m, q4k_gemm_workspace_bytes(rows, nk[0], nk[1]));
   }
@@ -502,7 +503,9 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
   // partial sums that the consumer adds while reading (views).
   int8_t *stage = plan.mb ? static_cast<int8_t *>(b.mb_stage) : nullptr;
   RowsIn vq, vk, vv, vo, vg, vu, vd;
-  auto proj = [&](const float *A, int K, std::initializer_list<MbMat> mats, std::initializer_list<RowsIn *> views) {
+  // (plan.mb requires every projection in Q4_K; other formats take their own GEMM)
+  auto proj = [&](const float *A, int K, std::initializer_list<int> fmts, std::initializer_list<MbMat> mats,
+                  std::initializer_list<RowsIn *> views) {
     if (plan.mb) {
       RowsIn out[3];
       hipError_t r = launch_q4k_gemv_mb(mats.begin(), (int)mats.size(), n, K, b.mb_stage, b.mb_part, st, out);
@@ -512,7 +515,9 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
     }
     int i = 0;
     for (const MbMat &m : mats) {
-      hipError_t r = launch_q4k_gemm(A, false, m.w, m.y, n, m.n, K, b.ws, st);
+      const int fmt = fmts.begin()[i];
+      hipError_t r = fmt == RT_LINEAR_Q4K ? launch_q4k_gemm(A, false, m.w, m.y, n, m.n, K, b.ws, st)
+                                          : launch_proj_gemm(A, fmt, m.w, m.y, n, m.n, K, b.ws, st);
       if (r != hipSuccess) return r;
       *views.begin()[i++] = rows_plain(m.y, m.n);
     }
@@ -525,7 +530,7 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
     if (li == 0)
       PF_CHECK(hipLaunchKernelGGL(k_pf_norm<false>, dim3(n), dim3(256), 0, st, nullptr, rows_plain(b.hid, H), nullptr,
                                   L.g_in, nullptr, b.xn, H, a.eps, stage));
-    PF_TRY(proj(b.xn, H, {MbMat{L.wq, b.q, QD, 0, 0}, MbMat{L.wk, b.k, KVD, 0, 0}, MbMat{L.wv, b.v, KVD, 0, 0}},
+    PF_TRY(proj(b.xn, H, {L.fmt[kProjQ], L.fmt[kProjK], L.fmt[kProjV]}, {MbMat{L.wq, b.q, QD, 0, 0}, MbMat{L.wk, b.k, KVD, 0, 0}, MbMat{L.wv, b.v, KVD, 0, 0}},
                 {&vq, &vk, &vv}));
     const int items = n * (nq + nkv);
     const int cs_off = L.global ? D : 0;
@@ -560,14 +565,14 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
     if (stage && !pa.split_stages) return hipErrorInvalidValue;  // the batched path stages in the merge kernel
     if (D == 256) PF_TRY(launch_pf_attn<256>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa, stage));
     else PF_TRY(launch_pf_attn<128>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa, stage));
-    PF_TRY(proj(b.attn, QD, {MbMat{L.wo, b.o, H, 0, 0}}, {&vo}));
+    PF_TRY(proj(b.attn, QD, {L.fmt[kProjO]}, {MbMat{L.wo, b.o, H, 0, 0}}, {&vo}));
     PF_CHECK(hipLaunchKernelGGL(k_pf_norm<true>, dim3(n), dim3(256), 0, st, b.hid, vo, L.g_post_attn, L.g_pre_ffn,
                                 b.x2, b.xn, H, a.eps, stage));
-    PF_TRY(proj(b.xn, H, {MbMat{L.wgate, b.g, F, 0, 0}, MbMat{L.wup, b.u, F, 0, 0}}, {&vg, &vu}));
+    PF_TRY(proj(b.xn, H, {L.fmt[kProjGate], L.fmt[kProjUp]}, {MbMat{L.wgate, b.g, F, 0, 0}, MbMat{L.wup, b.u, F, 0, 0}}, {&vg, &vu}));
     const size_t n4 = (size_t)n * F / 4;
     const unsigned eg = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
     PF_CHECK(hipLaunchKernelGGL(k_pf_gelu_mul, dim3(eg), dim3(256), 0, st, vg, vu, b.g, n, F, stage));
-    PF_TRY(proj(b.g, F, {MbMat{L.wdown, b.dn, H, 0, 0}}, {&vd}));
+    PF_TRY(proj(b.g, F, {L.fmt[kProjDown]}, {MbMat{L.wdown, b.dn, H, 0, 0}}, {&vd}));
     if (li + 1 < s.n_layers)
       PF_CHECK(hipLaunchKernelGGL(k_pf_norm<true>, dim3(n), dim3(256), 0, st, b.x2, vd, L.g_post_ffn,
                                   layers[li + 1].g_in, b.hid, b.xn, H, a.eps, stage));

@@ -43,14 +43,6 @@ constexpr int kBK = 64;  // K per pipeline stage = one Q4_K chunk (32 qs bytes, 
 // Prep: A -> f16 with a per-row exponent; W row exponents from block headers.
 // Workgroups [0, M) take one A row each, the rest four W rows each.
 // ---------------------------------------------------------------------------
-RT_DEV int f16_exponent_for(float bound) {
-  // 2^-e * bound in [2^14, 2^15); 0 for zero / non-finite bounds (those propagate).
-  if (!(bound > 0.f) || !__builtin_isfinite(bound)) return 0;
-  int E;
-  (void)frexpf(bound, &E);  // bound = f * 2^E, f in [0.5, 1)
-  return E - 15;
-}
-
 template <typename TA>
 RT_DEV void load8(const TA *p, float v[8]);
 template <>
@@ -616,6 +608,11 @@ int gemm_ksplit(int M, int N, int K) {
   const int ntiles = ((M + 127) / 128) * ((N + 255) / 256);
   const int by_cus = 256 / ntiles, by_k = (K / kBK) / 16;
   return max(1, min(by_cus, by_k));
+}
+
+hipError_t launch_gemm_prep_a(const float *a, int M, int K, _Float16 *a16, int *ea, hipStream_t s) {
+  hipLaunchKernelGGL((k_gemm_prep<float>), dim3(M), dim3(256), 0, s, a, a16, ea, nullptr, nullptr, M, 0, K);
+  return hipGetLastError();
 }
 
 size_t q4k_gemm_workspace_bytes(int M, int N, int K) {

@@ -35,6 +35,15 @@ RT_DEV float ubyte1(uint32_t v) { return (float)((v >> 8) & 0xFFu); }
 RT_DEV float ubyte2(uint32_t v) { return (float)((v >> 16) & 0xFFu); }
 RT_DEV float ubyte3(uint32_t v) { return (float)(v >> 24); }
 
+// Power-of-two exponent e with 2^-e * bound in [2^14, 2^15): values scaled by
+// 2^-e fit f16 without overflow.  0 for zero / non-finite bounds (those propagate).
+RT_DEV int f16_exponent_for(float bound) {
+  if (!(bound > 0.f) || !__builtin_isfinite(bound)) return 0;
+  int E;
+  (void)frexpf(bound, &E);  // bound = f * 2^E, f in [0.5, 1)
+  return E - 15;
+}
+
 RT_DEV float bf16_lo(uint32_t pair) { return bits_f32(pair << 16); }
 RT_DEV float bf16_hi(uint32_t pair) { return bits_f32(pair & 0xFFFF0000u); }
 

@@ -20,6 +20,14 @@ hipError_t launch_q6k_dequant(const void *w, size_t n_blocks, float *out, hipStr
 hipError_t launch_q8_0_dequant(const void *w, size_t n_elem, float *out, hipStream_t s);
 hipError_t launch_q6k_gemv(const void *W, const float *x, float *y, int N, int K, hipStream_t s);
 hipError_t launch_q8_0_gemv(const void *W, const float *x, float *y, int N, int K, hipStream_t s);
+// A (f32 [M][K]) -> f16 with a per-row power-of-two exponent (the GEMMs' A prep).
+hipError_t launch_gemm_prep_a(const float *a, int M, int K, _Float16 *a16, int *ea, hipStream_t s);
+// C[M,N] = A[M,K] . W[N,K]^T for a projection stored as RT_LINEAR_Q6K, _Q8_0
+// or _BF16 (planar layouts of kquant.hip): its rows are widened to f16 with a
+// per-row power-of-two scale and multiplied on the matrix cores in f32.
+size_t proj_gemm_workspace_bytes(int M, int N, int K);
+hipError_t launch_proj_gemm(const float *a, int fmt, const void *w, float *c, int M, int N, int K, void *ws,
+                            hipStream_t s);
 // Q4_K GEMM C[M,N] = A[M,K] . W[N,K]^T; A bf16 bits (a_bf16) or f32; ws holds
 // q4k_gemm_workspace_bytes(M, N, K) bytes of device scratch.
 size_t q4k_gemm_workspace_bytes(int M, int N, int K);

@@ -187,6 +187,31 @@ def test_oracle_proj_gemv_formats(orc):
         assert rel_l2(y, ref) < 1e-6, fmt
 
 
+def test_oracle_proj_matmul_formats(orc):
+    """orc_proj_matmul (the prefill GEMM of each format) against float64
+    products of the pinned dequantisers; row by row it equals orc_proj_gemv
+    (Q4_K: orc_q4k_matmul, the GEMV keeps the reference's blocked order)."""
+    rng = np.random.default_rng(12)
+    m, rows, cols = 3, 20, 512
+    a = rng.standard_normal((m, cols)).astype(np.float32)
+    q6 = synth_q6k(rng, rows * cols // 256)
+    q8 = synth_q8_0(rng, rows * cols // 32)
+    bf = orc.synth_bf16(14, rows * cols)
+    q4 = orc.synth_q4k(15, rows, cols)
+    cases = [(4, q6, orc.q6k_dequant(q6, rows * cols)), (5, q8, orc.q8_0_dequant(q8, rows * cols)),
+             (2, bf, (bf.astype(np.uint32) << 16).view(np.float32)),
+             (1, q4, orc.q4k_dequant(q4, rows, cols).reshape(-1))]
+    for fmt, w, deq in cases:
+        c = orc.proj_matmul(fmt, a, w, rows, cols)
+        ref = a.astype(np.float64) @ deq.reshape(rows, cols).astype(np.float64).T
+        assert rel_l2(c, ref) < 1e-6, fmt
+        if fmt == 1:
+            assert np.array_equal(c, orc.q4k_matmul(a, w, rows, cols))
+            continue
+        for i in range(m):
+            assert np.array_equal(c[i], orc.proj_gemv(fmt, w, rows, cols, a[i])), fmt
+
+
 # ---------------------------------------------------------------------------
 # decode step with per-projection formats (GPU)
 # ---------------------------------------------------------------------------
@@ -262,8 +287,6 @@ def test_mixed_format_decode_matches_oracle(rt, orc, pos):
     for i, tok in enumerate((5, 6, 7)):
         ref = orc.gemma3_decode_step(cfg, layers, embed, fnorm, token=tok, pos=pos + 3 + i)
         assert rel_l2(batch[i], ref) < 1e-3, (i, rel_l2(batch[i], ref))
-    with pytest.raises(rt.RtError):
-        d.prefill([1, 2, 3], 0, 0)  # prefill runs Q4_K projections only
     d.close()
 
 
@@ -295,3 +318,143 @@ def test_q4_k_m_layout_at_gemma3_4b_shape(rt, orc):
     assert rel_l2(got, ref) < 1e-3, rel_l2(got, ref)
     assert rel_l2(got, ref) < rel_l2(ref_bf16, ref)
     d.close()
+
+
+# ---------------------------------------------------------------------------
+# prefill with per-projection formats
+# ---------------------------------------------------------------------------
+def test_oracle_mixed_prefill_equals_decode_steps(orc):
+    """Per-row sliding window: the oracle prefill of a model with projections
+    in every format is T decode steps of the decode-step oracle (whose
+    per-format GEMV is pinned above)."""
+    from test_gpu_decode import tiny
+    from test_oracle import make_model
+    from test_prefill import fresh_caches
+    cfg = tiny(2)
+    T = 12
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=T, ctx=0, seed=7350)
+    apply_formats(orc, cfg, layers, MIXED_PLAN, seed=7351)
+    toks = [(5 * i + 1) % cfg["vocab"] for i in range(T)]
+    a = fresh_caches(layers)
+    got = orc.gemma3_prefill(cfg, a, embed, fnorm, toks, 0, mode=1)
+    b = fresh_caches(layers)
+    for i, t in enumerate(toks):
+        ref = orc.gemma3_decode_step(cfg, b, embed, fnorm, token=t, pos=i)
+    assert rel_l2(got, ref) < 2e-5
+    for La, Lb in zip(a, b):
+        assert rel_l2(La["k_cache"], Lb["k_cache"]) < 2e-5
+        assert rel_l2(La["v_cache"], Lb["v_cache"]) < 2e-5
+
+
+GEMM_CASES = [(4, 1, 256, 512), (4, 77, 300, 2560), (5, 130, 200, 96), (5, 8, 1000, 1024), (2, 5, 129, 64),
+              (2, 200, 384, 2048), (1, 33, 256, 512)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt,m,n,k", GEMM_CASES)
+def test_linear_gemm_matches_float64(rt, orc, dev, fmt, m, n, k):
+    """rt_linear_gemm_f32 against the float64 product of the exactly
+    dequantised weights; shapes with partial 128-row and 128-column tiles."""
+    import torch
+    rng = np.random.default_rng(100 + fmt * 7 + m)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    if fmt == 4:
+        src = synth_q6k(rng, n * k // 256)
+        w, deq = rt.q6k_repack(src), orc.q6k_dequant(src, n * k)
+    elif fmt == 5:
+        src = synth_q8_0(rng, n * k // 32)
+        w, deq = rt.q8_0_repack(src), orc.q8_0_dequant(src, n * k)
+    elif fmt == 2:
+        w = orc.synth_bf16(200 + m, n * k)
+        deq = (w.astype(np.uint32) << 16).view(np.float32)
+    else:
+        w = orc.synth_q4k(300 + m, n, k)
+        deq = orc.q4k_dequant(w, n, k).reshape(-1)
+    c = torch.empty((m, n), dtype=torch.float32, device=dev)
+    rt.linear_gemm_f32(fmt, to_dev(w, dev), to_dev(a, dev), c, m, n, k)
+    torch.cuda.synchronize()
+    ref = a.astype(np.float64) @ deq.reshape(n, k).astype(np.float64).T
+    got = c.cpu().numpy()
+    assert np.all(np.isfinite(got))
+    # f16 operands (11-bit significands) with f32 accumulation: ~2e-4
+    assert rel_l2(got, ref) < 1e-3, rel_l2(got, ref)
+
+
+def test_linear_gemm_rejects_bad_shapes(rt):
+    with pytest.raises(rt.RtError):
+        rt.linear_gemm_f32(3, 16, 16, 16, 1, 1, 256)  # RT_LINEAR_F32 has no GEMM here
+    with pytest.raises(rt.RtError):
+        rt.linear_gemm_f32(4, 16, 16, 16, 1, 1, 96)  # Q6_K rows are 256-element blocks
+    with pytest.raises(rt.RtError):
+        rt.linear_gemm_f32(5, 16, 16, 16, 0, 1, 64)
+
+
+def plain_ctx(rt, cfg, dev_layers, fmts, embed, fnorm, max_seq):
+    d = rt.HipDecodeContext(cfg, max_seq)
+    for i, (D, f) in enumerate(zip(dev_layers, fmts)):
+        d.set_layer(i, D, formats=f)
+    d.set_embed(embed, fnorm)
+    return d
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,mode,chunk", [(3, 1, 0), (20, 0, 0), (30, 1, 7)])
+def test_mixed_format_prefill_matches_oracle(rt, orc, T, mode, chunk):
+    """Prefill of a model with projections in Q6_K, Q8_0 and BF16 (the GEMM
+    on f16-widened rows) against the oracle's prefill; chunks of 7 rows take
+    the GEMM too (the batched GEMV reads Q4_K only).  The next decode step
+    reads the prefilled cache."""
+    from test_gpu_decode import tiny
+    from test_oracle import make_model
+    from test_prefill import KV_TOL, LOGITS_TOL, fresh_caches, read_kv
+    cfg = tiny(2)
+    max_seq = 40
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=0, seed=7400 + T)
+    dev_layers, fmts = apply_formats(orc, cfg, layers, MIXED_PLAN, seed=7401 + T)
+    d = plain_ctx(rt, cfg, dev_layers, fmts, embed, fnorm, max_seq)
+    if chunk:
+        d.set_prefill_chunk(chunk)
+    toks = [(17 * i + 4) % cfg["vocab"] for i in range(T)]
+    got = d.prefill(toks, 0, mode)
+    ref_layers = fresh_caches(layers)
+    ref = orc.gemma3_prefill(cfg, ref_layers, embed, fnorm, toks, 0, mode)
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, ref) < LOGITS_TOL, rel_l2(got, ref)
+    for li in range(cfg["n_layers"]):
+        k, v = read_kv(d, cfg, li, T)
+        assert rel_l2(k, ref_layers[li]["k_cache"][:T]) < KV_TOL, li
+        assert rel_l2(v, ref_layers[li]["v_cache"][:T]) < KV_TOL, li
+    if mode == 1:
+        nxt = d.decode_step(9, T)
+        ref = orc.gemma3_decode_step(cfg, ref_layers, embed, fnorm, token=9, pos=T)
+        assert rel_l2(nxt, ref) < LOGITS_TOL
+    d.close()
+
+
+@pytest.mark.gpu
+def test_q4_k_m_layout_prefill_at_gemma3_4b_shape(rt, orc):
+    """Gemma-3-4B layer shapes with v and down in Q6_K: a 200-token prefill
+    equals 200 GPU decode steps (native Q6_K GEMV, pinned to the oracle above)."""
+    from test_gpu_decode import d2h
+    from test_oracle import make_model
+    from test_prefill import KV_TOL, LOGITS_TOL, read_kv
+    cfg = dict(rt.GEMMA3_4B, n_layers=2, global_every=2, vocab=4096)
+    T, max_seq = 200, 224
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=0, seed=7500)
+    plan = {0: dict(v=4, down=4), 1: dict(v=4, down=4)}
+    dev_layers, fmts = apply_formats(orc, cfg, layers, plan, seed=7501)
+    toks = [(89 * i + 3) % cfg["vocab"] for i in range(T)]
+    d1 = plain_ctx(rt, cfg, dev_layers, fmts, embed, fnorm, max_seq)
+    got = d1.prefill(toks, 0, 1)
+    d2 = plain_ctx(rt, cfg, dev_layers, fmts, embed, fnorm, max_seq)
+    for i, t in enumerate(toks):
+        d2.decode_step_async(t, i)
+    d2.synchronize()
+    ref = d2h(d2.logits_ptr(), cfg["vocab"])
+    assert rel_l2(got, ref) < LOGITS_TOL, rel_l2(got, ref)
+    for li in range(2):
+        k1, v1 = read_kv(d1, cfg, li, T)
+        k2, v2 = read_kv(d2, cfg, li, T)
+        assert rel_l2(k1, k2) < KV_TOL and rel_l2(v1, v2) < KV_TOL
+    d1.close()
+    d2.close()
