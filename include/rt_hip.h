@@ -189,7 +189,7 @@ rt_status rt_decode_set_layer(rt_decode *d, int32_t layer, const rt_gemma3_layer
  * (the device layouts of rt_gguf_load_linear_ex).  The reference's context
  * takes Q4_K or BF16 per projection (upload_linear_detect_type,
  * metal_decode.rs:1259-1277, with Q6_K/Q8_0 widened to BF16 at load); here
- * Q6_K and Q8_0 also run natively.  rt_decode_prefill needs Q4_K projections. */
+ * Q6_K and Q8_0 also run natively, in decode, batch and prefill. */
 rt_status rt_decode_set_layer_formats(rt_decode *d, int32_t layer, const rt_gemma3_layer *w,
                                       const int32_t *formats, int32_t device_ptrs);
 /* BF16 [vocab, hidden] embedding, also the tied lm_head (1097-1105), and the final norm gamma. */
