@@ -54,14 +54,15 @@ __global__ __launch_bounds__(256) void k_pf_embed(const int *__restrict__ tokens
 //   RESID:  x = base + rms(add)(1 + g_add);  x_out = x;  xn = rms(x)(1 + g_out)
 //   !RESID: x = add;                                     xn = rms(x)(1 + g_out)
 // `add` may be split-K partial sums.  With st_dig, xn is also staged as the
-// input of a batched GEMV.
-template <bool RESID>
-__global__ __launch_bounds__(256) void k_pf_norm(const float *__restrict__ base, RowsIn add,
+// input of a batched GEMV.  T = 1024 for a few rows (more loads in flight
+// per row when `add` is a sum of many slices), 256 otherwise.
+template <bool RESID, int T>
+__global__ __launch_bounds__(T) void k_pf_norm(const float *__restrict__ base, RowsIn add,
                                                  const float *__restrict__ g_add, const float *__restrict__ g_out,
                                                  float *__restrict__ x_out, float *__restrict__ xn_out, int H,
                                                  float eps, int8_t *__restrict__ st_dig) {
-  constexpr int PER = 4;
-  __shared__ float red[4];
+  constexpr int PER = 1024 / T;
+  __shared__ float red[T / 64];
   const int t = (int)blockIdx.x;
   const size_t off = (size_t)t * (H / 4);
   const int F4 = H / 4;
@@ -70,18 +71,18 @@ __global__ __launch_bounds__(256) void k_pf_norm(const float *__restrict__ base,
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
-    const int f = threadIdx.x + i * 256;
+    const int f = threadIdx.x + i * T;
     x[i] = f < F4 ? rows_in4(add, t, 4 * f) : make_float4(0.f, 0.f, 0.f, 0.f);
     ss += sumsq4(x[i]);
   }
   if constexpr (RESID) {
-    const float ra = rms_inv_from_sumsq(block_sum<256>(ss, red), inv_k, eps);
+    const float ra = rms_inv_from_sumsq(block_sum<T>(ss, red), inv_k, eps);
     const float4 *b4 = reinterpret_cast<const float4 *>(base) + off;
     float4 *xo = reinterpret_cast<float4 *>(x_out) + off;
     ss = 0.f;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int f = threadIdx.x + i * 256;
+      const int f = threadIdx.x + i * T;
       if (f < F4) {
         x[i] = add4(b4[f], norm4(x[i], ra, reinterpret_cast<const float4 *>(g_add)[f]));
         xo[f] = x[i];
@@ -89,17 +90,29 @@ __global__ __launch_bounds__(256) void k_pf_norm(const float *__restrict__ base,
       }
     }
   }
-  const float rx = rms_inv_from_sumsq(block_sum<256>(ss, red), inv_k, eps);
+  const float rx = rms_inv_from_sumsq(block_sum<T>(ss, red), inv_k, eps);
   float4 *xn = reinterpret_cast<float4 *>(xn_out) + off;
   float *st_stats = st_dig ? mb_stats(st_dig, H) : nullptr;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
-    const int f = threadIdx.x + i * 256;
-    if (i * 256 >= F4) break;  // block-uniform
+    const int f = threadIdx.x + i * T;
+    if (i * T >= F4) break;  // block-uniform
     const float4 v = norm4(x[i], rx, reinterpret_cast<const float4 *>(g_out)[min(f, F4 - 1)]);
     if (f < F4) xn[f] = v;
     if (st_dig) mb_stage4(st_dig, st_stats, t, min(f, F4 - 1) >> 4, f & 15, v, f < F4);  // 16 lanes per chunk
   }
+}
+
+template <bool RESID>
+hipError_t launch_pf_norm(int n, hipStream_t st, const float *base, RowsIn add, const float *g_add,
+                          const float *g_out, float *x_out, float *xn_out, int H, float eps, int8_t *st_dig) {
+  if (n <= 64)
+    hipLaunchKernelGGL((k_pf_norm<RESID, 1024>), dim3(n), dim3(1024), 0, st, base, add, g_add, g_out, x_out, xn_out, H,
+                       eps, st_dig);
+  else
+    hipLaunchKernelGGL((k_pf_norm<RESID, 256>), dim3(n), dim3(256), 0, st, base, add, g_add, g_out, x_out, xn_out, H,
+                       eps, st_dig);
+  return hipGetLastError();
 }
 
 // One wave per (row, head): q heads in place, k heads into the cache row
@@ -528,9 +541,10 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
   for (int li = 0; li < s.n_layers; ++li) {
     const LayerArgs &L = layers[li];
     if (li == 0)
-      PF_CHECK(hipLaunchKernelGGL(k_pf_norm<false>, dim3(n), dim3(256), 0, st, nullptr, rows_plain(b.hid, H), nullptr,
+      PF_TRY(launch_pf_norm<false>(n, st, nullptr, rows_plain(b.hid, H), nullptr,
                                   L.g_in, nullptr, b.xn, H, a.eps, stage));
-    PF_TRY(proj(b.xn, H, {L.fmt[kProjQ], L.fmt[kProjK], L.fmt[kProjV]}, {MbMat{L.wq, b.q, QD, 0, 0}, MbMat{L.wk, b.k, KVD, 0, 0}, MbMat{L.wv, b.v, KVD, 0, 0}},
+    PF_TRY(proj(b.xn, H, {L.fmt[kProjQ], L.fmt[kProjK], L.fmt[kProjV]},
+                {MbMat{L.wq, b.q, QD, 0, 0}, MbMat{L.wk, b.k, KVD, 0, 0}, MbMat{L.wv, b.v, KVD, 0, 0}},
                 {&vq, &vk, &vv}));
     const int items = n * (nq + nkv);
     const int cs_off = L.global ? D : 0;
@@ -566,15 +580,16 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
     if (D == 256) PF_TRY(launch_pf_attn<256>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa, stage));
     else PF_TRY(launch_pf_attn<128>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa, stage));
     PF_TRY(proj(b.attn, QD, {L.fmt[kProjO]}, {MbMat{L.wo, b.o, H, 0, 0}}, {&vo}));
-    PF_CHECK(hipLaunchKernelGGL(k_pf_norm<true>, dim3(n), dim3(256), 0, st, b.hid, vo, L.g_post_attn, L.g_pre_ffn,
+    PF_TRY(launch_pf_norm<true>(n, st, b.hid, vo, L.g_post_attn, L.g_pre_ffn,
                                 b.x2, b.xn, H, a.eps, stage));
-    PF_TRY(proj(b.xn, H, {L.fmt[kProjGate], L.fmt[kProjUp]}, {MbMat{L.wgate, b.g, F, 0, 0}, MbMat{L.wup, b.u, F, 0, 0}}, {&vg, &vu}));
+    PF_TRY(proj(b.xn, H, {L.fmt[kProjGate], L.fmt[kProjUp]},
+                {MbMat{L.wgate, b.g, F, 0, 0}, MbMat{L.wup, b.u, F, 0, 0}}, {&vg, &vu}));
     const size_t n4 = (size_t)n * F / 4;
     const unsigned eg = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
     PF_CHECK(hipLaunchKernelGGL(k_pf_gelu_mul, dim3(eg), dim3(256), 0, st, vg, vu, b.g, n, F, stage));
     PF_TRY(proj(b.g, F, {L.fmt[kProjDown]}, {MbMat{L.wdown, b.dn, H, 0, 0}}, {&vd}));
     if (li + 1 < s.n_layers)
-      PF_CHECK(hipLaunchKernelGGL(k_pf_norm<true>, dim3(n), dim3(256), 0, st, b.x2, vd, L.g_post_ffn,
+      PF_TRY(launch_pf_norm<true>(n, st, b.x2, vd, L.g_post_ffn,
                                   layers[li + 1].g_in, b.hid, b.xn, H, a.eps, stage));
   }
   const LayerArgs &last = layers[s.n_layers - 1];
@@ -582,7 +597,7 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
     // the final residual and final norm of every row (transformer4.rs:2131-2139,
     // 2370-2380), then the tied lm_head of the last row or of every row
     float *xn_out = plan.logits == RowsPlan::kEveryRow ? plan.xn_b : b.xn;
-    PF_CHECK(hipLaunchKernelGGL(k_pf_norm<true>, dim3(n), dim3(256), 0, st, b.x2, vd, last.g_post_ffn, a.g_final,
+    PF_TRY(launch_pf_norm<true>(n, st, b.x2, vd, last.g_post_ffn, a.g_final,
                                 b.hid, xn_out, H, a.eps, nullptr));
     if (plan.logits == RowsPlan::kEveryRow)
       PF_TRY(enqueue_lm_head_batch(s, a, plan.xn_b, plan.logits_b, n, st));

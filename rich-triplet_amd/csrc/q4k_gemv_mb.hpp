@@ -40,36 +40,32 @@ struct RowsIn {
 };
 __host__ __device__ inline RowsIn rows_plain(const float *p, int cols) { return RowsIn{p, 1, 0, cols, 0}; }
 
-// Loads of four slices are issued together, then added in slice order.
+// Slices are loaded eight at a time (the last group at clamped, in-bounds
+// slices that are not added), all eight in flight, then added in slice order.
 __device__ __forceinline__ float4 rows_in4(const RowsIn &r, int t, int i) {
   const float *b = r.p + (size_t)t * r.row_stride + r.col_off + i;
   float4 s = *reinterpret_cast<const float4 *>(b);
-  int z = 1;
-  for (; z + 4 <= r.ks; z += 4) {
-    float4 v[4];
+  for (int z = 1; z < r.ks; z += 8) {
+    float4 v[8];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const float4 *>(b + (size_t)(z + u) * r.slice_stride);
+    for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const float4 *>(b + (size_t)min(z + u, r.ks - 1) * r.slice_stride);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) s.x += v[u].x, s.y += v[u].y, s.z += v[u].z, s.w += v[u].w;
-  }
-  for (; z < r.ks; ++z) {
-    const float4 v = *reinterpret_cast<const float4 *>(b + (size_t)z * r.slice_stride);
-    s.x += v.x, s.y += v.y, s.z += v.z, s.w += v.w;
+    for (int u = 0; u < 8; ++u)
+      if (z + u < r.ks) s.x += v[u].x, s.y += v[u].y, s.z += v[u].z, s.w += v[u].w;
   }
   return s;
 }
 __device__ __forceinline__ float rows_in1(const RowsIn &r, int t, int i) {
   const float *b = r.p + (size_t)t * r.row_stride + r.col_off + i;
   float s = *b;
-  int z = 1;
-  for (; z + 4 <= r.ks; z += 4) {
-    float v[4];
+  for (int z = 1; z < r.ks; z += 8) {
+    float v[8];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = b[(size_t)(z + u) * r.slice_stride];
+    for (int u = 0; u < 8; ++u) v[u] = b[(size_t)min(z + u, r.ks - 1) * r.slice_stride];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) s += v[u];
+    for (int u = 0; u < 8; ++u)
+      if (z + u < r.ks) s += v[u];
   }
-  for (; z < r.ks; ++z) s += b[(size_t)z * r.slice_stride];
   return s;
 }
 
