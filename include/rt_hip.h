@@ -127,7 +127,7 @@ rt_status rt_q8_0_gemv(const void *w, const float *x, float *y, int64_t n, int64
  * the BF16-widened Q6_K / Q8_0 weights, and matmul_q4k_t for RT_LINEAR_Q4K
  * (as rt_q4k_gemm_f32).  Non-Q4_K rows are widened to f16 with a
  * power-of-two scale per row, A likewise, f32 accumulation on the matrix
- * cores; k % 256 == 0 (Q6_K, Q4_K) or k % 32 == 0; device pointers, a and w
+ * cores; k % 256 == 0 (Q6_K, Q4_K) or k % 64 == 0; device pointers, a and w
  * 16-byte aligned.  Uses the per-thread workspace of rt_q4k_gemm_f32, about
  * (m + n) * k * 2 bytes. */
 rt_status rt_linear_gemm_f32(int32_t fmt, const void *w, const float *a, float *c, int64_t m, int64_t n, int64_t k,

@@ -171,7 +171,7 @@ rt_status rt_linear_gemm_f32(int32_t fmt, const void *w, const float *a, float *
   if (m <= 0 || n <= 0 || k <= 0)
     return set_error(RT_EINVAL, "%s: m=%lld n=%lld k=%lld must be positive", who, (long long)m, (long long)n,
                      (long long)k);
-  const int align = fmt == RT_LINEAR_Q6K ? 256 : 32;
+  const int align = fmt == RT_LINEAR_Q6K ? 256 : 64;  // the f16 GEMM moves K in stages of 64
   if (k % align != 0) return set_error(RT_EINVAL, "%s: k=%lld must be a multiple of %d", who, (long long)k, align);
   if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX) return set_error(RT_EINVAL, "%s: m, n or k exceeds int32", who);
   if (!a || !w || !c) return set_error(RT_EINVAL, "%s: null pointer", who);

@@ -14,14 +14,12 @@
 #include <algorithm>
 
 #include "../../include/rt_hip.h"
+#include "mfma_common.hpp"
 #include "rt_device.hpp"
 #include "rt_kernels.hpp"
 
 namespace rt {
 namespace {
-
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 // Element e of row n of a projection in format FMT (decode_*_to_f32 values).
 template <int FMT>
@@ -63,86 +61,210 @@ __global__ __launch_bounds__(256) void k_rows_to_f16(const uint8_t *__restrict__
     w16[(size_t)n * K + e] = (_Float16)__builtin_amdgcn_ldexpf(proj_value<FMT>(W, N, K, n, e), -ex);
 }
 
-// C[M][N] = 2^(ea[m]+ew[n]) * sum_k a16[m][k] w16[n][k].  128 x 128 tile per
-// workgroup, four waves of 64 x 64 (2 x 2 v_mfma_f32_32x32x16_f16 tiles),
-// K in steps of 32 through double-buffered LDS with the next step's global
-// loads in registers during the MFMAs.  Lane l: A row / B column l%32,
-// halves 8*(l/32) + [0, 8) of a 16-wide k step.
-constexpr int kFP = 40;  // LDS row pitch in halves (32 + 8): rows 80 B apart
-__global__ __launch_bounds__(256) void k_gemm_f16w(const _Float16 *__restrict__ a16, const int *__restrict__ ea,
-                                                   const _Float16 *__restrict__ w16, const int *__restrict__ ew,
-                                                   float *__restrict__ c, int M, int N, int K) {
-  __shared__ __attribute__((aligned(16))) _Float16 as[2][128 * kFP], bs[2][128 * kFP];
-  const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
-  const int l32 = lane & 31, g = lane >> 5;
-  const int m0 = (int)blockIdx.y * 128, n0 = (int)blockIdx.x * 128;
-  // global -> LDS copy: thread t moves 32 B of row t/2 (halves 16*(t%2) .. +16)
-  const int cr = tid >> 1, ch = 16 * (tid & 1);
-  const _Float16 *ga = a16 + (size_t)min(m0 + cr, M - 1) * K + ch;
-  const _Float16 *gb = w16 + (size_t)min(n0 + cr, N - 1) * K + ch;
-  uint4 ra[2], rb[2];
-  auto gload = [&](int k0) __attribute__((always_inline)) {
-    ra[0] = *reinterpret_cast<const uint4 *>(ga + k0);
-    ra[1] = *reinterpret_cast<const uint4 *>(ga + k0 + 8);
-    rb[0] = *reinterpret_cast<const uint4 *>(gb + k0);
-    rb[1] = *reinterpret_cast<const uint4 *>(gb + k0 + 8);
-  };
-  auto sstore = [&](int buf) __attribute__((always_inline)) {
-    *reinterpret_cast<uint4 *>(&as[buf][cr * kFP + ch]) = ra[0];
-    *reinterpret_cast<uint4 *>(&as[buf][cr * kFP + ch + 8]) = ra[1];
-    *reinterpret_cast<uint4 *>(&bs[buf][cr * kFP + ch]) = rb[0];
-    *reinterpret_cast<uint4 *>(&bs[buf][cr * kFP + ch + 8]) = rb[1];
-  };
-  floatx16 acc[2][2];
+// C[M][N] = 2^(ea[m]+ew[n]) * sum_k a16[m][k] w16[n][k] on
+// v_mfma_f32_32x32x16_f16.  C tile 256 x 256 per workgroup of four waves
+// (2 x 2), each wave 128 x 128 = 4 x 4 MFMA tiles with its 256 accumulator
+// registers in AGPRs (one wave per SIMD issues MFMAs back to back).
+//   Operands: K moves in stages of 64 through two LDS slots per operand,
+//   filled by global_load_lds_dwordx4 (no VGPRs), each copy instruction
+//   moving whole 128-B row pieces.  A slot row is 128 B (8 segments of 8
+//   halves) and holds logical segment s at physical segment
+//   s ^ ((row >> 1) & 7), so the 16 lanes served together by a ds_read_b128
+//   (16 consecutive rows) hit 16 distinct bank groups.  Lane l of an MFMA
+//   reads row l%32 of its 32-row tile; k-step t of a stage is logical
+//   segment 2t + l/32.
+//   Schedule per stage: each k-step's MFMAs run while the next k-step's
+//   fragments are read; before the last k-step's MFMAs, the barrier that
+//   publishes the next stage (and frees this slot), the refill of this slot
+//   two stages ahead, and the next stage's first fragment reads.
+//   Epilogue: each wave stages 32-row slices of its tile in LDS (row pitch
+//   136 floats: the two row groups of a 4-byte write land on disjoint banks)
+//   and writes C rows with 16-byte stores.
+//   Measured on the config-4 shapes (4608 x 9216 x 3072): loads and LDS reads
+//   alone take about 60% of the kernel's time; the two-slot ring keeps one
+//   stage in flight, which is what bounds the overlap with the MFMAs.
+constexpr int kFTile = 256, kFK = 64;
+constexpr int kFSlot = kFTile * kFK * 2;  // 32 KB per operand per stage
+constexpr int kFPitch = 136;
+
+__global__ __launch_bounds__(256) void k_gemm_f16_t256(const _Float16 *__restrict__ a16, const int *__restrict__ ea,
+                                                       const _Float16 *__restrict__ w16, const int *__restrict__ ew,
+                                                       float *__restrict__ c, int M, int N, int K, int tiles_m,
+                                                       int tiles_n, int ksplit) {
+  // [A slot 0 | A slot 1 | B slot 0 | B slot 1]; the epilogue reuses the start
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * kFSlot];
+  auto slot_a = [&](int i) __attribute__((always_inline)) { return lds + i * kFSlot; };
+  auto slot_b = [&](int i) __attribute__((always_inline)) { return lds + (2 + i) * kFSlot; };
+  const int tid = (int)threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  // Workgroup b runs on XCD b % 8: give each XCD a contiguous run of tiles,
+  // walked in groups of eight tile rows so neighbours share A and W in L2.
+  const int ntiles = tiles_m * tiles_n, per_xcd = (ntiles + 7) / 8;
+  const int bid = (int)blockIdx.x;
+  const int tile = ntiles % 8 == 0 ? (bid & 7) * per_xcd + (bid >> 3) : bid;
+  const int group = tile / (8 * tiles_n), in_group = tile % (8 * tiles_n);
+  const int gm = min(8, tiles_m - group * 8);
+  const int m0 = (group * 8 + in_group % gm) * kFTile, n0 = (in_group / gm) * kFTile;
+  // Split-K: blockIdx.y = s takes stages [s*nk/ksplit, (s+1)*nk/ksplit) and,
+  // with ksplit > 1, writes its scaled partial tile to c + s*M*N.
+  const int nk_all = K / kFK, split = (int)blockIdx.y;
+  const int kb = split * nk_all / ksplit, nk = (split + 1) * nk_all / ksplit - kb;  // nk >= 1 (host)
+  if (ksplit > 1) c += (size_t)split * M * N;
+
+  // Copies: wave w moves rows [64w, 64w+64) of both operands, eight 1 KB
+  // instructions each; lane -> row 8*(8w+i) + lane/8, physical segment lane%8.
+  const _Float16 *a_src[8], *b_src[8];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = floatx16{};
-  const int nk = K / 32;
-  gload(0);
-  sstore(0);
-  __syncthreads();
-#pragma unroll 1
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) gload(32 * (kt + 1));
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      half8 af[2], bf[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        af[i] = *reinterpret_cast<const half8 *>(&as[buf][(64 * wm + 32 * i + l32) * kFP + 16 * ks + 8 * g]);
-        bf[i] = *reinterpret_cast<const half8 *>(&bs[buf][(64 * wn + 32 * i + l32) * kFP + 16 * ks + 8 * g]);
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-    if (kt + 1 < nk) sstore(buf ^ 1);
-    __syncthreads();
+  for (int i = 0; i < 8; ++i) {
+    const int r = 64 * wave + 8 * i + (lane >> 3);
+    const int seg = (lane & 7) ^ ((r >> 1) & 7);
+    a_src[i] = a16 + (size_t)min(m0 + r, M - 1) * K + 8 * seg;
+    b_src[i] = w16 + (size_t)min(n0 + r, N - 1) * K + 8 * seg;
   }
-  // register r of tile (i, j): C[64wm + 32i + 8(r/4) + 4g + r%4][64wn + 32j + l32]
+  auto issue = [&](int kt, int slot) __attribute__((always_inline)) {  // kt: stage of this split
+    uint8_t *da = slot_a(slot), *db = slot_b(slot);
+    kt += kb;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int col = n0 + 64 * wn + 32 * j + l32;
-    if (col >= N) continue;
-    const int ec = ew[col];
+    for (int i = 0; i < 8; ++i)
+      __builtin_amdgcn_global_load_lds((gvoid *)(a_src[i] + (size_t)kt * kFK), (lvoid *)(da + (8 * wave + i) * 1024),
+                                       16, 0, 0);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 8; ++i)
+      __builtin_amdgcn_global_load_lds((gvoid *)(b_src[i] + (size_t)kt * kFK), (lvoid *)(db + (8 * wave + i) * 1024),
+                                       16, 0, 0);
+  };
+  int ra[4], rb[4];  // this lane's fragment rows
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (row < M) c[(size_t)row * N + col] = __builtin_amdgcn_ldexpf(acc[i][j][r], ea[row] + ec);
+  for (int i = 0; i < 4; ++i) {
+    ra[i] = 128 * wm + 32 * i + l32;
+    rb[i] = 128 * wn + 32 * i + l32;
+  }
+  auto frag_off = [&](int r, int s) __attribute__((always_inline)) { return r * 128 + 16 * (s ^ ((r >> 1) & 7)); };
+  auto read = [&](int slot, int s, u32x4 (&af)[4], u32x4 (&bf)[4]) __attribute__((always_inline)) {
+    const uint8_t *pa = slot_a(slot), *pb = slot_b(slot);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      af[i] = lds_read16(pa + frag_off(ra[i], s));
+      bf[i] = lds_read16(pb + frag_off(rb[i], s));
+    }
+  };
+  auto await = [&](u32x4 (&af)[4], u32x4 (&bf)[4]) __attribute__((always_inline)) {
+    lds_wait(af[0], af[1], af[2], af[3]);
+    lds_wait(bf[0], bf[1], bf[2], bf[3]);
+  };
+  floatx16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = floatx16{};
+  auto mfma16 = [&](const u32x4 (&af)[4], const u32x4 (&bf)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, af[i]),
+                                                            __builtin_bit_cast(half8, bf[j]), acc[i][j], 0, 0, 0);
+  };
+
+  issue(0, 0);
+  if (nk > 1) issue(1, 1);
+  u32x4 a0[4], b0[4], a1[4], b1[4];
+  if (nk > 1) wait_vmcnt<16>();  // stage 0 landed, stage 1 may be in flight
+  else wait_vmcnt<0>();
+  wg_barrier();
+  read(0, g, a0, b0);
+  await(a0, b0);
+  auto step = [&](int kt, int slot) __attribute__((always_inline)) {
+    read(slot, 2 + g, a1, b1);
+    mfma16(a0, b0);
+    await(a1, b1);
+    read(slot, 4 + g, a0, b0);
+    mfma16(a1, b1);
+    await(a0, b0);
+    read(slot, 6 + g, a1, b1);
+    mfma16(a0, b0);
+    await(a1, b1);
+    if (kt + 1 < nk) {
+      wait_vmcnt<0>();  // stage kt+1, the only one in flight, has landed
+      wg_barrier();     // everywhere, and this slot is read out everywhere
+      __builtin_amdgcn_sched_barrier(0);
+      if (kt + 2 < nk) issue(kt + 2, slot);
+      __builtin_amdgcn_sched_barrier(0);
+      read(slot ^ 1, g, a0, b0);
+    }
+    mfma16(a1, b1);
+    if (kt + 1 < nk) await(a0, b0);
+  };
+  int kt = 0;
+  for (; kt + 2 <= nk; kt += 2) {
+    step(kt, 0);
+    step(kt + 1, 1);
+  }
+  if (kt < nk) step(kt, 0);
+
+  // Epilogue, in four passes of 32 rows of every wave's tile (pass i = MFMA
+  // row tile i).  Register r of tile (i, j) is element (32i + 8(r/4) + 4g +
+  // r%4, 32j + l32) of the wave tile.
+  int ec[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) ec[j] = ew[min(n0 + rb[j], N - 1)];
+  wg_barrier();  // the slots are free: every wave's last fragments are read
+  float *stage = reinterpret_cast<float *>(lds) + wave * 32 * kFPitch;  // 17 KB per wave
+  const bool vec = (N & 3) == 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    int er[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) er[r] = ea[min(m0 + 128 * wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3), M - 1)];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        stage[(8 * (r >> 2) + 4 * g + (r & 3)) * kFPitch + 32 * j + l32] =
+            __builtin_amdgcn_ldexpf(acc[i][j][r], er[r] + ec[j]);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // lane -> rows 2q + l/32 of the slice, columns 4*(l%32) .. +3
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int rl = 2 * q + g;
+      const int row = m0 + 128 * wm + 32 * i + rl, col = n0 + 128 * wn + 4 * l32;
+      const float4 v = *reinterpret_cast<const float4 *>(stage + rl * kFPitch + 4 * l32);
+      if (row < M) {
+        float *dst = c + (size_t)row * N + col;
+        if (vec && col + 4 <= N) {
+          *reinterpret_cast<float4 *>(dst) = v;
+        } else {
+          if (col < N) dst[0] = v.x;
+          if (col + 1 < N) dst[1] = v.y;
+          if (col + 2 < N) dst[2] = v.z;
+          if (col + 3 < N) dst[3] = v.w;
+        }
       }
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 }
 
 }  // namespace
 
+// Split-K count: enough workgroups to cover the 256 CUs when the output has
+// few 256 x 256 tiles (M = 512, N = 2560: 20 tiles), at least 8 stages
+// (K = 512) per split.
+static int proj_ksplit(int M, int N, int K) {
+  const int ntiles = ((M + kFTile - 1) / kFTile) * ((N + kFTile - 1) / kFTile);
+  return std::max(1, std::min(256 / ntiles, (K / kFK) / 8));
+}
+
 size_t proj_gemm_workspace_bytes(int M, int N, int K) {
   auto r256 = [](size_t b) { return (b + 255) & ~size_t(255); };
-  return r256((size_t)M * K * 2) + r256((size_t)M * 4) + r256((size_t)N * K * 2) + r256((size_t)N * 4);
+  const int ks = proj_ksplit(M, N, K);
+  return r256((size_t)M * K * 2) + r256((size_t)M * 4) + r256((size_t)N * K * 2) + r256((size_t)N * 4) +
+         (ks > 1 ? (size_t)ks * M * N * 4 : 0);
 }
 
 hipError_t launch_proj_gemm(const float *a, int fmt, const void *w, float *c, int M, int N, int K, void *ws,
@@ -156,6 +278,7 @@ hipError_t launch_proj_gemm(const float *a, int fmt, const void *w, float *c, in
   _Float16 *w16 = reinterpret_cast<_Float16 *>(p);
   p += r256((size_t)N * K * 2);
   int *ew = reinterpret_cast<int *>(p);
+  p += r256((size_t)N * 4);
   const uint8_t *wb = static_cast<const uint8_t *>(w);
   switch (fmt) {
     case RT_LINEAR_Q6K: hipLaunchKernelGGL(k_rows_to_f16<RT_LINEAR_Q6K>, dim3(N), dim3(256), 0, s, wb, N, K, w16, ew); break;
@@ -166,9 +289,14 @@ hipError_t launch_proj_gemm(const float *a, int fmt, const void *w, float *c, in
   hipError_t e = hipGetLastError();
   if (e == hipSuccess) e = launch_gemm_prep_a(a, M, K, a16, ea, s);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_gemm_f16w, dim3((N + 127) / 128, (M + 127) / 128), dim3(256), 0, s, a16, ea, w16, ew, c, M, N,
-                     K);
-  return hipGetLastError();
+  const int tiles_m = (M + kFTile - 1) / kFTile, tiles_n = (N + kFTile - 1) / kFTile;
+  const int ks = proj_ksplit(M, N, K);
+  float *out = ks > 1 ? reinterpret_cast<float *>(p) : c;
+  hipLaunchKernelGGL(k_gemm_f16_t256, dim3(tiles_m * tiles_n, ks), dim3(256), 0, s, a16, ea, w16, ew, out, M, N, K,
+                     tiles_m, tiles_n, ks);
+  e = hipGetLastError();
+  if (e == hipSuccess && ks > 1) e = launch_gemm_splitk_sum(out, c, (size_t)M * N, ks, s);
+  return e;
 }
 
 }  // namespace rt

@@ -26,16 +26,12 @@
 
 #include <algorithm>
 
+#include "mfma_common.hpp"
 #include "rt_device.hpp"
 #include "rt_kernels.hpp"
 
 namespace rt {
 namespace {
-
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-// Native vectors for staging registers: HIP's uint4 is a union-wrapped struct
-// whose copies become memcpys, which LLVM turns back into global reloads.
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBK = 64;  // K per pipeline stage = one Q4_K chunk (32 qs bytes, 2 sub-blocks)
 
@@ -123,43 +119,6 @@ __global__ __launch_bounds__(256) void k_gemm_prep(const TA *__restrict__ a, _Fl
 // bytes of its own column straight into the MFMA B operand, so no
 // dequantised weight is written back to LDS.
 // ---------------------------------------------------------------------------
-typedef float floatx16 __attribute__((ext_vector_type(16)));
-typedef __attribute__((address_space(1))) void gvoid;
-typedef __attribute__((address_space(3))) void lvoid;
-
-// s_waitcnt with only a vector-memory bound (expcnt / lgkmcnt left open), gfx9 encoding.
-template <int N>
-RT_DEV void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-// s_waitcnt lgkmcnt(0) alone (vmcnt 63 and expcnt 7 mean "no wait").
-RT_DEV void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); }
-// Workgroup barrier that keeps memory operations on their side of it in the
-// compiler (s_barrier alone is a no-memory intrinsic) without the release
-// fence's wait for every outstanding load.
-RT_DEV void wg_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// LDS reads the compiler does not see as LDS reads.  Its wait insertion
-// cannot tell which ring slot an in-flight global_load_lds targets once the
-// loop back-edge merges its state, and would drain every copy (vmcnt(0))
-// before the first read of each block.  The kernel orders the copies itself
-// (explicit vmcnt + barrier per chunk) and waits for these reads with
-// lds_wait, whose register operands keep every consumer after the wait.
-RT_DEV u32x4 lds_read16(const void *p) {
-  u32x4 v;
-  const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a));
-  return v;
-}
-RT_DEV void lds_wait(u32x4 &a, u32x4 &b, u32x4 &c, u32x4 &d) {
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
-}
-
 // Eight f16 weights of one k-step from two qs words (low or high nibbles).
 // v_perm builds halves 1024+q (low nibbles) or 1024+16q (high nibbles), and
 // each v_fma_mix computes f16(s*h - c) from them in f32 with one rounding.
@@ -610,6 +569,12 @@ int gemm_ksplit(int M, int N, int K) {
   return max(1, min(by_cus, by_k));
 }
 
+hipError_t launch_gemm_splitk_sum(const float *part, float *c, size_t mn, int ksplit, hipStream_t s) {
+  const unsigned grid = (unsigned)std::min<size_t>((mn / 4 + 255) / 256 + 1, 2048);
+  hipLaunchKernelGGL(k_gemm_splitk_sum, dim3(grid), dim3(256), 0, s, part, c, mn, ksplit);
+  return hipGetLastError();
+}
+
 hipError_t launch_gemm_prep_a(const float *a, int M, int K, _Float16 *a16, int *ea, hipStream_t s) {
   hipLaunchKernelGGL((k_gemm_prep<float>), dim3(M), dim3(256), 0, s, a, a16, ea, nullptr, nullptr, M, 0, K);
   return hipGetLastError();
@@ -650,9 +615,8 @@ hipError_t launch_q4k_gemm(const void *a, bool a_bf16, const void *w, float *c, 
                        K, tiles_m, tiles_n, ks);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const size_t mn = (size_t)M * N;
-    const unsigned grid = (unsigned)std::min<size_t>((mn / 4 + 255) / 256 + 1, 2048);
-    hipLaunchKernelGGL(k_gemm_splitk_sum, dim3(grid), dim3(256), 0, s, part, c, mn, ks);
+    e = launch_gemm_splitk_sum(part, c, (size_t)M * N, ks, s);
+    if (e != hipSuccess) return e;
   } else if (M <= 1024)
     hipLaunchKernelGGL(k_q4k_gemm_w8b<1>, dim3(tiles_m * tiles_n), dim3(512), 0, s, a16, ea, wb, ew, c, M, N, K,
                        tiles_m, tiles_n, 1);

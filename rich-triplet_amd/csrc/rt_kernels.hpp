@@ -20,6 +20,8 @@ hipError_t launch_q6k_dequant(const void *w, size_t n_blocks, float *out, hipStr
 hipError_t launch_q8_0_dequant(const void *w, size_t n_elem, float *out, hipStream_t s);
 hipError_t launch_q6k_gemv(const void *W, const float *x, float *y, int N, int K, hipStream_t s);
 hipError_t launch_q8_0_gemv(const void *W, const float *x, float *y, int N, int K, hipStream_t s);
+// c[i] = sum over s < ksplit of part[s*mn + i], in split order.
+hipError_t launch_gemm_splitk_sum(const float *part, float *c, size_t mn, int ksplit, hipStream_t s);
 // A (f32 [M][K]) -> f16 with a per-row power-of-two exponent (the GEMMs' A prep).
 hipError_t launch_gemm_prep_a(const float *a, int M, int K, _Float16 *a16, int *ea, hipStream_t s);
 // C[M,N] = A[M,K] . W[N,K]^T for a projection stored as RT_LINEAR_Q6K, _Q8_0

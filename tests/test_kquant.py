@@ -346,8 +346,12 @@ def test_oracle_mixed_prefill_equals_decode_steps(orc):
         assert rel_l2(La["v_cache"], Lb["v_cache"]) < 2e-5
 
 
-GEMM_CASES = [(4, 1, 256, 512), (4, 77, 300, 2560), (5, 130, 200, 96), (5, 8, 1000, 1024), (2, 5, 129, 64),
-              (2, 200, 384, 2048), (1, 33, 256, 512)]
+# partial 256-row/column tiles, K of one to five stages of 64 and long K, and
+# tile grids with a multiple of 8 tiles (the per-XCD tile order) and without
+GEMM_CASES = [(4, 1, 256, 512), (4, 77, 300, 2560), (5, 130, 200, 192), (5, 8, 1000, 1024), (2, 5, 129, 64),
+              (2, 200, 384, 2048), (1, 33, 256, 512), (2, 512, 1024, 256), (5, 1100, 520, 320),
+              (4, 600, 2048, 1024), (2, 300, 260, 128),
+              (2, 300, 512, 4096), (4, 64, 2560, 10240)]  # split-K (8 and 20 slices)
 
 
 @pytest.mark.gpu
@@ -387,6 +391,8 @@ def test_linear_gemm_rejects_bad_shapes(rt):
         rt.linear_gemm_f32(4, 16, 16, 16, 1, 1, 96)  # Q6_K rows are 256-element blocks
     with pytest.raises(rt.RtError):
         rt.linear_gemm_f32(5, 16, 16, 16, 0, 1, 64)
+    with pytest.raises(rt.RtError):
+        rt.linear_gemm_f32(2, 16, 16, 16, 1, 1, 96)  # K moves in stages of 64
 
 
 def plain_ctx(rt, cfg, dev_layers, fmts, embed, fnorm, max_seq):
