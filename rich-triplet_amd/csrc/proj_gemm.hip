@@ -7,7 +7,7 @@
 // widened to f16 with a power-of-two scale 2^-ew[n] (max |w'| in
 // [2^14, 2^15), exact for BF16, Q8_0 and Q6_K codes times their f16 scales up
 // to f16 rounding), A gets the same treatment per row (k_gemm_prep), and
-// k_gemm_f16w multiplies on v_mfma_f32_32x32x16_f16 with the scales
+// k_gemm_f16_t256 multiplies on v_mfma_f32_32x32x16_f16 with the scales
 // restored in the epilogue, as the Q4_K GEMM does.
 #include <hip/hip_runtime.h>
 
