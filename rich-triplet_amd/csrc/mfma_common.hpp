@@ -53,4 +53,55 @@ RT_DEV void lds_wait(u32x4 &a, u32x4 &b, u32x4 &c, u32x4 &d) {
 }
 
 
+// Stores a wave's C tile from v_mfma_f32_32x32x16 accumulators: four row
+// tiles of 32 rows by NT column tiles of 32 columns, register r of tile (i, j)
+// being C[row0 + 32i + 8(r/4) + 4(lane/32) + r%4][col0 + 32j + lane%32],
+// scaled by 2^(ea[row] + ecol[j]).  One 32-row slice at a time goes through
+// `stage` (32 x (32NT + 8) floats of LDS that only this wave uses; the pitch
+// puts the two row groups of a 4-byte write on disjoint banks) and leaves as
+// whole rows in 16-byte lanes, so no store waits on a load and every store
+// instruction writes full row pieces.
+template <int NT>
+RT_DEV void store_c_tile(const floatx16 (&acc)[4][NT], float *stage, float *c, int M, int N, int row0, int col0,
+                         const int *ea, const int (&ecol)[NT]) {
+  constexpr int P = 32 * NT + 8, F4 = 8 * NT, RPI = 64 / F4;
+  const int lane = (int)(threadIdx.x & 63), g = lane >> 5, l32 = lane & 31;
+  const bool vec = (N & 3) == 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    int er[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) er[r] = ea[min(row0 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3), M - 1)];
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        stage[(8 * (r >> 2) + 4 * g + (r & 3)) * P + 32 * j + l32] =
+            __builtin_amdgcn_ldexpf(acc[i][j][r], er[r] + ecol[j]);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int q = 0; q < 32 / RPI; ++q) {
+      const int rl = q * RPI + lane / F4, f = lane % F4;
+      const int row = row0 + 32 * i + rl, col = col0 + 4 * f;
+      const float4 v = *reinterpret_cast<const float4 *>(stage + rl * P + 4 * f);
+      if (row < M) {
+        float *dst = c + (size_t)row * N + col;
+        if (vec && col + 4 <= N) {
+          *reinterpret_cast<float4 *>(dst) = v;
+        } else {
+          if (col < N) dst[0] = v.x;
+          if (col + 1 < N) dst[1] = v.y;
+          if (col + 2 < N) dst[2] = v.z;
+          if (col + 3 < N) dst[3] = v.w;
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
 }  // namespace rt

@@ -77,15 +77,12 @@ __global__ __launch_bounds__(256) void k_rows_to_f16(const uint8_t *__restrict__
 //   fragments are read; before the last k-step's MFMAs, the barrier that
 //   publishes the next stage (and frees this slot), the refill of this slot
 //   two stages ahead, and the next stage's first fragment reads.
-//   Epilogue: each wave stages 32-row slices of its tile in LDS (row pitch
-//   136 floats: the two row groups of a 4-byte write land on disjoint banks)
-//   and writes C rows with 16-byte stores.
+//   Epilogue: store_c_tile (32-row slices staged in LDS, 16-byte stores).
 //   Measured on the config-4 shapes (4608 x 9216 x 3072): loads and LDS reads
 //   alone take about 60% of the kernel's time; the two-slot ring keeps one
 //   stage in flight, which is what bounds the overlap with the MFMAs.
 constexpr int kFTile = 256, kFK = 64;
 constexpr int kFSlot = kFTile * kFK * 2;  // 32 KB per operand per stage
-constexpr int kFPitch = 136;
 
 __global__ __launch_bounds__(256) void k_gemm_f16_t256(const _Float16 *__restrict__ a16, const int *__restrict__ ea,
                                                        const _Float16 *__restrict__ w16, const int *__restrict__ ew,
@@ -203,51 +200,14 @@ __global__ __launch_bounds__(256) void k_gemm_f16_t256(const _Float16 *__restric
   }
   if (kt < nk) step(kt, 0);
 
-  // Epilogue, in four passes of 32 rows of every wave's tile (pass i = MFMA
-  // row tile i).  Register r of tile (i, j) is element (32i + 8(r/4) + 4g +
-  // r%4, 32j + l32) of the wave tile.
+  // Epilogue: the wave's 128 x 128 tile through LDS in 32-row slices (17 KB
+  // per wave at the start of the free slots), 16-byte stores.
   int ec[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) ec[j] = ew[min(n0 + rb[j], N - 1)];
   wg_barrier();  // the slots are free: every wave's last fragments are read
-  float *stage = reinterpret_cast<float *>(lds) + wave * 32 * kFPitch;  // 17 KB per wave
-  const bool vec = (N & 3) == 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    int er[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) er[r] = ea[min(m0 + 128 * wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3), M - 1)];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        stage[(8 * (r >> 2) + 4 * g + (r & 3)) * kFPitch + 32 * j + l32] =
-            __builtin_amdgcn_ldexpf(acc[i][j][r], er[r] + ec[j]);
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // lane -> rows 2q + l/32 of the slice, columns 4*(l%32) .. +3
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const int rl = 2 * q + g;
-      const int row = m0 + 128 * wm + 32 * i + rl, col = n0 + 128 * wn + 4 * l32;
-      const float4 v = *reinterpret_cast<const float4 *>(stage + rl * kFPitch + 4 * l32);
-      if (row < M) {
-        float *dst = c + (size_t)row * N + col;
-        if (vec && col + 4 <= N) {
-          *reinterpret_cast<float4 *>(dst) = v;
-        } else {
-          if (col < N) dst[0] = v.x;
-          if (col + 1 < N) dst[1] = v.y;
-          if (col + 2 < N) dst[2] = v.z;
-          if (col + 3 < N) dst[3] = v.w;
-        }
-      }
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  }
+  store_c_tile<4>(acc, reinterpret_cast<float *>(lds) + wave * 32 * (32 * 4 + 8), c, M, N, m0 + 128 * wm,
+                  n0 + 128 * wn, ea, ec);
 }
 
 }  // namespace

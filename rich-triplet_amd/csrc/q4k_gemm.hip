@@ -329,28 +329,18 @@ __global__ __launch_bounds__(512) void k_q4k_gemm_w8b(const _Float16 *__restrict
   if (lc < nloc) chunk(lc, 0);
   if (lc + 1 < nloc) chunk(lc + 1, 1);
 
-  // Epilogue: register r of tile (i, j) is C[128wm + 32i + 8(r/4) + 4g + r%4][colw[j]].
+  // Epilogue: the wave's 128 x 32NT tile through LDS (the ring is free once
+  // every wave has passed the barrier; wave w stages in slot array w % 6,
+  // at 8 KB for waves 6 and 7).
   int ecol[NT];
-  bool cok[NT];
 #pragma unroll
-  for (int j = 0; j < NT; ++j) {
-    const int col = n0 + colw[j];
-    cok[j] = col < N;
-    ecol[j] = cok[j] ? ew[col] : 0;
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = m0 + 128 * wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
-      if (row >= M) continue;
-      const int er = ea[row];
-      float *crow = c + (size_t)row * N + n0;
-#pragma unroll
-      for (int j = 0; j < NT; ++j)
-        if (cok[j]) crow[colw[j]] = __builtin_amdgcn_ldexpf(acc[i][j][r], er + ecol[j]);
-    }
-  }
+  for (int j = 0; j < NT; ++j) ecol[j] = ew[min(n0 + colw[j], N - 1)];
+  wg_barrier();
+  static_assert(32 * (32 * NT + 8) * 4 <= 8192 && SLOT_A >= 16384, "staging slice fits in half a slot");
+  const int ws = wave % 6;
+  uint8_t *sbase = ws == 0 ? sa0 : ws == 1 ? sa1 : ws == 2 ? sa2 : ws == 3 ? sw0 : ws == 4 ? sw1 : sw2;
+  float *stage = reinterpret_cast<float *>(sbase + (wave / 6) * 8192);
+  store_c_tile<NT>(acc, stage, c, M, N, m0 + 128 * wm, n0 + (256 / WN) * wn, ea, ecol);
 }
 
 // ---------------------------------------------------------------------------
@@ -514,27 +504,15 @@ __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restric
     }
   }
 
+  // Epilogue: the wave's 128 x 64 tile through LDS, wave w staging in slot
+  // array w once every wave has passed the barrier.
   int ecol[2];
-  bool cok[2];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int col = n0 + colw[j];
-    cok[j] = col < N;
-    ecol[j] = cok[j] ? ew[col] : 0;
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = m0 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
-      if (row >= M) continue;
-      const int er = ea[row];
-      float *crow = c + (size_t)row * N + n0;
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        if (cok[j]) crow[colw[j]] = __builtin_amdgcn_ldexpf(acc[i][j][r], er + ecol[j]);
-    }
-  }
+  for (int j = 0; j < 2; ++j) ecol[j] = ew[min(n0 + colw[j], N - 1)];
+  wg_barrier();
+  static_assert(32 * 72 * 4 <= kHSlotA && kHSlotA <= kHSlotW, "staging slice fits in a slot");
+  uint8_t *sbase = wave == 0 ? sa0 : wave == 1 ? sa1 : wave == 2 ? sw0 : sw1;
+  store_c_tile<2>(acc, reinterpret_cast<float *>(sbase), c, M, N, m0, n0 + 64 * wave, ea, ecol);
 }
 
 }  // namespace
