@@ -526,11 +526,19 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
       for (RowsIn *v : views) *v = out[i++];
       return r;
     }
+    // A is prepared once for every matrix of the set (q|k|v, gate|up)
+    auto r256 = [](size_t v) { return (v + 255) & ~size_t(255); };
+    char *ws = static_cast<char *>(b.ws);
+    _Float16 *a16 = reinterpret_cast<_Float16 *>(ws);
+    int *ea = reinterpret_cast<int *>(ws + r256((size_t)n * K * 2));
+    char *rest = ws + r256((size_t)n * K * 2) + r256((size_t)n * 4);
+    hipError_t r = launch_gemm_prep_a(A, n, K, a16, ea, st);
+    if (r != hipSuccess) return r;
     int i = 0;
     for (const MbMat &m : mats) {
       const int fmt = fmts.begin()[i];
-      hipError_t r = fmt == RT_LINEAR_Q4K ? launch_q4k_gemm(A, false, m.w, m.y, n, m.n, K, b.ws, st)
-                                          : launch_proj_gemm(A, fmt, m.w, m.y, n, m.n, K, b.ws, st);
+      r = fmt == RT_LINEAR_Q4K ? launch_q4k_gemm_prepped(a16, ea, m.w, m.y, n, m.n, K, rest, st)
+                               : launch_proj_gemm_prepped(a16, ea, fmt, m.w, m.y, n, m.n, K, rest, st);
       if (r != hipSuccess) return r;
       *views.begin()[i++] = rows_plain(m.y, m.n);
     }

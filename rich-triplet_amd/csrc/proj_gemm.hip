@@ -227,27 +227,28 @@ size_t proj_gemm_workspace_bytes(int M, int N, int K) {
          (ks > 1 ? (size_t)ks * M * N * 4 : 0);
 }
 
-hipError_t launch_proj_gemm(const float *a, int fmt, const void *w, float *c, int M, int N, int K, void *ws,
-                            hipStream_t s) {
+hipError_t launch_proj_gemm_prepped(const _Float16 *a16, const int *ea, int fmt, const void *w, float *c, int M,
+                                    int N, int K, void *ws, hipStream_t s) {
   auto r256 = [](size_t b) { return (b + 255) & ~size_t(255); };
   char *p = static_cast<char *>(ws);
-  _Float16 *a16 = reinterpret_cast<_Float16 *>(p);
-  p += r256((size_t)M * K * 2);
-  int *ea = reinterpret_cast<int *>(p);
-  p += r256((size_t)M * 4);
   _Float16 *w16 = reinterpret_cast<_Float16 *>(p);
   p += r256((size_t)N * K * 2);
   int *ew = reinterpret_cast<int *>(p);
   p += r256((size_t)N * 4);
   const uint8_t *wb = static_cast<const uint8_t *>(w);
   switch (fmt) {
-    case RT_LINEAR_Q6K: hipLaunchKernelGGL(k_rows_to_f16<RT_LINEAR_Q6K>, dim3(N), dim3(256), 0, s, wb, N, K, w16, ew); break;
-    case RT_LINEAR_Q8_0: hipLaunchKernelGGL(k_rows_to_f16<RT_LINEAR_Q8_0>, dim3(N), dim3(256), 0, s, wb, N, K, w16, ew); break;
-    case RT_LINEAR_BF16: hipLaunchKernelGGL(k_rows_to_f16<RT_LINEAR_BF16>, dim3(N), dim3(256), 0, s, wb, N, K, w16, ew); break;
+    case RT_LINEAR_Q6K:
+      hipLaunchKernelGGL(k_rows_to_f16<RT_LINEAR_Q6K>, dim3(N), dim3(256), 0, s, wb, N, K, w16, ew);
+      break;
+    case RT_LINEAR_Q8_0:
+      hipLaunchKernelGGL(k_rows_to_f16<RT_LINEAR_Q8_0>, dim3(N), dim3(256), 0, s, wb, N, K, w16, ew);
+      break;
+    case RT_LINEAR_BF16:
+      hipLaunchKernelGGL(k_rows_to_f16<RT_LINEAR_BF16>, dim3(N), dim3(256), 0, s, wb, N, K, w16, ew);
+      break;
     default: return hipErrorInvalidValue;
   }
   hipError_t e = hipGetLastError();
-  if (e == hipSuccess) e = launch_gemm_prep_a(a, M, K, a16, ea, s);
   if (e != hipSuccess) return e;
   const int tiles_m = (M + kFTile - 1) / kFTile, tiles_n = (N + kFTile - 1) / kFTile;
   const int ks = proj_ksplit(M, N, K);
@@ -257,6 +258,17 @@ hipError_t launch_proj_gemm(const float *a, int fmt, const void *w, float *c, in
   e = hipGetLastError();
   if (e == hipSuccess && ks > 1) e = launch_gemm_splitk_sum(out, c, (size_t)M * N, ks, s);
   return e;
+}
+
+hipError_t launch_proj_gemm(const float *a, int fmt, const void *w, float *c, int M, int N, int K, void *ws,
+                            hipStream_t s) {
+  auto r256 = [](size_t b) { return (b + 255) & ~size_t(255); };
+  char *p = static_cast<char *>(ws);
+  _Float16 *a16 = reinterpret_cast<_Float16 *>(p);
+  int *ea = reinterpret_cast<int *>(p + r256((size_t)M * K * 2));
+  hipError_t e = launch_gemm_prep_a(a, M, K, a16, ea, s);
+  if (e != hipSuccess) return e;
+  return launch_proj_gemm_prepped(a16, ea, fmt, w, c, M, N, K, p + r256((size_t)M * K * 2) + r256((size_t)M * 4), s);
 }
 
 }  // namespace rt

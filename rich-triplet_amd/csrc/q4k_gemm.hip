@@ -565,6 +565,31 @@ size_t q4k_gemm_workspace_bytes(int M, int N, int K) {
          (ks > 1 ? r256((size_t)ks * M * N * 4) : 0);
 }
 
+// The matrix-core launch on prepared operands; `part` holds the split-K
+// partials when the shape splits K.
+static hipError_t q4k_gemm_core(const _Float16 *a16, const int *ea, const uint8_t *wb, const int *ew, float *part,
+                                float *c, int M, int N, int K, hipStream_t s) {
+  // Up to 1024 rows: 128 x 256 tiles on eight waves (a prefill of a few
+  // hundred tokens gives too few 256-row tiles to fill the chip); above that
+  // the half-block kernel, two workgroups per CU.
+  const int tiles_m = (M + 127) / 128, tiles_n = (N + 255) / 256;
+  const int ks = gemm_ksplit(M, N, K);
+  if (ks > 1) {
+    hipLaunchKernelGGL(k_q4k_gemm_w8b<1>, dim3(tiles_m * tiles_n, ks), dim3(512), 0, s, a16, ea, wb, ew, part, M, N,
+                       K, tiles_m, tiles_n, ks);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_gemm_splitk_sum(part, c, (size_t)M * N, ks, s);
+  }
+  if (M <= 1024)
+    hipLaunchKernelGGL(k_q4k_gemm_w8b<1>, dim3(tiles_m * tiles_n), dim3(512), 0, s, a16, ea, wb, ew, c, M, N, K,
+                       tiles_m, tiles_n, 1);
+  else
+    hipLaunchKernelGGL(k_q4k_gemm_h, dim3(tiles_m * tiles_n), dim3(256), 0, s, a16, ea, wb, ew, c, M, N, K, tiles_m,
+                       tiles_n);
+  return hipGetLastError();
+}
+
 hipError_t launch_q4k_gemm(const void *a, bool a_bf16, const void *w, float *c, int M, int N, int K, void *ws,
                            hipStream_t s) {
   auto r256 = [](size_t b) { return (b + 255) & ~size_t(255); };
@@ -572,6 +597,7 @@ hipError_t launch_q4k_gemm(const void *a, bool a_bf16, const void *w, float *c, 
   _Float16 *a16 = reinterpret_cast<_Float16 *>(p);
   int *ea = reinterpret_cast<int *>(p + r256((size_t)M * K * 2));
   int *ew = reinterpret_cast<int *>(p + r256((size_t)M * K * 2) + r256((size_t)M * 4));
+  float *part = reinterpret_cast<float *>(p + r256((size_t)M * K * 2) + r256((size_t)M * 4) + r256((size_t)N * 4));
   const uint8_t *wb = static_cast<const uint8_t *>(w);
   const int prep_blocks = M + (N + 3) / 4;
   if (a_bf16)
@@ -582,26 +608,22 @@ hipError_t launch_q4k_gemm(const void *a, bool a_bf16, const void *w, float *c, 
                        ea, wb, ew, M, N, K);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  // Up to 1024 rows: 128 x 256 tiles on eight waves (a prefill of a few
-  // hundred tokens gives too few 256-row tiles to fill the chip); above that
-  // the half-block kernel, two workgroups per CU.
-  const int tiles_m = (M + 127) / 128, tiles_n = (N + 255) / 256;
-  const int ks = gemm_ksplit(M, N, K);
-  if (ks > 1) {
-    float *part = reinterpret_cast<float *>(p + r256((size_t)M * K * 2) + r256((size_t)M * 4) + r256((size_t)N * 4));
-    hipLaunchKernelGGL(k_q4k_gemm_w8b<1>, dim3(tiles_m * tiles_n, ks), dim3(512), 0, s, a16, ea, wb, ew, part, M, N,
-                       K, tiles_m, tiles_n, ks);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    e = launch_gemm_splitk_sum(part, c, (size_t)M * N, ks, s);
-    if (e != hipSuccess) return e;
-  } else if (M <= 1024)
-    hipLaunchKernelGGL(k_q4k_gemm_w8b<1>, dim3(tiles_m * tiles_n), dim3(512), 0, s, a16, ea, wb, ew, c, M, N, K,
-                       tiles_m, tiles_n, 1);
-  else
-    hipLaunchKernelGGL(k_q4k_gemm_h, dim3(tiles_m * tiles_n), dim3(256), 0, s, a16, ea, wb, ew, c, M, N, K, tiles_m,
-                       tiles_n);
-  return hipGetLastError();
+  return q4k_gemm_core(a16, ea, wb, ew, part, c, M, N, K, s);
+}
+
+hipError_t launch_q4k_gemm_prepped(const _Float16 *a16, const int *ea, const void *w, float *c, int M, int N, int K,
+                                   void *ws, hipStream_t s) {
+  auto r256 = [](size_t b) { return (b + 255) & ~size_t(255); };
+  char *p = static_cast<char *>(ws);
+  int *ew = reinterpret_cast<int *>(p);
+  float *part = reinterpret_cast<float *>(p + r256((size_t)N * 4));
+  const uint8_t *wb = static_cast<const uint8_t *>(w);
+  // W row exponents only (no A rows: M = 0 in the prep's indexing)
+  hipLaunchKernelGGL((k_gemm_prep<float>), dim3((N + 3) / 4), dim3(256), 0, s, nullptr, nullptr, nullptr, wb, ew, 0,
+                     N, K);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return q4k_gemm_core(a16, ea, wb, ew, part, c, M, N, K, s);
 }
 
 }  // namespace rt

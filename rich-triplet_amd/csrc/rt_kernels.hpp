@@ -30,6 +30,13 @@ hipError_t launch_gemm_prep_a(const float *a, int M, int K, _Float16 *a16, int *
 size_t proj_gemm_workspace_bytes(int M, int N, int K);
 hipError_t launch_proj_gemm(const float *a, int fmt, const void *w, float *c, int M, int N, int K, void *ws,
                             hipStream_t s);
+// The same two GEMMs on an A prepared once (launch_gemm_prep_a) for several
+// matrices; ws needs the respective workspace bytes minus the A part
+// (M*K*2 and M*4 bytes, each rounded up to 256).
+hipError_t launch_proj_gemm_prepped(const _Float16 *a16, const int *ea, int fmt, const void *w, float *c, int M,
+                                    int N, int K, void *ws, hipStream_t s);
+hipError_t launch_q4k_gemm_prepped(const _Float16 *a16, const int *ea, const void *w, float *c, int M, int N, int K,
+                                   void *ws, hipStream_t s);
 // Q4_K GEMM C[M,N] = A[M,K] . W[N,K]^T; A bf16 bits (a_bf16) or f32; ws holds
 // q4k_gemm_workspace_bytes(M, N, K) bytes of device scratch.
 size_t q4k_gemm_workspace_bytes(int M, int N, int K);
