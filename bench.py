@@ -142,11 +142,12 @@ def main() -> int:
         torch.cuda.synchronize()
         b.copy_(a)  # calibration: reads and writes exactly 256 MiB
         torch.cuda.synchronize()
-        ws = [synth_q4k(torch, F, H, gen) for _ in range(20)]
+        # the dominant kernel: gate|up of 20 distinct layers, one launch each
+        ws = [(synth_q4k(torch, F, H, gen), synth_q4k(torch, F, H, gen)) for _ in range(20)]
         x = torch.randn(H, device=dev, generator=gen)
-        y = torch.empty(F, device=dev)
-        for w in ws:
-            rt.q4k_gemv(w, x, y, F, H)
+        ys = [torch.empty(F, device=dev), torch.empty(F, device=dev)]
+        for wg, wu in ws:
+            rt.q4k_gemv_multi([wg, wu], ys, [F, F], x, H)
         torch.cuda.synchronize()
         print(json.dumps({"traffic_probe": "done", "copy_bytes": 256 << 20, "gemv_launches": len(ws)}))
         return 0
@@ -170,18 +171,33 @@ def main() -> int:
     torch.cuda.synchronize()
     log(f"synthetic weights ready ({time.time() - t0:.1f}s)")
 
-    step_bytes = 0
-    for name, n, k in Q4K_SHAPES:
-        step_bytes += L * gemv_bytes(n, k, q4k_bytes(n, k))
+    # The step launches the projections as the decode step does: q|k|v and
+    # gate|up share their input and run as one multi-matrix GEMV each.
+    shape = {name: (n, k) for name, n, k in Q4K_SHAPES}
+    step_launches = [("qkv", ("q", "k", "v"), x_h), ("o", ("o",), x_q), ("gateup", ("gate", "up"), x_h),
+                     ("down", ("down",), x_f)]
+
+    def launch_bytes(names):
+        k = shape[names[0]][1]
+        return sum(q4k_bytes(*shape[nm]) + 4 * shape[nm][0] for nm in names) + 4 * k
+
+    step_bytes = L * sum(launch_bytes(names) for _, names, _ in step_launches)
     q4k_step_bytes = step_bytes
     step_bytes += gemv_bytes(V, H, V * H * 2)
+
+    def enqueue_layer(w, names, x, stream):
+        k = shape[names[0]][1]
+        if len(names) == 1:
+            rt.q4k_gemv(w[names[0]], x, outs[names[0]], shape[names[0]][0], k, stream=stream)
+        else:
+            rt.q4k_gemv_multi([w[nm] for nm in names], [outs[nm] for nm in names], [shape[nm][0] for nm in names],
+                              x, k, stream=stream)
 
     # ---------------- the config-1 step as one graph ---------------------------
     def enqueue_step(stream):
         for w in layers:
-            for name, n, k in Q4K_SHAPES:
-                x = x_q if name == "o" else (x_f if name == "down" else x_h)
-                rt.q4k_gemv(w[name], x, outs[name], n, k, stream=stream)
+            for _, names, x in step_launches:
+                enqueue_layer(w, names, x, stream)
         rt.bf16_gemv(embed, x_h, logits, V, H, stream=stream)
 
     cap = torch.cuda.Stream()
@@ -234,6 +250,29 @@ def main() -> int:
         per_shape[name] = {"n": n, "k": k, "us_per_launch": round(us, 3), "GBps": round(byts / us / 1e3, 1),
                            "bytes_per_launch": byts}
         del g
+    for fused, names, x in step_launches:
+        if len(names) == 1:
+            continue
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap):
+            s = torch.cuda.current_stream()
+            for w in layers:
+                enqueue_layer(w, names, x, s)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / (reps * L)
+        byts = launch_bytes(names)
+        per_shape[fused + "_fused"] = {"n": [shape[nm][0] for nm in names], "k": shape[names[0]][1],
+                                       "us_per_launch": round(us, 3), "GBps": round(byts / us / 1e3, 1),
+                                       "bytes_per_launch": byts}
+        del g
     # ---------------- Q6_K / Q8_0 kept packed vs widened to BF16 ---------------
     # Q4_K_M files hold attn_v and ffn_down in Q6_K; the reference widens them
     # (and Q8_0) to BF16 at load (transformer4.rs:1233-1242).
@@ -276,12 +315,19 @@ def main() -> int:
         log(f"{name} {n}x{k}: Q6_K {kquant['q6k_' + name]['us_per_launch']} us, "
             f"Q8_0 {kquant['q8_0_' + name]['us_per_launch']} us, BF16 (reference widening) "
             f"{kquant['bf16_' + name]['us_per_launch']} us")
-    dom = per_shape["gate"]
+    # dominant kernel of the step (largest share of its time): the gate|up GEMV
+    dom = per_shape["gateup_fused"]
     roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(dom["GBps"] / PEAK_HBM_GBS, 4), "traffic": measured_traffic(),
-                "kernel": "k_q4k_gemv_dig<NB=10,T=960,ITERS=2> (Q4_K GEMV 10240x2560)",
-                "bytes_per_launch": dom["bytes_per_launch"], "us_per_launch": dom["us_per_launch"]}
-    log(f"dominant kernel gate 10240x2560: {dom['us_per_launch']} us/launch, {dom['GBps']} GB/s")
+                "kernel": "k_q4k_gemv_dig_multi<NB=10,T=320,ITERS=2> (Q4_K GEMV, gate|up 2 x 10240x2560 in one "
+                          "launch)",
+                "bytes_per_launch": dom["bytes_per_launch"], "us_per_launch": dom["us_per_launch"],
+                "single_matrix": {"kernel": "k_q4k_gemv_dig<NB=10,T=960,ITERS=2> (10240x2560)",
+                                  "us_per_launch": per_shape["gate"]["us_per_launch"],
+                                  "GBps": per_shape["gate"]["GBps"],
+                                  "frac": round(per_shape["gate"]["GBps"] / PEAK_HBM_GBS, 4)}}
+    log(f"dominant kernel gate|up 2x10240x2560: {dom['us_per_launch']} us/launch, {dom['GBps']} GB/s "
+        f"(one 10240x2560 matrix alone: {per_shape['gate']['us_per_launch']} us)")
 
     # ---------------- config 3: full decode step -------------------------------
     decode = None
@@ -434,7 +480,8 @@ def main() -> int:
         "data": "synthetic",
         "frac_of_hbm_peak": round(value / PEAK_HBM_GBS, 4),
         "config": {"workload": "config 1: Gemma-3-4B projection set of one decode token, 34 distinct layers x "
-                               "{q,k,v,o,gate,up,down} Q4_K GEMV + BF16 lm_head 2560->262144, one hipGraph",
+                               "{q,k,v,o,gate,up,down} Q4_K GEMV (q|k|v and gate|up, which share their input, "
+                               "one launch each) + BF16 lm_head 2560->262144, one hipGraph",
                    "bytes_per_step": step_bytes, "parallelism": "single GPU"},
         "roofline": roofline,
         "per_shape": per_shape,
@@ -451,7 +498,7 @@ def measured_traffic():
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3
     --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy calibration),
     or None when the summary is absent."""
-    f = REPO / "profiles" / "q4k_gemv_10240x2560_traffic.txt"
+    f = REPO / "profiles" / "q4k_gemv_gateup_2x10240x2560_traffic.txt"
     try:
         for line in f.read_text().splitlines():
             if line.startswith("traffic_bytes_per_launch="):

@@ -60,6 +60,12 @@ rt_status rt_q4k_dequant_bf16(const void *blocks_dev, size_t n_blocks, uint16_t 
 rt_status rt_q4k_gemv(const void *w_dev, const float *x_dev, float *y_dev, int64_t n, int64_t k, void *stream);
 rt_status rt_bf16_gemv(const uint16_t *w_dev, const float *x_dev, float *y_dev, int64_t n, int64_t k,
                        void *stream);
+/* y_i = W_i . x for count <= 4 Q4_K matrices sharing x, in one launch: the
+ * q, k, v (or gate, up) GEMVs the reference dispatches one by one
+ * (metal_decode.rs:1948-1954, 2001-2004).  Host arrays of device pointers and
+ * row counts; each as rt_q4k_gemv requires. */
+rt_status rt_q4k_gemv_multi(const void *const *w_dev, float *const *y_dev, const int64_t *n, int32_t count,
+                            const float *x_dev, int64_t k, void *stream);
 
 /* ---------------------------------------------------------------------------
  * Host-pointer drop-ins for the reference's per-call GPU API

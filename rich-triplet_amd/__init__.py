@@ -61,6 +61,7 @@ _SIGNATURES = {
     "rt_q6k_gemv": (_i32, [_vp, _vp, _vp, _i64, _i64, _vp]),
     "rt_q8_0_gemv": (_i32, [_vp, _vp, _vp, _i64, _i64, _vp]),
     "rt_linear_gemm_f32": (_i32, [_i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "rt_q4k_gemv_multi": (_i32, [_vp, _vp, _vp, _i32, _vp, _i64, _vp]),
     "rt_q4k_gemm_bf16": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "rt_q4k_gemm_f32": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "rt_matmul_q4k_t": (_i32, [_vp, _sz, _sz, _vp, _sz, _vp]),
@@ -181,6 +182,17 @@ def q6k_gemv(w, x, y, n: int, k: int, stream=None) -> None:
 def q8_0_gemv(w, x, y, n: int, k: int, stream=None) -> None:
     """y = W x on planar Q8_0 weights (q8_0_repack)."""
     check(lib().rt_q8_0_gemv(_p(w), _p(x), _p(y), n, k, _stream(stream)))
+
+
+def q4k_gemv_multi(ws, ys, ns, x, k: int, stream=None) -> None:
+    """y_i = W_i x for up to 4 Q4_K matrices sharing x, one launch (q|k|v, gate|up)."""
+    cnt = len(ws)
+    if not (len(ys) == cnt == len(ns)):
+        raise ValueError("ws, ys and ns must have the same length")
+    wa = (C.c_void_p * max(cnt, 1))(*[_p(w) for w in ws])
+    ya = (C.c_void_p * max(cnt, 1))(*[_p(y) for y in ys])
+    na = (C.c_int64 * max(cnt, 1))(*[int(n) for n in ns])
+    check(lib().rt_q4k_gemv_multi(wa, ya, na, cnt, _p(x), k, _stream(stream)))
 
 
 def linear_gemm_f32(fmt: int, w, a, c, m: int, n: int, k: int, stream=None) -> None:

@@ -80,6 +80,27 @@ rt_status rt_q4k_gemv(const void *w, const float *x, float *y, int64_t n, int64_
   return hip_error(launch_q4k_gemv(w, x, y, (int)n, (int)k, (hipStream_t)stream), "rt_q4k_gemv");
 }
 
+// The q, k, v (or gate, up) GEMVs of one step share their input and are
+// dispatched one by one by the reference (metal_decode.rs:1948-1954,
+// 2001-2004); one launch covers them here.
+rt_status rt_q4k_gemv_multi(const void *const *w, float *const *y, const int64_t *n, int32_t count, const float *x,
+                            int64_t k, void *stream) {
+  static const char *who = "rt_q4k_gemv_multi";
+  if (!w || !y || !n) return set_error(RT_EINVAL, "%s: null array", who);
+  if (count < 1 || count > kGemvMaxMats)
+    return set_error(RT_EINVAL, "%s: count=%d outside [1, %d]", who, count, kGemvMaxMats);
+  int ni[kGemvMaxMats];
+  int64_t total = 0;
+  for (int i = 0; i < count; ++i) {
+    rt_status st = check_gemv_shape(who, w[i], x, y[i], n[i], k, 256);
+    if (st != RT_OK) return st;
+    ni[i] = (int)n[i];
+    total += n[i];
+  }
+  if (total > INT32_MAX) return set_error(RT_EINVAL, "%s: total rows exceed int32", who);
+  return hip_error(launch_q4k_gemv_multi(w, y, ni, count, x, (int)k, (hipStream_t)stream), who);
+}
+
 rt_status rt_bf16_gemv(const uint16_t *w, const float *x, float *y, int64_t n, int64_t k, void *stream) {
   rt_status st = check_gemv_shape("rt_bf16_gemv", w, x, y, n, k, 8);
   if (st != RT_OK) return st;

@@ -101,15 +101,15 @@ __global__ __launch_bounds__(T) void k_q4k_gemv_cr(const uint8_t *__restrict__ W
 }
 
 
-// Digit-staged activations, all ITERS row-iterations of a workgroup in flight.
+// Digit-staged activations, all ITERS row-iterations of a workgroup in flight:
+// rows [row0, row0 + ROWS) of W.
 template <int NB, int T, int ITERS>
-__global__ __launch_bounds__(T) void k_q4k_gemv_dig(const uint8_t *__restrict__ W, const float *__restrict__ x,
-                                                    float *__restrict__ y, int N) {
+RT_DEV void gemv_dig_tile(const uint8_t *__restrict__ W, const float *__restrict__ x, float *__restrict__ y, int N,
+                          int row0) {
   using Tile = Q4KTile<NB, T, ITERS>;
   __shared__ __attribute__((aligned(16))) uint32_t dl[NB * 4 * kDPitch];
   __shared__ float red[Tile::ROWS * NB];
   Tile tile;
-  const int row0 = (int)blockIdx.x * Tile::ROWS;
   const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
   XRegs<NB * 256, T> xr;
   x_load<NB * 256, T>(x, xr);
@@ -127,6 +127,31 @@ __global__ __launch_bounds__(T) void k_q4k_gemv_dig(const uint8_t *__restrict__ 
     const int r = row0 + i;
     if (r < N) y[r] = reduce_row<NB>(red, i);
   }
+}
+
+template <int NB, int T, int ITERS>
+__global__ __launch_bounds__(T) void k_q4k_gemv_dig(const uint8_t *__restrict__ W, const float *__restrict__ x,
+                                                    float *__restrict__ y, int N) {
+  gemv_dig_tile<NB, T, ITERS>(W, x, y, N, (int)blockIdx.x * Q4KTile<NB, T, ITERS>::ROWS);
+}
+
+// Several matrices sharing x in one launch: workgroup b takes a row tile of
+// matrix i with tile0[i] <= b < tile0[i+1] (every matrix covers whole tiles;
+// rows past its end are masked).
+struct GemvMats {
+  const uint8_t *w[kGemvMaxMats];
+  float *y[kGemvMaxMats];
+  int n[kGemvMaxMats];
+  int tile0[kGemvMaxMats + 1];
+  int count;
+};
+
+template <int NB, int T, int ITERS>
+__global__ __launch_bounds__(T) void k_q4k_gemv_dig_multi(GemvMats m, const float *__restrict__ x) {
+  const int b = (int)blockIdx.x;
+  int i = 0;
+  while (i + 1 < m.count && b >= m.tile0[i + 1]) ++i;
+  gemv_dig_tile<NB, T, ITERS>(m.w[i], x, m.y[i], m.n[i], (b - m.tile0[i]) * Q4KTile<NB, T, ITERS>::ROWS);
 }
 
 // Any K (multiple of 256): one wave per row, lanes stride over the row's chunks.
@@ -217,6 +242,44 @@ static hipError_t launch_dig(const void *W, const float *x, float *y, int N, hip
 // up to 8k rows, 48 rows (960 threads, two row-iterations) up to 12k, 32 rows
 // beyond; K=2048 with 16 rows; K=10240 with 6 rows (960 threads).  Other K's
 // use the f32-staged tile.
+template <int NB, int T, int ITERS>
+static hipError_t launch_dig_multi(const void *const *w, float *const *y, const int *n, int count, const float *x,
+                                   hipStream_t s) {
+  constexpr int ROWS = Q4KTile<NB, T, ITERS>::ROWS;
+  GemvMats m{};
+  m.count = count;
+  m.tile0[0] = 0;
+  for (int i = 0; i < count; ++i) {
+    m.w[i] = static_cast<const uint8_t *>(w[i]);
+    m.y[i] = y[i];
+    m.n[i] = n[i];
+    m.tile0[i + 1] = m.tile0[i] + (n[i] + ROWS - 1) / ROWS;
+  }
+  hipLaunchKernelGGL((k_q4k_gemv_dig_multi<NB, T, ITERS>), dim3(m.tile0[count]), dim3(T), 0, s, m, x);
+  return hipGetLastError();
+}
+
+// Matrices sharing x in one launch (q|k|v, gate|up): the fixed cost of a
+// launch (about 2 us from the previous kernel's end to this one's first
+// weights) is paid once for all of them.  Tiles for K=2560 from measurements
+// of the combined row count; other K's run one launch per matrix.
+hipError_t launch_q4k_gemv_multi(const void *const *w, float *const *y, const int *n, int count, const float *x,
+                                 int K, hipStream_t s) {
+  if (count < 1 || count > kGemvMaxMats) return hipErrorInvalidValue;
+  if (K == 2560) {
+    int total = 0;
+    for (int i = 0; i < count; ++i) total += n[i];
+    if (total > 12288) return launch_dig_multi<10, 320, 2>(w, y, n, count, x, s);
+    if (total >= 8192) return launch_dig_multi<10, 960, 2>(w, y, n, count, x, s);
+    return launch_dig_multi<10, 640, 1>(w, y, n, count, x, s);
+  }
+  for (int i = 0; i < count; ++i) {
+    const hipError_t e = launch_q4k_gemv(w[i], x, y[i], n[i], K, s);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
 hipError_t launch_q4k_gemv(const void *W, const float *x, float *y, int N, int K, hipStream_t s) {
   switch (K / kQ4KBlockElems) {
     case 1: return launch_cr_auto<1, 256>(W, x, y, N, s);

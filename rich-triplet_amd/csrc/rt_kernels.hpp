@@ -10,6 +10,10 @@ namespace rt {
 
 hipError_t launch_q4k_dequant(const void *blocks, size_t n_blocks, void *out, bool bf16, hipStream_t s);
 hipError_t launch_q4k_gemv(const void *W, const float *x, float *y, int N, int K, hipStream_t s);
+// Up to kGemvMaxMats Q4_K matrices sharing the activation x in one launch.
+constexpr int kGemvMaxMats = 4;
+hipError_t launch_q4k_gemv_multi(const void *const *w, float *const *y, const int *n, int count, const float *x,
+                                 int K, hipStream_t s);
 hipError_t launch_q4k_gemv_generic(const void *W, const float *x, float *y, int N, int K, hipStream_t s);
 int q4k_gemv_rows_per_wg(int N, int K);
 hipError_t launch_bf16_gemv(const uint16_t *W, const float *x, float *y, int N, int K, hipStream_t s);

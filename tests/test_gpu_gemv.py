@@ -132,3 +132,35 @@ def test_bf16_gemv_reference_fixtures(rt, orc):
         exp = orc.bf16_gemv(w, n, k, a)
         assert np.all(np.abs(got - exp) < 1e-2)
     rt.weight_cache_clear()
+
+
+MULTI_SETS = [((2048, 1024, 1024), 2560), ((10240, 10240), 2560), ((1000, 37, 513), 2560), ((4096,), 2560),
+              ((700, 300), 2048), ((64, 8, 200, 1), 512)]
+
+
+@pytest.mark.parametrize("ns,k", MULTI_SETS)
+def test_q4k_gemv_multi_equals_single_launches(rt, orc, dev, ns, k):
+    """One launch over matrices sharing x (q|k|v, gate|up, ragged row counts,
+    a K without its own tile) gives every matrix's single-launch result bit
+    for bit (the per-row arithmetic does not depend on the tile), and the
+    oracle's within the GEMV bound."""
+    import torch
+    rng = np.random.default_rng(sum(ns) + k)
+    x = rng.standard_normal(k).astype(np.float32)
+    xd = to_dev(x, dev)
+    blocks = [orc.synth_q4k(900 + i, n, k) for i, n in enumerate(ns)]
+    ws = [to_dev(b, dev) for b in blocks]
+    ys = [torch.full((n,), float("nan"), dtype=torch.float32, device=dev) for n in ns]
+    rt.q4k_gemv_multi(ws, ys, list(ns), xd, k)
+    singles = []
+    for w, n in zip(ws, ns):
+        y1 = torch.empty(n, dtype=torch.float32, device=dev)
+        rt.q4k_gemv(w, xd, y1, n, k)
+        singles.append(y1)
+    _sync()
+    for i, (y, y1, b, n) in enumerate(zip(ys, singles, blocks, ns)):
+        got = y.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), y1.cpu().numpy().view(np.uint32)), i
+        if n * k <= 2048 * 2560:
+            ref = orc.q4k_gemv(b, n, k, x)
+            assert rel_l2(got, ref) < GEMV_TOL, (i, rel_l2(got, ref))

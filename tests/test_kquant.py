@@ -464,3 +464,14 @@ def test_q4_k_m_layout_prefill_at_gemma3_4b_shape(rt, orc):
         assert rel_l2(k1, k2) < KV_TOL and rel_l2(v1, v2) < KV_TOL
     d1.close()
     d2.close()
+
+
+def test_gemv_multi_rejects_bad_calls(rt):
+    with pytest.raises(rt.RtError):
+        rt.q4k_gemv_multi([], [], [], 16, 2560)  # no matrix
+    with pytest.raises(rt.RtError):
+        rt.q4k_gemv_multi([16] * 5, [16] * 5, [256] * 5, 16, 2560)  # more than four
+    with pytest.raises(rt.RtError):
+        rt.q4k_gemv_multi([16, 16], [16, 16], [256, 256], 16, 2000)  # K not whole blocks
+    with pytest.raises(rt.RtError):
+        rt.q4k_gemv_multi([16, 16], [16, 16], [256, 0], 16, 2560)  # empty matrix
