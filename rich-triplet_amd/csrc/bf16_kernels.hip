@@ -139,7 +139,7 @@ hipError_t launch_bf16_gemv(const uint16_t *W, const float *x, float *y, int N, 
     constexpr int U = 2;
     const int waves_needed = (N + U - 1) / U;
     int grid = (waves_needed + 3) / 4;
-    if (grid > 256 * 8) grid = 256 * 8;
+    if (grid > 256 * 32) grid = 256 * 32;  // 262144 rows: 8192 workgroups (measured 4% over 2048)
     hipLaunchKernelGGL((k_bf16_gemv<5, U>), dim3(grid), dim3(256), 0, s, W, x, y, N);
     return hipGetLastError();
   }

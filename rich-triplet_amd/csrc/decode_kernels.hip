@@ -773,7 +773,7 @@ static hipError_t enqueue_layers(const DecodeShape &s, const DecodeArgs &a, cons
 
 hipError_t enqueue_lm_head(const DecodeShape &s, const DecodeArgs &a, const LayerArgs &last, hipStream_t stream) {
   Launch l{stream};
-  const dim3 grid(1024);
+  const dim3 grid(2048);
   if (s.hidden == 2560) hipLaunchKernelGGL((k_lmhead<5>), grid, dim3(256), 0, l.s, a, last);
   else hipLaunchKernelGGL((k_lmhead<1>), grid, dim3(256), 0, l.s, a, last);
   l.check();

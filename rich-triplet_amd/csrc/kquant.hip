@@ -34,24 +34,12 @@
 
 #include "q4k_gemv.hpp"
 #include "rt_device.hpp"
+#include "kquant_layout.hpp"
 #include "rt_kernels.hpp"
 
 namespace rt {
 namespace {
 
-constexpr int kQ6KBlockBytes = 210;
-constexpr int kQ8Block = 32, kQ8BlockBytes = 34;
-
-struct Q6KPlanes {
-  const uint8_t *ql, *qh;
-  const uint8_t *sc;
-  const uint16_t *d;
-};
-
-__host__ __device__ inline Q6KPlanes q6k_planes(const void *w, size_t nbt) {
-  const uint8_t *p = static_cast<const uint8_t *>(w);
-  return {p, p + nbt * 128, p + nbt * 192, reinterpret_cast<const uint16_t *>(p + nbt * 208)};
-}
 
 // ---------------------------------------------------------------------------
 // Dequantisation (bit-exact with decode_q6k_to_f32 / decode_q8_0_to_f32:
@@ -62,24 +50,15 @@ __global__ __launch_bounds__(256) void k_q6k_dequant(const uint8_t *__restrict__
 #pragma clang fp contract(off)
   const Q6KPlanes P = q6k_planes(w, nbt);
   const size_t total = nbt * 256;
-  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (size_t)gridDim.x * 256) {
-    const size_t blk = e >> 8;
-    const int i = (int)(e & 255), j = i >> 7, h = i & 127, m = h >> 5, l = h & 31;
-    const uint8_t ql = P.ql[blk * 128 + 64 * j + 32 * (m & 1) + l];
-    const uint8_t qh = P.qh[blk * 64 + 32 * j + l];
-    const int q = (int)(((m < 2 ? ql & 15 : ql >> 4)) | (((qh >> (2 * m)) & 3) << 4)) - 32;
-    const float d = half_bits_to_f32(P.d[blk]);
-    const float s = d * (float)(int8_t)P.sc[blk * 16 + 8 * j + (l >> 4) + 2 * m];
-    out[e] = s * (float)q;
-  }
+  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (size_t)gridDim.x * 256)
+    out[e] = q6k_value(P, e >> 8, (int)(e & 255));
 }
 
 __global__ __launch_bounds__(256) void k_q8_0_dequant(const uint8_t *__restrict__ w, size_t n_elem,
                                                       float *__restrict__ out) {
 #pragma clang fp contract(off)
-  const uint16_t *D = reinterpret_cast<const uint16_t *>(w + n_elem);
   for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n_elem; e += (size_t)gridDim.x * 256)
-    out[e] = half_bits_to_f32(D[e / kQ8Block]) * (float)(int8_t)w[e];
+    out[e] = q8_0_value(w, n_elem, e);
 }
 
 // ---------------------------------------------------------------------------

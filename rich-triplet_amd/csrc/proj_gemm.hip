@@ -14,6 +14,7 @@
 #include <algorithm>
 
 #include "../../include/rt_hip.h"
+#include "kquant_layout.hpp"
 #include "mfma_common.hpp"
 #include "rt_device.hpp"
 #include "rt_kernels.hpp"
@@ -28,18 +29,9 @@ RT_DEV float proj_value(const uint8_t *__restrict__ W, int N, int K, int n, int 
   if constexpr (FMT == RT_LINEAR_BF16) {
     return bf16_lo((uint32_t) reinterpret_cast<const uint16_t *>(W)[(size_t)n * K + e]);
   } else if constexpr (FMT == RT_LINEAR_Q8_0) {
-    const size_t i = (size_t)n * K + e;
-    const uint16_t *D = reinterpret_cast<const uint16_t *>(W + (size_t)N * K);
-    return half_bits_to_f32(D[i / 32]) * (float)(int8_t)W[i];
+    return q8_0_value(W, (size_t)N * K, (size_t)n * K + e);
   } else {  // RT_LINEAR_Q6K, planar
-    const size_t nbt = (size_t)N * (K / 256), blk = (size_t)n * (K / 256) + e / 256;
-    const int i = e & 255, j = i >> 7, h = i & 127, m = h >> 5, l = h & 31;
-    const uint8_t ql = W[blk * 128 + 64 * j + 32 * (m & 1) + l];
-    const uint8_t qh = W[nbt * 128 + blk * 64 + 32 * j + l];
-    const int q = (int)(((m < 2 ? ql & 15 : ql >> 4)) | (((qh >> (2 * m)) & 3) << 4)) - 32;
-    const float d = half_bits_to_f32(reinterpret_cast<const uint16_t *>(W + nbt * 208)[blk]);
-    const float s = d * (float)(int8_t)W[nbt * 192 + blk * 16 + 8 * j + (l >> 4) + 2 * m];
-    return s * (float)q;
+    return q6k_value(q6k_planes(W, (size_t)N * (K / 256)), (size_t)n * (K / 256) + e / 256, e & 255);
   }
 }
 
