@@ -221,6 +221,7 @@ size_t proj_gemm_workspace_bytes(int M, int N, int K) {
 
 hipError_t launch_proj_gemm_prepped(const _Float16 *a16, const int *ea, int fmt, const void *w, float *c, int M,
                                     int N, int K, void *ws, hipStream_t s) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % kFK != 0) return hipErrorInvalidValue;  // K moves in stages of 64
   auto r256 = [](size_t b) { return (b + 255) & ~size_t(255); };
   char *p = static_cast<char *>(ws);
   _Float16 *w16 = reinterpret_cast<_Float16 *>(p);
