@@ -54,13 +54,17 @@ __global__ __launch_bounds__(256) void k_pf_embed(const int *__restrict__ tokens
 //   RESID:  x = base + rms(add)(1 + g_add);  x_out = x;  xn = rms(x)(1 + g_out)
 //   !RESID: x = add;                                     xn = rms(x)(1 + g_out)
 // `add` may be split-K partial sums.  With st_dig, xn is also staged as the
-// input of a batched GEMV.  T = 1024 for a few rows (more loads in flight
-// per row when `add` is a sum of many slices), 256 otherwise.
+// input of a batched GEMV; with a16, it is written as the next GEMM's A
+// operand (f16 row scaled by 2^-ea[t], bit-identical to the GEMM's own
+// preparation of the f32 row) instead of going through xn_out.  T = 1024 for
+// a few rows (more loads in flight per row when `add` is a sum of many
+// slices), 256 otherwise.
 template <bool RESID, int T>
 __global__ __launch_bounds__(T) void k_pf_norm(const float *__restrict__ base, RowsIn add,
                                                  const float *__restrict__ g_add, const float *__restrict__ g_out,
                                                  float *__restrict__ x_out, float *__restrict__ xn_out, int H,
-                                                 float eps, int8_t *__restrict__ st_dig) {
+                                                 float eps, int8_t *__restrict__ st_dig, _Float16 *__restrict__ a16,
+                                                 int *__restrict__ ea) {
   constexpr int PER = 1024 / T;
   __shared__ float red[T / 64];
   const int t = (int)blockIdx.x;
@@ -93,25 +97,41 @@ __global__ __launch_bounds__(T) void k_pf_norm(const float *__restrict__ base, R
   const float rx = rms_inv_from_sumsq(block_sum<T>(ss, red), inv_k, eps);
   float4 *xn = reinterpret_cast<float4 *>(xn_out) + off;
   float *st_stats = st_dig ? mb_stats(st_dig, H) : nullptr;
+  float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int f = threadIdx.x + i * T;
     if (i * T >= F4) break;  // block-uniform
     const float4 v = norm4(x[i], rx, reinterpret_cast<const float4 *>(g_out)[min(f, F4 - 1)]);
-    if (f < F4) xn[f] = v;
+    x[i] = v;
+    if (f < F4) {
+      if (xn_out) xn[f] = v;
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
     if (st_dig) mb_stage4(st_dig, st_stats, t, min(f, F4 - 1) >> 4, f & 15, v, f < F4);  // 16 lanes per chunk
+  }
+  if (a16) {
+    const int e = f16_exponent_for(block_max<T>(amax, red));
+    if (threadIdx.x == 0) ea[t] = e;
+    uint2 *dst = reinterpret_cast<uint2 *>(a16 + (size_t)t * H);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int f = threadIdx.x + i * T;
+      if (f < F4) dst[f] = f16x4_scaled(x[i], e);
+    }
   }
 }
 
 template <bool RESID>
 hipError_t launch_pf_norm(int n, hipStream_t st, const float *base, RowsIn add, const float *g_add,
-                          const float *g_out, float *x_out, float *xn_out, int H, float eps, int8_t *st_dig) {
+                          const float *g_out, float *x_out, float *xn_out, int H, float eps, int8_t *st_dig,
+                          _Float16 *a16 = nullptr, int *ea = nullptr) {
   if (n <= 64)
     hipLaunchKernelGGL((k_pf_norm<RESID, 1024>), dim3(n), dim3(1024), 0, st, base, add, g_add, g_out, x_out, xn_out, H,
-                       eps, st_dig);
+                       eps, st_dig, a16, ea);
   else
     hipLaunchKernelGGL((k_pf_norm<RESID, 256>), dim3(n), dim3(256), 0, st, base, add, g_add, g_out, x_out, xn_out, H,
-                       eps, st_dig);
+                       eps, st_dig, a16, ea);
   return hipGetLastError();
 }
 
@@ -160,6 +180,36 @@ __global__ __launch_bounds__(256) void k_pf_gelu_mul(RowsIn g, RowsIn u, float *
                                  mul_nc(gelu_tanh(a.z), b.z), mul_nc(gelu_tanh(a.w), b.w));
     reinterpret_cast<float4 *>(h)[i] = r;
     if (st_dig) mb_stage4(st_dig, st_stats, t, c4 >> 4, c4 & 15, r, true);
+  }
+}
+
+// The same product for the GEMM path, one row per workgroup (F <= 16384): h
+// goes straight out as the down GEMM's A operand (f16 row, exponent ea[t]),
+// bit-identical to preparing the f32 row.
+__global__ __launch_bounds__(256) void k_pf_gelu_rows(RowsIn g, RowsIn u, int F, _Float16 *__restrict__ a16,
+                                                      int *__restrict__ ea) {
+  constexpr int MAXP = 16;
+  __shared__ float red[4];
+  const int t = (int)blockIdx.x, f4 = F / 4;
+  float4 r[MAXP];
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXP; ++i) {
+    const int c4 = (int)threadIdx.x + 256 * i;
+    if (c4 < f4) {
+      const float4 a = rows_in4(g, t, 4 * c4), b = rows_in4(u, t, 4 * c4);
+      r[i] = make_float4(mul_nc(gelu_tanh(a.x), b.x), mul_nc(gelu_tanh(a.y), b.y), mul_nc(gelu_tanh(a.z), b.z),
+                         mul_nc(gelu_tanh(a.w), b.w));
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(r[i].x), fabsf(r[i].y)), fmaxf(fabsf(r[i].z), fabsf(r[i].w))));
+    }
+  }
+  const int e = f16_exponent_for(block_max<256>(amax, red));
+  if (threadIdx.x == 0) ea[t] = e;
+  uint2 *dst = reinterpret_cast<uint2 *>(a16 + (size_t)t * F);
+#pragma unroll
+  for (int i = 0; i < MAXP; ++i) {
+    const int c4 = (int)threadIdx.x + 256 * i;
+    if (c4 < f4) dst[c4] = f16x4_scaled(r[i], e);
   }
 }
 
@@ -516,6 +566,16 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
   // partial sums that the consumer adds while reading (views).
   int8_t *stage = plan.mb ? static_cast<int8_t *>(b.mb_stage) : nullptr;
   RowsIn vq, vk, vv, vo, vg, vu, vd;
+  // The GEMM path's A operand (f16 rows + exponents) at the start of the
+  // workspace, for rows of length K.
+  auto r256 = [](size_t v) { return (v + 255) & ~size_t(255); };
+  auto gemm_a16 = [&](int K) { return reinterpret_cast<_Float16 *>(b.ws); };
+  auto gemm_ea = [&](int K) {
+    return reinterpret_cast<int *>(static_cast<char *>(b.ws) + r256((size_t)n * K * 2));
+  };
+  _Float16 *a16_h = plan.mb ? nullptr : gemm_a16(H);  // producers that write A directly
+  int *ea_h = plan.mb ? nullptr : gemm_ea(H);
+  float *xn_f32 = plan.mb ? b.xn : nullptr;
   // (plan.mb requires every projection in Q4_K; other formats take their own GEMM)
   auto proj = [&](const float *A, int K, std::initializer_list<int> fmts, std::initializer_list<MbMat> mats,
                   std::initializer_list<RowsIn *> views) {
@@ -526,13 +586,12 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
       for (RowsIn *v : views) *v = out[i++];
       return r;
     }
-    // A is prepared once for every matrix of the set (q|k|v, gate|up)
-    auto r256 = [](size_t v) { return (v + 255) & ~size_t(255); };
-    char *ws = static_cast<char *>(b.ws);
-    _Float16 *a16 = reinterpret_cast<_Float16 *>(ws);
-    int *ea = reinterpret_cast<int *>(ws + r256((size_t)n * K * 2));
-    char *rest = ws + r256((size_t)n * K * 2) + r256((size_t)n * 4);
-    hipError_t r = launch_gemm_prep_a(A, n, K, a16, ea, st);
+    // A is prepared once for every matrix of the set (q|k|v, gate|up); the
+    // norms and the gelu product write it themselves (A == nullptr)
+    _Float16 *a16 = gemm_a16(K);
+    int *ea = gemm_ea(K);
+    char *rest = reinterpret_cast<char *>(ea) + r256((size_t)n * 4);
+    hipError_t r = A ? launch_gemm_prep_a(A, n, K, a16, ea, st) : hipSuccess;
     if (r != hipSuccess) return r;
     int i = 0;
     for (const MbMat &m : mats) {
@@ -549,9 +608,9 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
   for (int li = 0; li < s.n_layers; ++li) {
     const LayerArgs &L = layers[li];
     if (li == 0)
-      PF_TRY(launch_pf_norm<false>(n, st, nullptr, rows_plain(b.hid, H), nullptr,
-                                  L.g_in, nullptr, b.xn, H, a.eps, stage));
-    PF_TRY(proj(b.xn, H, {L.fmt[kProjQ], L.fmt[kProjK], L.fmt[kProjV]},
+      PF_TRY(launch_pf_norm<false>(n, st, nullptr, rows_plain(b.hid, H), nullptr, L.g_in, nullptr, xn_f32, H, a.eps,
+                                   stage, a16_h, ea_h));
+    PF_TRY(proj(plan.mb ? b.xn : nullptr, H, {L.fmt[kProjQ], L.fmt[kProjK], L.fmt[kProjV]},
                 {MbMat{L.wq, b.q, QD, 0, 0}, MbMat{L.wk, b.k, KVD, 0, 0}, MbMat{L.wv, b.v, KVD, 0, 0}},
                 {&vq, &vk, &vv}));
     const int items = n * (nq + nkv);
@@ -588,17 +647,21 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
     if (D == 256) PF_TRY(launch_pf_attn<256>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa, stage));
     else PF_TRY(launch_pf_attn<128>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa, stage));
     PF_TRY(proj(b.attn, QD, {L.fmt[kProjO]}, {MbMat{L.wo, b.o, H, 0, 0}}, {&vo}));
-    PF_TRY(launch_pf_norm<true>(n, st, b.hid, vo, L.g_post_attn, L.g_pre_ffn,
-                                b.x2, b.xn, H, a.eps, stage));
-    PF_TRY(proj(b.xn, H, {L.fmt[kProjGate], L.fmt[kProjUp]},
+    PF_TRY(launch_pf_norm<true>(n, st, b.hid, vo, L.g_post_attn, L.g_pre_ffn, b.x2, xn_f32, H, a.eps, stage, a16_h,
+                                ea_h));
+    PF_TRY(proj(plan.mb ? b.xn : nullptr, H, {L.fmt[kProjGate], L.fmt[kProjUp]},
                 {MbMat{L.wgate, b.g, F, 0, 0}, MbMat{L.wup, b.u, F, 0, 0}}, {&vg, &vu}));
-    const size_t n4 = (size_t)n * F / 4;
-    const unsigned eg = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
-    PF_CHECK(hipLaunchKernelGGL(k_pf_gelu_mul, dim3(eg), dim3(256), 0, st, vg, vu, b.g, n, F, stage));
-    PF_TRY(proj(b.g, F, {L.fmt[kProjDown]}, {MbMat{L.wdown, b.dn, H, 0, 0}}, {&vd}));
+    if (plan.mb) {
+      const size_t n4 = (size_t)n * F / 4;
+      const unsigned eg = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
+      PF_CHECK(hipLaunchKernelGGL(k_pf_gelu_mul, dim3(eg), dim3(256), 0, st, vg, vu, b.g, n, F, stage));
+    } else {
+      PF_CHECK(hipLaunchKernelGGL(k_pf_gelu_rows, dim3(n), dim3(256), 0, st, vg, vu, F, gemm_a16(F), gemm_ea(F)));
+    }
+    PF_TRY(proj(plan.mb ? b.g : nullptr, F, {L.fmt[kProjDown]}, {MbMat{L.wdown, b.dn, H, 0, 0}}, {&vd}));
     if (li + 1 < s.n_layers)
-      PF_TRY(launch_pf_norm<true>(n, st, b.x2, vd, L.g_post_ffn,
-                                  layers[li + 1].g_in, b.hid, b.xn, H, a.eps, stage));
+      PF_TRY(launch_pf_norm<true>(n, st, b.x2, vd, L.g_post_ffn, layers[li + 1].g_in, b.hid, xn_f32, H, a.eps,
+                                  stage, a16_h, ea_h));
   }
   const LayerArgs &last = layers[s.n_layers - 1];
   if (plan.logits != RowsPlan::kNone) {

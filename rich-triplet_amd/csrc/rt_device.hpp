@@ -141,6 +141,26 @@ RT_DEV float block_sum(float v, float *red) {
   return s;
 }
 
+template <int NT>
+RT_DEV float block_max(float v, float *red) {
+  v = wave_max(v);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();  // red may still be read from a previous call
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float m = red[0];
+#pragma unroll
+  for (int i = 1; i < NT / 64; ++i) m = fmaxf(m, red[i]);
+  return m;
+}
+
+// Four values of a GEMM A row as f16 scaled by 2^-e (e = f16_exponent_for of
+// the row's max |x|, the GEMM's A preparation), packed for one 8-byte store.
+RT_DEV uint2 f16x4_scaled(float4 v, int e) {
+  auto hb = [](float x, int ex) { return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)__builtin_amdgcn_ldexpf(x, -ex)); };
+  return make_uint2(hb(v.x, e) | (hb(v.y, e) << 16), hb(v.z, e) | (hb(v.w, e) << 16));
+}
+
 RT_DEV float gelu_tanh(float v) {
   // 0.5 v (1 + tanh(sqrt(2/pi) (v + 0.044715 v^3))), precise tanhf
   const float inner = 0.7978845608028654f * (v + 0.044715f * v * v * v);
