@@ -529,7 +529,7 @@ size_t prefill_gemm_workspace_bytes(const DecodeShape &s, int cap) {
   size_t m = 0;
   for (auto &nk : shapes) {
     m = std::max({m, q4k_gemm_workspace_bytes(cap, nk[0], nk[1]), proj_gemm_workspace_bytes(cap, nk[0], nk[1])});
-    for (int rows = 1; rows <= std::min(cap, 1024); ++rows)
+    for (int rows = 1; rows <= cap; ++rows)
       m = std::max(m, q4k_gemm_workspace_bytes(rows, nk[0], nk[1]));
   }
   return m;

@@ -354,6 +354,8 @@ __global__ __launch_bounds__(512) void k_q4k_gemm_w8b(const _Float16 *__restrict
 //            80 contiguous LDS bytes per column, two slots.  Five adjacent
 //            lanes read one column's bytes, so a copy instruction touches a
 //            few cache lines instead of one line per lane.
+// Split-K as in the eight-wave kernel, by whole super-blocks: blockIdx.y = s
+// takes blocks [s*nblocks/ksplit, (s+1)*nblocks/ksplit).
 // ---------------------------------------------------------------------------
 constexpr int kHSlotA = 128 * 128;       // bytes
 constexpr int kHSlotW = 256 * 80;        // bytes
@@ -361,7 +363,7 @@ constexpr int kHSlotW = 256 * 80;        // bytes
 __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restrict__ a16, const int *__restrict__ ea,
                                                        const uint8_t *__restrict__ w, const int *__restrict__ ew,
                                                        float *__restrict__ c, int M, int N, int K, int tiles_m,
-                                                       int tiles_n) {
+                                                       int tiles_n, int ksplit) {
   __shared__ __attribute__((aligned(1024))) uint8_t sa0[kHSlotA], sa1[kHSlotA];
   __shared__ __attribute__((aligned(1024))) uint8_t sw0[kHSlotW], sw1[kHSlotW];
 
@@ -375,8 +377,11 @@ __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restric
   const int gm = min(4, tiles_m - group * 4);
   const int tm = group * 4 + in_group % gm, tn = in_group / gm;
   const int m0 = tm * 128, n0 = tn * 256;
-  const int nblocks = K / 256, nchunks = K / kBK;
+  const int nblocks = K / 256;
   const size_t row_bytes = (size_t)nblocks * kQ4KBlockBytes;
+  const int split = (int)blockIdx.y;
+  const int b0 = split * nblocks / ksplit, b1 = (split + 1) * nblocks / ksplit;  // >= 1 block (host: ksplit <= nblocks)
+  if (ksplit > 1) c += (size_t)split * M * N;
 
   // A copy i (0..3) of this wave: rows 8*(4*wave+i) + [0,8); lane -> row
   // r = 8*(4*wave+i) + lane/8, physical segment lane%8, logical segment
@@ -427,13 +432,12 @@ __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restric
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = floatx16{};
 
-  issue_w(0, sw0);
-  issue_a(0, sa0);
+  issue_w(2 * b0, sw0);
+  issue_a(4 * b0, sa0);
   wait_vmcnt<0>();
   wg_barrier();
 
-  const int nhalves = 2 * nblocks;
-  for (int b = 0; b < nblocks; ++b) {
+  for (int b = b0; b < b1; ++b) {
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) {
       const int kc = 4 * b + cc;
@@ -442,14 +446,14 @@ __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restric
       // Chunk kc's A copy and (at an even chunk) its half-block's W copy were
       // issued one chunk ago: drain, then every wave's copies are in LDS and
       // every wave has finished with the slots the copies below overwrite.
-      if (kc > 0) {
+      if (kc > 4 * b0) {
         wait_vmcnt<0>();
         wait_lgkmcnt0();
         wg_barrier();
       }
       __builtin_amdgcn_sched_barrier(0);
-      if ((cc & 1) == 0) issue_w(min(2 * b + (cc >> 1) + 1, nhalves - 1), (cc >> 1) ? sw0 : sw1);
-      issue_a(min(kc + 1, nchunks - 1), (cc & 1) ? sa0 : sa1);
+      if ((cc & 1) == 0) issue_w(min(2 * b + (cc >> 1) + 1, 2 * b1 - 1), (cc >> 1) ? sw0 : sw1);
+      issue_a(min(kc + 1, 4 * b1 - 1), (cc & 1) ? sa0 : sa1);
       __builtin_amdgcn_sched_barrier(0);
 
       auto read_a = [&](int t, u32x4 (&af)[4]) __attribute__((always_inline)) {
@@ -537,14 +541,34 @@ __global__ __launch_bounds__(256) void k_gemm_splitk_sum(const float *__restrict
   }
 }
 
-// Split-K count for the eight-wave kernel: enough workgroups to cover the 256
-// CUs when the output has few 128x256 tiles (a prefill's down projection,
-// M=512 N=2560: 40 tiles), keeping at least 16 chunks (K=1024) per split.
+// Split-K count.
+// Up to 1024 rows (eight-wave kernel, one workgroup per CU): enough
+// workgroups to cover the 256 CUs when the output has few 128x256 tiles (a
+// prefill's down projection, M=512 N=2560: 40 tiles), keeping at least 16
+// chunks (K=1024) per split.
+// Above (half-block kernel, two workgroups per CU, 512 slots): the split that
+// minimises a time model fitted to MI355X measurements:
+//   ceil(tiles*ks/512)/ks rounds of 0.032 us per K element (x0.75 when at most
+//   256 workgroups run, one per CU), plus (2*ks+1)*M*N*4 bytes of partial
+//   tiles at 5 TB/s.
+// 4096x2560 outputs (320 tiles) split K=10240 three ways: 2 rounds of a third
+// instead of 1.25 rounds of the whole K.
 int gemm_ksplit(int M, int N, int K) {
-  if (M > 1024) return 1;
   const int ntiles = ((M + 127) / 128) * ((N + 255) / 256);
-  const int by_cus = 256 / ntiles, by_k = (K / kBK) / 16;
-  return max(1, min(by_cus, by_k));
+  if (M <= 1024) {
+    const int by_cus = 256 / ntiles, by_k = (K / kBK) / 16;
+    return max(1, min(by_cus, by_k));
+  }
+  auto est_us = [&](int ks) {
+    const int wgs = ntiles * ks;
+    const double rounds = (double)((wgs + 511) / 512) * (wgs <= 256 ? 0.75 : 1.0);
+    const double partial = ks > 1 ? (2.0 * ks + 1.0) * M * N * 4.0 / 5e6 : 0.0;
+    return rounds / ks * K * 0.032 + partial;
+  };
+  int best = 1;
+  for (int ks = 2; ks <= 4 && ks <= K / 256; ++ks)
+    if (est_us(ks) < est_us(best)) best = ks;
+  return best;
 }
 
 hipError_t launch_gemm_splitk_sum(const float *part, float *c, size_t mn, int ksplit, hipStream_t s) {
@@ -575,8 +599,12 @@ static hipError_t q4k_gemm_core(const _Float16 *a16, const int *ea, const uint8_
   const int tiles_m = (M + 127) / 128, tiles_n = (N + 255) / 256;
   const int ks = gemm_ksplit(M, N, K);
   if (ks > 1) {
-    hipLaunchKernelGGL(k_q4k_gemm_w8b<1>, dim3(tiles_m * tiles_n, ks), dim3(512), 0, s, a16, ea, wb, ew, part, M, N,
-                       K, tiles_m, tiles_n, ks);
+    if (M <= 1024)
+      hipLaunchKernelGGL(k_q4k_gemm_w8b<1>, dim3(tiles_m * tiles_n, ks), dim3(512), 0, s, a16, ea, wb, ew, part, M,
+                         N, K, tiles_m, tiles_n, ks);
+    else
+      hipLaunchKernelGGL(k_q4k_gemm_h, dim3(tiles_m * tiles_n, ks), dim3(256), 0, s, a16, ea, wb, ew, part, M, N, K,
+                         tiles_m, tiles_n, ks);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return launch_gemm_splitk_sum(part, c, (size_t)M * N, ks, s);
@@ -586,7 +614,7 @@ static hipError_t q4k_gemm_core(const _Float16 *a16, const int *ea, const uint8_
                        tiles_m, tiles_n, 1);
   else
     hipLaunchKernelGGL(k_q4k_gemm_h, dim3(tiles_m * tiles_n), dim3(256), 0, s, a16, ea, wb, ew, c, M, N, K, tiles_m,
-                       tiles_n);
+                       tiles_n, 1);
   return hipGetLastError();
 }
 

@@ -49,6 +49,8 @@ def _run_bf16(rt, dev, a_bits, blocks, m, n, k):
     (64, 2048, 2560, 4),     # Gemma q-projection shape, short prompt
     (512, 10240, 2560, 5),   # prefill, gate/up shape
     (512, 2560, 10240, 6),   # prefill, down-projection shape
+    (1100, 1024, 2560, 7),   # above 1024 rows: half-block kernel, K split 4 ways, ragged M
+    (2100, 2560, 10240, 8),  # half-block kernel, K split 3 ways (long-prompt down shape)
 ])
 def test_gemm_bf16_vs_oracle(rt, orc, dev, m, n, k, seed):
     blocks = orc.synth_q4k(100 + seed, n, k)
