@@ -523,15 +523,23 @@ hipError_t launch_pf_attn(int G, dim3 grid, hipStream_t st, const float *q, cons
 
 size_t prefill_gemm_workspace_bytes(const DecodeShape &s, int cap) {
   const int H = s.hidden, F = s.ffn, QD = s.n_q_heads * s.head_dim, KVD = s.n_kv_heads * s.head_dim;
-  const int shapes[5][2] = {{QD, H}, {KVD, H}, {H, QD}, {F, H}, {H, F}};
+  // The projection sets (K, then the rows of each matrix): the A part of the
+  // largest K, then each matrix's own region, which may keep split-K
+  // partials for the consumer.
+  const int sets[4][4] = {{H, QD, KVD, KVD}, {QD, H, 0, 0}, {H, F, F, 0}, {F, H, 0, 0}};
+  const int kmax = std::max({H, QD, F});
+  auto r256 = [](size_t v) { return (v + 255) & ~size_t(255); };
   // A chunk may hold fewer rows than cap, and a smaller M may split K more
   // ways: take the largest requirement over every row count up to cap.
   size_t m = 0;
-  for (auto &nk : shapes) {
-    m = std::max({m, q4k_gemm_workspace_bytes(cap, nk[0], nk[1]), proj_gemm_workspace_bytes(cap, nk[0], nk[1])});
-    for (int rows = 1; rows <= cap; ++rows)
-      m = std::max(m, q4k_gemm_workspace_bytes(rows, nk[0], nk[1]));
-  }
+  for (int rows = 1; rows <= cap; ++rows)
+    for (auto &st : sets) {
+      const int K = st[0];
+      size_t b = r256((size_t)rows * kmax * 2) + r256((size_t)rows * 4);
+      for (int i = 1; i < 4 && st[i]; ++i)
+        b += std::max(q4k_gemm_prepped_ws_bytes(rows, st[i], K), proj_gemm_prepped_ws_bytes(rows, st[i], K));
+      m = std::max(m, b);
+    }
   return m;
 }
 
@@ -573,6 +581,7 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
   auto gemm_ea = [&](int K) {
     return reinterpret_cast<int *>(static_cast<char *>(b.ws) + r256((size_t)n * K * 2));
   };
+  const int kmax = std::max({H, QD, F});
   _Float16 *a16_h = plan.mb ? nullptr : gemm_a16(H);  // producers that write A directly
   int *ea_h = plan.mb ? nullptr : gemm_ea(H);
   float *xn_f32 = plan.mb ? b.xn : nullptr;
@@ -590,16 +599,29 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
     // norms and the gelu product write it themselves (A == nullptr)
     _Float16 *a16 = gemm_a16(K);
     int *ea = gemm_ea(K);
-    char *rest = reinterpret_cast<char *>(ea) + r256((size_t)n * 4);
+    // The matrices' regions start after the A part of the largest K: the
+    // producer of the next set's A (a norm, the gelu product) writes it
+    // while it reads partials left here.
+    char *rest = static_cast<char *>(b.ws) + r256((size_t)n * kmax * 2) + r256((size_t)n * 4);
     hipError_t r = A ? launch_gemm_prep_a(A, n, K, a16, ea, st) : hipSuccess;
     if (r != hipSuccess) return r;
+    // each matrix in its own region; a split Q4_K GEMM leaves its partials
+    // there and the consumer adds them while reading (views)
     int i = 0;
     for (const MbMat &m : mats) {
       const int fmt = fmts.begin()[i];
-      r = fmt == RT_LINEAR_Q4K ? launch_q4k_gemm_prepped(a16, ea, m.w, m.y, n, m.n, K, rest, st)
-                               : launch_proj_gemm_prepped(a16, ea, fmt, m.w, m.y, n, m.n, K, rest, st);
+      RowsIn &v = *views.begin()[i++];
+      if (fmt == RT_LINEAR_Q4K) {
+        GemmLeft left{};
+        r = launch_q4k_gemm_prepped(a16, ea, m.w, m.y, n, m.n, K, rest, st, &left);
+        v = left.ks > 1 ? RowsIn{left.part, left.ks, (size_t)n * m.n, m.n, 0} : rows_plain(m.y, m.n);
+        rest += q4k_gemm_prepped_ws_bytes(n, m.n, K);
+      } else {
+        r = launch_proj_gemm_prepped(a16, ea, fmt, m.w, m.y, n, m.n, K, rest, st);
+        v = rows_plain(m.y, m.n);
+        rest += proj_gemm_prepped_ws_bytes(n, m.n, K);
+      }
       if (r != hipSuccess) return r;
-      *views.begin()[i++] = rows_plain(m.y, m.n);
     }
     return hipSuccess;
   };

@@ -219,6 +219,11 @@ size_t proj_gemm_workspace_bytes(int M, int N, int K) {
          (ks > 1 ? (size_t)ks * M * N * 4 : 0);
 }
 
+size_t proj_gemm_prepped_ws_bytes(int M, int N, int K) {
+  auto r256 = [](size_t b) { return (b + 255) & ~size_t(255); };
+  return proj_gemm_workspace_bytes(M, N, K) - r256((size_t)M * K * 2) - r256((size_t)M * 4);
+}
+
 hipError_t launch_proj_gemm_prepped(const _Float16 *a16, const int *ea, int fmt, const void *w, float *c, int M,
                                     int N, int K, void *ws, hipStream_t s) {
   if (M <= 0 || N <= 0 || K <= 0 || K % kFK != 0) return hipErrorInvalidValue;  // K moves in stages of 64

@@ -592,7 +592,7 @@ size_t q4k_gemm_workspace_bytes(int M, int N, int K) {
 // The matrix-core launch on prepared operands; `part` holds the split-K
 // partials when the shape splits K.
 static hipError_t q4k_gemm_core(const _Float16 *a16, const int *ea, const uint8_t *wb, const int *ew, float *part,
-                                float *c, int M, int N, int K, hipStream_t s) {
+                                float *c, int M, int N, int K, hipStream_t s, GemmLeft *left = nullptr) {
   // Up to 1024 rows: 128 x 256 tiles on eight waves (a prefill of a few
   // hundred tokens gives too few 256-row tiles to fill the chip); above that
   // the half-block kernel, two workgroups per CU.
@@ -607,8 +607,13 @@ static hipError_t q4k_gemm_core(const _Float16 *a16, const int *ea, const uint8_
                          tiles_m, tiles_n, ks);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (left) {
+      *left = GemmLeft{part, ks};
+      return hipSuccess;
+    }
     return launch_gemm_splitk_sum(part, c, (size_t)M * N, ks, s);
   }
+  if (left) *left = GemmLeft{c, 1};
   if (M <= 1024)
     hipLaunchKernelGGL(k_q4k_gemm_w8b<1>, dim3(tiles_m * tiles_n), dim3(512), 0, s, a16, ea, wb, ew, c, M, N, K,
                        tiles_m, tiles_n, 1);
@@ -639,8 +644,13 @@ hipError_t launch_q4k_gemm(const void *a, bool a_bf16, const void *w, float *c, 
   return q4k_gemm_core(a16, ea, wb, ew, part, c, M, N, K, s);
 }
 
+size_t q4k_gemm_prepped_ws_bytes(int M, int N, int K) {
+  auto r256 = [](size_t b) { return (b + 255) & ~size_t(255); };
+  return q4k_gemm_workspace_bytes(M, N, K) - r256((size_t)M * K * 2) - r256((size_t)M * 4);
+}
+
 hipError_t launch_q4k_gemm_prepped(const _Float16 *a16, const int *ea, const void *w, float *c, int M, int N, int K,
-                                   void *ws, hipStream_t s) {
+                                   void *ws, hipStream_t s, GemmLeft *left) {
   auto r256 = [](size_t b) { return (b + 255) & ~size_t(255); };
   char *p = static_cast<char *>(ws);
   int *ew = reinterpret_cast<int *>(p);
@@ -651,7 +661,7 @@ hipError_t launch_q4k_gemm_prepped(const _Float16 *a16, const int *ea, const voi
                      N, K);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  return q4k_gemm_core(a16, ea, wb, ew, part, c, M, N, K, s);
+  return q4k_gemm_core(a16, ea, wb, ew, part, c, M, N, K, s, left);
 }
 
 }  // namespace rt

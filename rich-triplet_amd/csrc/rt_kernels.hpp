@@ -39,8 +39,18 @@ hipError_t launch_proj_gemm(const float *a, int fmt, const void *w, float *c, in
 // (M*K*2 and M*4 bytes, each rounded up to 256).
 hipError_t launch_proj_gemm_prepped(const _Float16 *a16, const int *ea, int fmt, const void *w, float *c, int M,
                                     int N, int K, void *ws, hipStream_t s);
+// With `left`, a Q4_K GEMM that splits K leaves its partial tiles in ws
+// (left->part = [left->ks][M][N], summed by the consumer in split order)
+// instead of summing them into c; left->ks = 1 means the result is in c.
+struct GemmLeft {
+  const float *part;
+  int ks;
+};
 hipError_t launch_q4k_gemm_prepped(const _Float16 *a16, const int *ea, const void *w, float *c, int M, int N, int K,
-                                   void *ws, hipStream_t s);
+                                   void *ws, hipStream_t s, GemmLeft *left = nullptr);
+// Workspace bytes of the two prepped calls.
+size_t q4k_gemm_prepped_ws_bytes(int M, int N, int K);
+size_t proj_gemm_prepped_ws_bytes(int M, int N, int K);
 // Q4_K GEMM C[M,N] = A[M,K] . W[N,K]^T; A bf16 bits (a_bf16) or f32; ws holds
 // q4k_gemm_workspace_bytes(M, N, K) bytes of device scratch.
 size_t q4k_gemm_workspace_bytes(int M, int N, int K);
