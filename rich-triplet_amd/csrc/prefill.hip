@@ -289,16 +289,19 @@ RT_DEV f32x4_t mfma3(u32x4_t ahi, u32x4_t alo, u32x4_t bhi, u32x4_t blo, f32x4_t
                                                  acc, 0, 0, 0);
 }
 
-template <int D, int G>
-__global__ __launch_bounds__(256) void k_pf_attn(const float *__restrict__ q, const float *__restrict__ kc,
-                                                 const float *__restrict__ vc, float *__restrict__ out, PfAttnArgs p) {
+template <int D, int G, int W>
+__global__ __launch_bounds__(64 * W) void k_pf_attn(const float *__restrict__ q, const float *__restrict__ kc,
+                                                    const float *__restrict__ vc, float *__restrict__ out,
+                                                    PfAttnArgs p) {
   if (p.p0_dev) p.p0 = p.p0_dev[0];
+  constexpr int NT = 64 * W;                  // threads: W waves of 16 columns share each K/V stage
+  constexpr int NC = 16 * W;                  // columns per workgroup
   constexpr int KB = kPfKeys;
   constexpr int DS = D / 32;                  // k steps of the score MFMA
   constexpr int DT = D / 16;                  // 16-dim tiles of the output
   constexpr int KQ = D / 4;                   // float4 per cache row
-  constexpr int K_ITEMS = KB * KQ / 256;      // K float4 per thread per stage
-  constexpr int V_ITEMS = KB / 2 * KQ / 256;  // V key pairs x float4 per thread per stage
+  constexpr int K_ITEMS = KB * KQ / NT;       // K float4 per thread per stage
+  constexpr int V_ITEMS = KB / 2 * KQ / NT;   // V key pairs x float4 per thread per stage
   static_assert(K_ITEMS >= 1 && V_ITEMS >= 1, "D too small");
   using S = PfAttnSmem<D>;
   __shared__ __attribute__((aligned(16))) S sm;
@@ -307,10 +310,10 @@ __global__ __launch_bounds__(256) void k_pf_attn(const float *__restrict__ q, co
   const int kvh = (int)blockIdx.y;
   const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63), n16 = lane & 15, g = lane >> 4;
   const size_t qd = (size_t)p.n_kv_heads * G * D, kvd = (size_t)p.n_kv_heads * D;
-  const int col0 = b * 64;
+  const int col0 = b * NC;
   const int last_row = p.n - 1;
   const int key_first = pf_key_lo(p, p.p0 + col0 / G) & ~(KB - 1);
-  const int key_last = p.p0 + min(last_row, (col0 + 63) / G);
+  const int key_last = p.p0 + min(last_row, (col0 + NC - 1) / G);
   const int wt0 = (col0 + 16 * wave) / G;
   const bool wave_live = wt0 <= last_row;
   const int wkey_lo = pf_key_lo(p, p.p0 + wt0);
@@ -341,12 +344,12 @@ __global__ __launch_bounds__(256) void k_pf_attn(const float *__restrict__ q, co
   auto load_stage = [&](int k0) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < K_ITEMS; ++i) {
-      const int it = (int)threadIdx.x + 256 * i, key = it / KQ, qq = it % KQ;
+      const int it = (int)threadIdx.x + NT * i, key = it / KQ, qq = it % KQ;
       kr[i] = *reinterpret_cast<const float4 *>(kbase + (size_t)min(k0 + key, key_last) * kvd + 4 * qq);
     }
 #pragma unroll
     for (int i = 0; i < V_ITEMS; ++i) {
-      const int it = (int)threadIdx.x + 256 * i, pr = it / KQ, qq = it % KQ;
+      const int it = (int)threadIdx.x + NT * i, pr = it / KQ, qq = it % KQ;
       vr[i][0] = *reinterpret_cast<const float4 *>(vbase + (size_t)min(k0 + 2 * pr, key_last) * kvd + 4 * qq);
       vr[i][1] = *reinterpret_cast<const float4 *>(vbase + (size_t)min(k0 + 2 * pr + 1, key_last) * kvd + 4 * qq);
     }
@@ -354,14 +357,14 @@ __global__ __launch_bounds__(256) void k_pf_attn(const float *__restrict__ q, co
   auto store_stage = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < K_ITEMS; ++i) {
-      const int it = (int)threadIdx.x + 256 * i, key = it / KQ, qq = it % KQ;
+      const int it = (int)threadIdx.x + NT * i, key = it / KQ, qq = it % KQ;
       const uint2 p0 = split_pair(kr[i].x, kr[i].y), p1 = split_pair(kr[i].z, kr[i].w);
       *reinterpret_cast<uint2 *>(&sm.khi[key * S::KP + 4 * qq]) = make_uint2(p0.x, p1.x);
       *reinterpret_cast<uint2 *>(&sm.klo[key * S::KP + 4 * qq]) = make_uint2(p0.y, p1.y);
     }
 #pragma unroll
     for (int i = 0; i < V_ITEMS; ++i) {
-      const int it = (int)threadIdx.x + 256 * i, pr = it / KQ, qq = it % KQ;
+      const int it = (int)threadIdx.x + NT * i, pr = it / KQ, qq = it % KQ;
       const float a[4] = {vr[i][0].x, vr[i][0].y, vr[i][0].z, vr[i][0].w};
       const float c[4] = {vr[i][1].x, vr[i][1].y, vr[i][1].z, vr[i][1].w};
 #pragma unroll
@@ -502,16 +505,31 @@ __global__ __launch_bounds__(D) void k_pf_attn_combine(const float *__restrict__
   }
 }
 
+template <int D, int W>
+hipError_t launch_pf_attn_w(int G, dim3 grid, hipStream_t st, const float *q, const float *kc, const float *vc,
+                            float *out, const PfAttnArgs &p) {
+  switch (G) {
+    case 1: hipLaunchKernelGGL((k_pf_attn<D, 1, W>), grid, dim3(64 * W), 0, st, q, kc, vc, out, p); break;
+    case 2: hipLaunchKernelGGL((k_pf_attn<D, 2, W>), grid, dim3(64 * W), 0, st, q, kc, vc, out, p); break;
+    case 4: hipLaunchKernelGGL((k_pf_attn<D, 4, W>), grid, dim3(64 * W), 0, st, q, kc, vc, out, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// grid: (column blocks of 64, KV heads, key splits).  Without a key split and
+// from 256 columns on, workgroups of eight waves take 128 columns each, which
+// halves the K/V stage loads and bf16 splits per column.
 template <int D>
 hipError_t launch_pf_attn(int G, dim3 grid, hipStream_t st, const float *q, const float *kc, const float *vc,
                           float *out, const PfAttnArgs &p, int8_t *st_dig) {
-  switch (G) {
-    case 1: hipLaunchKernelGGL((k_pf_attn<D, 1>), grid, dim3(256), 0, st, q, kc, vc, out, p); break;
-    case 2: hipLaunchKernelGGL((k_pf_attn<D, 2>), grid, dim3(256), 0, st, q, kc, vc, out, p); break;
-    case 4: hipLaunchKernelGGL((k_pf_attn<D, 4>), grid, dim3(256), 0, st, q, kc, vc, out, p); break;
-    default: return hipErrorInvalidValue;
+  hipError_t e;
+  if (!p.split_stages && p.n * G >= 256) {
+    grid.x = (unsigned)((p.n * G + 127) / 128);
+    e = launch_pf_attn_w<D, 8>(G, grid, st, q, kc, vc, out, p);
+  } else {
+    e = launch_pf_attn_w<D, 4>(G, grid, st, q, kc, vc, out, p);
   }
-  hipError_t e = hipGetLastError();
   if (e != hipSuccess || !p.split_stages) return e;
   const int ncols = p.n * p.n_kv_heads * G;
   hipLaunchKernelGGL((k_pf_attn_combine<D>), dim3(ncols), dim3(D), 0, st, p.part_ml, p.part_o, out, ncols,
