@@ -183,19 +183,21 @@ __global__ __launch_bounds__(256) void k_pf_gelu_mul(RowsIn g, RowsIn u, float *
   }
 }
 
-// The same product for the GEMM path, one row per workgroup (F <= 16384): h
-// goes straight out as the down GEMM's A operand (f16 row, exponent ea[t]),
-// bit-identical to preparing the f32 row.
-__global__ __launch_bounds__(256) void k_pf_gelu_rows(RowsIn g, RowsIn u, int F, _Float16 *__restrict__ a16,
+// The same product for the GEMM path, one row per workgroup of kGeluRowT
+// threads (F <= 16384; 1024 threads measured 1% faster over a 4096-row
+// prefill than 256): h goes straight out as the down GEMM's A operand (f16
+// row, exponent ea[t]), bit-identical to preparing the f32 row.
+constexpr int kGeluRowT = 1024;
+__global__ __launch_bounds__(kGeluRowT) void k_pf_gelu_rows(RowsIn g, RowsIn u, int F, _Float16 *__restrict__ a16,
                                                       int *__restrict__ ea) {
-  constexpr int MAXP = 16;
-  __shared__ float red[4];
+  constexpr int MAXP = 16384 / 4 / kGeluRowT;
+  __shared__ float red[kGeluRowT / 64];
   const int t = (int)blockIdx.x, f4 = F / 4;
   float4 r[MAXP];
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < MAXP; ++i) {
-    const int c4 = (int)threadIdx.x + 256 * i;
+    const int c4 = (int)threadIdx.x + kGeluRowT * i;
     if (c4 < f4) {
       const float4 a = rows_in4(g, t, 4 * c4), b = rows_in4(u, t, 4 * c4);
       r[i] = make_float4(mul_nc(gelu_tanh(a.x), b.x), mul_nc(gelu_tanh(a.y), b.y), mul_nc(gelu_tanh(a.z), b.z),
@@ -203,12 +205,12 @@ __global__ __launch_bounds__(256) void k_pf_gelu_rows(RowsIn g, RowsIn u, int F,
       amax = fmaxf(amax, fmaxf(fmaxf(fabsf(r[i].x), fabsf(r[i].y)), fmaxf(fabsf(r[i].z), fabsf(r[i].w))));
     }
   }
-  const int e = f16_exponent_for(block_max<256>(amax, red));
+  const int e = f16_exponent_for(block_max<kGeluRowT>(amax, red));
   if (threadIdx.x == 0) ea[t] = e;
   uint2 *dst = reinterpret_cast<uint2 *>(a16 + (size_t)t * F);
 #pragma unroll
   for (int i = 0; i < MAXP; ++i) {
-    const int c4 = (int)threadIdx.x + 256 * i;
+    const int c4 = (int)threadIdx.x + kGeluRowT * i;
     if (c4 < f4) dst[c4] = f16x4_scaled(r[i], e);
   }
 }
@@ -696,7 +698,7 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
       const unsigned eg = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
       PF_CHECK(hipLaunchKernelGGL(k_pf_gelu_mul, dim3(eg), dim3(256), 0, st, vg, vu, b.g, n, F, stage));
     } else {
-      PF_CHECK(hipLaunchKernelGGL(k_pf_gelu_rows, dim3(n), dim3(256), 0, st, vg, vu, F, gemm_a16(F), gemm_ea(F)));
+      PF_CHECK(hipLaunchKernelGGL(k_pf_gelu_rows, dim3(n), dim3(kGeluRowT), 0, st, vg, vu, F, gemm_a16(F), gemm_ea(F)));
     }
     PF_TRY(proj(plan.mb ? b.g : nullptr, F, {L.fmt[kProjDown]}, {MbMat{L.wdown, b.dn, H, 0, 0}}, {&vd}));
     if (li + 1 < s.n_layers)
