@@ -206,6 +206,29 @@ def test_gpu_prefill_matches_oracle(rt, orc, group, mode, T):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("mode", [0, 1])
+def test_gpu_long_prompt_prefill_matches_oracle(rt, orc, mode):
+    """1100 rows: the projections run on the half-block GEMM with K split
+    (the consumers add the partial tiles while reading them), attention on
+    eight-wave workgroups of 128 columns; logits and KV rows vs the oracle."""
+    cfg = tiny(2, sliding_window=300)
+    T, max_seq = 1100, 1104
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=0, seed=6400 + mode)
+    toks = [(29 * i + 7) % cfg["vocab"] for i in range(T)]
+    d = gpu_ctx(rt, cfg, layers, embed, fnorm, max_seq)
+    got = d.prefill(toks, 0, mode)
+    ref_layers = fresh_caches(layers)
+    ref = orc.gemma3_prefill(cfg, ref_layers, embed, fnorm, toks, 0, mode)
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, ref) < LOGITS_TOL, rel_l2(got, ref)
+    for li in range(cfg["n_layers"]):
+        k, v = read_kv(d, cfg, li, T)
+        assert rel_l2(k, ref_layers[li]["k_cache"][:T]) < KV_TOL
+        assert rel_l2(v, ref_layers[li]["v_cache"][:T]) < KV_TOL
+    d.close()
+
+
+@pytest.mark.gpu
 def test_gpu_prefill_chunks_and_continuation(rt, orc):
     """Chunked prefill (7 rows per chunk: chunks of up to 8 rows run their
     projections on the batched GEMV, larger ones on the GEMM) and a prefill
