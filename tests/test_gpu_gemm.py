@@ -51,6 +51,8 @@ def _run_bf16(rt, dev, a_bits, blocks, m, n, k):
     (512, 2560, 10240, 6),   # prefill, down-projection shape
     (1100, 1024, 2560, 7),   # above 1024 rows: half-block kernel, K split 4 ways, ragged M
     (2100, 2560, 10240, 8),  # half-block kernel, K split 3 ways (long-prompt down shape)
+    (1024, 2560, 2048, 9),   # the kernel switch: eight-wave kernel up to 1024 rows (K split 2 ways) ...
+    (1025, 2560, 2048, 10),  # ... half-block kernel from 1025 (K split 2 ways), one ragged row
 ])
 def test_gemm_bf16_vs_oracle(rt, orc, dev, m, n, k, seed):
     blocks = orc.synth_q4k(100 + seed, n, k)
