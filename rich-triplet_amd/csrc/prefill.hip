@@ -625,6 +625,25 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
     char *rest = static_cast<char *>(b.ws) + r256((size_t)n * kmax * 2) + r256((size_t)n * 4);
     hipError_t r = A ? launch_gemm_prep_a(A, n, K, a16, ea, st) : hipSuccess;
     if (r != hipSuccess) return r;
+    // Long prompts, a set of Q4_K matrices: one matrix-core launch for the
+    // set (its tiles fill the CUs in whole rounds), row exponents of each
+    // matrix at the start of its region
+    bool all_q4k = true;
+    for (int f : fmts) all_q4k = all_q4k && f == RT_LINEAR_Q4K;
+    if (all_q4k && mats.size() > 1 && q4k_gemm_multi_ok(n, (int)mats.size())) {
+      const void *w[3];
+      float *c[3];
+      int nn[3];
+      void *ew[3];
+      int i = 0;
+      char *reg = rest;
+      for (const MbMat &m : mats) {
+        w[i] = m.w, c[i] = m.y, nn[i] = m.n, ew[i] = reg;
+        reg += q4k_gemm_prepped_ws_bytes(n, m.n, K);
+        *views.begin()[i++] = rows_plain(m.y, m.n);
+      }
+      return launch_q4k_gemm_multi_prepped(a16, ea, i, w, c, nn, ew, n, K, st);
+    }
     // each matrix in its own region; a split Q4_K GEMM leaves its partials
     // there and the consumer adds them while reading (views)
     int i = 0;

@@ -356,14 +356,25 @@ __global__ __launch_bounds__(512) void k_q4k_gemm_w8b(const _Float16 *__restrict
 //            few cache lines instead of one line per lane.
 // Split-K as in the eight-wave kernel, by whole super-blocks: blockIdx.y = s
 // takes blocks [s*nblocks/ksplit, (s+1)*nblocks/ksplit).
+// Up to three matrices sharing A (q|k|v, gate|up) run as one launch: their
+// 256-column tiles are numbered one after another (HMats::tn0), and a
+// workgroup takes the matrix its column tile falls in.
 // ---------------------------------------------------------------------------
 constexpr int kHSlotA = 128 * 128;       // bytes
 constexpr int kHSlotW = 256 * 80;        // bytes
 
+struct HMats {
+  const uint8_t *w[3];
+  const int *ew[3];
+  float *c[3];
+  int n[3];
+  int tn0[3];  // first column tile of each matrix
+  int count;
+};
+
 __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restrict__ a16, const int *__restrict__ ea,
-                                                       const uint8_t *__restrict__ w, const int *__restrict__ ew,
-                                                       float *__restrict__ c, int M, int N, int K, int tiles_m,
-                                                       int tiles_n, int ksplit) {
+                                                       HMats mats, int M, int K, int tiles_m, int tiles_n,
+                                                       int ksplit) {
   __shared__ __attribute__((aligned(1024))) uint8_t sa0[kHSlotA], sa1[kHSlotA];
   __shared__ __attribute__((aligned(1024))) uint8_t sw0[kHSlotW], sw1[kHSlotW];
 
@@ -376,7 +387,13 @@ __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restric
   const int group = tile / (4 * tiles_n), in_group = tile % (4 * tiles_n);
   const int gm = min(4, tiles_m - group * 4);
   const int tm = group * 4 + in_group % gm, tn = in_group / gm;
-  const int m0 = tm * 128, n0 = tn * 256;
+  int mi = 0;
+  while (mi + 1 < mats.count && tn >= mats.tn0[mi + 1]) ++mi;  // wave-uniform
+  const uint8_t *__restrict__ w = mats.w[mi];
+  const int *__restrict__ ew = mats.ew[mi];
+  float *__restrict__ c = mats.c[mi];
+  const int N = mats.n[mi];
+  const int m0 = tm * 128, n0 = (tn - mats.tn0[mi]) * 256;
   const int nblocks = K / 256;
   const size_t row_bytes = (size_t)nblocks * kQ4KBlockBytes;
   const int split = (int)blockIdx.y;
@@ -603,8 +620,8 @@ static hipError_t q4k_gemm_core(const _Float16 *a16, const int *ea, const uint8_
       hipLaunchKernelGGL(k_q4k_gemm_w8b<1>, dim3(tiles_m * tiles_n, ks), dim3(512), 0, s, a16, ea, wb, ew, part, M,
                          N, K, tiles_m, tiles_n, ks);
     else
-      hipLaunchKernelGGL(k_q4k_gemm_h, dim3(tiles_m * tiles_n, ks), dim3(256), 0, s, a16, ea, wb, ew, part, M, N, K,
-                         tiles_m, tiles_n, ks);
+      hipLaunchKernelGGL(k_q4k_gemm_h, dim3(tiles_m * tiles_n, ks), dim3(256), 0, s, a16, ea,
+                         HMats{{wb}, {ew}, {part}, {N}, {0}, 1}, M, K, tiles_m, tiles_n, ks);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (left) {
@@ -618,8 +635,8 @@ static hipError_t q4k_gemm_core(const _Float16 *a16, const int *ea, const uint8_
     hipLaunchKernelGGL(k_q4k_gemm_w8b<1>, dim3(tiles_m * tiles_n), dim3(512), 0, s, a16, ea, wb, ew, c, M, N, K,
                        tiles_m, tiles_n, 1);
   else
-    hipLaunchKernelGGL(k_q4k_gemm_h, dim3(tiles_m * tiles_n), dim3(256), 0, s, a16, ea, wb, ew, c, M, N, K, tiles_m,
-                       tiles_n, 1);
+    hipLaunchKernelGGL(k_q4k_gemm_h, dim3(tiles_m * tiles_n), dim3(256), 0, s, a16, ea,
+                       HMats{{wb}, {ew}, {c}, {N}, {0}, 1}, M, K, tiles_m, tiles_n, 1);
   return hipGetLastError();
 }
 
@@ -662,6 +679,36 @@ hipError_t launch_q4k_gemm_prepped(const _Float16 *a16, const int *ea, const voi
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   return q4k_gemm_core(a16, ea, wb, ew, part, c, M, N, K, s, left);
+}
+
+bool q4k_gemm_multi_ok(int M, int count) { return M > 1024 && count >= 1 && count <= 3; }
+
+hipError_t launch_q4k_gemm_multi_prepped(const _Float16 *a16, const int *ea, int count, const void *const *w,
+                                         float *const *c, const int *n, void *const *ws, int M, int K,
+                                         hipStream_t s) {
+  if (!q4k_gemm_multi_ok(M, count) || K % 256 != 0) return hipErrorInvalidValue;
+  HMats mats{};
+  int tiles_n = 0;
+  for (int i = 0; i < count; ++i) {
+    if (n[i] <= 0) return hipErrorInvalidValue;
+    int *ew = static_cast<int *>(ws[i]);
+    const uint8_t *wb = static_cast<const uint8_t *>(w[i]);
+    hipLaunchKernelGGL((k_gemm_prep<float>), dim3((n[i] + 3) / 4), dim3(256), 0, s, nullptr, nullptr, nullptr, wb,
+                       ew, 0, n[i], K);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    mats.w[i] = wb;
+    mats.ew[i] = ew;
+    mats.c[i] = c[i];
+    mats.n[i] = n[i];
+    mats.tn0[i] = tiles_n;
+    tiles_n += (n[i] + 255) / 256;
+  }
+  mats.count = count;
+  const int tiles_m = (M + 127) / 128;
+  hipLaunchKernelGGL(k_q4k_gemm_h, dim3(tiles_m * tiles_n), dim3(256), 0, s, a16, ea, mats, M, K, tiles_m, tiles_n,
+                     1);
+  return hipGetLastError();
 }
 
 }  // namespace rt

@@ -48,6 +48,13 @@ struct GemmLeft {
 };
 hipError_t launch_q4k_gemm_prepped(const _Float16 *a16, const int *ea, const void *w, float *c, int M, int N, int K,
                                    void *ws, hipStream_t s, GemmLeft *left = nullptr);
+// Up to three Q4_K matrices sharing a prepared A (q|k|v, gate|up) in one
+// matrix-core launch, for M > 1024 (q4k_gemm_multi_ok); ws[i] holds at least
+// n[i]*4 bytes (matrix i's row exponents); no K split.
+bool q4k_gemm_multi_ok(int M, int count);
+hipError_t launch_q4k_gemm_multi_prepped(const _Float16 *a16, const int *ea, int count, const void *const *w,
+                                         float *const *c, const int *n, void *const *ws, int M, int K,
+                                         hipStream_t s);
 // Workspace bytes of the two prepped calls.
 size_t q4k_gemm_prepped_ws_bytes(int M, int N, int K);
 size_t proj_gemm_prepped_ws_bytes(int M, int N, int K);
