@@ -56,6 +56,20 @@ RT_DEV void load8<float>(const float *p, float v[8]) {
 RT_DEV uint32_t half_bits(_Float16 h) { return (uint32_t)__builtin_bit_cast(uint16_t, h); }
 
 
+// Row exponent of W row n (one wave, one block header per lane: a strided
+// walk by a single thread is latency-bound at K = 12288).
+RT_DEV void prep_w_row(const uint8_t *__restrict__ w, int *__restrict__ ew, int n, int K, int lane) {
+  const int kb = K / 256;
+  const uint8_t *row = w + (size_t)n * kb * kQ4KBlockBytes;
+  float bound = 0.f;  // |w| <= max(15*63*|d|, 63*|dmin|)
+  for (int i = lane; i < kb; i += 64) {
+    const uint32_t h = *reinterpret_cast<const uint32_t *>(row + (size_t)i * kQ4KBlockBytes);
+    bound = fmaxf(bound, fmaxf(945.f * fabsf(half_bits_to_f32(h & 0xFFFFu)), 63.f * fabsf(half_bits_to_f32(h >> 16))));
+  }
+  bound = wave_max(bound);
+  if (lane == 0) ew[n] = f16_exponent_for(bound);
+}
+
 template <typename TA>
 __global__ __launch_bounds__(256) void k_gemm_prep(const TA *__restrict__ a, _Float16 *__restrict__ a16,
                                                    int *__restrict__ ea, const uint8_t *__restrict__ w,
@@ -90,19 +104,9 @@ __global__ __launch_bounds__(256) void k_gemm_prep(const TA *__restrict__ a, _Fl
       *reinterpret_cast<uint4 *>(out + g * 8) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
     }
   } else {
-    // One wave per W row, one block header per lane (a strided walk by a
-    // single thread is latency-bound at K = 12288).
-    const int n = (b - M) * 4 + (int)(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (n >= N) return;
-    const int kb = K / 256;
-    const uint8_t *row = w + (size_t)n * kb * kQ4KBlockBytes;
-    float bound = 0.f;  // |w| <= max(15*63*|d|, 63*|dmin|)
-    for (int i = lane; i < kb; i += 64) {
-      const uint32_t h = *reinterpret_cast<const uint32_t *>(row + (size_t)i * kQ4KBlockBytes);
-      bound = fmaxf(bound, fmaxf(945.f * fabsf(half_bits_to_f32(h & 0xFFFFu)), 63.f * fabsf(half_bits_to_f32(h >> 16))));
-    }
-    bound = wave_max(bound);
-    if (lane == 0) ew[n] = f16_exponent_for(bound);
+    // one wave per W row
+    const int n = (b - M) * 4 + (int)(threadIdx.x >> 6);
+    if (n < N) prep_w_row(w, ew, n, K, threadIdx.x & 63);
   }
 }
 
@@ -371,6 +375,14 @@ struct HMats {
   int tn0[3];  // first column tile of each matrix
   int count;
 };
+
+// The W row exponents of every matrix of a set in one launch: wave r takes
+// row r of the matrices' rows laid end to end.
+__global__ __launch_bounds__(256) void k_gemm_prep_w_multi(HMats mats, int K) {
+  int r = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6), i = 0;
+  while (i + 1 < mats.count && r >= mats.n[i]) r -= mats.n[i++];  // wave-uniform
+  if (r < mats.n[i]) prep_w_row(mats.w[i], const_cast<int *>(mats.ew[i]), r, K, threadIdx.x & 63);
+}
 
 __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restrict__ a16, const int *__restrict__ ea,
                                                        HMats mats, int M, int K, int tiles_m, int tiles_n,
@@ -688,23 +700,21 @@ hipError_t launch_q4k_gemm_multi_prepped(const _Float16 *a16, const int *ea, int
                                          hipStream_t s) {
   if (!q4k_gemm_multi_ok(M, count) || K % 256 != 0) return hipErrorInvalidValue;
   HMats mats{};
-  int tiles_n = 0;
+  int tiles_n = 0, rows = 0;
   for (int i = 0; i < count; ++i) {
     if (n[i] <= 0) return hipErrorInvalidValue;
-    int *ew = static_cast<int *>(ws[i]);
-    const uint8_t *wb = static_cast<const uint8_t *>(w[i]);
-    hipLaunchKernelGGL((k_gemm_prep<float>), dim3((n[i] + 3) / 4), dim3(256), 0, s, nullptr, nullptr, nullptr, wb,
-                       ew, 0, n[i], K);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    mats.w[i] = wb;
-    mats.ew[i] = ew;
+    mats.w[i] = static_cast<const uint8_t *>(w[i]);
+    mats.ew[i] = static_cast<const int *>(ws[i]);
     mats.c[i] = c[i];
     mats.n[i] = n[i];
     mats.tn0[i] = tiles_n;
     tiles_n += (n[i] + 255) / 256;
+    rows += n[i];
   }
   mats.count = count;
+  hipLaunchKernelGGL(k_gemm_prep_w_multi, dim3((rows + 3) / 4), dim3(256), 0, s, mats, K);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
   const int tiles_m = (M + 127) / 128;
   hipLaunchKernelGGL(k_q4k_gemm_h, dim3(tiles_m * tiles_n), dim3(256), 0, s, a16, ea, mats, M, K, tiles_m, tiles_n,
                      1);
