@@ -126,6 +126,9 @@ __global__ __launch_bounds__(T) void k_qkv(DecodeArgs a, LayerArgs L, LayerArgs 
   const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
   ProRegs<K, T> pr;
   pro_load<K, T, MODE>(a, a.x2, a.dn, prev.g_post_ffn, L.g_in, pr);
+  // every wave's prologue loads go out before any weight load of the
+  // workgroup: they return ahead of the weight stream
+  __syncthreads();
   Tile tile;
   tile.load([&](int rl) -> const uint8_t * { return W + (size_t)(r0 + rl) * row_bytes; }, W);
   pro_finish<K, T, MODE, true>(a, pr, a.hid, dl, bred, a.xn);
@@ -183,34 +186,34 @@ __global__ __launch_bounds__(256) void k_gelu_mul_vec(float *h, const float *__r
 
 // ---------------------------------------------------------------------------
 // k_gateup: x2 = hid + rms(o)(1+g_pa); n2 = rms(x2)(1+g_pf); each workgroup
-// then computes RPI gate rows and the same RPI up rows and stores
+// then computes GR gate rows and the same GR up rows, walked as one list of
+// 2*GR rows (gate first) in iterations of RPI rows, and stores
 // h[j] = gelu_tanh(gate[j]) * up[j]  (transformer4.rs:328-334)
 // ---------------------------------------------------------------------------
-template <int NB, int T>
+template <int NB, int T, int GR>
 __global__ __launch_bounds__(T) void k_gateup(DecodeArgs a, LayerArgs L) {
-  using Tile = Q4KTile<NB, T, 2>;  // iteration 0: gate rows, 1: up rows
+  constexpr int RPI = T / (4 * NB);
+  using Tile = Q4KTile<NB, T, (2 * GR + RPI - 1) / RPI>;
   constexpr int K = NB * 256;
-  constexpr int RPI = Tile::RPI;
   __shared__ __attribute__((aligned(16))) uint32_t dl[NB * 4 * kDPitch];
   __shared__ float red[Tile::ROWS * NB];
   __shared__ float bred[T / 64];
   const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
-  const int j0 = (int)blockIdx.x * RPI;  // RPI divides ffn (checked on the host)
+  const int j0 = (int)blockIdx.x * GR;  // GR divides ffn (checked on the host)
   ProRegs<K, T> pr;
   pro_load<K, T, Pro::Resid>(a, a.hid, a.o, L.g_post_attn, L.g_pre_ffn, pr);
   Tile tile;
   tile.load([&](int rl) -> const uint8_t * {
-    return rl < RPI ? L.wgate + (size_t)(j0 + rl) * row_bytes : L.wup + (size_t)(j0 + rl - RPI) * row_bytes;
+    return rl < GR ? L.wgate + (size_t)(j0 + rl) * row_bytes
+                   : (rl < 2 * GR ? L.wup + (size_t)(j0 + rl - GR) * row_bytes : nullptr);
   }, L.wgate);
   pro_finish<K, T, Pro::Resid, true>(a, pr, a.x2, dl, bred);
   __syncthreads();
-  ChunkD cx;
-  chunkd_from_lds(dl, tile.slot, cx);
-  tile.compute_digits(cx, red);
+  tile.compute_digits_lds(dl, red);
   __syncthreads();
-  for (int i = threadIdx.x; i < RPI; i += T) {
+  for (int i = threadIdx.x; i < GR; i += T) {
     const float g = reduce_row<NB>(red, i);
-    const float u = reduce_row<NB>(red, RPI + i);
+    const float u = reduce_row<NB>(red, GR + i);
     a.h[j0 + i] = mul_nc(gelu_tanh(g), u);
   }
 }
@@ -626,6 +629,8 @@ __global__ __launch_bounds__(256) void k_lmhead_batch(const uint16_t *__restrict
 // ---------------------------------------------------------------------------
 template <int NB, int T>
 static constexpr int rows_per_iter() { return T / (NB * 4); }
+// gate rows (and as many up rows) per k_gateup workgroup
+constexpr int kGateRowsBig = 20, kGateRowsSmall = 32;
 
 struct Launch {
   hipStream_t s;
@@ -647,10 +652,9 @@ static void launch_qkv(Launch &l, const DecodeArgs &a, const LayerArgs &L, const
   l.check();
 }
 
-template <int NB, int T>
+template <int NB, int T, int GR>
 static void launch_gateup(Launch &l, const DecodeArgs &a, const LayerArgs &L, int ffn) {
-  constexpr int RPI = T / (NB * 4);
-  hipLaunchKernelGGL((k_gateup<NB, T>), dim3(ffn / RPI), dim3(T), 0, l.s, a, L);
+  hipLaunchKernelGGL((k_gateup<NB, T, GR>), dim3(ffn / GR), dim3(T), 0, l.s, a, L);
   l.check();
 }
 
@@ -753,8 +757,9 @@ static hipError_t enqueue_layers(const DecodeShape &s, const DecodeArgs &a, cons
     else if (qd == 2048) launch_gemv<8, 512, 1>(l, L.wo, a.attn, a.o, s.hidden);
     else launch_gemv<2, 256, 1>(l, L.wo, a.attn, a.o, s.hidden);
     if (q4(kProjGate) && q4(kProjUp)) {
-      if (big) launch_gateup<10, 640>(l, a, L, s.ffn);
-      else launch_gateup<2, 256>(l, a, L, s.ffn);
+      // 20 gate + 20 up rows per workgroup: 512 workgroups, all resident at once
+      if (big) launch_gateup<10, 640, kGateRowsBig>(l, a, L, s.ffn);
+      else launch_gateup<2, 256, kGateRowsSmall>(l, a, L, s.ffn);
     } else {
       launch_prologue<Pro::Resid>(l, s, a, a.hid, a.o, L.g_post_attn, L.g_pre_ffn, a.x2);
       launch_proj(l, L.fmt[kProjGate], L.wgate, a.xn, a.h, s.ffn, s.hidden);
@@ -773,7 +778,8 @@ static hipError_t enqueue_layers(const DecodeShape &s, const DecodeArgs &a, cons
 
 hipError_t enqueue_lm_head(const DecodeShape &s, const DecodeArgs &a, const LayerArgs &last, hipStream_t stream) {
   Launch l{stream};
-  const dim3 grid(2048);
+  // three workgroups per CU stay resident for the whole pass (grid-stride rows)
+  const dim3 grid(768);
   if (s.hidden == 2560) hipLaunchKernelGGL((k_lmhead<5>), grid, dim3(256), 0, l.s, a, last);
   else hipLaunchKernelGGL((k_lmhead<1>), grid, dim3(256), 0, l.s, a, last);
   l.check();
@@ -822,7 +828,8 @@ bool decode_rows_divisible(const DecodeShape &s, const char **why) {
   const bool big = s.hidden == 2560;
   const int qkv_rows_per_wg = big ? rows_per_iter<10, 640>() : rows_per_iter<2, 256>();
   if (qd % qkv_rows_per_wg || kvd % qkv_rows_per_wg) return *why = "q/kv rows must divide into workgroup tiles", false;
-  if (s.ffn % qkv_rows_per_wg) return *why = "ffn rows must divide into gate/up tiles", false;
+  const int gate_rows_per_wg = big ? kGateRowsBig : kGateRowsSmall;
+  if (s.ffn % gate_rows_per_wg) return *why = "ffn rows must divide into gate/up tiles", false;
   return true;  // the o and down GEMVs bound their rows themselves
 }
 

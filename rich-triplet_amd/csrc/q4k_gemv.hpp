@@ -222,6 +222,23 @@ RT_DEV void q4k_scale_min_pair(uint32_t s0, uint32_t s1, uint32_t s2, int c, uin
   mvp = c < 2 ? mv_lo : mv_hi;
 }
 
+// f32 combine of one chunk's exact integer sums (low digit l0/h0, high digit
+// l1/h1 of the low and high 32-element halves) with the block's scales.
+RT_DEV float q4k_digits_combine(const uint4 hd, int c, uint32_t l0, int l1, uint32_t h0, int h1, float delta,
+                                float sum_lo, float sum_hi) {
+  const float d = half_bits_to_f32(hd.x & 0xFFFFu);
+  const float dm = half_bits_to_f32(hd.x >> 16);
+  uint32_t svp, mvp;
+  q4k_scale_min_pair(hd.y, hd.z, hd.w, c, svp, mvp);
+  const float dot_lo = fmaf((float)l1, 256.0f, (float)l0);  // exact: |value| < 2^24
+  const float dot_hi = fmaf((float)h1, 256.0f, (float)h0);
+  const float sv1 = (float)(svp & 0xFFu), sv2 = (float)(svp >> 8);
+  const float mv1 = (float)(mvp & 0xFFu), mv2 = (float)(mvp >> 8);
+  const float qsum = fmaf(sv2, dot_hi, sv1 * dot_lo);
+  const float msum = fmaf(mv2, sum_hi, mv1 * sum_lo);
+  return fmaf(d * delta, qsum, -(dm * msum));
+}
+
 RT_DEV float q4k_chunk_dot_digits(const uint4 hd, const uint4 qa, const uint4 qb, int c, const ChunkD &x,
                                   uint32_t m4) {
   const float d = half_bits_to_f32(hd.x & 0xFFFFu);
@@ -290,6 +307,47 @@ struct Q4KTile {
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
       float p = q4k_chunk_dot_digits(hd[it], qa[it], qb[it], c, x, m4);
+      p = quad_sum(p);
+      if (c == 0 && valid[it]) red[(it * RPI + rsub) * NB + b] = p;
+    }
+  }
+
+  // compute_digits with the digit words read from LDS four at a time and
+  // applied to every iteration's nibbles before the next four: 16 digit
+  // registers live instead of 35, for tiles with several iterations.
+  RT_DEV void compute_digits_lds(const uint32_t *dl, float *red) {
+    const uint32_t m4 = opaque_u32(0x0F0F0F0Fu);
+    const uint32_t *base = dl + slot * kDPitch;
+    uint32_t l0[ITERS], h0[ITERS];
+    int l1[ITERS], h1[ITERS];
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) l0[it] = h0[it] = 0u, l1[it] = h1[it] = 0;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const uint4 a0 = *reinterpret_cast<const uint4 *>(base + 4 * g);       // x0 of low-half words 4g..4g+3
+      const uint4 b0 = *reinterpret_cast<const uint4 *>(base + 8 + 4 * g);   // x0 of high-half words
+      const uint4 a1 = *reinterpret_cast<const uint4 *>(base + 16 + 4 * g);  // x1 of low-half words
+      const uint4 b1 = *reinterpret_cast<const uint4 *>(base + 24 + 4 * g);  // x1 of high-half words
+      const uint32_t A0[4] = {a0.x, a0.y, a0.z, a0.w}, B0[4] = {b0.x, b0.y, b0.z, b0.w};
+      const uint32_t A1[4] = {a1.x, a1.y, a1.z, a1.w}, B1[4] = {b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+      for (int it = 0; it < ITERS; ++it) {
+        const uint4 q = g ? qb[it] : qa[it];
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t lo = w[j] & m4, hi = (w[j] >> 4) & m4;
+          l0[it] = __builtin_amdgcn_udot4(lo, A0[j], l0[it], false);
+          l1[it] = __builtin_amdgcn_sdot4((int)lo, (int)A1[j], l1[it], false);
+          h0[it] = __builtin_amdgcn_udot4(hi, B0[j], h0[it], false);
+          h1[it] = __builtin_amdgcn_sdot4((int)hi, (int)B1[j], h1[it], false);
+        }
+      }
+    }
+    const float4 f = *reinterpret_cast<const float4 *>(base + 32);  // delta, sum_lo, sum_hi
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      float p = q4k_digits_combine(hd[it], c, l0[it], l1[it], h0[it], h1[it], f.x, f.y, f.z);
       p = quad_sum(p);
       if (c == 0 && valid[it]) red[(it * RPI + rsub) * NB + b] = p;
     }
