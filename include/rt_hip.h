@@ -145,6 +145,20 @@ rt_status rt_linear_gemm_f32(int32_t fmt, const void *w, const float *a, float *
  * aligned, k % 256 == 0. */
 rt_status rt_q4k_gemv_batch(const void *w, const float *a, float *c, int64_t m, int64_t n, int64_t k, void *stream);
 
+/* rt_q4k_gemv_batch that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and results as rt_q4k_gemv_batch; its
+ * workspace is a fixed per-GPU device array of rt_noalloc_scratch_bytes()
+ * (8 MiB), which bounds n and k: the staged rows, (k/64)*1152 bytes rounded
+ * up to 256, plus the split-K partials, (k/512)*32*n bytes for k/256 even
+ * (else (k/256)*32*n), must fit, else RT_EINVAL.  Every call on one GPU
+ * shares that array: calls that overlap on one GPU (two streams, two host
+ * threads) race and must be serialised by the caller. */
+rt_status rt_q4k_gemv_batch_noalloc(const void *w, const float *a, float *c, int64_t m, int64_t n, int64_t k,
+                                    void *stream);
+size_t rt_noalloc_scratch_bytes(void);
+
 /* Host drop-in for Q4KMat::matmul_q4k_t_exact (autograd2.rs:1490-1625):
  * a is [m, k] f32, out receives [m, rows] f32.  m == 1 takes the GEMV path, as
  * matmul_q4k_t does (autograd2.rs:1440-1443).  Weights are cached like

@@ -54,6 +54,8 @@ _SIGNATURES = {
     "rt_gemv_bf16_t": (_i32, [_vp, _sz, _vp, _sz, _vp]),
     "rt_weight_cache_clear": (_i32, []),
     "rt_q4k_gemv_batch": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "rt_q4k_gemv_batch_noalloc": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "rt_noalloc_scratch_bytes": (_sz, []),
     "rt_q6k_repack": (_i32, [_vp, _sz, _vp]),
     "rt_q8_0_repack": (_i32, [_vp, _sz, _vp]),
     "rt_q6k_dequant_f32": (_i32, [_vp, _sz, _vp, _vp]),
@@ -172,6 +174,12 @@ def bf16_gemv(w, x, y, n: int, k: int, stream=None) -> None:
 def q4k_gemv_batch(w, a, c, m: int, n: int, k: int, stream=None) -> None:
     """c[m][n] = a[m][k] . W[n][k] for m <= 8 rows (gemv_q4k_t_batch)."""
     check(lib().rt_q4k_gemv_batch(_p(w), _p(a), _p(c), m, n, k, _stream(stream)))
+
+
+def q4k_gemv_batch_noalloc(w, a, c, m: int, n: int, k: int, stream=None) -> None:
+    """q4k_gemv_batch on a fixed per-GPU workspace: no device allocation.
+    Calls that overlap on one GPU share that workspace and race."""
+    check(lib().rt_q4k_gemv_batch_noalloc(_p(w), _p(a), _p(c), m, n, k, _stream(stream)))
 
 
 def q6k_gemv(w, x, y, n: int, k: int, stream=None) -> None:

@@ -226,6 +226,71 @@ rt_status rt_q4k_gemv_batch(const void *w, const float *a, float *c, int64_t m, 
 }  // extern "C"
 
 // ---------------------------------------------------------------------------
+// Allocation-free batched GEMV.  Its workspace (staged activation digits and
+// split-K partial sums) is a fixed device array, `scratch`, one copy per GPU
+// the library runs on, held until the process ends.  The host side never
+// passes the array's name to a kernel: the first call on a device looks up
+// that device's copy with hipGetSymbolAddress and keeps the address.
+// Every call on one GPU shares its array; calls that overlap on one GPU
+// (different streams, or host threads) race on it.  The stage is fully
+// written by the staging kernel and every partial by the GEMV before it is
+// read, so nothing has to start at zero.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
+constexpr int kNoAllocMaxDevices = 64;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kNoAllocMaxDevices] = {};
+
+rt_status scratch_address(const char *who, void **out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_error(e, who);
+  if (dev < 0 || dev >= kNoAllocMaxDevices) return set_error(RT_EINVAL, "%s: device %d beyond %d", who, dev, kNoAllocMaxDevices);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_error(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return set_error(RT_EHIP, "%s: hipGetSymbolAddress returned null", who);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return RT_OK;
+}
+}  // namespace
+
+extern "C" {
+
+size_t rt_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+rt_status rt_q4k_gemv_batch_noalloc(const void *w, const float *a, float *c, int64_t m, int64_t n, int64_t k,
+                                    void *stream) {
+  static const char *who = "rt_q4k_gemv_batch_noalloc";
+  rt_status st = check_gemv_shape(who, w, a, c, n, k, 256);
+  if (st != RT_OK) return st;
+  if (m < 1 || m > kMbMaxRows) return set_error(RT_EINVAL, "%s: m=%lld outside [1, 8]", who, (long long)m);
+  const size_t stage = (mb_stage_bytes((int)k) + 255) & ~size_t(255);
+  const size_t need = stage + mb_part_bytes((int)n, (int)k);
+  if (need > kNoAllocScratchBytes)
+    return set_error(RT_EINVAL, "%s: n=%lld k=%lld needs %zu bytes of workspace, more than the fixed %zu", who,
+                     (long long)n, (long long)k, need, kNoAllocScratchBytes);
+  void *ws = nullptr;
+  st = scratch_address(who, &ws);
+  if (st != RT_OK) return st;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = launch_mb_stage(a, (int)m, (int)k, ws, s);
+  if (e == hipSuccess) {
+    MbMat mat{static_cast<const uint8_t *>(w), c, (int)n, 0, 0};
+    e = launch_q4k_gemv_mb(&mat, 1, (int)m, (int)k, ws, reinterpret_cast<float *>(static_cast<char *>(ws) + stage), s);
+  }
+  return hip_error(e, who);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
 // Host-pointer drop-ins with a weight cache keyed by (host pointer, bytes).
 // ---------------------------------------------------------------------------
 namespace {
