@@ -91,8 +91,12 @@ rt_status rt_weight_cache_clear(void);
  * weights (the reference's GPU path) give ~1.6e-3.
  * A is bf16 bits (rt_q4k_gemm_bf16) or f32 (rt_q4k_gemm_f32), row-major
  * [m,k]; every row of A must start 16-byte aligned (k % 256 == 0 ensures it).
- * The library keeps a per-thread, per-device workspace of about m*k*2 bytes,
- * grown on demand (growth synchronises the device).
+ * The library keeps a workspace of about m*k*2 bytes per (host thread,
+ * device, stream), shared with rt_linear_gemm_f32 and rt_q4k_gemv_batch on
+ * that stream.  It grows on demand, but not while the stream is being
+ * captured: a captured call that would need more returns RT_ESTATE, so make
+ * the same call once outside capture first.  Outgrown buffers stay
+ * allocated (a graph captured earlier may still read them).
  * ------------------------------------------------------------------------- */
 rt_status rt_q4k_gemm_bf16(const uint16_t *a_dev, const void *w_dev, float *c_dev, int64_t m, int64_t n, int64_t k,
                            void *stream);
@@ -134,15 +138,16 @@ rt_status rt_q8_0_gemv(const void *w, const float *x, float *y, int64_t n, int64
  * (as rt_q4k_gemm_f32).  Non-Q4_K rows are widened to f16 with a
  * power-of-two scale per row, A likewise, f32 accumulation on the matrix
  * cores; k % 256 == 0 (Q6_K, Q4_K) or k % 64 == 0; device pointers, a and w
- * 16-byte aligned.  Uses the per-thread workspace of rt_q4k_gemm_f32, about
- * (m + n) * k * 2 bytes. */
+ * 16-byte aligned.  Uses the per-(thread, device, stream) workspace of
+ * rt_q4k_gemm_f32, about (m + n) * k * 2 bytes. */
 rt_status rt_linear_gemm_f32(int32_t fmt, const void *w, const float *a, float *c, int64_t m, int64_t n, int64_t k,
                              void *stream);
 
 /* gemv_q4k_t_batch (metal_decode.rs:459-521): c[m][n] = a[m][k] . W[n][k]
  * for m = 1..8 rows (the speculative verify batch), reading the weights once
  * for all rows (int8 matrix cores); device pointers, a and w 16-byte
- * aligned, k % 256 == 0. */
+ * aligned, k % 256 == 0.  Uses the per-(thread, device, stream) workspace of
+ * rt_q4k_gemm_f32 (see there for graph capture). */
 rt_status rt_q4k_gemv_batch(const void *w, const float *a, float *c, int64_t m, int64_t n, int64_t k, void *stream);
 
 /* rt_q4k_gemv_batch that allocates nothing.  No counterpart in the

@@ -12,6 +12,8 @@
 #include <mutex>
 #include <string>
 #include <utility>
+#include <vector>
+#include <algorithm>
 
 #include "../../include/rt_hip.h"
 #include "rt_capi_util.hpp"
@@ -151,7 +153,7 @@ rt_status rt_q8_0_gemv(const void *w, const float *x, float *y, int64_t n, int64
 }  // extern "C"
 
 namespace {
-rt_status gemm_workspace(size_t bytes, void **out);
+rt_status gemm_workspace(size_t bytes, hipStream_t stream, void **out);
 
 rt_status q4k_gemm_entry(const char *who, const void *a, bool a_bf16, const void *w, float *c, int64_t m, int64_t n,
                          int64_t k, void *stream) {
@@ -164,7 +166,7 @@ rt_status q4k_gemm_entry(const char *who, const void *a, bool a_bf16, const void
   if (!aligned16(a) || !aligned16(w)) return set_error(RT_EINVAL, "%s: a and w must be 16-byte aligned", who);
   if ((reinterpret_cast<uintptr_t>(c) & 3u) != 0) return set_error(RT_EINVAL, "%s: c must be 4-byte aligned", who);
   void *ws = nullptr;
-  rt_status st = gemm_workspace(q4k_gemm_workspace_bytes((int)m, (int)n, (int)k), &ws);
+  rt_status st = gemm_workspace(q4k_gemm_workspace_bytes((int)m, (int)n, (int)k), (hipStream_t)stream, &ws);
   if (st != RT_OK) return st;
   return hip_error(launch_q4k_gemm(a, a_bf16, w, c, (int)m, (int)n, (int)k, ws, (hipStream_t)stream), who);
 }
@@ -199,7 +201,7 @@ rt_status rt_linear_gemm_f32(int32_t fmt, const void *w, const float *a, float *
   if (!aligned16(a) || !aligned16(w)) return set_error(RT_EINVAL, "%s: a and w must be 16-byte aligned", who);
   if ((reinterpret_cast<uintptr_t>(c) & 3u) != 0) return set_error(RT_EINVAL, "%s: c must be 4-byte aligned", who);
   void *ws = nullptr;
-  rt_status st = gemm_workspace(proj_gemm_workspace_bytes((int)m, (int)n, (int)k), &ws);
+  rt_status st = gemm_workspace(proj_gemm_workspace_bytes((int)m, (int)n, (int)k), (hipStream_t)stream, &ws);
   if (st != RT_OK) return st;
   return hip_error(launch_proj_gemm(a, fmt, w, c, (int)m, (int)n, (int)k, ws, (hipStream_t)stream), who);
 }
@@ -212,7 +214,7 @@ rt_status rt_q4k_gemv_batch(const void *w, const float *a, float *c, int64_t m, 
   if (m < 1 || m > kMbMaxRows) return set_error(RT_EINVAL, "rt_q4k_gemv_batch: m=%lld outside [1, 8]", (long long)m);
   const size_t stage = (mb_stage_bytes((int)k) + 255) & ~size_t(255);
   void *ws = nullptr;
-  st = gemm_workspace(stage + mb_part_bytes((int)n, (int)k), &ws);
+  st = gemm_workspace(stage + mb_part_bytes((int)n, (int)k), (hipStream_t)stream, &ws);
   if (st != RT_OK) return st;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e = launch_mb_stage(a, (int)m, (int)k, ws, s);
@@ -353,31 +355,40 @@ rt_status stage(size_t bytes, void **out) {
   return RT_OK;
 }
 
-// GEMM workspace (A in f16 plus row exponents), one per (thread, device),
-// grow-only.  Growth synchronises the device before freeing the old buffer,
-// which kernels queued by earlier calls may still read.
+// GEMM / batched-GEMV workspace (A in f16 plus row exponents, staged digits,
+// split-K partials), one per (host thread, device, stream), so calls queued
+// on different streams never share one.  It grows on demand, by at least
+// doubling, but never while its stream is being captured into a graph (such a
+// call returns RT_ESTATE: run it once uncaptured first).  A buffer it
+// outgrows is kept, not freed: a graph captured earlier may still read it.
 struct GemmWorkspace {
   void *buf = nullptr;
   size_t cap = 0;
+  std::vector<void *> retired;
 };
-thread_local std::map<int, GemmWorkspace> g_gemm_ws;
+thread_local std::map<std::pair<int, hipStream_t>, GemmWorkspace> g_gemm_ws;
 
-rt_status gemm_workspace(size_t bytes, void **out) {
+rt_status gemm_workspace(size_t bytes, hipStream_t stream, void **out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_error(e, "hipGetDevice");
-  GemmWorkspace &w = g_gemm_ws[dev];
+  GemmWorkspace &w = g_gemm_ws[{dev, stream}];
   if (w.cap < bytes) {
-    if (w.buf) {
-      e = hipDeviceSynchronize();
-      if (e != hipSuccess) return hip_error(e, "gemm workspace sync");
-      (void)hipFree(w.buf);
-    }
-    w.buf = nullptr;
-    w.cap = 0;
-    e = hipMalloc(&w.buf, bytes);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &cs);
+    if (e != hipSuccess) return hip_error(e, "hipStreamIsCapturing");
+    if (cs != hipStreamCaptureStatusNone)
+      return set_error(RT_ESTATE,
+                       "workspace must grow to %zu bytes while its stream is being captured; make the same call once "
+                       "outside capture first",
+                       bytes);
+    const size_t grow = std::max(bytes, 2 * w.cap);
+    void *nb = nullptr;
+    e = hipMalloc(&nb, grow);
     if (e != hipSuccess) return hip_error(e, "gemm workspace hipMalloc");
-    w.cap = bytes;
+    if (w.buf) w.retired.push_back(w.buf);
+    w.buf = nb;
+    w.cap = grow;
   }
   *out = w.buf;
   return RT_OK;
@@ -439,7 +450,7 @@ rt_status rt_matmul_q4k_t(const float *a, size_t m, size_t k, const uint8_t *blo
   const size_t abytes = (m * k * sizeof(float) + 255) & ~size_t(255);
   st = stage(abytes + m * rows * sizeof(float), &buf);
   if (st != RT_OK) return st;
-  st = gemm_workspace(q4k_gemm_workspace_bytes((int)m, (int)rows, (int)k), &ws);
+  st = gemm_workspace(q4k_gemm_workspace_bytes((int)m, (int)rows, (int)k), nullptr, &ws);
   if (st != RT_OK) return st;
   float *ad = static_cast<float *>(buf);
   float *cd = reinterpret_cast<float *>(static_cast<char *>(buf) + abytes);

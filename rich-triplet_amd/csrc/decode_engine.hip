@@ -254,7 +254,10 @@ static rt_status bind_buf(rt_decode *d, const void *src, size_t bytes, int32_t d
   rt_status st = dalloc(d, bytes, &p);
   if (st != RT_OK) return st;
   hipError_t e = hipMemcpy(p, src, bytes, hipMemcpyHostToDevice);
-  if (e != hipSuccess) return hip_error(e, what);
+  if (e != hipSuccess) {
+    dfree(d, p);
+    return hip_error(e, what);
+  }
   owned.push_back(p);
   *dst = p;
   return RT_OK;
@@ -279,30 +282,54 @@ rt_status rt_decode_set_layer(rt_decode *d, int32_t layer, const rt_gemma3_layer
 
 rt_status rt_decode_set_layer_formats(rt_decode *d, int32_t layer, const rt_gemma3_layer *w, const int32_t *formats,
                                       int32_t device_ptrs) {
-  if (!d || !w || !formats) return set_error(RT_EINVAL, "rt_decode_set_layer: null pointer");
+  if (!d) return set_error(RT_EINVAL, "rt_decode_set_layer: null context");
   const rt_gemma3_config &c = d->cfg;
   if (layer < 0 || layer >= c.n_layers) return set_error(RT_EINVAL, "rt_decode_set_layer: layer %d out of range", layer);
+  // Any failure from here on leaves the layer unset: its old uploads are
+  // freed, the captured graphs dropped, and rt_decode_step answers RT_ESTATE
+  // until the layer is set again.  Nothing is freed or uploaded before every
+  // argument has been checked.
+  auto unset = [&](rt_status st) {
+    (void)hipStreamSynchronize(d->stream);
+    for (void *q : d->owned_layer[layer]) dfree(d, q);
+    d->owned_layer[layer].clear();
+    d->layer_set[layer] = 0;
+    drop_graph(d);
+    return st;
+  };
+  if (!w || !formats) return unset(set_error(RT_EINVAL, "rt_decode_set_layer: null pointer"));
   {
     const size_t H = c.hidden, F = c.ffn, QD = (size_t)c.n_q_heads * c.head_dim, KVD = (size_t)c.n_kv_heads * c.head_dim;
     const size_t shape[7][2] = {{QD, H}, {KVD, H}, {KVD, H}, {H, QD}, {F, H}, {F, H}, {H, F}};
     static const char *names[7] = {"q", "k", "v", "o", "gate", "up", "down"};
     for (int p = 0; p < 7; ++p)
       if (!proj_bytes(formats[p], shape[p][0], shape[p][1]))
-        return set_error(RT_EINVAL, "rt_decode_set_layer: projection %s has unsupported format %d", names[p], formats[p]);
+        return unset(set_error(RT_EINVAL, "rt_decode_set_layer: projection %s has unsupported format %d", names[p],
+                               formats[p]));
+  }
+  // Every pointer is checked before anything is freed or uploaded; the new
+  // binding is built aside and replaces the old one only when it is whole.
+  const void *srcs[13] = {w->q, w->k, w->v, w->o, w->gate, w->up, w->down, w->in_norm, w->post_attn_norm,
+                          w->pre_ffn_norm, w->post_ffn_norm, w->q_norm, w->k_norm};
+  static const char *src_names[13] = {"q", "k", "v", "o", "gate", "up", "down", "in_norm", "post_attn_norm",
+                                      "pre_ffn_norm", "post_ffn_norm", "q_norm", "k_norm"};
+  for (int i = 0; i < 13; ++i) {
+    if (!srcs[i]) return unset(set_error(RT_EINVAL, "rt_decode_set_layer: %s is null", src_names[i]));
+    if (device_ptrs && (reinterpret_cast<uintptr_t>(srcs[i]) & 15u) != 0)
+      return unset(set_error(RT_EINVAL, "rt_decode_set_layer: %s must be 16-byte aligned", src_names[i]));
   }
   (void)hipStreamSynchronize(d->stream);
-  for (void *p : d->owned_layer[layer]) dfree(d, p);
-  d->owned_layer[layer].clear();
   const size_t H = c.hidden, F = c.ffn, D = c.head_dim;
   const size_t QD = (size_t)c.n_q_heads * D, KVD = (size_t)c.n_kv_heads * D;
-  LayerArgs &L = d->layers[layer];
-  std::vector<void *> &own = d->owned_layer[layer];
+  LayerArgs L = d->layers[layer];  // keeps the cache, RoPE table and window of the layer
+  std::vector<void *> own;
   const void *p;
-  rt_status st;
-#define B(field, src, bytes, cast)                                         \
-  st = bind_buf(d, src, bytes, device_ptrs, own, &p, #field);                  \
-  if (st != RT_OK) return st;                                              \
-  L.field = (cast)p;
+  rt_status st = RT_OK;
+#define B(field, src, bytes, cast)                                  \
+  if (st == RT_OK) {                                                \
+    st = bind_buf(d, src, bytes, device_ptrs, own, &p, #field);     \
+    if (st == RT_OK) L.field = (cast)p;                             \
+  }
   B(wq, w->q, proj_bytes(formats[kProjQ], QD, H), const uint8_t *);
   B(wk, w->k, proj_bytes(formats[kProjK], KVD, H), const uint8_t *);
   B(wv, w->v, proj_bytes(formats[kProjV], KVD, H), const uint8_t *);
@@ -310,10 +337,6 @@ rt_status rt_decode_set_layer_formats(rt_decode *d, int32_t layer, const rt_gemm
   B(wgate, w->gate, proj_bytes(formats[kProjGate], F, H), const uint8_t *);
   B(wup, w->up, proj_bytes(formats[kProjUp], F, H), const uint8_t *);
   B(wdown, w->down, proj_bytes(formats[kProjDown], H, F), const uint8_t *);
-  for (int p = 0; p < 7; ++p) L.fmt[p] = formats[p];
-  d->all_q4k = true;
-  for (const LayerArgs &X : d->layers)
-    for (int p = 0; p < 7; ++p) d->all_q4k = d->all_q4k && X.fmt[p] == RT_LINEAR_Q4K;
   B(g_in, w->in_norm, H * 4, const float *);
   B(g_post_attn, w->post_attn_norm, H * 4, const float *);
   B(g_pre_ffn, w->pre_ffn_norm, H * 4, const float *);
@@ -321,29 +344,49 @@ rt_status rt_decode_set_layer_formats(rt_decode *d, int32_t layer, const rt_gemm
   B(g_q, w->q_norm, D * 4, const float *);
   B(g_k, w->k_norm, D * 4, const float *);
 #undef B
-  d->layer_set[layer] = 1;
+  if (st != RT_OK) {
+    for (void *q : own) dfree(d, q);
+    return unset(st);
+  }
+  for (void *q : d->owned_layer[layer]) dfree(d, q);  // replaced by the new binding
+  d->owned_layer[layer].clear();
   drop_graph(d);
+  for (int i = 0; i < 7; ++i) L.fmt[i] = formats[i];
+  d->layers[layer] = L;
+  d->owned_layer[layer] = std::move(own);
+  d->all_q4k = true;
+  for (const LayerArgs &X : d->layers)
+    for (int i = 0; i < 7; ++i) d->all_q4k = d->all_q4k && X.fmt[i] == RT_LINEAR_Q4K;
+  d->layer_set[layer] = 1;
   return RT_OK;
 }
 
 rt_status rt_decode_set_embed(rt_decode *d, const uint16_t *embed, const float *final_norm, int32_t device_ptrs) {
-  if (!d) return set_error(RT_EINVAL, "rt_decode_set_embed: null pointer");
+  if (!d) return set_error(RT_EINVAL, "rt_decode_set_embed: null context");
+  // as rt_decode_set_layer: a failure leaves the embedding unset
   (void)hipStreamSynchronize(d->stream);
   std::vector<void *> own;
+  const void *pe = nullptr, *pf = nullptr;
+  rt_status st = RT_OK;
+  if (!embed || !final_norm) st = set_error(RT_EINVAL, "rt_decode_set_embed: %s is null", embed ? "final_norm" : "embed");
+  if (st == RT_OK) st = bind_buf(d, embed, (size_t)d->cfg.vocab * d->cfg.hidden * 2, device_ptrs, own, &pe, "embed");
+  if (st == RT_OK) st = bind_buf(d, final_norm, (size_t)d->cfg.hidden * 4, device_ptrs, own, &pf, "final_norm");
   dfree(d, d->embed_owned);
   dfree(d, d->final_owned);
   d->embed_owned = d->final_owned = nullptr;
-  const void *p;
-  rt_status st = bind_buf(d, embed, (size_t)d->cfg.vocab * d->cfg.hidden * 2, device_ptrs, own, &p, "embed");
-  if (st != RT_OK) return st;
-  d->args.embed = (const uint16_t *)p;
-  if (!device_ptrs) d->embed_owned = (void *)p;
-  st = bind_buf(d, final_norm, (size_t)d->cfg.hidden * 4, device_ptrs, own, &p, "final_norm");
-  if (st != RT_OK) return st;
-  d->args.g_final = (const float *)p;
-  if (!device_ptrs) d->final_owned = (void *)p;
-  d->embed_set = true;
   drop_graph(d);
+  if (st != RT_OK) {
+    for (void *q : own) dfree(d, q);
+    d->embed_set = false;
+    return st;
+  }
+  d->args.embed = (const uint16_t *)pe;
+  d->args.g_final = (const float *)pf;
+  if (!device_ptrs) {
+    d->embed_owned = (void *)pe;
+    d->final_owned = (void *)pf;
+  }
+  d->embed_set = true;
   return RT_OK;
 }
 

@@ -13,6 +13,8 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <exception>
+#include <new>
 #include <string>
 #include <thread>
 #include <unordered_map>
@@ -373,10 +375,13 @@ const MetaValue *meta(const rt_gguf *g, const char *key) {
 }
 
 rt_status read_bytes(const rt_gguf *g, const TensorEntry &t, void *dst) {
-  const uint64_t at = g->data_start + t.offset;
-  if (t.n_bytes == 0 || at < g->data_start || at + t.n_bytes > g->file_size)
-    return set_error(RT_EINVAL, "gguf: tensor '%s' (%llu bytes at %llu) lies outside the file", t.name.c_str(),
-                     (unsigned long long)t.n_bytes, (unsigned long long)at);
+  // every comparison is against the file size, so no sum can wrap
+  const bool inside = t.n_bytes > 0 && t.offset <= g->file_size && g->data_start <= g->file_size - t.offset &&
+                      t.n_bytes <= g->file_size - (g->data_start + t.offset);
+  const uint64_t at = inside ? g->data_start + t.offset : t.offset;
+  if (!inside)
+    return set_error(RT_EINVAL, "gguf: tensor '%s' (%llu bytes at data offset %llu) lies outside the file",
+                     t.name.c_str(), (unsigned long long)t.n_bytes, (unsigned long long)t.offset);
   uint8_t *d = static_cast<uint8_t *>(dst);
   uint64_t done = 0;
   while (done < t.n_bytes) {
@@ -388,11 +393,26 @@ rt_status read_bytes(const rt_gguf *g, const TensorEntry &t, void *dst) {
   return RT_OK;
 }
 
+// The loader's extern "C" entry points allocate host memory (std::vector,
+// std::string, threads): no C++ exception may cross the C boundary.
+template <class F>
+rt_status guarded(const char *who, F body) {
+  try {
+    return body();
+  } catch (const std::bad_alloc &) {
+    return set_error(RT_ENOMEM, "%s: out of host memory", who);
+  } catch (const std::exception &e) {
+    return set_error(RT_EINVAL, "%s: %s", who, e.what());
+  } catch (...) {
+    return set_error(RT_EINVAL, "%s: unexpected exception", who);
+  }
+}
+
 }  // namespace
 
 extern "C" {
 
-rt_status rt_gguf_open(const char *path, rt_gguf **out) {
+static rt_status gguf_open(const char *path, rt_gguf **out) {
   if (!path || !out) return set_error(RT_EINVAL, "rt_gguf_open: null pointer");
   *out = nullptr;
   const int fd = open(path, O_RDONLY | O_CLOEXEC);
@@ -402,8 +422,15 @@ rt_status rt_gguf_open(const char *path, rt_gguf **out) {
     close(fd);
     return set_error(RT_EINVAL, "rt_gguf_open: cannot stat '%s'", path);
   }
-  auto *g = new rt_gguf();
+  rt_gguf *g = nullptr;
+  try {
+    g = new rt_gguf();
+  } catch (...) {
+    close(fd);
+    throw;
+  }
   g->path = path, g->fd = fd, g->file_size = (uint64_t)st.st_size;
+  try {
   Reader r(fd, g->file_size);
   auto fail = [&](const char *what) {
     rt_status s = set_error(RT_EINVAL, "rt_gguf_open: %s: %s (at byte %llu)", path, what, (unsigned long long)r.pos());
@@ -445,6 +472,7 @@ rt_status rt_gguf_open(const char *path, rt_gguf **out) {
     t.type = (int32_t)type;
     uint64_t bpb, epb;
     t.n_bytes = block_info(t.type, bpb, epb) ? (t.n_elem + epb - 1) / epb * bpb : 0;
+    if (t.n_bytes > g->file_size) return fail("a tensor is larger than the file");
   }
   uint64_t align = 32;  // general.alignment when it is an integer (gguf_loader.rs:218-221)
   if (meta(g, "general.alignment")) {
@@ -454,6 +482,14 @@ rt_status rt_gguf_open(const char *path, rt_gguf **out) {
   g->data_start = (r.pos() + align - 1) / align * align;
   *out = g;
   return RT_OK;
+  } catch (...) {
+    rt_gguf_close(g);
+    throw;
+  }
+}
+
+rt_status rt_gguf_open(const char *path, rt_gguf **out) {
+  return guarded("rt_gguf_open", [&] { return gguf_open(path, out); });
 }
 
 rt_status rt_gguf_close(rt_gguf *g) {
@@ -553,7 +589,7 @@ rt_status rt_gguf_read_tensor(const rt_gguf *g, int64_t idx, void *dst, uint64_t
   return read_bytes(g, *t, dst);
 }
 
-rt_status rt_gguf_tensor_to_f32(const rt_gguf *g, int64_t idx, float *dst, uint64_t n_elem) {
+static rt_status gguf_tensor_to_f32(const rt_gguf *g, int64_t idx, float *dst, uint64_t n_elem) {
   const TensorEntry *t = entry(g, idx);
   if (!t || !dst) return set_error(RT_EINVAL, "rt_gguf_tensor_to_f32: bad handle, index or buffer");
   if (n_elem < t->n_elem)
@@ -567,7 +603,11 @@ rt_status rt_gguf_tensor_to_f32(const rt_gguf *g, int64_t idx, float *dst, uint6
   return decode_to_f32(t->type, raw.data(), t->n_elem, dst);
 }
 
-rt_status rt_q4k_quantize(const float *src, size_t rows, size_t cols, uint8_t *blocks) {
+rt_status rt_gguf_tensor_to_f32(const rt_gguf *g, int64_t idx, float *dst, uint64_t n_elem) {
+  return guarded("rt_gguf_tensor_to_f32", [&] { return gguf_tensor_to_f32(g, idx, dst, n_elem); });
+}
+
+static rt_status q4k_quantize(const float *src, size_t rows, size_t cols, uint8_t *blocks) {
   if (!src || !blocks) return set_error(RT_EINVAL, "rt_q4k_quantize: null pointer");
   if (cols == 0 || cols % 256 != 0)
     return set_error(RT_EINVAL, "rt_q4k_quantize: cols must be a multiple of 256, got %zu", cols);
@@ -579,7 +619,11 @@ rt_status rt_q4k_quantize(const float *src, size_t rows, size_t cols, uint8_t *b
   return RT_OK;
 }
 
-rt_status rt_gguf_load_linear_ex(const rt_gguf *g, int64_t idx, int32_t flags, rt_linear *out) {
+rt_status rt_q4k_quantize(const float *src, size_t rows, size_t cols, uint8_t *blocks) {
+  return guarded("rt_q4k_quantize", [&] { return q4k_quantize(src, rows, cols, blocks); });
+}
+
+static rt_status gguf_load_linear(const rt_gguf *g, int64_t idx, int32_t flags, rt_linear *out) {
   const TensorEntry *t = entry(g, idx);
   if (!t || !out) return set_error(RT_EINVAL, "rt_gguf_load_linear: bad handle or index");
   std::memset(out, 0, sizeof *out);
@@ -671,6 +715,10 @@ rt_status rt_gguf_load_linear_ex(const rt_gguf *g, int64_t idx, int32_t flags, r
   out->format = format, out->src_type = t->type, out->rows = rows, out->cols = cols;
   out->data = dev, out->bytes = host.size();
   return RT_OK;
+}
+
+rt_status rt_gguf_load_linear_ex(const rt_gguf *g, int64_t idx, int32_t flags, rt_linear *out) {
+  return guarded("rt_gguf_load_linear", [&] { return gguf_load_linear(g, idx, flags, out); });
 }
 
 rt_status rt_gguf_load_linear(const rt_gguf *g, int64_t idx, rt_linear *out) {

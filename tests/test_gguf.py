@@ -322,6 +322,29 @@ def test_reader_rejects_bad_files(rt, orc, tmp_path):
         rt.GgufFile(str(tmp_path / "does-not-exist.gguf"))
 
 
+def test_reader_rejects_oversized_and_wrapping_tensors(rt, orc, tmp_path):
+    """A tensor whose byte size exceeds the file fails at open; a data offset
+    near 2^64 (offset + size would wrap) fails the read instead of passing a
+    wrapped bounds check."""
+    import struct
+    big = tmp_path / "big.gguf"
+    write_gguf(big, [], [("huge", [1 << 60], GG_F32, np.zeros(64, np.uint8))])
+    with pytest.raises(rt.RtError, match="larger than the file"):
+        rt.GgufFile(str(big))
+    wrap = tmp_path / "wrap.gguf"
+    write_gguf(wrap, [], [("w", [16], GG_F32, np.zeros(64, np.uint8))])
+    blob = bytearray(wrap.read_bytes())
+    name = b"w"
+    at = blob.index(struct.pack("<Q", len(name)) + name) + 8 + len(name)
+    at += 4 + 8 + 4  # n_dims, one dimension, type -> the offset field
+    blob[at:at + 8] = struct.pack("<Q", (1 << 64) - 32)
+    wrap.write_bytes(bytes(blob))
+    g = rt.GgufFile(str(wrap))
+    with pytest.raises(rt.RtError, match="outside the file"):
+        g.read_tensor_bytes(0)
+    g.close()
+
+
 def test_load_linear_rejects_before_upload(rt, orc, tmp_path):
     """Shape and type errors are reported on the host, before any device call."""
     path = tmp_path / "w.gguf"

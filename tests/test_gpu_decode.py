@@ -307,3 +307,31 @@ def test_gemma3_4b_shape_batch_matches_sequential(rt, orc, dev):
         assert err < 1e-3
         assert int(np.argmax(got[i])) == int(np.argmax(ref))
     d_s.close()
+
+
+def test_failed_set_unsets_layer_and_embed(rt, orc):
+    """A re-set that fails (a null norm pointer, a null final norm) is refused
+    before anything is uploaded and leaves that layer (embedding) unset: the
+    next step answers RT_ESTATE instead of running a graph over freed
+    weights.  Setting it again restores the step bit for bit."""
+    import ctypes as C
+    cfg = tiny(2)
+    max_seq, pos = 32, 6
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=pos, seed=31)
+    d = build_ctx(rt, cfg, layers, embed, fnorm, pos, max_seq)
+    first = d.decode_step(9, pos)
+    L = rt.lib()
+    out = np.empty(cfg["vocab"], np.float32)
+    fields = {k: (0 if k == "q_norm" else rt._addr(layers[1][k])) for k, _ in rt.Gemma3Layer._fields_}
+    bad = rt.Gemma3Layer(**fields)
+    fmts = (C.c_int32 * 7)(*([rt.LINEAR_Q4K] * 7))
+    assert L.rt_decode_set_layer_formats(d._h, 1, C.byref(bad), fmts, 0) == rt.RT_EINVAL
+    assert "q_norm is null" in L.rt_last_error().decode()
+    assert L.rt_decode_step(d._h, 9, pos, out.ctypes.data) == rt.RT_ESTATE
+    d.set_layer(1, layers[1])
+    assert np.array_equal(d.decode_step(9, pos), first)
+    assert L.rt_decode_set_embed(d._h, rt._addr(embed), None, 0) == rt.RT_EINVAL
+    assert L.rt_decode_step(d._h, 9, pos, out.ctypes.data) == rt.RT_ESTATE
+    d.set_embed(embed, fnorm)
+    assert np.array_equal(d.decode_step(9, pos), first)
+    d.close()

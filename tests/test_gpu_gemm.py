@@ -183,3 +183,39 @@ def test_matmul_q4k_t_host(rt, orc):
     one = rt.matmul_q4k_t(a[:1], blocks, n)
     assert np.array_equal(one[0], rt.gemv_q4k_t(a[0], blocks, n))
     rt.weight_cache_clear()
+
+
+def test_gemm_workspace_under_graph_capture(rt, orc, dev):
+    """A stream's workspace does not grow during a capture: the call returns
+    RT_ESTATE before launching anything.  After one uncaptured call of that
+    size the same call captures, and every replay (with eager work on the
+    stream between replays) equals the eager result."""
+    import ctypes as C
+    import torch
+    hip = C.CDLL("libamdhip64.so")
+    m, n, k = 300, 1024, 2560
+    blocks = to_dev(orc.synth_q4k(55, n, k), dev)
+    a_bits, _ = _bf16_activations(56, m, k, orc)
+    a = a_bits.to(dev)
+    s = torch.cuda.Stream()
+    c = torch.zeros(m, n, dtype=torch.float32, device=dev)
+    assert hip.hipStreamBeginCapture(C.c_void_p(s.cuda_stream), 2) == 0  # hipStreamCaptureModeRelaxed
+    with pytest.raises(rt.RtError) as err:
+        rt.q4k_gemm(a, blocks, c, m, n, k, stream=s)
+    graph = C.c_void_p()
+    assert hip.hipStreamEndCapture(C.c_void_p(s.cuda_stream), C.byref(graph)) == 0
+    if graph.value:
+        hip.hipGraphDestroy(graph)
+    assert err.value.code == rt.RT_ESTATE
+    rt.q4k_gemm(a, blocks, c, m, n, k, stream=s)  # uncaptured: the workspace grows
+    s.synchronize()
+    eager = c.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        rt.q4k_gemm(a, blocks, c, m, n, k, stream=s)
+    for _ in range(3):
+        c.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(c, eager)
