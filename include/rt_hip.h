@@ -131,17 +131,35 @@ rt_status rt_q8_0_dequant_f32(const void *w, size_t n_elem, float *out, void *st
  * weights; device pointers, w and x 16-byte aligned. */
 rt_status rt_q6k_gemv(const void *w, const float *x, float *y, int64_t n, int64_t k, void *stream);
 rt_status rt_q8_0_gemv(const void *w, const float *x, float *y, int64_t n, int64_t k, void *stream);
-/* c[m][n] = a[m][k] . W[n][k] for a weight in any RT_LINEAR_* format but
- * F32 (Q6_K and Q8_0 planar): the prefill GEMM of a projection.  Replaces
- * MatBf16::matmul_by_t (autograd2.rs:757-852), which the reference runs on
- * the BF16-widened Q6_K / Q8_0 weights, and matmul_q4k_t for RT_LINEAR_Q4K
- * (as rt_q4k_gemm_f32).  Non-Q4_K rows are widened to f16 with a
- * power-of-two scale per row, A likewise, f32 accumulation on the matrix
- * cores; k % 256 == 0 (Q6_K, Q4_K) or k % 64 == 0; device pointers, a and w
- * 16-byte aligned.  Uses the per-(thread, device, stream) workspace of
- * rt_q4k_gemm_f32, about (m + n) * k * 2 bytes. */
+/* c[m][n] = a[m][k] . W[n][k] for a weight in any RT_LINEAR_* format (Q6_K
+ * and Q8_0 planar): the matmul of QLinear::forward (qlinear.rs:82-111).
+ * Replaces matmul_q4k_t_exact for RT_LINEAR_Q4K (as rt_q4k_gemm_f32),
+ * MatBf16::matmul_by_t (autograd2.rs:757-852) for BF16 and for the Q6_K /
+ * Q8_0 weights the reference widens to BF16, and Mat::matmul_bt
+ * (autograd2.rs:378-429) for RT_LINEAR_F32.  Non-Q4_K rows are widened to f16
+ * with a power-of-two scale per row, A likewise, f32 accumulation on the
+ * matrix cores (f32 weights: ~2e-4 rel-L2 from the f32 product); F32 and
+ * BF16 weights with m <= 8, or k not a multiple of 64, run a GEMV that streams
+ * them once per 8 rows in f32.  k % 256 == 0 (Q4_K, Q6_K), k % 64 == 0
+ * (Q8_0, and BF16 with m > 8), k % 8 == 0 (BF16, m <= 8), k % 4 == 0 (F32);
+ * device pointers, a and w 16-byte aligned.  Uses the
+ * per-(thread, device, stream) workspace of rt_q4k_gemm_f32, about
+ * (m + n) * k * 2 bytes (none for the f32 GEMV). */
 rt_status rt_linear_gemm_f32(int32_t fmt, const void *w, const float *a, float *c, int64_t m, int64_t n, int64_t k,
                              void *stream);
+/* QLinear::forward (qlinear.rs:82-111): out[m][n] = x[m][k] . W[n][k], then
+ * add_bias_rows (qlinear.rs:49-60), out[r][j] += bias[j] in f32, when bias
+ * (n floats, device) is not NULL.  Formats and constraints as
+ * rt_linear_gemm_f32. */
+rt_status rt_qlinear_forward(int32_t fmt, const void *w, const float *bias, const float *x, float *out, int64_t m,
+                             int64_t n, int64_t k, void *stream);
+/* Host drop-in for QLinear::forward (qlinear.rs:82-111) on the formats a
+ * QLinear holds: RT_LINEAR_Q4K (w_bytes = n*(k/256)*144), RT_LINEAR_BF16
+ * (n*k*2) or RT_LINEAR_F32 (n*k*4).  The weight is uploaded once and cached
+ * by (host pointer, bytes) like rt_gemv_q4k_t's (rt_weight_cache_clear drops
+ * it); x [m, k], bias [n] (or NULL) and out [m, n] are host f32; synchronous. */
+rt_status rt_qlinear_forward_host(int32_t fmt, const void *w, size_t w_bytes, const float *bias, const float *x,
+                                  float *out, int64_t m, int64_t n, int64_t k);
 
 /* gemv_q4k_t_batch (metal_decode.rs:459-521): c[m][n] = a[m][k] . W[n][k]
  * for m = 1..8 rows (the speculative verify batch), reading the weights once
@@ -262,6 +280,14 @@ rt_status rt_decode_set_prefill_chunk(rt_decode *d, int32_t rows);
 rt_status rt_decode_synchronize(rt_decode *d);
 /* Use the captured hipGraph (default) or launch the kernels one by one. */
 rt_status rt_decode_set_graph(rt_decode *d, int32_t enabled);
+/* print_metal_memory (metal_decode.rs:1285-1354): device bytes of a context by
+ * what they hold.  weights counts uploads and device-pointer bindings alike
+ * (projections, norms, embedding / tied lm_head); prefill is the chunk
+ * scratch, 0 until the first rt_decode_prefill. */
+typedef struct {
+  uint64_t weights, kv_cache, activation, batch, prefill, total;
+} rt_decode_memory_info;
+rt_status rt_decode_memory(const rt_decode *d, rt_decode_memory_info *out);
 /* Device buffers of the context, for inspection. */
 rt_status rt_decode_logits(rt_decode *d, float **logits_dev);
 rt_status rt_decode_kv(rt_decode *d, int32_t layer, float **k_dev, float **v_dev);

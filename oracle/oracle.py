@@ -344,6 +344,19 @@ def proj_matmul(fmt: int, a: np.ndarray, w: np.ndarray, n: int, k: int, threads:
     return c
 
 
+def qlinear_forward(fmt: int, a: np.ndarray, w: np.ndarray, n: int, k: int, bias=None, threads: int = 0) -> np.ndarray:
+    """orc_qlinear_forward: QLinear::forward, C = A W^T (+ bias) for a weight of
+    format fmt (1 Q4_K, 2 BF16, 3 F32 [n, k], 4 Q6_K, 5 Q8_0 GGUF blocks)."""
+    a = np.ascontiguousarray(a, np.float32)
+    m = a.shape[0]
+    c = np.empty((m, n), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    lib().orc_qlinear_forward(C.c_int(fmt), C.c_void_p(_ptr(a)), C.c_size_t(m),
+                              C.c_void_p(_ptr(np.ascontiguousarray(w))), C.c_void_p(None if b is None else _ptr(b)),
+                              C.c_size_t(n), C.c_size_t(k), C.c_void_p(_ptr(c)), C.c_int(threads))
+    return c
+
+
 def gqa_attention_prefill(q, k_cache, v_cache, p0, T, lo_fixed, window, n_q_heads, n_kv_heads, d_head, scale):
     """orc_gqa_attention_prefill: rows p0 .. p0+T-1, keys [lo(r), r]."""
     q = np.ascontiguousarray(q, np.float32)

@@ -605,6 +605,18 @@ void orc_proj_matmul(int fmt, const float *a, size_t m, const uint8_t *w, size_t
     mm_ctx ctx = {a, m, w, n, k, c, NULL, fmt};
     run_bands(n, hw_threads, 1, mm_band, &ctx);
 }
+/* QLinear::forward (qlinear.rs:82-111): the format's matmul (Q4_K:
+ * matmul_q4k_t_exact, BF16: matmul_by_t, F32: matmul_bt -- each a dot per
+ * output of the widened row, as orc_proj_matmul), then add_bias_rows
+ * (qlinear.rs:49-60): out[r][c] += bias[c], skipped when bias is NULL. */
+void orc_qlinear_forward(int fmt, const float *a, size_t m, const uint8_t *w, const float *bias, size_t n, size_t k,
+                         float *c, int hw_threads)
+{
+    orc_proj_matmul(fmt, a, m, w, n, k, c, hw_threads);
+    if (!bias) return;
+    for (size_t r = 0; r < m; r++)
+        for (size_t j = 0; j < n; j++) c[r * n + j] += bias[j];
+}
 void orc_q4k_matmul_f64(const float *a, size_t m, const uint8_t *blocks, size_t n, size_t k, double *c, int hw_threads)
 {
     mm_ctx ctx = {a, m, blocks, n, k, NULL, c, 1};
@@ -707,6 +719,8 @@ static void proj_row(int fmt, const uint8_t *w, size_t cols, size_t j, float *ro
     if (fmt == 2) {
         const uint16_t *r = (const uint16_t *)w + j * cols;
         for (size_t i = 0; i < cols; i++) row[i] = orc_bf16_to_f32(r[i]);
+    } else if (fmt == 3) {  /* f32 weights: Mat::matmul_bt, scalar branch (autograd2.rs:410-429) */
+        memcpy(row, (const float *)w + j * cols, cols * sizeof(float));
     } else if (fmt == 4) orc_q6k_dequant(w + j * (cols / 256) * 210, cols, row);
     else if (fmt == 5) orc_q8_0_dequant(w + j * (cols / 32) * 34, cols, row);
     else orc_q4k_dequant_row(w, cols, j, row);

@@ -95,6 +95,11 @@ void orc_proj_gemv(int fmt, const uint8_t *w, size_t rows, size_t cols, const fl
  * a sequential f32 dot per output, as orc_q4k_matmul. */
 void orc_proj_matmul(int fmt, const float *a, size_t m, const uint8_t *w, size_t n, size_t k, float *c,
                      int hw_threads);
+/* QLinear::forward (qlinear.rs:82-111): orc_proj_matmul of fmt (3 = F32
+ * weights, Mat::matmul_bt) plus add_bias_rows (qlinear.rs:49-60); bias may be
+ * NULL (no bias). */
+void orc_qlinear_forward(int fmt, const float *a, size_t m, const uint8_t *w, const float *bias, size_t n, size_t k,
+                         float *c, int hw_threads);
 
 /* One CPU decode step (transformer4.rs:2358-2385 with forward_cached 1900-1964).
  * Appends K/V at row `pos` of every layer's cache and writes vocab logits.

@@ -18,6 +18,7 @@ from __future__ import annotations
 import ctypes as C
 import pathlib
 import subprocess
+import sys
 
 PKG_DIR = pathlib.Path(__file__).resolve().parent
 LIB_PATH = PKG_DIR / "librt_hip.so"
@@ -55,6 +56,9 @@ _SIGNATURES = {
     "rt_weight_cache_clear": (_i32, []),
     "rt_q4k_gemv_batch": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "rt_q4k_gemv_batch_noalloc": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "rt_qlinear_forward": (_i32, [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "rt_decode_memory": (_i32, [_vp, _vp]),
+    "rt_qlinear_forward_host": (_i32, [_i32, _vp, _sz, _vp, _vp, _vp, _i64, _i64, _i64]),
     "rt_noalloc_scratch_bytes": (_sz, []),
     "rt_q6k_repack": (_i32, [_vp, _sz, _vp]),
     "rt_q8_0_repack": (_i32, [_vp, _sz, _vp]),
@@ -209,6 +213,29 @@ def linear_gemm_f32(fmt: int, w, a, c, m: int, n: int, k: int, stream=None) -> N
     check(lib().rt_linear_gemm_f32(fmt, _p(w), _p(a), _p(c), m, n, k, _stream(stream)))
 
 
+def qlinear_forward(fmt: int, w, x, out, m: int, n: int, k: int, bias=None, stream=None) -> None:
+    """QLinear::forward: out[m][n] = x[m][k] . W[n][k] (+ bias[n]) for a weight of
+    format fmt (LINEAR_Q4K, LINEAR_BF16, LINEAR_F32, LINEAR_Q6K or LINEAR_Q8_0)."""
+    check(lib().rt_qlinear_forward(fmt, _p(w), None if bias is None else _p(bias), _p(x), _p(out), m, n, k,
+                                   _stream(stream)))
+
+
+def qlinear_forward_host(fmt: int, w, x, bias=None):
+    """QLinear::forward on host numpy arrays: w (Q4_K blocks, BF16 bits or f32
+    [n, k]), x [m, k] f32, bias [n] or None -> [m, n] f32 (weights cached)."""
+    import numpy as np
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w)
+    m, k = x.shape
+    n = {LINEAR_Q4K: w.size // (k // 256 * 144) if k % 256 == 0 else 0, LINEAR_BF16: w.size // k,
+         LINEAR_F32: w.size // k}.get(fmt, 0)
+    out = np.empty((m, max(n, 1)), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    check(lib().rt_qlinear_forward_host(fmt, w.ctypes.data, w.nbytes, None if b is None else b.ctypes.data,
+                                        x.ctypes.data, out.ctypes.data, m, n, k))
+    return out
+
+
 def q6k_dequant_f32(w, out, n_blocks: int, stream=None) -> None:
     check(lib().rt_q6k_dequant_f32(_p(w), n_blocks, _p(out), _stream(stream)))
 
@@ -324,6 +351,10 @@ def _addr(x) -> int:
     return x.ctypes.data
 
 
+class DecodeMemory(C.Structure):
+    _fields_ = [(k, C.c_uint64) for k in ("weights", "kv_cache", "activation", "batch", "prefill", "total")]
+
+
 class HipDecodeContext:
     """One Gemma-3 decode context on the current HIP device.
 
@@ -429,6 +460,19 @@ class HipDecodeContext:
 
     def set_graph(self, enabled: bool) -> None:
         check(lib().rt_decode_set_graph(self._h, int(enabled)))
+
+    def memory(self) -> dict:
+        """Device bytes by what they hold (print_metal_memory, metal_decode.rs:1285-1354)."""
+        m = DecodeMemory()
+        check(lib().rt_decode_memory(self._h, C.byref(m)))
+        return {k: int(getattr(m, k)) for k, _ in DecodeMemory._fields_}
+
+    def print_memory(self) -> None:
+        """The reference's one-line report, in MB."""
+        m = self.memory()
+        print("[ HIP ] GPU buffer memory: " + "  ".join(
+            f"{k}={m[k] / 1048576.0:.1f} MB" for k in ("weights", "kv_cache", "activation", "batch", "prefill", "total")),
+            file=sys.stderr)
 
     def logits_ptr(self) -> int:
         p = C.c_void_p()

@@ -183,27 +183,62 @@ rt_status rt_q4k_gemm_f32(const float *a, const void *w, float *c, int64_t m, in
   return q4k_gemm_entry("rt_q4k_gemm_f32", a, false, w, c, m, n, k, stream);
 }
 
-// MatBf16::matmul_by_t (autograd2.rs:757-852) on the BF16, Q6_K or Q8_0
-// weight of a projection; Q4_K goes to the Q4_K GEMM.
-rt_status rt_linear_gemm_f32(int32_t fmt, const void *w, const float *a, float *c, int64_t m, int64_t n, int64_t k,
-                             void *stream) {
-  static const char *who = "rt_linear_gemm_f32";
-  if (fmt == RT_LINEAR_Q4K) return q4k_gemm_entry(who, a, false, w, c, m, n, k, stream);
-  if (fmt != RT_LINEAR_BF16 && fmt != RT_LINEAR_Q6K && fmt != RT_LINEAR_Q8_0)
+// The matmul of QLinear::forward (qlinear.rs:82-111) for a weight of any
+// format: Q4_K -> matmul_q4k_t_exact (the Q4_K GEMM); BF16, and Q6_K / Q8_0
+// which the reference widens to BF16 -> MatBf16::matmul_by_t
+// (autograd2.rs:757-852); F32 -> Mat::matmul_bt (autograd2.rs:378-429).  With
+// a bias, add_bias_rows (qlinear.rs:49-60) follows.
+static rt_status linear_forward(const char *who, int32_t fmt, const void *w, const float *bias, const float *a,
+                                float *c, int64_t m, int64_t n, int64_t k, void *stream) {
+  hipStream_t s = (hipStream_t)stream;
+  if (fmt != RT_LINEAR_Q4K && fmt != RT_LINEAR_BF16 && fmt != RT_LINEAR_Q6K && fmt != RT_LINEAR_Q8_0 &&
+      fmt != RT_LINEAR_F32)
     return set_error(RT_EINVAL, "%s: unsupported format %d", who, fmt);
   if (m <= 0 || n <= 0 || k <= 0)
     return set_error(RT_EINVAL, "%s: m=%lld n=%lld k=%lld must be positive", who, (long long)m, (long long)n,
                      (long long)k);
-  const int align = fmt == RT_LINEAR_Q6K ? 256 : 64;  // the f16 GEMM moves K in stages of 64
+  // K granularity: Q4_K / Q6_K super-blocks, the f16 GEMM's 64-wide stages,
+  // or (f32 weights) 16-byte row loads
+  const bool few = m <= 8;  // f32 / bf16 weights: the row-group GEMV
+  const int align = (fmt == RT_LINEAR_Q4K || fmt == RT_LINEAR_Q6K) ? 256
+                    : fmt == RT_LINEAR_F32                         ? 4
+                    : fmt == RT_LINEAR_BF16 && (few || k % 64)     ? 8
+                                                                   : 64;
   if (k % align != 0) return set_error(RT_EINVAL, "%s: k=%lld must be a multiple of %d", who, (long long)k, align);
   if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX) return set_error(RT_EINVAL, "%s: m, n or k exceeds int32", who);
   if (!a || !w || !c) return set_error(RT_EINVAL, "%s: null pointer", who);
   if (!aligned16(a) || !aligned16(w)) return set_error(RT_EINVAL, "%s: a and w must be 16-byte aligned", who);
   if ((reinterpret_cast<uintptr_t>(c) & 3u) != 0) return set_error(RT_EINVAL, "%s: c must be 4-byte aligned", who);
+  if (bias && (reinterpret_cast<uintptr_t>(bias) & 3u) != 0)
+    return set_error(RT_EINVAL, "%s: bias must be 4-byte aligned", who);
+  if (fmt == RT_LINEAR_Q4K) {
+    rt_status st = q4k_gemm_entry(who, a, false, w, c, m, n, k, stream);
+    if (st != RT_OK || !bias) return st;
+    return hip_error(launch_add_bias_rows(c, bias, (int)m, (int)n, s), who);
+  }
+  // f32 / bf16 weights with a few rows, or a K the 64-wide GEMM stages do not
+  // divide: the weights stream once per 8 rows, the bias add fused
+  if (fmt == RT_LINEAR_F32 && (few || k % 64 != 0))
+    return hip_error(launch_f32_gemv_rows(static_cast<const float *>(w), a, bias, c, (int)m, (int)n, (int)k, s), who);
+  if (fmt == RT_LINEAR_BF16 && (few || k % 64 != 0))
+    return hip_error(launch_bf16_gemv_rows(static_cast<const uint16_t *>(w), a, bias, c, (int)m, (int)n, (int)k, s),
+                     who);
   void *ws = nullptr;
-  rt_status st = gemm_workspace(proj_gemm_workspace_bytes((int)m, (int)n, (int)k), (hipStream_t)stream, &ws);
+  rt_status st = gemm_workspace(proj_gemm_workspace_bytes((int)m, (int)n, (int)k), s, &ws);
   if (st != RT_OK) return st;
-  return hip_error(launch_proj_gemm(a, fmt, w, c, (int)m, (int)n, (int)k, ws, (hipStream_t)stream), who);
+  hipError_t e = launch_proj_gemm(a, fmt, w, c, (int)m, (int)n, (int)k, ws, s);
+  if (e == hipSuccess && bias) e = launch_add_bias_rows(c, bias, (int)m, (int)n, s);
+  return hip_error(e, who);
+}
+
+rt_status rt_linear_gemm_f32(int32_t fmt, const void *w, const float *a, float *c, int64_t m, int64_t n, int64_t k,
+                             void *stream) {
+  return linear_forward("rt_linear_gemm_f32", fmt, w, nullptr, a, c, m, n, k, stream);
+}
+
+rt_status rt_qlinear_forward(int32_t fmt, const void *w, const float *bias, const float *x, float *out, int64_t m,
+                             int64_t n, int64_t k, void *stream) {
+  return linear_forward("rt_qlinear_forward", fmt, w, bias, x, out, m, n, k, stream);
 }
 
 // gemv_q4k_t_batch (metal_decode.rs:459-521): c[m][n] = a[m][k] . W[n][k]
@@ -460,6 +495,46 @@ rt_status rt_matmul_q4k_t(const float *a, size_t m, size_t k, const uint8_t *blo
   if (e != hipSuccess) return hip_error(e, "rt_matmul_q4k_t");
   e = hipMemcpy(out, cd, m * rows * sizeof(float), hipMemcpyDeviceToHost);
   return hip_error(e, "rt_matmul_q4k_t");
+}
+
+// Host drop-in for QLinear::forward (qlinear.rs:82-111) on the formats a
+// QLinear holds (Q4_K, BF16, F32): the weight is uploaded once and cached by
+// (host pointer, bytes) like rt_gemv_q4k_t's; x, the bias and the output are
+// staged per call; synchronous.
+rt_status rt_qlinear_forward_host(int32_t fmt, const void *w, size_t w_bytes, const float *bias, const float *x,
+                                  float *out, int64_t m, int64_t n, int64_t k) {
+  static const char *who = "rt_qlinear_forward_host";
+  if (!w || !x || !out) return set_error(RT_EINVAL, "%s: null pointer", who);
+  if (fmt != RT_LINEAR_Q4K && fmt != RT_LINEAR_BF16 && fmt != RT_LINEAR_F32)
+    return set_error(RT_EINVAL, "%s: format %d (a QLinear holds Q4_K, BF16 or F32)", who, fmt);
+  if (m <= 0 || n <= 0 || k <= 0 || m > INT32_MAX || n > INT32_MAX || k > INT32_MAX)
+    return set_error(RT_EINVAL, "%s: m=%lld n=%lld k=%lld", who, (long long)m, (long long)n, (long long)k);
+  size_t need = 0;
+  switch (fmt) {
+    case RT_LINEAR_Q4K: need = k % 256 ? 0 : (size_t)n * (size_t)(k / 256) * 144; break;
+    case RT_LINEAR_BF16: need = (size_t)n * (size_t)k * 2; break;
+    case RT_LINEAR_F32: need = (size_t)n * (size_t)k * 4; break;
+    default: return set_error(RT_EINVAL, "%s: format %d (a QLinear holds Q4_K, BF16 or F32)", who, fmt);
+  }
+  if (need == 0 || w_bytes != need)
+    return set_error(RT_EINVAL, "%s: weight of %zu bytes, format %d [%lld, %lld] needs %zu", who, w_bytes, fmt,
+                     (long long)n, (long long)k, need);
+  void *wdev = nullptr, *buf = nullptr;
+  rt_status st = cached_upload(w, w_bytes, &wdev);
+  if (st != RT_OK) return st;
+  auto r256 = [](size_t b) { return (b + 255) & ~size_t(255); };
+  const size_t xb = r256((size_t)m * k * 4), ob = r256((size_t)m * n * 4), bb = bias ? r256((size_t)n * 4) : 0;
+  st = stage(xb + ob + bb, &buf);
+  if (st != RT_OK) return st;
+  float *xd = static_cast<float *>(buf);
+  float *od = reinterpret_cast<float *>(static_cast<char *>(buf) + xb);
+  float *bd = bias ? reinterpret_cast<float *>(static_cast<char *>(buf) + xb + ob) : nullptr;
+  hipError_t e = hipMemcpy(xd, x, (size_t)m * k * 4, hipMemcpyHostToDevice);
+  if (e == hipSuccess && bias) e = hipMemcpy(bd, bias, (size_t)n * 4, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return hip_error(e, who);
+  st = rt_qlinear_forward(fmt, wdev, bd, xd, od, m, n, k, nullptr);
+  if (st != RT_OK) return st;
+  return hip_error(hipMemcpy(out, od, (size_t)m * n * 4, hipMemcpyDeviceToHost), who);
 }
 
 rt_status rt_weight_cache_clear(void) {

@@ -25,7 +25,15 @@ struct rt_decode {
   DecodeShape shape{};
   int device = 0;
   hipStream_t stream = nullptr;
-  std::vector<void *> owned;             // every hipMalloc of this context
+  // every hipMalloc of this context, with its size and what it holds
+  enum Mem { kWeights, kKv, kActivation, kBatch, kPrefill, kMemKinds };
+  struct Alloc {
+    void *p;
+    size_t bytes;
+    int kind;
+  };
+  std::vector<Alloc> owned;
+  size_t bound_weight_bytes[65] = {};    // weights bound by device pointer: per layer, [64] embedding + final norm
   std::vector<LayerArgs> layers;
   std::vector<char> layer_set;
   std::vector<void *> owned_layer[64];  // per-layer uploads (replaced on re-set)
@@ -54,11 +62,11 @@ struct rt_decode {
 
 namespace {
 
-rt_status dalloc(rt_decode *d, size_t bytes, void **out) {
+rt_status dalloc(rt_decode *d, size_t bytes, void **out, int kind = rt_decode::kActivation) {
   void *p = nullptr;
   hipError_t e = hipMalloc(&p, bytes);
   if (e != hipSuccess) return hip_error(e, "rt_decode hipMalloc");
-  d->owned.push_back(p);
+  d->owned.push_back({p, bytes, kind});
   *out = p;
   return RT_OK;
 }
@@ -66,9 +74,10 @@ rt_status dalloc(rt_decode *d, size_t bytes, void **out) {
 void dfree(rt_decode *d, void *p) {
   if (!p) return;
   for (auto &q : d->owned)
-    if (q == p) {
-      (void)hipFree(q);
-      q = nullptr;
+    if (q.p == p) {
+      (void)hipFree(q.p);
+      q.p = nullptr;
+      q.bytes = 0;
     }
 }
 
@@ -152,9 +161,10 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
     TRY(dalloc(d, d->params_bytes, &p)); d->params_dev = (int *)p;
     TRYH(hipMemset(d->params_dev, 0, d->params_bytes), "hipMemset");
     DecodeArgs &a = d->args;
+    int kind = rt_decode::kActivation;  // what the next fbuf holds
     auto fbuf = [&](size_t n, float **dst) -> rt_status {
       void *q = nullptr;
-      rt_status r = dalloc(d, std::max<size_t>(n, 4) * sizeof(float), &q);
+      rt_status r = dalloc(d, std::max<size_t>(n, 4) * sizeof(float), &q, kind);
       if (r == RT_OK) {
         *dst = (float *)q;
         hipError_t z = hipMemset(q, 0, std::max<size_t>(n, 4) * sizeof(float));
@@ -168,6 +178,7 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
     TRY(fbuf((size_t)c.vocab, &a.logits));
     TRY(fbuf((size_t)c.n_q_heads * nch, &a.part_m)); TRY(fbuf((size_t)c.n_q_heads * nch, &a.part_l));
     TRY(fbuf((size_t)c.n_q_heads * nch * D, &a.part_o));
+    kind = rt_decode::kBatch;
     TRY(fbuf((size_t)kMaxBatch * H, &d->xn_batch));
     TRY(fbuf((size_t)kMaxBatch * c.vocab, &d->logits_batch));
     {
@@ -177,7 +188,7 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
       TRY(fbuf(R * H, &vb.dn)); TRY(fbuf(R * QD, &vb.q)); TRY(fbuf(R * QD, &vb.attn)); TRY(fbuf(R * KVD, &vb.k));
       TRY(fbuf(R * KVD, &vb.v)); TRY(fbuf(R * F, &vb.g)); TRY(fbuf(R * F, &vb.u));
       void *q = nullptr;
-      TRY(dalloc(d, rows_mb_stage_bytes(s), &q)); vb.mb_stage = q;
+      TRY(dalloc(d, rows_mb_stage_bytes(s), &q, kind)); vb.mb_stage = q;
       TRY(fbuf(rows_mb_part_bytes(s) / 4, &vb.mb_part));
       TRY(fbuf(attn_part_floats(s, kMaxBatch, false), &vb.attn_ml));
       TRY(fbuf(attn_part_floats(s, kMaxBatch, true), &vb.attn_o));
@@ -208,6 +219,7 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
     for (int l = 0; l < c.n_layers; ++l) {
       LayerArgs &L = d->layers[l];
       std::memset(&L, 0, sizeof L);
+      kind = rt_decode::kKv;
       TRY(fbuf((size_t)c.max_seq * KVD, &L.kc));
       TRY(fbuf((size_t)c.max_seq * KVD, &L.vc));
       const bool g = is_global(c, l);
@@ -230,8 +242,8 @@ rt_status rt_decode_destroy(rt_decode *d) {
   if (!d) return RT_OK;
   if (d->stream) (void)hipStreamSynchronize(d->stream);
   drop_graph(d);
-  for (void *p : d->owned)
-    if (p) (void)hipFree(p);
+  for (auto &a : d->owned)
+    if (a.p) (void)hipFree(a.p);
   if (d->params_host) (void)hipHostFree(d->params_host);
   if (d->pf_tokens_host) (void)hipHostFree(d->pf_tokens_host);
   if (d->pf_cs_host) (void)hipHostFree(d->pf_cs_host);
@@ -251,7 +263,7 @@ static rt_status bind_buf(rt_decode *d, const void *src, size_t bytes, int32_t d
     return RT_OK;
   }
   void *p = nullptr;
-  rt_status st = dalloc(d, bytes, &p);
+  rt_status st = dalloc(d, bytes, &p, rt_decode::kWeights);
   if (st != RT_OK) return st;
   hipError_t e = hipMemcpy(p, src, bytes, hipMemcpyHostToDevice);
   if (e != hipSuccess) {
@@ -294,6 +306,7 @@ rt_status rt_decode_set_layer_formats(rt_decode *d, int32_t layer, const rt_gemm
     for (void *q : d->owned_layer[layer]) dfree(d, q);
     d->owned_layer[layer].clear();
     d->layer_set[layer] = 0;
+    d->bound_weight_bytes[layer] = 0;
     drop_graph(d);
     return st;
   };
@@ -354,6 +367,13 @@ rt_status rt_decode_set_layer_formats(rt_decode *d, int32_t layer, const rt_gemm
   for (int i = 0; i < 7; ++i) L.fmt[i] = formats[i];
   d->layers[layer] = L;
   d->owned_layer[layer] = std::move(own);
+  d->bound_weight_bytes[layer] = 0;
+  if (device_ptrs) {  // borrowed: counted in rt_decode_memory's weights all the same
+    const size_t sh[7][2] = {{QD, H}, {KVD, H}, {KVD, H}, {H, QD}, {F, H}, {F, H}, {H, F}};
+    size_t b = (4 * H + 2 * D) * 4;
+    for (int i = 0; i < 7; ++i) b += proj_bytes(formats[i], sh[i][0], sh[i][1]);
+    d->bound_weight_bytes[layer] = b;
+  }
   d->all_q4k = true;
   for (const LayerArgs &X : d->layers)
     for (int i = 0; i < 7; ++i) d->all_q4k = d->all_q4k && X.fmt[i] == RT_LINEAR_Q4K;
@@ -378,10 +398,12 @@ rt_status rt_decode_set_embed(rt_decode *d, const uint16_t *embed, const float *
   if (st != RT_OK) {
     for (void *q : own) dfree(d, q);
     d->embed_set = false;
+    d->bound_weight_bytes[64] = 0;
     return st;
   }
   d->args.embed = (const uint16_t *)pe;
   d->args.g_final = (const float *)pf;
+  d->bound_weight_bytes[64] = device_ptrs ? (size_t)d->cfg.vocab * d->cfg.hidden * 2 + (size_t)d->cfg.hidden * 4 : 0;
   if (!device_ptrs) {
     d->embed_owned = (void *)pe;
     d->final_owned = (void *)pf;
@@ -576,7 +598,7 @@ static rt_status prefill_reserve(rt_decode *d, int cap) {
   const size_t H = c.hidden, F = c.ffn, D = c.head_dim, QD = (size_t)c.n_q_heads * D, KVD = (size_t)c.n_kv_heads * D;
   const size_t rows = (size_t)cap;
   auto get = [&](size_t bytes, void **dst) -> rt_status {
-    rt_status st = dalloc(d, std::max<size_t>(bytes, 256), dst);
+    rt_status st = dalloc(d, std::max<size_t>(bytes, 256), dst, rt_decode::kPrefill);
     if (st == RT_OK) d->pf_owned.push_back(*dst);
     return st;
   };
@@ -723,6 +745,25 @@ rt_status rt_decode_set_graph(rt_decode *d, int32_t enabled) {
   (void)hipStreamSynchronize(d->stream);
   d->graph_enabled = enabled != 0;
   drop_graph(d);
+  return RT_OK;
+}
+
+// print_metal_memory (metal_decode.rs:1285-1354): the device memory of the
+// context by what it holds.  Weights bound by device pointer count too, as
+// the reference's uploads do; the prefill scratch appears once a prefill has
+// sized it.
+rt_status rt_decode_memory(const rt_decode *d, rt_decode_memory_info *out) {
+  if (!d || !out) return set_error(RT_EINVAL, "rt_decode_memory: null pointer");
+  uint64_t by[rt_decode::kMemKinds] = {};
+  for (const auto &a : d->owned)
+    if (a.p) by[a.kind] += a.bytes;
+  for (size_t b : d->bound_weight_bytes) by[rt_decode::kWeights] += b;
+  out->weights = by[rt_decode::kWeights];
+  out->kv_cache = by[rt_decode::kKv];
+  out->activation = by[rt_decode::kActivation];
+  out->batch = by[rt_decode::kBatch];
+  out->prefill = by[rt_decode::kPrefill];
+  out->total = out->weights + out->kv_cache + out->activation + out->batch + out->prefill;
   return RT_OK;
 }
 

@@ -1,5 +1,6 @@
-// proj_gemm.hip -- the GEMM of a projection that is not Q4_K (Q6_K, Q8_0 or
-// BF16 kept in their device layouts), for prefill rows.
+// proj_gemm.hip -- the GEMM of a projection that is not Q4_K (Q6_K, Q8_0,
+// BF16 kept in their device layouts, or f32), for prefill rows, and the f32
+// weight GEMV of a few rows.
 //
 // The reference runs these weights as BF16 after widening them at load
 // (transformer4.rs:1233-1242) and multiplies on the CPU in f32
@@ -28,6 +29,8 @@ RT_DEV float proj_value(const uint8_t *__restrict__ W, int N, int K, int n, int 
 #pragma clang fp contract(off)
   if constexpr (FMT == RT_LINEAR_BF16) {
     return bf16_lo((uint32_t) reinterpret_cast<const uint16_t *>(W)[(size_t)n * K + e]);
+  } else if constexpr (FMT == RT_LINEAR_F32) {
+    return reinterpret_cast<const float *>(W)[(size_t)n * K + e];
   } else if constexpr (FMT == RT_LINEAR_Q8_0) {
     return q8_0_value(W, (size_t)N * K, (size_t)n * K + e);
   } else {  // RT_LINEAR_Q6K, planar
@@ -202,7 +205,150 @@ __global__ __launch_bounds__(256) void k_gemm_f16_t256(const _Float16 *__restric
                   n0 + 128 * wn, ea, ec);
 }
 
+// ---------------------------------------------------------------------------
+// f32 weights with a few activation rows (QLinear's f32 branch, x.matmul_bt(W),
+// qlinear.rs:102-106, for M <= 8 per launch row group): each wave owns four
+// weight rows and streams them once for the MR activation rows of its group
+// (blockIdx.y), 16-byte loads along K; per output a lane-strided f32 sum, then
+// the wave's DPP sum.  With a bias, out = sum + bias[n], the one f32 add of
+// add_bias_rows (qlinear.rs:49-60).
+// ---------------------------------------------------------------------------
+template <int MR>
+__global__ __launch_bounds__(256) void k_f32_gemv_rows(const float *__restrict__ W, const float *__restrict__ a,
+                                                       const float *__restrict__ bias, float *__restrict__ c, int M,
+                                                       int N, int K) {
+  constexpr int RW = 4;
+  const int lane = (int)threadIdx.x & 63;
+  const int n0 = (int)((blockIdx.x * 256u + threadIdx.x) >> 6) * RW;
+  const int m0 = (int)blockIdx.y * 8;
+  if (n0 >= N) return;  // whole waves
+  const int K4 = K / 4;
+  const float4 *w4 = reinterpret_cast<const float4 *>(W);
+  const float4 *a4 = reinterpret_cast<const float4 *>(a) + (size_t)m0 * K4;
+  float acc[RW][MR];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int i = 0; i < MR; ++i) acc[r][i] = 0.f;
+#pragma unroll 2
+  for (int k4 = lane; k4 < K4; k4 += 64) {
+    float4 w[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) w[r] = w4[(size_t)min(n0 + r, N - 1) * K4 + k4];
+#pragma unroll
+    for (int i = 0; i < MR; ++i) {
+      const float4 x = a4[(size_t)min(i, M - 1 - m0) * K4 + k4];  // rows past M re-read row M-1, unstored
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        acc[r][i] = fmaf(w[r].x, x.x, acc[r][i]);
+        acc[r][i] = fmaf(w[r].y, x.y, acc[r][i]);
+        acc[r][i] = fmaf(w[r].z, x.z, acc[r][i]);
+        acc[r][i] = fmaf(w[r].w, x.w, acc[r][i]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int i = 0; i < MR; ++i) {
+      const float v = wave_sum(acc[r][i]);
+      if (lane == 0 && n0 + r < N && m0 + i < M) c[(size_t)(m0 + i) * N + n0 + r] = bias ? v + bias[n0 + r] : v;
+    }
+}
+
+// The same for BF16 weights (MatBf16::matmul_by_t, autograd2.rs:757-852, of a
+// few rows): 16-byte loads of eight weights, each widened exactly.
+template <int MR>
+__global__ __launch_bounds__(256) void k_bf16_gemv_rows(const uint16_t *__restrict__ W, const float *__restrict__ a,
+                                                        const float *__restrict__ bias, float *__restrict__ c, int M,
+                                                        int N, int K) {
+  constexpr int RW = 4;
+  const int lane = (int)threadIdx.x & 63;
+  const int n0 = (int)((blockIdx.x * 256u + threadIdx.x) >> 6) * RW;
+  const int m0 = (int)blockIdx.y * 8;
+  if (n0 >= N) return;
+  const int K8 = K / 8;
+  const uint4 *w8 = reinterpret_cast<const uint4 *>(W);
+  const float4 *a4 = reinterpret_cast<const float4 *>(a) + (size_t)m0 * (K / 4);
+  float acc[RW][MR];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int i = 0; i < MR; ++i) acc[r][i] = 0.f;
+#pragma unroll 2
+  for (int k8 = lane; k8 < K8; k8 += 64) {
+    float wf[RW][8];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const uint4 q = w8[(size_t)min(n0 + r, N - 1) * K8 + k8];
+      const uint32_t u[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wf[r][2 * j] = bf16_lo(u[j]), wf[r][2 * j + 1] = bf16_hi(u[j]);
+    }
+#pragma unroll
+    for (int i = 0; i < MR; ++i) {
+      const float4 *xr = a4 + (size_t)min(i, M - 1 - m0) * (K / 4) + 2 * k8;
+      const float4 x0 = xr[0], x1 = xr[1];
+      const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+      for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[r][i] = fmaf(wf[r][j], xv[j], acc[r][i]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int i = 0; i < MR; ++i) {
+      const float v = wave_sum(acc[r][i]);
+      if (lane == 0 && n0 + r < N && m0 + i < M) c[(size_t)(m0 + i) * N + n0 + r] = bias ? v + bias[n0 + r] : v;
+    }
+}
+
+// add_bias_rows (qlinear.rs:49-60): c[r][j] += bias[j].
+__global__ __launch_bounds__(256) void k_add_bias_rows(float *__restrict__ c, const float *__restrict__ bias,
+                                                       size_t total, int N) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256)
+    c[i] += bias[i % (size_t)N];
+}
+
 }  // namespace
+
+hipError_t launch_f32_gemv_rows(const float *w, const float *a, const float *bias, float *c, int M, int N, int K,
+                                hipStream_t s) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 4 != 0) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + 7) / 8));
+  const int mr = std::min(M, 8);  // rows of the last group are bounded by M inside
+  switch (mr) {
+    case 1: hipLaunchKernelGGL(k_f32_gemv_rows<1>, grid, dim3(256), 0, s, w, a, bias, c, M, N, K); break;
+    case 2: hipLaunchKernelGGL(k_f32_gemv_rows<2>, grid, dim3(256), 0, s, w, a, bias, c, M, N, K); break;
+    case 3: hipLaunchKernelGGL(k_f32_gemv_rows<3>, grid, dim3(256), 0, s, w, a, bias, c, M, N, K); break;
+    case 4: hipLaunchKernelGGL(k_f32_gemv_rows<4>, grid, dim3(256), 0, s, w, a, bias, c, M, N, K); break;
+    default: hipLaunchKernelGGL(k_f32_gemv_rows<8>, grid, dim3(256), 0, s, w, a, bias, c, M, N, K); break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_bf16_gemv_rows(const uint16_t *w, const float *a, const float *bias, float *c, int M, int N, int K,
+                                 hipStream_t s) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 8 != 0) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + 7) / 8));
+  switch (std::min(M, 8)) {
+    case 1: hipLaunchKernelGGL(k_bf16_gemv_rows<1>, grid, dim3(256), 0, s, w, a, bias, c, M, N, K); break;
+    case 2: hipLaunchKernelGGL(k_bf16_gemv_rows<2>, grid, dim3(256), 0, s, w, a, bias, c, M, N, K); break;
+    case 3: hipLaunchKernelGGL(k_bf16_gemv_rows<3>, grid, dim3(256), 0, s, w, a, bias, c, M, N, K); break;
+    case 4: hipLaunchKernelGGL(k_bf16_gemv_rows<4>, grid, dim3(256), 0, s, w, a, bias, c, M, N, K); break;
+    default: hipLaunchKernelGGL(k_bf16_gemv_rows<8>, grid, dim3(256), 0, s, w, a, bias, c, M, N, K); break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_add_bias_rows(float *c, const float *bias, int M, int N, hipStream_t s) {
+  const size_t total = (size_t)M * N;
+  const unsigned grid = (unsigned)std::min<size_t>((total + 255) / 256, 4096);
+  hipLaunchKernelGGL(k_add_bias_rows, dim3(grid), dim3(256), 0, s, c, bias, total, N);
+  return hipGetLastError();
+}
 
 // Split-K count: enough workgroups to cover the 256 CUs when the output has
 // few 256 x 256 tiles (M = 512, N = 2560: 20 tiles), at least 8 stages
@@ -243,6 +389,9 @@ hipError_t launch_proj_gemm_prepped(const _Float16 *a16, const int *ea, int fmt,
       break;
     case RT_LINEAR_BF16:
       hipLaunchKernelGGL(k_rows_to_f16<RT_LINEAR_BF16>, dim3(N), dim3(256), 0, s, wb, N, K, w16, ew);
+      break;
+    case RT_LINEAR_F32:
+      hipLaunchKernelGGL(k_rows_to_f16<RT_LINEAR_F32>, dim3(N), dim3(256), 0, s, wb, N, K, w16, ew);
       break;
     default: return hipErrorInvalidValue;
   }

@@ -32,6 +32,15 @@ hipError_t launch_gemm_prep_a(const float *a, int M, int K, _Float16 *a16, int *
 // or _BF16 (planar layouts of kquant.hip): its rows are widened to f16 with a
 // per-row power-of-two scale and multiplied on the matrix cores in f32.
 size_t proj_gemm_workspace_bytes(int M, int N, int K);
+// c[m][n] = a[m][k] . W[n][k] (+ bias[n]) on f32 weights, rows of A in groups
+// of 8 (each weight row read once per group); k % 4 == 0, w and a 16-byte aligned.
+hipError_t launch_f32_gemv_rows(const float *w, const float *a, const float *bias, float *c, int M, int N, int K,
+                                hipStream_t s);
+// the same on BF16 weights; k % 8 == 0
+hipError_t launch_bf16_gemv_rows(const uint16_t *w, const float *a, const float *bias, float *c, int M, int N, int K,
+                                 hipStream_t s);
+// c[m][n] += bias[n]
+hipError_t launch_add_bias_rows(float *c, const float *bias, int M, int N, hipStream_t s);
 hipError_t launch_proj_gemm(const float *a, int fmt, const void *w, float *c, int M, int N, int K, void *ws,
                             hipStream_t s);
 // The same two GEMMs on an A prepared once (launch_gemm_prep_a) for several

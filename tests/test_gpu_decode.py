@@ -335,3 +335,38 @@ def test_failed_set_unsets_layer_and_embed(rt, orc):
     d.set_embed(embed, fnorm)
     assert np.array_equal(d.decode_step(9, pos), first)
     d.close()
+
+
+def test_memory_report(rt, orc):
+    """rt_decode_memory (print_metal_memory, metal_decode.rs:1285-1354): the
+    weights and KV cache of a context add up to what its shapes hold, for
+    uploaded and for device-bound weights; prefill scratch appears after a
+    prefill."""
+    import torch
+    cfg = tiny(2)
+    max_seq, pos = 40, 4
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=pos, seed=61)
+    H, F, D = cfg["hidden"], cfg["ffn"], cfg["head_dim"]
+    QD, KVD = cfg["n_q_heads"] * D, cfg["n_kv_heads"] * D
+    proj = sum(r * (c // 256) * 144 for r, c in ((QD, H), (KVD, H), (KVD, H), (H, QD), (F, H), (F, H), (H, F)))
+    weights = cfg["n_layers"] * (proj + (4 * H + 2 * D) * 4) + cfg["vocab"] * H * 2 + H * 4
+    kv = cfg["n_layers"] * 2 * max_seq * KVD * 4
+    d = build_ctx(rt, cfg, layers, embed, fnorm, pos, max_seq)
+    m = d.memory()
+    assert m["weights"] == weights and m["kv_cache"] == kv and m["prefill"] == 0
+    assert m["activation"] > 0 and m["batch"] > 0
+    assert m["total"] == sum(m[k] for k in ("weights", "kv_cache", "activation", "batch", "prefill"))
+    d.prefill([1, 2, 3], 0, 1)
+    assert d.memory()["prefill"] > 0
+    d.print_memory()
+    d.close()
+    # the same weights bound by device pointer
+    dev = torch.device("cuda:0")
+    dl = [{k: torch.from_numpy(np.ascontiguousarray(v)).to(dev) for k, v in L.items() if k not in ("k_cache", "v_cache")}
+          for L in layers]
+    d2 = rt.HipDecodeContext(cfg, max_seq)
+    for i, L in enumerate(dl):
+        d2.set_layer(i, L)
+    d2.set_embed(torch.from_numpy(embed).to(dev), torch.from_numpy(fnorm).to(dev))
+    assert d2.memory()["weights"] == weights
+    d2.close()

@@ -386,13 +386,17 @@ def test_linear_gemm_matches_float64(rt, orc, dev, fmt, m, n, k):
 
 def test_linear_gemm_rejects_bad_shapes(rt):
     with pytest.raises(rt.RtError):
-        rt.linear_gemm_f32(3, 16, 16, 16, 1, 1, 256)  # RT_LINEAR_F32 has no GEMM here
+        rt.linear_gemm_f32(3, 16, 16, 16, 1, 1, 258)  # f32 rows are read as 16-byte vectors
+    with pytest.raises(rt.RtError):
+        rt.linear_gemm_f32(6, 16, 16, 16, 1, 1, 256)  # no such format
     with pytest.raises(rt.RtError):
         rt.linear_gemm_f32(4, 16, 16, 16, 1, 1, 96)  # Q6_K rows are 256-element blocks
     with pytest.raises(rt.RtError):
         rt.linear_gemm_f32(5, 16, 16, 16, 0, 1, 64)
     with pytest.raises(rt.RtError):
-        rt.linear_gemm_f32(2, 16, 16, 16, 1, 1, 96)  # K moves in stages of 64
+        rt.linear_gemm_f32(2, 16, 16, 16, 9, 1, 96)  # above 8 rows K moves in stages of 64
+    with pytest.raises(rt.RtError):
+        rt.linear_gemm_f32(2, 16, 16, 16, 1, 1, 100)  # eight bf16 weights per load
 
 
 def plain_ctx(rt, cfg, dev_layers, fmts, embed, fnorm, max_seq):
