@@ -122,6 +122,10 @@ rt_status rt_q4k_gemm_f32(const float *a_dev, const void *w_dev, float *c_dev, i
  * Matrices are row-major [rows][k] in block order, as in the file.
  * ------------------------------------------------------------------------- */
 /* GGUF block bytes (host) -> planar layout (host); n_blocks*210 / *34 bytes. */
+/* y = gelu_tanh(x) (autograd2.rs:3082-3091), n floats, device pointers: the
+ * activation exactly as the decode step and prefill kernels compute it. */
+rt_status rt_gelu_tanh(const float *x, float *y, size_t n, void *stream);
+
 rt_status rt_q6k_repack(const void *gguf_blocks, size_t n_blocks, void *dst);
 rt_status rt_q8_0_repack(const void *gguf_blocks, size_t n_blocks, void *dst);
 /* Device dequantisation, bit-exact with decode_q6k_to_f32 / decode_q8_0_to_f32. */

@@ -58,6 +58,7 @@ _SIGNATURES = {
     "rt_q4k_gemv_batch_noalloc": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "rt_qlinear_forward": (_i32, [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "rt_decode_memory": (_i32, [_vp, _vp]),
+    "rt_gelu_tanh": (_i32, [_vp, _vp, _sz, _vp]),
     "rt_qlinear_forward_host": (_i32, [_i32, _vp, _sz, _vp, _vp, _vp, _i64, _i64, _i64]),
     "rt_noalloc_scratch_bytes": (_sz, []),
     "rt_q6k_repack": (_i32, [_vp, _sz, _vp]),
@@ -178,6 +179,11 @@ def bf16_gemv(w, x, y, n: int, k: int, stream=None) -> None:
 def q4k_gemv_batch(w, a, c, m: int, n: int, k: int, stream=None) -> None:
     """c[m][n] = a[m][k] . W[n][k] for m <= 8 rows (gemv_q4k_t_batch)."""
     check(lib().rt_q4k_gemv_batch(_p(w), _p(a), _p(c), m, n, k, _stream(stream)))
+
+
+def gelu_tanh(x, y, stream=None) -> None:
+    """y = gelu_tanh(x) on the device, as the decode and prefill kernels compute it."""
+    check(lib().rt_gelu_tanh(_p(x), _p(y), x.numel(), _stream(stream)))
 
 
 def q4k_gemv_batch_noalloc(w, a, c, m: int, n: int, k: int, stream=None) -> None:

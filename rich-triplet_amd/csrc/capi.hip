@@ -109,6 +109,13 @@ rt_status rt_bf16_gemv(const uint16_t *w, const float *x, float *y, int64_t n, i
   return hip_error(launch_bf16_gemv(w, x, y, (int)n, (int)k, (hipStream_t)stream), "rt_bf16_gemv");
 }
 
+// gelu_tanh (autograd2.rs:3082-3091) as the decode step and prefill apply it.
+rt_status rt_gelu_tanh(const float *x, float *y, size_t n, void *stream) {
+  if (n == 0) return RT_OK;
+  if (!x || !y) return set_error(RT_EINVAL, "rt_gelu_tanh: null pointer");
+  return hip_error(launch_gelu_tanh(x, y, n, (hipStream_t)stream), "rt_gelu_tanh");
+}
+
 rt_status rt_q6k_repack(const void *gguf_blocks, size_t n_blocks, void *dst) {
   if (n_blocks == 0) return RT_OK;
   if (!gguf_blocks || !dst) return set_error(RT_EINVAL, "rt_q6k_repack: null pointer");

@@ -15,6 +15,7 @@
 // After the last layer k_lmhead applies the final residual, the final norm
 // and the BF16 lm_head GEMV.  Token id and position are read from device
 // memory so the whole step replays as one hipGraph.
+#include <algorithm>
 #include <vector>
 
 #include "../../include/rt_hip.h"
@@ -178,6 +179,17 @@ __global__ __launch_bounds__(256) void k_prologue(DecodeArgs a, const float *__r
       reinterpret_cast<float4 *>(x_out)[f] = x[i];
       reinterpret_cast<float4 *>(xn_out)[f] = norm4(x[i], rx, pr.go[i]);
     }
+}
+
+// gelu_tanh of n values (the activation of the decode step and prefill).
+__global__ __launch_bounds__(256) void k_gelu_tanh(const float *__restrict__ x, float *__restrict__ y, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) y[i] = gelu_tanh(x[i]);
+}
+
+hipError_t launch_gelu_tanh(const float *x, float *y, size_t n, hipStream_t s) {
+  const unsigned grid = (unsigned)std::min<size_t>((n + 255) / 256, 8192);
+  hipLaunchKernelGGL(k_gelu_tanh, dim3(grid), dim3(256), 0, s, x, y, n);
+  return hipGetLastError();
 }
 
 __global__ __launch_bounds__(256) void k_gelu_mul_vec(float *h, const float *__restrict__ u, int n) {

@@ -39,6 +39,8 @@ hipError_t launch_f32_gemv_rows(const float *w, const float *a, const float *bia
 // the same on BF16 weights; k % 8 == 0
 hipError_t launch_bf16_gemv_rows(const uint16_t *w, const float *a, const float *bias, float *c, int M, int N, int K,
                                  hipStream_t s);
+// y = gelu_tanh(x), elementwise (the decode step's and prefill's activation)
+hipError_t launch_gelu_tanh(const float *x, float *y, size_t n, hipStream_t s);
 // c[m][n] += bias[n]
 hipError_t launch_add_bias_rows(float *c, const float *bias, int M, int N, hipStream_t s);
 hipError_t launch_proj_gemm(const float *a, int fmt, const void *w, float *c, int M, int N, int K, void *ws,

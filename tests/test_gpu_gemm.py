@@ -65,9 +65,9 @@ def test_gemm_bf16_vs_oracle(rt, orc, dev, m, n, k, seed):
     assert err < GEMM_TOL
 
 
-@pytest.mark.parametrize("m,n,k", [(4608, 9216, 3072), (4608, 3072, 12288)])
+@pytest.mark.parametrize("m,n,k", [(4608, 9216, 3072), (4608, 12288, 3072), (4608, 3072, 12288)])
 def test_gemm_flux_shapes(rt, orc, dev, m, n, k):
-    """FLUX-12B shapes (QKV and MLP-down); reference on the GPU in f32 from the
+    """FLUX-12B shapes (QKV, MLP-up, MLP-down); reference on the GPU in f32 from the
     oracle's dequantised weights (a library GEMM, not this library's kernels)."""
     import torch
     blocks = orc.synth_q4k(7 + n, n, k)
