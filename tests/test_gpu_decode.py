@@ -370,3 +370,21 @@ def test_memory_report(rt, orc):
     d2.set_embed(torch.from_numpy(embed).to(dev), torch.from_numpy(fnorm).to(dev))
     assert d2.memory()["weights"] == weights
     d2.close()
+
+
+def test_gelu_tanh_matches_oracle(rt, orc):
+    """The device gelu_tanh against the oracle's (glibc tanhf, as Rust's f32
+    tanh): identical wherever tanh saturates (|x| >= 6, where the FFN of the
+    synthetic models sends most gate values), and elsewhere within the two
+    ulps of tanh that separate two libm's, |dy| <= |x| 2^-23 + |y| 2^-23."""
+    import torch
+    x = np.concatenate([np.linspace(-40, 40, 160_001, dtype=np.float32),
+                        np.array([0.0, -0.0, 1e-30, -1e-30, 1e30, -1e30], np.float32)])
+    ref = np.array([orc.gelu_tanh(float(v)) for v in x], np.float32)
+    y = torch.empty(len(x), device="cuda")
+    rt.gelu_tanh(torch.from_numpy(x).cuda(), y)
+    got = y.cpu().numpy()
+    sat = np.abs(x) >= 6
+    assert np.array_equal(got[sat].view(np.int32), ref[sat].view(np.int32))
+    tol = (np.abs(x) + np.abs(ref)) * 2.0 ** -23
+    assert np.all(np.abs(got - ref) <= tol)
