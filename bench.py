@@ -120,6 +120,9 @@ def main() -> int:
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the PMC probe: a 256 MiB copy (calibration) and 20 launches of the dominant "
                          "kernel on distinct weights; meant to run under rocprofv3 --pmc")
+    ap.add_argument("--decode-profile", action="store_true",
+                    help="only run the config-3 decode step (a 256 MiB copy first, as the counter calibration), "
+                         "--warmup then --steps tokens; meant to run under rocprofv3")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -163,6 +166,28 @@ def main() -> int:
         layers.append(w)
     embed = (torch.randn(V * H, device=dev, generator=gen) * 0.02).to(torch.bfloat16).view(torch.int16)
     final_norm = torch.randn(H, device=dev, generator=gen) * 0.1
+    if args.decode_profile:
+        a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        a.fill_(1)
+        torch.cuda.synchronize()
+        b.copy_(a)  # counter calibration: reads and writes exactly 256 MiB
+        torch.cuda.synchronize()
+        del a, b
+        d, pos = build_decode(rt, torch, dev, gen, layers, embed, final_norm, args)
+        for _ in range(args.warmup):
+            d.decode_step_async(pos % V, pos)
+            pos += 1
+        d.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(args.steps):
+            d.decode_step_async(pos % V, pos)
+            pos += 1
+        d.synchronize()
+        dt = (time.perf_counter() - t1) / args.steps
+        print(json.dumps({"decode_profile": "done", "steps": args.steps, "ms_per_token": round(dt * 1e3, 4)}))
+        d.close()
+        return 0
     x_h = torch.randn(H, device=dev, generator=gen)
     x_q = torch.randn(QD, device=dev, generator=gen)
     x_f = torch.randn(F, device=dev, generator=gen)
@@ -220,6 +245,38 @@ def main() -> int:
     step_ms = e0.elapsed_time(e1) / args.steps
     value = step_bytes / (step_ms * 1e-3) / 1e9
     log(f"config-1 step {step_ms:.3f} ms -> {value:.0f} GB/s ({step_bytes / 1e9:.3f} GB per step)")
+
+    def time_graph(enqueue, reps):
+        """Average ms of one replay of a graph of enqueue(stream) (one eager warm-up run first)."""
+        with torch.cuda.stream(cap):
+            enqueue(cap)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap):
+            enqueue(torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        del g
+        return a.elapsed_time(b) / reps
+
+    # the same step without the BF16 lm_head: the Q4_K GEMVs alone
+    def enqueue_q4k_only(stream):
+        for w in layers:
+            for _, names, x in step_launches:
+                enqueue_layer(w, names, x, stream)
+
+    q4k_ms = time_graph(enqueue_q4k_only, max(5, args.steps // 2))
+    q4k_only = {"ms": round(q4k_ms, 4), "bytes": q4k_step_bytes,
+                "GBps": round(q4k_step_bytes / (q4k_ms * 1e-3) / 1e9, 1),
+                "frac_of_hbm_peak": round(q4k_step_bytes / (q4k_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+    log(f"config-1 Q4_K GEMVs alone: {q4k_ms:.3f} ms -> {q4k_only['GBps']} GB/s")
 
     # ---------------- per-shape kernel timings (dominant kernel = gate/up) ------
     per_shape = {}
@@ -315,6 +372,28 @@ def main() -> int:
         log(f"{name} {n}x{k}: Q6_K {kquant['q6k_' + name]['us_per_launch']} us, "
             f"Q8_0 {kquant['q8_0_' + name]['us_per_launch']} us, BF16 (reference widening) "
             f"{kquant['bf16_' + name]['us_per_launch']} us")
+    # Streaming-read floor: a kernel that only reads, with 16-byte loads, the
+    # same bytes per launch as the GEMV, from 34 distinct buffers in one graph.
+    sink = torch.zeros(64, dtype=torch.int32, device=dev)
+    floor = {}
+    for label, nbytes in (("gateup_fused", per_shape["gateup_fused"]["bytes_per_launch"]),
+                          ("gate", per_shape["gate"]["bytes_per_launch"])):
+        nb16 = (nbytes + 15) // 16 * 16
+        bufs = torch.empty(L, nb16, dtype=torch.uint8, device=dev)
+        bufs.fill_(7)
+
+        def enqueue_reads(stream, bufs=bufs, nb16=nb16):
+            for i in range(L):
+                rt.stream_read(bufs[i], nb16, sink, stream=stream)
+
+        us = time_graph(enqueue_reads, reps) * 1e3 / L
+        gbps = nbytes / us / 1e3
+        floor[label] = {"bytes_per_launch": nbytes, "us_per_launch": round(us, 3), "GBps": round(gbps, 1),
+                        "frac_of_hbm_peak": round(gbps / PEAK_HBM_GBS, 4),
+                        "gemv_frac_of_floor": round(per_shape[label]["GBps"] / gbps, 4)}
+        log(f"streaming-read floor, {nbytes / 1e6:.1f} MB per launch: {us:.2f} us, {gbps:.0f} GB/s; "
+            f"the GEMV reaches {per_shape[label]['GBps'] / gbps:.2f} of it")
+        del bufs
     # dominant kernel of the step (largest share of its time): the gate|up GEMV
     dom = per_shape["gateup_fused"]
     roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
@@ -322,10 +401,12 @@ def main() -> int:
                 "kernel": "k_q4k_gemv_dig_multi<NB=10,T=320,ITERS=2> (Q4_K GEMV, gate|up 2 x 10240x2560 in one "
                           "launch)",
                 "bytes_per_launch": dom["bytes_per_launch"], "us_per_launch": dom["us_per_launch"],
+                "copy_floor": floor["gateup_fused"],
                 "single_matrix": {"kernel": "k_q4k_gemv_dig<NB=10,T=960,ITERS=2> (10240x2560)",
                                   "us_per_launch": per_shape["gate"]["us_per_launch"],
                                   "GBps": per_shape["gate"]["GBps"],
-                                  "frac": round(per_shape["gate"]["GBps"] / PEAK_HBM_GBS, 4)}}
+                                  "frac": round(per_shape["gate"]["GBps"] / PEAK_HBM_GBS, 4),
+                                  "copy_floor": floor["gate"]}}
     log(f"dominant kernel gate|up 2x10240x2560: {dom['us_per_launch']} us/launch, {dom['GBps']} GB/s "
         f"(one 10240x2560 matrix alone: {per_shape['gate']['us_per_launch']} us)")
 
@@ -333,16 +414,7 @@ def main() -> int:
     decode = None
     if not args.skip_decode:
         ctx = 4096
-        cfg = dict(rt.GEMMA3_4B)
-        d = rt.HipDecodeContext(cfg, ctx + args.warmup + args.steps + 8 * (2 + max(2, args.steps // 4)) + 8)
-        for li, w in enumerate(layers):
-            d.set_layer(li, w)
-            kv = torch.randn(2, ctx, KVD, device=dev, generator=gen)
-            d.sync_kv_from_cpu(li, kv[0], kv[1], ctx)
-            del kv
-        d.set_embed(embed, final_norm)
-        torch.cuda.synchronize()
-        pos = ctx
+        d, pos = build_decode(rt, torch, dev, gen, layers, embed, final_norm, args)
         for _ in range(args.warmup):
             d.decode_step_async(pos % V, pos)
             pos += 1
@@ -441,8 +513,12 @@ def main() -> int:
     cpu = None
     if not args.skip_cpu:
         sys.path.insert(0, str(REPO))
+        import tempfile
         from oracle import oracle as orc
-        threads = orc.hw_threads()
+        native_dir = tempfile.mkdtemp(prefix="rt_oracle_native_")
+        orc.use_native_build(native_dir)  # gcc -O3 -march=native on this host
+        nproc = os.cpu_count() or 1
+        threads = min(nproc, 16)  # gemv_mt's hardware count, capped at the box's 16-CPU share
         host = [(name, n, k, orc.synth_q4k(77 + i, n, k)) for i, (name, n, k) in enumerate(Q4K_SHAPES)]
         xs = {H: orc.synth_normal(5, H), QD: orc.synth_normal(6, QD), F: orc.synth_normal(7, F)}
         lm_rows = 16384
@@ -459,9 +535,14 @@ def main() -> int:
             reps_done += 1
         cpu_gbs = sample_bytes * reps_done / t_cpu / 1e9
         cpu = {"value": round(cpu_gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+               "nproc": nproc,
+               "threads_rule": "gemv_mt (autograd2.rs:1961-1968): min(hw, N/128) threads per GEMV, hw = "
+                               f"min(nproc={nproc}, 16); 16 is the CPU share of one GPU on this box",
+               "build": "gcc -O3 -march=native -ffp-contract=off -fno-fast-math (oracle/rt_oracle.c, built on "
+                        "this host at bench time)",
                "sample": f"one layer's 7 Q4_K projection GEMVs + {lm_rows} lm_head rows, "
                          f"{reps_done} reps in {t_cpu:.1f}s; oracle/rt_oracle.c dot_row/gemv_mt "
-                         f"(scalar x86 branch of autograd2.rs), {threads} threads",
+                         f"(scalar x86 branch of autograd2.rs)",
                "cpu_model": cpu_model()}
         log(f"cpu baseline {cpu_gbs:.2f} GB/s on {threads} threads")
 
@@ -476,13 +557,15 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "q4_k weights, f32 accumulate; GEMV activations staged as 16-bit fixed point per 64-element "
+                 "chunk (3e-5 rel-L2)",
         "data": "synthetic",
         "frac_of_hbm_peak": round(value / PEAK_HBM_GBS, 4),
         "config": {"workload": "config 1: Gemma-3-4B projection set of one decode token, 34 distinct layers x "
                                "{q,k,v,o,gate,up,down} Q4_K GEMV (q|k|v and gate|up, which share their input, "
                                "one launch each) + BF16 lm_head 2560->262144, one hipGraph",
                    "bytes_per_step": step_bytes, "parallelism": "single GPU"},
+        "q4k_only": q4k_only,
         "roofline": roofline,
         "per_shape": per_shape,
         "kquant_gemv": kquant,
@@ -492,6 +575,21 @@ def main() -> int:
     }
     print(json.dumps(out), flush=True)
     return 0
+
+
+def build_decode(rt, torch, dev, gen, layers, embed, final_norm, args, ctx: int = 4096):
+    """The config-3 decode context: the 34 synthetic layers, N(0,1) K/V rows
+    0..ctx-1 in every layer, the BF16 tied embedding; returns it and the
+    first position to decode (ctx)."""
+    d = rt.HipDecodeContext(dict(rt.GEMMA3_4B), ctx + args.warmup + args.steps + 8 * (2 + max(2, args.steps // 4)) + 8)
+    for li, w in enumerate(layers):
+        d.set_layer(li, w)
+        kv = torch.randn(2, ctx, KVD, device=dev, generator=gen)
+        d.sync_kv_from_cpu(li, kv[0], kv[1], ctx)
+        del kv
+    d.set_embed(embed, final_norm)
+    torch.cuda.synchronize()
+    return d, ctx
 
 
 def measured_traffic():

@@ -31,14 +31,29 @@ def build() -> None:
 
 
 _lib = None
+_lib_path = None
+
+
+def use_native_build(out_dir: str) -> str:
+    """Compile rt_oracle.c for this host's CPU (gcc -O3 -march=native, still
+    -ffp-contract=off: no fused multiply-adds, no reassociation, so the
+    results equal liboracle.so's) into out_dir, and bind that library
+    instead.  For the CPU baseline, which is timed on the GPU box's host."""
+    global _lib, _lib_path
+    so = os.path.join(out_dir, "liboracle_native.so")
+    subprocess.run(["gcc", "-O3", "-march=native", "-std=c11", "-fPIC", "-ffp-contract=off", "-fno-fast-math",
+                    "-pthread", "-shared", "-o", so, str(HERE / "rt_oracle.c"), "-lm"], check=True)
+    _lib, _lib_path = None, so
+    lib()
+    return so
 
 
 def lib() -> C.CDLL:
     global _lib
     if _lib is None:
-        if not LIB_PATH.exists():
+        if _lib_path is None and not LIB_PATH.exists():
             build()
-        L = C.CDLL(str(LIB_PATH))
+        L = C.CDLL(str(_lib_path or LIB_PATH))
         sig = {
             "orc_f16_to_f32": (C.c_float, [C.c_uint16]),
             "orc_f32_to_f16_rne": (C.c_uint16, [C.c_float]),

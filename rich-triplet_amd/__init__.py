@@ -59,6 +59,7 @@ _SIGNATURES = {
     "rt_qlinear_forward": (_i32, [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "rt_decode_memory": (_i32, [_vp, _vp]),
     "rt_gelu_tanh": (_i32, [_vp, _vp, _sz, _vp]),
+    "rt_stream_read": (_i32, [_vp, _sz, _vp, _vp]),
     "rt_qlinear_forward_host": (_i32, [_i32, _vp, _sz, _vp, _vp, _vp, _i64, _i64, _i64]),
     "rt_noalloc_scratch_bytes": (_sz, []),
     "rt_q6k_repack": (_i32, [_vp, _sz, _vp]),
@@ -179,6 +180,11 @@ def bf16_gemv(w, x, y, n: int, k: int, stream=None) -> None:
 def q4k_gemv_batch(w, a, c, m: int, n: int, k: int, stream=None) -> None:
     """c[m][n] = a[m][k] . W[n][k] for m <= 8 rows (gemv_q4k_t_batch)."""
     check(lib().rt_q4k_gemv_batch(_p(w), _p(a), _p(c), m, n, k, _stream(stream)))
+
+
+def stream_read(buf, nbytes: int, sink, stream=None) -> None:
+    """Read nbytes of buf with 16-byte loads and discard them (a bandwidth floor)."""
+    check(lib().rt_stream_read(_p(buf), nbytes, _p(sink), _stream(stream)))
 
 
 def gelu_tanh(x, y, stream=None) -> None:
