@@ -123,6 +123,9 @@ def main() -> int:
     ap.add_argument("--decode-profile", action="store_true",
                     help="only run the config-3 decode step (a 256 MiB copy first, as the counter calibration), "
                          "--warmup then --steps tokens; meant to run under rocprofv3")
+    ap.add_argument("--verify-rows", type=int, default=0,
+                    help="with --decode-profile: run decode_step_batch calls of this many rows (1..8) instead "
+                         "of single-token steps")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -175,17 +178,25 @@ def main() -> int:
         torch.cuda.synchronize()
         del a, b
         d, pos = build_decode(rt, torch, dev, gen, layers, embed, final_norm, args)
-        for _ in range(args.warmup):
+        bm = args.verify_rows
+
+        def one(pos):
+            if bm:
+                d.decode_step_batch_async([(pos + i) % V for i in range(bm)], pos)
+                return pos + bm
             d.decode_step_async(pos % V, pos)
-            pos += 1
+            return pos + 1
+
+        for _ in range(args.warmup):
+            pos = one(pos)
         d.synchronize()
         t1 = time.perf_counter()
         for _ in range(args.steps):
-            d.decode_step_async(pos % V, pos)
-            pos += 1
+            pos = one(pos)
         d.synchronize()
         dt = (time.perf_counter() - t1) / args.steps
-        print(json.dumps({"decode_profile": "done", "steps": args.steps, "ms_per_token": round(dt * 1e3, 4)}))
+        print(json.dumps({"decode_profile": "done", "steps": args.steps, "verify_rows": bm,
+                          "ms_per_call": round(dt * 1e3, 4)}))
         d.close()
         return 0
     x_h = torch.randn(H, device=dev, generator=gen)
@@ -581,7 +592,7 @@ def build_decode(rt, torch, dev, gen, layers, embed, final_norm, args, ctx: int 
     """The config-3 decode context: the 34 synthetic layers, N(0,1) K/V rows
     0..ctx-1 in every layer, the BF16 tied embedding; returns it and the
     first position to decode (ctx)."""
-    d = rt.HipDecodeContext(dict(rt.GEMMA3_4B), ctx + args.warmup + args.steps + 8 * (2 + max(2, args.steps // 4)) + 8)
+    d = rt.HipDecodeContext(dict(rt.GEMMA3_4B), ctx + 8 * (args.warmup + args.steps) + 8 * (2 + max(2, args.steps // 4)) + 8)
     for li, w in enumerate(layers):
         d.set_layer(li, w)
         kv = torch.randn(2, ctx, KVD, device=dev, generator=gen)

@@ -185,8 +185,9 @@ rt_status rt_q4k_gemv_batch(const void *w, const float *a, float *c, int64_t m, 
  * hipMalloc).  Same arguments and results as rt_q4k_gemv_batch; its
  * workspace is a fixed per-GPU device array of rt_noalloc_scratch_bytes()
  * (8 MiB), which bounds n and k: the staged rows, (k/64)*1152 bytes rounded
- * up to 256, plus the split-K partials, (k/512)*32*n bytes for k/256 even
- * (else (k/256)*32*n), must fit, else RT_EINVAL.  Every call on one GPU
+ * up to 256, plus the split-K partials, (k/256)*32*n bytes for
+ * 256 < k < 8192 ((k/1024)*32*n for k >= 8192 divisible by 1024), must fit,
+ * else RT_EINVAL.  Every call on one GPU
  * shares that array: calls that overlap on one GPU (two streams, two host
  * threads) race and must be serialised by the caller. */
 rt_status rt_q4k_gemv_batch_noalloc(const void *w, const float *a, float *c, int64_t m, int64_t n, int64_t k,

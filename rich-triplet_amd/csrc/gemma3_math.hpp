@@ -34,23 +34,17 @@ RT_DEV float sumsq4(float4 v) { return v.x * v.x + v.y * v.y + v.z * v.z + v.w *
 // Per-head RMSNorm (apply_per_head_norm, transformer4.rs:2485-2508, gamma
 // shared by the heads) followed by NeoX RoPE (apply_rope_at_offset,
 // 2742-2772) of one head of D values, by one wave.  Lane owns pairs
-// i = lane*P + p (p < P) with partners i + D/2; cs[i] = cos and
-// cs[D/2 + i] = sin of the pair's angle; src(i) loads element i.  The source
-// may be dst: every lane reads its own elements before it writes them.
-template <int D, class Load>
-RT_DEV void norm_rope_head_ld(Load src, const float *__restrict__ gamma, const float *__restrict__ cs, float eps,
-                              float *dst) {
+// i = lane*P + p (p < P) with partners i + D/2, held in x0[p] / x1[p];
+// cs[i] = cos and cs[D/2 + i] = sin of the pair's angle.  The source may be
+// dst: every lane has read its own elements before it writes them.
+template <int D>
+RT_DEV void norm_rope_head_regs(float (&x0)[D / 128], float (&x1)[D / 128], const float *__restrict__ gamma,
+                                const float *__restrict__ cs, float eps, float *dst) {
   constexpr int P = D / 128;
   const int lane = threadIdx.x & 63;
-  float x0[P], x1[P];
   float ss = 0.f;
 #pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int i = lane * P + p;
-    x0[p] = src(i);
-    x1[p] = src(i + D / 2);
-    ss += x0[p] * x0[p] + x1[p] * x1[p];
-  }
+  for (int p = 0; p < P; ++p) ss += x0[p] * x0[p] + x1[p] * x1[p];
   const float rinv = rms_inv_from_sumsq(wave_sum(ss), 1.0f / (float)D, eps);
 #pragma unroll
   for (int p = 0; p < P; ++p) {
@@ -62,6 +56,22 @@ RT_DEV void norm_rope_head_ld(Load src, const float *__restrict__ gamma, const f
     dst[i] = a0 * c - a1 * sn;
     dst[i + D / 2] = a0 * sn + a1 * c;
   }
+}
+
+// The same with element i from src(i).
+template <int D, class Load>
+RT_DEV void norm_rope_head_ld(Load src, const float *__restrict__ gamma, const float *__restrict__ cs, float eps,
+                              float *dst) {
+  constexpr int P = D / 128;
+  const int lane = threadIdx.x & 63;
+  float x0[P], x1[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int i = lane * P + p;
+    x0[p] = src(i);
+    x1[p] = src(i + D / 2);
+  }
+  norm_rope_head_regs<D>(x0, x1, gamma, cs, eps, dst);
 }
 
 template <int D>

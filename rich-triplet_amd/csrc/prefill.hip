@@ -153,14 +153,30 @@ __global__ __launch_bounds__(256) void k_pf_qk_rope(RowsIn q, RowsIn k, RowsIn v
   if (p0_dev) p0 = p0_dev[0];
   const int t = item / heads, h = item % heads;
   const float *c = cs + (size_t)t * cs_stride + cs_off;
+  // lane pairs (2l, 2l+1) and their partners + D/2 as float2 reads of the
+  // (split-K) projection output, every slice in flight at once
+  const int lane = (int)(threadIdx.x & 63);
+  auto head = [&](const RowsIn &r, int col, const float *g, float *dst) __attribute__((always_inline)) {
+    float x0[D / 128], x1[D / 128];
+    if constexpr (D == 256) {
+      const float2 a = rows_in2(r, t, col + 2 * lane), b = rows_in2(r, t, col + D / 2 + 2 * lane);
+      x0[0] = a.x, x0[1] = a.y, x1[0] = b.x, x1[1] = b.y;
+    } else {
+#pragma unroll
+      for (int pp = 0; pp < D / 128; ++pp) {
+        x0[pp] = rows_in1(r, t, col + lane * (D / 128) + pp);
+        x1[pp] = rows_in1(r, t, col + D / 2 + lane * (D / 128) + pp);
+      }
+    }
+    norm_rope_head_regs<D>(x0, x1, g, c, eps, dst);
+  };
   if (h < nq) {
-    norm_rope_head_ld<D>([&](int i) { return rows_in1(q, t, h * D + i); }, g_q, c, eps,
-                         q_out + ((size_t)t * nq + h) * D);
+    head(q, h * D, g_q, q_out + ((size_t)t * nq + h) * D);
   } else {
     const int kh = h - nq;
     const size_t dst = ((size_t)(p0 + t) * nkv + kh) * D;
-    norm_rope_head_ld<D>([&](int i) { return rows_in1(k, t, kh * D + i); }, g_k, c, eps, kc + dst);
-    for (int i = threadIdx.x & 63; i < D; i += 64) vc[dst + i] = rows_in1(v, t, kh * D + i);
+    head(k, kh * D, g_k, kc + dst);
+    for (int i = 2 * lane; i < D; i += 128) *reinterpret_cast<float2 *>(vc + dst + i) = rows_in2(v, t, kh * D + i);
   }
 }
 

@@ -15,20 +15,21 @@
 //   layout: dig[(chunk*8 + row)*2 + digit][64] bytes, stats[chunk*8 + row]
 //   = {delta, sum_lo, sum_hi, 0}; rows M..7 are zero.
 //
-// Product.  Lane l of a wave (j = l%16, g = l/16) is A row j = (row m = j/2,
-// digit d = j%2) and B column j = (weight row r = j/2, sub-block half
-// h = j%2); byte i of its operands is element 16g + i of the chunk.  A holds
-// digit d of row m; B holds the 4-bit codes of weight row r where the element
-// lies in half h (elements 0..31: low nibbles of qs[0..32), sub-block 2c;
-// 32..63: high nibbles, sub-block 2c+1) and zero elsewhere.  So
-//   C[(m,d)][(r,h)] = sum over sub-block 2c+h of q * x_d     (exact int32)
-// and lane (j, g) receives rows 4g..4g+3 of C: rows m = 2g, 2g+1, both
-// digits, for its (r, h).  The epilogue applies the scales:
+// Product (v_mfma_i32_16x16x32_i8, one MFMA per 32-element sub-block).  Lane
+// l of a wave (j = l%16, g = l/16) holds k-slots 8g..8g+7 of A row j =
+// (activation row m = j/2, digit d = j%2) and of B column j = weight row j of
+// the wave's 16.  A sub-block's 32 codes are the low (even sub-block) or high
+// (odd) nibbles of its chunk's 32 bytes, so one 8-byte load of bytes
+// 8g..8g+7 feeds both sub-blocks of a chunk and no B lane is padding:
+//   C[(m,d)][j] = sum over the sub-block of q * x_d     (exact int32)
+// Lane (j, g) receives rows 4g..4g+3 of C: rows m = 2g, 2g+1, both digits,
+// for weight row j, and applies the scales:
 //   acc[m] += d*sv*delta_m * (256 C1 + C0) - dmin*mv * sum_m(sub-block)
-// and lanes (r, 0) and (r, 1) add their halves at the end.  A wave owns 16
-// weight rows (two B operands against one A), a workgroup 64 rows and a
-// slice of one or two super-blocks; with several slices each writes partial
-// sums that k_mb_reduce adds in slice order.
+// A workgroup is four waves of 16 rows (64 rows) over a slice of KS
+// super-blocks; its activation slice is copied to LDS once.  With several
+// slices each writes partial sums that k_mb_reduce (or the consumer) adds in
+// slice order.  Many small workgroups at full occupancy overlap one
+// workgroup's arithmetic with the others' loads.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -52,108 +53,87 @@ __global__ __launch_bounds__(256) void k_mb_stage(const float *__restrict__ x, i
   mb_stage4(dig, stats, row, c, q, v, ci < nchunk);
 }
 
-template <int SB>
+typedef long i64_t;
+
+template <int KS>
 __global__ __launch_bounds__(256) void k_q4k_gemv_mb(MbArgs p) {
-  // A workgroup: 64 rows (16 per wave, two B operands of 8 rows) times a
-  // slice of SB super-blocks.  The slice's activation digits and stats are
-  // copied to LDS once; every weight load of the slice is issued before the
-  // first MFMA, so the many small workgroups hide each other's latency.
-  constexpr int CH = 4 * SB;  // chunks in the slice
+  constexpr int CH = 4 * KS;            // chunks in the slice
+  constexpr int NA = CH * 64 + CH * 8;  // 16-byte pieces of digits + stats
+  constexpr int AV = (NA + 255) / 256;
   __shared__ __attribute__((aligned(16))) int8_t a_lds[CH * 1024];
   __shared__ __attribute__((aligned(16))) float4 st_lds[CH * 8];
   const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
-  const int j = lane & 15, g = lane >> 4, r = j >> 1, h = j & 1;
+  const int j = lane & 15, g = lane >> 4;
   int rb = (int)blockIdx.x, mi = 0;
   while (mi + 1 < p.nmat && rb >= p.mat[mi].row_blocks) rb -= p.mat[mi++].row_blocks;
   const MbMat &M = p.mat[mi];
   const int nb = p.k / 256, slice = (int)blockIdx.y;
-  const int sb0 = slice * SB;  // the launcher makes SB divide nb
-  const size_t row_bytes = (size_t)nb * kQ4KBlockBytes;
-  int row[2];
-  const uint8_t *wp[2];
-#pragma unroll
-  for (int gi = 0; gi < 2; ++gi) {
-    row[gi] = rb * 64 + wave * 16 + 8 * gi + r;
-    wp[gi] = M.w + (size_t)min(row[gi], M.n - 1) * row_bytes + (size_t)sb0 * kQ4KBlockBytes;
-  }
-  const bool carries = (g >> 1) == h;  // this lane's k-slots lie in sub-block half h
-  const int qoff = 16 + 16 * (g & 1);
-  // weights of the whole slice
-  uint4 hd[2][SB], qw[2][SB][4];
-#pragma unroll
-  for (int gi = 0; gi < 2; ++gi)
-#pragma unroll
-    for (int b = 0; b < SB; ++b) {
-      hd[gi][b] = *reinterpret_cast<const uint4 *>(wp[gi] + b * kQ4KBlockBytes);
-#pragma unroll
-      for (int cc = 0; cc < 4; ++cc)
-        qw[gi][b][cc] = carries ? *reinterpret_cast<const uint4 *>(wp[gi] + b * kQ4KBlockBytes + qoff + 32 * cc)
-                                : make_uint4(0u, 0u, 0u, 0u);
-    }
-  // activations of the slice: CH KB of digits, CH*8 stats
+  const int sb0 = slice * KS;  // the launcher makes KS divide nb
+  // The slice's activations first (clamped, unconditional loads), so their
+  // wait leaves every weight load in flight.
+  uint4 av[AV];
   {
-    const uint4 *src = reinterpret_cast<const uint4 *>(p.dig + (size_t)sb0 * 4 * 1024);
-    uint4 *dst = reinterpret_cast<uint4 *>(a_lds);
+    const uint4 *dsrc = reinterpret_cast<const uint4 *>(p.dig + (size_t)sb0 * 4 * 1024);
+    const uint4 *ssrc = reinterpret_cast<const uint4 *>(p.stats) + (size_t)sb0 * 4 * 8;
 #pragma unroll
-    for (int i = (int)threadIdx.x; i < CH * 64; i += 256) dst[i] = src[i];
-    const float4 *ssrc = reinterpret_cast<const float4 *>(p.stats) + (size_t)sb0 * 4 * 8;
-    for (int i = (int)threadIdx.x; i < CH * 8; i += 256) st_lds[i] = ssrc[i];
+    for (int i = 0; i < AV; ++i) {
+      const int idx = min((int)threadIdx.x + 256 * i, NA - 1);
+      av[i] = idx < CH * 64 ? dsrc[idx] : ssrc[idx - CH * 64];
+    }
+  }
+  const int row = rb * 64 + wave * 16 + j;
+  const uint8_t *wp = M.w + (size_t)min(row, M.n - 1) * ((size_t)nb * kQ4KBlockBytes) + (size_t)sb0 * kQ4KBlockBytes;
+  uint4 hd[KS];
+  uint2 qw[KS][4];
+#pragma unroll
+  for (int b = 0; b < KS; ++b) {
+    hd[b] = *reinterpret_cast<const uint4 *>(wp + b * kQ4KBlockBytes);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) qw[b][c] = *reinterpret_cast<const uint2 *>(wp + b * kQ4KBlockBytes + 16 + 32 * c + 8 * g);
+  }
+#pragma unroll
+  for (int i = 0; i < AV; ++i) {
+    const int idx = (int)threadIdx.x + 256 * i;
+    if (idx < CH * 64) reinterpret_cast<uint4 *>(a_lds)[idx] = av[i];
+    else if (idx < NA) reinterpret_cast<uint4 *>(st_lds)[idx - CH * 64] = av[i];
   }
   __syncthreads();
   const uint32_t m4 = opaque_u32(0x0F0F0F0Fu);
-  float acc[2][2] = {};
+  float acc[2] = {};
 #pragma unroll
-  for (int b = 0; b < SB; ++b) {
-    float dsv[2][4], dmv[2][4];
+  for (int b = 0; b < KS; ++b) {
+    const float d = half_bits_to_f32(hd[b].x & 0xFFFFu), dm = half_bits_to_f32(hd[b].x >> 16);
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
-      const float d = half_bits_to_f32(hd[gi][b].x & 0xFFFFu), dm = half_bits_to_f32(hd[gi][b].x >> 16);
+    for (int c = 0; c < 4; ++c) {
+      const int ci = 4 * b + c;
+      const float4 st0 = st_lds[ci * 8 + 2 * g], st1 = st_lds[ci * 8 + 2 * g + 1];  // rows 2g, 2g+1
 #pragma unroll
-      for (int cc = 0; cc < 4; ++cc) {
+      for (int h = 0; h < 2; ++h) {
+        const i64_t A = *reinterpret_cast<const i64_t *>(a_lds + ci * 1024 + j * 64 + 32 * h + 8 * g);
         uint32_t sv, mv;
-        q4k_scale_min(hd[gi][b].y, hd[gi][b].z, hd[gi][b].w, 2 * cc + h, sv, mv);
-        dsv[gi][cc] = d * (float)sv;
-        dmv[gi][cc] = dm * (float)mv;
-      }
-    }
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
-      const int c = 4 * b + cc;
-      const i32x4_t A = *reinterpret_cast<const i32x4_t *>(a_lds + c * 1024 + j * 64 + 16 * g);
-      const float4 st0 = st_lds[c * 8 + 2 * g], st1 = st_lds[c * 8 + 2 * g + 1];  // rows 2g, 2g+1
-#pragma unroll
-      for (int gi = 0; gi < 2; ++gi) {
-        const uint4 q = qw[gi][b][cc];
-        const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
-        i32x4_t B;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) B[t] = (int)((h ? w4[t] >> 4 : w4[t]) & m4);
-        const i32x4_t C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, i32x4_t{0, 0, 0, 0}, 0, 0, 0);
+        q4k_scale_min(hd[b].y, hd[b].z, hd[b].w, 2 * c + h, sv, mv);
+        const float sc = d * (float)sv, mn = dm * (float)mv;
+        const uint32_t b0 = (h ? qw[b][c].x >> 4 : qw[b][c].x) & m4, b1 = (h ? qw[b][c].y >> 4 : qw[b][c].y) & m4;
+        const i64_t B = (i64_t)(((uint64_t)b1 << 32) | b0);
+        const i32x4_t C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, i32x4_t{0, 0, 0, 0}, 0, 0, 0);
         const float s0 = (float)(C[0] + 256 * C[1]), s1 = (float)(C[2] + 256 * C[3]);  // exact: < 2^24
-        acc[gi][0] = fmaf(dsv[gi][cc] * st0.x, s0, fmaf(-dmv[gi][cc], h ? st0.z : st0.y, acc[gi][0]));
-        acc[gi][1] = fmaf(dsv[gi][cc] * st1.x, s1, fmaf(-dmv[gi][cc], h ? st1.z : st1.y, acc[gi][1]));
+        acc[0] = fmaf(sc * st0.x, s0, fmaf(-mn, h ? st0.z : st0.y, acc[0]));
+        acc[1] = fmaf(sc * st1.x, s1, fmaf(-mn, h ? st1.z : st1.y, acc[1]));
+        // Keeps each sub-block's scaling beside its MFMA: sunk into the store
+        // branch, it holds every MFMA result live and halves the occupancy.
+        asm volatile("" : "+v"(acc[0]), "+v"(acc[1]));
       }
     }
   }
-  // add the two sub-block halves (lanes j and j^1), then rows 2g, 2g+1 out
+  if (row >= M.n) return;
 #pragma unroll
-  for (int gi = 0; gi < 2; ++gi)
-#pragma unroll
-    for (int t = 0; t < 2; ++t) acc[gi][t] += dpp<0xB1>(acc[gi][t]);
-  if (h == 0) {
-#pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
-      if (row[gi] >= M.n) continue;
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int m = 2 * g + t;
-        if (m >= p.m) continue;
-        if (p.ksplit == 1)
-          M.y[(size_t)m * M.n + row[gi]] = acc[gi][t];
-        else
-          p.part[((size_t)slice * 8 + m) * p.ntot + M.part_off + row[gi]] = acc[gi][t];
-      }
-    }
+  for (int t = 0; t < 2; ++t) {
+    const int m = 2 * g + t;
+    if (m >= p.m) continue;
+    if (p.ksplit == 1)
+      M.y[(size_t)m * M.n + row] = acc[t];
+    else
+      p.part[((size_t)slice * 8 + m) * p.ntot + M.part_off + row] = acc[t];
   }
 }
 
@@ -175,8 +155,13 @@ __global__ __launch_bounds__(256) void k_mb_reduce(MbArgs p) {
 
 size_t mb_stage_bytes(int k) { return (size_t)(k / 64) * 8 * (128 + 16); }
 
-// Super-blocks per K slice: two where they divide the row, else one.
-static int mb_slice_sb(int k) { return (k / 256) % 2 == 0 ? 2 : 1; }
+// Super-blocks per K slice.  One for rows up to 8192: the smallest
+// workgroups overlap best, and the partial sums they leave (32 bytes per row
+// and super-block, against 144 of weights) cost less than two-block slices'
+// longer workgroups.  Four for longer rows (the FFN down projection), whose
+// 40 one-block slices would leave its consumer, a row norm on one workgroup
+// per row, too many partials to add.
+static int mb_slice_sb(int k) { return k >= 8192 && (k / 256) % 4 == 0 ? 4 : 1; }
 
 int mb_ksplit(int n_total, int k) {
   (void)n_total;
@@ -214,8 +199,8 @@ hipError_t launch_q4k_gemv_mb(const MbMat *mats, int nmat, int m, int k, const v
   p.ntot = ntot;
   p.ksplit = mb_ksplit(ntot, k);
   p.part = part;
-  if (mb_slice_sb(k) == 2)
-    hipLaunchKernelGGL(k_q4k_gemv_mb<2>, dim3(blocks, p.ksplit), dim3(256), 0, s, p);
+  if (mb_slice_sb(k) == 4)
+    hipLaunchKernelGGL(k_q4k_gemv_mb<4>, dim3(blocks, p.ksplit), dim3(256), 0, s, p);
   else
     hipLaunchKernelGGL(k_q4k_gemv_mb<1>, dim3(blocks, p.ksplit), dim3(256), 0, s, p);
   hipError_t e = hipGetLastError();

@@ -40,30 +40,44 @@ struct RowsIn {
 };
 __host__ __device__ inline RowsIn rows_plain(const float *p, int cols) { return RowsIn{p, 1, 0, cols, 0}; }
 
-// Slices are loaded eight at a time (the last group at clamped, in-bounds
-// slices that are not added), all eight in flight, then added in slice order.
+// Slices are loaded sixteen at a time (the last group at clamped, in-bounds
+// slices that are not added), all sixteen in flight, then added in slice
+// order: one round trip for the ten slices of a k = 2560 GEMV.
 __device__ __forceinline__ float4 rows_in4(const RowsIn &r, int t, int i) {
   const float *b = r.p + (size_t)t * r.row_stride + r.col_off + i;
   float4 s = *reinterpret_cast<const float4 *>(b);
-  for (int z = 1; z < r.ks; z += 8) {
-    float4 v[8];
+  for (int z = 1; z < r.ks; z += 16) {
+    float4 v[16];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const float4 *>(b + (size_t)min(z + u, r.ks - 1) * r.slice_stride);
+    for (int u = 0; u < 16; ++u) v[u] = *reinterpret_cast<const float4 *>(b + (size_t)min(z + u, r.ks - 1) * r.slice_stride);
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < 16; ++u)
       if (z + u < r.ks) s.x += v[u].x, s.y += v[u].y, s.z += v[u].z, s.w += v[u].w;
+  }
+  return s;
+}
+__device__ __forceinline__ float2 rows_in2(const RowsIn &r, int t, int i) {  // i even
+  const float *b = r.p + (size_t)t * r.row_stride + r.col_off + i;
+  float2 s = *reinterpret_cast<const float2 *>(b);
+  for (int z = 1; z < r.ks; z += 16) {
+    float2 v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = *reinterpret_cast<const float2 *>(b + (size_t)min(z + u, r.ks - 1) * r.slice_stride);
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      if (z + u < r.ks) s.x += v[u].x, s.y += v[u].y;
   }
   return s;
 }
 __device__ __forceinline__ float rows_in1(const RowsIn &r, int t, int i) {
   const float *b = r.p + (size_t)t * r.row_stride + r.col_off + i;
   float s = *b;
-  for (int z = 1; z < r.ks; z += 8) {
-    float v[8];
+  for (int z = 1; z < r.ks; z += 16) {
+    float v[16];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = b[(size_t)min(z + u, r.ks - 1) * r.slice_stride];
+    for (int u = 0; u < 16; ++u) v[u] = b[(size_t)min(z + u, r.ks - 1) * r.slice_stride];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < 16; ++u)
       if (z + u < r.ks) s += v[u];
   }
   return s;

@@ -21,8 +21,8 @@ def test_batch_gemv_rejects_bad_calls(rt):
     assert L.rt_q4k_gemv_batch(addr, addr, addr, 2, 64, 300, None) == rt.RT_EINVAL
 
 
-# decode shapes (gate/up: one K slice; down, o, q, k/v: split K), ragged row
-# counts that end inside a 64-row workgroup and a 16-row wave, one super-block
+# decode shapes (K split into one-super-block slices), ragged row counts that
+# end inside a 64-row workgroup and a 16-row wave, one super-block (no split)
 SHAPES = [(10240, 2560), (2560, 10240), (2560, 2048), (2048, 2560), (1024, 2560), (100, 512), (37, 256)]
 
 

@@ -19,8 +19,8 @@ def test_noalloc_rejects_oversize_and_bad_calls(rt):
     L = rt.lib()
     cap = L.rt_noalloc_scratch_bytes()
     assert cap == 8 << 20
-    # k = 2560: 5 K slices x 8 rows x 4 bytes = 160 bytes of partials per output row
-    n_big = cap // 160 + 1
+    # k = 2560: 10 K slices x 8 rows x 4 bytes = 320 bytes of partials per output row
+    n_big = cap // 320 + 1
     assert L.rt_q4k_gemv_batch_noalloc(addr, addr, addr, 2, n_big, 2560, None) == rt.RT_EINVAL
     assert "workspace" in L.rt_last_error().decode()
     assert L.rt_q4k_gemv_batch_noalloc(addr, addr, addr, 9, 64, 256, None) == rt.RT_EINVAL
