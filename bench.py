@@ -123,6 +123,9 @@ def main() -> int:
     ap.add_argument("--decode-profile", action="store_true",
                     help="only run the config-3 decode step (a 256 MiB copy first, as the counter calibration), "
                          "--warmup then --steps tokens; meant to run under rocprofv3")
+    ap.add_argument("--prefill-profile", action="store_true",
+                    help="only run the 4096-token GPU prefill of the config-3 context, --warmup then --steps "
+                         "times; meant to run under rocprofv3")
     ap.add_argument("--verify-rows", type=int, default=0,
                     help="with --decode-profile: run decode_step_batch calls of this many rows (1..8) instead "
                          "of single-token steps")
@@ -169,6 +172,19 @@ def main() -> int:
         layers.append(w)
     embed = (torch.randn(V * H, device=dev, generator=gen) * 0.02).to(torch.bfloat16).view(torch.int16)
     final_norm = torch.randn(H, device=dev, generator=gen) * 0.1
+    if args.prefill_profile:
+        d, pos = build_decode(rt, torch, dev, gen, layers, embed, final_norm, args)
+        toks = [(7 * i + 3) % V for i in range(pos)]
+        for _ in range(args.warmup):
+            d.prefill(toks, 0, 0)
+        t1 = time.perf_counter()
+        for _ in range(args.steps):
+            d.prefill(toks, 0, 0)
+        dt = (time.perf_counter() - t1) / args.steps
+        print(json.dumps({"prefill_profile": "done", "tokens": pos, "steps": args.steps,
+                          "ms_per_prefill": round(dt * 1e3, 3)}))
+        d.close()
+        return 0
     if args.decode_profile:
         a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
         b = torch.empty_like(a)

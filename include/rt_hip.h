@@ -237,7 +237,9 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out);
 rt_status rt_decode_destroy(rt_decode *d);
 /* device_ptrs = 0: host pointers, copied (Q4_K bytes verbatim, 144-B blocks
  * stay packed; upload_linear_detect_type, metal_decode.rs:1259-1277).
- * device_ptrs = 1: device pointers, borrowed; the caller keeps them alive. */
+ * device_ptrs = 1: device pointers, borrowed; the caller keeps them alive
+ * and unchanged until the layer is set again (the prefill GEMM's per-row
+ * exponents of each Q4_K weight are computed here, once: 4 bytes per row). */
 rt_status rt_decode_set_layer(rt_decode *d, int32_t layer, const rt_gemma3_layer *w, int32_t device_ptrs);
 /* Same, with the format of each projection in the order q, k, v, o, gate,
  * up, down: RT_LINEAR_Q4K, RT_LINEAR_Q6K, RT_LINEAR_Q8_0 or RT_LINEAR_BF16
@@ -294,7 +296,8 @@ rt_status rt_decode_synchronize(rt_decode *d);
 rt_status rt_decode_set_graph(rt_decode *d, int32_t enabled);
 /* print_metal_memory (metal_decode.rs:1285-1354): device bytes of a context by
  * what they hold.  weights counts uploads and device-pointer bindings alike
- * (projections, norms, embedding / tied lm_head); prefill is the chunk
+ * (projections and their GEMM row exponents, norms, embedding / tied
+ * lm_head); prefill is the chunk
  * scratch, 0 until the first rt_decode_prefill. */
 typedef struct {
   uint64_t weights, kv_cache, activation, batch, prefill, total;

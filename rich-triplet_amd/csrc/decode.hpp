@@ -39,6 +39,7 @@ struct LayerArgs {
   int window;              // sliding window in keys, 0 = global layer
   int global;              // 1: global layer (RoPE theta_global; never windowed)
   int fmt[7];              // RT_LINEAR_* of q, k, v, o, gate, up, down (Q4K for the fused kernels)
+  const int *ew[7];        // Q4_K projections: the GEMM's row exponents of the weight, [rows] (else null)
 };
 enum Proj { kProjQ, kProjK, kProjV, kProjO, kProjGate, kProjUp, kProjDown };
 

@@ -17,6 +17,7 @@
 #include "../../include/rt_hip.h"
 #include "decode.hpp"
 #include "rt_capi_util.hpp"
+#include "rt_kernels.hpp"
 
 using namespace rt;
 
@@ -357,6 +358,25 @@ rt_status rt_decode_set_layer_formats(rt_decode *d, int32_t layer, const rt_gemm
   B(g_q, w->q_norm, D * 4, const float *);
   B(g_k, w->k_norm, D * 4, const float *);
 #undef B
+  // The prefill GEMM's row exponents of each Q4_K weight, computed once here
+  // (a weight bound to the context must not change until it is bound again).
+  {
+    const int rows[7] = {(int)QD, (int)KVD, (int)KVD, (int)H, (int)F, (int)F, (int)H};
+    const int cols[7] = {(int)H, (int)H, (int)H, (int)QD, (int)H, (int)H, (int)F};
+    const uint8_t *wp[7] = {L.wq, L.wk, L.wv, L.wo, L.wgate, L.wup, L.wdown};
+    for (int i = 0; i < 7; ++i) {
+      L.ew[i] = nullptr;
+      if (st != RT_OK || formats[i] != RT_LINEAR_Q4K) continue;
+      void *q = nullptr;
+      st = dalloc(d, (size_t)rows[i] * 4, &q, rt_decode::kWeights);
+      if (st != RT_OK) break;
+      own.push_back(q);
+      hipError_t e = launch_q4k_row_exponents(wp[i], rows[i], cols[i], static_cast<int *>(q), d->stream);
+      if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
+      if (e != hipSuccess) st = hip_error(e, "rt_decode_set_layer: weight row exponents");
+      L.ew[i] = static_cast<const int *>(q);
+    }
+  }
   if (st != RT_OK) {
     for (void *q : own) dfree(d, q);
     return unset(st);

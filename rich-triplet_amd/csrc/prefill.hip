@@ -623,7 +623,7 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
   float *xn_f32 = plan.mb ? b.xn : nullptr;
   // (plan.mb requires every projection in Q4_K; other formats take their own GEMM)
   auto proj = [&](const float *A, int K, std::initializer_list<int> fmts, std::initializer_list<MbMat> mats,
-                  std::initializer_list<RowsIn *> views) {
+                  std::initializer_list<RowsIn *> views, std::initializer_list<const int *> ews) {
     if (plan.mb) {
       RowsIn out[3];
       hipError_t r = launch_q4k_gemv_mb(mats.begin(), (int)mats.size(), n, K, b.mb_stage, b.mb_part, st, out);
@@ -658,7 +658,7 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
         reg += q4k_gemm_prepped_ws_bytes(n, m.n, K);
         *views.begin()[i++] = rows_plain(m.y, m.n);
       }
-      return launch_q4k_gemm_multi_prepped(a16, ea, i, w, c, nn, ew, n, K, st);
+      return launch_q4k_gemm_multi_prepped(a16, ea, i, w, c, nn, ew, n, K, st, ews.begin());
     }
     // each matrix in its own region; a split Q4_K GEMM leaves its partials
     // there and the consumer adds them while reading (views)
@@ -668,7 +668,7 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
       RowsIn &v = *views.begin()[i++];
       if (fmt == RT_LINEAR_Q4K) {
         GemmLeft left{};
-        r = launch_q4k_gemm_prepped(a16, ea, m.w, m.y, n, m.n, K, rest, st, &left);
+        r = launch_q4k_gemm_prepped(a16, ea, m.w, m.y, n, m.n, K, rest, st, &left, ews.begin()[i - 1]);
         v = left.ks > 1 ? RowsIn{left.part, left.ks, (size_t)n * m.n, m.n, 0} : rows_plain(m.y, m.n);
         rest += q4k_gemm_prepped_ws_bytes(n, m.n, K);
       } else {
@@ -689,7 +689,7 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
                                    stage, a16_h, ea_h));
     PF_TRY(proj(plan.mb ? b.xn : nullptr, H, {L.fmt[kProjQ], L.fmt[kProjK], L.fmt[kProjV]},
                 {MbMat{L.wq, b.q, QD, 0, 0}, MbMat{L.wk, b.k, KVD, 0, 0}, MbMat{L.wv, b.v, KVD, 0, 0}},
-                {&vq, &vk, &vv}));
+                {&vq, &vk, &vv}, {L.ew[kProjQ], L.ew[kProjK], L.ew[kProjV]}));
     const int items = n * (nq + nkv);
     const int cs_off = L.global ? D : 0;
     if (D == 256)
@@ -723,11 +723,12 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
     if (stage && !pa.split_stages) return hipErrorInvalidValue;  // the batched path stages in the merge kernel
     if (D == 256) PF_TRY(launch_pf_attn<256>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa, stage));
     else PF_TRY(launch_pf_attn<128>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa, stage));
-    PF_TRY(proj(b.attn, QD, {L.fmt[kProjO]}, {MbMat{L.wo, b.o, H, 0, 0}}, {&vo}));
+    PF_TRY(proj(b.attn, QD, {L.fmt[kProjO]}, {MbMat{L.wo, b.o, H, 0, 0}}, {&vo}, {L.ew[kProjO]}));
     PF_TRY(launch_pf_norm<true>(n, st, b.hid, vo, L.g_post_attn, L.g_pre_ffn, b.x2, xn_f32, H, a.eps, stage, a16_h,
                                 ea_h));
     PF_TRY(proj(plan.mb ? b.xn : nullptr, H, {L.fmt[kProjGate], L.fmt[kProjUp]},
-                {MbMat{L.wgate, b.g, F, 0, 0}, MbMat{L.wup, b.u, F, 0, 0}}, {&vg, &vu}));
+                {MbMat{L.wgate, b.g, F, 0, 0}, MbMat{L.wup, b.u, F, 0, 0}}, {&vg, &vu},
+                {L.ew[kProjGate], L.ew[kProjUp]}));
     if (plan.mb) {
       const size_t n4 = (size_t)n * F / 4;
       const unsigned eg = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
@@ -735,7 +736,8 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
     } else {
       PF_CHECK(hipLaunchKernelGGL(k_pf_gelu_rows, dim3(n), dim3(kGeluRowT), 0, st, vg, vu, F, gemm_a16(F), gemm_ea(F)));
     }
-    PF_TRY(proj(plan.mb ? b.g : nullptr, F, {L.fmt[kProjDown]}, {MbMat{L.wdown, b.dn, H, 0, 0}}, {&vd}));
+    PF_TRY(proj(plan.mb ? b.g : nullptr, F, {L.fmt[kProjDown]}, {MbMat{L.wdown, b.dn, H, 0, 0}}, {&vd},
+                {L.ew[kProjDown]}));
     if (li + 1 < s.n_layers)
       PF_TRY(launch_pf_norm<true>(n, st, b.x2, vd, L.g_post_ffn, layers[li + 1].g_in, b.hid, xn_f32, H, a.eps,
                                   stage, a16_h, ea_h));

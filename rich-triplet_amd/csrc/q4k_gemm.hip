@@ -678,18 +678,26 @@ size_t q4k_gemm_prepped_ws_bytes(int M, int N, int K) {
   return q4k_gemm_workspace_bytes(M, N, K) - r256((size_t)M * K * 2) - r256((size_t)M * 4);
 }
 
+hipError_t launch_q4k_row_exponents(const void *w, int N, int K, int *ew, hipStream_t s) {
+  // W rows only (no A rows: M = 0 in the prep's indexing)
+  hipLaunchKernelGGL((k_gemm_prep<float>), dim3((N + 3) / 4), dim3(256), 0, s, nullptr, nullptr, nullptr,
+                     static_cast<const uint8_t *>(w), ew, 0, N, K);
+  return hipGetLastError();
+}
+
 hipError_t launch_q4k_gemm_prepped(const _Float16 *a16, const int *ea, const void *w, float *c, int M, int N, int K,
-                                   void *ws, hipStream_t s, GemmLeft *left) {
+                                   void *ws, hipStream_t s, GemmLeft *left, const int *ew_pre) {
   auto r256 = [](size_t b) { return (b + 255) & ~size_t(255); };
   char *p = static_cast<char *>(ws);
-  int *ew = reinterpret_cast<int *>(p);
   float *part = reinterpret_cast<float *>(p + r256((size_t)N * 4));
   const uint8_t *wb = static_cast<const uint8_t *>(w);
-  // W row exponents only (no A rows: M = 0 in the prep's indexing)
-  hipLaunchKernelGGL((k_gemm_prep<float>), dim3((N + 3) / 4), dim3(256), 0, s, nullptr, nullptr, nullptr, wb, ew, 0,
-                     N, K);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  const int *ew = ew_pre;
+  if (!ew) {
+    int *ewp = reinterpret_cast<int *>(p);
+    hipError_t e = launch_q4k_row_exponents(wb, N, K, ewp, s);
+    if (e != hipSuccess) return e;
+    ew = ewp;
+  }
   return q4k_gemm_core(a16, ea, wb, ew, part, c, M, N, K, s, left);
 }
 
@@ -697,14 +705,18 @@ bool q4k_gemm_multi_ok(int M, int count) { return M > 1024 && count >= 1 && coun
 
 hipError_t launch_q4k_gemm_multi_prepped(const _Float16 *a16, const int *ea, int count, const void *const *w,
                                          float *const *c, const int *n, void *const *ws, int M, int K,
-                                         hipStream_t s) {
+                                         hipStream_t s, const int *const *ew_pre) {
   if (!q4k_gemm_multi_ok(M, count) || K % 256 != 0) return hipErrorInvalidValue;
   HMats mats{};
   int tiles_n = 0, rows = 0;
+  bool all_pre = ew_pre != nullptr;
   for (int i = 0; i < count; ++i) {
     if (n[i] <= 0) return hipErrorInvalidValue;
+    all_pre = all_pre && ew_pre[i];
+  }
+  for (int i = 0; i < count; ++i) {
     mats.w[i] = static_cast<const uint8_t *>(w[i]);
-    mats.ew[i] = static_cast<const int *>(ws[i]);
+    mats.ew[i] = all_pre ? ew_pre[i] : static_cast<const int *>(ws[i]);
     mats.c[i] = c[i];
     mats.n[i] = n[i];
     mats.tn0[i] = tiles_n;
@@ -712,9 +724,11 @@ hipError_t launch_q4k_gemm_multi_prepped(const _Float16 *a16, const int *ea, int
     rows += n[i];
   }
   mats.count = count;
-  hipLaunchKernelGGL(k_gemm_prep_w_multi, dim3((rows + 3) / 4), dim3(256), 0, s, mats, K);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (!all_pre) {
+    hipLaunchKernelGGL(k_gemm_prep_w_multi, dim3((rows + 3) / 4), dim3(256), 0, s, mats, K);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   const int tiles_m = (M + 127) / 128;
   hipLaunchKernelGGL(k_q4k_gemm_h, dim3(tiles_m * tiles_n), dim3(256), 0, s, a16, ea, mats, M, K, tiles_m, tiles_n,
                      1);

@@ -57,15 +57,22 @@ struct GemmLeft {
   const float *part;
   int ks;
 };
+// ew_pre: the weight's row exponents from launch_q4k_row_exponents, kept
+// with the weight (null: computed into ws by this call).
 hipError_t launch_q4k_gemm_prepped(const _Float16 *a16, const int *ea, const void *w, float *c, int M, int N, int K,
-                                   void *ws, hipStream_t s, GemmLeft *left = nullptr);
+                                   void *ws, hipStream_t s, GemmLeft *left = nullptr, const int *ew_pre = nullptr);
 // Up to three Q4_K matrices sharing a prepared A (q|k|v, gate|up) in one
 // matrix-core launch, for M > 1024 (q4k_gemm_multi_ok); ws[i] holds at least
-// n[i]*4 bytes (matrix i's row exponents); no K split.
+// n[i]*4 bytes (matrix i's row exponents, unless ew_pre[i] gives them); no K
+// split.
 bool q4k_gemm_multi_ok(int M, int count);
 hipError_t launch_q4k_gemm_multi_prepped(const _Float16 *a16, const int *ea, int count, const void *const *w,
                                          float *const *c, const int *n, void *const *ws, int M, int K,
-                                         hipStream_t s);
+                                         hipStream_t s, const int *const *ew_pre = nullptr);
+// The GEMM's power-of-two row exponents of a Q4_K weight [N][K] (from its
+// block headers) into ew[N]: they depend on the weight alone, so a caller
+// that keeps the weight can compute them once.
+hipError_t launch_q4k_row_exponents(const void *w, int N, int K, int *ew, hipStream_t s);
 // Workspace bytes of the two prepped calls.
 size_t q4k_gemm_prepped_ws_bytes(int M, int N, int K);
 size_t proj_gemm_prepped_ws_bytes(int M, int N, int K);

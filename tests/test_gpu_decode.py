@@ -349,7 +349,9 @@ def test_memory_report(rt, orc):
     H, F, D = cfg["hidden"], cfg["ffn"], cfg["head_dim"]
     QD, KVD = cfg["n_q_heads"] * D, cfg["n_kv_heads"] * D
     proj = sum(r * (c // 256) * 144 for r, c in ((QD, H), (KVD, H), (KVD, H), (H, QD), (F, H), (F, H), (H, F)))
-    weights = cfg["n_layers"] * (proj + (4 * H + 2 * D) * 4) + cfg["vocab"] * H * 2 + H * 4
+    # per Q4_K projection also its GEMM row exponents (4 bytes per output row)
+    exps = (QD + 2 * KVD + H + 2 * F + H) * 4
+    weights = cfg["n_layers"] * (proj + exps + (4 * H + 2 * D) * 4) + cfg["vocab"] * H * 2 + H * 4
     kv = cfg["n_layers"] * 2 * max_seq * KVD * 4
     d = build_ctx(rt, cfg, layers, embed, fnorm, pos, max_seq)
     m = d.memory()
