@@ -646,8 +646,10 @@ static rt_status prefill_reserve(rt_decode *d, int cap) {
   if ((st = get(rows_mb_stage_bytes(d->shape), &b.mb_stage)) != RT_OK) return st;
   if ((st = get(rows_mb_part_bytes(d->shape), &p)) != RT_OK) return st;
   b.mb_part = static_cast<float *>(p);
-  // key-split partials for chunks of up to 64 rows (one attention row block)
-  const int split_rows = std::min(cap, 64);
+  // key-split partials: 64 splits of 128 rows (two splits of a 4096-row
+  // chunk's causal attention, eight of a 1024-row window; more splits
+  // measured slower: the walk is bound by the K/V stage reads in aggregate)
+  const int split_rows = std::min(cap, 128);
   if ((st = get(attn_part_floats(d->shape, split_rows, false) * 4, &p)) != RT_OK) return st;
   b.attn_ml = static_cast<float *>(p);
   if ((st = get(attn_part_floats(d->shape, split_rows, true) * 4, &p)) != RT_OK) return st;

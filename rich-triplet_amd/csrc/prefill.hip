@@ -266,8 +266,11 @@ struct PfAttnArgs {
   // [z*split_stages, (z+1)*split_stages) of its key range and writes the
   // unnormalised (max, sum, O) of each column for k_pf_attn_combine.
   int split_stages;   // 0: no split, the kernel writes the output itself
-  float *part_ml;     // [splits][n*n_q_heads][2]
-  float *part_o;      // [splits][n*n_q_heads][D]
+  float *part_ml;     // [splits][(n - row_base)*n_q_heads][2]
+  float *part_o;      // [splits][(n - row_base)*n_q_heads][D]
+  // Rows [row_base, n) are computed (rows below see no key and are zeroed by
+  // the combine).
+  int row_base = 0;
 };
 
 template <int D>
@@ -324,12 +327,23 @@ __global__ __launch_bounds__(64 * W) void k_pf_attn(const float *__restrict__ q,
   using S = PfAttnSmem<D>;
   __shared__ __attribute__((aligned(16))) S sm;
 
-  const int b = (int)(gridDim.x - 1 - blockIdx.x);  // late rows (the longest key ranges) first
-  const int kvh = (int)blockIdx.y;
   const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63), n16 = lane & 15, g = lane >> 4;
   const size_t qd = (size_t)p.n_kv_heads * G * D, kvd = (size_t)p.n_kv_heads * D;
-  const int col0 = b * NC;
   const int last_row = p.n - 1;
+  const int nb = ((p.n - p.row_base) * G + NC - 1) / NC;  // row blocks of the launch
+  // Workgroups are dealt to the eight XCDs in turn (linear id mod 8).  When
+  // the KV heads divide the XCDs and the grid is whole rounds of them, the
+  // workgroups of one XCD all take the same KV head, so its L2 holds one
+  // head's K/V stages for every row block walking them.
+  int kvh = (int)blockIdx.y, bx = (int)blockIdx.x;
+  if (8 % p.n_kv_heads == 0 && ((int)gridDim.x * p.n_kv_heads) % 8 == 0) {
+    const int lin = (int)(blockIdx.x + blockIdx.y * gridDim.x), xcd = lin & 7, slot = lin >> 3;
+    const int per = 8 / p.n_kv_heads;  // XCDs per KV head
+    kvh = xcd / per;
+    bx = slot * per + xcd % per;
+  }
+  const int b = nb - 1 - bx;  // late rows (the longest key ranges) first
+  const int col0 = p.row_base * G + b * NC;
   const int key_first = pf_key_lo(p, p.p0 + col0 / G) & ~(KB - 1);
   const int key_last = p.p0 + min(last_row, (col0 + NC - 1) / G);
   const int wt0 = (col0 + 16 * wave) / G;
@@ -470,7 +484,9 @@ __global__ __launch_bounds__(64 * W) void k_pf_attn(const float *__restrict__ q,
 
   if (col_ok && p.split_stages) {
     // partial of this key split (an empty split leaves max -inf, sum 0, O 0)
-    const size_t cidx = (size_t)blockIdx.z * p.n * p.n_kv_heads * G + (size_t)t * p.n_kv_heads * G + hq;
+    const int na = p.n - p.row_base;
+    const size_t cidx =
+        (size_t)blockIdx.z * na * p.n_kv_heads * G + (size_t)(t - p.row_base) * p.n_kv_heads * G + hq;
     if (g == 0) {
       p.part_ml[2 * cidx] = m_run;
       p.part_ml[2 * cidx + 1] = l_run;
@@ -492,14 +508,24 @@ __global__ __launch_bounds__(64 * W) void k_pf_attn(const float *__restrict__ q,
 // Merge of the key splits of every (row, head) column:
 //   out = sum_s O_s e^(m_s - M) / sum_s l_s e^(m_s - M),  M = max_s m_s
 // (0 for a column with no key at all, as the reference's empty rows).
+// Columns below col_base (rows that see no key) are written as zeros; the
+// partials hold the columns from col_base on.
 template <int D>
 __global__ __launch_bounds__(D) void k_pf_attn_combine(const float *__restrict__ part_ml,
                                                        const float *__restrict__ part_o, float *__restrict__ out,
-                                                       int ncols, int splits, int nq, int8_t *__restrict__ st_dig) {
+                                                       int ncols, int splits, int nq, int8_t *__restrict__ st_dig,
+                                                       int col_base) {
   static_assert(D >= kPfMaxSplits, "one lane of wave 0 per split");
   __shared__ float w_lds[kPfMaxSplits];
   __shared__ float l_lds;
-  const int col = (int)blockIdx.x, d = (int)threadIdx.x;
+  const int col_out = (int)blockIdx.x, d = (int)threadIdx.x;
+  if (col_out < col_base) {  // block-uniform
+    out[(size_t)col_out * D + d] = 0.f;
+    if (st_dig) mb_stage1(st_dig, mb_stats(st_dig, nq * D), col_out / nq, ((col_out % nq) * D + d) >> 6, 0.f);
+    return;
+  }
+  const int col = col_out - col_base;
+  ncols -= col_base;
   if (d < 64) {  // wave 0: split z = lane
     const bool live = d < splits;
     const float m = live ? part_ml[2 * ((size_t)d * ncols + col)] : -INFINITY;
@@ -516,9 +542,9 @@ __global__ __launch_bounds__(D) void k_pf_attn_combine(const float *__restrict__
   for (int z = 0; z < splits; ++z) O = fmaf(part_o[((size_t)z * ncols + col) * D + d], w_lds[z], O);
   const float L = l_lds;
   const float r = L > 0.f ? O / L : 0.f;
-  out[(size_t)col * D + d] = r;
+  out[(size_t)col_out * D + d] = r;
   if (st_dig) {  // element (col % nq)*D + d of row col / nq; one 64-element chunk per wave
-    const int t = col / nq, e = (col % nq) * D + d;
+    const int t = col_out / nq, e = (col_out % nq) * D + d;
     mb_stage1(st_dig, mb_stats(st_dig, nq * D), t, e >> 6, r);
   }
 }
@@ -535,23 +561,25 @@ hipError_t launch_pf_attn_w(int G, dim3 grid, hipStream_t st, const float *q, co
   return hipGetLastError();
 }
 
-// grid: (column blocks of 64, KV heads, key splits).  Without a key split and
-// from 256 columns on, workgroups of eight waves take 128 columns each, which
-// halves the K/V stage loads and bf16 splits per column.
+// grid: (column blocks of 64, KV heads, key splits).  From 256 columns on,
+// workgroups of eight waves take 128 columns each, which halves the K/V stage
+// loads and bf16 splits per column.
 template <int D>
 hipError_t launch_pf_attn(int G, dim3 grid, hipStream_t st, const float *q, const float *kc, const float *vc,
                           float *out, const PfAttnArgs &p, int8_t *st_dig) {
   hipError_t e;
-  if (!p.split_stages && p.n * G >= 256) {
-    grid.x = (unsigned)((p.n * G + 127) / 128);
+  const int na = p.n - p.row_base;
+  if (na * G >= 256) {
+    grid.x = (unsigned)((na * G + 127) / 128);
     e = launch_pf_attn_w<D, 8>(G, grid, st, q, kc, vc, out, p);
   } else {
+    grid.x = (unsigned)((na * G + 63) / 64);
     e = launch_pf_attn_w<D, 4>(G, grid, st, q, kc, vc, out, p);
   }
   if (e != hipSuccess || !p.split_stages) return e;
   const int ncols = p.n * p.n_kv_heads * G;
   hipLaunchKernelGGL((k_pf_attn_combine<D>), dim3(ncols), dim3(D), 0, st, p.part_ml, p.part_o, out, ncols,
-                     (int)grid.z, p.n_kv_heads * G, st_dig);
+                     (int)grid.z, p.n_kv_heads * G, st_dig, p.row_base * p.n_kv_heads * G);
   return hipGetLastError();
 }
 
@@ -711,15 +739,44 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
     pa.split_stages = 0;
     pa.part_ml = b.attn_ml;
     pa.part_o = b.attn_o;
-    dim3 agrid((n * G + 63) / 64, nkv);
+    // Rows before a fixed window start (the reference's prefill rule) see no
+    // key: a key-split launch covers the rows from it on and its merge zeroes
+    // the rest (row_base returns to 0 below when the keys are not split).
+    if (!L.global && plan.lo_fixed > 0 && !plan.p0_dev && b.attn_ml)
+      pa.row_base = std::min(std::max(plan.lo_fixed - plan.p0, 0), n - 1);
+    int na = n - pa.row_base;
+    dim3 agrid((na * G + 63) / 64, nkv);
+    const bool causal = L.global || (plan.window <= 0 && plan.lo_fixed <= 0);
     if (agrid.x == 1 && b.attn_ml && n <= b.attn_rows) {
       // one row block: split the keys so about 256 workgroups share them
-      const int span = L.global || (plan.window <= 0 && plan.lo_fixed <= 0) ? plan.max_pos
-                       : std::min(plan.max_pos, (plan.window > 0 ? plan.window : plan.max_pos) + n + 32);
+      const int span = causal ? plan.max_pos
+                              : std::min(plan.max_pos, (plan.window > 0 ? plan.window : plan.max_pos) + n + 32);
       const int stages = (span + 31) / 32 + 1;
       pa.split_stages = (stages + kPfMaxSplits - 1) / kPfMaxSplits;
       agrid.z = (stages + pa.split_stages - 1) / pa.split_stages;
+    } else if (!stage) {
+      // Several row blocks with unequal key ranges (causal rows, the reference
+      // window rule) or too few workgroups for the CUs (a short prompt): split
+      // the keys as far as the partial buffers allow, so no workgroup walks
+      // many more key stages than the average.
+      const int splits_max = b.attn_ml ? std::min(kPfMaxSplits, b.attn_rows * kPfMaxSplits / na) : 0;
+      const int span = causal ? plan.max_pos
+                       : plan.window > 0 ? std::min(plan.max_pos, plan.window + 96)
+                                         : std::max(plan.max_pos - plan.lo_fixed, 1);
+      const int stages = (span + 31) / 32 + 1;
+      // Causal rows: the last row block walks every key, the first one stage.
+      if (splits_max >= 2 && (causal || plan.lo_fixed > 0 || (int)(agrid.x * agrid.y) < 512)) {
+        pa.split_stages = std::max(4, (stages + splits_max - 1) / splits_max);
+        agrid.z = (stages + pa.split_stages - 1) / pa.split_stages;
+        if (agrid.z < 2) pa.split_stages = 0, agrid.z = 1;
+      }
+      if (!pa.split_stages) {
+        pa.row_base = 0;  // the kernel writes the zero rows itself
+        na = n;
+        agrid.x = (na * G + 63) / 64;
+      }
     }
+    if (agrid.x == 1 || stage) pa.row_base = pa.split_stages ? pa.row_base : 0;
     if (stage && !pa.split_stages) return hipErrorInvalidValue;  // the batched path stages in the merge kernel
     if (D == 256) PF_TRY(launch_pf_attn<256>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa, stage));
     else PF_TRY(launch_pf_attn<128>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa, stage));
