@@ -55,8 +55,15 @@ struct DecodeArgs {
   int vocab, n_q_heads, n_kv_heads, head_dim;
 };
 
+// Shapes of the fused single-token kernels (templated on the Gemma-3-4B and
+// test widths) ...
 bool decode_shape_supported(const DecodeShape &s, const char **why);
 bool decode_rows_divisible(const DecodeShape &s, const char **why);
+// ... and the wider set the rows kernels serve (every projection Q4_K).
+bool decode_shape_generic(const DecodeShape &s, const char **why);
+constexpr int kLmHeadMaxHidden = 4096;
+// Allows the batched lm_head's LDS for `hidden` (once per process and width).
+hipError_t prepare_lm_head_batch(int hidden);
 hipError_t enqueue_decode_step(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers, hipStream_t stream);
 // Final residual, final norm and lm_head of the token whose last-layer x2
 // and down-projection output sit in a.x2 / a.dn; logits into a.logits.

@@ -55,6 +55,7 @@ struct rt_decode {
   PrefillBuffers pf;                     // rt_decode_prefill scratch (grown on demand)
   PrefillBuffers vb;                     // decode_step_batch rows (kMaxBatch), allocated at create
   bool all_q4k = true;                   // every projection Q4_K: batched-GEMV verify path
+  bool fused = true;                     // the fused single-token kernels serve this shape (else the rows path)
   int pf_chunk = 4096;                   // rows per prefill chunk (~180 KB of scratch per row at Gemma-3-4B)
   std::vector<void *> pf_owned;
   int *pf_tokens_host = nullptr;         // pinned staging: [pf.cap] tokens, [pf.cap][2][head_dim] cos/sin
@@ -117,10 +118,17 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
   s.head_dim = c.head_dim;
   s.n_layers = c.n_layers;
   s.vocab = c.vocab;
-  const char *why = "";
-  if (c.hidden <= 0 || c.ffn <= 0 || c.n_q_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0 ||
-      !decode_shape_supported(s, &why) || !decode_rows_divisible(s, &why))
-    return set_error(RT_EINVAL, "rt_decode_create: unsupported shape: %s", why);
+  const char *why = "", *why_generic = "";
+  if (c.hidden <= 0 || c.ffn <= 0 || c.n_q_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0)
+    return set_error(RT_EINVAL, "rt_decode_create: hidden, ffn, heads and head_dim must be positive");
+  // The fused single-token kernels where their templates cover the shape,
+  // else every step through the rows kernels (projections in Q4_K only).
+  const bool fused = decode_shape_supported(s, &why) && decode_rows_divisible(s, &why);
+  if (!fused && !decode_shape_generic(s, &why_generic))
+    return set_error(RT_EINVAL, "rt_decode_create: unsupported shape: %s (fused kernels), %s (rows kernels)", why,
+                     why_generic);
+  if (hipError_t pe = prepare_lm_head_batch(c.hidden); pe != hipSuccess)
+    return hip_error(pe, "rt_decode_create: batched lm_head");
   const int window = c.sliding_window;
   const int local_span = window > 0 ? std::min(window, c.max_seq) : c.max_seq;
   constexpr int kLocalKeys = kAttnChunkKeys * kAttnSubLocal, kGlobalKeys = kAttnChunkKeys * kAttnSubGlobal;
@@ -132,6 +140,7 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
   rt_decode *d = new rt_decode();
   d->cfg = c;
   d->shape = s;
+  d->fused = fused;
   hipError_t e = hipGetDevice(&d->device);
   rt_status st = RT_OK;
 #define TRY(x)                  \
@@ -316,10 +325,15 @@ rt_status rt_decode_set_layer_formats(rt_decode *d, int32_t layer, const rt_gemm
     const size_t H = c.hidden, F = c.ffn, QD = (size_t)c.n_q_heads * c.head_dim, KVD = (size_t)c.n_kv_heads * c.head_dim;
     const size_t shape[7][2] = {{QD, H}, {KVD, H}, {KVD, H}, {H, QD}, {F, H}, {F, H}, {H, F}};
     static const char *names[7] = {"q", "k", "v", "o", "gate", "up", "down"};
-    for (int p = 0; p < 7; ++p)
+    for (int p = 0; p < 7; ++p) {
       if (!proj_bytes(formats[p], shape[p][0], shape[p][1]))
         return unset(set_error(RT_EINVAL, "rt_decode_set_layer: projection %s has unsupported format %d", names[p],
                                formats[p]));
+      if (!d->fused && formats[p] != RT_LINEAR_Q4K)
+        return unset(set_error(RT_EINVAL,
+                               "rt_decode_set_layer: projection %s: this shape runs on the rows kernels, which take "
+                               "Q4_K projections only (format %d)", names[p], formats[p]));
+    }
   }
   // Every pointer is checked before anything is freed or uploaded; the new
   // binding is built aside and replaces the old one only when it is whole.
@@ -496,6 +510,24 @@ static rt_status params_send(rt_decode *d, int slots) {
   return RT_OK;
 }
 
+// m rows (m <= kMaxBatch) at the positions and tokens of the step parameter
+// slots, each attending its own window as a decode step does, projections
+// on the batched GEMV (every projection Q4_K).
+static RowsPlan rows_plan_params(rt_decode *d, int m) {
+  const int slot = param_slot_floats(d->cfg.head_dim);
+  RowsPlan plan;
+  plan.n = m;
+  plan.p0_dev = d->params_dev + 1;
+  plan.tokens = d->params_dev;
+  plan.tok_stride = slot;
+  plan.cs = reinterpret_cast<const float *>(d->params_dev) + kParamRopeLocal;
+  plan.cs_stride = slot;
+  plan.window = d->cfg.sliding_window;
+  plan.max_pos = d->cfg.max_seq;
+  plan.mb = true;
+  return plan;
+}
+
 // Launch `enqueue` through a graph captured on first use (or eagerly when
 // graphs are off).
 extern "C++" template <class F>
@@ -530,6 +562,12 @@ rt_status rt_decode_step_async(rt_decode *d, int32_t token, int32_t position) {
   if (st != RT_OK) return st;
   fill_slot(d, 0, token, position);
   if ((st = params_send(d, 1)) != RT_OK) return st;
+  if (!d->fused)  // one row through the rows kernels: batched GEMVs, row attention, lm_head
+    return run_graph(d, d->exec, [&] {
+      RowsPlan plan = rows_plan_params(d, 1);
+      plan.logits = RowsPlan::kLastRow;
+      return enqueue_rows(d->shape, d->args, d->layers.data(), d->vb, plan, d->stream);
+    }, "rt_decode_step");
   return run_graph(d, d->exec, [&] { return enqueue_decode_step(d->shape, d->args, d->layers.data(), d->stream); },
                    "rt_decode_step");
 }
@@ -554,17 +592,7 @@ rt_status rt_decode_step_batch_async(rt_decode *d, const int32_t *tokens, int32_
       return enqueue_decode_batch(d->shape, d->args, d->layers.data(), m, d->xn_batch, d->logits_batch, d->stream);
     // all rows through each layer at once: batched GEMVs (one pass over the
     // weights), the causal row attention, a batched lm_head
-    const int slot = param_slot_floats(d->cfg.head_dim);
-    RowsPlan plan;
-    plan.n = m;
-    plan.p0_dev = d->params_dev + 1;
-    plan.tokens = d->params_dev;
-    plan.tok_stride = slot;
-    plan.cs = reinterpret_cast<const float *>(d->params_dev) + kParamRopeLocal;
-    plan.cs_stride = slot;
-    plan.window = d->cfg.sliding_window;  // every row attends its own window, as a decode step does
-    plan.max_pos = d->cfg.max_seq;
-    plan.mb = true;
+    RowsPlan plan = rows_plan_params(d, m);
     plan.logits = RowsPlan::kEveryRow;
     plan.xn_b = d->xn_batch;
     plan.logits_b = d->logits_batch;

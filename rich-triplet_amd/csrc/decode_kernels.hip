@@ -578,11 +578,15 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-template <int K>
+// K (the hidden width, a multiple of 256) is a template constant for the
+// fused-kernel shapes and a run-time value (K = 0) otherwise; the staged A
+// takes K*32 bytes of dynamic LDS.
+template <int KC>
 __global__ __launch_bounds__(256) void k_lmhead_batch(const uint16_t *__restrict__ E, const float *__restrict__ xn,
-                                                      float *__restrict__ logits, int N, int M) {
-  constexpr int SEG = K / 32;
-  __shared__ __attribute__((aligned(16))) uint16_t xa[SEG * 16 * 32];
+                                                      float *__restrict__ logits, int N, int M, int Krt) {
+  const int K = KC ? KC : Krt;
+  const int SEG = K / 32;
+  extern __shared__ __attribute__((aligned(16))) uint16_t xa[];
   // stage: element e of vector v -> hi, lo bf16 at A rows 2v, 2v+1
 #pragma unroll 1
   for (int i = threadIdx.x; i < 8 * K; i += 256) {
@@ -823,15 +827,43 @@ hipError_t enqueue_decode_batch(const DecodeShape &s, const DecodeArgs &a, const
   return l.err == hipSuccess ? enqueue_lm_head_batch(s, a, xn, logits_b, m, stream) : l.err;
 }
 
+hipError_t prepare_lm_head_batch(int hidden) {
+  if (hidden % 256 != 0 || hidden > kLmHeadMaxHidden) return hipErrorInvalidValue;
+  const int bytes = hidden * 32;
+  if (hidden == 2560) return hipFuncSetAttribute((const void *)k_lmhead_batch<2560>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (hidden == 512) return hipSuccess;
+  return hipFuncSetAttribute((const void *)k_lmhead_batch<0>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+}
+
 hipError_t enqueue_lm_head_batch(const DecodeShape &s, const DecodeArgs &a, const float *xn, float *logits_b, int m,
                                  hipStream_t stream) {
   Launch l{stream};
+  const size_t lds = (size_t)s.hidden * 32;
   if (s.hidden == 2560)
-    hipLaunchKernelGGL((k_lmhead_batch<2560>), dim3(512), dim3(256), 0, l.s, a.embed, xn, logits_b, s.vocab, m);
+    hipLaunchKernelGGL((k_lmhead_batch<2560>), dim3(512), dim3(256), lds, l.s, a.embed, xn, logits_b, s.vocab, m, 0);
+  else if (s.hidden == 512)
+    hipLaunchKernelGGL((k_lmhead_batch<512>), dim3(512), dim3(256), lds, l.s, a.embed, xn, logits_b, s.vocab, m, 0);
   else
-    hipLaunchKernelGGL((k_lmhead_batch<512>), dim3(512), dim3(256), 0, l.s, a.embed, xn, logits_b, s.vocab, m);
+    hipLaunchKernelGGL((k_lmhead_batch<0>), dim3(512), dim3(256), lds, l.s, a.embed, xn, logits_b, s.vocab, m,
+                       s.hidden);
   l.check();
   return l.err;
+}
+
+// Shapes the rows kernels serve (every projection Q4_K): the decode step
+// then runs as a one-row pass of enqueue_rows.
+bool decode_shape_generic(const DecodeShape &s, const char **why) {
+  const int qd = s.n_q_heads * s.head_dim;
+  if (s.hidden % 256 != 0 || s.hidden > kLmHeadMaxHidden)
+    return *why = "hidden must be a multiple of 256 up to 4096", false;
+  if (qd % 256 != 0) return *why = "n_q_heads*head_dim must be a multiple of 256", false;
+  if (s.ffn % 256 != 0 || s.ffn > 16384) return *why = "ffn must be a multiple of 256 up to 16384", false;
+  if (s.head_dim != 128 && s.head_dim != 256) return *why = "head_dim must be 128 or 256", false;
+  if (s.n_kv_heads <= 0 || s.n_q_heads % s.n_kv_heads != 0) return *why = "n_q_heads must be a multiple of n_kv_heads", false;
+  const int g = s.n_q_heads / s.n_kv_heads;
+  if (g != 1 && g != 2 && g != 4) return *why = "GQA group must be 1, 2 or 4", false;
+  return true;
 }
 
 // Row-count divisibility the launches above rely on.

@@ -135,7 +135,7 @@ def test_decode_rejects_bad_calls(rt, orc):
         d.decode_step(0, 16)             # position beyond max_seq
     d.close()
     with pytest.raises(rt.RtError):
-        rt.HipDecodeContext(dict(cfg, hidden=768), 16)  # unsupported shape
+        rt.HipDecodeContext(dict(cfg, hidden=700), 16)  # unsupported shape (not whole Q4_K blocks)
 
 
 def test_gemma3_4b_shape_decode_step_matches_oracle(rt, orc, dev):
@@ -335,6 +335,73 @@ def test_failed_set_unsets_layer_and_embed(rt, orc):
     d.set_embed(embed, fnorm)
     assert np.array_equal(d.decode_step(9, pos), first)
     d.close()
+
+
+# ---------------------------------------------------------------------------
+# Shapes outside the fused kernels' templates: every step runs as a one-row
+# pass of the rows kernels (batched GEMV, row attention, batched lm_head).
+# ---------------------------------------------------------------------------
+def generic_cfg(**kw):
+    """hidden 768, 4 heads x 128 over 2 KV heads, ffn 1536: no fused template."""
+    base = dict(hidden=768, ffn=1536, n_q_heads=4, n_kv_heads=2, head_dim=128, attn_scale=1.0 / np.sqrt(128.0))
+    base.update(kw)
+    return tiny(2, **base)
+
+
+@pytest.mark.parametrize("pos", [0, 3, 20])
+def test_generic_shape_decode_step_matches_oracle(rt, orc, pos):
+    cfg = generic_cfg()
+    max_seq = 48
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=pos, seed=1500 + pos)
+    d = build_ctx(rt, cfg, layers, embed, fnorm, pos, max_seq)
+    got = d.decode_step(17, pos)
+    ref = orc.gemma3_decode_step(cfg, layers, embed, fnorm, token=17, pos=pos)
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, ref) < LOGITS_TOL, rel_l2(got, ref)
+    d.close()
+
+
+def test_generic_shape_steps_batch_and_graph(rt, orc):
+    """Consecutive steps replay one captured graph and append K/V rows as the
+    oracle does; a verify batch matches single steps; eager equals graph."""
+    import copy
+    cfg = generic_cfg(n_layers=3, global_every=3)
+    max_seq, ctx = 40, 5
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=ctx, seed=1600)
+    d = build_ctx(rt, cfg, layers, embed, fnorm, ctx, max_seq)
+    d_e = build_ctx(rt, cfg, layers, embed, fnorm, ctx, max_seq)
+    d_e.set_graph(False)
+    olayers = copy.deepcopy(layers)
+    for i, tok in enumerate([3, 999, 41, 7]):
+        got = d.decode_step(tok, ctx + i)
+        assert np.array_equal(got, d_e.decode_step(tok, ctx + i)), i
+        ref = orc.gemma3_decode_step(cfg, olayers, embed, fnorm, token=tok, pos=ctx + i)
+        assert rel_l2(got, ref) < LOGITS_TOL, i
+    kvd = cfg["n_kv_heads"] * cfg["head_dim"]
+    for li in range(cfg["n_layers"]):
+        kp, _ = d.kv_ptrs(li)
+        k = _read_dev(kp, (ctx + 4) * kvd * 4).view(np.float32).reshape(ctx + 4, kvd)
+        assert rel_l2(k[ctx:], olayers[li]["k_cache"][ctx:ctx + 4]) < 1e-3, li
+    toks = [5, 6, 7]
+    got = d.decode_step_batch(toks, ctx + 4)
+    seq = np.stack([d_e.decode_step(t, ctx + 4 + i) for i, t in enumerate(toks)])
+    for i in range(len(toks)):
+        assert rel_l2(got[i], seq[i]) < 2e-4, i
+    d.close()
+    d_e.close()
+
+
+def test_generic_shape_refusals(rt, orc):
+    """A non-Q4_K projection is refused on a rows-kernel shape; a shape that
+    neither kernel set serves is refused at create with both reasons."""
+    cfg = generic_cfg(n_layers=1, global_every=0)
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=16, ctx=0, seed=1700)
+    d = rt.HipDecodeContext(cfg, 16)
+    with pytest.raises(rt.RtError, match="Q4_K projections only"):
+        d.set_layer(0, layers[0], formats=[rt.LINEAR_Q4K] * 6 + [rt.LINEAR_BF16])
+    d.close()
+    with pytest.raises(rt.RtError, match="rows kernels"):
+        rt.HipDecodeContext(generic_cfg(hidden=5120), 16)
 
 
 def test_memory_report(rt, orc):

@@ -295,6 +295,35 @@ def test_gpu_prefill_matches_oracle(rt, orc, group, mode, T):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("T", [6, 77])
+def test_gpu_generic_shape_prefill_matches_oracle(rt, orc, mode, T):
+    """A shape outside the fused decode kernels (hidden 768, 4 heads x 128,
+    ffn 1536): prefill (batched GEMV at 6 rows, the GEMM at 77) and the
+    following decode step against the oracle."""
+    from test_gpu_decode import generic_cfg
+    import copy
+    cfg = generic_cfg()
+    max_seq = 96
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=0, seed=7000 + T + mode)
+    toks = [(13 * i + 5) % cfg["vocab"] for i in range(T)]
+    d = gpu_ctx(rt, cfg, layers, embed, fnorm, max_seq)
+    got = d.prefill(toks, 0, mode)
+    ref_layers = fresh_caches(layers)
+    ref = orc.gemma3_prefill(cfg, ref_layers, embed, fnorm, toks, 0, mode)
+    assert rel_l2(got, ref) < LOGITS_TOL, rel_l2(got, ref)
+    for li in range(cfg["n_layers"]):
+        k, v = read_kv(d, cfg, li, T)
+        assert rel_l2(k, ref_layers[li]["k_cache"][:T]) < KV_TOL
+        assert rel_l2(v, ref_layers[li]["v_cache"][:T]) < KV_TOL
+    if mode == 1:  # the step after a sliding-rule prefill sees the prefilled cache
+        step = d.decode_step(11, T)
+        rstep = orc.gemma3_decode_step(cfg, copy.deepcopy(ref_layers), embed, fnorm, token=11, pos=T)
+        assert rel_l2(step, rstep) < LOGITS_TOL
+    d.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", [0, 1])
 def test_gpu_long_prompt_prefill_matches_oracle(rt, orc, mode):
     """1100 rows: the projections run on the half-block GEMM with K split
     (the consumers add the partial tiles while reading them), attention on
