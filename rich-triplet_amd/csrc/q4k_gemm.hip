@@ -351,13 +351,15 @@ __global__ __launch_bounds__(512) void k_q4k_gemm_w8b(const _Float16 *__restrict
 // Half-block kernel: C tile 128 x 256, four waves side by side in N (wave
 // tile 128 x 64 = 4 x 2 tiles of v_mfma_f32_32x32x16_f16), two workgroups
 // per CU so one workgroup's barrier and LDS waits overlap the other's MFMAs.
-//   A (f16): one 64-wide chunk per copy (128 rows x 128 B), two LDS slots,
-//            one chunk ahead.  Row segments XOR-swizzled by (row >> 1) & 7.
-//   W (Q4_K): one half-block per copy (two chunks): for each of the 256
-//            columns the block header and the 64 qs bytes of those chunks,
-//            80 contiguous LDS bytes per column, two slots.  Five adjacent
-//            lanes read one column's bytes, so a copy instruction touches a
-//            few cache lines instead of one line per lane.
+//   A (f16): one 64-wide chunk per copy (128 rows x 128 B) by
+//            global_load_lds into a ring of four LDS slots, two chunks ahead.
+//            Row segments XOR-swizzled by (row >> 1) & 7.
+//   W (Q4_K): straight into VGPRs, also two chunks ahead.  A wave uses only
+//            its own 64 columns, so W has no reason to pass through LDS: per
+//            chunk a lane loads the 16 qs bytes of its column and k group
+//            (a ring of four register sets indexed by the chunk's place in
+//            its block; the loop over blocks is unrolled by four), and per
+//            block the 16-byte header.
 // Split-K as in the eight-wave kernel, by whole super-blocks: blockIdx.y = s
 // takes blocks [s*nblocks/ksplit, (s+1)*nblocks/ksplit).
 // Up to three matrices sharing A (q|k|v, gate|up) run as one launch: their
@@ -365,7 +367,6 @@ __global__ __launch_bounds__(512) void k_q4k_gemm_w8b(const _Float16 *__restrict
 // workgroup takes the matrix its column tile falls in.
 // ---------------------------------------------------------------------------
 constexpr int kHSlotA = 128 * 128;       // bytes
-constexpr int kHSlotW = 256 * 80;        // bytes
 
 struct HMats {
   const uint8_t *w[3];
@@ -387,8 +388,7 @@ __global__ __launch_bounds__(256) void k_gemm_prep_w_multi(HMats mats, int K) {
 __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restrict__ a16, const int *__restrict__ ea,
                                                        HMats mats, int M, int K, int tiles_m, int tiles_n,
                                                        int ksplit) {
-  __shared__ __attribute__((aligned(1024))) uint8_t sa0[kHSlotA], sa1[kHSlotA];
-  __shared__ __attribute__((aligned(1024))) uint8_t sw0[kHSlotW], sw1[kHSlotW];
+  __shared__ __attribute__((aligned(1024))) uint8_t sa0[kHSlotA], sa1[kHSlotA], sa2[kHSlotA], sa3[kHSlotA];
 
   const int tid = (int)threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -410,50 +410,52 @@ __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restric
   const size_t row_bytes = (size_t)nblocks * kQ4KBlockBytes;
   const int split = (int)blockIdx.y;
   const int b0 = split * nblocks / ksplit, b1 = (split + 1) * nblocks / ksplit;  // >= 1 block (host: ksplit <= nblocks)
+  const int klast = 4 * b1 - 1;                                                   // last chunk of this split
   if (ksplit > 1) c += (size_t)split * M * N;
 
+  // Addresses are a workgroup-uniform base (SGPRs) plus a 32-bit lane
+  // offset within the tile (at most 128 rows of A, 256 rows of W), which
+  // keeps one VGPR per stream.
   // A copy i (0..3) of this wave: rows 8*(4*wave+i) + [0,8); lane -> row
   // r = 8*(4*wave+i) + lane/8, physical segment lane%8, logical segment
   // (lane%8) ^ ((r >> 1) & 7).
-  const _Float16 *a_src[4];
+  const uint8_t *a_base = reinterpret_cast<const uint8_t *>(a16 + (size_t)m0 * K);
+  uint32_t a_off[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 8 * (4 * wave + i) + (lane >> 3);
-    a_src[i] = a16 + (size_t)min(m0 + r, M - 1) * K + 8 * ((lane & 7) ^ ((r >> 1) & 7));
+    a_off[i] = (uint32_t)((min(m0 + r, M - 1) - m0) * K + 8 * ((lane & 7) ^ ((r >> 1) & 7))) * 2u;
   }
-  // W copy i (0..4) of this wave: piece p = 64*(5*wave+i) + lane of the slot,
-  // column p/5, part p%5 (0 = header, 1..4 = qs bytes 16*(part-1) of the half).
-  const uint8_t *w_src[5];
-  int w_qs[5];
-#pragma unroll
-  for (int i = 0; i < 5; ++i) {
-    const int p = 64 * (5 * wave + i) + lane, col = p / 5, part = p - 5 * col;
-    w_src[i] = w + (size_t)min(n0 + col, N - 1) * row_bytes;
-    w_qs[i] = part == 0 ? 0 : 16 + 16 * (part - 1);  // plus 64 per half when part > 0
-  }
-
   auto issue_a = [&](int kc, uint8_t *slot) __attribute__((always_inline)) {
+    const uint8_t *base = a_base + (size_t)kc * (kBK * 2);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_global_load_lds((gvoid *)(a_src[i] + (size_t)kc * kBK), (lvoid *)(slot + (4 * wave + i) * 1024),
-                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds((gvoid *)(base + a_off[i]), (lvoid *)(slot + (4 * wave + i) * 1024), 16, 0, 0);
   };
-  auto issue_w = [&](int half, uint8_t *slot) __attribute__((always_inline)) {
-    const size_t boff = (size_t)(half >> 1) * kQ4KBlockBytes;
-    const int hoff = 64 * (half & 1);
-#pragma unroll
-    for (int i = 0; i < 5; ++i)
-      __builtin_amdgcn_global_load_lds((gvoid *)(w_src[i] + boff + w_qs[i] + (w_qs[i] ? hoff : 0)),
-                                       (lvoid *)(slot + (5 * wave + i) * 1024), 16, 0, 0);
-  };
-
-  int colw[2];
+  // W: column tile j (0, 1) of this wave, lane -> column colw[j], k group g
+  // -> qs bytes [16g, 16g+16) of each chunk's 32.
+  int colw[2], ewc[2];
   float bpw[2];
+  const uint8_t *w_base = w + (size_t)n0 * row_bytes;
+  uint32_t w_off[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     colw[j] = 64 * wave + 32 * j + l32;
-    bpw[j] = __builtin_amdgcn_ldexpf(g ? 0.0625f : 1.0f, -ew[min(n0 + colw[j], N - 1)]);
+    const int n = min(n0 + colw[j], N - 1);
+    ewc[j] = ew[n];
+    bpw[j] = __builtin_amdgcn_ldexpf(g ? 0.0625f : 1.0f, -ewc[j]);
+    w_off[j] = (uint32_t)(n - n0) * (uint32_t)row_bytes;
   }
+  auto load_qs = [&](int kc, u32x4 (&q)[2]) __attribute__((always_inline)) {
+    const uint8_t *base = w_base + (size_t)(kc >> 2) * kQ4KBlockBytes + 16 + 32 * (kc & 3);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) q[j] = *reinterpret_cast<const u32x4 *>(base + (w_off[j] + 16u * g));
+  };
+  auto load_hdr = [&](int blk, u32x4 (&h)[2]) __attribute__((always_inline)) {
+    const uint8_t *base = w_base + (size_t)blk * kQ4KBlockBytes;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) h[j] = *reinterpret_cast<const u32x4 *>(base + w_off[j]);
+  };
 
   floatx16 acc[4][2];
 #pragma unroll
@@ -461,29 +463,48 @@ __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restric
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = floatx16{};
 
-  issue_w(2 * b0, sw0);
+  // Loads issued per chunk k, in this order: qs of chunk k+2 (2), at the
+  // second chunk of a block the next block's headers (2), A copies of chunk
+  // k+2 (4).  Past the split's last chunk they repeat the last one, so every
+  // chunk issues the same count.  The prologue issues what chunks 4*b0-2 and
+  // 4*b0-1 would have.
+  u32x4 qs0[2], qs1[2], qs2[2], qs3[2], hnext[2], hcur[2];
+  load_qs(4 * b0, qs0);
+  load_hdr(b0, hnext);
   issue_a(4 * b0, sa0);
-  wait_vmcnt<0>();
-  wg_barrier();
+  load_qs(min(4 * b0 + 1, klast), qs1);
+  issue_a(min(4 * b0 + 1, klast), sa1);
 
   for (int b = b0; b < b1; ++b) {
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) {
       const int kc = 4 * b + cc;
-      uint8_t *pa = (cc & 1) ? sa1 : sa0;
-      uint8_t *pw = (cc >> 1) ? sw1 : sw0;
-      // Chunk kc's A copy and (at an even chunk) its half-block's W copy were
-      // issued one chunk ago: drain, then every wave's copies are in LDS and
-      // every wave has finished with the slots the copies below overwrite.
-      if (kc > 4 * b0) {
-        wait_vmcnt<0>();
-        wait_lgkmcnt0();
-        wg_barrier();
+      const uint8_t *pa = cc == 0 ? sa0 : cc == 1 ? sa1 : cc == 2 ? sa2 : sa3;
+      // Chunk kc's A copies were issued two chunks ago; the 6 loads issued
+      // one chunk ago (8 after a block's second chunk) may stay in flight.
+      // The barrier then shows every wave's copies, and the slot the copies
+      // below overwrite was last read two chunks ago.  (The compiler's own
+      // waits cover the W registers.)
+      __builtin_amdgcn_sched_barrier(0);
+      if (cc == 2)
+        wait_vmcnt<8>();
+      else
+        wait_vmcnt<6>();
+      wg_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      {
+        const int kn = min(kc + 2, klast);
+        u32x4(&qn)[2] = cc == 0 ? qs2 : cc == 1 ? qs3 : cc == 2 ? qs0 : qs1;
+        load_qs(kn, qn);
+        if (cc == 1) load_hdr(min(b + 1, b1 - 1), hnext);
+        issue_a(kn, cc == 0 ? sa2 : cc == 1 ? sa3 : cc == 2 ? sa0 : sa1);
       }
       __builtin_amdgcn_sched_barrier(0);
-      if ((cc & 1) == 0) issue_w(min(2 * b + (cc >> 1) + 1, 2 * b1 - 1), (cc >> 1) ? sw0 : sw1);
-      issue_a(min(kc + 1, 4 * b1 - 1), (cc & 1) ? sa0 : sa1);
-      __builtin_amdgcn_sched_barrier(0);
+      if (cc == 0) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) hcur[j] = hnext[j];
+      }
+      const u32x4(&qw)[2] = cc == 0 ? qs0 : cc == 1 ? qs1 : cc == 2 ? qs2 : qs3;
 
       auto read_a = [&](int t, u32x4 (&af)[4]) __attribute__((always_inline)) {
         const int seg = 2 * g + (t & 1) + 4 * (t >> 1);
@@ -493,20 +514,14 @@ __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restric
           af[i] = lds_read16(pa + rr * 128 + 16 * (seg ^ ((rr >> 1) & 7)));
         }
       };
-      u32x4 hw[2], qw[2], af[4], afn[4];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        hw[j] = lds_read16(pw + 80 * colw[j]);
-        qw[j] = lds_read16(pw + 80 * colw[j] + 16 + 32 * (cc & 1) + 16 * g);
-      }
+      u32x4 af[4], afn[4];
       read_a(0, afn);
-      lds_wait(hw[0], hw[1], qw[0], qw[1]);
       float sc_lo[2], sc_hi[2], nc_lo[2], nc_hi[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const float d = half_bits_to_f32(hw[j][0] & 0xFFFFu), dmin = half_bits_to_f32(hw[j][0] >> 16);
+        const float d = half_bits_to_f32(hcur[j][0] & 0xFFFFu), dmin = half_bits_to_f32(hcur[j][0] >> 16);
         uint32_t sv, mv;
-        q4k_scale_min(hw[j][1], hw[j][2], hw[j][3], 2 * cc + g, sv, mv);
+        q4k_scale_min(hcur[j][1], hcur[j][2], hcur[j][3], 2 * cc + g, sv, mv);
         const float sfac = d * (float)sv * bpw[j];
         const float mn = dmin * (float)mv * (bpw[j] * (g ? 16.f : 1.f));
         const float ncv = -(mn + 1024.f * sfac);
@@ -537,14 +552,16 @@ __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restric
     }
   }
 
-  // Epilogue: the wave's 128 x 64 tile through LDS, wave w staging in slot
-  // array w once every wave has passed the barrier.
+  // Epilogue: the wave's 128 x 64 tile through LDS, wave w staging in slot w
+  // once the tail's repeated copies have landed and every wave has passed
+  // the barrier.
   int ecol[2];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) ecol[j] = ew[min(n0 + colw[j], N - 1)];
+  for (int j = 0; j < 2; ++j) ecol[j] = ewc[j];
+  wait_vmcnt<0>();
   wg_barrier();
-  static_assert(32 * 72 * 4 <= kHSlotA && kHSlotA <= kHSlotW, "staging slice fits in a slot");
-  uint8_t *sbase = wave == 0 ? sa0 : wave == 1 ? sa1 : wave == 2 ? sw0 : sw1;
+  static_assert(32 * 72 * 4 <= kHSlotA, "staging slice fits in a slot");
+  uint8_t *sbase = wave == 0 ? sa0 : wave == 1 ? sa1 : wave == 2 ? sa2 : sa3;
   store_c_tile<2>(acc, reinterpret_cast<float *>(sbase), c, M, N, m0, n0 + 64 * wave, ea, ecol);
 }
 
