@@ -669,12 +669,16 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
     char *rest = static_cast<char *>(b.ws) + r256((size_t)n * kmax * 2) + r256((size_t)n * 4);
     hipError_t r = A ? launch_gemm_prep_a(A, n, K, a16, ea, st) : hipSuccess;
     if (r != hipSuccess) return r;
-    // Long prompts, a set of Q4_K matrices: one matrix-core launch for the
-    // set (its tiles fill the CUs in whole rounds), row exponents of each
-    // matrix at the start of its region
+    // A set of Q4_K matrices with enough rows or tiles for the half-block
+    // kernel (long prompts, or a gate|up set from about 900 rows at 4B
+    // widths): one matrix-core launch for the set (its tiles fill the CUs in
+    // whole rounds), row exponents of each matrix at the start of its region
     bool all_q4k = true;
+    int set_n[3] = {0, 0, 0}, ni = 0;
     for (int f : fmts) all_q4k = all_q4k && f == RT_LINEAR_Q4K;
-    if (all_q4k && mats.size() > 1 && q4k_gemm_multi_ok(n, (int)mats.size())) {
+    for (const MbMat &m : mats)
+      if (ni < 3) set_n[ni++] = m.n;
+    if (all_q4k && mats.size() > 1 && q4k_gemm_multi_ok(n, (int)mats.size(), set_n)) {
       const void *w[3];
       float *c[3];
       int nn[3];

@@ -637,15 +637,20 @@ size_t q4k_gemm_workspace_bytes(int M, int N, int K) {
 
 // The matrix-core launch on prepared operands; `part` holds the split-K
 // partials when the shape splits K.
+// The half-block kernel (two workgroups per CU) for outputs of at least 512
+// tiles of 128x256 or more than 1024 rows; below that the eight-wave kernel,
+// one workgroup per CU, fills the chip better (with K split when the tiles
+// are few).  At 1024x20480 (640 tiles) the half-block kernel takes 147 us
+// against 177 us; at 512x10240 (160 tiles) 61.6 against 54.9 us.
+static bool use_half_block(int M, int tiles) { return M > 1024 || tiles >= 512; }
+
 static hipError_t q4k_gemm_core(const _Float16 *a16, const int *ea, const uint8_t *wb, const int *ew, float *part,
                                 float *c, int M, int N, int K, hipStream_t s, GemmLeft *left = nullptr) {
-  // Up to 1024 rows: 128 x 256 tiles on eight waves (a prefill of a few
-  // hundred tokens gives too few 256-row tiles to fill the chip); above that
-  // the half-block kernel, two workgroups per CU.
   const int tiles_m = (M + 127) / 128, tiles_n = (N + 255) / 256;
+  const bool half = use_half_block(M, tiles_m * tiles_n);
   const int ks = gemm_ksplit(M, N, K);
   if (ks > 1) {
-    if (M <= 1024)
+    if (!half)
       hipLaunchKernelGGL(k_q4k_gemm_w8b<1>, dim3(tiles_m * tiles_n, ks), dim3(512), 0, s, a16, ea, wb, ew, part, M,
                          N, K, tiles_m, tiles_n, ks);
     else
@@ -660,7 +665,7 @@ static hipError_t q4k_gemm_core(const _Float16 *a16, const int *ea, const uint8_
     return launch_gemm_splitk_sum(part, c, (size_t)M * N, ks, s);
   }
   if (left) *left = GemmLeft{c, 1};
-  if (M <= 1024)
+  if (!half)
     hipLaunchKernelGGL(k_q4k_gemm_w8b<1>, dim3(tiles_m * tiles_n), dim3(512), 0, s, a16, ea, wb, ew, c, M, N, K,
                        tiles_m, tiles_n, 1);
   else
@@ -718,12 +723,17 @@ hipError_t launch_q4k_gemm_prepped(const _Float16 *a16, const int *ea, const voi
   return q4k_gemm_core(a16, ea, wb, ew, part, c, M, N, K, s, left);
 }
 
-bool q4k_gemm_multi_ok(int M, int count) { return M > 1024 && count >= 1 && count <= 3; }
+bool q4k_gemm_multi_ok(int M, int count, const int *n) {
+  if (count < 1 || count > 3) return false;
+  int tiles_n = 0;
+  for (int i = 0; i < count; ++i) tiles_n += (n[i] + 255) / 256;
+  return use_half_block(M, ((M + 127) / 128) * tiles_n);
+}
 
 hipError_t launch_q4k_gemm_multi_prepped(const _Float16 *a16, const int *ea, int count, const void *const *w,
                                          float *const *c, const int *n, void *const *ws, int M, int K,
                                          hipStream_t s, const int *const *ew_pre) {
-  if (!q4k_gemm_multi_ok(M, count) || K % 256 != 0) return hipErrorInvalidValue;
+  if (!q4k_gemm_multi_ok(M, count, n) || K % 256 != 0) return hipErrorInvalidValue;
   HMats mats{};
   int tiles_n = 0, rows = 0;
   bool all_pre = ew_pre != nullptr;

@@ -62,10 +62,10 @@ struct GemmLeft {
 hipError_t launch_q4k_gemm_prepped(const _Float16 *a16, const int *ea, const void *w, float *c, int M, int N, int K,
                                    void *ws, hipStream_t s, GemmLeft *left = nullptr, const int *ew_pre = nullptr);
 // Up to three Q4_K matrices sharing a prepared A (q|k|v, gate|up) in one
-// matrix-core launch, for M > 1024 (q4k_gemm_multi_ok); ws[i] holds at least
-// n[i]*4 bytes (matrix i's row exponents, unless ew_pre[i] gives them); no K
-// split.
-bool q4k_gemm_multi_ok(int M, int count);
+// matrix-core launch, for M > 1024 or at least 512 output tiles of 128x256
+// (q4k_gemm_multi_ok); ws[i] holds at least n[i]*4 bytes (matrix i's row
+// exponents, unless ew_pre[i] gives them); no K split.
+bool q4k_gemm_multi_ok(int M, int count, const int *n);
 hipError_t launch_q4k_gemm_multi_prepped(const _Float16 *a16, const int *ea, int count, const void *const *w,
                                          float *const *c, const int *n, void *const *ws, int M, int K,
                                          hipStream_t s, const int *const *ew_pre = nullptr);

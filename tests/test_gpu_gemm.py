@@ -53,6 +53,7 @@ def _run_bf16(rt, dev, a_bits, blocks, m, n, k):
     (2100, 2560, 10240, 8),  # half-block kernel, K split 3 ways (long-prompt down shape)
     (1024, 2560, 2048, 9),   # the kernel switch: eight-wave kernel up to 1024 rows (K split 2 ways) ...
     (1025, 2560, 2048, 10),  # ... half-block kernel from 1025 (K split 2 ways), one ragged row
+    (1000, 16384, 512, 11),  # under 1024 rows with 512 tiles: half-block kernel, ragged M
 ])
 def test_gemm_bf16_vs_oracle(rt, orc, dev, m, n, k, seed):
     blocks = orc.synth_q4k(100 + seed, n, k)
