@@ -4,8 +4,9 @@
 // dequantise a band of rows to f32 and sgemm it) and the FLUX GPU path
 // flux_dequant_q4k + flux_gemm_bt (metal_flux.rs:108-190, dequantise the whole
 // weight to bfloat scratch, then a 64x64 simdgroup GEMM).  Here the weight
-// stays packed in HBM (144-byte super-blocks): each workgroup copies the
-// packed bytes of the chunk it is about to multiply into LDS and every lane
+// stays packed in HBM (144-byte super-blocks): the packed bytes of the chunk
+// about to be multiplied reach each lane (through LDS in the eight-wave
+// kernel, straight into VGPRs in the half-block kernel) and every lane
 // dequantises its own column into registers.
 //
 // Arithmetic: v_mfma_f32_32x32x16_f16, f32 accumulation.
@@ -118,10 +119,11 @@ __global__ __launch_bounds__(256) void k_gemm_prep(const TA *__restrict__ a, _Fl
 //   (0..3) covers chunk-local k = 16g + 8(t&1) + 32(t>>1) + [0, 8): t < 2 are
 //   the low nibbles (sub-block 2c), t >= 2 the high nibbles of the same
 //   bytes (sub-block 2c+1).
-// Operands reach LDS by global_load_lds_dwordx4 (no VGPRs, no ds_write); each
-// ring slot is its own __shared__ variable.  Every lane dequantises the qs
-// bytes of its own column straight into the MFMA B operand, so no
-// dequantised weight is written back to LDS.
+// A (and in the eight-wave kernel the packed W bytes) reaches LDS by
+// global_load_lds_dwordx4 (no VGPRs, no ds_write); each ring slot is its own
+// __shared__ variable.  Every lane dequantises the qs bytes of its own column
+// straight into the MFMA B operand, so no dequantised weight is written back
+// to LDS.
 // ---------------------------------------------------------------------------
 // Eight f16 weights of one k-step from two qs words (low or high nibbles).
 // v_perm builds halves 1024+q (low nibbles) or 1024+16q (high nibbles), and
