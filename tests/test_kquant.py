@@ -429,6 +429,7 @@ def test_mixed_format_prefill_matches_oracle(rt, orc, T, mode, chunk):
     ref_layers = fresh_caches(layers)
     ref = orc.gemma3_prefill(cfg, ref_layers, embed, fnorm, toks, 0, mode)
     assert np.all(np.isfinite(got))
+    print(f"mixed-format prefill T={T} mode={mode} chunk={chunk}: logits rel-L2 {rel_l2(got, ref):.2e}", flush=True)
     assert rel_l2(got, ref) < LOGITS_TOL, rel_l2(got, ref)
     for li in range(cfg["n_layers"]):
         k, v = read_kv(d, cfg, li, T)
