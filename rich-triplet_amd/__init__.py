@@ -17,11 +17,14 @@ from __future__ import annotations
 
 import ctypes as C
 import pathlib
+import os
 import subprocess
 import sys
 
 PKG_DIR = pathlib.Path(__file__).resolve().parent
-LIB_PATH = PKG_DIR / "librt_hip.so"
+# RT_HIP_LIB selects another build of the library (e.g. the host-AddressSanitizer
+# one, `make -C rich-triplet_amd asan`); by default the in-tree librt_hip.so.
+LIB_PATH = pathlib.Path(os.environ["RT_HIP_LIB"]).resolve() if os.environ.get("RT_HIP_LIB") else PKG_DIR / "librt_hip.so"
 
 RT_OK, RT_EINVAL, RT_EHIP, RT_ENOMEM, RT_ESTATE = 0, 1, 2, 3, 4
 
