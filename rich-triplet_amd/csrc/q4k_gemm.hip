@@ -28,13 +28,13 @@
 #include <algorithm>
 
 #include "mfma_common.hpp"
+#include "q4k_gemm_dev.hpp"
 #include "rt_device.hpp"
 #include "rt_kernels.hpp"
 
 namespace rt {
 namespace {
 
-constexpr int kBK = 64;  // K per pipeline stage = one Q4_K chunk (32 qs bytes, 2 sub-blocks)
 
 // ---------------------------------------------------------------------------
 // Prep: A -> f16 with a per-row exponent; W row exponents from block headers.
@@ -109,51 +109,6 @@ __global__ __launch_bounds__(256) void k_gemm_prep(const TA *__restrict__ a, _Fl
     const int n = (b - M) * 4 + (int)(threadIdx.x >> 6);
     if (n < N) prep_w_row(w, ew, n, K, threadIdx.x & 63);
   }
-}
-
-// ---------------------------------------------------------------------------
-// Matrix-core kernels.  Both use v_mfma_f32_32x32x16_f16 (lane l: A row / B
-// column l%32, k group g = l/32, 8 halves each) and the same K order inside a
-// 64-wide chunk (A and B agree on it, so the sum is unchanged):
-//   lane group g holds qs bytes [16g, 16g+16) of the chunk's 32; k-step t
-//   (0..3) covers chunk-local k = 16g + 8(t&1) + 32(t>>1) + [0, 8): t < 2 are
-//   the low nibbles (sub-block 2c), t >= 2 the high nibbles of the same
-//   bytes (sub-block 2c+1).
-// A (and in the eight-wave kernel the packed W bytes) reaches LDS by
-// global_load_lds_dwordx4 (no VGPRs, no ds_write); each ring slot is its own
-// __shared__ variable.  Every lane dequantises the qs bytes of its own column
-// straight into the MFMA B operand, so no dequantised weight is written back
-// to LDS.
-// ---------------------------------------------------------------------------
-// Eight f16 weights of one k-step from two qs words (low or high nibbles).
-// v_perm builds halves 1024+q (low nibbles) or 1024+16q (high nibbles), and
-// each v_fma_mix computes f16(s*h - c) from them in f32 with one rounding.
-// The eight v_fma_mix sit in one asm block that ends with two wait states:
-// the compiler's hazard recognizer cannot tell that an asm block is VALU
-// work, so it would not separate it from an MFMA that reads its result
-// (a VALU write followed by an MFMA read of that VGPR needs two wait states).
-template <bool HIGH>
-RT_DEV half8 dq_step(uint32_t w0, uint32_t w1, float s, float negc) {
-  const uint32_t mask = HIGH ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
-  const uint32_t a = w0 & mask, b = w1 & mask;
-  const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, a, 0x04010400u);
-  const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u);
-  const uint32_t p2 = __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u);
-  const uint32_t p3 = __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u);
-  uint32_t r0, r1, r2, r3;
-  asm("v_fma_mixlo_f16 %0, %8, %4, %9 op_sel_hi:[0,1,0]\n\t"
-      "v_fma_mixhi_f16 %0, %8, %4, %9 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
-      "v_fma_mixlo_f16 %1, %8, %5, %9 op_sel_hi:[0,1,0]\n\t"
-      "v_fma_mixhi_f16 %1, %8, %5, %9 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
-      "v_fma_mixlo_f16 %2, %8, %6, %9 op_sel_hi:[0,1,0]\n\t"
-      "v_fma_mixhi_f16 %2, %8, %6, %9 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
-      "v_fma_mixlo_f16 %3, %8, %7, %9 op_sel_hi:[0,1,0]\n\t"
-      "v_fma_mixhi_f16 %3, %8, %7, %9 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
-      "s_nop 1"
-      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
-      : "v"(p0), "v"(p1), "v"(p2), "v"(p3), "v"(s), "v"(negc));
-  const u32x4 r = {r0, r1, r2, r3};
-  return __builtin_bit_cast(half8, r);
 }
 
 // ---------------------------------------------------------------------------
@@ -370,14 +325,6 @@ __global__ __launch_bounds__(512) void k_q4k_gemm_w8b(const _Float16 *__restrict
 // ---------------------------------------------------------------------------
 constexpr int kHSlotA = 128 * 128;       // bytes
 
-struct HMats {
-  const uint8_t *w[3];
-  const int *ew[3];
-  float *c[3];
-  int n[3];
-  int tn0[3];  // first column tile of each matrix
-  int count;
-};
 
 // The W row exponents of every matrix of a set in one launch: wave r takes
 // row r of the matrices' rows laid end to end.
@@ -594,34 +541,65 @@ __global__ __launch_bounds__(256) void k_gemm_splitk_sum(const float *__restrict
   }
 }
 
-// Split-K count.
-// Up to 1024 rows (eight-wave kernel, one workgroup per CU): enough
-// workgroups to cover the 256 CUs when the output has few 128x256 tiles (a
-// prefill's down projection, M=512 N=2560: 40 tiles), keeping at least 16
-// chunks (K=1024) per split.
-// Above (half-block kernel, two workgroups per CU, 512 slots): the split that
-// minimises a time model fitted to MI355X measurements:
-//   ceil(tiles*ks/512)/ks rounds of 0.032 us per K element (x0.75 when at most
-//   256 workgroups run, one per CU), plus (2*ks+1)*M*N*4 bytes of partial
-//   tiles at 5 TB/s.
-// 4096x2560 outputs (320 tiles) split K=10240 three ways: 2 rounds of a third
-// instead of 1.25 rounds of the whole K.
-int gemm_ksplit(int M, int N, int K) {
-  const int ntiles = ((M + 127) / 128) * ((N + 255) / 256);
-  if (M <= 1024) {
-    const int by_cus = 256 / ntiles, by_k = (K / kBK) / 16;
-    return max(1, min(by_cus, by_k));
+// Which matrix-core kernel takes an M x N output, and how many ways K is
+// split (blockIdx.y; a split of ks writes ks partial products of M x N).
+// Tiles are 128 x 256 (th) for the eight-wave and half-block kernels and
+// 256 x 256 (tw) for the wide one.
+//   w8b:   up to 1024 rows and th < 512; the eight-wave kernel, one
+//          workgroup per CU, fills the chip better with few tiles
+//          (512x10240, 160 tiles: 54.9 us against 61.6 us for the
+//          half-block kernel).  K splits into enough workgroups to cover the
+//          256 CUs (a prefill's down projection, M=512 N=2560: 40 tiles),
+//          keeping at least 16 chunks (K=1024) per split.
+//   wide:  a single matrix of more than 1024 rows with 128 < tw <= 256: one
+//          round of one workgroup per CU, where the half-block kernel runs
+//          two on most CUs.  4608x3072x12288 (216 tiles): 349 us against
+//          377 us; 4096x2560x10240 split 3 ways: 230 against 235 us.
+//   half:  the rest (and every set of matrices sharing A); two workgroups per
+//          CU.  4608x12288x3072 (864 wide tiles, 3.4 rounds): 375 us against
+//          425 us for the wide kernel, whose last round runs 96 workgroups
+//          on 256 CUs; with tw <= 128 its 128-row tiles, one workgroup per
+//          CU, spread the work over twice as many CUs.
+// Above 1024 rows K takes the split that minimises a time model fitted to
+// MI355X measurements:
+//   rounds/ks of c us per K element, plus (2*ks+1)*M*N*4 bytes of partial
+//   tiles at 5 TB/s;
+//   wide:  rounds = ceil(tw*ks/256), c = 0.036;
+//   half:  rounds = ceil(th*ks/512), x0.75 when at most 256 workgroups run
+//          (one per CU), c = 0.032.
+// 4096x2560 outputs (160 wide tiles) split K=10240 three ways: 2 rounds of a
+// third instead of 1 round of the whole K on 160 of the 256 CUs.
+enum class GemmKind { w8b, half, wide };
+struct GemmPlan {
+  GemmKind kind;
+  int ks;
+};
+static GemmKind gemm_kind(int M, int tiles_n, bool single) {
+  const int th = ((M + 127) / 128) * tiles_n, tw = ((M + 255) / 256) * tiles_n;
+  if (single && M > 1024 && tw > 128 && tw <= 256) return GemmKind::wide;
+  return M > 1024 || th >= 512 ? GemmKind::half : GemmKind::w8b;
+}
+
+static GemmPlan gemm_plan(int M, int N, int K) {
+  const int tiles_n = (N + 255) / 256;
+  const GemmKind kind = gemm_kind(M, tiles_n, true);
+  if (kind == GemmKind::w8b) {
+    const int by_cus = 256 / (((M + 127) / 128) * tiles_n), by_k = (K / kBK) / 16;
+    return {kind, max(1, min(by_cus, by_k))};
   }
+  if (M <= 1024) return {kind, 1};
+  const bool wide = kind == GemmKind::wide;
+  const int ntiles = wide ? ((M + 255) / 256) * tiles_n : ((M + 127) / 128) * tiles_n;
   auto est_us = [&](int ks) {
     const int wgs = ntiles * ks;
-    const double rounds = (double)((wgs + 511) / 512) * (wgs <= 256 ? 0.75 : 1.0);
+    const double rounds = wide ? (double)((wgs + 255) / 256) : (double)((wgs + 511) / 512) * (wgs <= 256 ? 0.75 : 1.0);
     const double partial = ks > 1 ? (2.0 * ks + 1.0) * M * N * 4.0 / 5e6 : 0.0;
-    return rounds / ks * K * 0.032 + partial;
+    return rounds / ks * K * (wide ? 0.036 : 0.032) + partial;
   };
   int best = 1;
   for (int ks = 2; ks <= 4 && ks <= K / 256; ++ks)
     if (est_us(ks) < est_us(best)) best = ks;
-  return best;
+  return {kind, best};
 }
 
 hipError_t launch_gemm_splitk_sum(const float *part, float *c, size_t mn, int ksplit, hipStream_t s) {
@@ -637,48 +615,38 @@ hipError_t launch_gemm_prep_a(const float *a, int M, int K, _Float16 *a16, int *
 
 size_t q4k_gemm_workspace_bytes(int M, int N, int K) {
   auto r256 = [](size_t b) { return (b + 255) & ~size_t(255); };
-  const int ks = gemm_ksplit(M, N, K);
+  const int ks = gemm_plan(M, N, K).ks;
   return r256((size_t)M * K * 2) + r256((size_t)M * 4) + r256((size_t)N * 4) +
          (ks > 1 ? r256((size_t)ks * M * N * 4) : 0);
 }
 
 // The matrix-core launch on prepared operands; `part` holds the split-K
 // partials when the shape splits K.
-// The half-block kernel (two workgroups per CU) for outputs of at least 512
-// tiles of 128x256 or more than 1024 rows; below that the eight-wave kernel,
-// one workgroup per CU, fills the chip better (with K split when the tiles
-// are few).  At 1024x20480 (640 tiles) the half-block kernel takes 147 us
-// against 177 us; at 512x10240 (160 tiles) 61.6 against 54.9 us.
-static bool use_half_block(int M, int tiles) { return M > 1024 || tiles >= 512; }
-
 static hipError_t q4k_gemm_core(const _Float16 *a16, const int *ea, const uint8_t *wb, const int *ew, float *part,
                                 float *c, int M, int N, int K, hipStream_t s, GemmLeft *left = nullptr) {
   const int tiles_m = (M + 127) / 128, tiles_n = (N + 255) / 256;
-  const bool half = use_half_block(M, tiles_m * tiles_n);
-  const int ks = gemm_ksplit(M, N, K);
-  if (ks > 1) {
-    if (!half)
-      hipLaunchKernelGGL(k_q4k_gemm_w8b<1>, dim3(tiles_m * tiles_n, ks), dim3(512), 0, s, a16, ea, wb, ew, part, M,
+  const GemmPlan plan = gemm_plan(M, N, K);
+  const GemmKind kind = plan.kind;
+  const int ks = plan.ks;
+  float *out = ks > 1 ? part : c;
+  hipError_t e = hipSuccess;
+  if (kind == GemmKind::wide) {
+    e = launch_q4k_gemm_wide(a16, ea, HMats{{wb}, {ew}, {out}, {N}, {0}, 1}, M, K, tiles_n, ks, s);
+  } else {
+    if (kind == GemmKind::w8b)
+      hipLaunchKernelGGL(k_q4k_gemm_w8b<1>, dim3(tiles_m * tiles_n, ks), dim3(512), 0, s, a16, ea, wb, ew, out, M,
                          N, K, tiles_m, tiles_n, ks);
     else
       hipLaunchKernelGGL(k_q4k_gemm_h, dim3(tiles_m * tiles_n, ks), dim3(256), 0, s, a16, ea,
-                         HMats{{wb}, {ew}, {part}, {N}, {0}, 1}, M, K, tiles_m, tiles_n, ks);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    if (left) {
-      *left = GemmLeft{part, ks};
-      return hipSuccess;
-    }
-    return launch_gemm_splitk_sum(part, c, (size_t)M * N, ks, s);
+                         HMats{{wb}, {ew}, {out}, {N}, {0}, 1}, M, K, tiles_m, tiles_n, ks);
+    e = hipGetLastError();
   }
-  if (left) *left = GemmLeft{c, 1};
-  if (!half)
-    hipLaunchKernelGGL(k_q4k_gemm_w8b<1>, dim3(tiles_m * tiles_n), dim3(512), 0, s, a16, ea, wb, ew, c, M, N, K,
-                       tiles_m, tiles_n, 1);
-  else
-    hipLaunchKernelGGL(k_q4k_gemm_h, dim3(tiles_m * tiles_n), dim3(256), 0, s, a16, ea,
-                       HMats{{wb}, {ew}, {c}, {N}, {0}, 1}, M, K, tiles_m, tiles_n, 1);
-  return hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (left) {
+    *left = GemmLeft{out, ks};
+    return hipSuccess;
+  }
+  return ks > 1 ? launch_gemm_splitk_sum(part, c, (size_t)M * N, ks, s) : hipSuccess;
 }
 
 hipError_t launch_q4k_gemm(const void *a, bool a_bf16, const void *w, float *c, int M, int N, int K, void *ws,
@@ -734,7 +702,7 @@ bool q4k_gemm_multi_ok(int M, int count, const int *n) {
   if (count < 1 || count > 3) return false;
   int tiles_n = 0;
   for (int i = 0; i < count; ++i) tiles_n += (n[i] + 255) / 256;
-  return use_half_block(M, ((M + 127) / 128) * tiles_n);
+  return gemm_kind(M, tiles_n, false) == GemmKind::half;
 }
 
 hipError_t launch_q4k_gemm_multi_prepped(const _Float16 *a16, const int *ea, int count, const void *const *w,

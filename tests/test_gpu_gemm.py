@@ -66,10 +66,19 @@ def test_gemm_bf16_vs_oracle(rt, orc, dev, m, n, k, seed):
     assert err < GEMM_TOL
 
 
-@pytest.mark.parametrize("m,n,k", [(4608, 9216, 3072), (4608, 12288, 3072), (4608, 3072, 12288)])
+@pytest.mark.parametrize("m,n,k", [
+    (4608, 9216, 3072),    # FLUX-12B QKV: half-block kernel (648 tiles of 256 x 256)
+    (4608, 12288, 3072),   # FLUX-12B MLP up: half-block kernel
+    (4608, 3072, 12288),   # FLUX-12B MLP down: 256 x 256 kernel (216 tiles), one round
+    (4096, 2560, 10240),   # 4096-row prefill down: 256 x 256 kernel, K split 3 ways
+    (4096, 2560, 2048),    # 4096-row prefill o: 256 x 256 kernel (160 tiles)
+    (1500, 5632, 8192),    # 256 x 256 kernel, K split 3 ways, ragged M
+    (1300, 9000, 2560),    # 256 x 256 kernel, ragged M and N
+])
 def test_gemm_flux_shapes(rt, orc, dev, m, n, k):
-    """FLUX-12B shapes (QKV, MLP-up, MLP-down); reference on the GPU in f32 from the
-    oracle's dequantised weights (a library GEMM, not this library's kernels)."""
+    """FLUX-12B shapes (QKV, MLP-up, MLP-down) and the shapes that take the
+    256 x 256-tile kernel; reference on the GPU in f32 from the oracle's
+    dequantised weights (a library GEMM, not this library's kernels)."""
     import torch
     blocks = orc.synth_q4k(7 + n, n, k)
     a = torch.from_numpy(orc.synth_normal(11 + k, m * k).reshape(m, k)).to(torch.bfloat16)
