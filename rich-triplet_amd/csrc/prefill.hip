@@ -202,8 +202,11 @@ __global__ __launch_bounds__(256) void k_pf_gelu_mul(RowsIn g, RowsIn u, float *
 // The same product for the GEMM path, one row per workgroup of kGeluRowT
 // threads (F <= 16384; 1024 threads measured 1% faster over a 4096-row
 // prefill than 256): h goes straight out as the down GEMM's A operand (f16
-// row, exponent ea[t]), bit-identical to preparing the f32 row.
+// row, exponent ea[t]), bit-identical to preparing the f32 row.  Without
+// GELU the rows of g are h already (the gate|up GEMM formed the product) and
+// are only prepared.
 constexpr int kGeluRowT = 1024;
+template <bool GELU>
 __global__ __launch_bounds__(kGeluRowT) void k_pf_gelu_rows(RowsIn g, RowsIn u, int F, _Float16 *__restrict__ a16,
                                                       int *__restrict__ ea) {
   constexpr int MAXP = 16384 / 4 / kGeluRowT;
@@ -215,9 +218,14 @@ __global__ __launch_bounds__(kGeluRowT) void k_pf_gelu_rows(RowsIn g, RowsIn u, 
   for (int i = 0; i < MAXP; ++i) {
     const int c4 = (int)threadIdx.x + kGeluRowT * i;
     if (c4 < f4) {
-      const float4 a = rows_in4(g, t, 4 * c4), b = rows_in4(u, t, 4 * c4);
-      r[i] = make_float4(mul_nc(gelu_tanh(a.x), b.x), mul_nc(gelu_tanh(a.y), b.y), mul_nc(gelu_tanh(a.z), b.z),
-                         mul_nc(gelu_tanh(a.w), b.w));
+      const float4 a = rows_in4(g, t, 4 * c4);
+      if constexpr (GELU) {
+        const float4 b = rows_in4(u, t, 4 * c4);
+        r[i] = make_float4(mul_nc(gelu_tanh(a.x), b.x), mul_nc(gelu_tanh(a.y), b.y), mul_nc(gelu_tanh(a.z), b.z),
+                           mul_nc(gelu_tanh(a.w), b.w));
+      } else {
+        r[i] = a;
+      }
       amax = fmaxf(amax, fmaxf(fmaxf(fabsf(r[i].x), fabsf(r[i].y)), fmaxf(fabsf(r[i].z), fabsf(r[i].w))));
     }
   }
@@ -787,15 +795,28 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
     PF_TRY(proj(b.attn, QD, {L.fmt[kProjO]}, {MbMat{L.wo, b.o, H, 0, 0}}, {&vo}, {L.ew[kProjO]}));
     PF_TRY(launch_pf_norm<true>(n, st, b.hid, vo, L.g_post_attn, L.g_pre_ffn, b.x2, xn_f32, H, a.eps, stage, a16_h,
                                 ea_h));
-    PF_TRY(proj(plan.mb ? b.xn : nullptr, H, {L.fmt[kProjGate], L.fmt[kProjUp]},
-                {MbMat{L.wgate, b.g, F, 0, 0}, MbMat{L.wup, b.u, F, 0, 0}}, {&vg, &vu},
-                {L.ew[kProjGate], L.ew[kProjUp]}));
-    if (plan.mb) {
-      const size_t n4 = (size_t)n * F / 4;
-      const unsigned eg = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
-      PF_CHECK(hipLaunchKernelGGL(k_pf_gelu_mul, dim3(eg), dim3(256), 0, st, vg, vu, b.g, n, F, stage));
+    // gate|up: Q4_K pairs that would run as one set launch form h = gelu(g)*u
+    // in the GEMM itself (b.g), and the f16 rows of h for the down GEMM are
+    // prepared from it
+    const bool gelu_gemm = !plan.mb && L.fmt[kProjGate] == RT_LINEAR_Q4K && L.fmt[kProjUp] == RT_LINEAR_Q4K &&
+                           L.ew[kProjGate] && L.ew[kProjUp] && q4k_gemm_gelu_ok(n, F);
+    if (gelu_gemm) {
+      PF_TRY(launch_q4k_gemm_gelu_prepped(gemm_a16(H), gemm_ea(H), L.wgate, L.wup, L.ew[kProjGate], L.ew[kProjUp],
+                                          b.g, n, F, H, st));
+      PF_CHECK(hipLaunchKernelGGL(k_pf_gelu_rows<false>, dim3(n), dim3(kGeluRowT), 0, st, rows_plain(b.g, F),
+                                  rows_plain(b.g, F), F, gemm_a16(F), gemm_ea(F)));
     } else {
-      PF_CHECK(hipLaunchKernelGGL(k_pf_gelu_rows, dim3(n), dim3(kGeluRowT), 0, st, vg, vu, F, gemm_a16(F), gemm_ea(F)));
+      PF_TRY(proj(plan.mb ? b.xn : nullptr, H, {L.fmt[kProjGate], L.fmt[kProjUp]},
+                  {MbMat{L.wgate, b.g, F, 0, 0}, MbMat{L.wup, b.u, F, 0, 0}}, {&vg, &vu},
+                  {L.ew[kProjGate], L.ew[kProjUp]}));
+      if (plan.mb) {
+        const size_t n4 = (size_t)n * F / 4;
+        const unsigned eg = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
+        PF_CHECK(hipLaunchKernelGGL(k_pf_gelu_mul, dim3(eg), dim3(256), 0, st, vg, vu, b.g, n, F, stage));
+      } else {
+        PF_CHECK(hipLaunchKernelGGL(k_pf_gelu_rows<true>, dim3(n), dim3(kGeluRowT), 0, st, vg, vu, F, gemm_a16(F),
+                                    gemm_ea(F)));
+      }
     }
     PF_TRY(proj(plan.mb ? b.g : nullptr, F, {L.fmt[kProjDown]}, {MbMat{L.wdown, b.dn, H, 0, 0}}, {&vd},
                 {L.ew[kProjDown]}));

@@ -27,6 +27,7 @@
 
 #include <algorithm>
 
+#include "gemma3_math.hpp"
 #include "mfma_common.hpp"
 #include "q4k_gemm_dev.hpp"
 #include "rt_device.hpp"
@@ -322,8 +323,61 @@ __global__ __launch_bounds__(512) void k_q4k_gemm_w8b(const _Float16 *__restrict
 // Up to three matrices sharing A (q|k|v, gate|up) run as one launch: their
 // 256-column tiles are numbered one after another (HMats::tn0), and a
 // workgroup takes the matrix its column tile falls in.
+// GELU: the gate and up matrices of an FFN (mats.w[0], mats.w[1], N rows
+// each) in one tile of 128 rows x 128 columns of both: a wave's column tile
+// j = 0 is 32 gate columns and j = 1 the same 32 up columns, so the lane
+// that holds g[m][n] also holds u[m][n], and the epilogue stores
+// h = gelu_tanh(g) * u (Gemma3Mlp::forward, transformer4.rs:328-334) to
+// mats.c[0] instead of g and u.  No K split.
 // ---------------------------------------------------------------------------
 constexpr int kHSlotA = 128 * 128;       // bytes
+
+// The GELU epilogue: like store_c_tile<1>, with each staged value
+// gelu_tanh(g) * u of the wave's gate (acc[i][0]) and up (acc[i][1])
+// accumulators, each scaled by 2^(ea[row] + ew of its matrix) as
+// store_c_tile scales them, so h equals the product of the two stored
+// matrices.
+RT_DEV void store_gelu_tile(const floatx16 (&acc)[4][2], float *stage, float *c, int M, int N, int row0, int col0,
+                            const int *ea, const int (&ecol)[2]) {
+  constexpr int P = 40, F4 = 8, RPI = 8;
+  const int lane = (int)(threadIdx.x & 63), g = lane >> 5, l32 = lane & 31;
+  const bool vec = (N & 3) == 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    int er[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) er[r] = ea[min(row0 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3), M - 1)];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float gv = __builtin_amdgcn_ldexpf(acc[i][0][r], er[r] + ecol[0]);
+      const float uv = __builtin_amdgcn_ldexpf(acc[i][1][r], er[r] + ecol[1]);
+      stage[(8 * (r >> 2) + 4 * g + (r & 3)) * P + l32] = mul_nc(gelu_tanh(gv), uv);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int q = 0; q < 32 / RPI; ++q) {
+      const int rl = q * RPI + lane / F4, f = lane % F4;
+      const int row = row0 + 32 * i + rl, col = col0 + 4 * f;
+      const float4 v = *reinterpret_cast<const float4 *>(stage + rl * P + 4 * f);
+      if (row < M) {
+        float *dst = c + (size_t)row * N + col;
+        if (vec && col + 4 <= N) {
+          *reinterpret_cast<float4 *>(dst) = v;
+        } else {
+          if (col < N) dst[0] = v.x;
+          if (col + 1 < N) dst[1] = v.y;
+          if (col + 2 < N) dst[2] = v.z;
+          if (col + 3 < N) dst[3] = v.w;
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
 
 
 // The W row exponents of every matrix of a set in one launch: wave r takes
@@ -334,6 +388,7 @@ __global__ __launch_bounds__(256) void k_gemm_prep_w_multi(HMats mats, int K) {
   if (r < mats.n[i]) prep_w_row(mats.w[i], const_cast<int *>(mats.ew[i]), r, K, threadIdx.x & 63);
 }
 
+template <bool GELU>
 __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restrict__ a16, const int *__restrict__ ea,
                                                        HMats mats, int M, int K, int tiles_m, int tiles_n,
                                                        int ksplit) {
@@ -349,12 +404,11 @@ __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restric
   const int gm = min(4, tiles_m - group * 4);
   const int tm = group * 4 + in_group % gm, tn = in_group / gm;
   int mi = 0;
-  while (mi + 1 < mats.count && tn >= mats.tn0[mi + 1]) ++mi;  // wave-uniform
-  const uint8_t *__restrict__ w = mats.w[mi];
-  const int *__restrict__ ew = mats.ew[mi];
+  if (!GELU)
+    while (mi + 1 < mats.count && tn >= mats.tn0[mi + 1]) ++mi;  // wave-uniform
   float *__restrict__ c = mats.c[mi];
   const int N = mats.n[mi];
-  const int m0 = tm * 128, n0 = (tn - mats.tn0[mi]) * 256;
+  const int m0 = tm * 128, n0 = GELU ? tn * 128 : (tn - mats.tn0[mi]) * 256;
   const int nblocks = K / 256;
   const size_t row_bytes = (size_t)nblocks * kQ4KBlockBytes;
   const int split = (int)blockIdx.y;
@@ -381,29 +435,31 @@ __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restric
     for (int i = 0; i < 4; ++i)
       __builtin_amdgcn_global_load_lds((gvoid *)(base + a_off[i]), (lvoid *)(slot + (4 * wave + i) * 1024), 16, 0, 0);
   };
-  // W: column tile j (0, 1) of this wave, lane -> column colw[j], k group g
-  // -> qs bytes [16g, 16g+16) of each chunk's 32.
+  // W: column tile j (0, 1) of this wave, lane -> column colw[j] of matrix
+  // wm[j], k group g -> qs bytes [16g, 16g+16) of each chunk's 32.
   int colw[2], ewc[2];
   float bpw[2];
-  const uint8_t *w_base = w + (size_t)n0 * row_bytes;
+  const uint8_t *w_base[2];
   uint32_t w_off[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    colw[j] = 64 * wave + 32 * j + l32;
+    const int wm = GELU ? j : mi;
+    colw[j] = GELU ? 32 * wave + l32 : 64 * wave + 32 * j + l32;
     const int n = min(n0 + colw[j], N - 1);
-    ewc[j] = ew[n];
+    ewc[j] = mats.ew[wm][n];
     bpw[j] = __builtin_amdgcn_ldexpf(g ? 0.0625f : 1.0f, -ewc[j]);
+    w_base[j] = mats.w[wm] + (size_t)n0 * row_bytes;
     w_off[j] = (uint32_t)(n - n0) * (uint32_t)row_bytes;
   }
   auto load_qs = [&](int kc, u32x4 (&q)[2]) __attribute__((always_inline)) {
-    const uint8_t *base = w_base + (size_t)(kc >> 2) * kQ4KBlockBytes + 16 + 32 * (kc & 3);
+    const size_t koff = (size_t)(kc >> 2) * kQ4KBlockBytes + 16 + 32 * (kc & 3);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) q[j] = *reinterpret_cast<const u32x4 *>(base + (w_off[j] + 16u * g));
+    for (int j = 0; j < 2; ++j) q[j] = *reinterpret_cast<const u32x4 *>(w_base[j] + koff + (w_off[j] + 16u * g));
   };
   auto load_hdr = [&](int blk, u32x4 (&h)[2]) __attribute__((always_inline)) {
-    const uint8_t *base = w_base + (size_t)blk * kQ4KBlockBytes;
+    const size_t koff = (size_t)blk * kQ4KBlockBytes;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) h[j] = *reinterpret_cast<const u32x4 *>(base + w_off[j]);
+    for (int j = 0; j < 2; ++j) h[j] = *reinterpret_cast<const u32x4 *>(w_base[j] + koff + w_off[j]);
   };
 
   floatx16 acc[4][2];
@@ -516,7 +572,10 @@ __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restric
   wg_barrier();
   static_assert(32 * 72 * 4 <= kHSlotA, "staging slice fits in a slot");
   uint8_t *sbase = wave == 0 ? sa0 : wave == 1 ? sa1 : wave == 2 ? sa2 : sa3;
-  store_c_tile<2>(acc, reinterpret_cast<float *>(sbase), c, M, N, m0, n0 + 64 * wave, ea, ecol);
+  if constexpr (GELU)
+    store_gelu_tile(acc, reinterpret_cast<float *>(sbase), c, M, N, m0, n0 + 32 * wave, ea, ecol);
+  else
+    store_c_tile<2>(acc, reinterpret_cast<float *>(sbase), c, M, N, m0, n0 + 64 * wave, ea, ecol);
 }
 
 }  // namespace
@@ -637,7 +696,7 @@ static hipError_t q4k_gemm_core(const _Float16 *a16, const int *ea, const uint8_
       hipLaunchKernelGGL(k_q4k_gemm_w8b<1>, dim3(tiles_m * tiles_n, ks), dim3(512), 0, s, a16, ea, wb, ew, out, M,
                          N, K, tiles_m, tiles_n, ks);
     else
-      hipLaunchKernelGGL(k_q4k_gemm_h, dim3(tiles_m * tiles_n, ks), dim3(256), 0, s, a16, ea,
+      hipLaunchKernelGGL(k_q4k_gemm_h<false>, dim3(tiles_m * tiles_n, ks), dim3(256), 0, s, a16, ea,
                          HMats{{wb}, {ew}, {out}, {N}, {0}, 1}, M, K, tiles_m, tiles_n, ks);
     e = hipGetLastError();
   }
@@ -705,6 +764,29 @@ bool q4k_gemm_multi_ok(int M, int count, const int *n) {
   return gemm_kind(M, tiles_n, false) == GemmKind::half;
 }
 
+bool q4k_gemm_gelu_ok(int M, int N) {
+  const int n[2] = {N, N};
+  return q4k_gemm_multi_ok(M, 2, n);
+}
+
+hipError_t launch_q4k_gemm_gelu_prepped(const _Float16 *a16, const int *ea, const void *w_gate, const void *w_up,
+                                        const int *ew_gate, const int *ew_up, float *h, int M, int N, int K,
+                                        hipStream_t s) {
+  if (!q4k_gemm_gelu_ok(M, N) || K % 256 != 0 || N <= 0 || !ew_gate || !ew_up) return hipErrorInvalidValue;
+  HMats mats{};
+  mats.w[0] = static_cast<const uint8_t *>(w_gate);
+  mats.w[1] = static_cast<const uint8_t *>(w_up);
+  mats.ew[0] = ew_gate;
+  mats.ew[1] = ew_up;
+  mats.c[0] = h;
+  mats.n[0] = mats.n[1] = N;
+  mats.count = 2;
+  const int tiles_m = (M + 127) / 128, tiles_n = (N + 127) / 128;
+  hipLaunchKernelGGL(k_q4k_gemm_h<true>, dim3(tiles_m * tiles_n), dim3(256), 0, s, a16, ea, mats, M, K, tiles_m,
+                     tiles_n, 1);
+  return hipGetLastError();
+}
+
 hipError_t launch_q4k_gemm_multi_prepped(const _Float16 *a16, const int *ea, int count, const void *const *w,
                                          float *const *c, const int *n, void *const *ws, int M, int K,
                                          hipStream_t s, const int *const *ew_pre) {
@@ -732,7 +814,7 @@ hipError_t launch_q4k_gemm_multi_prepped(const _Float16 *a16, const int *ea, int
     if (e != hipSuccess) return e;
   }
   const int tiles_m = (M + 127) / 128;
-  hipLaunchKernelGGL(k_q4k_gemm_h, dim3(tiles_m * tiles_n), dim3(256), 0, s, a16, ea, mats, M, K, tiles_m, tiles_n,
+  hipLaunchKernelGGL(k_q4k_gemm_h<false>, dim3(tiles_m * tiles_n), dim3(256), 0, s, a16, ea, mats, M, K, tiles_m, tiles_n,
                      1);
   return hipGetLastError();
 }

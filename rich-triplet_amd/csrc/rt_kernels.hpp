@@ -69,6 +69,15 @@ bool q4k_gemm_multi_ok(int M, int count, const int *n);
 hipError_t launch_q4k_gemm_multi_prepped(const _Float16 *a16, const int *ea, int count, const void *const *w,
                                          float *const *c, const int *n, void *const *ws, int M, int K,
                                          hipStream_t s, const int *const *ew_pre = nullptr);
+// An FFN's gate and up Q4_K matrices (N rows each) on a prepared A in one
+// launch that stores h = gelu_tanh(A.Wg^T) * (A.Wu^T) [M][N] in f32 instead
+// of the two products (equal to the product of the two stored matrices),
+// for the shapes q4k_gemm_multi_ok takes as a set; needs both weights' row
+// exponents (launch_q4k_row_exponents).
+bool q4k_gemm_gelu_ok(int M, int N);
+hipError_t launch_q4k_gemm_gelu_prepped(const _Float16 *a16, const int *ea, const void *w_gate, const void *w_up,
+                                        const int *ew_gate, const int *ew_up, float *h, int M, int N, int K,
+                                        hipStream_t s);
 // The GEMM's power-of-two row exponents of a Q4_K weight [N][K] (from its
 // block headers) into ew[N]: they depend on the weight alone, so a caller
 // that keeps the weight can compute them once.
