@@ -81,7 +81,6 @@ hipError_t enqueue_decode_batch(const DecodeShape &s, const DecodeArgs &a, const
 struct PrefillBuffers {
   int cap = 0;                      // rows the buffers hold
   int *tokens = nullptr;            // [cap]
-  float *cs = nullptr;              // [cap][2][head_dim]: local cos|sin, global cos|sin of each row's position
   float *hid = nullptr, *x2 = nullptr, *xn = nullptr, *o = nullptr, *dn = nullptr;  // [cap][hidden]
   float *q = nullptr, *attn = nullptr;  // [cap][n_q_heads*head_dim]
   float *k = nullptr, *v = nullptr;     // [cap][n_kv_heads*head_dim]

@@ -58,8 +58,9 @@ struct rt_decode {
   bool fused = true;                     // the fused single-token kernels serve this shape (else the rows path)
   int pf_chunk = 4096;                   // rows per prefill chunk (~180 KB of scratch per row at Gemma-3-4B)
   std::vector<void *> pf_owned;
-  int *pf_tokens_host = nullptr;         // pinned staging: [pf.cap] tokens, [pf.cap][2][head_dim] cos/sin
-  float *pf_cs_host = nullptr;
+  int *pf_tokens_host = nullptr;         // pinned staging: [pf.cap] tokens
+  float *rope_cs = nullptr;              // [rope_rows][2][head_dim] cos/sin of positions 0 .. rope_rows-1
+  int rope_rows = 0;
 };
 
 namespace {
@@ -256,7 +257,6 @@ rt_status rt_decode_destroy(rt_decode *d) {
     if (a.p) (void)hipFree(a.p);
   if (d->params_host) (void)hipHostFree(d->params_host);
   if (d->pf_tokens_host) (void)hipHostFree(d->pf_tokens_host);
-  if (d->pf_cs_host) (void)hipHostFree(d->pf_cs_host);
   if (d->params_copied) (void)hipEventDestroy(d->params_copied);
   if (d->stream) (void)hipStreamDestroy(d->stream);
   delete d;
@@ -638,9 +638,7 @@ static rt_status prefill_reserve(rt_decode *d, int cap) {
   for (void *p : d->pf_owned) dfree(d, p);
   d->pf_owned.clear();
   if (d->pf_tokens_host) (void)hipHostFree(d->pf_tokens_host);
-  if (d->pf_cs_host) (void)hipHostFree(d->pf_cs_host);
   d->pf_tokens_host = nullptr;
-  d->pf_cs_host = nullptr;
   b = PrefillBuffers{};
   const rt_gemma3_config &c = d->cfg;
   const size_t H = c.hidden, F = c.ffn, D = c.head_dim, QD = (size_t)c.n_q_heads * D, KVD = (size_t)c.n_kv_heads * D;
@@ -657,7 +655,6 @@ static rt_status prefill_reserve(rt_decode *d, int cap) {
     return st;                                         \
   b.field = static_cast<type *>(p);
   PF_GET(tokens, int, rows);
-  PF_GET(cs, float, rows * 2 * D);
   PF_GET(hid, float, rows * H);
   PF_GET(x2, float, rows * H);
   PF_GET(xn, float, rows * H);
@@ -684,23 +681,28 @@ static rt_status prefill_reserve(rt_decode *d, int cap) {
   b.attn_o = static_cast<float *>(p);
   b.attn_rows = split_rows;
   e = hipHostMalloc((void **)&d->pf_tokens_host, rows * sizeof(int), hipHostMallocDefault);
-  if (e == hipSuccess) e = hipHostMalloc((void **)&d->pf_cs_host, rows * 2 * D * sizeof(float), hipHostMallocDefault);
   if (e != hipSuccess) return hip_error(e, "rt_decode_prefill hipHostMalloc");
   b.cap = cap;
   return RT_OK;
 }
 
-// cos/sin tables of positions p0 .. p0+n-1, local then global per row, with
-// the host libm as fill_slot computes them for a decode step.
-static void prefill_rope_tables(rt_decode *d, int p0, int n) {
-  const int D = d->cfg.head_dim, P = D / 2;
+// The cos/sin tables of positions 0 .. `upto`-1 (rounded up to 4096, at most
+// max_seq), local then global per row, with the host libm as fill_slot
+// computes them for a decode step.  They depend on the position alone, so
+// they are computed once (about 2 ms of host time per 4096 positions on 16
+// threads) and every prefill reads its rows' slice; a prefill past the
+// table's end computes it again, longer.
+static rt_status prefill_rope_table(rt_decode *d, int upto) {
+  if (d->rope_rows >= upto) return RT_OK;
+  const int D = d->cfg.head_dim, P = D / 2, n = std::min(d->cfg.max_seq, (upto + 4095) / 4096 * 4096);
+  std::vector<float> host((size_t)n * 2 * D);
   auto rows = [&](int t0, int t1) {
     for (int t = t0; t < t1; ++t) {
-      float *cs = d->pf_cs_host + (size_t)t * 2 * D;
+      float *cs = host.data() + (size_t)t * 2 * D;
       for (int k = 0; k < 2; ++k, cs += D) {
         const float fs = k ? d->cfg.rope_fs_global : d->cfg.rope_fs_local;
         const float *den = k ? d->rope_den_global.data() : d->rope_den_local.data();
-        const float pf = (float)(p0 + t) * fs;
+        const float pf = (float)t * fs;
         for (int i = 0; i < P; ++i) {
           const float ang = pf / den[i];
           cs[i] = cosf(ang);
@@ -712,12 +714,28 @@ static void prefill_rope_tables(rt_decode *d, int p0, int n) {
   const int nt = std::max(1, std::min({16, (int)std::thread::hardware_concurrency(), n / 64}));
   if (nt == 1) {
     rows(0, n);
-    return;
+  } else {
+    std::vector<std::thread> pool;
+    const int per = (n + nt - 1) / nt;
+    for (int i = 0; i < nt; ++i) pool.emplace_back(rows, std::min(n, i * per), std::min(n, (i + 1) * per));
+    for (auto &th : pool) th.join();
   }
-  std::vector<std::thread> pool;
-  const int per = (n + nt - 1) / nt;
-  for (int i = 0; i < nt; ++i) pool.emplace_back(rows, std::min(n, i * per), std::min(n, (i + 1) * per));
-  for (auto &th : pool) th.join();
+  hipError_t e = hipStreamSynchronize(d->stream);  // no queued prefill reads the old table
+  if (e != hipSuccess) return hip_error(e, "rt_decode_prefill");
+  if (d->rope_cs) dfree(d, d->rope_cs);
+  d->rope_cs = nullptr;
+  d->rope_rows = 0;
+  void *p = nullptr;
+  rt_status st = dalloc(d, host.size() * sizeof(float), &p, rt_decode::kPrefill);
+  if (st != RT_OK) return st;
+  e = hipMemcpy(p, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    dfree(d, p);
+    return hip_error(e, "rt_decode_prefill position table");
+  }
+  d->rope_cs = static_cast<float *>(p);
+  d->rope_rows = n;
+  return RT_OK;
 }
 
 rt_status rt_decode_prefill(rt_decode *d, const int32_t *tokens, int32_t n, int32_t start_position, int32_t mode,
@@ -744,6 +762,7 @@ rt_status rt_decode_prefill(rt_decode *d, const int32_t *tokens, int32_t n, int3
     window = w;
   const int cap = std::min(n, d->pf_chunk);
   rt_status st = prefill_reserve(d, cap);
+  if (st == RT_OK) st = prefill_rope_table(d, start_position + n);
   if (st != RT_OK) return st;
   const int D = d->cfg.head_dim;
   hipError_t e = hipSuccess;
@@ -752,17 +771,13 @@ rt_status rt_decode_prefill(rt_decode *d, const int32_t *tokens, int32_t n, int3
     e = hipStreamSynchronize(d->stream);  // the staging buffers are free again
     if (e != hipSuccess) break;
     std::memcpy(d->pf_tokens_host, tokens + c0, (size_t)cn * sizeof(int));
-    prefill_rope_tables(d, start_position + c0, cn);
     e = hipMemcpyAsync(d->pf.tokens, d->pf_tokens_host, (size_t)cn * sizeof(int), hipMemcpyHostToDevice, d->stream);
-    if (e == hipSuccess)
-      e = hipMemcpyAsync(d->pf.cs, d->pf_cs_host, (size_t)cn * 2 * D * sizeof(float), hipMemcpyHostToDevice,
-                         d->stream);
     if (e == hipSuccess) {
       RowsPlan plan;
       plan.n = cn;
       plan.p0 = start_position + c0;
       plan.tokens = d->pf.tokens;
-      plan.cs = d->pf.cs;
+      plan.cs = d->rope_cs + (size_t)(start_position + c0) * 2 * D;
       plan.cs_stride = 2 * D;
       plan.lo_fixed = lo_fixed;
       plan.window = window;
