@@ -557,6 +557,61 @@ __global__ __launch_bounds__(D) void k_pf_attn_combine(const float *__restrict__
   }
 }
 
+// The same merge for the GEMM path with D = 256, one workgroup per row
+// (thread = dimension, the row's nq <= MAXH heads in turn): the merged row
+// goes out as the o projection's A operand, f16 scaled by 2^-ea[t] (bit-
+// identical to the GEMM's own preparation of the f32 row), instead of f32.
+// Rows below row_base (no key) are zero rows.
+template <int MAXH>
+__global__ __launch_bounds__(256) void k_pf_attn_combine_a16(const float *__restrict__ part_ml,
+                                                           const float *__restrict__ part_o, int n, int nq,
+                                                           int splits, int row_base, _Float16 *__restrict__ a16,
+                                                           int *__restrict__ ea) {
+  constexpr int D = 256;
+  __shared__ float w_lds[MAXH][kPfMaxSplits];
+  __shared__ float l_lds[MAXH];
+  __shared__ float red[4];
+  const int t = (int)blockIdx.x, d = (int)threadIdx.x, wave = d >> 6, lane = d & 63;
+  _Float16 *out = a16 + (size_t)t * nq * D;
+  if (t < row_base) {  // block-uniform
+    for (int h = 0; h < nq; ++h) out[h * D + d] = (_Float16)0.f;
+    if (d == 0) ea[t] = 0;
+    return;
+  }
+  const int ncols = (n - row_base) * nq, col0 = (t - row_base) * nq;
+  for (int h = wave; h < nq; h += 4) {  // wave-uniform: split z = lane
+    const bool live = lane < splits;
+    const size_t ci = (size_t)lane * ncols + col0 + h;
+    const float m = live ? part_ml[2 * ci] : -INFINITY;
+    const float l = live ? part_ml[2 * ci + 1] : 0.f;
+    const float M = wave_max(m);
+    const float w = (m == -INFINITY) ? 0.f : expf(m - M);
+    if (live) w_lds[h][lane] = w;
+    const float L = wave_sum(l * w);
+    if (lane == 0) l_lds[h] = L;
+  }
+  __syncthreads();
+  float r[MAXH];
+  float amax = 0.f;
+#pragma unroll
+  for (int h = 0; h < MAXH; ++h) {
+    r[h] = 0.f;
+    if (h < nq) {  // block-uniform
+      float O = 0.f;
+#pragma unroll 8
+      for (int z = 0; z < splits; ++z) O = fmaf(part_o[((size_t)z * ncols + col0 + h) * D + d], w_lds[h][z], O);
+      const float L = l_lds[h];
+      r[h] = L > 0.f ? O / L : 0.f;
+      amax = fmaxf(amax, fabsf(r[h]));
+    }
+  }
+  const int e = f16_exponent_for(block_max<256>(amax, red));
+  if (d == 0) ea[t] = e;
+#pragma unroll
+  for (int h = 0; h < MAXH; ++h)
+    if (h < nq) out[h * D + d] = (_Float16)__builtin_amdgcn_ldexpf(r[h], -e);
+}
+
 template <int D, int W>
 hipError_t launch_pf_attn_w(int G, dim3 grid, hipStream_t st, const float *q, const float *kc, const float *vc,
                             float *out, const PfAttnArgs &p) {
@@ -572,9 +627,12 @@ hipError_t launch_pf_attn_w(int G, dim3 grid, hipStream_t st, const float *q, co
 // grid: (column blocks of 64, KV heads, key splits).  From 256 columns on,
 // workgroups of eight waves take 128 columns each, which halves the K/V stage
 // loads and bf16 splits per column.
+// With a16 (the GEMM path, D = 256, at most 16 q heads) a key-split launch
+// merges straight into the o projection's f16 A operand and sets *a16_done.
 template <int D>
 hipError_t launch_pf_attn(int G, dim3 grid, hipStream_t st, const float *q, const float *kc, const float *vc,
-                          float *out, const PfAttnArgs &p, int8_t *st_dig) {
+                          float *out, const PfAttnArgs &p, int8_t *st_dig, _Float16 *a16 = nullptr,
+                          int *ea = nullptr, bool *a16_done = nullptr) {
   hipError_t e;
   const int na = p.n - p.row_base;
   if (na * G >= 256) {
@@ -585,6 +643,17 @@ hipError_t launch_pf_attn(int G, dim3 grid, hipStream_t st, const float *q, cons
     e = launch_pf_attn_w<D, 4>(G, grid, st, q, kc, vc, out, p);
   }
   if (e != hipSuccess || !p.split_stages) return e;
+  const int nq = p.n_kv_heads * G;
+  if (D == 256 && a16 && !st_dig && nq <= 16) {
+    if (nq <= 8)
+      hipLaunchKernelGGL(k_pf_attn_combine_a16<8>, dim3(p.n), dim3(256), 0, st, p.part_ml, p.part_o, p.n, nq,
+                         (int)grid.z, p.row_base, a16, ea);
+    else
+      hipLaunchKernelGGL(k_pf_attn_combine_a16<16>, dim3(p.n), dim3(256), 0, st, p.part_ml, p.part_o, p.n, nq,
+                         (int)grid.z, p.row_base, a16, ea);
+    *a16_done = true;
+    return hipGetLastError();
+  }
   const int ncols = p.n * p.n_kv_heads * G;
   hipLaunchKernelGGL((k_pf_attn_combine<D>), dim3(ncols), dim3(D), 0, st, p.part_ml, p.part_o, out, ncols,
                      (int)grid.z, p.n_kv_heads * G, st_dig, p.row_base * p.n_kv_heads * G);
@@ -790,9 +859,15 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
     }
     if (agrid.x == 1 || stage) pa.row_base = pa.split_stages ? pa.row_base : 0;
     if (stage && !pa.split_stages) return hipErrorInvalidValue;  // the batched path stages in the merge kernel
-    if (D == 256) PF_TRY(launch_pf_attn<256>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa, stage));
-    else PF_TRY(launch_pf_attn<128>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa, stage));
-    PF_TRY(proj(b.attn, QD, {L.fmt[kProjO]}, {MbMat{L.wo, b.o, H, 0, 0}}, {&vo}, {L.ew[kProjO]}));
+    // on the GEMM path a key-split merge writes the o projection's A itself
+    bool attn_a16 = false;
+    if (D == 256)
+      PF_TRY(launch_pf_attn<256>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa, stage, plan.mb ? nullptr : gemm_a16(QD),
+                                 plan.mb ? nullptr : gemm_ea(QD), &attn_a16));
+    else
+      PF_TRY(launch_pf_attn<128>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa, stage));
+    PF_TRY(proj(attn_a16 ? nullptr : b.attn, QD, {L.fmt[kProjO]}, {MbMat{L.wo, b.o, H, 0, 0}}, {&vo},
+                {L.ew[kProjO]}));
     PF_TRY(launch_pf_norm<true>(n, st, b.hid, vo, L.g_post_attn, L.g_pre_ffn, b.x2, xn_f32, H, a.eps, stage, a16_h,
                                 ea_h));
     // gate|up: Q4_K pairs that would run as one set launch form h = gelu(g)*u
