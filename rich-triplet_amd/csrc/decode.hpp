@@ -40,6 +40,7 @@ struct LayerArgs {
   int global;              // 1: global layer (RoPE theta_global; never windowed)
   int fmt[7];              // RT_LINEAR_* of q, k, v, o, gate, up, down (Q4K for the fused kernels)
   const int *ew[7];        // Q4_K projections: the GEMM's row exponents of the weight, [rows] (else null)
+  float gu_bound;          // Q4_K gate and up: >= max_n |Wgate row n| |Wup row n| (else 0)
 };
 enum Proj { kProjQ, kProjK, kProjV, kProjO, kProjGate, kProjUp, kProjDown };
 
@@ -85,6 +86,7 @@ struct PrefillBuffers {
   float *q = nullptr, *attn = nullptr;  // [cap][n_q_heads*head_dim]
   float *k = nullptr, *v = nullptr;     // [cap][n_kv_heads*head_dim]
   float *g = nullptr, *u = nullptr;     // [cap][ffn]
+  float *nrm2 = nullptr;                // [cap]: |xn|^2 of each row of the gate|up input
   void *ws = nullptr;                   // Q4_K GEMM workspace
   void *mb_stage = nullptr;             // batched-GEMV staging (rows <= 8)
   float *mb_part = nullptr;             // batched-GEMV partial sums

@@ -302,6 +302,26 @@ rt_status rt_decode_set_layer(rt_decode *d, int32_t layer, const rt_gemma3_layer
   return rt_decode_set_layer_formats(d, layer, w, all_q4k, device_ptrs);
 }
 
+// max over n of |Wgate row n| |Wup row n| (dequantised Q4_K rows, F rows of
+// K), rounded up by one part in 2^20; *out = 0 when the product is not finite.
+static rt_status gate_up_bound(rt_decode *d, const uint8_t *wg, const uint8_t *wu, int F, int K, float *out) {
+  void *p = nullptr;
+  rt_status st = dalloc(d, (size_t)2 * F * sizeof(float), &p);
+  if (st != RT_OK) return st;
+  float *nrm = static_cast<float *>(p);
+  hipError_t e = launch_q4k_row_norms(wg, F, K, nrm, d->stream);
+  if (e == hipSuccess) e = launch_q4k_row_norms(wu, F, K, nrm + F, d->stream);
+  std::vector<float> host((size_t)2 * F);
+  if (e == hipSuccess) e = hipMemcpyAsync(host.data(), nrm, host.size() * sizeof(float), hipMemcpyDeviceToHost, d->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
+  dfree(d, p);
+  if (e != hipSuccess) return hip_error(e, "rt_decode_set_layer: gate/up row norms");
+  double m = 0.0;
+  for (int n = 0; n < F; ++n) m = std::max(m, (double)host[n] * (double)host[F + n]);
+  *out = std::isfinite(m) && m < 1e37 ? (float)(m * (1.0 + 0x1p-20)) : 0.f;
+  return RT_OK;
+}
+
 rt_status rt_decode_set_layer_formats(rt_decode *d, int32_t layer, const rt_gemma3_layer *w, const int32_t *formats,
                                       int32_t device_ptrs) {
   if (!d) return set_error(RT_EINVAL, "rt_decode_set_layer: null context");
@@ -391,6 +411,11 @@ rt_status rt_decode_set_layer_formats(rt_decode *d, int32_t layer, const rt_gemm
       L.ew[i] = static_cast<const int *>(q);
     }
   }
+  // The prefill's GELU GEMM bounds h = gelu(g)*u of a row by
+  // |xn|^2 max_n |Wgate row n| |Wup row n|: that maximum, once here.
+  L.gu_bound = 0.f;
+  if (st == RT_OK && formats[kProjGate] == RT_LINEAR_Q4K && formats[kProjUp] == RT_LINEAR_Q4K)
+    st = gate_up_bound(d, L.wgate, L.wup, (int)F, (int)H, &L.gu_bound);
   if (st != RT_OK) {
     for (void *q : own) dfree(d, q);
     return unset(st);
@@ -666,6 +691,7 @@ static rt_status prefill_reserve(rt_decode *d, int cap) {
   PF_GET(v, float, rows * KVD);
   PF_GET(g, float, rows * F);
   PF_GET(u, float, rows * F);
+  PF_GET(nrm2, float, rows);
 #undef PF_GET
   if ((st = get(prefill_gemm_workspace_bytes(d->shape, cap), &b.ws)) != RT_OK) return st;
   if ((st = get(rows_mb_stage_bytes(d->shape), &b.mb_stage)) != RT_OK) return st;

@@ -64,7 +64,7 @@ __global__ __launch_bounds__(T) void k_pf_norm(const float *__restrict__ base, R
                                                  const float *__restrict__ g_add, const float *__restrict__ g_out,
                                                  float *__restrict__ x_out, float *__restrict__ xn_out, int H,
                                                  float eps, int8_t *__restrict__ st_dig, _Float16 *__restrict__ a16,
-                                                 int *__restrict__ ea) {
+                                                 int *__restrict__ ea, float *__restrict__ nrm2_out) {
   constexpr int PER = 1024 / T;
   __shared__ float red[T / 64];
   const int t = (int)blockIdx.x;
@@ -97,7 +97,7 @@ __global__ __launch_bounds__(T) void k_pf_norm(const float *__restrict__ base, R
   const float rx = rms_inv_from_sumsq(block_sum<T>(ss, red), inv_k, eps);
   float4 *xn = reinterpret_cast<float4 *>(xn_out) + off;
   float *st_stats = st_dig ? mb_stats(st_dig, H) : nullptr;
-  float amax = 0.f;
+  float amax = 0.f, nn = 0.f;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int f = threadIdx.x + i * T;
@@ -107,8 +107,13 @@ __global__ __launch_bounds__(T) void k_pf_norm(const float *__restrict__ base, R
     if (f < F4) {
       if (xn_out) xn[f] = v;
       amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+      nn += sumsq4(v);
     }
     if (st_dig) mb_stage4(st_dig, st_stats, t, min(f, F4 - 1) >> 4, f & 15, v, f < F4);  // 16 lanes per chunk
+  }
+  if (nrm2_out) {  // |xn|^2 of the row (block-uniform)
+    nn = block_sum<T>(nn, red);
+    if (threadIdx.x == 0) nrm2_out[t] = nn;
   }
   if (a16) {
     const int e = f16_exponent_for(block_max<T>(amax, red));
@@ -125,13 +130,13 @@ __global__ __launch_bounds__(T) void k_pf_norm(const float *__restrict__ base, R
 template <bool RESID>
 hipError_t launch_pf_norm(int n, hipStream_t st, const float *base, RowsIn add, const float *g_add,
                           const float *g_out, float *x_out, float *xn_out, int H, float eps, int8_t *st_dig,
-                          _Float16 *a16 = nullptr, int *ea = nullptr) {
+                          _Float16 *a16 = nullptr, int *ea = nullptr, float *nrm2_out = nullptr) {
   if (n <= 64)
     hipLaunchKernelGGL((k_pf_norm<RESID, 1024>), dim3(n), dim3(1024), 0, st, base, add, g_add, g_out, x_out, xn_out, H,
-                       eps, st_dig, a16, ea);
+                       eps, st_dig, a16, ea, nrm2_out);
   else
     hipLaunchKernelGGL((k_pf_norm<RESID, 256>), dim3(n), dim3(256), 0, st, base, add, g_add, g_out, x_out, xn_out, H,
-                       eps, st_dig, a16, ea);
+                       eps, st_dig, a16, ea, nrm2_out);
   return hipGetLastError();
 }
 
@@ -202,11 +207,8 @@ __global__ __launch_bounds__(256) void k_pf_gelu_mul(RowsIn g, RowsIn u, float *
 // The same product for the GEMM path, one row per workgroup of kGeluRowT
 // threads (F <= 16384; 1024 threads measured 1% faster over a 4096-row
 // prefill than 256): h goes straight out as the down GEMM's A operand (f16
-// row, exponent ea[t]), bit-identical to preparing the f32 row.  Without
-// GELU the rows of g are h already (the gate|up GEMM formed the product) and
-// are only prepared.
+// row, exponent ea[t]), bit-identical to preparing the f32 row.
 constexpr int kGeluRowT = 1024;
-template <bool GELU>
 __global__ __launch_bounds__(kGeluRowT) void k_pf_gelu_rows(RowsIn g, RowsIn u, int F, _Float16 *__restrict__ a16,
                                                       int *__restrict__ ea) {
   constexpr int MAXP = 16384 / 4 / kGeluRowT;
@@ -218,14 +220,9 @@ __global__ __launch_bounds__(kGeluRowT) void k_pf_gelu_rows(RowsIn g, RowsIn u, 
   for (int i = 0; i < MAXP; ++i) {
     const int c4 = (int)threadIdx.x + kGeluRowT * i;
     if (c4 < f4) {
-      const float4 a = rows_in4(g, t, 4 * c4);
-      if constexpr (GELU) {
-        const float4 b = rows_in4(u, t, 4 * c4);
-        r[i] = make_float4(mul_nc(gelu_tanh(a.x), b.x), mul_nc(gelu_tanh(a.y), b.y), mul_nc(gelu_tanh(a.z), b.z),
-                           mul_nc(gelu_tanh(a.w), b.w));
-      } else {
-        r[i] = a;
-      }
+      const float4 a = rows_in4(g, t, 4 * c4), b = rows_in4(u, t, 4 * c4);
+      r[i] = make_float4(mul_nc(gelu_tanh(a.x), b.x), mul_nc(gelu_tanh(a.y), b.y), mul_nc(gelu_tanh(a.z), b.z),
+                         mul_nc(gelu_tanh(a.w), b.w));
       amax = fmaxf(amax, fmaxf(fmaxf(fabsf(r[i].x), fabsf(r[i].y)), fmaxf(fabsf(r[i].z), fabsf(r[i].w))));
     }
   }
@@ -728,7 +725,8 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
   float *xn_f32 = plan.mb ? b.xn : nullptr;
   // (plan.mb requires every projection in Q4_K; other formats take their own GEMM)
   auto proj = [&](const float *A, int K, std::initializer_list<int> fmts, std::initializer_list<MbMat> mats,
-                  std::initializer_list<RowsIn *> views, std::initializer_list<const int *> ews) {
+                  std::initializer_list<RowsIn *> views, std::initializer_list<const int *> ews,
+                  _Float16 *a16_in = nullptr, int *ea_in = nullptr) {
     if (plan.mb) {
       RowsIn out[3];
       hipError_t r = launch_q4k_gemv_mb(mats.begin(), (int)mats.size(), n, K, b.mb_stage, b.mb_part, st, out);
@@ -737,9 +735,10 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
       return r;
     }
     // A is prepared once for every matrix of the set (q|k|v, gate|up); the
-    // norms and the gelu product write it themselves (A == nullptr)
-    _Float16 *a16 = gemm_a16(K);
-    int *ea = gemm_ea(K);
+    // norms and the gelu product write it themselves (A == nullptr), at
+    // a16_in / ea_in when given
+    _Float16 *a16 = a16_in ? a16_in : gemm_a16(K);
+    int *ea = a16_in ? ea_in : gemm_ea(K);
     // The matrices' regions start after the A part of the largest K: the
     // producer of the next set's A (a norm, the gelu product) writes it
     // while it reads partials left here.
@@ -868,18 +867,20 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
       PF_TRY(launch_pf_attn<128>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa, stage));
     PF_TRY(proj(attn_a16 ? nullptr : b.attn, QD, {L.fmt[kProjO]}, {MbMat{L.wo, b.o, H, 0, 0}}, {&vo},
                 {L.ew[kProjO]}));
-    PF_TRY(launch_pf_norm<true>(n, st, b.hid, vo, L.g_post_attn, L.g_pre_ffn, b.x2, xn_f32, H, a.eps, stage, a16_h,
-                                ea_h));
     // gate|up: Q4_K pairs that would run as one set launch form h = gelu(g)*u
-    // in the GEMM itself (b.g), and the f16 rows of h for the down GEMM are
-    // prepared from it
+    // in the GEMM itself, written as the down GEMM's f16 A operand (rows in
+    // b.g, exponents in b.u) with exponents from |xn|^2 of each row, which the
+    // norm returns
     const bool gelu_gemm = !plan.mb && L.fmt[kProjGate] == RT_LINEAR_Q4K && L.fmt[kProjUp] == RT_LINEAR_Q4K &&
-                           L.ew[kProjGate] && L.ew[kProjUp] && q4k_gemm_gelu_ok(n, F);
+                           L.ew[kProjGate] && L.ew[kProjUp] && L.gu_bound > 0.f && q4k_gemm_gelu_ok(n, F);
+    float *xn_nrm2 = b.nrm2;
+    PF_TRY(launch_pf_norm<true>(n, st, b.hid, vo, L.g_post_attn, L.g_pre_ffn, b.x2, xn_f32, H, a.eps, stage, a16_h,
+                                ea_h, gelu_gemm ? xn_nrm2 : nullptr));
+    _Float16 *h16 = reinterpret_cast<_Float16 *>(b.g);
+    int *eh = reinterpret_cast<int *>(b.u);
     if (gelu_gemm) {
-      PF_TRY(launch_q4k_gemm_gelu_prepped(gemm_a16(H), gemm_ea(H), L.wgate, L.wup, L.ew[kProjGate], L.ew[kProjUp],
-                                          b.g, n, F, H, st));
-      PF_CHECK(hipLaunchKernelGGL(k_pf_gelu_rows<false>, dim3(n), dim3(kGeluRowT), 0, st, rows_plain(b.g, F),
-                                  rows_plain(b.g, F), F, gemm_a16(F), gemm_ea(F)));
+      PF_TRY(launch_q4k_gemm_gelu_prepped(gemm_a16(H), gemm_ea(H), xn_nrm2, L.wgate, L.wup, L.ew[kProjGate],
+                                          L.ew[kProjUp], L.gu_bound, h16, eh, n, F, H, st));
     } else {
       PF_TRY(proj(plan.mb ? b.xn : nullptr, H, {L.fmt[kProjGate], L.fmt[kProjUp]},
                   {MbMat{L.wgate, b.g, F, 0, 0}, MbMat{L.wup, b.u, F, 0, 0}}, {&vg, &vu},
@@ -889,12 +890,12 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
         const unsigned eg = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
         PF_CHECK(hipLaunchKernelGGL(k_pf_gelu_mul, dim3(eg), dim3(256), 0, st, vg, vu, b.g, n, F, stage));
       } else {
-        PF_CHECK(hipLaunchKernelGGL(k_pf_gelu_rows<true>, dim3(n), dim3(kGeluRowT), 0, st, vg, vu, F, gemm_a16(F),
-                                    gemm_ea(F)));
+        PF_CHECK(
+            hipLaunchKernelGGL(k_pf_gelu_rows, dim3(n), dim3(kGeluRowT), 0, st, vg, vu, F, gemm_a16(F), gemm_ea(F)));
       }
     }
     PF_TRY(proj(plan.mb ? b.g : nullptr, F, {L.fmt[kProjDown]}, {MbMat{L.wdown, b.dn, H, 0, 0}}, {&vd},
-                {L.ew[kProjDown]}));
+                {L.ew[kProjDown]}, gelu_gemm ? h16 : nullptr, gelu_gemm ? eh : nullptr));
     if (li + 1 < s.n_layers)
       PF_TRY(launch_pf_norm<true>(n, st, b.x2, vd, L.g_post_ffn, layers[li + 1].g_in, b.hid, xn_f32, H, a.eps,
                                   stage, a16_h, ea_h));

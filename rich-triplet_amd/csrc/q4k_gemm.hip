@@ -332,13 +332,20 @@ __global__ __launch_bounds__(512) void k_q4k_gemm_w8b(const _Float16 *__restrict
 // ---------------------------------------------------------------------------
 constexpr int kHSlotA = 128 * 128;       // bytes
 
-// The GELU epilogue: like store_c_tile<1>, with each staged value
-// gelu_tanh(g) * u of the wave's gate (acc[i][0]) and up (acc[i][1])
-// accumulators, each scaled by 2^(ea[row] + ew of its matrix) as
-// store_c_tile scales them, so h equals the product of the two stored
-// matrices.
-RT_DEV void store_gelu_tile(const floatx16 (&acc)[4][2], float *stage, float *c, int M, int N, int row0, int col0,
-                            const int *ea, const int (&ecol)[2]) {
+// The GELU epilogue: each staged value is gelu_tanh(g) * u of the wave's gate
+// (acc[i][0]) and up (acc[i][1]) accumulators, each scaled by
+// 2^(ea[row] + ew of its matrix) as store_c_tile scales them, and h goes out
+// as the next GEMM's A operand: f16 scaled by 2^-eh[row] with eh[row] =
+// f16_exponent_for(2 * a_nrm2[row] * gu_bound).  By Cauchy-Schwarz
+// |g| <= |a| |w_gate|, |u| <= |a| |w_up| and |gelu_tanh(g)| <= |g|, so
+// |h| <= |a|^2 max_n |w_gate,n| |w_up,n|: a_nrm2 = |a|^2 of the row of A (f32,
+// before its f16 rounding) and gu_bound that maximum; the factor 2 covers
+// the f16 operands and the f32 sums.  No value overflows, and f16 rounding is
+// relative, so h rounds as with the exponent of its exact row maximum except
+// for elements below 2^-14 of the scale.
+RT_DEV void store_gelu_tile(const floatx16 (&acc)[4][2], float *stage, _Float16 *h16, int *eh, int M, int N,
+                            int row0, int col0, const int *ea, const int (&ecol)[2], const float *a_nrm2,
+                            float gu_bound) {
   constexpr int P = 40, F4 = 8, RPI = 8;
   const int lane = (int)(threadIdx.x & 63), g = lane >> 5, l32 = lane & 31;
   const bool vec = (N & 3) == 0;
@@ -362,14 +369,15 @@ RT_DEV void store_gelu_tile(const floatx16 (&acc)[4][2], float *stage, float *c,
       const int row = row0 + 32 * i + rl, col = col0 + 4 * f;
       const float4 v = *reinterpret_cast<const float4 *>(stage + rl * P + 4 * f);
       if (row < M) {
-        float *dst = c + (size_t)row * N + col;
+        const int e = f16_exponent_for(2.0f * a_nrm2[row] * gu_bound);
+        if (col == 0) eh[row] = e;
+        _Float16 *dst = h16 + (size_t)row * N + col;
         if (vec && col + 4 <= N) {
-          *reinterpret_cast<float4 *>(dst) = v;
+          *reinterpret_cast<uint2 *>(dst) = f16x4_scaled(v, e);
         } else {
-          if (col < N) dst[0] = v.x;
-          if (col + 1 < N) dst[1] = v.y;
-          if (col + 2 < N) dst[2] = v.z;
-          if (col + 3 < N) dst[3] = v.w;
+          const float x[4] = {v.x, v.y, v.z, v.w};
+          for (int k = 0; k < 4; ++k)
+            if (col + k < N) dst[k] = (_Float16)__builtin_amdgcn_ldexpf(x[k], -e);
         }
       }
     }
@@ -379,6 +387,33 @@ RT_DEV void store_gelu_tile(const floatx16 (&acc)[4][2], float *stage, float *c,
   }
 }
 
+// |W row n|_2 of a Q4_K weight [N][K] over its dequantised values (one wave
+// per row, f32 sums): the GELU GEMM's bound on |h| is built from them.
+__global__ __launch_bounds__(256) void k_q4k_row_norms(const uint8_t *__restrict__ w, float *__restrict__ nrm, int N,
+                                                       int K) {
+  const int n = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
+  if (n >= N) return;  // whole waves
+  const int kb = K / 256;
+  const uint8_t *row = w + (size_t)n * kb * kQ4KBlockBytes;
+  float ss = 0.f;
+  for (int i = lane; i < kb; i += 64) {
+    const uint8_t *blk = row + (size_t)i * kQ4KBlockBytes;
+    const uint32_t *hw = reinterpret_cast<const uint32_t *>(blk);
+    const float d = half_bits_to_f32(hw[0] & 0xFFFFu), dmin = half_bits_to_f32(hw[0] >> 16);
+    for (int j = 0; j < 8; ++j) {  // sub-block j: the low (even j) or high nibbles of qs[32*(j/2), +32)
+      uint32_t sv, mv;
+      q4k_scale_min(hw[1], hw[2], hw[3], j, sv, mv);
+      const float sc = d * (float)sv, mn = dmin * (float)mv;
+      const uint8_t *qs = blk + 16 + 32 * (j >> 1);
+      for (int b = 0; b < 32; ++b) {
+        const float v = sc * (float)((j & 1) ? (qs[b] >> 4) : (qs[b] & 15)) - mn;
+        ss += v * v;
+      }
+    }
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) nrm[n] = sqrtf(ss);
+}
 
 // The W row exponents of every matrix of a set in one launch: wave r takes
 // row r of the matrices' rows laid end to end.
@@ -388,10 +423,19 @@ __global__ __launch_bounds__(256) void k_gemm_prep_w_multi(HMats mats, int K) {
   if (r < mats.n[i]) prep_w_row(mats.w[i], const_cast<int *>(mats.ew[i]), r, K, threadIdx.x & 63);
 }
 
+// GELU mode's output: h16 [M][N] f16 and its row exponents eh [M]; a_nrm2 and
+// gu_bound as store_gelu_tile uses them.
+struct GeluOut {
+  _Float16 *h16;
+  int *eh;
+  const float *a_nrm2;
+  float gu_bound;
+};
+
 template <bool GELU>
 __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restrict__ a16, const int *__restrict__ ea,
                                                        HMats mats, int M, int K, int tiles_m, int tiles_n,
-                                                       int ksplit) {
+                                                       int ksplit, GeluOut go = {}) {
   __shared__ __attribute__((aligned(1024))) uint8_t sa0[kHSlotA], sa1[kHSlotA], sa2[kHSlotA], sa3[kHSlotA];
 
   const int tid = (int)threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
@@ -573,7 +617,8 @@ __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restric
   static_assert(32 * 72 * 4 <= kHSlotA, "staging slice fits in a slot");
   uint8_t *sbase = wave == 0 ? sa0 : wave == 1 ? sa1 : wave == 2 ? sa2 : sa3;
   if constexpr (GELU)
-    store_gelu_tile(acc, reinterpret_cast<float *>(sbase), c, M, N, m0, n0 + 32 * wave, ea, ecol);
+    store_gelu_tile(acc, reinterpret_cast<float *>(sbase), go.h16, go.eh, M, N, m0, n0 + 32 * wave, ea, ecol,
+                    go.a_nrm2, go.gu_bound);
   else
     store_c_tile<2>(acc, reinterpret_cast<float *>(sbase), c, M, N, m0, n0 + 64 * wave, ea, ecol);
 }
@@ -769,21 +814,26 @@ bool q4k_gemm_gelu_ok(int M, int N) {
   return q4k_gemm_multi_ok(M, 2, n);
 }
 
-hipError_t launch_q4k_gemm_gelu_prepped(const _Float16 *a16, const int *ea, const void *w_gate, const void *w_up,
-                                        const int *ew_gate, const int *ew_up, float *h, int M, int N, int K,
-                                        hipStream_t s) {
-  if (!q4k_gemm_gelu_ok(M, N) || K % 256 != 0 || N <= 0 || !ew_gate || !ew_up) return hipErrorInvalidValue;
+hipError_t launch_q4k_gemm_gelu_prepped(const _Float16 *a16, const int *ea, const float *a_nrm2, const void *w_gate,
+                                        const void *w_up, const int *ew_gate, const int *ew_up, float gu_bound,
+                                        _Float16 *h16, int *eh, int M, int N, int K, hipStream_t s) {
+  if (!q4k_gemm_gelu_ok(M, N) || K % 256 != 0 || N <= 0 || !ew_gate || !ew_up || !a_nrm2 || !(gu_bound >= 0.f))
+    return hipErrorInvalidValue;
   HMats mats{};
   mats.w[0] = static_cast<const uint8_t *>(w_gate);
   mats.w[1] = static_cast<const uint8_t *>(w_up);
   mats.ew[0] = ew_gate;
   mats.ew[1] = ew_up;
-  mats.c[0] = h;
   mats.n[0] = mats.n[1] = N;
   mats.count = 2;
   const int tiles_m = (M + 127) / 128, tiles_n = (N + 127) / 128;
   hipLaunchKernelGGL(k_q4k_gemm_h<true>, dim3(tiles_m * tiles_n), dim3(256), 0, s, a16, ea, mats, M, K, tiles_m,
-                     tiles_n, 1);
+                     tiles_n, 1, GeluOut{h16, eh, a_nrm2, gu_bound});
+  return hipGetLastError();
+}
+
+hipError_t launch_q4k_row_norms(const void *w, int N, int K, float *nrm, hipStream_t s) {
+  hipLaunchKernelGGL(k_q4k_row_norms, dim3((N + 3) / 4), dim3(256), 0, s, static_cast<const uint8_t *>(w), nrm, N, K);
   return hipGetLastError();
 }
 

@@ -70,14 +70,18 @@ hipError_t launch_q4k_gemm_multi_prepped(const _Float16 *a16, const int *ea, int
                                          float *const *c, const int *n, void *const *ws, int M, int K,
                                          hipStream_t s, const int *const *ew_pre = nullptr);
 // An FFN's gate and up Q4_K matrices (N rows each) on a prepared A in one
-// launch that stores h = gelu_tanh(A.Wg^T) * (A.Wu^T) [M][N] in f32 instead
-// of the two products (equal to the product of the two stored matrices),
-// for the shapes q4k_gemm_multi_ok takes as a set; needs both weights' row
+// launch that stores h = gelu_tanh(A.Wg^T) * (A.Wu^T) [M][N] instead of the
+// two products, as the next GEMM's A operand: f16 rows h16 with exponents
+// eh (|h| <= 2 a_nrm2[m] gu_bound sets them).  a_nrm2[m] = |A row m|^2 in f32,
+// gu_bound >= max_n |Wg row n| |Wu row n| (launch_q4k_row_norms); for the
+// shapes q4k_gemm_multi_ok takes as a set; needs both weights' row
 // exponents (launch_q4k_row_exponents).
 bool q4k_gemm_gelu_ok(int M, int N);
-hipError_t launch_q4k_gemm_gelu_prepped(const _Float16 *a16, const int *ea, const void *w_gate, const void *w_up,
-                                        const int *ew_gate, const int *ew_up, float *h, int M, int N, int K,
-                                        hipStream_t s);
+hipError_t launch_q4k_gemm_gelu_prepped(const _Float16 *a16, const int *ea, const float *a_nrm2, const void *w_gate,
+                                        const void *w_up, const int *ew_gate, const int *ew_up, float gu_bound,
+                                        _Float16 *h16, int *eh, int M, int N, int K, hipStream_t s);
+// |W row n|_2 of a Q4_K weight [N][K] (dequantised values) into nrm[N].
+hipError_t launch_q4k_row_norms(const void *w, int N, int K, float *nrm, hipStream_t s);
 // The GEMM's power-of-two row exponents of a Q4_K weight [N][K] (from its
 // block headers) into ew[N]: they depend on the weight alone, so a caller
 // that keeps the weight can compute them once.
