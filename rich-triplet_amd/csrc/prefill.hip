@@ -158,22 +158,41 @@ __global__ __launch_bounds__(256) void k_pf_qk_rope(RowsIn q, RowsIn k, RowsIn v
   if (p0_dev) p0 = p0_dev[0];
   const int t = item / heads, h = item % heads;
   const float *c = cs + (size_t)t * cs_stride + cs_off;
-  // lane pairs (2l, 2l+1) and their partners + D/2 as float2 reads of the
-  // (split-K) projection output, every slice in flight at once
   const int lane = (int)(threadIdx.x & 63);
   auto head = [&](const RowsIn &r, int col, const float *g, float *dst) __attribute__((always_inline)) {
-    float x0[D / 128], x1[D / 128];
     if constexpr (D == 256) {
-      const float2 a = rows_in2(r, t, col + 2 * lane), b = rows_in2(r, t, col + D / 2 + 2 * lane);
-      x0[0] = a.x, x0[1] = a.y, x1[0] = b.x, x1[1] = b.y;
+      // lane l: dims 4l .. 4l+3 in one 16-byte read of the (split-K)
+      // projection output; after the norm, v_permlane32_swap gives every
+      // lane the pair (dim p, dim p + 128), p = 4(l % 32) + e, and lane l
+      // writes its own dims: a0 c - a1 s below 128, a0 s + a1 c above, as
+      // norm_rope_head_regs computes them (sums of squares in another order)
+      const float4 xv = rows_in4(r, t, col + 4 * lane);
+      const float ss = xv.x * xv.x + xv.y * xv.y + xv.z * xv.z + xv.w * xv.w;
+      const float rinv = rms_inv_from_sumsq(wave_sum(ss), 1.0f / (float)D, eps);
+      const float4 gm = reinterpret_cast<const float4 *>(g)[lane];
+      const int pl = lane & 31;
+      const float4 cv = reinterpret_cast<const float4 *>(c)[pl], sv = reinterpret_cast<const float4 *>(c + D / 2)[pl];
+      const float x[4] = {xv.x, xv.y, xv.z, xv.w}, gg[4] = {gm.x, gm.y, gm.z, gm.w};
+      const float cc[4] = {cv.x, cv.y, cv.z, cv.w}, sn[4] = {sv.x, sv.y, sv.z, sv.w};
+      float o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+#pragma clang fp contract(off)
+        const float a = (x[e] * rinv) * (1.0f + gg[e]);
+        const auto sw = __builtin_amdgcn_permlane32_swap(f32_bits(a), f32_bits(a), false, false);
+        const float a0 = bits_f32(sw[0]), a1 = bits_f32(sw[1]);
+        o[e] = lane < 32 ? a0 * cc[e] - a1 * sn[e] : a0 * sn[e] + a1 * cc[e];
+      }
+      reinterpret_cast<float4 *>(dst)[lane] = make_float4(o[0], o[1], o[2], o[3]);
     } else {
+      float x0[D / 128], x1[D / 128];
 #pragma unroll
       for (int pp = 0; pp < D / 128; ++pp) {
         x0[pp] = rows_in1(r, t, col + lane * (D / 128) + pp);
         x1[pp] = rows_in1(r, t, col + D / 2 + lane * (D / 128) + pp);
       }
+      norm_rope_head_regs<D>(x0, x1, g, c, eps, dst);
     }
-    norm_rope_head_regs<D>(x0, x1, g, c, eps, dst);
   };
   if (h < nq) {
     head(q, h * D, g_q, q_out + ((size_t)t * nq + h) * D);
@@ -181,7 +200,10 @@ __global__ __launch_bounds__(256) void k_pf_qk_rope(RowsIn q, RowsIn k, RowsIn v
     const int kh = h - nq;
     const size_t dst = ((size_t)(p0 + t) * nkv + kh) * D;
     head(k, kh * D, g_k, kc + dst);
-    for (int i = 2 * lane; i < D; i += 128) *reinterpret_cast<float2 *>(vc + dst + i) = rows_in2(v, t, kh * D + i);
+    if constexpr (D == 256)
+      reinterpret_cast<float4 *>(vc + dst)[lane] = rows_in4(v, t, kh * D + 4 * lane);
+    else
+      for (int i = 2 * lane; i < D; i += 128) *reinterpret_cast<float2 *>(vc + dst + i) = rows_in2(v, t, kh * D + i);
   }
 }
 
@@ -576,6 +598,17 @@ __global__ __launch_bounds__(256) void k_pf_attn_combine_a16(const float *__rest
     return;
   }
   const int ncols = (n - row_base) * nq, col0 = (t - row_base) * nq;
+  // Up to 8 splits: every partial O of the row is loaded before the weights
+  // are formed (one memory round trip per row instead of two).
+  constexpr int ZP = 8;
+  float po[MAXH][ZP];
+  if (splits <= ZP) {  // block-uniform
+#pragma unroll
+    for (int h = 0; h < MAXH; ++h)
+#pragma unroll
+      for (int z = 0; z < ZP; ++z)
+        po[h][z] = (h < nq && z < splits) ? part_o[((size_t)z * ncols + col0 + h) * D + d] : 0.f;
+  }
   for (int h = wave; h < nq; h += 4) {  // wave-uniform: split z = lane
     const bool live = lane < splits;
     const size_t ci = (size_t)lane * ncols + col0 + h;
@@ -595,8 +628,14 @@ __global__ __launch_bounds__(256) void k_pf_attn_combine_a16(const float *__rest
     r[h] = 0.f;
     if (h < nq) {  // block-uniform
       float O = 0.f;
+      if (splits <= ZP) {
+#pragma unroll
+        for (int z = 0; z < ZP; ++z)
+          if (z < splits) O = fmaf(po[h][z], w_lds[h][z], O);
+      } else {
 #pragma unroll 8
-      for (int z = 0; z < splits; ++z) O = fmaf(part_o[((size_t)z * ncols + col0 + h) * D + d], w_lds[h][z], O);
+        for (int z = 0; z < splits; ++z) O = fmaf(part_o[((size_t)z * ncols + col0 + h) * D + d], w_lds[h][z], O);
+      }
       const float L = l_lds[h];
       r[h] = L > 0.f ? O / L : 0.f;
       amax = fmaxf(amax, fabsf(r[h]));
