@@ -834,19 +834,33 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
     if (li == 0)
       PF_TRY(launch_pf_norm<false>(n, st, nullptr, rows_plain(b.hid, H), nullptr, L.g_in, nullptr, xn_f32, H, a.eps,
                                    stage, a16_h, ea_h));
-    PF_TRY(proj(plan.mb ? b.xn : nullptr, H, {L.fmt[kProjQ], L.fmt[kProjK], L.fmt[kProjV]},
-                {MbMat{L.wq, b.q, QD, 0, 0}, MbMat{L.wk, b.k, KVD, 0, 0}, MbMat{L.wv, b.v, KVD, 0, 0}},
-                {&vq, &vk, &vv}, {L.ew[kProjQ], L.ew[kProjK], L.ew[kProjV]}));
-    const int items = n * (nq + nkv);
     const int cs_off = L.global ? D : 0;
-    if (D == 256)
-      PF_CHECK(hipLaunchKernelGGL(k_pf_qk_rope<256>, dim3((items + 3) / 4), dim3(256), 0, st, vq, vk, vv, b.q,
-                                  L.g_q, L.g_k, plan.cs, plan.cs_stride, cs_off, L.kc, L.vc, plan.p0, plan.p0_dev, n,
-                                  nq, nkv, a.eps));
-    else
-      PF_CHECK(hipLaunchKernelGGL(k_pf_qk_rope<128>, dim3((items + 3) / 4), dim3(256), 0, st, vq, vk, vv, b.q,
-                                  L.g_q, L.g_k, plan.cs, plan.cs_stride, cs_off, L.kc, L.vc, plan.p0, plan.p0_dev, n,
-                                  nq, nkv, a.eps));
+    // q|k|v of a long prompt in Q4_K at head_dim 256: one launch whose
+    // epilogue applies the q/k norms and RoPE and stores k and v straight into
+    // the cache rows (no k_pf_qk_rope)
+    const bool qkv_gemm = !plan.mb && !plan.p0_dev && L.fmt[kProjQ] == RT_LINEAR_Q4K &&
+                          L.fmt[kProjK] == RT_LINEAR_Q4K && L.fmt[kProjV] == RT_LINEAR_Q4K && L.ew[kProjQ] &&
+                          L.ew[kProjK] && L.ew[kProjV] && q4k_gemm_qkv_ok(n, QD, KVD, D);
+    if (qkv_gemm) {
+      const void *w3[3] = {L.wq, L.wk, L.wv};
+      const int *ew3[3] = {L.ew[kProjQ], L.ew[kProjK], L.ew[kProjV]};
+      PF_TRY(launch_q4k_gemm_qkv_prepped(gemm_a16(H), gemm_ea(H), w3, ew3, b.q, L.kc + (size_t)plan.p0 * KVD,
+                                         L.vc + (size_t)plan.p0 * KVD, n, QD, KVD, H, plan.cs + cs_off,
+                                         plan.cs_stride, L.g_q, L.g_k, a.eps, st));
+    } else {
+      PF_TRY(proj(plan.mb ? b.xn : nullptr, H, {L.fmt[kProjQ], L.fmt[kProjK], L.fmt[kProjV]},
+                  {MbMat{L.wq, b.q, QD, 0, 0}, MbMat{L.wk, b.k, KVD, 0, 0}, MbMat{L.wv, b.v, KVD, 0, 0}},
+                  {&vq, &vk, &vv}, {L.ew[kProjQ], L.ew[kProjK], L.ew[kProjV]}));
+      const int items = n * (nq + nkv);
+      if (D == 256)
+        PF_CHECK(hipLaunchKernelGGL(k_pf_qk_rope<256>, dim3((items + 3) / 4), dim3(256), 0, st, vq, vk, vv, b.q,
+                                    L.g_q, L.g_k, plan.cs, plan.cs_stride, cs_off, L.kc, L.vc, plan.p0, plan.p0_dev,
+                                    n, nq, nkv, a.eps));
+      else
+        PF_CHECK(hipLaunchKernelGGL(k_pf_qk_rope<128>, dim3((items + 3) / 4), dim3(256), 0, st, vq, vk, vv, b.q,
+                                    L.g_q, L.g_k, plan.cs, plan.cs_stride, cs_off, L.kc, L.vc, plan.p0, plan.p0_dev,
+                                    n, nq, nkv, a.eps));
+    }
     PfAttnArgs pa;
     pa.p0 = plan.p0;
     pa.p0_dev = plan.p0_dev;

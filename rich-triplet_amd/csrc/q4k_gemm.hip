@@ -432,10 +432,52 @@ struct GeluOut {
   float gu_bound;
 };
 
-template <bool GELU>
+// QKV mode: the per-head RMSNorm (gamma g_q for matrix 0, g_k for matrix 1)
+// and NeoX RoPE of row m with cos | sin at cs + m*cs_stride (+ head_dim),
+// applied before the store; matrix 2 (v) is stored as computed.
+struct QkRope {
+  const float *cs;
+  int cs_stride;
+  const float *g_q, *g_k;
+  float eps;
+};
+
+// Stores a wave's paired column tiles: column tile j of the wave holds the
+// 32 columns col[j] + [0, 32) (QKV mode: a head's columns c and c + 128).
+RT_DEV void store_pair_tile(const floatx16 (&v)[4][2], float *stage, float *c, int M, int N, int row0,
+                            const int (&col)[2]) {
+  constexpr int P = 72, F4 = 16, RPI = 4;
+  const int lane = (int)(threadIdx.x & 63), g = lane >> 5, l32 = lane & 31;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) stage[(8 * (r >> 2) + 4 * g + (r & 3)) * P + 32 * j + l32] = v[i][j][r];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int q = 0; q < 32 / RPI; ++q) {
+      const int rl = q * RPI + lane / F4, f = lane % F4;
+      const int row = row0 + 32 * i + rl, cc = (f < 8 ? col[0] : col[1]) + 4 * (f & 7);
+      const float4 x = *reinterpret_cast<const float4 *>(stage + rl * P + 4 * f);
+      if (row < M) *reinterpret_cast<float4 *>(c + (size_t)row * N + cc) = x;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
+enum HMode { kHPlain = 0, kHGelu = 1, kHQkv = 2 };
+
+template <int MODE>
 __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restrict__ a16, const int *__restrict__ ea,
                                                        HMats mats, int M, int K, int tiles_m, int tiles_n,
-                                                       int ksplit, GeluOut go = {}) {
+                                                       int ksplit, GeluOut go = {}, QkRope qr = {}) {
+  constexpr bool GELU = MODE == kHGelu, QKV = MODE == kHQkv;
+  __shared__ float wsum[4][128];  // QKV mode: each wave's sums of squares of the tile's rows
   __shared__ __attribute__((aligned(1024))) uint8_t sa0[kHSlotA], sa1[kHSlotA], sa2[kHSlotA], sa3[kHSlotA];
 
   const int tid = (int)threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
@@ -449,7 +491,7 @@ __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restric
   const int tm = group * 4 + in_group % gm, tn = in_group / gm;
   int mi = 0;
   if (!GELU)
-    while (mi + 1 < mats.count && tn >= mats.tn0[mi + 1]) ++mi;  // wave-uniform
+    while (mi + 1 < mats.count && tn >= mats.tn0[mi + 1]) ++mi;  // workgroup-uniform
   float *__restrict__ c = mats.c[mi];
   const int N = mats.n[mi];
   const int m0 = tm * 128, n0 = GELU ? tn * 128 : (tn - mats.tn0[mi]) * 256;
@@ -488,7 +530,7 @@ __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restric
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int wm = GELU ? j : mi;
-    colw[j] = GELU ? 32 * wave + l32 : 64 * wave + 32 * j + l32;
+    colw[j] = GELU ? 32 * wave + l32 : QKV ? 32 * wave + 128 * j + l32 : 64 * wave + 32 * j + l32;
     const int n = min(n0 + colw[j], N - 1);
     ewc[j] = mats.ew[wm][n];
     bpw[j] = __builtin_amdgcn_ldexpf(g ? 0.0625f : 1.0f, -ewc[j]);
@@ -616,11 +658,80 @@ __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restric
   wg_barrier();
   static_assert(32 * 72 * 4 <= kHSlotA, "staging slice fits in a slot");
   uint8_t *sbase = wave == 0 ? sa0 : wave == 1 ? sa1 : wave == 2 ? sa2 : sa3;
-  if constexpr (GELU)
+  if constexpr (GELU) {
     store_gelu_tile(acc, reinterpret_cast<float *>(sbase), go.h16, go.eh, M, N, m0, n0 + 32 * wave, ea, ecol,
                     go.a_nrm2, go.gu_bound);
-  else
+  } else if constexpr (QKV) {
+    // The tile is one head (256 columns) of 128 rows; lane (g, l32) of wave w
+    // holds columns c = 32w + l32 (j = 0) and c + 128 (j = 1), the RoPE pair.
+    floatx16(&val)[4][2] = acc;  // scaled in place
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int er = ea[min(m0 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3), M - 1)];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) val[i][j][r] = __builtin_amdgcn_ldexpf(acc[i][j][r], er + ecol[j]);
+      }
+    }
+    const int colp[2] = {n0 + 32 * wave, n0 + 128 + 32 * wave};
+    if (mi < 2) {
+      // sums of squares of the rows: this wave's 64 columns through its LDS
+      // slot ([row][l32], the 16-byte group index swizzled by the row), then
+      // the four waves' partial sums through wsum
+      float *red = reinterpret_cast<float *>(sbase);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int R = 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+          const float q2 = val[i][0][r] * val[i][0][r] + val[i][1][r] * val[i][1][r];
+          red[R * 32 + ((((l32 >> 2) ^ R) & 7) << 2) + (l32 & 3)] = q2;
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int R = lane + 64 * k;
+        float t = 0.f;
+#pragma unroll
+        for (int m4 = 0; m4 < 8; ++m4) {
+          const float4 x = *reinterpret_cast<const float4 *>(red + R * 32 + (((m4 ^ R) & 7) << 2));
+          t += (x.x + x.y) + (x.z + x.w);
+        }
+        wsum[wave][R] = t;
+      }
+      wg_barrier();
+      const float *gam = mi == 0 ? qr.g_q : qr.g_k;
+      const int cl = 32 * wave + l32;  // the pair's column within the head
+      const float g0 = 1.0f + gam[cl], g1 = 1.0f + gam[cl + 128];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        __builtin_amdgcn_sched_barrier(0);  // one 32-row tile's cos/sin loads in flight at a time
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+#pragma clang fp contract(off)
+          const int R = 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+          const float ss = (wsum[0][R] + wsum[1][R]) + (wsum[2][R] + wsum[3][R]);
+          const float rinv = rms_inv_from_sumsq(ss, 1.0f / 256.0f, qr.eps);
+          const int co = min(m0 + R, M - 1) * qr.cs_stride + cl;  // 32-bit offset from the uniform base
+          const float cv = qr.cs[co], sv = qr.cs[co + 128];
+          const float a0 = (val[i][0][r] * rinv) * g0, a1 = (val[i][1][r] * rinv) * g1;
+          val[i][0][r] = a0 * cv - a1 * sv;
+          val[i][1][r] = a0 * sv + a1 * cv;
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    store_pair_tile(val, reinterpret_cast<float *>(sbase), c, M, N, m0, colp);
+  } else {
     store_c_tile<2>(acc, reinterpret_cast<float *>(sbase), c, M, N, m0, n0 + 64 * wave, ea, ecol);
+  }
 }
 
 }  // namespace
@@ -741,7 +852,7 @@ static hipError_t q4k_gemm_core(const _Float16 *a16, const int *ea, const uint8_
       hipLaunchKernelGGL(k_q4k_gemm_w8b<1>, dim3(tiles_m * tiles_n, ks), dim3(512), 0, s, a16, ea, wb, ew, out, M,
                          N, K, tiles_m, tiles_n, ks);
     else
-      hipLaunchKernelGGL(k_q4k_gemm_h<false>, dim3(tiles_m * tiles_n, ks), dim3(256), 0, s, a16, ea,
+      hipLaunchKernelGGL(k_q4k_gemm_h<kHPlain>, dim3(tiles_m * tiles_n, ks), dim3(256), 0, s, a16, ea,
                          HMats{{wb}, {ew}, {out}, {N}, {0}, 1}, M, K, tiles_m, tiles_n, ks);
     e = hipGetLastError();
   }
@@ -827,8 +938,38 @@ hipError_t launch_q4k_gemm_gelu_prepped(const _Float16 *a16, const int *ea, cons
   mats.n[0] = mats.n[1] = N;
   mats.count = 2;
   const int tiles_m = (M + 127) / 128, tiles_n = (N + 127) / 128;
-  hipLaunchKernelGGL(k_q4k_gemm_h<true>, dim3(tiles_m * tiles_n), dim3(256), 0, s, a16, ea, mats, M, K, tiles_m,
+  hipLaunchKernelGGL(k_q4k_gemm_h<kHGelu>, dim3(tiles_m * tiles_n), dim3(256), 0, s, a16, ea, mats, M, K, tiles_m,
                      tiles_n, 1, GeluOut{h16, eh, a_nrm2, gu_bound});
+  return hipGetLastError();
+}
+
+bool q4k_gemm_qkv_ok(int M, int QD, int KVD, int head_dim) {
+  const int n[3] = {QD, KVD, KVD};
+  return head_dim == 256 && QD % 256 == 0 && KVD % 256 == 0 && q4k_gemm_multi_ok(M, 3, n);
+}
+
+hipError_t launch_q4k_gemm_qkv_prepped(const _Float16 *a16, const int *ea, const void *const *w, const int *const *ew,
+                                       float *q_out, float *k_rows, float *v_rows, int M, int QD, int KVD, int K,
+                                       const float *cs, int cs_stride, const float *g_q, const float *g_k, float eps,
+                                       hipStream_t s) {
+  if (!q4k_gemm_qkv_ok(M, QD, KVD, 256) || K % 256 != 0) return hipErrorInvalidValue;
+  HMats mats{};
+  float *out[3] = {q_out, k_rows, v_rows};
+  const int n[3] = {QD, KVD, KVD};
+  int tiles_n = 0;
+  for (int i = 0; i < 3; ++i) {
+    if (!w[i] || !ew[i]) return hipErrorInvalidValue;
+    mats.w[i] = static_cast<const uint8_t *>(w[i]);
+    mats.ew[i] = ew[i];
+    mats.c[i] = out[i];
+    mats.n[i] = n[i];
+    mats.tn0[i] = tiles_n;
+    tiles_n += n[i] / 256;
+  }
+  mats.count = 3;
+  const int tiles_m = (M + 127) / 128;
+  hipLaunchKernelGGL(k_q4k_gemm_h<kHQkv>, dim3(tiles_m * tiles_n), dim3(256), 0, s, a16, ea, mats, M, K, tiles_m,
+                     tiles_n, 1, GeluOut{}, QkRope{cs, cs_stride, g_q, g_k, eps});
   return hipGetLastError();
 }
 
@@ -864,7 +1005,7 @@ hipError_t launch_q4k_gemm_multi_prepped(const _Float16 *a16, const int *ea, int
     if (e != hipSuccess) return e;
   }
   const int tiles_m = (M + 127) / 128;
-  hipLaunchKernelGGL(k_q4k_gemm_h<false>, dim3(tiles_m * tiles_n), dim3(256), 0, s, a16, ea, mats, M, K, tiles_m, tiles_n,
+  hipLaunchKernelGGL(k_q4k_gemm_h<kHPlain>, dim3(tiles_m * tiles_n), dim3(256), 0, s, a16, ea, mats, M, K, tiles_m, tiles_n,
                      1);
   return hipGetLastError();
 }

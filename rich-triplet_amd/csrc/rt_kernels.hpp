@@ -80,6 +80,16 @@ bool q4k_gemm_gelu_ok(int M, int N);
 hipError_t launch_q4k_gemm_gelu_prepped(const _Float16 *a16, const int *ea, const float *a_nrm2, const void *w_gate,
                                         const void *w_up, const int *ew_gate, const int *ew_up, float gu_bound,
                                         _Float16 *h16, int *eh, int M, int N, int K, hipStream_t s);
+// The q, k and v Q4_K matrices of an attention layer (QD, KVD, KVD rows,
+// head_dim 256) on a prepared A in one launch that applies the per-head
+// RMSNorm (gammas g_q, g_k) and NeoX RoPE (row m's cos | sin at
+// cs + m*cs_stride, 128 each) to q and k before storing: q_out [M][QD],
+// k_rows and v_rows [M][KVD] (the KV cache rows of positions p0 .. p0+M-1).
+bool q4k_gemm_qkv_ok(int M, int QD, int KVD, int head_dim);
+hipError_t launch_q4k_gemm_qkv_prepped(const _Float16 *a16, const int *ea, const void *const *w, const int *const *ew,
+                                       float *q_out, float *k_rows, float *v_rows, int M, int QD, int KVD, int K,
+                                       const float *cs, int cs_stride, const float *g_q, const float *g_k, float eps,
+                                       hipStream_t s);
 // |W row n|_2 of a Q4_K weight [N][K] (dequantised values) into nrm[N].
 hipError_t launch_q4k_row_norms(const void *w, int N, int K, float *nrm, hipStream_t s);
 // The GEMM's power-of-two row exponents of a Q4_K weight [N][K] (from its
