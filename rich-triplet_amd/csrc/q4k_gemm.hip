@@ -442,34 +442,6 @@ struct QkRope {
   float eps;
 };
 
-// Stores a wave's paired column tiles: column tile j of the wave holds the
-// 32 columns col[j] + [0, 32) (QKV mode: a head's columns c and c + 128).
-RT_DEV void store_pair_tile(const floatx16 (&v)[4][2], float *stage, float *c, int M, int N, int row0,
-                            const int (&col)[2]) {
-  constexpr int P = 72, F4 = 16, RPI = 4;
-  const int lane = (int)(threadIdx.x & 63), g = lane >> 5, l32 = lane & 31;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) stage[(8 * (r >> 2) + 4 * g + (r & 3)) * P + 32 * j + l32] = v[i][j][r];
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int q = 0; q < 32 / RPI; ++q) {
-      const int rl = q * RPI + lane / F4, f = lane % F4;
-      const int row = row0 + 32 * i + rl, cc = (f < 8 ? col[0] : col[1]) + 4 * (f & 7);
-      const float4 x = *reinterpret_cast<const float4 *>(stage + rl * P + 4 * f);
-      if (row < M) *reinterpret_cast<float4 *>(c + (size_t)row * N + cc) = x;
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  }
-}
-
 enum HMode { kHPlain = 0, kHGelu = 1, kHQkv = 2 };
 
 template <int MODE>
@@ -477,7 +449,6 @@ __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restric
                                                        HMats mats, int M, int K, int tiles_m, int tiles_n,
                                                        int ksplit, GeluOut go = {}, QkRope qr = {}) {
   constexpr bool GELU = MODE == kHGelu, QKV = MODE == kHQkv;
-  __shared__ float wsum[4][128];  // QKV mode: each wave's sums of squares of the tile's rows
   __shared__ __attribute__((aligned(1024))) uint8_t sa0[kHSlotA], sa1[kHSlotA], sa2[kHSlotA], sa3[kHSlotA];
 
   const int tid = (int)threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
@@ -664,53 +635,50 @@ __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restric
   } else if constexpr (QKV) {
     // The tile is one head (256 columns) of 128 rows; lane (g, l32) of wave w
     // holds columns c = 32w + l32 (j = 0) and c + 128 (j = 1), the RoPE pair.
-    floatx16(&val)[4][2] = acc;  // scaled in place
+    // One 32-row MFMA tile (i) at a time, so its accumulators are free once
+    // it is stored.
+    float *stage = reinterpret_cast<float *>(sbase);
+    // each wave's sums of squares of the tile's rows: the last 2 KB of slot 3
+    // (the staging slices use the first 9 KB of each slot)
+    float(*wsum)[128] = reinterpret_cast<float(*)[128]>(sa3 + kHSlotA - 2048);
+    const int colp[2] = {n0 + 32 * wave, n0 + 128 + 32 * wave};
+    const int cl = 32 * wave + l32;  // the pair's column within the head
+    const float *gam = mi == 0 ? qr.g_q : qr.g_k;
+    const float g0 = mi < 2 ? 1.0f + gam[cl] : 0.f, g1 = mi < 2 ? 1.0f + gam[cl + 128] : 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_sched_barrier(0);
+      floatx16 v0, v1;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int er = ea[min(m0 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3), M - 1)];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) val[i][j][r] = __builtin_amdgcn_ldexpf(acc[i][j][r], er + ecol[j]);
+        v0[r] = __builtin_amdgcn_ldexpf(acc[i][0][r], er + ecol[0]);
+        v1[r] = __builtin_amdgcn_ldexpf(acc[i][1][r], er + ecol[1]);
       }
-    }
-    const int colp[2] = {n0 + 32 * wave, n0 + 128 + 32 * wave};
-    if (mi < 2) {
-      // sums of squares of the rows: this wave's 64 columns through its LDS
-      // slot ([row][l32], the 16-byte group index swizzled by the row), then
-      // the four waves' partial sums through wsum
-      float *red = reinterpret_cast<float *>(sbase);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        __builtin_amdgcn_sched_barrier(0);
+      if (mi < 2) {  // workgroup-uniform
+        // sums of squares of the 32 rows: this wave's 64 columns through its
+        // LDS slot ([row][l32], 16-byte groups swizzled by the row), two
+        // lanes per row, then the four waves' sums through wsum
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int R = 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
-          const float q2 = val[i][0][r] * val[i][0][r] + val[i][1][r] * val[i][1][r];
-          red[R * 32 + ((((l32 >> 2) ^ R) & 7) << 2) + (l32 & 3)] = q2;
+          const int R = 8 * (r >> 2) + 4 * g + (r & 3);
+          stage[R * 32 + ((((l32 >> 2) ^ R) & 7) << 2) + (l32 & 3)] = v0[r] * v0[r] + v1[r] * v1[r];
         }
-      }
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        {
+          const int R = lane >> 1;
+          float t = 0.f;
 #pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const int R = lane + 64 * k;
-        float t = 0.f;
-#pragma unroll
-        for (int m4 = 0; m4 < 8; ++m4) {
-          const float4 x = *reinterpret_cast<const float4 *>(red + R * 32 + (((m4 ^ R) & 7) << 2));
-          t += (x.x + x.y) + (x.z + x.w);
+          for (int m4 = 4 * (lane & 1); m4 < 4 * (lane & 1) + 4; ++m4) {
+            const float4 x = *reinterpret_cast<const float4 *>(stage + R * 32 + (((m4 ^ R) & 7) << 2));
+            t += (x.x + x.y) + (x.z + x.w);
+          }
+          t += __shfl_xor(t, 1);
+          if ((lane & 1) == 0) wsum[wave][32 * i + R] = t;
         }
-        wsum[wave][R] = t;
-      }
-      wg_barrier();
-      const float *gam = mi == 0 ? qr.g_q : qr.g_k;
-      const int cl = 32 * wave + l32;  // the pair's column within the head
-      const float g0 = 1.0f + gam[cl], g1 = 1.0f + gam[cl + 128];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        __builtin_amdgcn_sched_barrier(0);  // one 32-row tile's cos/sin loads in flight at a time
+        wg_barrier();
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
 #pragma clang fp contract(off)
@@ -719,16 +687,35 @@ __global__ __launch_bounds__(256, 2) void k_q4k_gemm_h(const _Float16 *__restric
           const float rinv = rms_inv_from_sumsq(ss, 1.0f / 256.0f, qr.eps);
           const int co = min(m0 + R, M - 1) * qr.cs_stride + cl;  // 32-bit offset from the uniform base
           const float cv = qr.cs[co], sv = qr.cs[co + 128];
-          const float a0 = (val[i][0][r] * rinv) * g0, a1 = (val[i][1][r] * rinv) * g1;
-          val[i][0][r] = a0 * cv - a1 * sv;
-          val[i][1][r] = a0 * sv + a1 * cv;
+          const float a0 = (v0[r] * rinv) * g0, a1 = (v1[r] * rinv) * g1;
+          v0[r] = a0 * cv - a1 * sv;
+          v1[r] = a0 * sv + a1 * cv;
         }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+      // stage and store the tile's 32 rows x (32 + 32) columns
+      constexpr int P = 72;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        stage[(8 * (r >> 2) + 4 * g + (r & 3)) * P + l32] = v0[r];
+        stage[(8 * (r >> 2) + 4 * g + (r & 3)) * P + 32 + l32] = v1[r];
+      }
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int rl = q * 4 + lane / 16, f = lane % 16;
+        const int row = m0 + 32 * i + rl, cc = colp[f >> 3] + 4 * (f & 7);
+        const float4 x = *reinterpret_cast<const float4 *>(stage + rl * P + 4 * f);
+        if (row < M) *reinterpret_cast<float4 *>(c + (size_t)row * N + cc) = x;
       }
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    store_pair_tile(val, reinterpret_cast<float *>(sbase), c, M, N, m0, colp);
   } else {
     store_c_tile<2>(acc, reinterpret_cast<float *>(sbase), c, M, N, m0, n0 + 64 * wave, ea, ecol);
   }
