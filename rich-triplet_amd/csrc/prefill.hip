@@ -64,7 +64,7 @@ __global__ __launch_bounds__(T) void k_pf_norm(const float *__restrict__ base, R
                                                  const float *__restrict__ g_add, const float *__restrict__ g_out,
                                                  float *__restrict__ x_out, float *__restrict__ xn_out, int H,
                                                  float eps, int8_t *__restrict__ st_dig, _Float16 *__restrict__ a16,
-                                                 int *__restrict__ ea, float *__restrict__ nrm2_out) {
+                                                 int *__restrict__ ea, float *__restrict__ nrm2_out, int add_row0) {
   constexpr int PER = 1024 / T;
   __shared__ float red[T / 64];
   const int t = (int)blockIdx.x;
@@ -76,7 +76,7 @@ __global__ __launch_bounds__(T) void k_pf_norm(const float *__restrict__ base, R
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int f = threadIdx.x + i * T;
-    x[i] = f < F4 ? rows_in4(add, t, 4 * f) : make_float4(0.f, 0.f, 0.f, 0.f);
+    x[i] = f < F4 && t >= add_row0 ? rows_in4(add, t, 4 * f) : make_float4(0.f, 0.f, 0.f, 0.f);
     ss += sumsq4(x[i]);
   }
   if constexpr (RESID) {
@@ -130,13 +130,13 @@ __global__ __launch_bounds__(T) void k_pf_norm(const float *__restrict__ base, R
 template <bool RESID>
 hipError_t launch_pf_norm(int n, hipStream_t st, const float *base, RowsIn add, const float *g_add,
                           const float *g_out, float *x_out, float *xn_out, int H, float eps, int8_t *st_dig,
-                          _Float16 *a16 = nullptr, int *ea = nullptr, float *nrm2_out = nullptr) {
+                          _Float16 *a16 = nullptr, int *ea = nullptr, float *nrm2_out = nullptr, int add_row0 = 0) {
   if (n <= 64)
     hipLaunchKernelGGL((k_pf_norm<RESID, 1024>), dim3(n), dim3(1024), 0, st, base, add, g_add, g_out, x_out, xn_out, H,
-                       eps, st_dig, a16, ea, nrm2_out);
+                       eps, st_dig, a16, ea, nrm2_out, add_row0);
   else
     hipLaunchKernelGGL((k_pf_norm<RESID, 256>), dim3(n), dim3(256), 0, st, base, add, g_add, g_out, x_out, xn_out, H,
-                       eps, st_dig, a16, ea, nrm2_out);
+                       eps, st_dig, a16, ea, nrm2_out, add_row0);
   return hipGetLastError();
 }
 
@@ -580,17 +580,18 @@ __global__ __launch_bounds__(D) void k_pf_attn_combine(const float *__restrict__
 // (thread = dimension, the row's nq <= MAXH heads in turn): the merged row
 // goes out as the o projection's A operand, f16 scaled by 2^-ea[t] (bit-
 // identical to the GEMM's own preparation of the f32 row), instead of f32.
-// Rows below row_base (no key) are zero rows.
+// Rows below row_base (no key) are zero rows; workgroup b takes row
+// row_first + b (row_first = row_base: the zero rows are not written).
 template <int MAXH>
 __global__ __launch_bounds__(256) void k_pf_attn_combine_a16(const float *__restrict__ part_ml,
                                                            const float *__restrict__ part_o, int n, int nq,
-                                                           int splits, int row_base, _Float16 *__restrict__ a16,
-                                                           int *__restrict__ ea) {
+                                                           int splits, int row_base, int row_first,
+                                                           _Float16 *__restrict__ a16, int *__restrict__ ea) {
   constexpr int D = 256;
   __shared__ float w_lds[MAXH][kPfMaxSplits];
   __shared__ float l_lds[MAXH];
   __shared__ float red[4];
-  const int t = (int)blockIdx.x, d = (int)threadIdx.x, wave = d >> 6, lane = d & 63;
+  const int t = row_first + (int)blockIdx.x, d = (int)threadIdx.x, wave = d >> 6, lane = d & 63;
   _Float16 *out = a16 + (size_t)t * nq * D;
   if (t < row_base) {  // block-uniform
     for (int h = 0; h < nq; ++h) out[h * D + d] = (_Float16)0.f;
@@ -664,11 +665,13 @@ hipError_t launch_pf_attn_w(int G, dim3 grid, hipStream_t st, const float *q, co
 // workgroups of eight waves take 128 columns each, which halves the K/V stage
 // loads and bf16 splits per column.
 // With a16 (the GEMM path, D = 256, at most 16 q heads) a key-split launch
-// merges straight into the o projection's f16 A operand and sets *a16_done.
+// merges straight into the o projection's f16 A operand and sets *a16_row0
+// to the first row it writes: p.row_base with skip_zero_rows (the rows below
+// see no key, their A rows are left unwritten), else 0.
 template <int D>
 hipError_t launch_pf_attn(int G, dim3 grid, hipStream_t st, const float *q, const float *kc, const float *vc,
                           float *out, const PfAttnArgs &p, int8_t *st_dig, _Float16 *a16 = nullptr,
-                          int *ea = nullptr, bool *a16_done = nullptr) {
+                          int *ea = nullptr, int *a16_row0 = nullptr, bool skip_zero_rows = false) {
   hipError_t e;
   const int na = p.n - p.row_base;
   if (na * G >= 256) {
@@ -681,13 +684,14 @@ hipError_t launch_pf_attn(int G, dim3 grid, hipStream_t st, const float *q, cons
   if (e != hipSuccess || !p.split_stages) return e;
   const int nq = p.n_kv_heads * G;
   if (D == 256 && a16 && !st_dig && nq <= 16) {
+    const int row_first = skip_zero_rows ? p.row_base : 0;
     if (nq <= 8)
-      hipLaunchKernelGGL(k_pf_attn_combine_a16<8>, dim3(p.n), dim3(256), 0, st, p.part_ml, p.part_o, p.n, nq,
-                         (int)grid.z, p.row_base, a16, ea);
+      hipLaunchKernelGGL(k_pf_attn_combine_a16<8>, dim3(p.n - row_first), dim3(256), 0, st, p.part_ml, p.part_o, p.n,
+                         nq, (int)grid.z, p.row_base, row_first, a16, ea);
     else
-      hipLaunchKernelGGL(k_pf_attn_combine_a16<16>, dim3(p.n), dim3(256), 0, st, p.part_ml, p.part_o, p.n, nq,
-                         (int)grid.z, p.row_base, a16, ea);
-    *a16_done = true;
+      hipLaunchKernelGGL(k_pf_attn_combine_a16<16>, dim3(p.n - row_first), dim3(256), 0, st, p.part_ml, p.part_o,
+                         p.n, nq, (int)grid.z, p.row_base, row_first, a16, ea);
+    *a16_row0 = row_first;
     return hipGetLastError();
   }
   const int ncols = p.n * p.n_kv_heads * G;
@@ -912,14 +916,30 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
     if (agrid.x == 1 || stage) pa.row_base = pa.split_stages ? pa.row_base : 0;
     if (stage && !pa.split_stages) return hipErrorInvalidValue;  // the batched path stages in the merge kernel
     // on the GEMM path a key-split merge writes the o projection's A itself
-    bool attn_a16 = false;
+    // (rows that see no key have a zero attention row, so a zero o row: with
+    // a Q4_K o the merge leaves them out, the o GEMM runs on the rows from
+    // o_row0 on, and the norm below adds nothing for the rows before)
+    int attn_row0 = -1;
+    const bool o_q4k = L.fmt[kProjO] == RT_LINEAR_Q4K;
     if (D == 256)
       PF_TRY(launch_pf_attn<256>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa, stage, plan.mb ? nullptr : gemm_a16(QD),
-                                 plan.mb ? nullptr : gemm_ea(QD), &attn_a16));
+                                 plan.mb ? nullptr : gemm_ea(QD), &attn_row0, o_q4k));
     else
       PF_TRY(launch_pf_attn<128>(G, agrid, st, b.q, L.kc, L.vc, b.attn, pa, stage));
-    PF_TRY(proj(attn_a16 ? nullptr : b.attn, QD, {L.fmt[kProjO]}, {MbMat{L.wo, b.o, H, 0, 0}}, {&vo},
-                {L.ew[kProjO]}));
+    int o_row0 = 0;
+    if (attn_row0 > 0) {
+      o_row0 = attn_row0;
+      const int m = n - o_row0;
+      char *rest = static_cast<char *>(b.ws) + r256((size_t)n * kmax * 2) + r256((size_t)n * 4);
+      GemmLeft left{};
+      PF_TRY(launch_q4k_gemm_prepped(gemm_a16(QD) + (size_t)o_row0 * QD, gemm_ea(QD) + o_row0, L.wo,
+                                     b.o + (size_t)o_row0 * H, m, H, QD, rest, st, &left, L.ew[kProjO]));
+      // rows indexed from 0: the partial tiles of row t start (t - o_row0) rows in
+      vo = left.ks > 1 ? RowsIn{left.part - (size_t)o_row0 * H, left.ks, (size_t)m * H, H, 0} : rows_plain(b.o, H);
+    } else {
+      PF_TRY(proj(attn_row0 >= 0 ? nullptr : b.attn, QD, {L.fmt[kProjO]}, {MbMat{L.wo, b.o, H, 0, 0}}, {&vo},
+                  {L.ew[kProjO]}));
+    }
     // gate|up: Q4_K pairs that would run as one set launch form h = gelu(g)*u
     // in the GEMM itself, written as the down GEMM's f16 A operand (rows in
     // b.g, exponents in b.u) with exponents from |xn|^2 of each row, which the
@@ -928,7 +948,7 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
                            L.ew[kProjGate] && L.ew[kProjUp] && L.gu_bound > 0.f && q4k_gemm_gelu_ok(n, F);
     float *xn_nrm2 = b.nrm2;
     PF_TRY(launch_pf_norm<true>(n, st, b.hid, vo, L.g_post_attn, L.g_pre_ffn, b.x2, xn_f32, H, a.eps, stage, a16_h,
-                                ea_h, gelu_gemm ? xn_nrm2 : nullptr));
+                                ea_h, gelu_gemm ? xn_nrm2 : nullptr, o_row0));
     _Float16 *h16 = reinterpret_cast<_Float16 *>(b.g);
     int *eh = reinterpret_cast<int *>(b.u);
     if (gelu_gemm) {
