@@ -123,6 +123,12 @@ struct RowsPlan {
   bool mb = false;
   int logits = kNone;
   float *xn_b = nullptr, *logits_b = nullptr;
+  // Layers [layer_begin, n_layers); qkv_done: the first of them has its
+  // q|k|v step done (normalised, rotated q in the buffers' q rows, K/V in
+  // the cache) and starts at its attention; last_layer_kv_only: the last
+  // layer stops after its q|k|v step (no logits then).
+  int layer_begin = 0;
+  bool qkv_done = false, last_layer_kv_only = false;
 };
 hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers, const PrefillBuffers &b,
                         const RowsPlan &plan, hipStream_t stream);

@@ -809,8 +809,39 @@ rt_status rt_decode_prefill(rt_decode *d, const int32_t *tokens, int32_t n, int3
       plan.window = window;
       plan.max_pos = start_position + c0 + cn;
       plan.mb = cn <= kMaxBatch && d->all_q4k;  // a few rows: one pass over the weights beats the GEMM's tiles
-      plan.logits = c0 + cn == n ? RowsPlan::kLastRow : RowsPlan::kNone;
-      e = enqueue_rows(d->shape, d->args, d->layers.data(), d->pf, plan, d->stream);
+      const bool last_chunk = c0 + cn == n;
+      if (cn == 1) {
+        plan.logits = last_chunk ? RowsPlan::kLastRow : RowsPlan::kNone;
+        e = enqueue_rows(d->shape, d->args, d->layers.data(), d->pf, plan, d->stream);
+      } else {
+        // The last layer's attention, o projection and FFN only feed the
+        // logits: every row runs up to the last layer's K/V rows, and the
+        // prompt's last row alone (if its logits are wanted) runs the rest.
+        plan.logits = RowsPlan::kNone;
+        plan.last_layer_kv_only = true;
+        e = enqueue_rows(d->shape, d->args, d->layers.data(), d->pf, plan, d->stream);
+        if (e == hipSuccess && last_chunk) {
+          const size_t r = (size_t)cn - 1;
+          const rt_gemma3_config &c = d->cfg;
+          const size_t Hs = c.hidden, Fs = c.ffn, QDs = (size_t)c.n_q_heads * D, KVDs = (size_t)c.n_kv_heads * D;
+          PrefillBuffers tb = d->pf;  // the buffers' rows from the last one on
+          tb.tokens += r;
+          tb.hid += r * Hs, tb.x2 += r * Hs, tb.xn += r * Hs, tb.o += r * Hs, tb.dn += r * Hs;
+          tb.q += r * QDs, tb.attn += r * QDs, tb.k += r * KVDs, tb.v += r * KVDs;
+          tb.g += r * Fs, tb.u += r * Fs, tb.nrm2 += r;
+          RowsPlan tail = plan;
+          tail.n = 1;
+          tail.p0 = plan.p0 + (int)r;
+          tail.tokens = tb.tokens;
+          tail.cs = plan.cs + r * 2 * D;
+          tail.mb = d->all_q4k;
+          tail.logits = RowsPlan::kLastRow;
+          tail.layer_begin = c.n_layers - 1;
+          tail.qkv_done = true;
+          tail.last_layer_kv_only = false;
+          e = enqueue_rows(d->shape, d->args, d->layers.data(), tb, tail, d->stream);
+        }
+      }
     }
   }
   if (e == hipSuccess && logits_host)

@@ -831,18 +831,22 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
     }
     return hipSuccess;
   };
-  PF_CHECK(hipLaunchKernelGGL(k_pf_embed, dim3(n), dim3(256), 0, st, plan.tokens, plan.tok_stride, a.embed,
-                              a.embed_scale, b.hid, H));
-  for (int li = 0; li < s.n_layers; ++li) {
+  if (plan.layer_begin == 0)
+    PF_CHECK(hipLaunchKernelGGL(k_pf_embed, dim3(n), dim3(256), 0, st, plan.tokens, plan.tok_stride, a.embed,
+                                a.embed_scale, b.hid, H));
+  for (int li = plan.layer_begin; li < s.n_layers; ++li) {
     const LayerArgs &L = layers[li];
-    if (li == 0)
+    const int cs_off = L.global ? D : 0;
+    // (a tail run starts after its first layer's q|k|v step: q in b.q, K/V
+    // in the cache)
+    const bool qkv_step = !(plan.qkv_done && li == plan.layer_begin);
+    if (li == 0 && qkv_step)
       PF_TRY(launch_pf_norm<false>(n, st, nullptr, rows_plain(b.hid, H), nullptr, L.g_in, nullptr, xn_f32, H, a.eps,
                                    stage, a16_h, ea_h));
-    const int cs_off = L.global ? D : 0;
     // q|k|v of a long prompt in Q4_K at head_dim 256: one launch whose
     // epilogue applies the q/k norms and RoPE and stores k and v straight into
     // the cache rows (no k_pf_qk_rope)
-    const bool qkv_gemm = !plan.mb && !plan.p0_dev && L.fmt[kProjQ] == RT_LINEAR_Q4K &&
+    const bool qkv_gemm = qkv_step && !plan.mb && !plan.p0_dev && L.fmt[kProjQ] == RT_LINEAR_Q4K &&
                           L.fmt[kProjK] == RT_LINEAR_Q4K && L.fmt[kProjV] == RT_LINEAR_Q4K && L.ew[kProjQ] &&
                           L.ew[kProjK] && L.ew[kProjV] && q4k_gemm_qkv_ok(n, QD, KVD, D);
     if (qkv_gemm) {
@@ -851,7 +855,7 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
       PF_TRY(launch_q4k_gemm_qkv_prepped(gemm_a16(H), gemm_ea(H), w3, ew3, b.q, L.kc + (size_t)plan.p0 * KVD,
                                          L.vc + (size_t)plan.p0 * KVD, n, QD, KVD, H, plan.cs + cs_off,
                                          plan.cs_stride, L.g_q, L.g_k, a.eps, st));
-    } else {
+    } else if (qkv_step) {
       PF_TRY(proj(plan.mb ? b.xn : nullptr, H, {L.fmt[kProjQ], L.fmt[kProjK], L.fmt[kProjV]},
                   {MbMat{L.wq, b.q, QD, 0, 0}, MbMat{L.wk, b.k, KVD, 0, 0}, MbMat{L.wv, b.v, KVD, 0, 0}},
                   {&vq, &vk, &vv}, {L.ew[kProjQ], L.ew[kProjK], L.ew[kProjV]}));
@@ -865,6 +869,9 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
                                     L.g_q, L.g_k, plan.cs, plan.cs_stride, cs_off, L.kc, L.vc, plan.p0, plan.p0_dev,
                                     n, nq, nkv, a.eps));
     }
+    // The last layer's attention, o and FFN feed only the logits: a run that
+    // needs no logits from these rows stops after the last K/V rows.
+    if (plan.last_layer_kv_only && li == s.n_layers - 1) break;
     PfAttnArgs pa;
     pa.p0 = plan.p0;
     pa.p0_dev = plan.p0_dev;
