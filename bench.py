@@ -65,21 +65,30 @@ def load_pkg():
 
 
 def prefill_flops(T: int, mode: int, window: int = 1024, global_every: int = 6, nq: int = 8, d: int = 256):
-    """Algorithmic flops of a T-token prefill: the 7 projections of every layer
-    (2*T*N*K each) and attention (2 flops per q.k product term and per p*v
-    term: 4*d*nq per visible key).  mode 0 (the reference's prefill window):
-    local rows r >= T - window see r - (T - window) + 1 keys, earlier rows none;
-    mode 1: min(r + 1, window) keys."""
-    gemm = 2 * T * L * sum(n * k for _, n, k in Q4K_SHAPES)
+    """Flops a T-token prefill needs: the 7 projections (2*N*K per row) and
+    attention (2 flops per q.k product term and per p*v term: 4*d*nq per
+    visible key) of every row, except where a row's result cannot reach the
+    KV cache or the last row's logits: in mode 0 (the reference's prefill
+    window) a local layer's rows r < T - window see no key, so their o
+    projection is zero; and the last layer's attention, o projection and FFN
+    only feed the last row's logits.  mode 0: local rows r >= T - window see
+    r - (T - window) + 1 keys; mode 1: min(r + 1, window) keys."""
+    shp = {name: (n, k) for name, n, k in Q4K_SHAPES}
+    per_row = {name: 2 * n * k for name, (n, k) in shp.items()}
+    qkv = per_row["q"] + per_row["k"] + per_row["v"]
+    rest = per_row["gate"] + per_row["up"] + per_row["down"]
+    w = min(window, T)
+    is_glob = [i % global_every == global_every - 1 for i in range(L)]
+    gemm = 0
+    for i in range(L - 1):
+        o_rows = T if (is_glob[i] or mode == 1) else w
+        gemm += T * (qkv + rest) + o_rows * per_row["o"]
+    gemm += T * qkv + per_row["o"] + rest  # last layer: K/V rows for every row, the rest for the last row
     glob_keys = T * (T + 1) // 2
-    if mode == 0:
-        w = min(window, T)
-        loc_keys = w * (w + 1) // 2
-    else:
-        loc_keys = sum(min(r + 1, window) for r in range(T))
-    n_glob = sum(1 for i in range(L) if i % global_every == global_every - 1)
-    attn = 4 * d * nq * (n_glob * glob_keys + (L - n_glob) * loc_keys)
-    return gemm, attn
+    loc_keys = w * (w + 1) // 2 if mode == 0 else sum(min(r + 1, window) for r in range(T))
+    attn_keys = sum(glob_keys if is_glob[i] else loc_keys for i in range(L - 1))
+    attn_keys += T if is_glob[L - 1] else w  # the last row's keys in the last layer
+    return gemm, 4 * d * nq * attn_keys
 
 
 def q4k_bytes(n: int, k: int) -> int:
