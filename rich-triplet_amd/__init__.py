@@ -506,3 +506,5 @@ class HipDecodeContext:
 
 
 from .gguf import GgufFile, GgufTensorInfo, Linear, load_linear_from_gguf, q4k_quantize  # noqa: E402,F401
+from . import generate  # noqa: E402,F401
+from .generate import GEMMA3_EOS, NgramDraftEngine, generate_greedy, greedy_token  # noqa: E402,F401
