@@ -442,8 +442,10 @@ __global__ __launch_bounds__(64 * W) void k_pf_attn(const float *__restrict__ q,
 
   int k_begin = key_first, k_end = key_last;
   if (p.split_stages) {
+    // the last split runs to key_last, so the splits cover the block's keys
+    // whatever span the host planned them for
     k_begin = key_first + (int)blockIdx.z * p.split_stages * KB;
-    k_end = min(key_last, k_begin + p.split_stages * KB - 1);
+    if ((int)blockIdx.z + 1 < (int)gridDim.z) k_end = min(key_last, k_begin + p.split_stages * KB - 1);
   }
   load_stage(k_begin);
 #pragma unroll 1
@@ -904,8 +906,11 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
       // the keys as far as the partial buffers allow, so no workgroup walks
       // many more key stages than the average.
       const int splits_max = b.attn_ml ? std::min(kPfMaxSplits, b.attn_rows * kPfMaxSplits / na) : 0;
+      // a row block of R rows walks at most window + R - 1 keys from a
+      // 32-aligned start; R follows the launch's workgroup width
+      const int rows_wg = ((na * G >= 256 ? 128 : 64) + G - 1) / G;
       const int span = causal ? plan.max_pos
-                       : plan.window > 0 ? std::min(plan.max_pos, plan.window + 96)
+                       : plan.window > 0 ? std::min(plan.max_pos, plan.window + rows_wg + 32)
                                          : std::max(plan.max_pos - plan.lo_fixed, 1);
       const int stages = (span + 31) / 32 + 1;
       // Causal rows: the last row block walks every key, the first one stage.

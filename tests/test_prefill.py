@@ -379,6 +379,34 @@ def test_gpu_prefill_chunks_and_continuation(rt, orc):
 
 
 @pytest.mark.gpu
+def test_gpu_prefill_wide_window_key_split_continuation(rt, orc):
+    """GQA group 1 (one q head per KV head), window 512, a continuation at
+    start_position 30 of 640 rows under the sliding rule: the attention runs
+    on eight-wave workgroups of 128 rows with the keys split, and a row
+    block's keys start 32-aligned below the window of its first row, so its
+    range is window + 128 + 30 keys here.  The prompt's last row is the last
+    row of a full block, so the logits see whether it attended to its own and
+    the 29 keys before it; every KV row against the oracle too."""
+    cfg = tiny(1, sliding_window=512)
+    p0, T = 30, 640
+    max_seq = p0 + T + 8
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=0, seed=6700)
+    toks = [(17 * i + 4) % cfg["vocab"] for i in range(p0 + T)]
+    d = gpu_ctx(rt, cfg, layers, embed, fnorm, max_seq)
+    d.prefill(toks[:p0], 0, 1)
+    got = d.prefill(toks[p0:], p0, 1)
+    ref_layers = fresh_caches(layers)
+    ref = orc.gemma3_prefill(cfg, ref_layers, embed, fnorm, toks, 0, 1)
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, ref) < LOGITS_TOL, rel_l2(got, ref)
+    for li in range(cfg["n_layers"]):
+        k, v = read_kv(d, cfg, li, p0 + T)
+        assert rel_l2(k, ref_layers[li]["k_cache"][:p0 + T]) < KV_TOL
+        assert rel_l2(v, ref_layers[li]["v_cache"][:p0 + T]) < KV_TOL
+    d.close()
+
+
+@pytest.mark.gpu
 def test_gpu_prefill_rejects_bad_calls(rt, orc):
     cfg = tiny(2)
     layers, embed, fnorm = make_model(orc, cfg, max_seq=16, ctx=0, seed=6200)
