@@ -7,12 +7,12 @@
 
 namespace rt {
 
-// Keys per attention sub-chunk.  A workgroup walks up to kAttnSubLocal
-// (sliding-window layers) or kAttnSubGlobal (global layers) sub-chunks; the
-// host sizes the chunk counts from the window and from max_seq.
-constexpr int kAttnChunkKeys = 16;
-constexpr int kAttnSubLocal = 1;
-constexpr int kAttnSubGlobal = 4;
+// Decode attention (k_attn): each wave of a workgroup walks kpw keys, so a
+// workgroup (chunk) covers kpw*waves keys; the host sizes the chunk counts
+// from the window (sliding-window layers) and from max_seq (global layers),
+// and k_attn_combine merges the chunks.
+constexpr int kAttnLocalKpw = 4, kAttnLocalWaves = 4;
+constexpr int kAttnGlobalKpw = 8, kAttnGlobalWaves = 8;
 // Upper bound on the number of chunks a KV head is split into.
 constexpr int kAttnMaxChunks = 4096;
 // Step parameter block (device): ints [0, 16) (token, position), then the

@@ -132,7 +132,7 @@ rt_status rt_decode_create(const rt_gemma3_config *cfg, rt_decode **out) {
     return hip_error(pe, "rt_decode_create: batched lm_head");
   const int window = c.sliding_window;
   const int local_span = window > 0 ? std::min(window, c.max_seq) : c.max_seq;
-  constexpr int kLocalKeys = kAttnChunkKeys * kAttnSubLocal, kGlobalKeys = kAttnChunkKeys * kAttnSubGlobal;
+  constexpr int kLocalKeys = kAttnLocalKpw * kAttnLocalWaves, kGlobalKeys = kAttnGlobalKpw * kAttnGlobalWaves;
   s.nchunk_local = (local_span + kLocalKeys - 1) / kLocalKeys;
   s.nchunk_global = (c.max_seq + kGlobalKeys - 1) / kGlobalKeys;
   if (s.nchunk_global > kAttnMaxChunks || s.nchunk_local > kAttnMaxChunks)

@@ -258,160 +258,169 @@ __global__ __launch_bounds__(T) void k_gemv(const uint8_t *__restrict__ W, const
 }
 
 // ---------------------------------------------------------------------------
-// k_attn: per (key chunk, KV head) workgroup of 256 threads.  A chunk is up to
-// SUB sub-chunks of 16 keys, walked with an online softmax.
-//   1. q heads of this KV group: per-head RMSNorm (gamma shared, 2485-2508)
-//      and NeoX RoPE (2742-2772) with cos/sin of (pos*fs)/theta^(2i/d)
-//      computed on the host for this position (the reference's own f32
-//      expression and libm); the chunk holding `pos` also rotates k, and
-//      writes k and v into the cache row `pos` (1813-1823).
-//   2. per sub-chunk: scores s_c = (q.k_c)*scale (16 lanes per key), running
-//      max m and sum l with the previous sums rescaled by e^(m_old - m_new),
-//      and o = sum_c e^(s_c - m) v_c (four dimensions per thread);
-//   3. partials (m, l, o) to global; k_attn_combine merges the chunks:
-//      out = sum_i o_i e^(m_i-M) / sum_i l_i e^(m_i-M).
-// Together they equal gqa_attention_cached's t_q == 1 branch (2806-2879).
+// k_attn: one layer's attention for the token at `pos` (gqa_attention_cached's
+// t_q == 1 branch, transformer4.rs:2806-2879).  Grid (key chunk, KV head);
+// a workgroup of WAVES waves takes a chunk of up to KPW*WAVES keys and each
+// wave walks its own KPW keys with a private softmax, so the key loop has no
+// barrier.  A lane holds D/64 consecutive dimensions of every vector (q, K
+// row, V row, output), so each K and V row is one coalesced wave load.
+//   1. Every wave forms the per-head RMSNorm (gamma shared, 2485-2508) and
+//      NeoX RoPE (2742-2772) of its G q heads itself, from the step's cos/sin
+//      table; the wave whose keys hold `pos` also normalises and rotates k,
+//      takes v, uses both for that key and writes them into cache row `pos`
+//      (1813-1823).
+//   2. s_c = (q . k_c) * scale per key (a wave sum), m = max s_c, p_c =
+//      e^(s_c - m), l = sum p_c, o = sum p_c v_c over the wave's keys.
+//   3. The waves' (m, l, o) merge through LDS into the chunk's partial
+//      (rescaled by e^(m_w - M)); k_attn_combine then merges the chunks.
 // ---------------------------------------------------------------------------
+template <int D>
+struct LaneRow {
+  static constexpr int N = D / 64;  // dimensions per lane: lane l holds [N*l, N*l + N)
+  float v[N];
+  // N floats at row + N*idx (idx = lane for a whole row)
+  RT_DEV void load(const float *__restrict__ row, int idx) {
+    if constexpr (N == 4) {
+      const float4 t = reinterpret_cast<const float4 *>(row)[idx];
+      v[0] = t.x, v[1] = t.y, v[2] = t.z, v[3] = t.w;
+    } else {
+      const float2 t = reinterpret_cast<const float2 *>(row)[idx];
+      v[0] = t.x, v[1] = t.y;
+    }
+  }
+  RT_DEV void store(float *row, int idx) const {
+    if constexpr (N == 4)
+      reinterpret_cast<float4 *>(row)[idx] = make_float4(v[0], v[1], v[2], v[3]);
+    else
+      reinterpret_cast<float2 *>(row)[idx] = make_float2(v[0], v[1]);
+  }
+};
 
-template <int D, int G, int SUB>
-__global__ __launch_bounds__(256) void k_attn(DecodeArgs a, LayerArgs L) {
-  constexpr int KC = kAttnChunkKeys;       // keys per sub-chunk
-  constexpr int DL = D / 16;               // score pass: 16 lanes per key, DL dims per lane
-                                           // (float4 j of lane `sub` = dims 64j + 4sub + [0,4))
-  constexpr int VL = D / 4;                // value pass: lanes per key row (float4 each)
-  constexpr int VG = 256 / VL;             // key groups in the value pass
-  constexpr int VK = KC / VG;              // keys per thread in the value pass
-  static_assert(KC == 16 && (D == 128 || D == 256), "chunk layout assumes 16 keys and D in {128, 256}");
-  __shared__ __attribute__((aligned(16))) float qs[G][D];
-  __shared__ __attribute__((aligned(16))) float knew[D], vnew[D];
-  __shared__ float sc[2][G][KC];           // scores, then probabilities (double-buffered by sub-chunk)
-  __shared__ float rescale[2][G];          // e^(m_old - m_new) of each sub-chunk
-  __shared__ __attribute__((aligned(16))) float vpart[VG][G][D];
+// Per-head RMSNorm and NeoX RoPE of one head held as a LaneRow (the
+// arithmetic of norm_rope_head_regs): lanes 0..31 hold the pairs' first
+// elements i < D/2, lanes 32..63 their partners i + D/2, exchanged across
+// the halves.  cs/sn: the cos and sin of the lane's pairs (table entries
+// N*(lane & 31) ..).
+template <int D>
+RT_DEV void norm_rope_lane(LaneRow<D> &x, const LaneRow<D> &g, const LaneRow<D> &cs, const LaneRow<D> &sn,
+                           float eps) {
+  constexpr int N = D / 64;
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < N; ++j) ss += x.v[j] * x.v[j];
+  const float rinv = rms_inv_from_sumsq(wave_sum(ss), 1.0f / (float)D, eps);
+  const bool upper = (threadIdx.x & 63) >= 32;
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+#pragma clang fp contract(off)
+    const float a = (x.v[j] * rinv) * (1.0f + g.v[j]);
+    const float b = __shfl_xor(a, 32);
+    x.v[j] = upper ? b * sn.v[j] + a * cs.v[j] : a * cs.v[j] - b * sn.v[j];
+  }
+}
+
+template <int D, int G, int KPW, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void k_attn(DecodeArgs a, LayerArgs L) {
+  constexpr int N = D / 64, NT = 64 * WAVES;
+  static_assert(D == 128 || D == 256, "head_dim 128 or 256");
+  __shared__ float sm_ml[WAVES][G][2];
+  __shared__ __attribute__((aligned(16))) float sm_o[WAVES][G][D];
   const int kvh = blockIdx.y, chunk = blockIdx.x, nchunk = gridDim.x;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int pos = a.params[1];
   const int t_end = pos + 1;
   const int t_start = L.window > 0 ? max(0, t_end - L.window) : 0;
-  const int t_kv = t_end - t_start;
-  const int csize = (t_kv + nchunk - 1) / nchunk;  // <= KC*SUB: the host sizes nchunk for max_seq / window
-  const int c0 = t_start + chunk * csize;
-  const int c1 = min(c0 + csize, t_end);
-  const int n = max(0, c1 - c0);
-  const bool has_new = c0 <= pos && pos < c1;
+  const int csize = (t_end - t_start + nchunk - 1) / nchunk;  // <= KPW*WAVES: the host sizes nchunk
+  const int c0 = t_start + chunk * csize, c1 = min(c0 + csize, t_end);
+  const int kw = (csize + WAVES - 1) / WAVES;  // <= KPW
+  const int w0 = c0 + wave * kw, w1 = min(w0 + kw, c1);
+  const int nk = max(0, w1 - w0);  // wave-uniform
+  const bool owner = w0 <= pos && pos < w1;
   const int kvd = a.n_kv_heads * D;
-  const float *kbase = L.kc + (size_t)kvh * D, *vbase = L.vc + (size_t)kvh * D;
-  const int kg = lane >> 4, sub = lane & 15;
-  const int kidx = wave * 4 + kg;                      // this lane's key in the score pass
-  const int vgrp = threadIdx.x / VL, vl = threadIdx.x % VL;
-  const int last = max(c1 - 1, 0);
 
-  // Sub-chunk loads, branch-free at clamped rows (row `pos` is replaced by the
-  // freshly rotated k / copied v when it is used).
-  auto load_sub = [&](int s, float (&kr)[DL], float4 (&vr)[VK]) __attribute__((always_inline)) {
-    const int k0 = c0 + s * KC;
-    const float4 *kp = reinterpret_cast<const float4 *>(kbase + (size_t)min(k0 + kidx, last) * kvd);
+  // loads, in the order they are consumed (vector loads return in order):
+  // q heads and the norm / RoPE inputs, then K rows, then V rows; rows past
+  // the wave's keys re-read its last row (or row 0) and are masked
+  LaneRow<D> q[G], gq, cs, sn, kn, vn, gk;
 #pragma unroll
-    for (int j = 0; j < DL / 4; ++j) {
-      const float4 v4 = kp[16 * j + sub];
-      kr[4 * j] = v4.x; kr[4 * j + 1] = v4.y; kr[4 * j + 2] = v4.z; kr[4 * j + 3] = v4.w;
-    }
+  for (int g = 0; g < G; ++g) q[g].load(a.q + (size_t)(kvh * G + g) * D, lane);
+  gq.load(L.g_q, lane);
+  cs.load(L.rope_cs, lane & 31);
+  sn.load(L.rope_cs + D / 2, lane & 31);
+  kn.load(a.k + (size_t)kvh * D, lane);
+  vn.load(a.v + (size_t)kvh * D, lane);
+  gk.load(L.g_k, lane);
+  const int last = max(w1 - 1, 0);
+  LaneRow<D> kr[KPW], vr[KPW];
 #pragma unroll
-    for (int j = 0; j < VK; ++j)
-      vr[j] = *reinterpret_cast<const float4 *>(vbase + (size_t)min(k0 + vgrp + VG * j, last) * kvd + 4 * vl);
-  };
-  float kr[DL];
-  float4 vr[VK];
-  load_sub(0, kr, vr);
+  for (int k = 0; k < KPW; ++k) kr[k].load(L.kc + (size_t)min(w0 + k, last) * kvd + (size_t)kvh * D, lane);
+#pragma unroll
+  for (int k = 0; k < KPW; ++k) vr[k].load(L.vc + (size_t)min(w0 + k, last) * kvd + (size_t)kvh * D, lane);
 
-  // 1. rotations (waves 0..G-1: q heads; the next wave: k, and the v copy)
-  if (wave < G) norm_rope_head<D>(a.q + (size_t)(kvh * G + wave) * D, L.g_q, L.rope_cs, a.eps, qs[wave]);
-  if (has_new && wave == (G % 4)) {  // for G == 4 wave 0 rotates k after its q head
-    norm_rope_head<D>(a.k + (size_t)kvh * D, L.g_k, L.rope_cs, a.eps, knew);
-    for (int i = lane; i < D; i += 64) vnew[i] = a.v[(size_t)kvh * D + i];
-  }
-  __syncthreads();
-  if (has_new && threadIdx.x < D) {
-    L.kc[(size_t)pos * kvd + (size_t)kvh * D + threadIdx.x] = knew[threadIdx.x];
-    L.vc[(size_t)pos * kvd + (size_t)kvh * D + threadIdx.x] = vnew[threadIdx.x];
+  // 1. q heads; the new key and value at `pos`
+#pragma unroll
+  for (int g = 0; g < G; ++g) norm_rope_lane<D>(q[g], gq, cs, sn, a.eps);
+  if (owner) {
+    norm_rope_lane<D>(kn, gk, cs, sn, a.eps);
+    kn.store(L.kc + (size_t)pos * kvd + (size_t)kvh * D, lane);
+    vn.store(L.vc + (size_t)pos * kvd + (size_t)kvh * D, lane);
+#pragma unroll
+    for (int k = 0; k < KPW; ++k)
+      if (w0 + k == pos) kr[k] = kn, vr[k] = vn;
   }
 
-  // 2. sub-chunks with a running softmax (wave g < G keeps head g's m and l)
-  float4 o[G];
+  // 2. scores, softmax and values of this wave's keys
+  float m[G], l[G];
+  LaneRow<D> o[G];
 #pragma unroll
-  for (int g = 0; g < G; ++g) o[g] = make_float4(0.f, 0.f, 0.f, 0.f);
-  float m_run = -INFINITY, l_run = 0.f;
+  for (int g = 0; g < G; ++g) {
+    float s[KPW];
 #pragma unroll
-  for (int s = 0; s < SUB; ++s) {
-    const int k0 = c0 + s * KC;
-    const int ns = max(0, min(KC, c1 - k0));
-    float kn[DL];
-    float4 vn[VK];
-    if (s + 1 < SUB) load_sub(s + 1, kn, vn);
-    if (k0 + kidx == pos) {
-#pragma unroll
-      for (int j = 0; j < DL; ++j) kr[j] = knew[64 * (j >> 2) + 4 * sub + (j & 3)];
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
+    for (int k = 0; k < KPW; ++k) {
       float d = 0.f;
 #pragma unroll
-      for (int j = 0; j < DL; ++j) d += qs[g][64 * (j >> 2) + 4 * sub + (j & 3)] * kr[j];
-      d = row16_sum(d);
-      if (kidx < ns && sub == 0) sc[s & 1][g][kidx] = d * a.attn_scale;
+      for (int j = 0; j < N; ++j) d += q[g].v[j] * kr[k].v[j];
+      s[k] = wave_sum(d) * a.attn_scale;
     }
-    __syncthreads();
-    if (wave < G) {
-      const float sv = lane < ns ? sc[s & 1][wave][lane] : -INFINITY;
-      const float m_new = fmaxf(m_run, wave_max(sv));
-      const float p = lane < ns ? expf(sv - m_new) : 0.f;
-      const float r = m_run == -INFINITY ? 0.f : expf(m_run - m_new);
-      l_run = l_run * r + wave_sum(p);
-      m_run = m_new;
-      if (lane < KC) sc[s & 1][wave][lane] = p;
-      if (lane == 0) rescale[s & 1][wave] = r;
-    }
-    __syncthreads();
+    m[g] = -INFINITY;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float r = rescale[s & 1][g];
-      o[g].x *= r; o[g].y *= r; o[g].z *= r; o[g].w *= r;
-    }
+    for (int k = 0; k < KPW; ++k)
+      if (k < nk) m[g] = fmaxf(m[g], s[k]);
+    l[g] = 0.f;
 #pragma unroll
-    for (int j = 0; j < VK; ++j) {
-      const int ki = vgrp + VG * j;
-      float4 v4 = vr[j];
-      if (k0 + ki == pos) v4 = *reinterpret_cast<const float4 *>(&vnew[4 * vl]);
-      if (ki < ns) {
+    for (int j = 0; j < N; ++j) o[g].v[j] = 0.f;
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const float p = sc[s & 1][g][ki];
-          o[g].x += p * v4.x; o[g].y += p * v4.y; o[g].z += p * v4.z; o[g].w += p * v4.w;
-        }
-      }
-    }
-    if (s + 1 < SUB) {
+    for (int k = 0; k < KPW; ++k) {
+      const float p = k < nk ? expf(s[k] - m[g]) : 0.f;
+      l[g] += p;
 #pragma unroll
-      for (int j = 0; j < DL; ++j) kr[j] = kn[j];
-#pragma unroll
-      for (int j = 0; j < VK; ++j) vr[j] = vn[j];
+      for (int j = 0; j < N; ++j) o[g].v[j] += p * vr[k].v[j];
     }
   }
 
-  // 3. the VG key groups are summed through LDS; partials to global
+  // 3. the waves' partials merged into the chunk's
 #pragma unroll
-  for (int g = 0; g < G; ++g) *reinterpret_cast<float4 *>(&vpart[vgrp][g][4 * vl]) = o[g];
-  __syncthreads();
-  for (int e = threadIdx.x; e < G * D; e += 256) {
-    const int g = e / D, d = e % D;
-    float acc = 0.f;
-#pragma unroll
-    for (int q = 0; q < VG; ++q) acc += vpart[q][g][d];
-    a.part_o[((size_t)(kvh * G + g) * nchunk + chunk) * D + d] = acc;
+  for (int g = 0; g < G; ++g) {
+    o[g].store(&sm_o[wave][g][0], lane);
+    if (lane == 0) sm_ml[wave][g][0] = m[g], sm_ml[wave][g][1] = l[g];
   }
-  if (wave < G && lane == 0) {
-    const int h = kvh * G + wave;
-    a.part_m[(size_t)h * nchunk + chunk] = n > 0 ? m_run : -INFINITY;
-    a.part_l[(size_t)h * nchunk + chunk] = n > 0 ? l_run : 0.f;
+  __syncthreads();
+  for (int e = threadIdx.x; e < G * D; e += NT) {
+    const int g = e / D, d = e % D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) M = fmaxf(M, sm_ml[w][g][0]);
+    float O = 0.f, Ls = 0.f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+      const float mw = sm_ml[w][g][0];
+      const float f = mw == -INFINITY ? 0.f : expf(mw - M);
+      O = fmaf(sm_o[w][g][d], f, O);
+      Ls = fmaf(sm_ml[w][g][1], f, Ls);
+    }
+    const size_t ci = (size_t)(kvh * G + g) * nchunk + chunk;
+    a.part_o[ci * D + d] = O;
+    if (d == 0) a.part_m[ci] = M, a.part_l[ci] = Ls;
   }
 }
 
@@ -425,7 +434,7 @@ __global__ __launch_bounds__(256) void k_attn(DecodeArgs a, LayerArgs L) {
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(256) void k_attn_combine(DecodeArgs a, int nchunk) {
-  constexpr int R = 20;  // 80 chunks per batch: one batch for the Gemma-3 shapes
+  constexpr int R = 20;  // 80 chunks per batch
   __shared__ float gm[4], gl[4];
   __shared__ float go[4][64];
   const int h = blockIdx.x, d0 = blockIdx.y * 64;
@@ -698,22 +707,22 @@ bool decode_shape_supported(const DecodeShape &s, const char **why) {
   return true;
 }
 
-template <int D, int SUB>
-static void launch_attn_ds(Launch &l, const DecodeArgs &a, const LayerArgs &L, int nchunk, int group) {
-  const dim3 grid(nchunk, a.n_kv_heads);
+template <int D, int KPW, int WAVES>
+static void launch_attn_kw(Launch &l, const DecodeArgs &a, const LayerArgs &L, int nchunk, int group) {
+  const dim3 grid(nchunk, a.n_kv_heads), block(64 * WAVES);
   switch (group) {
-    case 1: hipLaunchKernelGGL((k_attn<D, 1, SUB>), grid, dim3(256), 0, l.s, a, L); break;
-    case 2: hipLaunchKernelGGL((k_attn<D, 2, SUB>), grid, dim3(256), 0, l.s, a, L); break;
-    default: hipLaunchKernelGGL((k_attn<D, 4, SUB>), grid, dim3(256), 0, l.s, a, L); break;
+    case 1: hipLaunchKernelGGL((k_attn<D, 1, KPW, WAVES>), grid, block, 0, l.s, a, L); break;
+    case 2: hipLaunchKernelGGL((k_attn<D, 2, KPW, WAVES>), grid, block, 0, l.s, a, L); break;
+    default: hipLaunchKernelGGL((k_attn<D, 4, KPW, WAVES>), grid, block, 0, l.s, a, L); break;
   }
 }
 
 template <int D>
 static void launch_attn_d(Launch &l, const DecodeArgs &a, const LayerArgs &L, int nchunk, int group) {
   if (L.window > 0)
-    launch_attn_ds<D, kAttnSubLocal>(l, a, L, nchunk, group);
+    launch_attn_kw<D, kAttnLocalKpw, kAttnLocalWaves>(l, a, L, nchunk, group);
   else
-    launch_attn_ds<D, kAttnSubGlobal>(l, a, L, nchunk, group);
+    launch_attn_kw<D, kAttnGlobalKpw, kAttnGlobalWaves>(l, a, L, nchunk, group);
   l.check();
   hipLaunchKernelGGL((k_attn_combine<D>), dim3(a.n_q_heads, D / 64), dim3(256), 0, l.s, a, nchunk);
   l.check();
