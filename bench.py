@@ -46,6 +46,8 @@ GEMM_SHAPES = [("config2_gate_up", 512, 10240, 2560), ("config2_down", 512, 2560
                ("config4_mlp_down", 4608, 3072, 12288)]
 
 H, F, QD, KVD, L, V = 2560, 10240, 2048, 1024, 34, 262144
+# streaming-read floor candidates (rt_stream_read_cfg kind, grid; grid 0 = by size)
+READ_CFGS = [(0, 0), (0, 512), (0, 1024), (1, 512), (1, 1024), (1, 2048)]
 Q4K_SHAPES = [("q", QD, H), ("k", KVD, H), ("v", KVD, H), ("o", H, QD), ("gate", F, H), ("up", F, H),
               ("down", H, F)]
 
@@ -135,6 +137,9 @@ def main() -> int:
     ap.add_argument("--prefill-profile", action="store_true",
                     help="only run the 4096-token GPU prefill of the config-3 context, --warmup then --steps "
                          "times; meant to run under rocprofv3")
+    ap.add_argument("--launch-probe", action="store_true",
+                    help="only measure the launch floor inside a graph: empty dependent launches, and streaming "
+                         "reads of 4-118 MB fitted to a fixed cost per launch plus a rate")
     ap.add_argument("--verify-rows", type=int, default=0,
                     help="with --decode-profile: run decode_step_batch calls of this many rows (1..8) instead "
                          "of single-token steps")
@@ -152,6 +157,10 @@ def main() -> int:
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed)
     t0 = time.time()
+
+    if args.launch_probe:
+        print(json.dumps(launch_probe(rt, torch, dev)))
+        return 0
 
     if args.traffic_probe:
         a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
@@ -409,27 +418,41 @@ def main() -> int:
             f"Q8_0 {kquant['q8_0_' + name]['us_per_launch']} us, BF16 (reference widening) "
             f"{kquant['bf16_' + name]['us_per_launch']} us")
     # Streaming-read floor: a kernel that only reads, with 16-byte loads, the
-    # same bytes per launch as the GEMV, from 34 distinct buffers in one graph.
+    # same bytes per launch as the GEMV, from 34 distinct buffers in one graph
+    # (the lm_head's from the 1.34 GB embedding itself); the fastest of a few
+    # access patterns and grids.
     sink = torch.zeros(64, dtype=torch.int32, device=dev)
     floor = {}
     for label, nbytes in (("gateup_fused", per_shape["gateup_fused"]["bytes_per_launch"]),
-                          ("gate", per_shape["gate"]["bytes_per_launch"])):
+                          ("gate", per_shape["gate"]["bytes_per_launch"]),
+                          ("lm_head", per_shape["lm_head"]["bytes_per_launch"])):
         nb16 = (nbytes + 15) // 16 * 16
-        bufs = torch.empty(L, nb16, dtype=torch.uint8, device=dev)
-        bufs.fill_(7)
+        if label == "lm_head":
+            nb16 = embed.numel() * 2 // 16 * 16
+            srcs, nrep = [embed] * 4, 4
+        else:
+            bufs = torch.empty(L, nb16, dtype=torch.uint8, device=dev)
+            bufs.fill_(7)
+            srcs, nrep = [bufs[i] for i in range(L)], L
+        best = None
+        for kind, grid in READ_CFGS:
+            def enqueue_reads(stream, srcs=srcs, nb16=nb16, kind=kind, grid=grid):
+                for b in srcs:
+                    rt.stream_read(b, nb16, sink, stream=stream, kind=kind, grid=grid)
 
-        def enqueue_reads(stream, bufs=bufs, nb16=nb16):
-            for i in range(L):
-                rt.stream_read(bufs[i], nb16, sink, stream=stream)
-
-        us = time_graph(enqueue_reads, reps) * 1e3 / L
-        gbps = nbytes / us / 1e3
-        floor[label] = {"bytes_per_launch": nbytes, "us_per_launch": round(us, 3), "GBps": round(gbps, 1),
+            us = time_graph(enqueue_reads, max(2, reps // 4) if label == "lm_head" else reps) * 1e3 / nrep
+            if best is None or us < best[0]:
+                best = (us, kind, grid)
+        us = best[0]
+        gbps = nb16 / us / 1e3
+        floor[label] = {"bytes_per_launch": nb16, "us_per_launch": round(us, 3), "GBps": round(gbps, 1),
                         "frac_of_hbm_peak": round(gbps / PEAK_HBM_GBS, 4),
-                        "gemv_frac_of_floor": round(per_shape[label]["GBps"] / gbps, 4)}
-        log(f"streaming-read floor, {nbytes / 1e6:.1f} MB per launch: {us:.2f} us, {gbps:.0f} GB/s; "
-            f"the GEMV reaches {per_shape[label]['GBps'] / gbps:.2f} of it")
-        del bufs
+                        "read_kind_grid": [best[1], best[2]],
+                        "gemv_frac_of_floor": round(per_shape[label]["GBps"] / (nbytes / us / 1e3), 4)}
+        log(f"streaming-read floor, {nb16 / 1e6:.1f} MB per launch: {us:.2f} us, {gbps:.0f} GB/s "
+            f"(kind {best[1]}, grid {best[2]}); the GEMV reaches {floor[label]['gemv_frac_of_floor']:.2f} of it")
+        if label != "lm_head":
+            del bufs
     # dominant kernel of the step (largest share of its time): the gate|up GEMV
     dom = per_shape["gateup_fused"]
     roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
@@ -443,6 +466,7 @@ def main() -> int:
                                   "GBps": per_shape["gate"]["GBps"],
                                   "frac": round(per_shape["gate"]["GBps"] / PEAK_HBM_GBS, 4),
                                   "copy_floor": floor["gate"]}}
+    per_shape["lm_head"]["copy_floor"] = floor["lm_head"]
     log(f"dominant kernel gate|up 2x10240x2560: {dom['us_per_launch']} us/launch, {dom['GBps']} GB/s "
         f"(one 10240x2560 matrix alone: {per_shape['gate']['us_per_launch']} us)")
 
@@ -611,6 +635,60 @@ def main() -> int:
     }
     print(json.dumps(out), flush=True)
     return 0
+
+
+def launch_probe(rt, torch, dev) -> dict:
+    """The launch floor of this GPU inside a graph, the figures that set the
+    decode step's launch structure: (1) µs per launch of a graph of 100
+    dependent empty kernels (one wave, and 256 / 1024 workgroups), (2) µs per
+    launch of streaming reads (the fastest of READ_CFGS) of 4-118 MB from
+    distinct buffers (>= 600 MB per replay, beyond the 256 MB MALL), fitted by
+    least squares to t = fixed + bytes / rate."""
+    cap = torch.cuda.Stream()
+
+    def per_launch_us(enqueue, n, reps):
+        with torch.cuda.stream(cap):
+            enqueue(cap)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap):
+            enqueue(torch.cuda.current_stream())
+        g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        del g
+        return a.elapsed_time(b) * 1e3 / (reps * n)
+
+    out = {"empty_launch_us": {}, "stream_read": []}
+    for grid, thr in ((1, 64), (256, 256), (1024, 256)):
+        us = per_launch_us(lambda st, grid=grid, thr=thr: [rt.empty_launch(grid, thr, st) for _ in range(100)], 100, 20)
+        out["empty_launch_us"][f"{grid}x{thr}"] = round(us, 3)
+    sink = torch.zeros(64, dtype=torch.int32, device=dev)
+    xs, ys = [], []
+    for nbytes in (4 << 20, 8 << 20, 14796800, 29583360, 59166720, 118333440):
+        nbuf = min(160, -(-(600 << 20) // nbytes))
+        bufs = torch.empty(nbuf, nbytes, dtype=torch.uint8, device=dev)
+        bufs.fill_(3)
+        best = None
+        for kind, grid in READ_CFGS:
+            us = per_launch_us(lambda st, kind=kind, grid=grid: [rt.stream_read(bufs[i], nbytes, sink, stream=st,
+                                                                                kind=kind, grid=grid)
+                                                                 for i in range(nbuf)], nbuf, 10)
+            best = us if best is None else min(best, us)
+        out["stream_read"].append({"bytes": nbytes, "us": round(best, 3), "GBps": round(nbytes / best / 1e3, 1)})
+        xs.append(nbytes)
+        ys.append(best)
+        del bufs
+    n = len(xs)
+    mx, my = sum(xs) / n, sum(ys) / n
+    slope = sum((x - mx) * (y - my) for x, y in zip(xs, ys)) / sum((x - mx) ** 2 for x in xs)
+    out["fit"] = {"fixed_us": round(my - slope * mx, 3), "rate_GBps": round(1e-3 / slope, 1)}
+    return out
 
 
 def build_decode(rt, torch, dev, gen, layers, embed, final_norm, args, ctx: int = 4096):

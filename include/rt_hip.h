@@ -122,12 +122,18 @@ rt_status rt_q4k_gemm_f32(const float *a_dev, const void *w_dev, float *c_dev, i
  * Matrices are row-major [rows][k] in block order, as in the file.
  * ------------------------------------------------------------------------- */
 /* GGUF block bytes (host) -> planar layout (host); n_blocks*210 / *34 bytes. */
-/* Measurement floor (no counterpart in the reference): reads `bytes` of
- * device memory with 16-byte loads and discards them, on `stream`; `sink` is
- * a device word the kernel writes only on an impossible checksum.  bench.py
- * times it on the same bytes as a GEMV to give that GEMV's fraction of a
- * plain streaming read. */
+/* Measurement floors (no counterpart in the reference).  rt_stream_read
+ * reads `bytes` of device memory with 16-byte loads and discards them, on
+ * `stream`; `sink` is a device word the kernel writes only on an impossible
+ * checksum.  rt_stream_read_cfg picks the access pattern (kind 0: strided
+ * over all threads with the next batch of loads in flight; kind 1: one
+ * contiguous slice per workgroup) and the grid (0: by size).  bench.py times
+ * the fastest of several on the same bytes as a GEMV to give that GEMV's
+ * fraction of a plain streaming read.  rt_empty_launch launches a kernel with
+ * no body: in a graph, the cost of one dependent launch. */
 rt_status rt_stream_read(const void *buf, size_t bytes, void *sink, void *stream);
+rt_status rt_stream_read_cfg(const void *buf, size_t bytes, void *sink, void *stream, int kind, int grid);
+rt_status rt_empty_launch(int grid, int threads, void *stream);
 
 /* y = gelu_tanh(x) (autograd2.rs:3082-3091), n floats, device pointers: the
  * activation exactly as the decode step and prefill kernels compute it. */

@@ -63,6 +63,8 @@ _SIGNATURES = {
     "rt_decode_memory": (_i32, [_vp, _vp]),
     "rt_gelu_tanh": (_i32, [_vp, _vp, _sz, _vp]),
     "rt_stream_read": (_i32, [_vp, _sz, _vp, _vp]),
+    "rt_stream_read_cfg": (_i32, [_vp, _sz, _vp, _vp, _i32, _i32]),
+    "rt_empty_launch": (_i32, [_i32, _i32, _vp]),
     "rt_qlinear_forward_host": (_i32, [_i32, _vp, _sz, _vp, _vp, _vp, _i64, _i64, _i64]),
     "rt_noalloc_scratch_bytes": (_sz, []),
     "rt_q6k_repack": (_i32, [_vp, _sz, _vp]),
@@ -185,9 +187,15 @@ def q4k_gemv_batch(w, a, c, m: int, n: int, k: int, stream=None) -> None:
     check(lib().rt_q4k_gemv_batch(_p(w), _p(a), _p(c), m, n, k, _stream(stream)))
 
 
-def stream_read(buf, nbytes: int, sink, stream=None) -> None:
-    """Read nbytes of buf with 16-byte loads and discard them (a bandwidth floor)."""
-    check(lib().rt_stream_read(_p(buf), nbytes, _p(sink), _stream(stream)))
+def stream_read(buf, nbytes: int, sink, stream=None, kind: int = 0, grid: int = 0) -> None:
+    """Read nbytes of buf with 16-byte loads and discard them (a bandwidth
+    floor); kind 0 strided, 1 one slice per workgroup; grid 0 by size."""
+    check(lib().rt_stream_read_cfg(_p(buf), nbytes, _p(sink), _stream(stream), kind, grid))
+
+
+def empty_launch(grid: int = 1, threads: int = 64, stream=None) -> None:
+    """A kernel with no body (the cost of a launch)."""
+    check(lib().rt_empty_launch(grid, threads, _stream(stream)))
 
 
 def gelu_tanh(x, y, stream=None) -> None:
