@@ -185,6 +185,16 @@ rt_status rt_qlinear_forward_host(int32_t fmt, const void *w, size_t w_bytes, co
  * rt_q4k_gemm_f32 (see there for graph capture). */
 rt_status rt_q4k_gemv_batch(const void *w, const float *a, float *c, int64_t m, int64_t n, int64_t k, void *stream);
 
+/* The same batched GEMV for the other projection formats a decode layer can
+ * hold: gemv_bf16_t_batch (metal_decode.rs:527-558) for RT_LINEAR_BF16, and
+ * RT_LINEAR_Q6K / RT_LINEAR_Q8_0 kept packed (planar layout, rt_q6k_repack /
+ * rt_q8_0_repack) where the reference widens them to BF16 first.  Reads the
+ * weights once for all m = 1..8 rows; device pointers, a and w 16-byte
+ * aligned; k % 256 == 0 for Q6_K, k % 64 == 0 otherwise; fmt RT_LINEAR_Q4K
+ * is rt_q4k_gemv_batch.  Workspace as rt_q4k_gemv_batch. */
+rt_status rt_linear_gemv_batch(int32_t fmt, const void *w, const float *a, float *c, int64_t m, int64_t n, int64_t k,
+                               void *stream);
+
 /* rt_q4k_gemv_batch that allocates nothing.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
@@ -309,6 +319,12 @@ typedef struct {
   uint64_t weights, kv_cache, activation, batch, prefill, total;
 } rt_decode_memory_info;
 rt_status rt_decode_memory(const rt_decode *d, rt_decode_memory_info *out);
+/* How rt_decode_step_batch runs (no counterpart in the reference, whose
+ * verify batch always runs its batched GEMVs): *batched = 1 when every bound
+ * layer's projections are served by the batched GEMVs (Q4_K, Q6_K, Q8_0,
+ * BF16) and the M tokens go through each layer together, reading each
+ * weight once; 0 when they run as M single-token passes. */
+rt_status rt_decode_verify_batched(const rt_decode *d, int32_t *batched);
 /* Device buffers of the context, for inspection. */
 rt_status rt_decode_logits(rt_decode *d, float **logits_dev);
 rt_status rt_decode_kv(rt_decode *d, int32_t layer, float **k_dev, float **v_dev);

@@ -61,6 +61,8 @@ _SIGNATURES = {
     "rt_q4k_gemv_batch_noalloc": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "rt_qlinear_forward": (_i32, [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "rt_decode_memory": (_i32, [_vp, _vp]),
+    "rt_decode_verify_batched": (_i32, [_vp, _vp]),
+    "rt_linear_gemv_batch": (_i32, [_i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "rt_gelu_tanh": (_i32, [_vp, _vp, _sz, _vp]),
     "rt_stream_read": (_i32, [_vp, _sz, _vp, _vp]),
     "rt_stream_read_cfg": (_i32, [_vp, _sz, _vp, _vp, _i32, _i32]),
@@ -180,6 +182,12 @@ def q4k_gemv(w, x, y, n: int, k: int, stream=None) -> None:
 
 def bf16_gemv(w, x, y, n: int, k: int, stream=None) -> None:
     check(lib().rt_bf16_gemv(_p(w), _p(x), _p(y), n, k, _stream(stream)))
+
+
+def linear_gemv_batch(fmt: int, w, a, c, m: int, n: int, k: int, stream=None) -> None:
+    """c[m][n] = a[m][k] . W[n][k] for m <= 8 rows and a weight in Q4_K, Q6_K,
+    Q8_0 (planar) or BF16 (gemv_bf16_t_batch for BF16)."""
+    check(lib().rt_linear_gemv_batch(fmt, _p(w), _p(a), _p(c), m, n, k, _stream(stream)))
 
 
 def q4k_gemv_batch(w, a, c, m: int, n: int, k: int, stream=None) -> None:
@@ -483,6 +491,14 @@ class HipDecodeContext:
 
     def set_graph(self, enabled: bool) -> None:
         check(lib().rt_decode_set_graph(self._h, int(enabled)))
+
+    @property
+    def verify_batched(self) -> bool:
+        """True when decode_step_batch runs the M tokens through each layer
+        together (batched GEMVs, one pass over the weights)."""
+        v = C.c_int32(0)
+        check(lib().rt_decode_verify_batched(self._h, C.byref(v)))
+        return bool(v.value)
 
     def memory(self) -> dict:
         """Device bytes by what they hold (print_metal_memory, metal_decode.rs:1285-1354)."""

@@ -267,6 +267,29 @@ rt_status rt_q4k_gemv_batch(const void *w, const float *a, float *c, int64_t m, 
   return hip_error(e, "rt_q4k_gemv_batch");
 }
 
+rt_status rt_linear_gemv_batch(int32_t fmt, const void *w, const float *a, float *c, int64_t m, int64_t n, int64_t k,
+                               void *stream) {
+  static const char *who = "rt_linear_gemv_batch";
+  if (fmt == RT_LINEAR_Q4K) return rt_q4k_gemv_batch(w, a, c, m, n, k, stream);
+  if (fmt != RT_LINEAR_Q6K && fmt != RT_LINEAR_Q8_0 && fmt != RT_LINEAR_BF16)
+    return set_error(RT_EINVAL, "%s: format %d has no batched GEMV", who, fmt);
+  rt_status st = check_gemv_shape(who, w, a, c, n, k, fmt == RT_LINEAR_Q6K ? 256 : 64);
+  if (st != RT_OK) return st;
+  if (m < 1 || m > kMbMaxRows) return set_error(RT_EINVAL, "%s: m=%lld outside [1, 8]", who, (long long)m);
+  const size_t stage = fmt == RT_LINEAR_BF16 ? 0 : (mb_stage_bytes((int)k) + 255) & ~size_t(255);
+  void *ws = nullptr;
+  st = gemm_workspace(std::max<size_t>(stage + kquant_mb_part_bytes((int)n, (int)k), 256), (hipStream_t)stream, &ws);
+  if (st != RT_OK) return st;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = stage ? launch_mb_stage(a, (int)m, (int)k, ws, s) : hipSuccess;
+  if (e == hipSuccess) {
+    MbMat mat{static_cast<const uint8_t *>(w), c, (int)n, 0, 0};
+    e = launch_kquant_gemv_mb(fmt, &mat, 1, (int)m, (int)k, stage ? ws : nullptr, a,
+                              reinterpret_cast<float *>(static_cast<char *>(ws) + stage), s);
+  }
+  return hip_error(e, who);
+}
+
 }  // extern "C"
 
 // ---------------------------------------------------------------------------

@@ -102,6 +102,10 @@ size_t prefill_gemm_workspace_bytes(const DecodeShape &s, int cap);
 // Batched-GEMV staging and partial-sum bytes for every projection set.
 size_t rows_mb_stage_bytes(const DecodeShape &s);
 size_t rows_mb_part_bytes(const DecodeShape &s);
+// Whether the batched GEMVs serve a layer with these projection formats
+// (q, k, v, o, gate, up, down): Q4_K, Q6_K (rows of whole super-blocks),
+// Q8_0 and BF16 (rows of whole 64-element chunks).
+bool rows_mb_formats_ok(const DecodeShape &s, const int *fmt);
 
 // n rows through every layer: rows p0 .. p0+n-1 (p0 from *p0_dev when that
 // is set), token of row t at tokens[t*tok_stride], its cos/sin tables at

@@ -54,7 +54,7 @@ struct rt_decode {
   bool graph_dirty = true;
   PrefillBuffers pf;                     // rt_decode_prefill scratch (grown on demand)
   PrefillBuffers vb;                     // decode_step_batch rows (kMaxBatch), allocated at create
-  bool all_q4k = true;                   // every projection Q4_K: batched-GEMV verify path
+  bool rows_mb = true;                   // every layer's formats served by the batched GEMVs (verify, short chunks)
   bool fused = true;                     // the fused single-token kernels serve this shape (else the rows path)
   int pf_chunk = 4096;                   // rows per prefill chunk (~180 KB of scratch per row at Gemma-3-4B)
   std::vector<void *> pf_owned;
@@ -345,15 +345,14 @@ rt_status rt_decode_set_layer_formats(rt_decode *d, int32_t layer, const rt_gemm
     const size_t H = c.hidden, F = c.ffn, QD = (size_t)c.n_q_heads * c.head_dim, KVD = (size_t)c.n_kv_heads * c.head_dim;
     const size_t shape[7][2] = {{QD, H}, {KVD, H}, {KVD, H}, {H, QD}, {F, H}, {F, H}, {H, F}};
     static const char *names[7] = {"q", "k", "v", "o", "gate", "up", "down"};
-    for (int p = 0; p < 7; ++p) {
+    for (int p = 0; p < 7; ++p)
       if (!proj_bytes(formats[p], shape[p][0], shape[p][1]))
         return unset(set_error(RT_EINVAL, "rt_decode_set_layer: projection %s has unsupported format %d", names[p],
                                formats[p]));
-      if (!d->fused && formats[p] != RT_LINEAR_Q4K)
-        return unset(set_error(RT_EINVAL,
-                               "rt_decode_set_layer: projection %s: this shape runs on the rows kernels, which take "
-                               "Q4_K projections only (format %d)", names[p], formats[p]));
-    }
+    if (!d->fused && !rows_mb_formats_ok(d->shape, formats))
+      return unset(set_error(RT_EINVAL,
+                             "rt_decode_set_layer: this shape runs on the rows kernels, whose batched GEMVs take "
+                             "Q4_K, Q6_K (whole super-blocks), Q8_0 and BF16 projections"));
   }
   // Every pointer is checked before anything is freed or uploaded; the new
   // binding is built aside and replaces the old one only when it is whole.
@@ -433,9 +432,8 @@ rt_status rt_decode_set_layer_formats(rt_decode *d, int32_t layer, const rt_gemm
     for (int i = 0; i < 7; ++i) b += proj_bytes(formats[i], sh[i][0], sh[i][1]);
     d->bound_weight_bytes[layer] = b;
   }
-  d->all_q4k = true;
-  for (const LayerArgs &X : d->layers)
-    for (int i = 0; i < 7; ++i) d->all_q4k = d->all_q4k && X.fmt[i] == RT_LINEAR_Q4K;
+  d->rows_mb = true;
+  for (const LayerArgs &X : d->layers) d->rows_mb = d->rows_mb && rows_mb_formats_ok(d->shape, X.fmt);
   d->layer_set[layer] = 1;
   return RT_OK;
 }
@@ -613,7 +611,7 @@ rt_status rt_decode_step_batch_async(rt_decode *d, const int32_t *tokens, int32_
   for (int i = 0; i < m; ++i) fill_slot(d, i, tokens[i], start_position + i);
   if ((st = params_send(d, m)) != RT_OK) return st;
   return run_graph(d, d->exec_batch[m], [&] {
-    if (!d->all_q4k)  // per-token layer kernels (any projection format)
+    if (!d->rows_mb)  // per-token layer kernels (any projection format)
       return enqueue_decode_batch(d->shape, d->args, d->layers.data(), m, d->xn_batch, d->logits_batch, d->stream);
     // all rows through each layer at once: batched GEMVs (one pass over the
     // weights), the causal row attention, a batched lm_head
@@ -808,7 +806,7 @@ rt_status rt_decode_prefill(rt_decode *d, const int32_t *tokens, int32_t n, int3
       plan.lo_fixed = lo_fixed;
       plan.window = window;
       plan.max_pos = start_position + c0 + cn;
-      plan.mb = cn <= kMaxBatch && d->all_q4k;  // a few rows: one pass over the weights beats the GEMM's tiles
+      plan.mb = cn <= kMaxBatch && d->rows_mb;  // a few rows: one pass over the weights beats the GEMM's tiles
       const bool last_chunk = c0 + cn == n;
       if (cn == 1) {
         plan.logits = last_chunk ? RowsPlan::kLastRow : RowsPlan::kNone;
@@ -834,7 +832,7 @@ rt_status rt_decode_prefill(rt_decode *d, const int32_t *tokens, int32_t n, int3
           tail.p0 = plan.p0 + (int)r;
           tail.tokens = tb.tokens;
           tail.cs = plan.cs + r * 2 * D;
-          tail.mb = d->all_q4k;
+          tail.mb = d->rows_mb;
           tail.logits = RowsPlan::kLastRow;
           tail.layer_begin = c.n_layers - 1;
           tail.qkv_done = true;
@@ -874,6 +872,12 @@ rt_status rt_decode_set_graph(rt_decode *d, int32_t enabled) {
 // context by what it holds.  Weights bound by device pointer count too, as
 // the reference's uploads do; the prefill scratch appears once a prefill has
 // sized it.
+rt_status rt_decode_verify_batched(const rt_decode *d, int32_t *batched) {
+  if (!d || !batched) return set_error(RT_EINVAL, "rt_decode_verify_batched: null pointer");
+  *batched = d->rows_mb ? 1 : 0;
+  return RT_OK;
+}
+
 rt_status rt_decode_memory(const rt_decode *d, rt_decode_memory_info *out) {
   if (!d || !out) return set_error(RT_EINVAL, "rt_decode_memory: null pointer");
   uint64_t by[rt_decode::kMemKinds] = {};

@@ -732,7 +732,22 @@ size_t rows_mb_stage_bytes(const DecodeShape &s) {
 
 size_t rows_mb_part_bytes(const DecodeShape &s) {
   const int H = s.hidden, F = s.ffn, QD = s.n_q_heads * s.head_dim, KVD = s.n_kv_heads * s.head_dim;
-  return std::max({mb_part_bytes(QD + 2 * KVD, H), mb_part_bytes(H, QD), mb_part_bytes(2 * F, H), mb_part_bytes(H, F)});
+  // a set split by format takes one region per launch: at most the larger
+  // slice count of the two kernel families times the set's rows
+  auto set = [](int n, int k) {
+    return std::max(k % 256 == 0 ? mb_part_bytes(n, k) : (size_t)0, kquant_mb_part_bytes(n, k));
+  };
+  return std::max({set(QD + 2 * KVD, H), set(H, QD), set(2 * F, H), set(H, F)});
+}
+
+bool rows_mb_formats_ok(const DecodeShape &s, const int *fmt) {
+  const int H = s.hidden, F = s.ffn, QD = s.n_q_heads * s.head_dim;
+  const int kdim[7] = {H, H, H, QD, H, H, F};
+  for (int i = 0; i < 7; ++i) {
+    const bool ok = fmt[i] == RT_LINEAR_Q4K ? kdim[i] % 256 == 0 : kquant_mb_supported(fmt[i], kdim[i]);
+    if (!ok) return false;
+  }
+  return true;
 }
 
 hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerArgs *layers, const PrefillBuffers &b,
@@ -768,16 +783,31 @@ hipError_t enqueue_rows(const DecodeShape &s, const DecodeArgs &a, const LayerAr
   _Float16 *a16_h = plan.mb ? nullptr : gemm_a16(H);  // producers that write A directly
   int *ea_h = plan.mb ? nullptr : gemm_ea(H);
   float *xn_f32 = plan.mb ? b.xn : nullptr;
-  // (plan.mb requires every projection in Q4_K; other formats take their own GEMM)
   auto proj = [&](const float *A, int K, std::initializer_list<int> fmts, std::initializer_list<MbMat> mats,
                   std::initializer_list<RowsIn *> views, std::initializer_list<const int *> ews,
                   _Float16 *a16_in = nullptr, int *ea_in = nullptr) {
     if (plan.mb) {
-      RowsIn out[3];
-      hipError_t r = launch_q4k_gemv_mb(mats.begin(), (int)mats.size(), n, K, b.mb_stage, b.mb_part, st, out);
-      int i = 0;
-      for (RowsIn *v : views) *v = out[i++];
-      return r;
+      // the set's Q4_K matrices in one launch, each other format in one
+      // launch of its own (Q8_0 / Q6_K from the same staged digits, BF16 from
+      // the f32 rows A), each with its own region of the partial sums
+      float *part = b.mb_part;
+      for (int fmt : {RT_LINEAR_Q4K, RT_LINEAR_Q6K, RT_LINEAR_Q8_0, RT_LINEAR_BF16}) {
+        MbMat grp[3];
+        RowsIn *gv[3];
+        int cnt = 0, ntot = 0, i = 0;
+        for (const MbMat &m : mats) {
+          if (fmts.begin()[i] == fmt) grp[cnt] = m, gv[cnt++] = views.begin()[i], ntot += m.n;
+          ++i;
+        }
+        if (!cnt) continue;
+        RowsIn out[3];
+        hipError_t r = fmt == RT_LINEAR_Q4K ? launch_q4k_gemv_mb(grp, cnt, n, K, b.mb_stage, part, st, out)
+                                            : launch_kquant_gemv_mb(fmt, grp, cnt, n, K, b.mb_stage, A, part, st, out);
+        if (r != hipSuccess) return r;
+        for (int c = 0; c < cnt; ++c) *gv[c] = out[c];
+        part += (fmt == RT_LINEAR_Q4K ? mb_part_bytes(ntot, K) : kquant_mb_part_bytes(ntot, K)) / sizeof(float);
+      }
+      return hipSuccess;
     }
     // A is prepared once for every matrix of the set (q|k|v, gate|up); the
     // norms and the gelu product write it themselves (A == nullptr), at

@@ -209,7 +209,11 @@ hipError_t launch_q4k_gemv_mb(const MbMat *mats, int nmat, int m, int k, const v
       views[i] = p.ksplit == 1 ? rows_plain(mats[i].y, mats[i].n)
                                : RowsIn{part, p.ksplit, (size_t)8 * ntot, ntot, p.mat[i].part_off};
   if (e != hipSuccess || p.ksplit == 1 || views) return e;
-  const size_t total = (size_t)m * ntot;
+  return launch_mb_reduce(p, s);
+}
+
+hipError_t launch_mb_reduce(const MbArgs &p, hipStream_t s) {
+  const size_t total = (size_t)p.m * p.ntot;
   hipLaunchKernelGGL(k_mb_reduce, dim3((unsigned)std::min<size_t>((total + 255) / 256, 2048)), dim3(256), 0, s, p);
   return hipGetLastError();
 }

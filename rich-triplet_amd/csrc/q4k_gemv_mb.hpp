@@ -101,6 +101,17 @@ hipError_t launch_mb_stage(const float *x, int m, int k, void *stage, hipStream_
 // kernel writes every matrix's y.
 hipError_t launch_q4k_gemv_mb(const MbMat *mats, int nmat, int m, int k, const void *stage, float *part,
                               hipStream_t s, RowsIn *views = nullptr);
+// y of every matrix of p from its split-K partial sums (slice order).
+hipError_t launch_mb_reduce(const MbArgs &p, hipStream_t s);
+
+// The same batched GEMV for Q8_0 and Q6_K weights (planar layout, from the
+// staged digits) and BF16 weights (from the f32 rows x[m][k] themselves),
+// kquant_mb.hip.  k: a multiple of 256 for Q6_K, of 64 for Q8_0 and BF16.
+bool kquant_mb_supported(int fmt, int k);
+int kquant_mb_ksplit(int k);
+size_t kquant_mb_part_bytes(int n_total, int k);
+hipError_t launch_kquant_gemv_mb(int fmt, const MbMat *mats, int nmat, int m, int k, const void *stage,
+                                 const float *x, float *part, hipStream_t s, RowsIn *views = nullptr);
 
 // ---------------------------------------------------------------------------
 // Staging of a batched-GEMV input (device).  Each 64-element chunk of each

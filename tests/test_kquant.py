@@ -320,6 +320,34 @@ def test_q4_k_m_layout_at_gemma3_4b_shape(rt, orc):
     d.close()
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("m", [3, 8])
+def test_q4_k_m_layout_verify_batch_at_gemma3_4b_shape(rt, orc, m):
+    """decode_step_batch (metal_decode.rs:2079-2179) at Gemma-3-4B layer shapes
+    with v and down in Q6_K and one layer's q in Q8_0 and gate in BF16: the M
+    tokens go through each layer together on the batched GEMV of each format
+    (encode_layer_batch sends BF16 projections to gemv_bf16_t_batch,
+    2225-2239), against M consecutive oracle decode steps."""
+    import copy
+    from test_oracle import make_model
+    cfg = dict(rt.GEMMA3_4B, n_layers=2, global_every=2, vocab=4096)
+    ctx, max_seq = 40, 64
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=ctx, seed=7310 + m)
+    plan = {0: dict(v=4, down=4, q=5), 1: dict(v=4, down=4, gate=2)}
+    dev_layers, fmts = apply_formats(orc, cfg, layers, plan, seed=7311 + m)
+    d = mixed_ctx(rt, cfg, dev_layers, fmts, embed, fnorm, ctx, max_seq, layers)
+    assert d.verify_batched
+    toks = [(311 * i + 7) % cfg["vocab"] for i in range(m)]
+    got = d.decode_step_batch(toks, ctx)
+    ref_layers = copy.deepcopy(layers)
+    for i, t in enumerate(toks):
+        ref = orc.gemma3_decode_step(cfg, ref_layers, embed, fnorm, token=t, pos=ctx + i)
+        err = rel_l2(got[i], ref)
+        print(f"Q4_K_M verify batch m={m} token {i}: logits rel-L2 {err:.2e}", flush=True)
+        assert err < 1e-3, (i, err)
+    d.close()
+
+
 # ---------------------------------------------------------------------------
 # prefill with per-projection formats
 # ---------------------------------------------------------------------------
@@ -412,8 +440,8 @@ def plain_ctx(rt, cfg, dev_layers, fmts, embed, fnorm, max_seq):
 def test_mixed_format_prefill_matches_oracle(rt, orc, T, mode, chunk):
     """Prefill of a model with projections in Q6_K, Q8_0 and BF16 (the GEMM
     on f16-widened rows) against the oracle's prefill; chunks of 7 rows take
-    the GEMM too (the batched GEMV reads Q4_K only).  The next decode step
-    reads the prefilled cache."""
+    the batched GEMV of each format.  The next decode step reads the
+    prefilled cache."""
     from test_gpu_decode import tiny
     from test_oracle import make_model
     from test_prefill import KV_TOL, LOGITS_TOL, fresh_caches, read_kv
