@@ -511,6 +511,7 @@ def main() -> int:
                                   "note": "every layer runs the 8 rows at once: batched Q4_K GEMV (int8 MFMA, one "
                                           "pass over the weights), key-split causal attention, batched lm_head"}
         log(f"decode_step_batch M={bm}: {dtb * 1e3:.3f} ms per call -> {bm / dtb:.1f} tok/s")
+        decode["q4_k_m_layout"] = q4_k_m_layout_decode(rt, torch, dev, gen, layers, embed, final_norm, args)
         # GPU prefill of a config-3-length prompt (4096 tokens) on the same weights
         toks = [(7 * i + 3) % V for i in range(ctx)]
         pf = {"tokens": ctx}
@@ -704,6 +705,68 @@ def build_decode(rt, torch, dev, gen, layers, embed, final_norm, args, ctx: int 
     d.set_embed(embed, final_norm)
     torch.cuda.synchronize()
     return d, ctx
+
+
+def synth_q6k_planar(torch, n: int, k: int, gen) -> "torch.Tensor":
+    """Random planar Q6_K (rt_q6k_repack layout: ql | qh | int8 scales | f16 d),
+    d = f16 of |N(0, 0.02)|."""
+    nbt = n * k // 256
+    w = torch.randint(0, 256, (nbt * 210,), dtype=torch.uint8, device="cuda", generator=gen)
+    d = (torch.randn(nbt, device="cuda", generator=gen).abs() * 0.02).half()
+    w[nbt * 208:] = d.view(torch.uint8)
+    return w
+
+
+def q4_k_m_layout_decode(rt, torch, dev, gen, layers, embed, final_norm, args) -> dict:
+    """The config-3 step and the M = 8 verify batch with the Q4_K_M recipe's
+    layout: v and down in Q6_K (kept packed), the other projections Q4_K.
+    The verify reads every weight once per call (batched GEMV of each
+    format); weight bytes per call = the layers' projections + the lm_head."""
+    q6 = [{"v": synth_q6k_planar(torch, KVD, H, gen), "down": synth_q6k_planar(torch, H, F, gen)} for _ in range(L)]
+    ctx = 4096
+    d = rt.HipDecodeContext(dict(rt.GEMMA3_4B), ctx + 8 * (args.warmup + args.steps) + 8 * 12 + 8)
+    fmts = [1, 1, 4, 1, 1, 1, 4]
+    for li, w in enumerate(layers):
+        d.set_layer(li, dict(w, **q6[li]), formats=fmts)
+        kv = torch.randn(2, ctx, KVD, device=dev, generator=gen)
+        d.sync_kv_from_cpu(li, kv[0], kv[1], ctx)
+        del kv
+    d.set_embed(embed, final_norm)
+    torch.cuda.synchronize()
+    pos = ctx
+    for _ in range(args.warmup):
+        d.decode_step_async(pos % V, pos)
+        pos += 1
+    d.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        d.decode_step_async(pos % V, pos)
+        pos += 1
+    d.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    bm, reps = 8, max(4, args.steps // 2)
+    for _ in range(2):
+        d.decode_step_batch_async([(pos + i) % V for i in range(bm)], pos)
+        pos += bm
+    d.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        d.decode_step_batch_async([(pos + i) % V for i in range(bm)], pos)
+        pos += bm
+    d.synchronize()
+    dtb = (time.perf_counter() - t0) / reps
+    q6b = lambda n, k: n * k // 256 * 210  # noqa: E731
+    layer_bytes = sum(q4k_bytes(n, k) for name, n, k in Q4K_SHAPES if name not in ("v", "down")) + q6b(KVD, H) + q6b(H, F)
+    wbytes = L * layer_bytes + V * H * 2
+    out = {"formats": "q, k, o, gate, up Q4_K; v, down Q6_K (planar); BF16 tied lm_head",
+           "verify_batched": d.verify_batched, "decode_ms_per_token": round(dt * 1e3, 4),
+           "verify_m": bm, "verify_ms_per_call": round(dtb * 1e3, 4), "verify_tok_per_s": round(bm / dtb, 1),
+           "weight_bytes_per_call": wbytes, "weight_GBps": round(wbytes / dtb / 1e9, 1)}
+    log(f"Q4_K_M layout: decode step {dt * 1e3:.3f} ms; verify M={bm} {dtb * 1e3:.3f} ms per call "
+        f"({'batched' if d.verify_batched else 'per-token'}), weights {wbytes / dtb / 1e9:.0f} GB/s")
+    d.close()
+    del q6
+    return out
 
 
 def measured_traffic():

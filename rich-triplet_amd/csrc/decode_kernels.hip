@@ -587,7 +587,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-// K (the hidden width, a multiple of 256) is a template constant for the
+// K (the hidden width, a multiple of 32) is a template constant for the
 // fused-kernel shapes and a run-time value (K = 0) otherwise; the staged A
 // takes K*32 bytes of dynamic LDS.
 template <int KC>
@@ -623,15 +623,16 @@ __global__ __launch_bounds__(256) void k_lmhead_batch(const uint16_t *__restrict
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
     u32x4_t bw[B];
 #pragma unroll
-    for (int j = 0; j < B; ++j) bw[j] = *reinterpret_cast<const u32x4_t *>(row + 32 * j);
+    for (int j = 0; j < B; ++j) bw[j] = *reinterpret_cast<const u32x4_t *>(row + 32 * min(j, SEG - 1));
 #pragma unroll 1
     for (int s0 = 0; s0 < SEG; s0 += B) {
       u32x4_t bn[B];
       const int s1 = s0 + B < SEG ? s0 + B : s0;  // next batch (repeats the last one at the end)
 #pragma unroll
-      for (int j = 0; j < B; ++j) bn[j] = *reinterpret_cast<const u32x4_t *>(row + 32 * (s1 + j));
+      for (int j = 0; j < B; ++j) bn[j] = *reinterpret_cast<const u32x4_t *>(row + 32 * min(s1 + j, SEG - 1));
 #pragma unroll
       for (int j = 0; j < B; ++j) {
+        if (s0 + j >= SEG) break;  // a last batch of fewer than B segments (K % 256 != 0; wave-uniform)
         const u32x4_t af = *reinterpret_cast<const u32x4_t *>(xa + (s0 + j) * 512 + aoff);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, af),
                                                       __builtin_bit_cast(bf16x8_t, bw[j]), acc, 0, 0, 0);
@@ -837,7 +838,7 @@ hipError_t enqueue_decode_batch(const DecodeShape &s, const DecodeArgs &a, const
 }
 
 hipError_t prepare_lm_head_batch(int hidden) {
-  if (hidden % 256 != 0 || hidden > kLmHeadMaxHidden) return hipErrorInvalidValue;
+  if (hidden % 32 != 0 || hidden > kLmHeadMaxHidden) return hipErrorInvalidValue;
   const int bytes = hidden * 32;
   if (hidden == 2560) return hipFuncSetAttribute((const void *)k_lmhead_batch<2560>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
@@ -860,12 +861,14 @@ hipError_t enqueue_lm_head_batch(const DecodeShape &s, const DecodeArgs &a, cons
   return l.err;
 }
 
-// Shapes the rows kernels serve (every projection Q4_K): the decode step
-// then runs as a one-row pass of enqueue_rows.
+// Shapes the rows kernels serve: the decode step then runs as a one-row
+// pass of enqueue_rows.  Their projections take any format the batched
+// GEMVs take; a width that is not whole super-blocks (Gemma-3-1B's hidden
+// 1152) leaves the projections that read it to Q8_0 and BF16.
 bool decode_shape_generic(const DecodeShape &s, const char **why) {
   const int qd = s.n_q_heads * s.head_dim;
-  if (s.hidden % 256 != 0 || s.hidden > kLmHeadMaxHidden)
-    return *why = "hidden must be a multiple of 256 up to 4096", false;
+  if (s.hidden % 64 != 0 || s.hidden > kLmHeadMaxHidden)
+    return *why = "hidden must be a multiple of 64 up to 4096", false;
   if (qd % 256 != 0) return *why = "n_q_heads*head_dim must be a multiple of 256", false;
   if (s.ffn % 256 != 0 || s.ffn > 16384) return *why = "ffn must be a multiple of 256 up to 16384", false;
   if (s.head_dim != 128 && s.head_dim != 256) return *why = "head_dim must be 128 or 256", false;

@@ -392,16 +392,211 @@ def test_generic_shape_steps_batch_and_graph(rt, orc):
 
 
 def test_generic_shape_refusals(rt, orc):
-    """A non-Q4_K projection is refused on a rows-kernel shape; a shape that
-    neither kernel set serves is refused at create with both reasons."""
+    """A projection format a decode layer cannot hold (F32) is refused; a
+    shape that neither kernel set serves is refused at create with both
+    reasons."""
     cfg = generic_cfg(n_layers=1, global_every=0)
     layers, embed, fnorm = make_model(orc, cfg, max_seq=16, ctx=0, seed=1700)
     d = rt.HipDecodeContext(cfg, 16)
-    with pytest.raises(rt.RtError, match="Q4_K projections only"):
-        d.set_layer(0, layers[0], formats=[rt.LINEAR_Q4K] * 6 + [rt.LINEAR_BF16])
+    H, F = cfg["hidden"], cfg["ffn"]
+    w = dict(layers[0], down=np.zeros(H * F, np.float32))
+    with pytest.raises(rt.RtError, match="unsupported format"):
+        d.set_layer(0, w, formats=[rt.LINEAR_Q4K] * 6 + [rt.LINEAR_F32])
     d.close()
     with pytest.raises(rt.RtError, match="rows kernels"):
         rt.HipDecodeContext(generic_cfg(hidden=5120), 16)
+
+
+@pytest.mark.gpu
+def test_generic_shape_mixed_formats_match_oracle(rt, orc):
+    """A rows-kernel shape (hidden 768) with projections in Q6_K, Q8_0 and
+    BF16 beside Q4_K (layer 0's q|k|v set in three formats): single steps
+    and a verify batch run on the batched GEMV of each format, a 20-row
+    prefill on the f16 GEMM of each; all against the oracle.
+
+    The synthetic Q6_K / Q8_0 weights are about 30x larger than the Q4_K
+    ones, and some draws of such mixed models amplify rounding a hundredfold
+    (a 3e-5 change of the norm gammas moves the oracle's own logits by
+    1.7e-3).  This plan and seed keep that response under 1e-4, so the bar
+    measures the kernels and not the model's conditioning."""
+    import copy
+    from test_kquant import apply_formats
+    from test_prefill import KV_TOL, fresh_caches, read_kv
+    cfg = generic_cfg(n_layers=3, global_every=3)
+    max_seq, ctx = 48, 6
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=ctx, seed=1810)
+    plan = {0: dict(q=5, v=2, down=4), 1: dict(gate=2, o=5, k=4), 2: dict(up=5, down=2, v=4)}
+    dev_layers, fmts = apply_formats(orc, cfg, layers, plan, seed=1811)
+    d = rt.HipDecodeContext(cfg, max_seq)
+    for i, (D, f) in enumerate(zip(dev_layers, fmts)):
+        d.set_layer(i, D, formats=f)
+        d.sync_kv_from_cpu(i, np.ascontiguousarray(layers[i]["k_cache"][:ctx]),
+                           np.ascontiguousarray(layers[i]["v_cache"][:ctx]), ctx)
+    d.set_embed(embed, fnorm)
+    assert d.verify_batched
+    olayers = copy.deepcopy(layers)
+    for i, tok in enumerate([3, 999]):
+        got = d.decode_step(tok, ctx + i)
+        ref = orc.gemma3_decode_step(cfg, olayers, embed, fnorm, token=tok, pos=ctx + i)
+        assert rel_l2(got, ref) < LOGITS_TOL, (i, rel_l2(got, ref))
+    toks = [5, 6, 7]
+    got = d.decode_step_batch(toks, ctx + 2)
+    for i, t in enumerate(toks):
+        ref = orc.gemma3_decode_step(cfg, olayers, embed, fnorm, token=t, pos=ctx + 2 + i)
+        assert rel_l2(got[i], ref) < LOGITS_TOL, (i, rel_l2(got[i], ref))
+    d.close()
+    # prefill of 20 rows (GEMM) in chunks of 7 (batched GEMVs), sliding rule
+    T = 20
+    d = rt.HipDecodeContext(cfg, max_seq)
+    for i, (D, f) in enumerate(zip(dev_layers, fmts)):
+        d.set_layer(i, D, formats=f)
+    d.set_embed(embed, fnorm)
+    d.set_prefill_chunk(7)
+    ptoks = [(13 * i + 5) % cfg["vocab"] for i in range(T)]
+    got = d.prefill(ptoks, 0, 1)
+    ref_layers = fresh_caches(layers)
+    ref = orc.gemma3_prefill(cfg, ref_layers, embed, fnorm, ptoks, 0, 1)
+    assert rel_l2(got, ref) < LOGITS_TOL, rel_l2(got, ref)
+    for li in range(cfg["n_layers"]):
+        k, v = read_kv(d, cfg, li, T)
+        assert rel_l2(k, ref_layers[li]["k_cache"][:T]) < KV_TOL, li
+        assert rel_l2(v, ref_layers[li]["v_cache"][:T]) < KV_TOL, li
+    d.close()
+
+
+def gemma3_1b_cfg(**kw):
+    """The reference's gemma3_1b preset widths (transformer4.rs:84-104):
+    hidden 1152 (18 chunks of 64, not whole Q4_K super-blocks), 4 q heads
+    and 1 KV head of 256, FFN 6912, sliding window 512; few layers, a small
+    vocabulary."""
+    base = dict(hidden=1152, ffn=6912, n_q_heads=4, n_kv_heads=1, head_dim=256, n_layers=3, vocab=1024,
+                sliding_window=512, global_every=3, rope_theta_local=10000.0, rope_theta_global=1000000.0,
+                rope_fs_local=1.0, rope_fs_global=0.125, eps=1e-6, attn_scale=1.0 / 16.0)
+    base.update(kw)
+    return base
+
+
+def gemma3_1b_model(rt, orc, cfg, max_seq, ctx, seed):
+    """A model at those widths: the projections that read the hidden width
+    (q, k, v, gate, up) in Q8_0 or BF16 per layer, o in Q4_K, down in Q6_K;
+    returns the oracle's layers, the device layers and their formats."""
+    from test_kquant import synth_q6k, synth_q8_0
+    H, F, D = cfg["hidden"], cfg["ffn"], cfg["head_dim"]
+    QD, KVD = cfg["n_q_heads"] * D, cfg["n_kv_heads"] * D
+    rng = np.random.default_rng(seed)
+    shapes = dict(q=(QD, H), k=(KVD, H), v=(KVD, H), o=(H, QD), gate=(F, H), up=(F, H), down=(H, F))
+    layers, dev_layers, fmts = [], [], []
+    s = seed
+    for li in range(cfg["n_layers"]):
+        L, Dl, fmt = {}, {}, {}
+        wide = 5 if li % 2 == 0 else 2  # Q8_0 / BF16 for the hidden-width rows
+        for name, (rows, cols) in shapes.items():
+            s += 1
+            f = 1 if name == "o" else 4 if name == "down" else wide
+            if name == "k" and li == 1:
+                f = 5  # a k in Q8_0 beside BF16 q and v: one set, two formats
+            fmt[name] = f
+            if f == 1:
+                L[name] = Dl[name] = orc.synth_q4k(s, rows, cols)
+            elif f == 4:
+                L[name] = synth_q6k(rng, rows * cols // 256)
+                Dl[name] = rt.q6k_repack(L[name])
+            elif f == 5:
+                L[name] = synth_q8_0(rng, rows * cols // 32)
+                Dl[name] = rt.q8_0_repack(L[name])
+            else:
+                L[name] = Dl[name] = orc.synth_bf16(s, rows * cols)
+        for name, n in dict(in_norm=H, post_attn_norm=H, pre_ffn_norm=H, post_ffn_norm=H, q_norm=D,
+                            k_norm=D).items():
+            s += 1
+            L[name] = Dl[name] = orc.synth_normal(s, n, 0.0, 0.1)
+        kc = np.zeros((max_seq, KVD), np.float32)
+        vc = np.zeros((max_seq, KVD), np.float32)
+        kc[:ctx] = orc.synth_normal(s + 1, ctx * KVD).reshape(ctx, KVD)
+        vc[:ctx] = orc.synth_normal(s + 2, ctx * KVD).reshape(ctx, KVD)
+        s += 2
+        L["k_cache"], L["v_cache"], L["fmt"] = kc, vc, fmt
+        layers.append(L)
+        dev_layers.append(Dl)
+        fmts.append([fmt[p] for p in ("q", "k", "v", "o", "gate", "up", "down")])
+    embed = orc.synth_bf16(seed + 9999, cfg["vocab"] * H)
+    final_norm = orc.synth_normal(seed + 9998, H, 0.0, 0.1)
+    return layers, dev_layers, fmts, embed, final_norm
+
+
+def gemma3_1b_ctx(rt, cfg, layers, dev_layers, fmts, embed, fnorm, ctx, max_seq):
+    d = rt.HipDecodeContext(cfg, max_seq)
+    for i, (D, f) in enumerate(zip(dev_layers, fmts)):
+        d.set_layer(i, D, formats=f)
+        if ctx:
+            d.sync_kv_from_cpu(i, np.ascontiguousarray(layers[i]["k_cache"][:ctx]),
+                               np.ascontiguousarray(layers[i]["v_cache"][:ctx]), ctx)
+    d.set_embed(embed, fnorm)
+    return d
+
+
+@pytest.mark.parametrize("pos", [0, 3, 20])
+def test_gemma3_1b_shape_decode_matches_oracle(rt, orc, pos):
+    """The gemma3_1b preset's widths on the rows kernels (MetalDecodeContext::
+    new takes any Config4, metal_decode.rs:971-1277): a decode step, the next
+    step, and a verify batch of 3 against the oracle."""
+    import copy
+    cfg = gemma3_1b_cfg()
+    max_seq = 40
+    layers, dev_layers, fmts, embed, fnorm = gemma3_1b_model(rt, orc, cfg, max_seq, pos, seed=1900 + pos)
+    d = gemma3_1b_ctx(rt, cfg, layers, dev_layers, fmts, embed, fnorm, pos, max_seq)
+    assert d.verify_batched
+    olayers = copy.deepcopy(layers)
+    for i, tok in enumerate((17, 250)):
+        got = d.decode_step(tok, pos + i)
+        ref = orc.gemma3_decode_step(cfg, olayers, embed, fnorm, token=tok, pos=pos + i)
+        assert np.all(np.isfinite(got))
+        assert rel_l2(got, ref) < LOGITS_TOL, (i, rel_l2(got, ref))
+    toks = [5, 6, 700]
+    got = d.decode_step_batch(toks, pos + 2)
+    for i, t in enumerate(toks):
+        ref = orc.gemma3_decode_step(cfg, olayers, embed, fnorm, token=t, pos=pos + 2 + i)
+        assert rel_l2(got[i], ref) < LOGITS_TOL, (i, rel_l2(got[i], ref))
+    d.close()
+
+
+@pytest.mark.parametrize("T,mode,chunk", [(20, 1, 0), (20, 0, 0), (13, 1, 5)])
+def test_gemma3_1b_shape_prefill_matches_oracle(rt, orc, T, mode, chunk):
+    """Prefill at the gemma3_1b widths (the f16 GEMM of each format; chunks of
+    5 rows on the batched GEMVs) against the oracle, and the next step."""
+    from test_prefill import KV_TOL, fresh_caches, read_kv
+    cfg = gemma3_1b_cfg(sliding_window=8)
+    max_seq = 32
+    layers, dev_layers, fmts, embed, fnorm = gemma3_1b_model(rt, orc, cfg, max_seq, 0, seed=1950 + T)
+    d = gemma3_1b_ctx(rt, cfg, layers, dev_layers, fmts, embed, fnorm, 0, max_seq)
+    if chunk:
+        d.set_prefill_chunk(chunk)
+    toks = [(31 * i + 2) % cfg["vocab"] for i in range(T)]
+    got = d.prefill(toks, 0, mode)
+    ref_layers = fresh_caches(layers)
+    ref = orc.gemma3_prefill(cfg, ref_layers, embed, fnorm, toks, 0, mode)
+    assert rel_l2(got, ref) < LOGITS_TOL, rel_l2(got, ref)
+    for li in range(cfg["n_layers"]):
+        k, v = read_kv(d, cfg, li, T)
+        assert rel_l2(k, ref_layers[li]["k_cache"][:T]) < KV_TOL, li
+        assert rel_l2(v, ref_layers[li]["v_cache"][:T]) < KV_TOL, li
+    if mode == 1:
+        nxt = d.decode_step(9, T)
+        rstep = orc.gemma3_decode_step(cfg, ref_layers, embed, fnorm, token=9, pos=T)
+        assert rel_l2(nxt, rstep) < LOGITS_TOL
+    d.close()
+
+
+def test_gemma3_1b_shape_refuses_q4k_at_hidden_width(rt, orc):
+    """Q4_K rows are whole super-blocks: a q projection of 1152 columns in
+    Q4_K is refused (real gemma-3-1b files quantise those tensors with other
+    types)."""
+    cfg = gemma3_1b_cfg(n_layers=1, global_every=0)
+    layers, dev_layers, fmts, embed, fnorm = gemma3_1b_model(rt, orc, cfg, 8, 0, seed=1990)
+    d = rt.HipDecodeContext(cfg, 8)
+    with pytest.raises(rt.RtError, match="unsupported format"):
+        d.set_layer(0, dev_layers[0], formats=[1] + fmts[0][1:])
+    d.close()
 
 
 def test_memory_report(rt, orc):
