@@ -96,12 +96,26 @@ rt_status rt_weight_cache_clear(void);
  * that stream.  It grows on demand, but not while the stream is being
  * captured: a captured call that would need more returns RT_ESTATE, so make
  * the same call once outside capture first.  Outgrown buffers stay
- * allocated (a graph captured earlier may still read them).
+ * allocated (a graph captured earlier may still read them) until
+ * rt_gemm_workspace_release.  Cost per stream: the largest request made on
+ * it (e.g. m=512, n=k=2560 Q4_K GEMM: A as f16, 2.6 MB, plus the row scales
+ * and split-K partials), grown by at least doubling, plus every buffer it
+ * outgrew: at most about 2x the largest request in all.
  * ------------------------------------------------------------------------- */
 rt_status rt_q4k_gemm_bf16(const uint16_t *a_dev, const void *w_dev, float *c_dev, int64_t m, int64_t n, int64_t k,
                            void *stream);
 rt_status rt_q4k_gemm_f32(const float *a_dev, const void *w_dev, float *c_dev, int64_t m, int64_t n, int64_t k,
                           void *stream);
+/* Frees the calling host thread's workspace for `stream` on the current
+ * device (no counterpart in the reference, whose Metal buffers live as long
+ * as its context).  Synchronises `stream` first; RT_ESTATE while the stream
+ * is being captured.  A graph captured over calls on that stream must not be
+ * replayed afterwards (it reads the freed buffers).  The next call on the
+ * stream allocates again. */
+rt_status rt_gemm_workspace_release(void *stream);
+/* Bytes the calling thread's workspace for `stream` holds on the current
+ * device, outgrown buffers included (0 when none). */
+size_t rt_gemm_workspace_held(void *stream);
 /* Weight formats of a linear layer on the device. */
 #define RT_LINEAR_Q4K 1    /* 144-byte Q4_K blocks as in the file */
 #define RT_LINEAR_BF16 2   /* bf16 [rows][cols] */
@@ -262,7 +276,15 @@ rt_status rt_decode_set_layer(rt_decode *d, int32_t layer, const rt_gemma3_layer
  * (the device layouts of rt_gguf_load_linear_ex).  The reference's context
  * takes Q4_K or BF16 per projection (upload_linear_detect_type,
  * metal_decode.rs:1259-1277, with Q6_K/Q8_0 widened to BF16 at load); here
- * Q6_K and Q8_0 also run natively, in decode, batch and prefill. */
+ * Q6_K and Q8_0 also run natively, in decode, batch and prefill.
+ * Failure (a null or misaligned pointer, an unsupported format, a failed
+ * upload) is checked before anything is uploaded, and the new binding
+ * replaces the old one only when it is whole; but a failed call still
+ * leaves the layer UNSET (its previous binding released, captured graphs
+ * dropped) and rt_decode_step answers RT_ESTATE until the layer is set
+ * again.  A caller that frees borrowed weights and then re-binds therefore
+ * never runs over freed memory, whichever way the re-bind ends.
+ * rt_decode_set_embed behaves the same way for the embedding. */
 rt_status rt_decode_set_layer_formats(rt_decode *d, int32_t layer, const rt_gemma3_layer *w,
                                       const int32_t *formats, int32_t device_ptrs);
 /* BF16 [vocab, hidden] embedding, also the tied lm_head (1097-1105), and the final norm gamma. */

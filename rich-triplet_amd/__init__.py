@@ -57,6 +57,8 @@ _SIGNATURES = {
     "rt_gemv_q4k_t": (_i32, [_vp, _sz, _vp, _sz, _vp]),
     "rt_gemv_bf16_t": (_i32, [_vp, _sz, _vp, _sz, _vp]),
     "rt_weight_cache_clear": (_i32, []),
+    "rt_gemm_workspace_release": (_i32, [_vp]),
+    "rt_gemm_workspace_held": (_sz, [_vp]),
     "rt_q4k_gemv_batch": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "rt_q4k_gemv_batch_noalloc": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "rt_qlinear_forward": (_i32, [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
@@ -345,6 +347,16 @@ def matmul_q4k_t(a, blocks, rows: int):
 
 def weight_cache_clear() -> None:
     check(lib().rt_weight_cache_clear())
+
+
+def gemm_workspace_release(stream=None) -> None:
+    """Free this thread's GEMM / batched-GEMV workspace for `stream` (torch
+    stream or None for the null stream) on the current device."""
+    check(lib().rt_gemm_workspace_release(_stream(stream)))
+
+
+def gemm_workspace_held(stream=None) -> int:
+    return int(lib().rt_gemm_workspace_held(_stream(stream)))
 
 
 # ---------------------------------------------------------------------------

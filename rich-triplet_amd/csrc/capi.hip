@@ -430,6 +430,7 @@ struct GemmWorkspace {
   void *buf = nullptr;
   size_t cap = 0;
   std::vector<void *> retired;
+  size_t retired_bytes = 0;
 };
 thread_local std::map<std::pair<int, hipStream_t>, GemmWorkspace> g_gemm_ws;
 
@@ -451,7 +452,7 @@ rt_status gemm_workspace(size_t bytes, hipStream_t stream, void **out) {
     void *nb = nullptr;
     e = hipMalloc(&nb, grow);
     if (e != hipSuccess) return hip_error(e, "gemm workspace hipMalloc");
-    if (w.buf) w.retired.push_back(w.buf);
+    if (w.buf) w.retired.push_back(w.buf), w.retired_bytes += w.cap;
     w.buf = nb;
     w.cap = grow;
   }
@@ -565,6 +566,33 @@ rt_status rt_qlinear_forward_host(int32_t fmt, const void *w, size_t w_bytes, co
   st = rt_qlinear_forward(fmt, wdev, bd, xd, od, m, n, k, nullptr);
   if (st != RT_OK) return st;
   return hip_error(hipMemcpy(out, od, (size_t)m * n * 4, hipMemcpyDeviceToHost), who);
+}
+
+rt_status rt_gemm_workspace_release(void *stream) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_error(e, "hipGetDevice");
+  auto it = g_gemm_ws.find({dev, (hipStream_t)stream});
+  if (it == g_gemm_ws.end()) return RT_OK;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  e = hipStreamIsCapturing((hipStream_t)stream, &cs);
+  if (e != hipSuccess) return hip_error(e, "hipStreamIsCapturing");
+  if (cs != hipStreamCaptureStatusNone)
+    return set_error(RT_ESTATE, "rt_gemm_workspace_release: the stream is being captured");
+  // queued calls on the stream may still read the buffers
+  e = hipStreamSynchronize((hipStream_t)stream);
+  if (e != hipSuccess) return hip_error(e, "rt_gemm_workspace_release: hipStreamSynchronize");
+  for (void *q : it->second.retired) e = hipFree(q) == hipSuccess ? e : hipErrorInvalidValue;
+  if (it->second.buf && hipFree(it->second.buf) != hipSuccess) e = hipErrorInvalidValue;
+  g_gemm_ws.erase(it);
+  return hip_error(e, "rt_gemm_workspace_release: hipFree");
+}
+
+size_t rt_gemm_workspace_held(void *stream) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  auto it = g_gemm_ws.find({dev, (hipStream_t)stream});
+  return it == g_gemm_ws.end() ? 0 : it->second.cap + it->second.retired_bytes;
 }
 
 rt_status rt_weight_cache_clear(void) {

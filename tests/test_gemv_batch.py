@@ -146,3 +146,24 @@ def test_linear_gemv_batch_is_row_independent(rt, orc, dev, fmt):
     assert torch.equal(c1[0], c8[5])
     if fmt != BF16:
         assert torch.equal(c4[0], 4 * c1[0])
+
+
+@pytest.mark.gpu
+def test_gemm_workspace_release_frees_and_regrows(rt, orc, dev):
+    """rt_gemm_workspace_release frees the stream's workspace (held bytes
+    drop to 0) and the next call allocates it again with the same result."""
+    import torch
+    n, k = 1024, 2560
+    blocks = to_dev(orc.synth_q4k(55, n, k), dev)
+    a = to_dev(np.stack([orc.synth_normal(56 + i, k) for i in range(4)]), dev)
+    c0 = torch.empty((4, n), dtype=torch.float32, device=dev)
+    c1 = torch.empty_like(c0)
+    rt.q4k_gemv_batch(blocks, a, c0, 4, n, k)
+    assert rt.gemm_workspace_held() > 0
+    rt.gemm_workspace_release()
+    assert rt.gemm_workspace_held() == 0
+    rt.gemm_workspace_release()  # nothing held: a no-op
+    rt.q4k_gemv_batch(blocks, a, c1, 4, n, k)
+    torch.cuda.synchronize()
+    assert rt.gemm_workspace_held() > 0
+    assert torch.equal(c0, c1)
