@@ -421,7 +421,7 @@ def test_generic_shape_mixed_formats_match_oracle(rt, orc):
     measures the kernels and not the model's conditioning."""
     import copy
     from test_kquant import apply_formats
-    from test_prefill import KV_TOL, fresh_caches, read_kv
+    from test_prefill import assert_kv_rows, fresh_caches
     cfg = generic_cfg(n_layers=3, global_every=3)
     max_seq, ctx = 48, 6
     layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=ctx, seed=1810)
@@ -457,10 +457,7 @@ def test_generic_shape_mixed_formats_match_oracle(rt, orc):
     ref_layers = fresh_caches(layers)
     ref = orc.gemma3_prefill(cfg, ref_layers, embed, fnorm, ptoks, 0, 1)
     assert rel_l2(got, ref) < LOGITS_TOL, rel_l2(got, ref)
-    for li in range(cfg["n_layers"]):
-        k, v = read_kv(d, cfg, li, T)
-        assert rel_l2(k, ref_layers[li]["k_cache"][:T]) < KV_TOL, li
-        assert rel_l2(v, ref_layers[li]["v_cache"][:T]) < KV_TOL, li
+    assert_kv_rows(d, cfg, layers, embed, fnorm, ptoks, 1, False, ref_layers)
     d.close()
 
 
@@ -564,7 +561,7 @@ def test_gemma3_1b_shape_decode_matches_oracle(rt, orc, pos):
 def test_gemma3_1b_shape_prefill_matches_oracle(rt, orc, T, mode, chunk):
     """Prefill at the gemma3_1b widths (the f16 GEMM of each format; chunks of
     5 rows on the batched GEMVs) against the oracle, and the next step."""
-    from test_prefill import KV_TOL, fresh_caches, read_kv
+    from test_prefill import assert_kv_rows, fresh_caches
     cfg = gemma3_1b_cfg(sliding_window=8)
     max_seq = 32
     layers, dev_layers, fmts, embed, fnorm = gemma3_1b_model(rt, orc, cfg, max_seq, 0, seed=1950 + T)
@@ -576,10 +573,7 @@ def test_gemma3_1b_shape_prefill_matches_oracle(rt, orc, T, mode, chunk):
     ref_layers = fresh_caches(layers)
     ref = orc.gemma3_prefill(cfg, ref_layers, embed, fnorm, toks, 0, mode)
     assert rel_l2(got, ref) < LOGITS_TOL, rel_l2(got, ref)
-    for li in range(cfg["n_layers"]):
-        k, v = read_kv(d, cfg, li, T)
-        assert rel_l2(k, ref_layers[li]["k_cache"][:T]) < KV_TOL, li
-        assert rel_l2(v, ref_layers[li]["v_cache"][:T]) < KV_TOL, li
+    assert_kv_rows(d, cfg, layers, embed, fnorm, toks, mode, (chunk or T) > 8, ref_layers)
     if mode == 1:
         nxt = d.decode_step(9, T)
         rstep = orc.gemma3_decode_step(cfg, ref_layers, embed, fnorm, token=9, pos=T)

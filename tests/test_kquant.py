@@ -444,7 +444,7 @@ def test_mixed_format_prefill_matches_oracle(rt, orc, T, mode, chunk):
     prefilled cache."""
     from test_gpu_decode import tiny
     from test_oracle import make_model
-    from test_prefill import KV_TOL, LOGITS_TOL, fresh_caches, read_kv
+    from test_prefill import LOGITS_TOL, assert_kv_rows, fresh_caches
     cfg = tiny(2)
     max_seq = 40
     layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=0, seed=7400 + T)
@@ -459,10 +459,7 @@ def test_mixed_format_prefill_matches_oracle(rt, orc, T, mode, chunk):
     assert np.all(np.isfinite(got))
     print(f"mixed-format prefill T={T} mode={mode} chunk={chunk}: logits rel-L2 {rel_l2(got, ref):.2e}", flush=True)
     assert rel_l2(got, ref) < LOGITS_TOL, rel_l2(got, ref)
-    for li in range(cfg["n_layers"]):
-        k, v = read_kv(d, cfg, li, T)
-        assert rel_l2(k, ref_layers[li]["k_cache"][:T]) < KV_TOL, li
-        assert rel_l2(v, ref_layers[li]["v_cache"][:T]) < KV_TOL, li
+    assert_kv_rows(d, cfg, layers, embed, fnorm, toks, mode, (chunk or T) > 8, ref_layers)
     if mode == 1:
         nxt = d.decode_step(9, T)
         ref = orc.gemma3_decode_step(cfg, ref_layers, embed, fnorm, token=9, pos=T)
@@ -473,10 +470,12 @@ def test_mixed_format_prefill_matches_oracle(rt, orc, T, mode, chunk):
 @pytest.mark.gpu
 def test_q4_k_m_layout_prefill_at_gemma3_4b_shape(rt, orc):
     """Gemma-3-4B layer shapes with v and down in Q6_K: a 200-token prefill
-    equals 200 GPU decode steps (native Q6_K GEMV, pinned to the oracle above)."""
+    equals 200 GPU decode steps (native Q6_K GEMV, pinned to the oracle
+    above) in logits and KV rows, and its KV rows match np_prefill(gpu_ops)
+    (Q6_K widened to f16 for the GEMM) on every row."""
     from test_gpu_decode import d2h
     from test_oracle import make_model
-    from test_prefill import KV_TOL, LOGITS_TOL, read_kv
+    from test_prefill import LOGITS_TOL, assert_kv_rows, read_kv
     cfg = dict(rt.GEMMA3_4B, n_layers=2, global_every=2, vocab=4096)
     T, max_seq = 200, 224
     layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=0, seed=7500)
@@ -491,10 +490,8 @@ def test_q4_k_m_layout_prefill_at_gemma3_4b_shape(rt, orc):
     d2.synchronize()
     ref = d2h(d2.logits_ptr(), cfg["vocab"])
     assert rel_l2(got, ref) < LOGITS_TOL, rel_l2(got, ref)
-    for li in range(2):
-        k1, v1 = read_kv(d1, cfg, li, T)
-        k2, v2 = read_kv(d2, cfg, li, T)
-        assert rel_l2(k1, k2) < KV_TOL and rel_l2(v1, v2) < KV_TOL
+    steps = [dict(zip(("k_cache", "v_cache"), read_kv(d2, cfg, li, T))) for li in range(2)]
+    assert_kv_rows(d1, cfg, layers, embed, fnorm, toks, 1, True, agg_layers=steps)
     d1.close()
     d2.close()
 
