@@ -511,6 +511,7 @@ def main() -> int:
                                   "note": "every layer runs the 8 rows at once: batched Q4_K GEMV (int8 MFMA, one "
                                           "pass over the weights), key-split causal attention, batched lm_head"}
         log(f"decode_step_batch M={bm}: {dtb * 1e3:.3f} ms per call -> {bm / dtb:.1f} tok/s")
+        decode["q4k_lm_head"] = q4k_lm_head_decode(rt, torch, gen, d, ctx, dec_bytes, args)
         decode["q4_k_m_layout"] = q4_k_m_layout_decode(rt, torch, dev, gen, layers, embed, final_norm, args)
         # GPU prefill of a config-3-length prompt (4096 tokens) on the same weights
         toks = [(7 * i + 3) % V for i in range(ctx)]
@@ -705,6 +706,44 @@ def build_decode(rt, torch, dev, gen, layers, embed, final_norm, args, ctx: int 
     d.set_embed(embed, final_norm)
     torch.cuda.synchronize()
     return d, ctx
+
+
+def q4k_lm_head_decode(rt, torch, gen, d, ctx: int, dec_bytes: int, args) -> dict:
+    """The config-3 step and M = 8 verify with a Q4_K lm_head (the reference's
+    q4k-lm-head feature, metal_decode.rs:1082-1094): the same context and
+    positions from ctx, the 262144x2560 head as random Q4_K blocks (the same
+    bytes as a requantised embedding; parity is in the tests); the tied BF16
+    head is restored afterwards."""
+    head = synth_q4k(torch, V, H, gen)
+    d.set_lm_head(1, head)
+    pos = ctx
+    for _ in range(args.warmup):
+        d.decode_step_async(pos % V, pos)
+        pos += 1
+    d.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        d.decode_step_async(pos % V, pos)
+        pos += 1
+    d.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    bm, reps = 8, max(2, args.steps // 4)
+    d.decode_step_batch_async([(pos + i) % V for i in range(bm)], pos)
+    d.synchronize()
+    t0 = time.perf_counter()
+    for r in range(reps):
+        d.decode_step_batch_async([(pos + i) % V for i in range(bm)], pos)
+    d.synchronize()
+    dtb = (time.perf_counter() - t0) / reps
+    d.set_lm_head(0, None)
+    del head
+    nbytes = dec_bytes - V * H * 2 + q4k_bytes(V, H)
+    out = {"workload": "config 3 with a Q4_K lm_head (feature q4k-lm-head) instead of the BF16 tied one",
+           "tok_per_s": round(1.0 / dt, 1), "ms_per_token": round(dt * 1e3, 4), "bytes_per_token": nbytes,
+           "GBps": round(nbytes / dt / 1e9, 1), "frac_of_hbm_peak": round(nbytes / dt / 1e9 / PEAK_HBM_GBS, 4),
+           "verify_m": bm, "verify_ms_per_call": round(dtb * 1e3, 4), "verify_tok_per_s": round(bm / dtb, 1)}
+    log(f"Q4_K lm_head: decode step {dt * 1e3:.3f} ms -> {1 / dt:.1f} tok/s; verify M={bm} {dtb * 1e3:.3f} ms")
+    return out
 
 
 def synth_q6k_planar(torch, n: int, k: int, gen) -> "torch.Tensor":

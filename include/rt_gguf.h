@@ -91,6 +91,13 @@ rt_status rt_gguf_tensor_to_f32(const rt_gguf *g, int64_t idx, float *dst, uint6
  * f32 [rows, cols] -> Q4_K blocks, cols % 256 == 0. */
 rt_status rt_q4k_quantize(const float *src, size_t rows, size_t cols, uint8_t *blocks);
 
+/* Q4KMat::quantize_from_bf16 (autograd2.rs:1252-1289): bf16 [rows, cols] ->
+ * Q4_K blocks, row by row (no f32 copy of the whole matrix), cols % 256 == 0;
+ * the same blocks as rt_q4k_quantize of the widened rows.  The reference's
+ * q4k-lm-head feature requantises the tied lm_head this way at upload
+ * (metal_decode.rs:1082-1094); see rt_decode_set_lm_head. */
+rt_status rt_q4k_quantize_bf16(const uint16_t *src, size_t rows, size_t cols, uint8_t *blocks);
+
 /* The weight of a linear layer as the hot path consumes it (RT_LINEAR_*
  * formats are defined in rt_hip.h). */
 typedef struct {

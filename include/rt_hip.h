@@ -289,6 +289,18 @@ rt_status rt_decode_set_layer_formats(rt_decode *d, int32_t layer, const rt_gemm
                                       const int32_t *formats, int32_t device_ptrs);
 /* BF16 [vocab, hidden] embedding, also the tied lm_head (1097-1105), and the final norm gamma. */
 rt_status rt_decode_set_embed(rt_decode *d, const uint16_t *embed, const float *final_norm, int32_t device_ptrs);
+/* An lm_head apart from the embedding (metal_decode.rs:1079-1107):
+ * RT_LINEAR_Q4K, Q4_K blocks [vocab][hidden/256] (hidden % 256 == 0): the
+ * model's own Q4_K head, or the BF16 one requantised by rt_q4k_quantize_bf16
+ * (the reference's q4k-lm-head feature, 1082-1094); every logit then comes
+ * from the Q4_K GEMV (one token) or the batched Q4_K GEMV (verify, prefill)
+ * of the final-normed hidden state, as dispatch_gemv / dispatch_gemv_q4k_batch
+ * do (2053-2063, 2164-2172), reading 0.28x the BF16 head's bytes.
+ * RT_LINEAR_BF16: an untied BF16 head [vocab, hidden].  w = NULL (fmt
+ * ignored) restores the tied embedding, the default.  device_ptrs as for
+ * rt_decode_set_layer.  A failed call leaves the tied embedding as the
+ * head. */
+rt_status rt_decode_set_lm_head(rt_decode *d, int32_t fmt, const void *w, int32_t device_ptrs);
 /* sync_kv_from_cpu (metal_decode.rs:1366-1396) for one layer: seq_len rows of K and V. */
 rt_status rt_decode_sync_kv(rt_decode *d, int32_t layer, const float *k, const float *v, int32_t seq_len,
                             int32_t device_ptrs);

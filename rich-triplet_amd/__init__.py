@@ -118,6 +118,8 @@ _SIGNATURES = {
     "rt_gguf_read_tensor": (_i32, [_vp, _i64, _vp, C.c_uint64]),
     "rt_gguf_tensor_to_f32": (_i32, [_vp, _i64, _vp, C.c_uint64]),
     "rt_q4k_quantize": (_i32, [_vp, _sz, _sz, _vp]),
+    "rt_q4k_quantize_bf16": (_i32, [_vp, _sz, _sz, _vp]),
+    "rt_decode_set_lm_head": (_i32, [_vp, _i32, _vp, _i32]),
     "rt_gguf_load_linear": (_i32, [_vp, _i64, _vp]),
     "rt_gguf_load_linear_ex": (_i32, [_vp, _i64, _i32, _vp]),
     "rt_linear_free": (_i32, [_vp]),
@@ -454,6 +456,14 @@ class HipDecodeContext:
             self._keep.append((embed, final_norm))
         check(lib().rt_decode_set_embed(self._h, _addr(embed), _addr(final_norm), dev))
 
+    def set_lm_head(self, fmt: int = 0, w=None) -> None:
+        """An lm_head apart from the embedding: LINEAR_Q4K blocks [vocab][hidden/256]
+        or LINEAR_BF16 [vocab, hidden]; w None restores the tied embedding."""
+        dev = self._on_device(w) if w is not None else 0
+        if dev:
+            self._keep.append(w)
+        check(lib().rt_decode_set_lm_head(self._h, fmt, _addr(w) if w is not None else None, dev))
+
     def sync_kv_from_cpu(self, layer: int, k, v, seq_len: int) -> None:
         check(lib().rt_decode_sync_kv(self._h, layer, _addr(k), _addr(v), seq_len, self._on_device(k)))
 
@@ -541,6 +551,6 @@ class HipDecodeContext:
         return s.value
 
 
-from .gguf import GgufFile, GgufTensorInfo, Linear, load_linear_from_gguf, q4k_quantize  # noqa: E402,F401
+from .gguf import GgufFile, GgufTensorInfo, Linear, load_linear_from_gguf, q4k_quantize, q4k_quantize_bf16  # noqa: E402,F401
 from . import generate  # noqa: E402,F401
 from .generate import GEMMA3_EOS, NgramDraftEngine, generate_greedy, greedy_token  # noqa: E402,F401

@@ -47,7 +47,11 @@ enum Proj { kProjQ, kProjK, kProjV, kProjO, kProjGate, kProjUp, kProjDown };
 // Step-wide device buffers and constants.
 struct DecodeArgs {
   const int *params;       // {token, position}
-  const uint16_t *embed;   // [vocab, hidden] bf16, also the tied lm_head
+  const uint16_t *embed;   // [vocab, hidden] bf16 token embedding
+  const uint16_t *lm_bf16; // BF16 lm_head [vocab, hidden]: the tied embedding unless set apart
+  const uint8_t *lm_q4k;   // Q4_K lm_head [vocab][hidden/256] blocks (replaces lm_bf16), or null
+  void *lm_stage;          // Q4_K head, several rows: staged activations (mb_stage_bytes(hidden))
+  float *lm_part;          // and split-K partials (mb_head_part_bytes(vocab, hidden)), or null
   const float *g_final;
   float *hid, *x2, *q, *k, *v, *attn, *o, *h, *dn, *logits;
   float *xn, *u;           // normalised input of a split projection set [hidden]; up output [ffn]

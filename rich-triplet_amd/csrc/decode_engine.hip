@@ -16,6 +16,7 @@
 
 #include "../../include/rt_hip.h"
 #include "decode.hpp"
+#include "q4k_gemv_mb.hpp"
 #include "rt_capi_util.hpp"
 #include "rt_kernels.hpp"
 
@@ -34,12 +35,14 @@ struct rt_decode {
     int kind;
   };
   std::vector<Alloc> owned;
-  size_t bound_weight_bytes[65] = {};    // weights bound by device pointer: per layer, [64] embedding + final norm
+  size_t bound_weight_bytes[66] = {};    // weights bound by device pointer: per layer, [64] embedding + final norm, [65] lm_head
   std::vector<LayerArgs> layers;
   std::vector<char> layer_set;
   std::vector<void *> owned_layer[64];  // per-layer uploads (replaced on re-set)
   bool embed_set = false;
   void *embed_owned = nullptr, *final_owned = nullptr;
+  int lm_fmt = 0;                        // lm_head: 0 the tied embedding, else RT_LINEAR_Q4K / RT_LINEAR_BF16
+  std::vector<void *> lm_owned;          // its upload and (Q4_K) batched-head scratch
   DecodeArgs args{};
   int *params_dev = nullptr;             // kMaxBatch step parameter slots (kParamRopeLocal)
   int *params_host = nullptr;            // pinned
@@ -459,6 +462,7 @@ rt_status rt_decode_set_embed(rt_decode *d, const uint16_t *embed, const float *
     return st;
   }
   d->args.embed = (const uint16_t *)pe;
+  if (d->lm_fmt == 0) d->args.lm_bf16 = d->args.embed;
   d->args.g_final = (const float *)pf;
   d->bound_weight_bytes[64] = device_ptrs ? (size_t)d->cfg.vocab * d->cfg.hidden * 2 + (size_t)d->cfg.hidden * 4 : 0;
   if (!device_ptrs) {
@@ -466,6 +470,63 @@ rt_status rt_decode_set_embed(rt_decode *d, const uint16_t *embed, const float *
     d->final_owned = (void *)pf;
   }
   d->embed_set = true;
+  return RT_OK;
+}
+
+// The lm_head apart from the embedding (metal_decode.rs:1079-1107): a Q4_K
+// head (the model's own, or the BF16 one requantised: feature q4k-lm-head)
+// or an untied BF16 one; w == nullptr restores the tied embedding.
+rt_status rt_decode_set_lm_head(rt_decode *d, int32_t fmt, const void *w, int32_t device_ptrs) {
+  if (!d) return set_error(RT_EINVAL, "rt_decode_set_lm_head: null context");
+  const size_t V = (size_t)d->cfg.vocab, H = (size_t)d->cfg.hidden;
+  rt_status st = RT_OK;
+  size_t bytes = 0;
+  if (w) {
+    if (fmt == RT_LINEAR_Q4K && H % 256 == 0) bytes = V * (H / 256) * 144;
+    else if (fmt == RT_LINEAR_BF16) bytes = V * H * 2;
+    else
+      st = set_error(RT_EINVAL, "rt_decode_set_lm_head: format %d unsupported (RT_LINEAR_Q4K with hidden %% 256 == 0, "
+                     "or RT_LINEAR_BF16)", fmt);
+  }
+  // the new head is built aside; any failure leaves the tied embedding
+  (void)hipStreamSynchronize(d->stream);
+  std::vector<void *> own;
+  const void *pw = nullptr;
+  void *stage = nullptr, *part = nullptr;
+  if (st == RT_OK && w) st = bind_buf(d, w, bytes, device_ptrs, own, &pw, "lm_head");
+  if (st == RT_OK && w && fmt == RT_LINEAR_Q4K) {
+    st = dalloc(d, mb_stage_bytes((int)H), &stage, rt_decode::kBatch);
+    if (st == RT_OK) own.push_back(stage);
+    const size_t pb = mb_head_part_bytes((int)V, (int)H);
+    if (st == RT_OK && pb) {
+      st = dalloc(d, pb, &part, rt_decode::kBatch);
+      if (st == RT_OK) own.push_back(part);
+    }
+  }
+  for (void *q : d->lm_owned) dfree(d, q);
+  d->lm_owned.clear();
+  drop_graph(d);
+  d->lm_fmt = 0;
+  d->args.lm_q4k = nullptr;
+  d->args.lm_stage = nullptr;
+  d->args.lm_part = nullptr;
+  d->args.lm_bf16 = d->args.embed;
+  d->bound_weight_bytes[65] = 0;
+  if (st != RT_OK) {
+    for (void *q : own) dfree(d, q);
+    return st;
+  }
+  if (!w) return RT_OK;
+  d->lm_fmt = fmt;
+  d->lm_owned = std::move(own);
+  if (fmt == RT_LINEAR_Q4K) {
+    d->args.lm_q4k = static_cast<const uint8_t *>(pw);
+    d->args.lm_stage = stage;
+    d->args.lm_part = static_cast<float *>(part);
+  } else {
+    d->args.lm_bf16 = static_cast<const uint16_t *>(pw);
+  }
+  if (device_ptrs) d->bound_weight_bytes[65] = bytes;
   return RT_OK;
 }
 

@@ -22,6 +22,7 @@
 #include "decode.hpp"
 #include "gemma3_math.hpp"
 #include "q4k_gemv.hpp"
+#include "q4k_gemv_mb.hpp"
 #include "rt_device.hpp"
 #include "rt_kernels.hpp"
 
@@ -490,7 +491,8 @@ __global__ __launch_bounds__(256) void k_attn_combine(DecodeArgs a, int nchunk) 
 
 // ---------------------------------------------------------------------------
 // k_lmhead: x = x2 + rms(dn)(1+g_post_ffn_last); xn = rms(x)(1+g_final);
-// logits = E(bf16, tied embedding) . xn          (transformer4.rs:2380-2385)
+// logits = E(bf16 lm_head, the tied embedding by default) . xn
+// (transformer4.rs:2380-2385)
 // ---------------------------------------------------------------------------
 template <int CPL>
 __global__ __launch_bounds__(256) void k_lmhead(DecodeArgs a, LayerArgs last) {
@@ -516,7 +518,7 @@ __global__ __launch_bounds__(256) void k_lmhead(DecodeArgs a, LayerArgs last) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int r = min(r0 + u, N - 1);
-      const uint4 *rp = reinterpret_cast<const uint4 *>(a.embed + (size_t)r * K);
+      const uint4 *rp = reinterpret_cast<const uint4 *>(a.lm_bf16 + (size_t)r * K);
 #pragma unroll
       for (int i = 0; i < CPL; ++i) wv[u][i] = rp[i * 64 + lane];
     }
@@ -804,6 +806,18 @@ static hipError_t enqueue_layers(const DecodeShape &s, const DecodeArgs &a, cons
 
 hipError_t enqueue_lm_head(const DecodeShape &s, const DecodeArgs &a, const LayerArgs &last, hipStream_t stream) {
   Launch l{stream};
+  if (a.lm_q4k) {
+    // a Q4_K lm_head (metal_decode.rs:1079-1107, dispatch_gemv 2053-2063):
+    // the final norm into a.xn (free once the last layer is done), then the
+    // single-token Q4_K GEMV over the vocabulary rows
+    if (s.hidden == 2560)
+      hipLaunchKernelGGL((k_final_norm<2560>), dim3(1), dim3(256), 0, l.s, a, last, a.xn);
+    else
+      hipLaunchKernelGGL((k_final_norm<512>), dim3(1), dim3(256), 0, l.s, a, last, a.xn);
+    l.check();
+    if (l.err == hipSuccess) l.err = launch_q4k_gemv(a.lm_q4k, a.xn, a.logits, s.vocab, s.hidden, l.s);
+    return l.err;
+  }
   // three workgroups per CU stay resident for the whole pass (grid-stride rows)
   const dim3 grid(768);
   if (s.hidden == 2560) hipLaunchKernelGGL((k_lmhead<5>), grid, dim3(256), 0, l.s, a, last);
@@ -849,13 +863,21 @@ hipError_t prepare_lm_head_batch(int hidden) {
 hipError_t enqueue_lm_head_batch(const DecodeShape &s, const DecodeArgs &a, const float *xn, float *logits_b, int m,
                                  hipStream_t stream) {
   Launch l{stream};
+  if (a.lm_q4k) {
+    // gemv_q4k_t_batch over the vocabulary (metal_decode.rs:2168-2172): the
+    // m rows staged as digits once, the Q4_K head read once for all of them
+    l.err = launch_mb_stage(xn, m, s.hidden, a.lm_stage, l.s);
+    if (l.err == hipSuccess)
+      l.err = launch_q4k_gemv_mb_head(a.lm_q4k, logits_b, s.vocab, m, s.hidden, a.lm_stage, a.lm_part, l.s);
+    return l.err;
+  }
   const size_t lds = (size_t)s.hidden * 32;
   if (s.hidden == 2560)
-    hipLaunchKernelGGL((k_lmhead_batch<2560>), dim3(512), dim3(256), lds, l.s, a.embed, xn, logits_b, s.vocab, m, 0);
+    hipLaunchKernelGGL((k_lmhead_batch<2560>), dim3(512), dim3(256), lds, l.s, a.lm_bf16, xn, logits_b, s.vocab, m, 0);
   else if (s.hidden == 512)
-    hipLaunchKernelGGL((k_lmhead_batch<512>), dim3(512), dim3(256), lds, l.s, a.embed, xn, logits_b, s.vocab, m, 0);
+    hipLaunchKernelGGL((k_lmhead_batch<512>), dim3(512), dim3(256), lds, l.s, a.lm_bf16, xn, logits_b, s.vocab, m, 0);
   else
-    hipLaunchKernelGGL((k_lmhead_batch<0>), dim3(512), dim3(256), lds, l.s, a.embed, xn, logits_b, s.vocab, m,
+    hipLaunchKernelGGL((k_lmhead_batch<0>), dim3(512), dim3(256), lds, l.s, a.lm_bf16, xn, logits_b, s.vocab, m,
                        s.hidden);
   l.check();
   return l.err;

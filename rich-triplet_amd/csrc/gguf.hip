@@ -623,6 +623,30 @@ rt_status rt_q4k_quantize(const float *src, size_t rows, size_t cols, uint8_t *b
   return guarded("rt_q4k_quantize", [&] { return q4k_quantize(src, rows, cols, blocks); });
 }
 
+// Q4KMat::quantize_from_bf16 (autograd2.rs:1252-1289): each row widened to
+// f32 in a per-thread row buffer, then quantized block by block as above.
+static rt_status q4k_quantize_bf16(const uint16_t *src, size_t rows, size_t cols, uint8_t *blocks) {
+  if (!src || !blocks) return set_error(RT_EINVAL, "rt_q4k_quantize_bf16: null pointer");
+  if (cols == 0 || cols % 256 != 0)
+    return set_error(RT_EINVAL, "rt_q4k_quantize_bf16: cols must be a multiple of 256, got %zu", cols);
+  const size_t nb = cols / 256;
+  parallel_rows(rows, [&](size_t r0, size_t r1) {
+    std::vector<float> row(cols);
+    for (size_t r = r0; r < r1; ++r) {
+      for (size_t c = 0; c < cols; ++c) {
+        const uint32_t bits = (uint32_t)src[r * cols + c] << 16;
+        std::memcpy(&row[c], &bits, 4);
+      }
+      for (size_t b = 0; b < nb; ++b) quantize_q4k_block(row.data() + 256 * b, blocks + (r * nb + b) * 144);
+    }
+  });
+  return RT_OK;
+}
+
+rt_status rt_q4k_quantize_bf16(const uint16_t *src, size_t rows, size_t cols, uint8_t *blocks) {
+  return guarded("rt_q4k_quantize_bf16", [&] { return q4k_quantize_bf16(src, rows, cols, blocks); });
+}
+
 static rt_status gguf_load_linear(const rt_gguf *g, int64_t idx, int32_t flags, rt_linear *out) {
   const TensorEntry *t = entry(g, idx);
   if (!t || !out) return set_error(RT_EINVAL, "rt_gguf_load_linear: bad handle or index");

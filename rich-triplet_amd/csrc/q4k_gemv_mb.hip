@@ -212,6 +212,35 @@ hipError_t launch_q4k_gemv_mb(const MbMat *mats, int nmat, int m, int k, const v
   return launch_mb_reduce(p, s);
 }
 
+// One matrix of many rows (an lm_head over the vocabulary): for K of 2 or 10
+// super-blocks the whole row is one slice (no partial sums, no reduction;
+// the rows alone give thousands of workgroups), other K take the split path.
+static bool mb_head_whole_row(int k) { return k / 256 == 2 || k / 256 == 10; }
+
+size_t mb_head_part_bytes(int n, int k) { return mb_head_whole_row(k) ? 0 : mb_part_bytes(n, k); }
+
+hipError_t launch_q4k_gemv_mb_head(const uint8_t *w, float *y, int n, int m, int k, const void *stage, float *part,
+                                   hipStream_t s) {
+  if (!mb_head_whole_row(k)) {
+    const MbMat mat{w, y, n, 0, 0};
+    return launch_q4k_gemv_mb(&mat, 1, m, k, stage, part, s);
+  }
+  MbArgs p{};
+  p.nmat = 1;
+  p.mat[0] = MbMat{w, y, n, (n + 63) / 64, 0};
+  p.dig = static_cast<const int8_t *>(stage);
+  p.stats = reinterpret_cast<const float *>(p.dig + (size_t)(k / 64) * 8 * 128);
+  p.m = m;
+  p.k = k;
+  p.ntot = n;
+  p.ksplit = 1;
+  if (k / 256 == 10)
+    hipLaunchKernelGGL(k_q4k_gemv_mb<10>, dim3(p.mat[0].row_blocks, 1), dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(k_q4k_gemv_mb<2>, dim3(p.mat[0].row_blocks, 1), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
 hipError_t launch_mb_reduce(const MbArgs &p, hipStream_t s) {
   const size_t total = (size_t)p.m * p.ntot;
   hipLaunchKernelGGL(k_mb_reduce, dim3((unsigned)std::min<size_t>((total + 255) / 256, 2048)), dim3(256), 0, s, p);

@@ -103,6 +103,12 @@ hipError_t launch_q4k_gemv_mb(const MbMat *mats, int nmat, int m, int k, const v
                               hipStream_t s, RowsIn *views = nullptr);
 // y of every matrix of p from its split-K partial sums (slice order).
 hipError_t launch_mb_reduce(const MbArgs &p, hipStream_t s);
+// One matrix of n rows (an lm_head): y[m][n] from the staged activations,
+// the whole row per workgroup where K allows; part holds
+// mb_head_part_bytes(n, k) bytes (0 for k of 2 or 10 super-blocks).
+size_t mb_head_part_bytes(int n, int k);
+hipError_t launch_q4k_gemv_mb_head(const uint8_t *w, float *y, int n, int m, int k, const void *stage, float *part,
+                                   hipStream_t s);
 
 // The same batched GEMV for Q8_0 and Q6_K weights (planar layout, from the
 // staged digits) and BF16 weights (from the f32 rows x[m][k] themselves),

@@ -213,6 +213,16 @@ def load_linear_from_gguf(gguf: GgufFile, idx: int, keep_packed: bool = False) -
     return Linear(raw)
 
 
+def q4k_quantize_bf16(m: np.ndarray) -> np.ndarray:
+    """Q4KMat::quantize_from_bf16 (autograd2.rs:1252-1289): bf16 bits
+    [rows, cols] -> Q4_K blocks, row by row."""
+    m = np.ascontiguousarray(m, np.uint16)
+    rows, cols = m.shape
+    out = np.zeros(max(1, rows * (cols // 256) * 144), np.uint8)
+    check(lib().rt_q4k_quantize_bf16(m.ctypes.data, rows, cols, out.ctypes.data))
+    return out[: rows * (cols // 256) * 144]
+
+
 def q4k_quantize(m: np.ndarray) -> np.ndarray:
     """Q4KMat::quantize (autograd2.rs:1138-1168): f32 [rows, cols] -> Q4_K blocks."""
     m = np.ascontiguousarray(m, np.float32)

@@ -284,6 +284,19 @@ def test_quantize_matches_oracle(rt, orc):
         rt.q4k_quantize(np.zeros((2, 100), np.float32))
 
 
+def test_quantize_bf16_matches_oracle_on_widened_rows(rt, orc):
+    """quantize_from_bf16 (the q4k-lm-head requantisation): the blocks of
+    the f32-widened rows, as the oracle's quantiser makes them, on an
+    embedding-like bf16 matrix with a zero row and a row of one value."""
+    w = orc.synth_bf16(31, 37 * 512).reshape(37, 512)
+    w[5] = 0
+    w[9] = 0x3F80  # 1.0
+    widened = (w.astype(np.uint32) << 16).view(np.float32)
+    assert np.array_equal(rt.q4k_quantize_bf16(w), orc.q4k_quantize(widened))
+    with pytest.raises(rt.RtError):
+        rt.q4k_quantize_bf16(np.zeros((2, 100), np.uint16))
+
+
 def test_requant_path_matches_oracle_on_cpu(rt, orc, tmp_path):
     """The library's decode + quantise of a Q4_0 tensor equals the oracle's
     Q4_0 -> Q4_K requantisation (the device upload itself is a GPU test)."""

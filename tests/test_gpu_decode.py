@@ -593,6 +593,110 @@ def test_gemma3_1b_shape_refuses_q4k_at_hidden_width(rt, orc):
     d.close()
 
 
+# ---------------------------------------------------------------------------
+# An lm_head apart from the embedding (metal_decode.rs:1079-1107): Q4_K (the
+# model's own or the BF16 one requantised, feature q4k-lm-head) or untied BF16
+# ---------------------------------------------------------------------------
+def lm_head_ref(orc, cfg, fmt, w, hidden, fnorm):
+    """Logits of the final-normed hidden state (final_norm, transformer4.rs:
+    2370-2380, in float64) through the head: Q4_K dot_row in float64
+    (orc_q4k_gemv_f64) or the BF16 GEMV in float64."""
+    h = hidden.astype(np.float64)
+    xn = h / np.sqrt(np.mean(h * h) + cfg["eps"]) * (1.0 + fnorm.astype(np.float64))
+    if fmt == 1:
+        return orc.q4k_gemv_f64(w, cfg["vocab"], cfg["hidden"], xn.astype(np.float32))
+    W = (w.astype(np.uint32) << 16).view(np.float32).reshape(cfg["vocab"], cfg["hidden"])
+    return W.astype(np.float64) @ xn
+
+
+def check_head(rt, orc, cfg, fmt, head, d, layers, embed, fnorm, ctx, m):
+    """Steps at ctx, ctx+1 and a verify batch of m at ctx+2 through the head,
+    against the oracle's hidden state times the head."""
+    import copy
+    olayers = copy.deepcopy(layers)
+    for i, t in enumerate([7, 9]):
+        got = d.decode_step(t, ctx + i)
+        _, hid = orc.gemma3_decode_step(cfg, olayers, embed, fnorm, token=t, pos=ctx + i, want_hidden=True)
+        ref = lm_head_ref(orc, cfg, fmt, head, hid, fnorm)
+        assert rel_l2(got, ref) < LOGITS_TOL, (i, rel_l2(got, ref))
+        assert int(np.argmax(got)) == int(np.argmax(ref))
+    toks = [(37 * i + 5) % cfg["vocab"] for i in range(m)]
+    got = d.decode_step_batch(toks, ctx + 2)
+    for i, t in enumerate(toks):
+        _, hid = orc.gemma3_decode_step(cfg, olayers, embed, fnorm, token=t, pos=ctx + 2 + i, want_hidden=True)
+        ref = lm_head_ref(orc, cfg, fmt, head, hid, fnorm)
+        assert rel_l2(got[i], ref) < LOGITS_TOL, (i, rel_l2(got[i], ref))
+        assert int(np.argmax(got[i])) == int(np.argmax(ref))
+
+
+@pytest.mark.parametrize("fmt", [1, 2])
+def test_lm_head_apart_from_embedding(rt, orc, fmt):
+    """A Q4_K lm_head (the embedding requantised by quantize_from_bf16, as
+    the q4k-lm-head feature does) or an untied BF16 one: two decode steps, a
+    verify batch of 3 and a prefill's last row against the oracle's final
+    hidden state times the head; w = None restores the tied logits bit for
+    bit."""
+    from test_prefill import fresh_caches
+    cfg = tiny(2)
+    max_seq, ctx = 40, 6
+    H, V = cfg["hidden"], cfg["vocab"]
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=ctx, seed=2100 + fmt)
+    head = rt.q4k_quantize_bf16(embed.reshape(V, H)) if fmt == 1 else orc.synth_bf16(2200, V * H)
+    d = build_ctx(rt, cfg, layers, embed, fnorm, ctx, max_seq)
+    tied = d.decode_step(7, ctx)
+    d.set_lm_head(fmt, head)
+    check_head(rt, orc, cfg, fmt, head, d, layers, embed, fnorm, ctx, 3)
+    d.set_lm_head(0, None)
+    assert np.array_equal(d.decode_step(7, ctx), tied)
+    d.close()
+    # prefill (12 rows: the GEMM path) and its last row's logits
+    d = build_ctx(rt, cfg, layers, embed, fnorm, 0, max_seq)
+    d.set_lm_head(fmt, head)
+    toks = [(13 * i + 2) % V for i in range(12)]
+    got = d.prefill(toks, 0, 1)
+    olayers = fresh_caches(layers)
+    for i, t in enumerate(toks):
+        _, hid = orc.gemma3_decode_step(cfg, olayers, embed, fnorm, token=t, pos=i, want_hidden=True)
+    ref = lm_head_ref(orc, cfg, fmt, head, hid, fnorm)
+    assert rel_l2(got, ref) < LOGITS_TOL, rel_l2(got, ref)
+    d.close()
+
+
+def test_gemma3_4b_shape_q4k_lm_head(rt, orc):
+    """The Q4_K lm_head at Gemma-3-4B widths (K = 2560: the single-token
+    GEMV and the one-slice batched GEMV over the vocabulary rows), 2 layers,
+    vocab 4096: steps and a verify batch of 8 against the oracle; a head
+    bound by device pointer gives the same logits."""
+    import torch
+    cfg = dict(rt.GEMMA3_4B, n_layers=2, global_every=2, vocab=4096)
+    H, V = cfg["hidden"], cfg["vocab"]
+    max_seq, ctx = 64, 40
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=ctx, seed=2300)
+    head = rt.q4k_quantize_bf16(embed.reshape(V, H))
+    d = build_ctx(rt, cfg, layers, embed, fnorm, ctx, max_seq)
+    d.set_lm_head(1, head)
+    check_head(rt, orc, cfg, 1, head, d, layers, embed, fnorm, ctx, 8)
+    first = d.decode_step(7, ctx)
+    d.set_lm_head(1, torch.from_numpy(head).to("cuda:0"))
+    assert np.array_equal(d.decode_step(7, ctx), first)
+    d.close()
+
+
+def test_lm_head_rejects_bad_calls(rt, orc):
+    import ctypes as C
+    cfg = gemma3_1b_cfg(n_layers=1, global_every=0)  # hidden 1152: no Q4_K head
+    layers, dev_layers, fmts, embed, fnorm = gemma3_1b_model(rt, orc, cfg, 8, 0, seed=2400)
+    d = gemma3_1b_ctx(rt, cfg, layers, dev_layers, fmts, embed, fnorm, 0, 8)
+    first = d.decode_step(3, 0)
+    L = rt.lib()
+    blocks = (C.c_uint8 * 144)()
+    assert L.rt_decode_set_lm_head(d._h, rt.LINEAR_Q4K, C.addressof(blocks), 0) == rt.RT_EINVAL
+    assert "unsupported" in L.rt_last_error().decode()
+    assert L.rt_decode_set_lm_head(d._h, 3, C.addressof(blocks), 0) == rt.RT_EINVAL  # F32
+    assert np.array_equal(d.decode_step(3, 0), first)  # the tied head serves on
+    d.close()
+
+
 def test_memory_report(rt, orc):
     """rt_decode_memory (print_metal_memory, metal_decode.rs:1285-1354): the
     weights and KV cache of a context add up to what its shapes hold, for
