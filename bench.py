@@ -140,6 +140,8 @@ def main() -> int:
     ap.add_argument("--launch-probe", action="store_true",
                     help="only measure the launch floor inside a graph: empty dependent launches, and streaming "
                          "reads of 4-118 MB fitted to a fixed cost per launch plus a rate")
+    ap.add_argument("--q4k-lm-head", action="store_true",
+                    help="with --decode-profile: a Q4_K lm_head (random blocks) instead of the BF16 tied one")
     ap.add_argument("--verify-rows", type=int, default=0,
                     help="with --decode-profile: run decode_step_batch calls of this many rows (1..8) instead "
                          "of single-token steps")
@@ -212,6 +214,9 @@ def main() -> int:
         torch.cuda.synchronize()
         del a, b
         d, pos = build_decode(rt, torch, dev, gen, layers, embed, final_norm, args)
+        if args.q4k_lm_head:
+            head = synth_q4k(torch, V, H, gen)
+            d.set_lm_head(1, head)
         bm = args.verify_rows
 
         def one(pos):
@@ -230,7 +235,7 @@ def main() -> int:
         d.synchronize()
         dt = (time.perf_counter() - t1) / args.steps
         print(json.dumps({"decode_profile": "done", "steps": args.steps, "verify_rows": bm,
-                          "ms_per_call": round(dt * 1e3, 4)}))
+                          "q4k_lm_head": args.q4k_lm_head, "ms_per_call": round(dt * 1e3, 4)}))
         d.close()
         return 0
     x_h = torch.randn(H, device=dev, generator=gen)
