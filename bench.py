@@ -140,6 +140,8 @@ def main() -> int:
     ap.add_argument("--launch-probe", action="store_true",
                     help="only measure the launch floor inside a graph: empty dependent launches, and streaming "
                          "reads of 4-118 MB fitted to a fixed cost per launch plus a rate")
+    ap.add_argument("--q4-k-m", action="store_true",
+                    help="with --decode-profile: the Q4_K_M layout (v and down in Q6_K)")
     ap.add_argument("--q4k-lm-head", action="store_true",
                     help="with --decode-profile: a Q4_K lm_head (random blocks) instead of the BF16 tied one")
     ap.add_argument("--verify-rows", type=int, default=0,
@@ -213,7 +215,11 @@ def main() -> int:
         b.copy_(a)  # counter calibration: reads and writes exactly 256 MiB
         torch.cuda.synchronize()
         del a, b
-        d, pos = build_decode(rt, torch, dev, gen, layers, embed, final_norm, args)
+        if args.q4_k_m:
+            layers = [dict(w, v=synth_q6k_planar(torch, KVD, H, gen), down=synth_q6k_planar(torch, H, F, gen))
+                      for w in layers]
+        d, pos = build_decode(rt, torch, dev, gen, layers, embed, final_norm, args,
+                              formats=[1, 1, 4, 1, 1, 1, 4] if args.q4_k_m else None)
         if args.q4k_lm_head:
             head = synth_q4k(torch, V, H, gen)
             d.set_lm_head(1, head)
@@ -235,7 +241,8 @@ def main() -> int:
         d.synchronize()
         dt = (time.perf_counter() - t1) / args.steps
         print(json.dumps({"decode_profile": "done", "steps": args.steps, "verify_rows": bm,
-                          "q4k_lm_head": args.q4k_lm_head, "ms_per_call": round(dt * 1e3, 4)}))
+                          "q4k_lm_head": args.q4k_lm_head, "q4_k_m": args.q4_k_m,
+                          "ms_per_call": round(dt * 1e3, 4)}))
         d.close()
         return 0
     x_h = torch.randn(H, device=dev, generator=gen)
@@ -698,13 +705,16 @@ def launch_probe(rt, torch, dev) -> dict:
     return out
 
 
-def build_decode(rt, torch, dev, gen, layers, embed, final_norm, args, ctx: int = 4096):
+def build_decode(rt, torch, dev, gen, layers, embed, final_norm, args, ctx: int = 4096, formats=None):
     """The config-3 decode context: the 34 synthetic layers, N(0,1) K/V rows
     0..ctx-1 in every layer, the BF16 tied embedding; returns it and the
     first position to decode (ctx)."""
     d = rt.HipDecodeContext(dict(rt.GEMMA3_4B), ctx + 8 * (args.warmup + args.steps) + 8 * (2 + max(2, args.steps // 4)) + 8)
     for li, w in enumerate(layers):
-        d.set_layer(li, w)
+        if formats:
+            d.set_layer(li, w, formats=formats)
+        else:
+            d.set_layer(li, w)
         kv = torch.randn(2, ctx, KVD, device=dev, generator=gen)
         d.sync_kv_from_cpu(li, kv[0], kv[1], ctx)
         del kv

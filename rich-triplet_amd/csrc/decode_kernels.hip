@@ -23,6 +23,7 @@
 #include "gemma3_math.hpp"
 #include "q4k_gemv.hpp"
 #include "q4k_gemv_mb.hpp"
+#include "kquant_tile.hpp"
 #include "rt_device.hpp"
 #include "rt_kernels.hpp"
 
@@ -105,10 +106,14 @@ RT_DEV void pro_finish(const DecodeArgs &a, ProRegs<K, T> &r, float *__restrict_
 
 // ---------------------------------------------------------------------------
 // k_qkv: [prologue] + GEMV over q|k|v rows (each workgroup inside one matrix).
+// V6: v is Q6_K (planar), as in Q4_K_M files; its workgroups run the Q6_K
+// tile on the same staged input, so the layer keeps one launch for q|k|v.
 // ---------------------------------------------------------------------------
-template <int NB, int T, int ITERS, Pro MODE>
+template <int NB, int T, int ITERS, Pro MODE, bool V6 = false>
 __global__ __launch_bounds__(T) void k_qkv(DecodeArgs a, LayerArgs L, LayerArgs prev) {
   using Tile = Q4KTile<NB, T, ITERS>;
+  using Tile6 = Q6KTile<NB, T, ITERS>;
+  static_assert(Tile6::ROWS == Tile::ROWS, "both tiles cover the same rows per workgroup");
   constexpr int K = NB * 256;
   __shared__ __attribute__((aligned(16))) uint32_t dl[NB * 4 * kDPitch];
   __shared__ float red[Tile::ROWS * NB];
@@ -125,6 +130,7 @@ __global__ __launch_bounds__(T) void k_qkv(DecodeArgs a, LayerArgs L, LayerArgs 
   } else {
     W = L.wv, y = a.v, r0 = row0 - qd - kvd;
   }
+  const bool six = V6 && row0 >= qd + kvd;  // workgroup-uniform
   const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
   ProRegs<K, T> pr;
   pro_load<K, T, MODE>(a, a.x2, a.dn, prev.g_post_ffn, L.g_in, pr);
@@ -132,12 +138,20 @@ __global__ __launch_bounds__(T) void k_qkv(DecodeArgs a, LayerArgs L, LayerArgs 
   // workgroup: they return ahead of the weight stream
   __syncthreads();
   Tile tile;
-  tile.load([&](int rl) -> const uint8_t * { return W + (size_t)(r0 + rl) * row_bytes; }, W);
+  Tile6 tile6;
+  if (six)
+    tile6.load(q6k_planes(L.wv, (size_t)kvd * NB), r0, kvd);
+  else
+    tile.load([&](int rl) -> const uint8_t * { return W + (size_t)(r0 + rl) * row_bytes; }, W);
   pro_finish<K, T, MODE, true>(a, pr, a.hid, dl, bred, a.xn);
   __syncthreads();
-  ChunkD cx;
-  chunkd_from_lds(dl, tile.slot, cx);
-  tile.compute_digits(cx, red);
+  if (six) {
+    tile6.compute(dl, red);
+  } else {
+    ChunkD cx;
+    chunkd_from_lds(dl, tile.slot, cx);
+    tile.compute_digits(cx, red);
+  }
   __syncthreads();
   for (int i = threadIdx.x; i < Tile::ROWS; i += T) y[r0 + i] = reduce_row<NB>(red, i);
 }
@@ -670,13 +684,19 @@ struct Launch {
 
 template <int NB, int T, int ITERS>
 static void launch_qkv(Launch &l, const DecodeArgs &a, const LayerArgs &L, const LayerArgs &prev, bool first,
-                       int rows_total) {
+                       int rows_total, bool v6 = false) {
   constexpr int ROWS = Q4KTile<NB, T, ITERS>::ROWS;
   const dim3 grid(rows_total / ROWS);
-  if (first)
+  if (v6) {
+    if (first)
+      hipLaunchKernelGGL((k_qkv<NB, T, ITERS, Pro::Embed, true>), grid, dim3(T), 0, l.s, a, L, prev);
+    else
+      hipLaunchKernelGGL((k_qkv<NB, T, ITERS, Pro::Resid, true>), grid, dim3(T), 0, l.s, a, L, prev);
+  } else if (first) {
     hipLaunchKernelGGL((k_qkv<NB, T, ITERS, Pro::Embed>), grid, dim3(T), 0, l.s, a, L, prev);
-  else
+  } else {
     hipLaunchKernelGGL((k_qkv<NB, T, ITERS, Pro::Resid>), grid, dim3(T), 0, l.s, a, L, prev);
+  }
   l.check();
 }
 
@@ -764,11 +784,13 @@ static hipError_t enqueue_layers(const DecodeShape &s, const DecodeArgs &a, cons
     const LayerArgs &P = layers[li > 0 ? li - 1 : 0];
     auto q4 = [&](int p) { return L.fmt[p] == RT_LINEAR_Q4K; };
     if (q4(kProjQ) && q4(kProjK)) {
-      // fused prologue + GEMV over q|k(|v) rows; it also leaves xn for a split v
-      const int qkv_rows = qd + kvd + (q4(kProjV) ? kvd : 0);
-      if (big) launch_qkv<10, 640, 1>(l, a, L, P, li == 0, qkv_rows);
-      else launch_qkv<2, 256, 1>(l, a, L, P, li == 0, qkv_rows);
-      if (!q4(kProjV)) launch_proj(l, L.fmt[kProjV], L.wv, a.xn, a.v, kvd, s.hidden);
+      // fused prologue + GEMV over q|k|v rows (v in Q4_K or Q6_K); it also
+      // leaves xn for a v of another format
+      const bool v6 = L.fmt[kProjV] == RT_LINEAR_Q6K;
+      const int qkv_rows = qd + kvd + (q4(kProjV) || v6 ? kvd : 0);
+      if (big) launch_qkv<10, 640, 1>(l, a, L, P, li == 0, qkv_rows, v6);
+      else launch_qkv<2, 256, 1>(l, a, L, P, li == 0, qkv_rows, v6);
+      if (!q4(kProjV) && !v6) launch_proj(l, L.fmt[kProjV], L.wv, a.xn, a.v, kvd, s.hidden);
     } else {
       if (li == 0) launch_prologue<Pro::Embed>(l, s, a, nullptr, nullptr, nullptr, L.g_in, a.hid);
       else launch_prologue<Pro::Resid>(l, s, a, a.x2, a.dn, P.g_post_ffn, L.g_in, a.hid);
