@@ -682,6 +682,21 @@ def test_gemma3_4b_shape_q4k_lm_head(rt, orc):
     d.close()
 
 
+def test_generic_shape_q4k_lm_head(rt, orc):
+    """A Q4_K lm_head at hidden 768 (three super-blocks per row: the batched
+    head splits K and adds the partials; the rows path serves even the
+    single token): steps and a verify batch of 5 against the oracle."""
+    cfg = generic_cfg()
+    H, V = cfg["hidden"], cfg["vocab"]
+    max_seq, ctx = 32, 6
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=ctx, seed=2500)
+    head = rt.q4k_quantize_bf16(embed.reshape(V, H))
+    d = build_ctx(rt, cfg, layers, embed, fnorm, ctx, max_seq)
+    d.set_lm_head(1, head)
+    check_head(rt, orc, cfg, 1, head, d, layers, embed, fnorm, ctx, 5)
+    d.close()
+
+
 def test_lm_head_rejects_bad_calls(rt, orc):
     import ctypes as C
     cfg = gemma3_1b_cfg(n_layers=1, global_every=0)  # hidden 1152: no Q4_K head
