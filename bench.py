@@ -142,6 +142,8 @@ def main() -> int:
                          "reads of 4-118 MB fitted to a fixed cost per launch plus a rate")
     ap.add_argument("--q4-k-m", action="store_true",
                     help="with --decode-profile: the Q4_K_M layout (v and down in Q6_K)")
+    ap.add_argument("--q8-0", action="store_true",
+                    help="with --decode-profile: every projection in Q8_0 (planar)")
     ap.add_argument("--q4k-lm-head", action="store_true",
                     help="with --decode-profile: a Q4_K lm_head (random blocks) instead of the BF16 tied one")
     ap.add_argument("--verify-rows", type=int, default=0,
@@ -215,11 +217,16 @@ def main() -> int:
         b.copy_(a)  # counter calibration: reads and writes exactly 256 MiB
         torch.cuda.synchronize()
         del a, b
+        fmts = None
         if args.q4_k_m:
             layers = [dict(w, v=synth_q6k_planar(torch, KVD, H, gen), down=synth_q6k_planar(torch, H, F, gen))
                       for w in layers]
-        d, pos = build_decode(rt, torch, dev, gen, layers, embed, final_norm, args,
-                              formats=[1, 1, 4, 1, 1, 1, 4] if args.q4_k_m else None)
+            fmts = [1, 1, 4, 1, 1, 1, 4]
+        elif args.q8_0:
+            layers = [dict(w, **{name: synth_q8_0_planar(torch, n, k, gen) for name, n, k in Q4K_SHAPES})
+                      for w in layers]
+            fmts = [5] * 7
+        d, pos = build_decode(rt, torch, dev, gen, layers, embed, final_norm, args, formats=fmts)
         if args.q4k_lm_head:
             head = synth_q4k(torch, V, H, gen)
             d.set_lm_head(1, head)
@@ -241,7 +248,7 @@ def main() -> int:
         d.synchronize()
         dt = (time.perf_counter() - t1) / args.steps
         print(json.dumps({"decode_profile": "done", "steps": args.steps, "verify_rows": bm,
-                          "q4k_lm_head": args.q4k_lm_head, "q4_k_m": args.q4_k_m,
+                          "q4k_lm_head": args.q4k_lm_head, "q4_k_m": args.q4_k_m, "q8_0": args.q8_0,
                           "ms_per_call": round(dt * 1e3, 4)}))
         d.close()
         return 0
@@ -759,6 +766,16 @@ def q4k_lm_head_decode(rt, torch, gen, d, ctx: int, dec_bytes: int, args) -> dic
            "verify_m": bm, "verify_ms_per_call": round(dtb * 1e3, 4), "verify_tok_per_s": round(bm / dtb, 1)}
     log(f"Q4_K lm_head: decode step {dt * 1e3:.3f} ms -> {1 / dt:.1f} tok/s; verify M={bm} {dtb * 1e3:.3f} ms")
     return out
+
+
+def synth_q8_0_planar(torch, n: int, k: int, gen) -> "torch.Tensor":
+    """Random planar Q8_0 (rt_q8_0_repack layout: int8 q [n][k] | f16 d [n*k/32]),
+    d = f16 of |N(0, 0.02)|."""
+    nq = n * k
+    w = torch.randint(0, 256, (nq + nq // 32 * 2,), dtype=torch.uint8, device="cuda", generator=gen)
+    d = (torch.randn(nq // 32, device="cuda", generator=gen).abs() * 0.02).half()
+    w[nq:] = d.view(torch.uint8)
+    return w
 
 
 def synth_q6k_planar(torch, n: int, k: int, gen) -> "torch.Tensor":

@@ -246,6 +246,73 @@ __global__ __launch_bounds__(T) void k_gateup(DecodeArgs a, LayerArgs L) {
 }
 
 // ---------------------------------------------------------------------------
+// The same two launches for a layer whose q, k, v (k_qkv8) or gate, up
+// (k_gateup8) are Q8_0 (planar: codes [n][K] | f16 scales [n][K/32]), as in
+// Q8_0 files: the prologue and the staged digits as above, then Q8Tile
+// (kquant_tile.hpp) rows, 16 per workgroup at K = 2560 like the Q4_K tiles.
+// ---------------------------------------------------------------------------
+template <int NB32, int T, int ITERS, Pro MODE>
+__global__ __launch_bounds__(T) void k_qkv8(DecodeArgs a, LayerArgs L, LayerArgs prev) {
+  using Tile = Q8Tile<NB32, T, ITERS>;
+  constexpr int K = NB32 * 32;
+  __shared__ __attribute__((aligned(16))) uint32_t dl[K / 64 * kDPitch];
+  __shared__ float red[Tile::ROWS * Tile::RED];
+  __shared__ float bred[T / 64];
+  const int qd = a.n_q_heads * a.head_dim, kvd = a.n_kv_heads * a.head_dim;
+  const int row0 = (int)blockIdx.x * Tile::ROWS;  // ROWS divides qd and kvd (checked on the host)
+  const uint8_t *W;
+  float *y;
+  int r0, nrows;
+  if (row0 < qd) {
+    W = L.wq, y = a.q, r0 = row0, nrows = qd;
+  } else if (row0 < qd + kvd) {
+    W = L.wk, y = a.k, r0 = row0 - qd, nrows = kvd;
+  } else {
+    W = L.wv, y = a.v, r0 = row0 - qd - kvd, nrows = kvd;
+  }
+  const uint16_t *D = reinterpret_cast<const uint16_t *>(W + (size_t)nrows * K);
+  ProRegs<K, T> pr;
+  pro_load<K, T, MODE>(a, a.x2, a.dn, prev.g_post_ffn, L.g_in, pr);
+  __syncthreads();
+  Tile tile;
+  tile.load([&](int rl) { return W + (size_t)(r0 + rl) * K; }, [&](int rl) { return D + (size_t)(r0 + rl) * NB32; });
+  pro_finish<K, T, MODE, true>(a, pr, a.hid, dl, bred, a.xn);
+  __syncthreads();
+  tile.compute(dl, red);
+  __syncthreads();
+  for (int i = threadIdx.x; i < Tile::ROWS; i += T) y[r0 + i] = Tile::reduce(red, i);
+}
+
+template <int NB32, int T, int GR>
+__global__ __launch_bounds__(T) void k_gateup8(DecodeArgs a, LayerArgs L, int ffn) {
+  constexpr int RPI = T / NB32;
+  using Tile = Q8Tile<NB32, T, (2 * GR + RPI - 1) / RPI>;
+  constexpr int K = NB32 * 32;
+  __shared__ __attribute__((aligned(16))) uint32_t dl[K / 64 * kDPitch];
+  __shared__ float red[Tile::ROWS * Tile::RED];
+  __shared__ float bred[T / 64];
+  const int j0 = (int)blockIdx.x * GR;  // GR divides ffn (checked on the host)
+  const uint16_t *Dg = reinterpret_cast<const uint16_t *>(L.wgate + (size_t)ffn * K);
+  const uint16_t *Du = reinterpret_cast<const uint16_t *>(L.wup + (size_t)ffn * K);
+  ProRegs<K, T> pr;
+  pro_load<K, T, Pro::Resid>(a, a.hid, a.o, L.g_post_attn, L.g_pre_ffn, pr);
+  Tile tile;
+  // tile rows [0, GR) are gate rows j0.., [GR, 2GR) the same up rows; slots
+  // past 2GR re-read the last up row and are never stored
+  tile.load([&](int rl) {
+    return rl < GR ? L.wgate + (size_t)(j0 + rl) * K : L.wup + (size_t)(j0 + min(rl - GR, GR - 1)) * K;
+  }, [&](int rl) {
+    return rl < GR ? Dg + (size_t)(j0 + rl) * NB32 : Du + (size_t)(j0 + min(rl - GR, GR - 1)) * NB32;
+  });
+  pro_finish<K, T, Pro::Resid, true>(a, pr, a.x2, dl, bred);
+  __syncthreads();
+  tile.compute(dl, red);
+  __syncthreads();
+  for (int i = threadIdx.x; i < GR; i += T)
+    a.h[j0 + i] = mul_nc(gelu_tanh(Tile::reduce(red, i)), Tile::reduce(red, GR + i));
+}
+
+// ---------------------------------------------------------------------------
 // k_gemv: plain GEMV with the activation vector read from global memory.
 // ---------------------------------------------------------------------------
 template <int NB, int T, int ITERS>
@@ -700,6 +767,24 @@ static void launch_qkv(Launch &l, const DecodeArgs &a, const LayerArgs &L, const
   l.check();
 }
 
+template <int NB32, int T, int ITERS>
+static void launch_qkv8(Launch &l, const DecodeArgs &a, const LayerArgs &L, const LayerArgs &prev, bool first,
+                        int rows_total) {
+  constexpr int ROWS = Q8Tile<NB32, T, ITERS>::ROWS;
+  const dim3 grid(rows_total / ROWS);
+  if (first)
+    hipLaunchKernelGGL((k_qkv8<NB32, T, ITERS, Pro::Embed>), grid, dim3(T), 0, l.s, a, L, prev);
+  else
+    hipLaunchKernelGGL((k_qkv8<NB32, T, ITERS, Pro::Resid>), grid, dim3(T), 0, l.s, a, L, prev);
+  l.check();
+}
+
+template <int NB32, int T, int GR>
+static void launch_gateup8(Launch &l, const DecodeArgs &a, const LayerArgs &L, int ffn) {
+  hipLaunchKernelGGL((k_gateup8<NB32, T, GR>), dim3(ffn / GR), dim3(T), 0, l.s, a, L, ffn);
+  l.check();
+}
+
 template <int NB, int T, int GR>
 static void launch_gateup(Launch &l, const DecodeArgs &a, const LayerArgs &L, int ffn) {
   hipLaunchKernelGGL((k_gateup<NB, T, GR>), dim3(ffn / GR), dim3(T), 0, l.s, a, L);
@@ -783,6 +868,7 @@ static hipError_t enqueue_layers(const DecodeShape &s, const DecodeArgs &a, cons
     const LayerArgs &L = layers[li];
     const LayerArgs &P = layers[li > 0 ? li - 1 : 0];
     auto q4 = [&](int p) { return L.fmt[p] == RT_LINEAR_Q4K; };
+    auto q8 = [&](int p) { return L.fmt[p] == RT_LINEAR_Q8_0; };
     if (q4(kProjQ) && q4(kProjK)) {
       // fused prologue + GEMV over q|k|v rows (v in Q4_K or Q6_K); it also
       // leaves xn for a v of another format
@@ -791,6 +877,9 @@ static hipError_t enqueue_layers(const DecodeShape &s, const DecodeArgs &a, cons
       if (big) launch_qkv<10, 640, 1>(l, a, L, P, li == 0, qkv_rows, v6);
       else launch_qkv<2, 256, 1>(l, a, L, P, li == 0, qkv_rows, v6);
       if (!q4(kProjV) && !v6) launch_proj(l, L.fmt[kProjV], L.wv, a.xn, a.v, kvd, s.hidden);
+    } else if (q8(kProjQ) && q8(kProjK) && q8(kProjV)) {
+      if (big) launch_qkv8<80, 640, 2>(l, a, L, P, li == 0, qd + 2 * kvd);
+      else launch_qkv8<16, 256, 2>(l, a, L, P, li == 0, qd + 2 * kvd);
     } else {
       if (li == 0) launch_prologue<Pro::Embed>(l, s, a, nullptr, nullptr, nullptr, L.g_in, a.hid);
       else launch_prologue<Pro::Resid>(l, s, a, a.x2, a.dn, P.g_post_ffn, L.g_in, a.hid);
@@ -810,6 +899,9 @@ static hipError_t enqueue_layers(const DecodeShape &s, const DecodeArgs &a, cons
       // 20 gate + 20 up rows per workgroup: 512 workgroups, all resident at once
       if (big) launch_gateup<10, 640, kGateRowsBig>(l, a, L, s.ffn);
       else launch_gateup<2, 256, kGateRowsSmall>(l, a, L, s.ffn);
+    } else if (q8(kProjGate) && q8(kProjUp)) {
+      if (big) launch_gateup8<80, 640, kGateRowsBig>(l, a, L, s.ffn);
+      else launch_gateup8<16, 256, kGateRowsSmall>(l, a, L, s.ffn);
     } else {
       launch_prologue<Pro::Resid>(l, s, a, a.hid, a.o, L.g_post_attn, L.g_pre_ffn, a.x2);
       launch_proj(l, L.fmt[kProjGate], L.wgate, a.xn, a.h, s.ffn, s.hidden);
@@ -923,6 +1015,10 @@ bool decode_shape_generic(const DecodeShape &s, const char **why) {
 }
 
 // Row-count divisibility the launches above rely on.
+static_assert(Q8Tile<80, 640, 2>::ROWS == Q4KTile<10, 640, 1>::ROWS &&
+                  Q8Tile<16, 256, 2>::ROWS == Q4KTile<2, 256, 1>::ROWS,
+              "the Q8_0 q|k|v tiles cover the Q4_K tiles' rows, so one divisibility check serves both");
+
 bool decode_rows_divisible(const DecodeShape &s, const char **why) {
   const int qd = s.n_q_heads * s.head_dim, kvd = s.n_kv_heads * s.head_dim;
   const bool big = s.hidden == 2560;

@@ -1,7 +1,8 @@
-// kquant_tile.hpp -- the Q6_K GEMV tile on staged activation digits, shared
-// by the stand-alone Q6_K GEMV (kquant.hip) and the decode step's q|k|v
-// launch (decode_kernels.hip), which runs a Q6_K v projection beside its
-// Q4_K q and k rows on the same staged input.
+// kquant_tile.hpp -- the Q6_K and Q8_0 GEMV tiles on staged activation
+// digits, shared by the stand-alone GEMVs (kquant.hip) and the decode step's
+// fused launches (decode_kernels.hip): a Q6_K v projection beside Q4_K q and
+// k rows, and the q|k|v and gate|up sets of a Q8_0 model, each on the input
+// its own prologue normalises and stages.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -103,6 +104,78 @@ struct Q6KTile {
       p = quad_sum(p);
       if ((s & 3) == 0) red[(it * RPI + rsub()) * NB + b] = p;
     }
+  }
+};
+
+// Q8_0 tile on staged digits.  Slot s = threadIdx % S (S = NB32, the
+// 32-element blocks of a row) owns block s of RPI = T/S rows per iteration:
+// its 32 code bytes (two 16-byte loads) and its f16 scale.  q is signed; with
+// q' = q ^ 0x80 = q + 128 unsigned, sum x0 q = sum x0 q' - 128 sum x0, so both
+// digits run on v_dot4 forms of matching signedness.  Per (row, 64-element
+// chunk) the pair of block sums goes to red[row * RED + chunk].
+template <int NB32, int T, int ITERS>
+struct Q8Tile {
+  static constexpr int S = NB32, RPI = T / S, ROWS = RPI * ITERS, RED = (NB32 + 1) / 2;
+  static_assert(T % S == 0 && T % 64 == 0 && S % 2 == 0, "a tile covers whole rows and whole waves");
+  uint4 qa[ITERS], qb[ITERS];
+  uint32_t dd[ITERS];
+
+  RT_DEV static int slot() { return (int)threadIdx.x % S; }
+  RT_DEV static int rsub() { return (int)threadIdx.x / S; }
+
+  // rowq(rl) / rowd(rl): the code bytes and the f16 scales of tile row rl.
+  template <typename RowQ, typename RowD>
+  RT_DEV void load(RowQ rowq, RowD rowd) {
+    const int s = slot();
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      const int rl = it * RPI + rsub();
+      const uint8_t *p = rowq(rl) + 32 * s;
+      qa[it] = *reinterpret_cast<const uint4 *>(p);
+      qb[it] = *reinterpret_cast<const uint4 *>(p + 16);
+      dd[it] = rowd(rl)[s];
+    }
+  }
+
+  RT_DEV void compute(const uint32_t *dl, float *red) const {
+    const int s = slot();
+    uint32_t x0[8];
+    int x1[8];
+    const uint32_t *px = dl + (s >> 1) * kDPitch + 8 * (s & 1);
+    uint32_t sx0 = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      x0[k] = px[k];
+      x1[k] = (int)px[16 + k];
+      sx0 = __builtin_amdgcn_udot4(x0[k], 0x01010101u, sx0, false);
+    }
+    const int corr = 128 * (int)sx0;
+    const float delta = __uint_as_float(dl[(s >> 1) * kDPitch + 32]);
+    const uint32_t flip = opaque_u32(0x80808080u);
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      const uint32_t w[8] = {qa[it].x, qa[it].y, qa[it].z, qa[it].w, qb[it].x, qb[it].y, qb[it].z, qb[it].w};
+      uint32_t s0 = 0;
+      int s1 = 0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        s0 = __builtin_amdgcn_udot4(w[k] ^ flip, x0[k], s0, false);
+        s1 = __builtin_amdgcn_sdot4((int)w[k], x1[k], s1, false);
+      }
+      // sum X q = (sum x0 q' - 128 sum x0) + 256 sum x1 q; |.| < 2^31
+      const int t = (int)(s0 - (uint32_t)corr) + 256 * s1;
+      float p = half_bits_to_f32(dd[it]) * delta * (float)t;
+      p += dpp<0xB1>(p);  // pair of blocks = one 64-element chunk
+      if ((s & 1) == 0) red[(it * RPI + rsub()) * RED + (s >> 1)] = p;
+    }
+  }
+
+  // y of tile row rl from its chunk sums (chunk order)
+  RT_DEV static float reduce(const float *red, int rl) {
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < RED; ++c) acc += red[rl * RED + c];
+    return acc;
   }
 };
 

@@ -351,6 +351,39 @@ def test_q4_k_m_layout_verify_batch_at_gemma3_4b_shape(rt, orc, m):
 # ---------------------------------------------------------------------------
 # prefill with per-projection formats
 # ---------------------------------------------------------------------------
+ALL_Q8_0 = {p: 5 for p in ("q", "k", "v", "o", "gate", "up", "down")}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", ["tiny", "gemma3_4b"])
+def test_q8_0_model_fused_decode_matches_oracle(rt, orc, shape):
+    """Every projection in Q8_0 (a Q8_0 file): q|k|v and gate|up run as the
+    fused Q8_0 launches beside their prologues (k_qkv8, k_gateup8; the tiny
+    and the Gemma-3-4B tiles), o and down as Q8_0 GEMVs.  Steps at three
+    positions (the first eager, the others graph replays) and a verify batch
+    against the oracle's exact dequantisation."""
+    from test_gpu_decode import tiny
+    from test_oracle import make_model
+    if shape == "tiny":
+        cfg, ctx, max_seq = tiny(2), 6, 32
+    else:
+        cfg, ctx, max_seq = dict(rt.GEMMA3_4B, n_layers=2, global_every=2, vocab=4096), 40, 64
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=ctx, seed=7700 + ctx)
+    plan = {li: dict(ALL_Q8_0) for li in range(cfg["n_layers"])}
+    dev_layers, fmts = apply_formats(orc, cfg, layers, plan, seed=7701 + ctx)
+    d = mixed_ctx(rt, cfg, dev_layers, fmts, embed, fnorm, ctx, max_seq, layers)
+    for i, tok in enumerate((11, 3, 900)):
+        got = d.decode_step(tok, ctx + i)
+        ref = orc.gemma3_decode_step(cfg, layers, embed, fnorm, token=tok, pos=ctx + i)
+        assert np.all(np.isfinite(got))
+        assert rel_l2(got, ref) < 1e-3, (i, rel_l2(got, ref))
+    batch = d.decode_step_batch([5, 6, 7], ctx + 3)
+    for i, tok in enumerate((5, 6, 7)):
+        ref = orc.gemma3_decode_step(cfg, layers, embed, fnorm, token=tok, pos=ctx + 3 + i)
+        assert rel_l2(batch[i], ref) < 1e-3, (i, rel_l2(batch[i], ref))
+    d.close()
+
+
 def test_oracle_mixed_prefill_equals_decode_steps(orc):
     """Per-row sliding window: the oracle prefill of a model with projections
     in every format is T decode steps of the decode-step oracle (whose
