@@ -532,6 +532,7 @@ def main() -> int:
         log(f"decode_step_batch M={bm}: {dtb * 1e3:.3f} ms per call -> {bm / dtb:.1f} tok/s")
         decode["q4k_lm_head"] = q4k_lm_head_decode(rt, torch, gen, d, ctx, dec_bytes, args)
         decode["q4_k_m_layout"] = q4_k_m_layout_decode(rt, torch, dev, gen, layers, embed, final_norm, args)
+        decode["q8_0_model"] = q8_0_model_decode(rt, torch, dev, gen, layers, embed, final_norm, args)
         # GPU prefill of a config-3-length prompt (4096 tokens) on the same weights
         toks = [(7 * i + 3) % V for i in range(ctx)]
         pf = {"tokens": ctx}
@@ -765,6 +766,53 @@ def q4k_lm_head_decode(rt, torch, gen, d, ctx: int, dec_bytes: int, args) -> dic
            "GBps": round(nbytes / dt / 1e9, 1), "frac_of_hbm_peak": round(nbytes / dt / 1e9 / PEAK_HBM_GBS, 4),
            "verify_m": bm, "verify_ms_per_call": round(dtb * 1e3, 4), "verify_tok_per_s": round(bm / dtb, 1)}
     log(f"Q4_K lm_head: decode step {dt * 1e3:.3f} ms -> {1 / dt:.1f} tok/s; verify M={bm} {dtb * 1e3:.3f} ms")
+    return out
+
+
+def q8_0_model_decode(rt, torch, dev, gen, layers, embed, final_norm, args) -> dict:
+    """The config-3 step and the M = 8 verify with every projection in Q8_0
+    (a Q8_0 file; planar layout, random codes and scales): q|k|v and gate|up
+    run as the fused Q8_0 launches."""
+    ctx = 4096
+    q8 = [{name: synth_q8_0_planar(torch, n, k, gen) for name, n, k in Q4K_SHAPES} for _ in range(L)]
+    d = rt.HipDecodeContext(dict(rt.GEMMA3_4B), ctx + 8 * (args.warmup + args.steps) + 8 * 12 + 8)
+    for li, w in enumerate(layers):
+        d.set_layer(li, dict(w, **q8[li]), formats=[5] * 7)
+        kv = torch.randn(2, ctx, KVD, device=dev, generator=gen)
+        d.sync_kv_from_cpu(li, kv[0], kv[1], ctx)
+        del kv
+    d.set_embed(embed, final_norm)
+    torch.cuda.synchronize()
+    pos = ctx
+    for _ in range(args.warmup):
+        d.decode_step_async(pos % V, pos)
+        pos += 1
+    d.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        d.decode_step_async(pos % V, pos)
+        pos += 1
+    d.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    bm, reps = 8, max(4, args.steps // 2)
+    for _ in range(2):
+        d.decode_step_batch_async([(pos + i) % V for i in range(bm)], pos)
+        pos += bm
+    d.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        d.decode_step_batch_async([(pos + i) % V for i in range(bm)], pos)
+        pos += bm
+    d.synchronize()
+    dtb = (time.perf_counter() - t0) / reps
+    wbytes = L * sum(n * k // 32 * 34 for _, n, k in Q4K_SHAPES) + V * H * 2
+    out = {"formats": "every projection Q8_0 (planar); BF16 tied lm_head", "decode_ms_per_token": round(dt * 1e3, 4),
+           "decode_tok_per_s": round(1.0 / dt, 1), "weight_bytes_per_token": wbytes,
+           "GBps": round(wbytes / dt / 1e9, 1), "verify_m": bm, "verify_ms_per_call": round(dtb * 1e3, 4)}
+    log(f"Q8_0 model: decode step {dt * 1e3:.3f} ms ({wbytes / dt / 1e9:.0f} GB/s of weights); "
+        f"verify M={bm} {dtb * 1e3:.3f} ms per call")
+    d.close()
+    del q8
     return out
 
 
