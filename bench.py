@@ -144,6 +144,8 @@ def main() -> int:
                     help="with --decode-profile: the Q4_K_M layout (v and down in Q6_K)")
     ap.add_argument("--q8-0", action="store_true",
                     help="with --decode-profile: every projection in Q8_0 (planar)")
+    ap.add_argument("--bf16-model", action="store_true",
+                    help="with --decode-profile: every projection in BF16")
     ap.add_argument("--q4k-lm-head", action="store_true",
                     help="with --decode-profile: a Q4_K lm_head (random blocks) instead of the BF16 tied one")
     ap.add_argument("--verify-rows", type=int, default=0,
@@ -226,6 +228,10 @@ def main() -> int:
             layers = [dict(w, **{name: synth_q8_0_planar(torch, n, k, gen) for name, n, k in Q4K_SHAPES})
                       for w in layers]
             fmts = [5] * 7
+        elif args.bf16_model:
+            layers = [dict(w, **{name: (torch.randn(n * k, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+                                 .view(torch.int16) for name, n, k in Q4K_SHAPES}) for w in layers]
+            fmts = [2] * 7
         d, pos = build_decode(rt, torch, dev, gen, layers, embed, final_norm, args, formats=fmts)
         if args.q4k_lm_head:
             head = synth_q4k(torch, V, H, gen)
@@ -249,6 +255,7 @@ def main() -> int:
         dt = (time.perf_counter() - t1) / args.steps
         print(json.dumps({"decode_profile": "done", "steps": args.steps, "verify_rows": bm,
                           "q4k_lm_head": args.q4k_lm_head, "q4_k_m": args.q4_k_m, "q8_0": args.q8_0,
+                          "bf16_model": args.bf16_model,
                           "ms_per_call": round(dt * 1e3, 4)}))
         d.close()
         return 0

@@ -313,6 +313,99 @@ __global__ __launch_bounds__(T) void k_gateup8(DecodeArgs a, LayerArgs L, int ff
 }
 
 // ---------------------------------------------------------------------------
+// And for BF16 q, k, v (k_qkv16) or gate, up (k_gateup16), as in BF16 files:
+// the prologue stages xn in LDS as f32 (k_lmhead's layout), then one wave per
+// row as in the BF16 GEMV: lane l holds elements (64 i + l) * 8 .. + 8 of the
+// row for i < CPL (K = 512 CPL), two rows' loads in flight per wave.
+// ---------------------------------------------------------------------------
+template <int CPL>
+RT_DEV float bf16_dot_lane(const uint4 (&w)[CPL], const float (&xr)[CPL][8]) {
+  float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    acc0 += bf16_lo(w[i].x) * xr[i][0];
+    acc1 += bf16_hi(w[i].x) * xr[i][1];
+    acc0 += bf16_lo(w[i].y) * xr[i][2];
+    acc1 += bf16_hi(w[i].y) * xr[i][3];
+    acc0 += bf16_lo(w[i].z) * xr[i][4];
+    acc1 += bf16_hi(w[i].z) * xr[i][5];
+    acc0 += bf16_lo(w[i].w) * xr[i][6];
+    acc1 += bf16_hi(w[i].w) * xr[i][7];
+  }
+  return wave_sum(acc0 + acc1);
+}
+
+template <int CPL>
+RT_DEV void bf16_x_from_lds(const float *xl, float (&xr)[CPL][8]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xr[i][j] = xl[xlds_index((i * 64 + lane) * 8 + j)];
+}
+
+template <int CPL, Pro MODE>
+__global__ __launch_bounds__(256) void k_qkv16(DecodeArgs a, LayerArgs L, LayerArgs prev) {
+  constexpr int K = CPL * 512;
+  __shared__ __attribute__((aligned(16))) float xl[K / 64 * kXPitch];
+  __shared__ float bred[4];
+  ProRegs<K, 256> pr;
+  pro_load<K, 256, MODE>(a, a.x2, a.dn, prev.g_post_ffn, L.g_in, pr);
+  pro_finish<K, 256, MODE>(a, pr, a.hid, xl, bred, a.xn);
+  __syncthreads();
+  float xr[CPL][8];
+  bf16_x_from_lds<CPL>(xl, xr);
+  const int lane = threadIdx.x & 63;
+  const int qd = a.n_q_heads * a.head_dim, kvd = a.n_kv_heads * a.head_dim, total = qd + 2 * kvd;
+  const int wave = (int)((blockIdx.x * 256u + threadIdx.x) >> 6), nwaves = (int)(gridDim.x * 4u);
+  // rows r0, r0 + 1 of the stacked q|k|v (qd and kvd are even: a pair never
+  // straddles two matrices)
+  for (int r0 = 2 * wave; r0 < total; r0 += 2 * nwaves) {
+    const uint16_t *W;
+    float *y;
+    int lr;
+    if (r0 < qd) {
+      W = reinterpret_cast<const uint16_t *>(L.wq), y = a.q, lr = r0;
+    } else if (r0 < qd + kvd) {
+      W = reinterpret_cast<const uint16_t *>(L.wk), y = a.k, lr = r0 - qd;
+    } else {
+      W = reinterpret_cast<const uint16_t *>(L.wv), y = a.v, lr = r0 - qd - kvd;
+    }
+    uint4 w0[CPL], w1[CPL];
+    const uint4 *p0 = reinterpret_cast<const uint4 *>(W + (size_t)lr * K), *p1 = p0 + K / 8;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) w0[i] = p0[i * 64 + lane], w1[i] = p1[i * 64 + lane];
+    const float d0 = bf16_dot_lane<CPL>(w0, xr), d1 = bf16_dot_lane<CPL>(w1, xr);
+    if (lane == 0) y[lr] = d0, y[lr + 1] = d1;
+  }
+}
+
+template <int CPL>
+__global__ __launch_bounds__(256) void k_gateup16(DecodeArgs a, LayerArgs L, int ffn) {
+  constexpr int K = CPL * 512;
+  __shared__ __attribute__((aligned(16))) float xl[K / 64 * kXPitch];
+  __shared__ float bred[4];
+  ProRegs<K, 256> pr;
+  pro_load<K, 256, Pro::Resid>(a, a.hid, a.o, L.g_post_attn, L.g_pre_ffn, pr);
+  pro_finish<K, 256, Pro::Resid>(a, pr, a.x2, xl, bred);
+  __syncthreads();
+  float xr[CPL][8];
+  bf16_x_from_lds<CPL>(xl, xr);
+  const int lane = threadIdx.x & 63;
+  const int wave = (int)((blockIdx.x * 256u + threadIdx.x) >> 6), nwaves = (int)(gridDim.x * 4u);
+  const uint16_t *Wg = reinterpret_cast<const uint16_t *>(L.wgate), *Wu = reinterpret_cast<const uint16_t *>(L.wup);
+  for (int j = wave; j < ffn; j += nwaves) {  // gate row j and up row j: h[j] = gelu(g) u
+    uint4 wg[CPL], wu[CPL];
+    const uint4 *pg = reinterpret_cast<const uint4 *>(Wg + (size_t)j * K);
+    const uint4 *pu = reinterpret_cast<const uint4 *>(Wu + (size_t)j * K);
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) wg[i] = pg[i * 64 + lane], wu[i] = pu[i * 64 + lane];
+    const float g = bf16_dot_lane<CPL>(wg, xr), u = bf16_dot_lane<CPL>(wu, xr);
+    if (lane == 0) a.h[j] = mul_nc(gelu_tanh(g), u);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // k_gemv: plain GEMV with the activation vector read from global memory.
 // ---------------------------------------------------------------------------
 template <int NB, int T, int ITERS>
@@ -785,6 +878,25 @@ static void launch_gateup8(Launch &l, const DecodeArgs &a, const LayerArgs &L, i
   l.check();
 }
 
+template <int CPL>
+static void launch_qkv16(Launch &l, const DecodeArgs &a, const LayerArgs &L, const LayerArgs &prev, bool first,
+                         int rows_total) {
+  // at most two workgroups per CU, each paying the prologue once (a BF16
+  // model's step: 2.211 ms at 512, 2.238 at 256, 2.213 at 1024)
+  const dim3 grid((unsigned)std::min((rows_total / 2 + 3) / 4, 512));
+  if (first)
+    hipLaunchKernelGGL((k_qkv16<CPL, Pro::Embed>), grid, dim3(256), 0, l.s, a, L, prev);
+  else
+    hipLaunchKernelGGL((k_qkv16<CPL, Pro::Resid>), grid, dim3(256), 0, l.s, a, L, prev);
+  l.check();
+}
+
+template <int CPL>
+static void launch_gateup16(Launch &l, const DecodeArgs &a, const LayerArgs &L, int ffn) {
+  hipLaunchKernelGGL((k_gateup16<CPL>), dim3((unsigned)std::min((ffn + 3) / 4, 512)), dim3(256), 0, l.s, a, L, ffn);
+  l.check();
+}
+
 template <int NB, int T, int GR>
 static void launch_gateup(Launch &l, const DecodeArgs &a, const LayerArgs &L, int ffn) {
   hipLaunchKernelGGL((k_gateup<NB, T, GR>), dim3(ffn / GR), dim3(T), 0, l.s, a, L);
@@ -869,6 +981,7 @@ static hipError_t enqueue_layers(const DecodeShape &s, const DecodeArgs &a, cons
     const LayerArgs &P = layers[li > 0 ? li - 1 : 0];
     auto q4 = [&](int p) { return L.fmt[p] == RT_LINEAR_Q4K; };
     auto q8 = [&](int p) { return L.fmt[p] == RT_LINEAR_Q8_0; };
+    auto b16 = [&](int p) { return L.fmt[p] == RT_LINEAR_BF16; };
     if (q4(kProjQ) && q4(kProjK)) {
       // fused prologue + GEMV over q|k|v rows (v in Q4_K or Q6_K); it also
       // leaves xn for a v of another format
@@ -880,6 +993,9 @@ static hipError_t enqueue_layers(const DecodeShape &s, const DecodeArgs &a, cons
     } else if (q8(kProjQ) && q8(kProjK) && q8(kProjV)) {
       if (big) launch_qkv8<80, 640, 2>(l, a, L, P, li == 0, qd + 2 * kvd);
       else launch_qkv8<16, 256, 2>(l, a, L, P, li == 0, qd + 2 * kvd);
+    } else if (b16(kProjQ) && b16(kProjK) && b16(kProjV)) {
+      if (big) launch_qkv16<5>(l, a, L, P, li == 0, qd + 2 * kvd);
+      else launch_qkv16<1>(l, a, L, P, li == 0, qd + 2 * kvd);
     } else {
       if (li == 0) launch_prologue<Pro::Embed>(l, s, a, nullptr, nullptr, nullptr, L.g_in, a.hid);
       else launch_prologue<Pro::Resid>(l, s, a, a.x2, a.dn, P.g_post_ffn, L.g_in, a.hid);
@@ -902,6 +1018,9 @@ static hipError_t enqueue_layers(const DecodeShape &s, const DecodeArgs &a, cons
     } else if (q8(kProjGate) && q8(kProjUp)) {
       if (big) launch_gateup8<80, 640, kGateRowsBig>(l, a, L, s.ffn);
       else launch_gateup8<16, 256, kGateRowsSmall>(l, a, L, s.ffn);
+    } else if (b16(kProjGate) && b16(kProjUp)) {
+      if (big) launch_gateup16<5>(l, a, L, s.ffn);
+      else launch_gateup16<1>(l, a, L, s.ffn);
     } else {
       launch_prologue<Pro::Resid>(l, s, a, a.hid, a.o, L.g_post_attn, L.g_pre_ffn, a.x2);
       launch_proj(l, L.fmt[kProjGate], L.wgate, a.xn, a.h, s.ffn, s.hidden);

@@ -351,15 +351,17 @@ def test_q4_k_m_layout_verify_batch_at_gemma3_4b_shape(rt, orc, m):
 # ---------------------------------------------------------------------------
 # prefill with per-projection formats
 # ---------------------------------------------------------------------------
-ALL_Q8_0 = {p: 5 for p in ("q", "k", "v", "o", "gate", "up", "down")}
+PROJS = ("q", "k", "v", "o", "gate", "up", "down")
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("fmt", [5, 2])
 @pytest.mark.parametrize("shape", ["tiny", "gemma3_4b"])
-def test_q8_0_model_fused_decode_matches_oracle(rt, orc, shape):
-    """Every projection in Q8_0 (a Q8_0 file): q|k|v and gate|up run as the
-    fused Q8_0 launches beside their prologues (k_qkv8, k_gateup8; the tiny
-    and the Gemma-3-4B tiles), o and down as Q8_0 GEMVs.  Steps at three
+def test_uniform_format_model_fused_decode_matches_oracle(rt, orc, shape, fmt):
+    """Every projection in Q8_0 (a Q8_0 file) or in BF16 (a BF16 file): q|k|v
+    and gate|up run as the fused launches of that format beside their
+    prologues (k_qkv8 / k_gateup8, k_qkv16 / k_gateup16; the tiny and the
+    Gemma-3-4B widths), o and down as GEMVs of the format.  Steps at three
     positions (the first eager, the others graph replays) and a verify batch
     against the oracle's exact dequantisation."""
     from test_gpu_decode import tiny
@@ -368,9 +370,9 @@ def test_q8_0_model_fused_decode_matches_oracle(rt, orc, shape):
         cfg, ctx, max_seq = tiny(2), 6, 32
     else:
         cfg, ctx, max_seq = dict(rt.GEMMA3_4B, n_layers=2, global_every=2, vocab=4096), 40, 64
-    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=ctx, seed=7700 + ctx)
-    plan = {li: dict(ALL_Q8_0) for li in range(cfg["n_layers"])}
-    dev_layers, fmts = apply_formats(orc, cfg, layers, plan, seed=7701 + ctx)
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=ctx, seed=7700 + ctx + fmt)
+    plan = {li: {p: fmt for p in PROJS} for li in range(cfg["n_layers"])}
+    dev_layers, fmts = apply_formats(orc, cfg, layers, plan, seed=7701 + ctx + fmt)
     d = mixed_ctx(rt, cfg, dev_layers, fmts, embed, fnorm, ctx, max_seq, layers)
     for i, tok in enumerate((11, 3, 900)):
         got = d.decode_step(tok, ctx + i)
