@@ -137,6 +137,9 @@ def main() -> int:
     ap.add_argument("--prefill-profile", action="store_true",
                     help="only run the 4096-token GPU prefill of the config-3 context, --warmup then --steps "
                          "times; meant to run under rocprofv3")
+    ap.add_argument("--gemm-tiles", action="store_true",
+                    help="only time the M=512 Q4_K GEMM at 128, 160 and 256 tiles of 128x256 (one per CU): how "
+                         "the time per K-chunk grows with the tiles in flight")
     ap.add_argument("--launch-probe", action="store_true",
                     help="only measure the launch floor inside a graph: empty dependent launches, and streaming "
                          "reads of 4-118 MB fitted to a fixed cost per launch plus a rate")
@@ -168,6 +171,9 @@ def main() -> int:
 
     if args.launch_probe:
         print(json.dumps(launch_probe(rt, torch, dev)))
+        return 0
+    if args.gemm_tiles:
+        print(json.dumps(gemm_tiles_probe(rt, torch, dev, torch.Generator(device=dev).manual_seed(args.seed))))
         return 0
 
     if args.traffic_probe:
@@ -664,6 +670,30 @@ def main() -> int:
     }
     print(json.dumps(out), flush=True)
     return 0
+
+
+def gemm_tiles_probe(rt, torch, dev, gen) -> dict:
+    """Whole rt_q4k_gemm_bf16 calls at M = 512, K = 2560 with 128, 160 and 256
+    output tiles (N = 8192, 10240, 16384), and config 2's down shape: with
+    one tile per CU, how the time of a tile's 40 K-chunks grows with the
+    number of tiles in flight (what a balanced split of config 2 could gain)."""
+    out = []
+    for m, n, k in ((512, 8192, 2560), (512, 10240, 2560), (512, 16384, 2560), (512, 2560, 10240)):
+        w = synth_q4k(torch, n, k, gen)
+        a = torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16).view(torch.int16)
+        c = torch.empty(m, n, device=dev)
+        for _ in range(3):
+            rt.q4k_gemm(a, w, c, m, n, k)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(20):
+            rt.q4k_gemm(a, w, c, m, n, k)
+        e1.record()
+        torch.cuda.synchronize()
+        out.append({"m": m, "n": n, "k": k, "tiles": (m // 128) * (n // 256), "us": round(e0.elapsed_time(e1) * 1e3 / 20, 1)})
+        del w, a, c
+    return {"gemm_tiles": out}
 
 
 def launch_probe(rt, torch, dev) -> dict:
