@@ -151,6 +151,10 @@ def main() -> int:
                     help="with --decode-profile: every projection in BF16")
     ap.add_argument("--q4k-lm-head", action="store_true",
                     help="with --decode-profile: a Q4_K lm_head (random blocks) instead of the BF16 tied one")
+    ap.add_argument("--shared-weights", action="store_true",
+                    help="with --decode-profile: bind every layer to layer 0's projections and norms (53 MB, "
+                         "which stays in the 256 MB last-level cache between layers), to see how much of each "
+                         "layer kernel's time is HBM traffic")
     ap.add_argument("--verify-rows", type=int, default=0,
                     help="with --decode-profile: run decode_step_batch calls of this many rows (1..8) instead "
                          "of single-token steps")
@@ -238,6 +242,8 @@ def main() -> int:
             layers = [dict(w, **{name: (torch.randn(n * k, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
                                  .view(torch.int16) for name, n, k in Q4K_SHAPES}) for w in layers]
             fmts = [2] * 7
+        if args.shared_weights:
+            layers = [layers[0]] * L
         d, pos = build_decode(rt, torch, dev, gen, layers, embed, final_norm, args, formats=fmts)
         if args.q4k_lm_head:
             head = synth_q4k(torch, V, H, gen)
@@ -261,7 +267,7 @@ def main() -> int:
         dt = (time.perf_counter() - t1) / args.steps
         print(json.dumps({"decode_profile": "done", "steps": args.steps, "verify_rows": bm,
                           "q4k_lm_head": args.q4k_lm_head, "q4_k_m": args.q4_k_m, "q8_0": args.q8_0,
-                          "bf16_model": args.bf16_model,
+                          "bf16_model": args.bf16_model, "shared_weights": args.shared_weights,
                           "ms_per_call": round(dt * 1e3, 4)}))
         d.close()
         return 0
