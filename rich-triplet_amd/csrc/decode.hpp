@@ -12,7 +12,10 @@ namespace rt {
 // from the window (sliding-window layers) and from max_seq (global layers),
 // and k_attn_combine merges the chunks.
 constexpr int kAttnLocalKpw = 4, kAttnLocalWaves = 4;
-constexpr int kAttnGlobalKpw = 8, kAttnGlobalWaves = 8;
+constexpr int kAttnGlobalKpw = 8, kAttnGlobalWaves = 4;
+// Dimensions per k_attn_combine workgroup (the rest of its 256 threads are
+// chunk groups).
+constexpr int kCombineDims = 32;
 // Upper bound on the number of chunks a KV head is split into.
 constexpr int kAttnMaxChunks = 4096;
 // Step parameter block (device): ints [0, 16) (token, position), then the

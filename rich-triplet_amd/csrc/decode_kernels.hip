@@ -600,29 +600,31 @@ __global__ __launch_bounds__(64 * WAVES) void k_attn(DecodeArgs a, LayerArgs L) 
 }
 
 // ---------------------------------------------------------------------------
-// k_attn_combine: merge the chunk partials of one q head and 64 dimensions.
+// k_attn_combine: merge the chunk partials of one q head and DW dimensions.
 //   out[d] = sum_i o_i[d] e^(m_i - M) / sum_i l_i e^(m_i - M),  M = max_i m_i
-// 256 threads = 4 chunk groups x 64 dimensions.  A thread loads the partials
-// of up to R chunks at once (all loads in flight together), folds them into
-// its running (M, L, O), and the four groups merge through LDS; grid
-// (n_q_heads, D/64).
+// 256 threads = CG = 256/DW chunk groups x DW dimensions.  A thread loads the
+// partials of up to R chunks at once (all loads in flight together), folds
+// them into its running (M, L, O), and the CG groups merge through LDS; grid
+// (n_q_heads, D/DW).
 // ---------------------------------------------------------------------------
-template <int D>
+template <int D, int DW>
 __global__ __launch_bounds__(256) void k_attn_combine(DecodeArgs a, int nchunk) {
-  constexpr int R = 20;  // 80 chunks per batch
-  __shared__ float gm[4], gl[4];
-  __shared__ float go[4][64];
-  const int h = blockIdx.x, d0 = blockIdx.y * 64;
-  const int cg = threadIdx.x >> 6, dl = threadIdx.x & 63;
+  constexpr int CG = 256 / DW;
+  constexpr int R = (80 + CG - 1) / CG;  // at least 80 chunks per batch
+  static_assert(D % DW == 0 && 256 % DW == 0, "DW divides D and the workgroup");
+  __shared__ float gm[CG], gl[CG];
+  __shared__ float go[CG][DW];
+  const int h = blockIdx.x, d0 = blockIdx.y * DW;
+  const int cg = threadIdx.x / DW, dl = threadIdx.x % DW;
   const float *pm = a.part_m + (size_t)h * nchunk;
   const float *pl = a.part_l + (size_t)h * nchunk;
   const float *po = a.part_o + (size_t)h * nchunk * D + d0 + dl;
   float M = -INFINITY, Ls = 0.f, O = 0.f;
-  for (int base = cg; base < nchunk; base += 4 * R) {
+  for (int base = cg; base < nchunk; base += CG * R) {
     float mi[R], li[R], oi[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int i = min(base + 4 * r, nchunk - 1);  // clamped, unconditional loads
+      const int i = min(base + CG * r, nchunk - 1);  // clamped, unconditional loads
       mi[r] = pm[i];
       li[r] = pl[i];
       oi[r] = po[(size_t)i * D];
@@ -630,14 +632,14 @@ __global__ __launch_bounds__(256) void k_attn_combine(DecodeArgs a, int nchunk) 
     float mb = M;
 #pragma unroll
     for (int r = 0; r < R; ++r)
-      if (base + 4 * r < nchunk) mb = fmaxf(mb, mi[r]);  // empty chunks carry m = -inf, l = 0
+      if (base + CG * r < nchunk) mb = fmaxf(mb, mi[r]);  // empty chunks carry m = -inf, l = 0
     if (mb != -INFINITY) {
       const float sc = expf(M - mb);  // 0 while M is still -inf
       Ls *= sc;
       O *= sc;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const float w = (base + 4 * r < nchunk && mi[r] != -INFINITY) ? expf(mi[r] - mb) : 0.f;
+        const float w = (base + CG * r < nchunk && mi[r] != -INFINITY) ? expf(mi[r] - mb) : 0.f;
         Ls = fmaf(li[r], w, Ls);
         O = fmaf(oi[r], w, O);
       }
@@ -651,10 +653,12 @@ __global__ __launch_bounds__(256) void k_attn_combine(DecodeArgs a, int nchunk) 
   go[cg][dl] = O;
   __syncthreads();
   if (cg == 0) {
-    const float Mx = fmaxf(fmaxf(gm[0], gm[1]), fmaxf(gm[2], gm[3]));
+    float Mx = gm[0];
+#pragma unroll
+    for (int q = 1; q < CG; ++q) Mx = fmaxf(Mx, gm[q]);
     float Lt = 0.f, Ot = 0.f;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < CG; ++q) {
       const float w = gm[q] == -INFINITY ? 0.f : expf(gm[q] - Mx);
       Lt += gl[q] * w;
       Ot += go[q][dl] * w;
@@ -944,7 +948,8 @@ static void launch_attn_d(Launch &l, const DecodeArgs &a, const LayerArgs &L, in
   else
     launch_attn_kw<D, kAttnGlobalKpw, kAttnGlobalWaves>(l, a, L, nchunk, group);
   l.check();
-  hipLaunchKernelGGL((k_attn_combine<D>), dim3(a.n_q_heads, D / 64), dim3(256), 0, l.s, a, nchunk);
+  hipLaunchKernelGGL((k_attn_combine<D, kCombineDims>), dim3(a.n_q_heads, D / kCombineDims), dim3(256), 0, l.s, a,
+                     nchunk);
   l.check();
 }
 
