@@ -992,7 +992,7 @@ static hipError_t enqueue_layers(const DecodeShape &s, const DecodeArgs &a, cons
       // leaves xn for a v of another format
       const bool v6 = L.fmt[kProjV] == RT_LINEAR_Q6K;
       const int qkv_rows = qd + kvd + (q4(kProjV) || v6 ? kvd : 0);
-      if (big) launch_qkv<10, 640, 1>(l, a, L, P, li == 0, qkv_rows, v6);
+      if (big) launch_qkv<10, 320, 2>(l, a, L, P, li == 0, qkv_rows, v6);
       else launch_qkv<2, 256, 1>(l, a, L, P, li == 0, qkv_rows, v6);
       if (!q4(kProjV) && !v6) launch_proj(l, L.fmt[kProjV], L.wv, a.xn, a.v, kvd, s.hidden);
     } else if (q8(kProjQ) && q8(kProjK) && q8(kProjV)) {
