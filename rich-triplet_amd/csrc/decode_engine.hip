@@ -929,16 +929,18 @@ rt_status rt_decode_set_graph(rt_decode *d, int32_t enabled) {
   return RT_OK;
 }
 
-// print_metal_memory (metal_decode.rs:1285-1354): the device memory of the
-// context by what it holds.  Weights bound by device pointer count too, as
-// the reference's uploads do; the prefill scratch appears once a prefill has
-// sized it.
+// Whether decode_step_batch runs every layer through the batched GEMVs (one
+// pass over the weights for all rows) or falls back to per-token passes.
 rt_status rt_decode_verify_batched(const rt_decode *d, int32_t *batched) {
   if (!d || !batched) return set_error(RT_EINVAL, "rt_decode_verify_batched: null pointer");
   *batched = d->rows_mb ? 1 : 0;
   return RT_OK;
 }
 
+// print_metal_memory (metal_decode.rs:1285-1354): the device memory of the
+// context by what it holds.  Weights bound by device pointer count too, as
+// the reference's uploads do; the prefill scratch appears once a prefill has
+// sized it.
 rt_status rt_decode_memory(const rt_decode *d, rt_decode_memory_info *out) {
   if (!d || !out) return set_error(RT_EINVAL, "rt_decode_memory: null pointer");
   uint64_t by[rt_decode::kMemKinds] = {};

@@ -833,8 +833,10 @@ __global__ __launch_bounds__(256) void k_lmhead_batch(const uint16_t *__restrict
 // ---------------------------------------------------------------------------
 // Host-side step encoder
 // ---------------------------------------------------------------------------
-template <int NB, int T>
-static constexpr int rows_per_iter() { return T / (NB * 4); }
+// q|k|v tiles (Q4_K rows, the Q6_K v beside them): hidden 2560 runs 320
+// threads of two row iterations, hidden 512 one iteration of 256 threads
+using QkvTileBig = Q4KTile<10, 320, 2>;
+using QkvTileSmall = Q4KTile<2, 256, 1>;
 // gate rows (and as many up rows) per k_gateup workgroup
 constexpr int kGateRowsBig = 20, kGateRowsSmall = 32;
 
@@ -992,8 +994,8 @@ static hipError_t enqueue_layers(const DecodeShape &s, const DecodeArgs &a, cons
       // leaves xn for a v of another format
       const bool v6 = L.fmt[kProjV] == RT_LINEAR_Q6K;
       const int qkv_rows = qd + kvd + (q4(kProjV) || v6 ? kvd : 0);
-      if (big) launch_qkv<10, 320, 2>(l, a, L, P, li == 0, qkv_rows, v6);
-      else launch_qkv<2, 256, 1>(l, a, L, P, li == 0, qkv_rows, v6);
+      if (big) launch_qkv<10, QkvTileBig::kThreads, QkvTileBig::kIters>(l, a, L, P, li == 0, qkv_rows, v6);
+      else launch_qkv<2, QkvTileSmall::kThreads, QkvTileSmall::kIters>(l, a, L, P, li == 0, qkv_rows, v6);
       if (!q4(kProjV) && !v6) launch_proj(l, L.fmt[kProjV], L.wv, a.xn, a.v, kvd, s.hidden);
     } else if (q8(kProjQ) && q8(kProjK) && q8(kProjV)) {
       if (big) launch_qkv8<80, 640, 2>(l, a, L, P, li == 0, qd + 2 * kvd);
@@ -1139,14 +1141,13 @@ bool decode_shape_generic(const DecodeShape &s, const char **why) {
 }
 
 // Row-count divisibility the launches above rely on.
-static_assert(Q8Tile<80, 640, 2>::ROWS == Q4KTile<10, 640, 1>::ROWS &&
-                  Q8Tile<16, 256, 2>::ROWS == Q4KTile<2, 256, 1>::ROWS,
+static_assert(Q8Tile<80, 640, 2>::ROWS == QkvTileBig::ROWS && Q8Tile<16, 256, 2>::ROWS == QkvTileSmall::ROWS,
               "the Q8_0 q|k|v tiles cover the Q4_K tiles' rows, so one divisibility check serves both");
 
 bool decode_rows_divisible(const DecodeShape &s, const char **why) {
   const int qd = s.n_q_heads * s.head_dim, kvd = s.n_kv_heads * s.head_dim;
   const bool big = s.hidden == 2560;
-  const int qkv_rows_per_wg = big ? rows_per_iter<10, 640>() : rows_per_iter<2, 256>();
+  const int qkv_rows_per_wg = big ? QkvTileBig::ROWS : QkvTileSmall::ROWS;
   if (qd % qkv_rows_per_wg || kvd % qkv_rows_per_wg) return *why = "q/kv rows must divide into workgroup tiles", false;
   const int gate_rows_per_wg = big ? kGateRowsBig : kGateRowsSmall;
   if (s.ffn % gate_rows_per_wg) return *why = "ffn rows must divide into gate/up tiles", false;

@@ -271,6 +271,7 @@ struct Q4KTile {
   static constexpr int S = NB * 4;
   static constexpr int RPI = T / S;
   static constexpr int ROWS = RPI * ITERS;
+  static constexpr int kThreads = T, kIters = ITERS;
   static_assert(T % S == 0 && T % 64 == 0, "a tile covers whole rows and whole waves");
 
   int slot, rsub, b, c;
