@@ -55,10 +55,10 @@ def test_tiny_decode_step_matches_oracle(rt, orc, group, pos):
 @pytest.mark.parametrize("group", [2, 4])
 @pytest.mark.parametrize("window,max_seq,pos", [(40, 300, 250), (37, 200, 63), (0, 130, 129)])
 def test_tiny_decode_ragged_chunks(rt, orc, group, window, max_seq, pos):
-    """Key spans that split into several chunks whose last 16-key sub-chunk is
-    partly filled (global: 251 keys over 5 chunks of 51; window 40 over 3
-    chunks of 14), a window that does not divide into 16, and global_every 0
-    with the new row the last of max_seq."""
+    """Key spans that split into several chunks whose last wave's keys are
+    partly filled (global: 251 keys over 10 chunks of 26, waves of 7; window
+    40 over 3 chunks of 14, waves of 4), a window that does not divide into
+    16, and global_every 0 with the new row the last of max_seq."""
     cfg = tiny(group, sliding_window=window, global_every=0 if window == 0 else 6)
     layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=pos, seed=900 + pos + group)
     d = build_ctx(rt, cfg, layers, embed, fnorm, pos, max_seq)
@@ -66,6 +66,31 @@ def test_tiny_decode_ragged_chunks(rt, orc, group, window, max_seq, pos):
     ref = orc.gemma3_decode_step(cfg, layers, embed, fnorm, token=5, pos=pos)
     assert np.all(np.isfinite(got))
     assert rel_l2(got, ref) < LOGITS_TOL
+    d.close()
+
+
+@pytest.mark.parametrize("group", [2, 4])
+def test_tiny_decode_long_context(rt, orc, group):
+    """A context of 19,990 rows in a max_seq of 20,000: the global layer's
+    keys split into 625 chunks, so the chunk merge folds its partials in
+    several batches, and an 8-token verify batch splits the same keys for its
+    row attention; both against the oracle (the batch against 8 sequential
+    oracle steps)."""
+    import copy
+    cfg = tiny(group, n_layers=3, global_every=3)
+    max_seq, ctx = 20000, 19990
+    layers, embed, fnorm = make_model(orc, cfg, max_seq=max_seq, ctx=ctx, seed=2000 + group)
+    d = build_ctx(rt, cfg, layers, embed, fnorm, ctx, max_seq)
+    olayers = copy.deepcopy(layers)
+    got = d.decode_step(11, ctx)
+    ref = orc.gemma3_decode_step(cfg, olayers, embed, fnorm, token=11, pos=ctx)
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, ref) < LOGITS_TOL
+    toks = [(13 * i + 5) % cfg["vocab"] for i in range(8)]
+    gb = d.decode_step_batch(toks, ctx + 1)
+    for i, t in enumerate(toks):
+        r = orc.gemma3_decode_step(cfg, olayers, embed, fnorm, token=t, pos=ctx + 1 + i)
+        assert rel_l2(gb[i], r) < LOGITS_TOL, i
     d.close()
 
 
