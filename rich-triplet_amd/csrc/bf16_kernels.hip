@@ -52,7 +52,7 @@ RT_DEV void bf16_rows(const uint16_t *__restrict__ W, const Bf16X<CPL> &xr, int 
     const int r = r0 + u;
     const uint4 *rp = reinterpret_cast<const uint4 *>(W + (size_t)(r < N ? r : 0) * K);
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) wv[u][i] = rp[i * 64 + lane];
+    for (int i = 0; i < CPL; ++i) wv[u][i] = ld_nt16(rp + i * 64 + lane);
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {

@@ -374,7 +374,7 @@ __global__ __launch_bounds__(256) void k_qkv16(DecodeArgs a, LayerArgs L, LayerA
     uint4 w0[CPL], w1[CPL];
     const uint4 *p0 = reinterpret_cast<const uint4 *>(W + (size_t)lr * K), *p1 = p0 + K / 8;
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) w0[i] = p0[i * 64 + lane], w1[i] = p1[i * 64 + lane];
+    for (int i = 0; i < CPL; ++i) w0[i] = ld_nt16(p0 + i * 64 + lane), w1[i] = ld_nt16(p1 + i * 64 + lane);
     const float d0 = bf16_dot_lane<CPL>(w0, xr), d1 = bf16_dot_lane<CPL>(w1, xr);
     if (lane == 0) y[lr] = d0, y[lr + 1] = d1;
   }
@@ -399,7 +399,7 @@ __global__ __launch_bounds__(256) void k_gateup16(DecodeArgs a, LayerArgs L, int
     const uint4 *pg = reinterpret_cast<const uint4 *>(Wg + (size_t)j * K);
     const uint4 *pu = reinterpret_cast<const uint4 *>(Wu + (size_t)j * K);
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) wg[i] = pg[i * 64 + lane], wu[i] = pu[i * 64 + lane];
+    for (int i = 0; i < CPL; ++i) wg[i] = ld_nt16(pg + i * 64 + lane), wu[i] = ld_nt16(pu + i * 64 + lane);
     const float g = bf16_dot_lane<CPL>(wg, xr), u = bf16_dot_lane<CPL>(wu, xr);
     if (lane == 0) a.h[j] = mul_nc(gelu_tanh(g), u);
   }
@@ -698,7 +698,7 @@ __global__ __launch_bounds__(256) void k_lmhead(DecodeArgs a, LayerArgs last) {
       const int r = min(r0 + u, N - 1);
       const uint4 *rp = reinterpret_cast<const uint4 *>(a.lm_bf16 + (size_t)r * K);
 #pragma unroll
-      for (int i = 0; i < CPL; ++i) wv[u][i] = rp[i * 64 + lane];
+      for (int i = 0; i < CPL; ++i) wv[u][i] = ld_nt16(rp + i * 64 + lane);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
