@@ -46,8 +46,9 @@ GEMM_SHAPES = [("config2_gate_up", 512, 10240, 2560), ("config2_down", 512, 2560
                ("config4_mlp_down", 4608, 3072, 12288)]
 
 H, F, QD, KVD, L, V = 2560, 10240, 2048, 1024, 34, 262144
-# streaming-read floor candidates (rt_stream_read_cfg kind, grid; grid 0 = by size)
-READ_CFGS = [(0, 0), (0, 512), (0, 1024), (1, 512), (1, 1024), (1, 2048)]
+# streaming-read floor candidates (rt_stream_read_cfg kind, grid; grid 0 = by size;
+# kinds 2 and 3 load with the nontemporal hint)
+READ_CFGS = [(0, 0), (0, 512), (0, 1024), (1, 512), (1, 1024), (1, 2048), (2, 0), (2, 768), (2, 1024), (3, 1024)]
 Q4K_SHAPES = [("q", QD, H), ("k", KVD, H), ("v", KVD, H), ("o", H, QD), ("gate", F, H), ("up", F, H),
               ("down", H, F)]
 

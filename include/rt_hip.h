@@ -141,7 +141,8 @@ size_t rt_gemm_workspace_held(void *stream);
  * `stream`; `sink` is a device word the kernel writes only on an impossible
  * checksum.  rt_stream_read_cfg picks the access pattern (kind 0: strided
  * over all threads with the next batch of loads in flight; kind 1: one
- * contiguous slice per workgroup) and the grid (0: by size).  bench.py times
+ * contiguous slice per workgroup; kinds 2 and 3: the same with nontemporal
+ * loads) and the grid (0: by size).  bench.py times
  * the fastest of several on the same bytes as a GEMV to give that GEMV's
  * fraction of a plain streaming read.  rt_empty_launch launches a kernel with
  * no body: in a graph, the cost of one dependent launch. */

@@ -201,7 +201,8 @@ def q4k_gemv_batch(w, a, c, m: int, n: int, k: int, stream=None) -> None:
 
 def stream_read(buf, nbytes: int, sink, stream=None, kind: int = 0, grid: int = 0) -> None:
     """Read nbytes of buf with 16-byte loads and discard them (a bandwidth
-    floor); kind 0 strided, 1 one slice per workgroup; grid 0 by size."""
+    floor); kind 0 strided, 1 one slice per workgroup, 2 and 3 the same with
+    nontemporal loads; grid 0 by size."""
     check(lib().rt_stream_read_cfg(_p(buf), nbytes, _p(sink), _stream(stream), kind, grid))
 
 

@@ -9,23 +9,31 @@
 
 #include "../../include/rt_hip.h"
 #include "rt_capi_util.hpp"
+#include "rt_device.hpp"
 
 namespace {
+
+// A 16-byte load, with the nontemporal hint when NT.
+template <bool NT>
+__device__ __forceinline__ uint4 ld16(const uint4 *p) {
+  if constexpr (NT) return rt::ld_nt16(p);
+  else return *p;
+}
 
 // Strided: thread i reads 16-byte words i, i + nth, i + 2 nth, ... in
 // batches of U, and the next batch's loads are issued before the current
 // batch is folded, so each thread always has loads in flight.
-template <int U>
+template <int U, bool NT>
 __global__ __launch_bounds__(256) void k_stream_read(const uint4 *__restrict__ p, size_t n16, uint32_t *sink) {
   const size_t tid = (size_t)blockIdx.x * 256 + threadIdx.x, nth = (size_t)gridDim.x * 256;
   uint32_t acc = 0;
   uint4 v[U];
 #pragma unroll
-  for (int u = 0; u < U; ++u) v[u] = p[std::min(tid + u * nth, n16 - 1)];
+  for (int u = 0; u < U; ++u) v[u] = ld16<NT>(p + std::min(tid + u * nth, n16 - 1));
   for (size_t i = tid; i < n16; i += nth * U) {
     uint4 w[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) w[u] = p[std::min(i + (U + u) * nth, n16 - 1)];
+    for (int u = 0; u < U; ++u) w[u] = ld16<NT>(p + std::min(i + (U + u) * nth, n16 - 1));
 #pragma unroll
     for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
 #pragma unroll
@@ -35,7 +43,7 @@ __global__ __launch_bounds__(256) void k_stream_read(const uint4 *__restrict__ p
 }
 
 // Blocked: workgroup b reads its own contiguous slice, 256 x U words per batch.
-template <int U>
+template <int U, bool NT>
 __global__ __launch_bounds__(256) void k_stream_read_blk(const uint4 *__restrict__ p, size_t n16, uint32_t *sink) {
   const size_t per = (n16 + gridDim.x - 1) / gridDim.x;
   const size_t b0 = (size_t)blockIdx.x * per, b1 = std::min(b0 + per, n16);
@@ -43,7 +51,7 @@ __global__ __launch_bounds__(256) void k_stream_read_blk(const uint4 *__restrict
   for (size_t i = b0 + threadIdx.x; i < b1; i += 256 * U) {
     uint4 v[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = p[std::min(i + u * 256, b1 - 1)];
+    for (int u = 0; u < U; ++u) v[u] = ld16<NT>(p + std::min(i + u * 256, b1 - 1));
 #pragma unroll
     for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
   }
@@ -59,8 +67,8 @@ extern "C" rt_status rt_stream_read_cfg(const void *buf, size_t bytes, void *sin
   if (!buf || !sink) return rt::set_error(RT_EINVAL, "rt_stream_read: null pointer");
   if (bytes % 16 != 0 || (reinterpret_cast<uintptr_t>(buf) & 15u) != 0)
     return rt::set_error(RT_EINVAL, "rt_stream_read: bytes and buf must be multiples of 16");
-  if (kind < 0 || kind > 1 || grid < 0 || grid > 65536)
-    return rt::set_error(RT_EINVAL, "rt_stream_read_cfg: kind must be 0 or 1 and grid 0..65536");
+  if (kind < 0 || kind > 3 || grid < 0 || grid > 65536)
+    return rt::set_error(RT_EINVAL, "rt_stream_read_cfg: kind must be 0..3 and grid 0..65536");
   const size_t n16 = bytes / 16;
   // grid 0: one batch per thread for reads up to 32 MB (single-launch
   // GEMV sizes), 512 workgroups looping beyond
@@ -69,10 +77,12 @@ extern "C" rt_status rt_stream_read_cfg(const void *buf, size_t bytes, void *sin
   hipStream_t s = (hipStream_t)stream;
   const uint4 *p = static_cast<const uint4 *>(buf);
   uint32_t *k = static_cast<uint32_t *>(sink);
-  if (kind == 0)
-    hipLaunchKernelGGL(k_stream_read<4>, dim3(g), dim3(256), 0, s, p, n16, k);
-  else
-    hipLaunchKernelGGL(k_stream_read_blk<8>, dim3(g), dim3(256), 0, s, p, n16, k);
+  switch (kind) {
+    case 0: hipLaunchKernelGGL((k_stream_read<4, false>), dim3(g), dim3(256), 0, s, p, n16, k); break;
+    case 1: hipLaunchKernelGGL((k_stream_read_blk<8, false>), dim3(g), dim3(256), 0, s, p, n16, k); break;
+    case 2: hipLaunchKernelGGL((k_stream_read<4, true>), dim3(g), dim3(256), 0, s, p, n16, k); break;
+    default: hipLaunchKernelGGL((k_stream_read_blk<8, true>), dim3(g), dim3(256), 0, s, p, n16, k); break;
+  }
   return rt::hip_error(hipGetLastError(), "rt_stream_read");
 }
 

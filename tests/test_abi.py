@@ -76,5 +76,22 @@ def test_q4k_gemm_rejects_null_and_misaligned(rt):
     assert L.rt_matmul_q4k_t(addr, 2, 100, addr, 4, addr) == rt.RT_EINVAL
 
 
+def test_measurement_probes_reject_bad_arguments_before_launch(rt):
+    """rt_stream_read_cfg (kinds 0..3: strided or sliced, plain or nontemporal
+    loads) and rt_empty_launch check their arguments before any HIP call."""
+    L = rt.lib()
+    buf = (C.c_uint8 * 64)()
+    addr = (C.addressof(buf) + 15) & ~15
+    assert L.rt_stream_read_cfg(addr, 16, addr, None, 4, 0) == rt.RT_EINVAL
+    assert "kind" in L.rt_last_error().decode()
+    assert L.rt_stream_read_cfg(addr, 16, addr, None, -1, 0) == rt.RT_EINVAL
+    assert L.rt_stream_read_cfg(addr, 16, addr, None, 2, 70000) == rt.RT_EINVAL
+    assert L.rt_stream_read_cfg(addr + 4, 16, addr, None, 3, 0) == rt.RT_EINVAL
+    assert L.rt_stream_read_cfg(None, 16, addr, None, 0, 0) == rt.RT_EINVAL
+    assert L.rt_stream_read_cfg(addr, 0, addr, None, 3, 0) == rt.RT_OK  # nothing to read
+    assert L.rt_empty_launch(0, 64, None) == rt.RT_EINVAL
+    assert L.rt_empty_launch(1, 2048, None) == rt.RT_EINVAL
+
+
 def test_zero_block_dequant_is_a_no_op(rt):
     assert rt.lib().rt_q4k_dequant_f32(None, 0, None, None) == rt.RT_OK
