@@ -767,18 +767,24 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
+// One workgroup of 16 waves per CU (the staged A fills half the LDS), each
+// wave with 16 segments of its 16 rows in flight: 2.671 against 2.697 ms per
+// M = 8 verify call for 4 waves and 8 segments.
+constexpr int kHeadBatchThreads = 1024, kHeadBatchGrid = 256;
+
 // K (the hidden width, a multiple of 32) is a template constant for the
 // fused-kernel shapes and a run-time value (K = 0) otherwise; the staged A
 // takes K*32 bytes of dynamic LDS.
 template <int KC>
-__global__ __launch_bounds__(256) void k_lmhead_batch(const uint16_t *__restrict__ E, const float *__restrict__ xn,
-                                                      float *__restrict__ logits, int N, int M, int Krt) {
+__global__ __launch_bounds__(kHeadBatchThreads) void k_lmhead_batch(const uint16_t *__restrict__ E,
+                                                                    const float *__restrict__ xn,
+                                                                    float *__restrict__ logits, int N, int M, int Krt) {
   const int K = KC ? KC : Krt;
   const int SEG = K / 32;
   extern __shared__ __attribute__((aligned(16))) uint16_t xa[];
   // stage: element e of vector v -> hi, lo bf16 at A rows 2v, 2v+1
 #pragma unroll 1
-  for (int i = threadIdx.x; i < 8 * K; i += 256) {
+  for (int i = threadIdx.x; i < 8 * K; i += kHeadBatchThreads) {
     const int v = i / K, e = i % K;
     uint16_t hi = 0, lo = 0;
     if (v < M) {
@@ -795,8 +801,9 @@ __global__ __launch_bounds__(256) void k_lmhead_batch(const uint16_t *__restrict
   __syncthreads();
   const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
   const int aoff = n * 32 + 8 * (g ^ ((n >> 2) & 3));  // this lane's A fragment inside a segment
-  const int wave = (int)((blockIdx.x * 256u + threadIdx.x) >> 6), nwaves = (int)(gridDim.x * 4u);
-  constexpr int B = 8;  // segments in flight per batch
+  const int wave = (int)((blockIdx.x * (unsigned)kHeadBatchThreads + threadIdx.x) >> 6);
+  const int nwaves = (int)gridDim.x * (kHeadBatchThreads / 64);
+  constexpr int B = 16;  // segments in flight per batch
 #pragma unroll 1
   for (int r0 = wave * 16; r0 < N; r0 += nwaves * 16) {
     const uint16_t *row = E + (size_t)min(r0 + n, N - 1) * K + 8 * g;
@@ -1113,12 +1120,14 @@ hipError_t enqueue_lm_head_batch(const DecodeShape &s, const DecodeArgs &a, cons
   }
   const size_t lds = (size_t)s.hidden * 32;
   if (s.hidden == 2560)
-    hipLaunchKernelGGL((k_lmhead_batch<2560>), dim3(512), dim3(256), lds, l.s, a.lm_bf16, xn, logits_b, s.vocab, m, 0);
+    hipLaunchKernelGGL((k_lmhead_batch<2560>), dim3(kHeadBatchGrid), dim3(kHeadBatchThreads), lds, l.s, a.lm_bf16, xn,
+                       logits_b, s.vocab, m, 0);
   else if (s.hidden == 512)
-    hipLaunchKernelGGL((k_lmhead_batch<512>), dim3(512), dim3(256), lds, l.s, a.lm_bf16, xn, logits_b, s.vocab, m, 0);
+    hipLaunchKernelGGL((k_lmhead_batch<512>), dim3(kHeadBatchGrid), dim3(kHeadBatchThreads), lds, l.s, a.lm_bf16, xn,
+                       logits_b, s.vocab, m, 0);
   else
-    hipLaunchKernelGGL((k_lmhead_batch<0>), dim3(512), dim3(256), lds, l.s, a.lm_bf16, xn, logits_b, s.vocab, m,
-                       s.hidden);
+    hipLaunchKernelGGL((k_lmhead_batch<0>), dim3(kHeadBatchGrid), dim3(kHeadBatchThreads), lds, l.s, a.lm_bf16, xn,
+                       logits_b, s.vocab, m, s.hidden);
   l.check();
   return l.err;
 }
