@@ -58,8 +58,9 @@ __global__ __launch_bounds__(256) void k_pf_embed(const int *__restrict__ tokens
 // operand (f16 row scaled by 2^-ea[t], bit-identical to the GEMM's own
 // preparation of the f32 row) instead of going through xn_out.  T = 1024 for
 // a few rows (more loads in flight per row when `add` is a sum of many
-// slices), 256 otherwise.
-template <bool RESID, int T>
+// slices), 256 otherwise.  FEW: `add` holds at most four slices (the prefill
+// GEMMs' split-K partials), read with rows_in4_few.
+template <bool RESID, int T, bool FEW>
 __global__ __launch_bounds__(T) void k_pf_norm(const float *__restrict__ base, RowsIn add,
                                                  const float *__restrict__ g_add, const float *__restrict__ g_out,
                                                  float *__restrict__ x_out, float *__restrict__ xn_out, int H,
@@ -76,7 +77,8 @@ __global__ __launch_bounds__(T) void k_pf_norm(const float *__restrict__ base, R
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int f = threadIdx.x + i * T;
-    x[i] = f < F4 && t >= add_row0 ? rows_in4(add, t, 4 * f) : make_float4(0.f, 0.f, 0.f, 0.f);
+    x[i] = f < F4 && t >= add_row0 ? (FEW ? rows_in4_few(add, t, 4 * f) : rows_in4(add, t, 4 * f))
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
     ss += sumsq4(x[i]);
   }
   if constexpr (RESID) {
@@ -131,12 +133,21 @@ template <bool RESID>
 hipError_t launch_pf_norm(int n, hipStream_t st, const float *base, RowsIn add, const float *g_add,
                           const float *g_out, float *x_out, float *xn_out, int H, float eps, int8_t *st_dig,
                           _Float16 *a16 = nullptr, int *ea = nullptr, float *nrm2_out = nullptr, int add_row0 = 0) {
-  if (n <= 64)
-    hipLaunchKernelGGL((k_pf_norm<RESID, 1024>), dim3(n), dim3(1024), 0, st, base, add, g_add, g_out, x_out, xn_out, H,
-                       eps, st_dig, a16, ea, nrm2_out, add_row0);
-  else
-    hipLaunchKernelGGL((k_pf_norm<RESID, 256>), dim3(n), dim3(256), 0, st, base, add, g_add, g_out, x_out, xn_out, H,
-                       eps, st_dig, a16, ea, nrm2_out, add_row0);
+  // two to four slices: the prefill GEMMs' split-K partials (a 4096-row
+  // prefill 34.51 ms against 35.29-35.48 with the sixteen-slice reader);
+  // the verify's GEMV slices keep rows_in4
+  const bool few = add.ks >= 2 && add.ks <= 4;
+  auto go = [&](auto kern, int threads) {
+    hipLaunchKernelGGL(kern, dim3(n), dim3(threads), 0, st, base, add, g_add, g_out, x_out, xn_out, H, eps, st_dig,
+                       a16, ea, nrm2_out, add_row0);
+  };
+  if (n <= 64) {
+    if (few) go(k_pf_norm<RESID, 1024, true>, 1024);
+    else go(k_pf_norm<RESID, 1024, false>, 1024);
+  } else {
+    if (few) go(k_pf_norm<RESID, 256, true>, 256);
+    else go(k_pf_norm<RESID, 256, false>, 256);
+  }
   return hipGetLastError();
 }
 

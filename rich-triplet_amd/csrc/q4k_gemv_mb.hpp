@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "rt_device.hpp"
+
 namespace rt {
 
 // One weight matrix of a batched GEMV launch: y[m][n] = sum_k A[m][k] w[n][k].
@@ -54,6 +56,22 @@ __device__ __forceinline__ float4 rows_in4(const RowsIn &r, int t, int i) {
     for (int u = 0; u < 16; ++u)
       if (z + u < r.ks) s.x += v[u].x, s.y += v[u].y, s.z += v[u].z, s.w += v[u].w;
   }
+  return s;
+}
+// rows_in4 for at most four slices (the prefill GEMMs' split-K partials,
+// each read once: nontemporal loads), without the sixteen-slice batch.
+__device__ __forceinline__ float4 rows_in4_few(const RowsIn &r, int t, int i) {
+  const float *b = r.p + (size_t)t * r.row_stride + r.col_off + i;
+  float4 v[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const uint4 q = ld_nt16(b + (size_t)min(u, r.ks - 1) * r.slice_stride);
+    v[u] = make_float4(__uint_as_float(q.x), __uint_as_float(q.y), __uint_as_float(q.z), __uint_as_float(q.w));
+  }
+  float4 s = v[0];
+#pragma unroll
+  for (int u = 1; u < 4; ++u)
+    if (u < r.ks) s.x += v[u].x, s.y += v[u].y, s.z += v[u].z, s.w += v[u].w;
   return s;
 }
 __device__ __forceinline__ float2 rows_in2(const RowsIn &r, int t, int i) {  // i even
