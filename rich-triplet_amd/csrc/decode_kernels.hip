@@ -68,6 +68,8 @@ RT_DEV void pro_load(const DecodeArgs &a, const float *__restrict__ base, const 
   }
 }
 
+// `red`: 2*T/64 floats of LDS, one half per reduction (no barrier between
+// them protects a reused array).
 template <int K, int T, Pro MODE, bool DIG = false>
 RT_DEV void pro_finish(const DecodeArgs &a, ProRegs<K, T> &r, float *__restrict__ x_out, void *lds, float *red,
                        float *__restrict__ xn_out = nullptr) {
@@ -79,14 +81,14 @@ RT_DEV void pro_finish(const DecodeArgs &a, ProRegs<K, T> &r, float *__restrict_
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < R::PER; ++i) ss += live(i) ? sumsq4(r.add[i]) : 0.f;
-    const float ra = rms_inv_from_sumsq(block_sum<T>(ss, red), inv_k, a.eps);
+    const float ra = rms_inv_from_sumsq(block_sum_fresh<T>(ss, red + T / 64), inv_k, a.eps);
 #pragma unroll
     for (int i = 0; i < R::PER; ++i) x[i] = add4(r.base[i], norm4(r.add[i], ra, r.ga[i]));
   }
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < R::PER; ++i) ss += live(i) ? sumsq4(x[i]) : 0.f;
-  const float rx = rms_inv_from_sumsq(block_sum<T>(ss, red), inv_k, a.eps);
+  const float rx = rms_inv_from_sumsq(block_sum_fresh<T>(ss, red), inv_k, a.eps);
 #pragma unroll
   for (int i = 0; i < R::PER; ++i) {
     const int f = threadIdx.x + i * T;
@@ -117,7 +119,7 @@ __global__ __launch_bounds__(T) void k_qkv(DecodeArgs a, LayerArgs L, LayerArgs 
   constexpr int K = NB * 256;
   __shared__ __attribute__((aligned(16))) uint32_t dl[NB * 4 * kDPitch];
   __shared__ float red[Tile::ROWS * NB];
-  __shared__ float bred[T / 64];
+  __shared__ float bred[2 * (T / 64)];
   const int qd = a.n_q_heads * a.head_dim, kvd = a.n_kv_heads * a.head_dim;
   const int row0 = (int)blockIdx.x * Tile::ROWS;  // ROWS divides qd and kvd (checked on the host)
   const uint8_t *W;
@@ -168,7 +170,7 @@ __global__ __launch_bounds__(256) void k_prologue(DecodeArgs a, const float *__r
                                                   const float *__restrict__ g_out, float *__restrict__ x_out,
                                                   float *__restrict__ xn_out) {
   constexpr int T = 256;
-  __shared__ float bred[T / 64];
+  __shared__ float bred[2 * (T / 64)];
   ProRegs<K, T> pr;
   pro_load<K, T, MODE>(a, base, add, g_add, g_out, pr);
   using R = ProRegs<K, T>;
@@ -224,7 +226,7 @@ __global__ __launch_bounds__(T) void k_gateup(DecodeArgs a, LayerArgs L) {
   constexpr int K = NB * 256;
   __shared__ __attribute__((aligned(16))) uint32_t dl[NB * 4 * kDPitch];
   __shared__ float red[Tile::ROWS * NB];
-  __shared__ float bred[T / 64];
+  __shared__ float bred[2 * (T / 64)];
   const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
   const int j0 = (int)blockIdx.x * GR;  // GR divides ffn (checked on the host)
   ProRegs<K, T> pr;
@@ -257,7 +259,7 @@ __global__ __launch_bounds__(T) void k_qkv8(DecodeArgs a, LayerArgs L, LayerArgs
   constexpr int K = NB32 * 32;
   __shared__ __attribute__((aligned(16))) uint32_t dl[K / 64 * kDPitch];
   __shared__ float red[Tile::ROWS * Tile::RED];
-  __shared__ float bred[T / 64];
+  __shared__ float bred[2 * (T / 64)];
   const int qd = a.n_q_heads * a.head_dim, kvd = a.n_kv_heads * a.head_dim;
   const int row0 = (int)blockIdx.x * Tile::ROWS;  // ROWS divides qd and kvd (checked on the host)
   const uint8_t *W;
@@ -290,7 +292,7 @@ __global__ __launch_bounds__(T) void k_gateup8(DecodeArgs a, LayerArgs L, int ff
   constexpr int K = NB32 * 32;
   __shared__ __attribute__((aligned(16))) uint32_t dl[K / 64 * kDPitch];
   __shared__ float red[Tile::ROWS * Tile::RED];
-  __shared__ float bred[T / 64];
+  __shared__ float bred[2 * (T / 64)];
   const int j0 = (int)blockIdx.x * GR;  // GR divides ffn (checked on the host)
   const uint16_t *Dg = reinterpret_cast<const uint16_t *>(L.wgate + (size_t)ffn * K);
   const uint16_t *Du = reinterpret_cast<const uint16_t *>(L.wup + (size_t)ffn * K);
@@ -348,7 +350,7 @@ template <int CPL, Pro MODE>
 __global__ __launch_bounds__(256) void k_qkv16(DecodeArgs a, LayerArgs L, LayerArgs prev) {
   constexpr int K = CPL * 512;
   __shared__ __attribute__((aligned(16))) float xl[K / 64 * kXPitch];
-  __shared__ float bred[4];
+  __shared__ float bred[8];
   ProRegs<K, 256> pr;
   pro_load<K, 256, MODE>(a, a.x2, a.dn, prev.g_post_ffn, L.g_in, pr);
   pro_finish<K, 256, MODE>(a, pr, a.hid, xl, bred, a.xn);
@@ -384,7 +386,7 @@ template <int CPL>
 __global__ __launch_bounds__(256) void k_gateup16(DecodeArgs a, LayerArgs L, int ffn) {
   constexpr int K = CPL * 512;
   __shared__ __attribute__((aligned(16))) float xl[K / 64 * kXPitch];
-  __shared__ float bred[4];
+  __shared__ float bred[8];
   ProRegs<K, 256> pr;
   pro_load<K, 256, Pro::Resid>(a, a.hid, a.o, L.g_post_attn, L.g_pre_ffn, pr);
   pro_finish<K, 256, Pro::Resid>(a, pr, a.x2, xl, bred);
@@ -677,7 +679,7 @@ __global__ __launch_bounds__(256) void k_lmhead(DecodeArgs a, LayerArgs last) {
   constexpr int K = CPL * 512;
   constexpr int U = 2;
   __shared__ __attribute__((aligned(16))) float xl[K / 64 * kXPitch];
-  __shared__ float bred[4];
+  __shared__ float bred[8];
   ProRegs<K, 256> pr;
   pro_load<K, 256, Pro::Resid>(a, a.x2, a.dn, last.g_post_ffn, a.g_final, pr);
   pro_finish<K, 256, Pro::Resid>(a, pr, nullptr, xl, bred);
@@ -729,7 +731,7 @@ __global__ __launch_bounds__(256) void k_lmhead(DecodeArgs a, LayerArgs last) {
 template <int K>
 __global__ __launch_bounds__(256) void k_final_norm(DecodeArgs a, LayerArgs last, float *__restrict__ out) {
   constexpr int T = 256;
-  __shared__ float bred[T / 64];
+  __shared__ float bred[2 * (T / 64)];
   ProRegs<K, T> pr;
   pro_load<K, T, Pro::Resid>(a, a.x2, a.dn, last.g_post_ffn, a.g_final, pr);
   using R = ProRegs<K, T>;

@@ -148,6 +148,19 @@ RT_DEV float block_sum(float v, float *red) {
   return s;
 }
 
+// block_sum into `red` that no earlier call in the kernel reads (a fresh
+// array per reduction): the barrier that protects a reused array is not needed.
+template <int NT>
+RT_DEV float block_sum_fresh(float v, float *red) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NT / 64; ++i) s += red[i];
+  return s;
+}
+
 template <int NT>
 RT_DEV float block_max(float v, float *red) {
   v = wave_max(v);
