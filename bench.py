@@ -152,6 +152,10 @@ def main() -> int:
                     help="with --decode-profile: every projection in BF16")
     ap.add_argument("--q4k-lm-head", action="store_true",
                     help="with --decode-profile: a Q4_K lm_head (random blocks) instead of the BF16 tied one")
+    ap.add_argument("--decode-timeline", action="store_true",
+                    help="per-wave timeline of the last layer of a config-3 decode step and of the lm_head: needs "
+                         "the traced library (make -C rich-triplet_amd trace; RT_HIP_LIB=rich-triplet_amd/"
+                         "librt_hip_trace.so)")
     ap.add_argument("--shared-weights", action="store_true",
                     help="with --decode-profile: bind every layer to layer 0's projections and norms (53 MB, "
                          "which stays in the 256 MB last-level cache between layers), to see how much of each "
@@ -220,6 +224,27 @@ def main() -> int:
         dt = (time.perf_counter() - t1) / args.steps
         print(json.dumps({"prefill_profile": "done", "tokens": pos, "steps": args.steps,
                           "ms_per_prefill": round(dt * 1e3, 3)}))
+        d.close()
+        return 0
+    if args.decode_timeline:
+        try:
+            rt.trace_read()
+        except rt.RtError as e:
+            print(json.dumps({"error": f"--decode-timeline needs the traced library: {e}"}))
+            return 2
+        d, pos = build_decode(rt, torch, dev, gen, layers, embed, final_norm, args)
+        for _ in range(args.warmup + args.steps):
+            d.decode_step_async(pos % V, pos)
+            pos += 1
+        d.synchronize()
+        out = decode_timeline(rt.trace_read())
+        for row in out["kernels"]:
+            log(f"{row['kernel']:7s} waves {row['waves']:5d}  gap before {row['gap_before_us']:5.2f} us | last wave "
+                f"starts {row['start_max']:.2f} | staged p50 {row['staged_p50']:.2f} max {row['staged_max']:.2f} | "
+                f"loads landed p50 {row['landed_p50']:.2f} max {row['landed_max']:.2f} | end p50 "
+                f"{row['end_p50']:.2f} max {row['end_max']:.2f} us")
+        log(f"layer span (q|k|v start to down end): {out['layer_span_us']:.2f} us")
+        print(json.dumps({"decode_timeline": out, "steps": args.steps, "warmup": args.warmup}))
         d.close()
         return 0
     if args.decode_profile:
@@ -755,6 +780,35 @@ def launch_probe(rt, torch, dev) -> dict:
     slope = sum((x - mx) * (y - my) for x, y in zip(xs, ys)) / sum((x - mx) ** 2 for x in xs)
     out["fit"] = {"fixed_us": round(my - slope * mx, 3), "rate_GBps": round(1e-3 / slope, 1)}
     return out
+
+
+def decode_timeline(tr) -> dict:
+    """Per-kernel statistics of a traced decode step (rt_trace_read's record:
+    [kernel][slot][entry, staged, landed, exit] in 10 ns ticks).  Slots hold
+    the last launch of each kernel: the last layer's six and the lm_head.
+    Slots not rewritten by that launch (a smaller grid than an earlier layer's)
+    carry older stamps and are dropped: only stamps from the last q|k|v launch
+    on count.  Times are us from each kernel's first wave; the gap is from the
+    previous kernel's last wave end to this kernel's first wave start."""
+    import numpy as np
+    names = ["q|k|v", "attn", "merge", "o", "gate|up", "down", "lm_head"]
+    live = [tr[k][tr[k][:, 0] > 0].astype(np.int64) for k in range(len(names))]
+    t0 = int(live[0][:, 0].min())
+    rows, prev_end = [], None
+    for k, name in enumerate(names):
+        a = live[k][live[k][:, 0] >= t0]
+        s0, end = int(a[:, 0].min()), int(a[:, 3].max())
+        rel = (a - s0) * 0.01
+        p50 = lambda c: round(float(np.percentile(rel[:, c], 50)), 3)
+        rows.append({"kernel": name, "waves": int(len(a)),
+                     "gap_before_us": round((s0 - prev_end) * 0.01, 3) if prev_end is not None else 0.0,
+                     "start_max": round(float(rel[:, 0].max()), 3), "staged_p50": p50(1),
+                     "staged_max": round(float(rel[:, 1].max()), 3), "landed_p50": p50(2),
+                     "landed_max": round(float(rel[:, 2].max()), 3), "end_p50": p50(3),
+                     "end_max": round(float(rel[:, 3].max()), 3)})
+        prev_end = end
+    span = (int(live[5][live[5][:, 0] >= t0][:, 3].max()) - t0) * 0.01
+    return {"kernels": rows, "layer_span_us": round(span, 3)}
 
 
 def build_decode(rt, torch, dev, gen, layers, embed, final_norm, args, ctx: int = 4096, formats=None):

@@ -150,6 +150,20 @@ rt_status rt_stream_read(const void *buf, size_t bytes, void *sink, void *stream
 rt_status rt_stream_read_cfg(const void *buf, size_t bytes, void *sink, void *stream, int kind, int grid);
 rt_status rt_empty_launch(int grid, int threads, void *stream);
 
+/* Per-wave timeline of the decode step's launches (no counterpart in the
+ * reference; the tracing of the survey's auxiliary subsystems).  Only a
+ * library built with RT_TRACE=1 (`make -C rich-triplet_amd trace`, which writes
+ * librt_hip_trace.so) records it; librt_hip.so returns RT_ESTATE.  The record
+ * is uint64 [kernels][slots][4]: per wave (slot = workgroup * waves + wave) the
+ * 100 MHz real-time counter at entry, once the activation staging is done,
+ * once every load of the wave has landed (an explicit wait the traced build
+ * adds), and at exit.  Kernels: 0 q|k|v, 1 attention, 2 chunk merge, 3 o
+ * projection, 4 gate|up, 5 down projection, 6 lm_head; each launch overwrites
+ * its kernel's slots, so after a step they hold the last layer's launches.
+ * With host_dst NULL only *kernels and *slots are set; otherwise bytes must be
+ * kernels * slots * 32. */
+rt_status rt_trace_read(void *host_dst, size_t bytes, int32_t *kernels, int32_t *slots);
+
 /* y = gelu_tanh(x) (autograd2.rs:3082-3091), n floats, device pointers: the
  * activation exactly as the decode step and prefill kernels compute it. */
 rt_status rt_gelu_tanh(const float *x, float *y, size_t n, void *stream);

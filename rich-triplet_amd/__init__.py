@@ -69,6 +69,7 @@ _SIGNATURES = {
     "rt_stream_read": (_i32, [_vp, _sz, _vp, _vp]),
     "rt_stream_read_cfg": (_i32, [_vp, _sz, _vp, _vp, _i32, _i32]),
     "rt_empty_launch": (_i32, [_i32, _i32, _vp]),
+    "rt_trace_read": (_i32, [_vp, _sz, C.POINTER(_i32), C.POINTER(_i32)]),
     "rt_qlinear_forward_host": (_i32, [_i32, _vp, _sz, _vp, _vp, _vp, _i64, _i64, _i64]),
     "rt_noalloc_scratch_bytes": (_sz, []),
     "rt_q6k_repack": (_i32, [_vp, _sz, _vp]),
@@ -197,6 +198,18 @@ def linear_gemv_batch(fmt: int, w, a, c, m: int, n: int, k: int, stream=None) ->
 def q4k_gemv_batch(w, a, c, m: int, n: int, k: int, stream=None) -> None:
     """c[m][n] = a[m][k] . W[n][k] for m <= 8 rows (gemv_q4k_t_batch)."""
     check(lib().rt_q4k_gemv_batch(_p(w), _p(a), _p(c), m, n, k, _stream(stream)))
+
+
+def trace_read():
+    """The decode-step timeline of a library built with RT_TRACE=1, as a uint64
+    array [kernels][slots][4] (see rt_trace_read); raises RtError(RT_ESTATE)
+    for a library built without it."""
+    import numpy as np
+    k, s = C.c_int32(0), C.c_int32(0)
+    check(lib().rt_trace_read(None, 0, C.byref(k), C.byref(s)))
+    buf = np.zeros((k.value, s.value, 4), dtype=np.uint64)
+    check(lib().rt_trace_read(buf.ctypes.data_as(C.c_void_p), buf.nbytes, None, None))
+    return buf
 
 
 def stream_read(buf, nbytes: int, sink, stream=None, kind: int = 0, grid: int = 0) -> None:

@@ -26,8 +26,49 @@
 #include "kquant_tile.hpp"
 #include "rt_device.hpp"
 #include "rt_kernels.hpp"
+#include "rt_capi_util.hpp"
 
 namespace rt {
+
+// ---------------------------------------------------------------------------
+// Optional per-wave timeline of the decode step (built with RT_TRACE=1,
+// `make -C rich-triplet_amd trace`; off in librt_hip.so, where every call
+// below compiles to nothing).  Each traced kernel records, per wave, the
+// 100 MHz real-time counter at entry, once its activation (or prologue)
+// staging is done, once all its loads have landed (an explicit wait, which
+// the traced build adds) and at exit.  Every launch of a kernel overwrites
+// its slots, so after a step they hold the last layer's launches.
+// ---------------------------------------------------------------------------
+#ifndef RT_TRACE
+#define RT_TRACE 0
+#endif
+constexpr bool kTrace = RT_TRACE != 0;
+constexpr int kTraceKernels = 7, kTraceSlots = 8192;  // qkv, attn, merge, o, gateup, down, lm_head
+enum TraceKernel { kTrQkv = 0, kTrAttn, kTrMerge, kTrO, kTrGateup, kTrDown, kTrHead };
+__device__ unsigned long long g_trace[kTrace ? kTraceKernels : 1][kTrace ? kTraceSlots : 1][4];
+
+struct Trace {
+  unsigned long long t[3] = {0, 0, 0};
+  RT_DEV void mark(int i) {
+    if constexpr (kTrace) t[i] = __builtin_amdgcn_s_memrealtime();
+  }
+  // stamp 2: wait for every outstanding load of the wave first
+  RT_DEV void mark_landed() {
+    if constexpr (kTrace) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      t[2] = __builtin_amdgcn_s_memrealtime();
+    }
+  }
+  RT_DEV void put(int kernel, int slot) const {
+    if constexpr (kTrace) {
+      const unsigned long long t3 = __builtin_amdgcn_s_memrealtime();
+      if ((threadIdx.x & 63) == 0 && slot < kTraceSlots) {
+        unsigned long long *p = g_trace[kernel][slot];
+        p[0] = t[0], p[1] = t[1], p[2] = t[2], p[3] = t3;
+      }
+    }
+  }
+};
 
 // ---------------------------------------------------------------------------
 // Prologues: build the normalised activation vector in the LDS x layout.
@@ -113,6 +154,8 @@ RT_DEV void pro_finish(const DecodeArgs &a, ProRegs<K, T> &r, float *__restrict_
 // ---------------------------------------------------------------------------
 template <int NB, int T, int ITERS, Pro MODE, bool V6 = false>
 __global__ __launch_bounds__(T) void k_qkv(DecodeArgs a, LayerArgs L, LayerArgs prev) {
+  Trace tr;
+  tr.mark(0);
   using Tile = Q4KTile<NB, T, ITERS>;
   using Tile6 = Q6KTile<NB, T, ITERS>;
   static_assert(Tile6::ROWS == Tile::ROWS, "both tiles cover the same rows per workgroup");
@@ -147,6 +190,8 @@ __global__ __launch_bounds__(T) void k_qkv(DecodeArgs a, LayerArgs L, LayerArgs 
     tile.load([&](int rl) -> const uint8_t * { return W + (size_t)(r0 + rl) * row_bytes; }, W);
   pro_finish<K, T, MODE, true>(a, pr, a.hid, dl, bred, a.xn);
   __syncthreads();
+  tr.mark(1);
+  tr.mark_landed();
   if (six) {
     tile6.compute(dl, red);
   } else {
@@ -156,6 +201,7 @@ __global__ __launch_bounds__(T) void k_qkv(DecodeArgs a, LayerArgs L, LayerArgs 
   }
   __syncthreads();
   for (int i = threadIdx.x; i < Tile::ROWS; i += T) y[r0 + i] = reduce_row<NB>(red, i);
+  tr.put(kTrQkv, (int)blockIdx.x * (T / 64) + (int)(threadIdx.x >> 6));
 }
 
 // ---------------------------------------------------------------------------
@@ -221,6 +267,8 @@ __global__ __launch_bounds__(256) void k_gelu_mul_vec(float *h, const float *__r
 // ---------------------------------------------------------------------------
 template <int NB, int T, int GR>
 __global__ __launch_bounds__(T) void k_gateup(DecodeArgs a, LayerArgs L) {
+  Trace tr;
+  tr.mark(0);
   constexpr int RPI = T / (4 * NB);
   using Tile = Q4KTile<NB, T, (2 * GR + RPI - 1) / RPI>;
   constexpr int K = NB * 256;
@@ -231,6 +279,9 @@ __global__ __launch_bounds__(T) void k_gateup(DecodeArgs a, LayerArgs L) {
   const int j0 = (int)blockIdx.x * GR;  // GR divides ffn (checked on the host)
   ProRegs<K, T> pr;
   pro_load<K, T, Pro::Resid>(a, a.hid, a.o, L.g_post_attn, L.g_pre_ffn, pr);
+  // every wave's prologue loads go out before any weight load of the
+  // workgroup: they return ahead of its weight stream
+  __syncthreads();
   Tile tile;
   tile.load([&](int rl) -> const uint8_t * {
     return rl < GR ? L.wgate + (size_t)(j0 + rl) * row_bytes
@@ -238,6 +289,8 @@ __global__ __launch_bounds__(T) void k_gateup(DecodeArgs a, LayerArgs L) {
   }, L.wgate);
   pro_finish<K, T, Pro::Resid, true>(a, pr, a.x2, dl, bred);
   __syncthreads();
+  tr.mark(1);
+  tr.mark_landed();
   tile.compute_digits_lds(dl, red);
   __syncthreads();
   for (int i = threadIdx.x; i < GR; i += T) {
@@ -245,6 +298,7 @@ __global__ __launch_bounds__(T) void k_gateup(DecodeArgs a, LayerArgs L) {
     const float u = reduce_row<NB>(red, GR + i);
     a.h[j0 + i] = mul_nc(gelu_tanh(g), u);
   }
+  tr.put(kTrGateup, (int)blockIdx.x * (T / 64) + (int)(threadIdx.x >> 6));
 }
 
 // ---------------------------------------------------------------------------
@@ -413,6 +467,8 @@ __global__ __launch_bounds__(256) void k_gateup16(DecodeArgs a, LayerArgs L, int
 template <int NB, int T, int ITERS>
 __global__ __launch_bounds__(T) void k_gemv(const uint8_t *__restrict__ W, const float *__restrict__ x,
                                             float *__restrict__ y, int n) {
+  Trace tr;
+  tr.mark(0);
   using Tile = Q4KTile<NB, T, ITERS>;
   __shared__ __attribute__((aligned(16))) uint32_t dl[NB * 4 * kDPitch];
   __shared__ float red[Tile::ROWS * NB];
@@ -426,12 +482,15 @@ __global__ __launch_bounds__(T) void k_gemv(const uint8_t *__restrict__ W, const
   }, W);
   x_store_digits<NB * 256, T>(xr, dl);
   __syncthreads();
+  tr.mark(1);
+  tr.mark_landed();
   ChunkD cx;
   chunkd_from_lds(dl, tile.slot, cx);
   tile.compute_digits(cx, red);
   __syncthreads();
   for (int i = threadIdx.x; i < Tile::ROWS; i += T)
     if (row0 + i < n) y[row0 + i] = reduce_row<NB>(red, i);
+  tr.put(NB == 40 ? kTrDown : kTrO, (int)blockIdx.x * (T / 64) + (int)(threadIdx.x >> 6));
 }
 
 // ---------------------------------------------------------------------------
@@ -498,6 +557,8 @@ RT_DEV void norm_rope_lane(LaneRow<D> &x, const LaneRow<D> &g, const LaneRow<D> 
 
 template <int D, int G, int KPW, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void k_attn(DecodeArgs a, LayerArgs L) {
+  Trace tr;
+  tr.mark(0);
   constexpr int N = D / 64, NT = 64 * WAVES;
   static_assert(D == 128 || D == 256, "head_dim 128 or 256");
   __shared__ float sm_ml[WAVES][G][2];
@@ -546,6 +607,8 @@ __global__ __launch_bounds__(64 * WAVES) void k_attn(DecodeArgs a, LayerArgs L) 
       if (w0 + k == pos) kr[k] = kn, vr[k] = vn;
   }
 
+  tr.mark(1);
+  tr.mark_landed();
   // 2. scores, softmax and values of this wave's keys
   float m[G], l[G];
   LaneRow<D> o[G];
@@ -599,6 +662,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_attn(DecodeArgs a, LayerArgs L) 
     a.part_o[ci * D + d] = O;
     if (d == 0) a.part_m[ci] = M, a.part_l[ci] = Ls;
   }
+  tr.put(kTrAttn, ((int)blockIdx.x + (int)gridDim.x * (int)blockIdx.y) * WAVES + (int)(threadIdx.x >> 6));
 }
 
 // ---------------------------------------------------------------------------
@@ -611,6 +675,8 @@ __global__ __launch_bounds__(64 * WAVES) void k_attn(DecodeArgs a, LayerArgs L) 
 // ---------------------------------------------------------------------------
 template <int D, int DW>
 __global__ __launch_bounds__(256) void k_attn_combine(DecodeArgs a, int nchunk) {
+  Trace tr;
+  tr.mark(0);
   constexpr int CG = 256 / DW;
   constexpr int R = (80 + CG - 1) / CG;  // at least 80 chunks per batch
   static_assert(D % DW == 0 && 256 % DW == 0, "DW divides D and the workgroup");
@@ -648,6 +714,8 @@ __global__ __launch_bounds__(256) void k_attn_combine(DecodeArgs a, int nchunk) 
       M = mb;
     }
   }
+  tr.mark(1);
+  tr.mark_landed();
   if (dl == 0) {
     gm[cg] = M;
     gl[cg] = Ls;
@@ -667,6 +735,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(DecodeArgs a, int nchunk) 
     }
     a.attn[(size_t)h * D + d0 + dl] = Ot / Lt;
   }
+  tr.put(kTrMerge, ((int)blockIdx.x + (int)gridDim.x * (int)blockIdx.y) * 4 + (int)(threadIdx.x >> 6));
 }
 
 // ---------------------------------------------------------------------------
@@ -676,6 +745,8 @@ __global__ __launch_bounds__(256) void k_attn_combine(DecodeArgs a, int nchunk) 
 // ---------------------------------------------------------------------------
 template <int CPL>
 __global__ __launch_bounds__(256) void k_lmhead(DecodeArgs a, LayerArgs last) {
+  Trace tr;
+  tr.mark(0);
   constexpr int K = CPL * 512;
   constexpr int U = 2;
   __shared__ __attribute__((aligned(16))) float xl[K / 64 * kXPitch];
@@ -684,6 +755,8 @@ __global__ __launch_bounds__(256) void k_lmhead(DecodeArgs a, LayerArgs last) {
   pro_load<K, 256, Pro::Resid>(a, a.x2, a.dn, last.g_post_ffn, a.g_final, pr);
   pro_finish<K, 256, Pro::Resid>(a, pr, nullptr, xl, bred);
   __syncthreads();
+  tr.mark(1);
+  tr.t[2] = tr.t[1];
   const int lane = threadIdx.x & 63;
   float xr[CPL][8];
 #pragma unroll
@@ -721,6 +794,7 @@ __global__ __launch_bounds__(256) void k_lmhead(DecodeArgs a, LayerArgs last) {
       if (lane == 0 && r0 + u < N) a.logits[r0 + u] = acc;
     }
   }
+  tr.put(kTrHead, (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
 }
 
 // ---------------------------------------------------------------------------
@@ -1166,3 +1240,14 @@ bool decode_rows_divisible(const DecodeShape &s, const char **why) {
 }
 
 }  // namespace rt
+
+extern "C" rt_status rt_trace_read(void *host_dst, size_t bytes, int32_t *kernels, int32_t *slots) {
+  if (!rt::kTrace) return rt::set_error(RT_ESTATE, "rt_trace_read: this library is built without RT_TRACE (make trace)");
+  if (kernels) *kernels = rt::kTraceKernels;
+  if (slots) *slots = rt::kTraceSlots;
+  if (!host_dst) return RT_OK;
+  if (bytes != sizeof(rt::g_trace))
+    return rt::set_error(RT_EINVAL, "rt_trace_read: bytes must be %zu", sizeof(rt::g_trace));
+  return rt::hip_error(hipMemcpyFromSymbol(host_dst, HIP_SYMBOL(rt::g_trace), bytes, 0, hipMemcpyDeviceToHost),
+                       "rt_trace_read");
+}

@@ -95,3 +95,16 @@ def test_measurement_probes_reject_bad_arguments_before_launch(rt):
 
 def test_zero_block_dequant_is_a_no_op(rt):
     assert rt.lib().rt_q4k_dequant_f32(None, 0, None, None) == rt.RT_OK
+
+
+def test_trace_read_refused_without_traced_build(rt):
+    """rt_trace_read belongs to the RT_TRACE build (librt_hip_trace.so); the
+    product library refuses it with RT_ESTATE and a message naming the build,
+    before any HIP call."""
+    if "trace" in str(rt.LIB_PATH):
+        pytest.skip("the traced build is loaded")
+    L = rt.lib()
+    k, s = C.c_int32(-1), C.c_int32(-1)
+    assert L.rt_trace_read(None, 0, C.byref(k), C.byref(s)) == rt.RT_ESTATE
+    assert "RT_TRACE" in L.rt_last_error().decode()
+    assert k.value == -1 and s.value == -1
