@@ -46,12 +46,6 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef long i64_t;
 
-// Which matrix of the launch (and its row block) workgroup column rb is.
-__device__ __forceinline__ const MbMat &mb_pick(const MbArgs &p, int &rb) {
-  int mi = 0;
-  while (mi + 1 < p.nmat && rb >= p.mat[mi].row_blocks) rb -= p.mat[mi++].row_blocks;
-  return p.mat[mi];
-}
 
 // The slice's staged digits and statistics (chunks c0 .. c0+CH-1) into LDS;
 // the loads are issued by load_stage before the weight loads, the stores by
@@ -103,7 +97,7 @@ __global__ __launch_bounds__(256) void k_q8_0_gemv_mb(MbArgs p) {
   const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
   const int j = lane & 15, g = lane >> 4;
   int rb = (int)blockIdx.x;
-  const MbMat &M = mb_pick(p, rb);
+  const MbMat M = mb_pick(p, rb);
   const int slice = (int)blockIdx.y, c0 = slice * CH;
   StageSlice<CH> sa;
   sa.load(p, c0);
@@ -151,7 +145,7 @@ __global__ __launch_bounds__(256) void k_q6k_gemv_mb(MbArgs p) {
   const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
   const int j = lane & 15, g = lane >> 4;
   int rb = (int)blockIdx.x;
-  const MbMat &M = mb_pick(p, rb);
+  const MbMat M = mb_pick(p, rb);
   const int nb = p.k / 256, slice = (int)blockIdx.y, sb0 = slice * SB;
   StageSlice<CH> sa;
   sa.load(p, sb0 * 4);
@@ -224,7 +218,7 @@ __global__ __launch_bounds__(256) void k_bf16_gemv_mb(MbArgs p, const float *__r
   const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
   const int j = lane & 15, g = lane >> 4;
   int rb = (int)blockIdx.x;
-  const MbMat &M = mb_pick(p, rb);
+  const MbMat M = mb_pick(p, rb);
   const int slice = (int)blockIdx.y, e0 = slice * CH * 64;
   // x: 8 rows x 64*CH elements, one float4 per thread per step
   constexpr int XV = (8 * CH * 16 + 255) / 256;

@@ -64,9 +64,8 @@ __global__ __launch_bounds__(256) void k_q4k_gemv_mb(MbArgs p) {
   __shared__ __attribute__((aligned(16))) float4 st_lds[CH * 8];
   const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
   const int j = lane & 15, g = lane >> 4;
-  int rb = (int)blockIdx.x, mi = 0;
-  while (mi + 1 < p.nmat && rb >= p.mat[mi].row_blocks) rb -= p.mat[mi++].row_blocks;
-  const MbMat &M = p.mat[mi];
+  int rb = (int)blockIdx.x;
+  const MbMat M = mb_pick(p, rb);
   const int nb = p.k / 256, slice = (int)blockIdx.y;
   const int sb0 = slice * KS;  // the launcher makes KS divide nb
   // The slice's activations first (clamped, unconditional loads), so their
@@ -144,9 +143,8 @@ __global__ __launch_bounds__(256) void k_mb_reduce(MbArgs p) {
     const int m = (int)(i / p.ntot), col = (int)(i % p.ntot);
     float s = 0.f;
     for (int sl = 0; sl < p.ksplit; ++sl) s += p.part[((size_t)sl * 8 + m) * p.ntot + col];
-    int mi = 0;
-    while (mi + 1 < p.nmat && col >= p.mat[mi + 1].part_off) ++mi;
-    const MbMat &M = p.mat[mi];
+    const bool in1 = p.nmat > 1 && col >= p.mat[1].part_off, in2 = p.nmat > 2 && col >= p.mat[2].part_off;
+    const MbMat M = in2 ? p.mat[2] : (in1 ? p.mat[1] : p.mat[0]);
     M.y[(size_t)m * M.n + (col - M.part_off)] = s;
   }
 }

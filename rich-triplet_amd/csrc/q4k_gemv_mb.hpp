@@ -30,6 +30,23 @@ struct MbArgs {
 
 constexpr int kMbMaxRows = 8;
 
+// The matrix of a launch that workgroup column rb falls in, and rb within it.
+// Constant indices only: every row_blocks and pointer is read from the kernel
+// arguments at once and then selected (a loop over them makes a chain of
+// dependent scalar loads ahead of the workgroup's first memory loads).
+RT_DEV MbMat mb_pick(const MbArgs &p, int &rb) {
+  const int c1 = p.mat[0].row_blocks, c2 = c1 + p.mat[1].row_blocks;
+  const bool in1 = p.nmat > 1 && rb >= c1, in2 = p.nmat > 2 && rb >= c2;
+  rb -= in2 ? c2 : (in1 ? c1 : 0);
+  MbMat m;
+  m.w = in2 ? p.mat[2].w : (in1 ? p.mat[1].w : p.mat[0].w);
+  m.y = in2 ? p.mat[2].y : (in1 ? p.mat[1].y : p.mat[0].y);
+  m.n = in2 ? p.mat[2].n : (in1 ? p.mat[1].n : p.mat[0].n);
+  m.row_blocks = in2 ? p.mat[2].row_blocks : (in1 ? p.mat[1].row_blocks : p.mat[0].row_blocks);
+  m.part_off = in2 ? p.mat[2].part_off : (in1 ? p.mat[1].part_off : p.mat[0].part_off);
+  return m;
+}
+
 // A [rows][cols] f32 operand that may be split-K partial sums: element (t, i)
 // = sum over z < ks of p[z*slice_stride + t*row_stride + col_off + i], added
 // in slice order (col_off, row_stride, slice_stride and i multiples of 4 for

@@ -146,12 +146,25 @@ struct GemvMats {
   int count;
 };
 
+// The matrix is picked with constant indices only (every bound and pointer is
+// read from the kernel arguments at once, then selected): a loop over
+// tile0[i] makes a chain of dependent scalar loads that holds back the first
+// activation and weight loads by about 0.25 us.
 template <int NB, int T, int ITERS>
 __global__ __launch_bounds__(T) void k_q4k_gemv_dig_multi(GemvMats m, const float *__restrict__ x) {
   const int b = (int)blockIdx.x;
-  int i = 0;
-  while (i + 1 < m.count && b >= m.tile0[i + 1]) ++i;
-  gemv_dig_tile<NB, T, ITERS>(m.w[i], x, m.y[i], m.n[i], (b - m.tile0[i]) * Q4KTile<NB, T, ITERS>::ROWS);
+  const uint8_t *w = m.w[0];
+  float *y = m.y[0];
+  int n = m.n[0], t0 = 0;
+#pragma unroll
+  for (int j = 1; j < kGemvMaxMats; ++j) {
+    const bool in = j < m.count && b >= m.tile0[j];
+    w = in ? m.w[j] : w;
+    y = in ? m.y[j] : y;
+    n = in ? m.n[j] : n;
+    t0 = in ? m.tile0[j] : t0;
+  }
+  gemv_dig_tile<NB, T, ITERS>(w, x, y, n, (b - t0) * Q4KTile<NB, T, ITERS>::ROWS);
 }
 
 // Any K (multiple of 256): one wave per row, lanes stride over the row's chunks.
