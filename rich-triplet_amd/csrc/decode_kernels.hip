@@ -565,20 +565,13 @@ __global__ __launch_bounds__(64 * WAVES) void k_attn(DecodeArgs a, LayerArgs L) 
   __shared__ __attribute__((aligned(16))) float sm_o[WAVES][G][D];
   const int kvh = blockIdx.y, chunk = blockIdx.x, nchunk = gridDim.x;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int pos = a.params[1];
-  const int t_end = pos + 1;
-  const int t_start = L.window > 0 ? max(0, t_end - L.window) : 0;
-  const int csize = (t_end - t_start + nchunk - 1) / nchunk;  // <= KPW*WAVES: the host sizes nchunk
-  const int c0 = t_start + chunk * csize, c1 = min(c0 + csize, t_end);
-  const int kw = (csize + WAVES - 1) / WAVES;  // <= KPW
-  const int w0 = c0 + wave * kw, w1 = min(w0 + kw, c1);
-  const int nk = max(0, w1 - w0);  // wave-uniform
-  const bool owner = w0 <= pos && pos < w1;
   const int kvd = a.n_kv_heads * D;
 
   // loads, in the order they are consumed (vector loads return in order):
   // q heads and the norm / RoPE inputs, then K rows, then V rows; rows past
-  // the wave's keys re-read its last row (or row 0) and are masked
+  // the wave's keys re-read its last row (or row 0) and are masked.  The
+  // first group does not depend on the step's position, so it goes out
+  // before the position (a load from the parameter block) has landed.
   LaneRow<D> q[G], gq, cs, sn, kn, vn, gk;
 #pragma unroll
   for (int g = 0; g < G; ++g) q[g].load(a.q + (size_t)(kvh * G + g) * D, lane);
@@ -588,12 +581,23 @@ __global__ __launch_bounds__(64 * WAVES) void k_attn(DecodeArgs a, LayerArgs L) 
   kn.load(a.k + (size_t)kvh * D, lane);
   vn.load(a.v + (size_t)kvh * D, lane);
   gk.load(L.g_k, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  const int pos = a.params[1];
+  const int t_end = pos + 1;
+  const int t_start = L.window > 0 ? max(0, t_end - L.window) : 0;
+  const int csize = (t_end - t_start + nchunk - 1) / nchunk;  // <= KPW*WAVES: the host sizes nchunk
+  const int c0 = t_start + chunk * csize, c1 = min(c0 + csize, t_end);
+  const int kw = (csize + WAVES - 1) / WAVES;  // <= KPW
+  const int w0 = c0 + wave * kw, w1 = min(w0 + kw, c1);
+  const int nk = max(0, w1 - w0);  // wave-uniform
+  const bool owner = w0 <= pos && pos < w1;
   const int last = max(w1 - 1, 0);
   LaneRow<D> kr[KPW], vr[KPW];
 #pragma unroll
   for (int k = 0; k < KPW; ++k) kr[k].load(L.kc + (size_t)min(w0 + k, last) * kvd + (size_t)kvh * D, lane);
 #pragma unroll
   for (int k = 0; k < KPW; ++k) vr[k].load(L.vc + (size_t)min(w0 + k, last) * kvd + (size_t)kvh * D, lane);
+  __builtin_amdgcn_sched_barrier(0);
 
   // 1. q heads; the new key and value at `pos`
 #pragma unroll
