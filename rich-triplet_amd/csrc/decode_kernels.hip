@@ -163,22 +163,18 @@ __global__ __launch_bounds__(T) void k_qkv(DecodeArgs a, LayerArgs L, LayerArgs 
   __shared__ __attribute__((aligned(16))) uint32_t dl[NB * 4 * kDPitch];
   __shared__ float red[Tile::ROWS * NB];
   __shared__ float bred[2 * (T / 64)];
-  const int qd = a.n_q_heads * a.head_dim, kvd = a.n_kv_heads * a.head_dim;
-  const int row0 = (int)blockIdx.x * Tile::ROWS;  // ROWS divides qd and kvd (checked on the host)
-  const uint8_t *W;
-  float *y;
-  int r0;
-  if (row0 < qd) {
-    W = L.wq, y = a.q, r0 = row0;
-  } else if (row0 < qd + kvd) {
-    W = L.wk, y = a.k, r0 = row0 - qd;
-  } else {
-    W = L.wv, y = a.v, r0 = row0 - qd - kvd;
-  }
-  const bool six = V6 && row0 >= qd + kvd;  // workgroup-uniform
-  const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
   ProRegs<K, T> pr;
   pro_load<K, T, MODE>(a, a.x2, a.dn, prev.g_post_ffn, L.g_in, pr);
+  // the matrix of this workgroup, picked by selects once the prologue loads
+  // are out (branches here load their arguments in a round of their own)
+  const int qd = a.n_q_heads * a.head_dim, kvd = a.n_kv_heads * a.head_dim;
+  const int row0 = (int)blockIdx.x * Tile::ROWS;  // ROWS divides qd and kvd (checked on the host)
+  const bool in_q = row0 < qd, in_k = !in_q && row0 < qd + kvd;
+  const uint8_t *W = in_q ? L.wq : (in_k ? L.wk : L.wv);
+  float *y = in_q ? a.q : (in_k ? a.k : a.v);
+  const int r0 = row0 - (in_q ? 0 : (in_k ? qd : qd + kvd));
+  const bool six = V6 && row0 >= qd + kvd;  // workgroup-uniform
+  const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
   // every wave's prologue loads go out before any weight load of the
   // workgroup: they return ahead of the weight stream
   __syncthreads();
@@ -692,7 +688,11 @@ __global__ __launch_bounds__(256) void k_attn_combine(DecodeArgs a, int nchunk) 
   const float *pl = a.part_l + (size_t)h * nchunk;
   const float *po = a.part_o + (size_t)h * nchunk * D + d0 + dl;
   float M = -INFINITY, Ls = 0.f, O = 0.f;
-  for (int base = cg; base < nchunk; base += CG * R) {
+  // the first batch runs unconditionally (nchunk >= 1; the loads are clamped
+  // and chunks past nchunk are masked), so the partial-buffer arguments are
+  // read with the others at the start rather than inside a branch
+  int base = cg;
+  do {
     float mi[R], li[R], oi[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -717,7 +717,8 @@ __global__ __launch_bounds__(256) void k_attn_combine(DecodeArgs a, int nchunk) 
       }
       M = mb;
     }
-  }
+    base += CG * R;
+  } while (base < nchunk);
   tr.mark(1);
   tr.mark_landed();
   if (dl == 0) {
