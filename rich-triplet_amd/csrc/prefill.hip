@@ -164,9 +164,12 @@ __global__ __launch_bounds__(256) void k_pf_qk_rope(RowsIn q, RowsIn k, RowsIn v
                                                     const int *__restrict__ p0_dev, int n, int nq, int nkv,
                                                     float eps) {
   const int heads = nq + nkv;
-  const int item = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
-  if (item >= n * heads) return;  // whole waves
-  if (p0_dev) p0 = p0_dev[0];
+  // Waves past the last item compute item n*heads-1 again and store nothing;
+  // the operands are picked by selects: no early exit or branch makes the
+  // arguments load in rounds of their own before the first data loads.
+  const int item_raw = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  const bool live = item_raw < n * heads;  // whole waves
+  const int item = min(item_raw, n * heads - 1);
   const int t = item / heads, h = item % heads;
   const float *c = cs + (size_t)t * cs_stride + cs_off;
   const int lane = (int)(threadIdx.x & 63);
@@ -205,16 +208,27 @@ __global__ __launch_bounds__(256) void k_pf_qk_rope(RowsIn q, RowsIn k, RowsIn v
       norm_rope_head_regs<D>(x0, x1, g, c, eps, dst);
     }
   };
-  if (h < nq) {
-    head(q, h * D, g_q, q_out + ((size_t)t * nq + h) * D);
+  const bool is_q = h < nq;
+  const int kh = is_q ? 0 : h - nq;
+  if constexpr (D == 256) {
+    // the v row of a k head goes with it (q heads load one they do not store)
+    const float4 vv = rows_in4(v, t, kh * D + 4 * lane);
+    if (p0_dev) p0 = p0_dev[0];  // the step's first position, read after the data loads are out
+    const size_t kdst = ((size_t)(p0 + t) * nkv + kh) * D;
+    float *dst = is_q ? q_out + ((size_t)t * nq + h) * D : kc + kdst;
+    if (!live) return;
+    head(is_q ? q : k, is_q ? h * D : kh * D, is_q ? g_q : g_k, dst);
+    if (!is_q) reinterpret_cast<float4 *>(vc + kdst)[lane] = vv;
   } else {
-    const int kh = h - nq;
-    const size_t dst = ((size_t)(p0 + t) * nkv + kh) * D;
-    head(k, kh * D, g_k, kc + dst);
-    if constexpr (D == 256)
-      reinterpret_cast<float4 *>(vc + dst)[lane] = rows_in4(v, t, kh * D + 4 * lane);
-    else
+    if (!live) return;
+    if (p0_dev) p0 = p0_dev[0];
+    if (is_q) {
+      head(q, h * D, g_q, q_out + ((size_t)t * nq + h) * D);
+    } else {
+      const size_t dst = ((size_t)(p0 + t) * nkv + kh) * D;
+      head(k, kh * D, g_k, kc + dst);
       for (int i = 2 * lane; i < D; i += 128) *reinterpret_cast<float2 *>(vc + dst + i) = rows_in2(v, t, kh * D + i);
+    }
   }
 }
 
@@ -225,16 +239,25 @@ __global__ __launch_bounds__(256) void k_pf_qk_rope(RowsIn q, RowsIn k, RowsIn v
 __global__ __launch_bounds__(256) void k_pf_gelu_mul(RowsIn g, RowsIn u, float *h, int n, int F,
                                                      int8_t *__restrict__ st_dig) {
   const int f4 = F / 4;  // a multiple of 16: the 16 lanes of a chunk stay in one row
-  const size_t n4 = (size_t)n * f4;
-  float *st_stats = st_dig ? mb_stats(st_dig, F) : nullptr;
-  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
-    const int t = (int)(i / f4), c4 = (int)(i % f4);
+  const int n4 = n * f4;  // at most 8 rows of F <= 16384 (32-bit indices: no 64-bit division)
+  // The first pass runs unconditionally at a clamped index (the launcher
+  // sizes the grid for one pass), so every argument is read at the start;
+  // lanes past n4 store nothing (whole 16-lane groups: n4 and f4 are
+  // multiples of 16).
+  int i = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  do {
+    const bool live = i < n4;
+    const int ic = min(i, n4 - 1);
+    const int t = ic / f4, c4 = ic - t * f4;
     const float4 a = rows_in4(g, t, 4 * c4), b = rows_in4(u, t, 4 * c4);
     const float4 r = make_float4(mul_nc(gelu_tanh(a.x), b.x), mul_nc(gelu_tanh(a.y), b.y),
                                  mul_nc(gelu_tanh(a.z), b.z), mul_nc(gelu_tanh(a.w), b.w));
-    reinterpret_cast<float4 *>(h)[i] = r;
-    if (st_dig) mb_stage4(st_dig, st_stats, t, c4 >> 4, c4 & 15, r, true);
-  }
+    if (live) reinterpret_cast<float4 *>(h)[i] = r;
+    // every lane runs the staging (its digits need the chunk's 16 lanes); it
+    // writes only with st_dig set
+    mb_stage4(st_dig, st_dig ? mb_stats(st_dig, F) : nullptr, t, c4 >> 4, c4 & 15, r, live && st_dig != nullptr);
+    i += (int)gridDim.x * 256;
+  } while (i < n4);
 }
 
 // The same product for the GEMM path, one row per workgroup of kGeluRowT
