@@ -242,7 +242,7 @@ def main() -> int:
             log(f"{row['kernel']:7s} waves {row['waves']:5d}  gap before {row['gap_before_us']:5.2f} us | last wave "
                 f"starts {row['start_max']:.2f} | staged p50 {row['staged_p50']:.2f} max {row['staged_max']:.2f} | "
                 f"loads landed p50 {row['landed_p50']:.2f} max {row['landed_max']:.2f} | end p50 "
-                f"{row['end_p50']:.2f} max {row['end_max']:.2f} us")
+                f"{row['end_p50']:.2f} p90 {row['end_p90']:.2f} p99 {row['end_p99']:.2f} max {row['end_max']:.2f} us")
         log(f"layer span (q|k|v start to down end): {out['layer_span_us']:.2f} us")
         print(json.dumps({"decode_timeline": out, "steps": args.steps, "warmup": args.warmup}))
         d.close()
@@ -805,6 +805,8 @@ def decode_timeline(tr) -> dict:
                      "start_max": round(float(rel[:, 0].max()), 3), "staged_p50": p50(1),
                      "staged_max": round(float(rel[:, 1].max()), 3), "landed_p50": p50(2),
                      "landed_max": round(float(rel[:, 2].max()), 3), "end_p50": p50(3),
+                     "end_p90": round(float(np.percentile(rel[:, 3], 90)), 3),
+                     "end_p99": round(float(np.percentile(rel[:, 3], 99)), 3),
                      "end_max": round(float(rel[:, 3].max()), 3)})
         prev_end = end
     span = (int(live[5][live[5][:, 0] >= t0][:, 3].max()) - t0) * 0.01

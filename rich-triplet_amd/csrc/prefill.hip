@@ -375,7 +375,6 @@ template <int D, int G, int W>
 __global__ __launch_bounds__(64 * W) void k_pf_attn(const float *__restrict__ q, const float *__restrict__ kc,
                                                     const float *__restrict__ vc, float *__restrict__ out,
                                                     PfAttnArgs p) {
-  if (p.p0_dev) p.p0 = p.p0_dev[0];
   constexpr int NT = 64 * W;                  // threads: W waves of 16 columns share each K/V stage
   constexpr int NC = 16 * W;                  // columns per workgroup
   constexpr int KB = kPfKeys;
@@ -405,30 +404,40 @@ __global__ __launch_bounds__(64 * W) void k_pf_attn(const float *__restrict__ q,
   }
   const int b = nb - 1 - bx;  // late rows (the longest key ranges) first
   const int col0 = p.row_base * G + b * NC;
-  const int key_first = pf_key_lo(p, p.p0 + col0 / G) & ~(KB - 1);
-  const int key_last = p.p0 + min(last_row, (col0 + NC - 1) / G);
   const int wt0 = (col0 + 16 * wave) / G;
   const bool wave_live = wt0 <= last_row;
-  const int wkey_lo = pf_key_lo(p, p.p0 + wt0);
-  const int wkey_hi = p.p0 + min(last_row, (col0 + 16 * wave + 15) / G);
   const int col = col0 + 16 * wave + n16;
   const int t = col / G;
   const bool col_ok = t <= last_row;
-  const int r = p.p0 + t;
-  const int klo = pf_key_lo(p, r);
   const int hq = kvh * G + col % G;
 
   // this lane's query fragment: dims 32s + 8g + [0, 8) of column `col`
-  u32x4_t qh[DS], ql[DS];
+  // (loaded here, split into bf16 parts below)
+  float4 qx0[DS], qx1[DS];
   {
     const float *qrow = q + (size_t)min(t, last_row) * qd + (size_t)hq * D + 8 * g;
 #pragma unroll
     for (int s = 0; s < DS; ++s) {
-      const float4 x0 = *reinterpret_cast<const float4 *>(qrow + 32 * s);
-      const float4 x1 = *reinterpret_cast<const float4 *>(qrow + 32 * s + 4);
-      const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-      split8(x, qh[s], ql[s]);
+      qx0[s] = *reinterpret_cast<const float4 *>(qrow + 32 * s);
+      qx1[s] = *reinterpret_cast<const float4 *>(qrow + 32 * s + 4);
     }
+  }
+
+  // the step's first position (a load from the parameter block) is read
+  // once the query loads, which do not depend on it, are out
+  __builtin_amdgcn_sched_barrier(0);
+  if (p.p0_dev) p.p0 = p.p0_dev[0];
+  const int key_first = pf_key_lo(p, p.p0 + col0 / G) & ~(KB - 1);
+  const int key_last = p.p0 + min(last_row, (col0 + NC - 1) / G);
+  const int wkey_lo = pf_key_lo(p, p.p0 + wt0);
+  const int wkey_hi = p.p0 + min(last_row, (col0 + 16 * wave + 15) / G);
+  const int r = p.p0 + t;
+  const int klo = pf_key_lo(p, r);
+  u32x4_t qh[DS], ql[DS];
+#pragma unroll
+  for (int s = 0; s < DS; ++s) {
+    const float x[8] = {qx0[s].x, qx0[s].y, qx0[s].z, qx0[s].w, qx1[s].x, qx1[s].y, qx1[s].z, qx1[s].w};
+    split8(x, qh[s], ql[s]);
   }
 
   // stage loads: rows clamped to key_last (keys past it are masked)
