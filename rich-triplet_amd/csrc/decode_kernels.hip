@@ -472,6 +472,11 @@ __global__ __launch_bounds__(T) void k_gemv(const uint8_t *__restrict__ W, const
   const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
   XRegs<NB * 256, T> xr;
   x_load<NB * 256, T>(x, xr);
+  // With a 40 KB activation vector every wave's activation loads go out
+  // before any weight load of the workgroup, so they do not queue behind
+  // the first waves' weight stream (smaller vectors do better without the
+  // barrier)
+  if constexpr (NB >= 40) __syncthreads();
   Tile tile;
   tile.load([&](int rl) -> const uint8_t * {
     return row0 + rl < n ? W + (size_t)(row0 + rl) * row_bytes : nullptr;
@@ -1126,7 +1131,7 @@ static hipError_t enqueue_layers(const DecodeShape &s, const DecodeArgs &a, cons
       }
     }
     if (!q4(kProjDown)) launch_proj(l, L.fmt[kProjDown], L.wdown, a.h, a.dn, s.hidden, s.ffn);
-    else if (s.ffn == 10240) launch_gemv<40, 960, 1>(l, L.wdown, a.h, a.dn, s.hidden);
+    else if (s.ffn == 10240) launch_gemv<40, 960, 2>(l, L.wdown, a.h, a.dn, s.hidden);
     else launch_gemv<4, 256, 1>(l, L.wdown, a.h, a.dn, s.hidden);
   }
   return l.err;

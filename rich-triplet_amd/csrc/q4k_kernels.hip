@@ -113,6 +113,11 @@ RT_DEV void gemv_dig_tile(const uint8_t *__restrict__ W, const float *__restrict
   const size_t row_bytes = (size_t)NB * kQ4KBlockBytes;
   XRegs<NB * 256, T> xr;
   x_load<NB * 256, T>(x, xr);
+  // With a 40 KB activation vector every wave's activation loads go out
+  // before any weight load of the workgroup, so they do not queue behind
+  // the first waves' weight stream (smaller vectors do better without the
+  // barrier)
+  if constexpr (NB >= 40) __syncthreads();
   tile.load([&](int rl) -> const uint8_t * {
     const int r = row0 + rl;
     return r < N ? W + (size_t)r * row_bytes : nullptr;
@@ -304,7 +309,7 @@ hipError_t launch_q4k_gemv(const void *W, const float *x, float *y, int N, int K
       if (N >= 8192) return launch_dig<10, 960, 2>(W, x, y, N, s);
       return launch_dig<10, 320, 1>(W, x, y, N, s);
     case 16: return launch_cr_auto<16, 256>(W, x, y, N, s);
-    case 40: return launch_dig<40, 960, 1>(W, x, y, N, s);
+    case 40: return launch_dig<40, 960, 2>(W, x, y, N, s);
     default: break;
   }
   return launch_q4k_gemv_generic(W, x, y, N, K, s);
