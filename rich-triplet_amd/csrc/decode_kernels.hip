@@ -930,8 +930,10 @@ __global__ __launch_bounds__(kHeadBatchThreads) void k_lmhead_batch(const uint16
 // threads of two row iterations, hidden 512 one iteration of 256 threads
 using QkvTileBig = Q4KTile<10, 320, 2>;
 using QkvTileSmall = Q4KTile<2, 256, 1>;
-// gate rows (and as many up rows) per k_gateup workgroup
-constexpr int kGateRowsBig = 20, kGateRowsSmall = 32;
+// gate rows (and as many up rows) per k_gateup workgroup; k_gateup8 (Q8_0)
+// takes 20 at hidden 2560
+constexpr int kGateRowsBig = 40, kGateRowsSmall = 32, kGateRowsBig8 = 20;
+static_assert(kGateRowsBig % kGateRowsBig8 == 0, "one divisibility check serves both gate/up tiles");
 
 struct Launch {
   hipStream_t s;
@@ -1112,11 +1114,12 @@ static hipError_t enqueue_layers(const DecodeShape &s, const DecodeArgs &a, cons
     else if (qd == 2048) launch_gemv<8, 512, 1>(l, L.wo, a.attn, a.o, s.hidden);
     else launch_gemv<2, 256, 1>(l, L.wo, a.attn, a.o, s.hidden);
     if (q4(kProjGate) && q4(kProjUp)) {
-      // 20 gate + 20 up rows per workgroup: 512 workgroups, all resident at once
+      // 40 gate + 40 up rows per workgroup (five 16-row iterations): 256
+      // workgroups, one per CU
       if (big) launch_gateup<10, 640, kGateRowsBig>(l, a, L, s.ffn);
       else launch_gateup<2, 256, kGateRowsSmall>(l, a, L, s.ffn);
     } else if (q8(kProjGate) && q8(kProjUp)) {
-      if (big) launch_gateup8<80, 640, kGateRowsBig>(l, a, L, s.ffn);
+      if (big) launch_gateup8<80, 640, kGateRowsBig8>(l, a, L, s.ffn);
       else launch_gateup8<16, 256, kGateRowsSmall>(l, a, L, s.ffn);
     } else if (b16(kProjGate) && b16(kProjUp)) {
       if (big) launch_gateup16<5>(l, a, L, s.ffn);
